@@ -1,0 +1,298 @@
+"""Benchmark: fused VQ-key decode attention on one MI355X.
+
+Default workload (the north-star target): Llama-3-8B-shaped
+paged decode at 2 bits/dim -- batch 64, 32 query / 8 KV heads, head_dim 128, 32 blocks
+of dim 4 (256 fp32 codewords each), context 32768 in 16-token vLLM-style pages, uint8
+codes, bf16 V and queries, bf16 output.  One step = one ssq_decode launch over the whole
+batch with inputs resident in HBM.
+
+Prints ONE JSON line: keys scored/s (B*Hkv*T per step / time), achieved HBM GB/s on the
+algorithmic bytes and its fraction of the 8 TB/s peak, the kernel's average launch time
+from HIP events on its own stream, and a bounded CPU-oracle baseline timed on the host.
+
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5enc] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "VQ-key decode attention: keys scored/sec/GPU + achieved HBM GB/s (% peak)"
+HBM_PEAK_GBPS = 8000.0
+MFMA_F32_PEAK_TFLOPS = 157.3
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5enc"])
+    ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+def _traffic_from_profiles(name: str):
+    """HBM bytes per launch recorded from rocprofv3 --pmc runs (profiles/<name>.md), or None."""
+    path = os.path.join(ROOT, "profiles", f"{name}.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+# ----------------------------------------------------------------------------- workloads
+def _decode_workload(name, dev, kernel):
+    import torch
+
+    from sunshape_amd import _native as N
+    from sunshape_amd import hip_ops, synthetic
+
+    if name == "c4":
+        p = synthetic.config4(dev)
+        B, Hq, Hkv, T, D, bd = 64, 32, 8, 32768, 128, 4
+        paged = True
+    else:
+        p = synthetic.config3(dev)
+        B, Hq, Hkv, T, D, bd = 16, 14, 2, 8192, 64, 2
+        paged = False
+    nb = D // bd
+    Dv = D
+    # one call through the Python surface checks shapes and builds the launch once;
+    # the timed loop replays the same C-ABI call with preallocated outputs
+    out = torch.empty(B, Hq, 1, Dv, device=dev, dtype=torch.bfloat16)
+    perm, cent = p["perm"].contiguous(), p["centroids"].contiguous()
+    q = p["q"]
+    if paged:
+        codes, v = p["code_pages"], p["v_pages"]
+        bt, sl = p["block_table"], p["seq_lens"]
+        ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], block_table=bt, seq_lens=sl, kernel=kernel)
+    else:
+        codes, v = p["codes"], p["v"]
+        ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], kernel=kernel)
+    a = N.DecodeArgs(
+        q=q.data_ptr(), q_dtype=N.SSQ_BF16, q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
+        batch=B, num_q_heads=Hq, q_len=1, head_dim=D, num_kv_heads=Hkv, has_scale=1, scale=p.meta["scale"],
+        perm=perm.data_ptr(), perm_sh=D, cent=cent.data_ptr(), cent_sh=nb * 256 * bd,
+        block_dim=bd, n_blocks=nb, n_centroids=256,
+        layout=N.SSQ_PAGED if paged else N.SSQ_CONTIGUOUS, seq_len=T,
+        codes=codes.data_ptr(), c_sb=codes.stride(0), c_sh=codes.stride(1), c_st=codes.stride(2),
+        block_table=bt.data_ptr() if paged else None, bt_sb=bt.stride(0) if paged else 0,
+        seq_lens=sl.data_ptr() if paged else None, page_size=16 if paged else 0,
+        v=v.data_ptr(), v_dtype=N.SSQ_BF16, value_dim=Dv, v_sb=v.stride(0), v_sh=v.stride(1), v_st=v.stride(2),
+        out=out.data_ptr(), o_sb=out.stride(0), o_sh=out.stride(1), o_sl=out.stride(2), kernel=kernel,
+    )
+    L = N.lib()
+    ws_bytes = L.ssq_decode_workspace_size(ctypes.byref(a))
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def step():
+        rc = L.ssq_decode(ctypes.byref(a), ws.data_ptr(), ws_bytes, stream)
+        if rc:
+            N.check(rc)
+
+    step()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref), "timed launch differs from the checked Python-surface launch"
+    keys = B * Hkv * T
+    algo_bytes = (B * Hkv * T * nb                 # uint8 codes
+                  + B * Hkv * T * Dv * 2           # bf16 V
+                  + B * Hq * D * 2                 # bf16 q
+                  + B * Hq * Dv * 2                # bf16 out
+                  + Hkv * nb * 256 * bd * 4        # fp32 codebooks
+                  + Hkv * D * 8                    # int64 permutations
+                  + (B * (T // 16) * 4 if paged else 0))  # int32 block table
+    cfg = {"workload": "C4 paged fused decode (Llama-3-8B layer, 2 bits/dim)" if paged else
+           "C3 contiguous fused decode (Qwen2.5-0.5B layer, 4 bits/dim)",
+           "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "context": T, "block_dim": bd,
+           "bits_per_dim": 8 / bd, "n_centroids": 256, "layout": "paged16" if paged else "contiguous",
+           "kernel": kernel}
+    unit_data = (p, paged)
+    return step, keys, algo_bytes, cfg, unit_data, "ssq_decode"
+
+
+def _scores_workload(dev):
+    import torch
+
+    from sunshape_amd import _native as N
+    from sunshape_amd import synthetic
+
+    p = synthetic.config2(dev)
+    B, Hq, Hkv, T, D, bd = 16, 14, 2, 8192, 64, 8
+    nb = D // bd
+    out = torch.empty(B, Hq, 1, T, device=dev, dtype=torch.float32)
+    q, codes, perm, cent = p["q"], p["codes"], p["perm"], p["centroids"]
+    a = N.DecodeArgs(
+        q=q.data_ptr(), q_dtype=N.SSQ_BF16, q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
+        batch=B, num_q_heads=Hq, q_len=1, head_dim=D, num_kv_heads=Hkv, has_scale=1, scale=p.meta["scale"],
+        perm=perm.data_ptr(), perm_sh=D, cent=cent.data_ptr(), cent_sh=nb * 256 * bd,
+        block_dim=bd, n_blocks=nb, n_centroids=256, layout=N.SSQ_CONTIGUOUS, seq_len=T,
+        codes=codes.data_ptr(), c_sb=codes.stride(0), c_sh=codes.stride(1), c_st=codes.stride(2),
+        scores=out.data_ptr(), s_sb=out.stride(0), s_sh=out.stride(1), s_sl=out.stride(2),
+    )
+    L = N.lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def step():
+        rc = L.ssq_attention_scores(ctypes.byref(a), stream)
+        if rc:
+            N.check(rc)
+
+    keys = B * Hkv * T
+    algo = B * Hkv * T * nb + B * Hq * T * 4 + B * Hq * D * 2 + Hkv * nb * 256 * bd * 4 + Hkv * D * 8
+    cfg = {"workload": "C2 GQA scores (Qwen2.5-0.5B layer, 1 bit/dim)", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+           "head_dim": D, "context": T, "block_dim": bd, "bits_per_dim": 1.0, "layout": "contiguous"}
+    return step, keys, algo, cfg, None, "ssq_attention_scores"
+
+
+def _encode_workload(dev, kernel):
+    import torch
+
+    from sunshape_amd import hip_ops, synthetic
+
+    p = synthetic.config5(dev)
+    heavy = p["heavy"].tolist()
+    keys_t = p["keys"]
+    B, Hkv, S, D = keys_t.shape
+
+    def step():
+        hip_ops.encode(keys_t, p["perm"], p["centroids"], heavy=heavy, kernel=kernel)
+
+    n = B * Hkv * S
+    algo = n * D * 2 + n * 32 + n * 4 * 2 * 2 + Hkv * 32 * 256 * 2 * 4
+    cfg = {"workload": "C5 encode (16 x 2 x 16384 bf16 keys, 28 VQ + 4 bf16 blocks of dim 2)", "keys": n,
+           "head_dim": D, "block_dim": 2, "heavy_blocks": 4, "kernel": kernel}
+    return step, n, algo, cfg, None, "ssq_encode"
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+def _cpu_baseline(unit_data, seconds):
+    """The oracle's eager restatement of the reference decode path, one (batch, KV head) at a time."""
+    import numpy as np
+    import torch
+
+    from oracle import vq_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_limits
+    except Exception:  # pragma: no cover
+        threadpool_limits = None
+    p, paged = unit_data
+    G = p.meta["Hq"] // p.meta["Hkv"] if "Hq" in p.meta else 7
+    T = p.meta["T"]
+    perm, cent = p["perm"].cpu().numpy(), p["centroids"].cpu().numpy()
+    q = p["q"].float().cpu().numpy()
+    rng = np.random.default_rng(0)
+    units, elapsed = 0, 0.0
+    import contextlib
+
+    limit = threadpool_limits(limits=1) if threadpool_limits else contextlib.nullcontext()
+    with limit:
+        while elapsed < seconds and units < 64:
+            b = int(rng.integers(p.meta["B"]))
+            kv = int(rng.integers(p.meta["Hkv"]))
+            if paged:
+                pages = p["block_table"][b].long()
+                codes = p["code_pages"][pages][:, kv].reshape(-1, p["code_pages"].shape[-1]).cpu().numpy()
+                v = p["v_pages"][pages][:, kv].permute(0, 2, 1).reshape(-1, p["v_pages"].shape[2]).float().cpu().numpy()
+            else:
+                codes = p["codes"][b, kv].cpu().numpy()
+                v = p["v"][b, kv].float().cpu().numpy()
+            qu = q[b, kv * G:(kv + 1) * G][None]
+            t0 = time.perf_counter()
+            O.decode_attention(qu, codes[None, None], v[None, None], cent[kv][None], perm[kv][None], p.meta["scale"],
+                               "bf16", "bf16")
+            elapsed += time.perf_counter() - t0
+            units += 1
+    return {"value": units * T / elapsed, "unit": "keys/s", "cores": 1, "kind": "port",
+            "sample": f"{units} (batch, KV head) units x {T} keys, numpy oracle (dequantize, LUT scores, fp32 "
+                      f"softmax, bf16 cast, P.V), single thread, {elapsed:.1f} s"}
+
+
+# ----------------------------------------------------------------------------- main
+def main():
+    args = _args()
+    if args.gpus != 1:
+        sys.exit(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}")
+    import torch
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.workload in ("c4", "c3"):
+        step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
+    elif args.workload == "c2":
+        step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev)
+    else:
+        step, keys, algo_bytes, cfg, unit_data, kname = _encode_workload(dev, args.kernel)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # per-launch HIP events on the launch stream (torch's current stream, which the C ABI is given)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record()
+        step()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    avg_ms = sum(launch_ms) / len(launch_ms)
+    ms_per_step = wall * 1e3 / args.steps
+    achieved_gbps = algo_bytes / (avg_ms * 1e-3) / 1e9
+    traffic = _traffic_from_profiles(f"{kname}_{args.workload}_pmc")
+    line = {
+        "metric": METRIC,
+        "value": keys / (ms_per_step * 1e-3),
+        "unit": "keys/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": cfg,
+        "hbm_GBps": achieved_gbps,
+        "pct_hbm_peak": 100.0 * achieved_gbps / HBM_PEAK_GBPS,
+        "kernel_avg_ms": avg_ms,
+        "kernel_min_ms": min(launch_ms),
+        "roofline": {"bound": "hbm", "achieved": achieved_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved_gbps / HBM_PEAK_GBPS, "traffic": traffic,
+                     "kernel": kname, "algorithmic_bytes_per_launch": algo_bytes},
+    }
+    if args.workload == "c5enc":
+        flop = keys * 28 * 256 * 2 * 4
+        tf = flop / (avg_ms * 1e-3) / 1e12
+        line["unit"] = "keys/s"
+        line["metric"] = "VQ encode: keys encoded/sec/GPU"
+        line["roofline"] = {"bound": "mfma", "achieved": tf, "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": tf / MFMA_F32_PEAK_TFLOPS, "traffic": traffic, "kernel": kname,
+                            "algorithmic_flop_per_launch": flop}
+    if not args.no_cpu and unit_data is not None:
+        line["cpu_baseline"] = _cpu_baseline(unit_data, args.cpu_seconds)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

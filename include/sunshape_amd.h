@@ -1,0 +1,168 @@
+/*
+ * sunshape_amd -- C ABI of the MI355X (gfx950) VQ-key decode-attention library.
+ *
+ * Plain pointers, sizes and strides only.  Every tensor pointer is a device
+ * pointer; strides are in ELEMENTS of the tensor's own dtype.  `stream` is a
+ * hipStream_t passed as void* (NULL = the null stream).  All entry points are
+ * asynchronous on `stream`, allocate no device memory, and return SSQ_OK or an
+ * error code whose message ssq_last_error() returns (thread-local).
+ *
+ * Each argument struct starts with `struct_size`; the library rejects a caller
+ * whose struct layout differs from this header (SSQ_ERR_ABI).
+ *
+ * Reference interfaces (paths relative to the gauravsaini/sunshape tree):
+ *   ssq_attention_scores  <- sunshape/triton_kernels.py:549-609
+ *                            sunshape_attention_scores[_strict](codec, query, quantized_key)
+ *                            and sunshape/codec.py:403-422 SunShapeBlockCodec.attention_scores
+ *   ssq_decode            <- sunshape/vllm_attn_backend.py:216-253 _apply_quantized_attention
+ *                            (called from SunShapeAttentionImpl.forward, :271-305)
+ *   ssq_lut_build         <- sunshape/triton_kernels.py:381-408 _precompute_query_centroid_dots
+ *   ssq_encode            <- sunshape/codec.py:362-385 SunShapeBlockCodec.quantize and
+ *                            sunshape/vllm_attn_backend.py:101-123 quantize_key_states
+ *   ssq_dequantize        <- sunshape/codec.py:387-398 SunShapeBlockCodec.dequantize
+ */
+#ifndef SUNSHAPE_AMD_H
+#define SUNSHAPE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SSQ_ABI_VERSION 1
+
+enum ssq_status {
+    SSQ_OK = 0,
+    SSQ_ERR_INVALID = 1,   /* argument check failed; message names the argument */
+    SSQ_ERR_HIP = 2,       /* a HIP runtime call failed (launch, attribute) */
+    SSQ_ERR_ABI = 3,       /* struct_size mismatch between caller and library */
+    SSQ_ERR_UNSUPPORTED = 4 /* valid input outside what the kernels implement */
+};
+
+enum ssq_dtype { SSQ_F32 = 0, SSQ_BF16 = 1, SSQ_F16 = 2 };
+
+/* Layout of the key codes and values. */
+enum ssq_layout {
+    SSQ_CONTIGUOUS = 0, /* codes [B, Hkv, T, nb] uint8, V [B, Hkv, T, Dv] (token-major) */
+    SSQ_PAGED = 1       /* vLLM-style pages: codes [P, Hkv, page, nb] uint8,
+                           V [P, Hkv, Dv, page] (dim-major inside a page, vLLM's value layout),
+                           block_table [B, max_pages] int32, seq_lens [B] int32 */
+};
+
+/*
+ * One decode (or scores-only) problem.  Rows: for batch b and KV head kv the
+ * G*Lq query rows q[b, kv*G + g, i, :] (g < G = Hq/Hkv, i < Lq) share the KV
+ * head's codes and values; row index r = g*Lq + i, as in the reference's
+ * query_slice.reshape(-1, D).
+ *
+ * Codec: permutation perm[kv*perm_sh + j] (int64, x_perm[j] = x[perm[j]]),
+ * codebook cent[kv*cent_sh + (blk*nc + c)*bd + d] fp32.  perm_sh / cent_sh are
+ * 0 for the reference's one-codec-per-layer layout.
+ *
+ * Passthrough (SunShape-Mixed) blocks: heavy_mask bit blk (blk < 128) marks a
+ * block scored from stored values instead of codes.  pt holds them; the slot of
+ * heavy block blk is blk itself when pt_dense != 0 (the reference's dense
+ * [T, nb, bd] layout, codec.py:368) and its ordinal among heavy blocks otherwise.
+ * Contiguous: pt[b*pt_sb + kv*pt_sh + t*pt_st + slot*bd + d].
+ * Paged:      pt[page*pt_sb + kv*pt_sh + (t % page_size)*pt_st + slot*bd + d].
+ */
+typedef struct ssq_decode_args {
+    uint32_t struct_size;
+    /* query [B, Hq, Lq, D]; D contiguous */
+    const void* q; int32_t q_dtype; int64_t q_sb, q_sh, q_sl;
+    int32_t batch, num_q_heads, q_len, head_dim, num_kv_heads;
+    int32_t has_scale;   /* 1: q <- round_to_q_dtype(q * scale), as query_slice * float(scale) */
+    float scale;
+    /* codec */
+    const int64_t* perm; int64_t perm_sh;
+    const float* cent; int64_t cent_sh;
+    int32_t block_dim, n_blocks, n_centroids;
+    /* passthrough blocks */
+    uint64_t heavy_mask[2];
+    int32_t pt_dense; int32_t pt_dtype;
+    const void* pt; int64_t pt_sb, pt_sh, pt_st;
+    /* keys */
+    int32_t layout;      /* enum ssq_layout */
+    int32_t seq_len;     /* T (contiguous) / max context (paged) */
+    const uint8_t* codes; int64_t c_sb, c_sh, c_st;  /* contiguous: b,kv,t strides; paged: page,kv,t strides */
+    const int32_t* block_table; int64_t bt_sb; const int32_t* seq_lens; int32_t page_size;
+    /* values (NULL for scores-only); Dv contiguous (contiguous) / page contiguous (paged) */
+    const void* v; int32_t v_dtype; int32_t value_dim;
+    int64_t v_sb, v_sh, v_st;   /* contiguous: b,kv,t strides; paged: page,kv,dv strides */
+    /* additive fp32 mask [b, h, i, t] via strides (0 = broadcast); NULL = none */
+    const float* mask; int64_t m_sb, m_sh, m_sl, m_st;
+    /* outputs */
+    void* out; int64_t o_sb, o_sh, o_sl;      /* [B, Hq, Lq, Dv] in v_dtype; NULL for scores-only */
+    float* lse;                                /* [B, Hq, Lq] fp32 contiguous or NULL */
+    float* scores; int64_t s_sb, s_sh, s_sl;  /* raw logits [B, Hq, Lq, T] fp32 (t contiguous) or NULL */
+    /* tuning: 0 = library heuristic */
+    int32_t num_splits;
+    int32_t kernel;      /* 0 auto, 1 generic LUT/VALU kernel, 2 MFMA paged kernel */
+} ssq_decode_args;
+
+/* Bytes of device workspace ssq_decode / ssq_attention_scores need (0 if none). */
+size_t ssq_decode_workspace_size(const ssq_decode_args* a);
+
+/* Fused decode: out = softmax(q.k_hat + mask) @ V per row, plus lse / raw scores on request.
+ * Replaces sunshape/vllm_attn_backend.py:216-253 (scores from :238, mask :241-249,
+ * softmax and cast :251, P.V :252) for all batches and KV heads in one call. */
+int ssq_decode(const ssq_decode_args* a, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Scores only (a->v == NULL, a->scores != NULL): scores[r, t] = q_r . k_hat_t (unscaled
+ * unless has_scale).  Replaces sunshape/triton_kernels.py:570-609 and codec.py:403-422. */
+int ssq_attention_scores(const ssq_decode_args* a, void* stream);
+
+/* LUT[r, blk, c] = sum_d q_perm[r, blk*bd + d] * cent[blk, c, d], fp32 [R, nb, nc].
+ * q: [R, D] (row stride q_sr), perm [D], cent [nb, nc, bd].
+ * Replaces sunshape/triton_kernels.py:381-408. */
+int ssq_lut_build(const void* q, int32_t q_dtype, int64_t q_sr, int32_t rows, int32_t head_dim,
+                  const int64_t* perm, const float* cent, int32_t block_dim, int32_t n_centroids,
+                  int32_t has_scale, float scale, float* lut, void* stream);
+
+/*
+ * Nearest-codeword encode of keys [B, Hkv, S, D] (k[b*k_sb + kv*k_sh + s*k_ss + d]).
+ * codes[b, kv, s, blk] = argmin_c sqrt(max(0, |x_blk|^2 - 2 x_blk.c + |c|^2)) evaluated
+ * with torch.cdist's mm formulation, lowest index on ties; heavy blocks get code 0 and
+ * their values are copied to pt in pt_dtype (slot = ordinal among heavy blocks, or the
+ * block index itself when pt_dense != 0: the reference's dense [.., nb, bd] layout, whose
+ * light-block entries the caller pre-fills with zeros).
+ * Contiguous output: codes[b*c_sb + kv*c_sh + s*c_st + blk], pt[b*pt_sb + kv*pt_sh + s*pt_st + slot*bd + d].
+ * Paged output (slot_mapping != NULL, [B, S] int64 token slots): slot -> page = slot / page_size,
+ *   off = slot % page_size; codes[page*c_sb + kv*c_sh + off*c_st + blk] (pt likewise).
+ * Replaces sunshape/codec.py:362-385 and the loop of sunshape/vllm_attn_backend.py:101-123.
+ */
+typedef struct ssq_encode_args {
+    uint32_t struct_size;
+    const void* keys; int32_t k_dtype; int64_t k_sb, k_sh, k_ss;
+    int32_t batch, num_kv_heads, seq_len, head_dim;
+    const int64_t* perm; int64_t perm_sh;
+    const float* cent; int64_t cent_sh;
+    int32_t block_dim, n_blocks, n_centroids;
+    uint64_t heavy_mask[2];
+    uint8_t* codes; int64_t c_sb, c_sh, c_st;
+    void* pt; int32_t pt_dtype; int32_t pt_dense; int64_t pt_sb, pt_sh, pt_st;
+    const int64_t* slot_mapping; int64_t sm_sb; int32_t page_size;
+    int32_t kernel;      /* 0 auto, 1 VALU exact scan, 2 MFMA screen + exact certification */
+} ssq_encode_args;
+
+int ssq_encode(const ssq_encode_args* a, void* stream);
+
+/* k_hat[t, j] (original basis, fp32 [T, D] with row stride o_st) from codes [T, nb]
+ * (row stride c_st) and optional passthrough pt (dense [T, nb, bd] fp32 when pt_dense,
+ * else compact [T, n_heavy, bd]; row stride pt_st).  Replaces sunshape/codec.py:387-398. */
+int ssq_dequantize(const uint8_t* codes, int64_t c_st, int32_t tokens,
+                   const int64_t* perm, const float* cent, int32_t head_dim, int32_t block_dim,
+                   int32_t n_centroids, const uint64_t* heavy_mask, int32_t pt_dense,
+                   const void* pt, int32_t pt_dtype, int64_t pt_st,
+                   float* out, int64_t o_st, void* stream);
+
+const char* ssq_last_error(void);
+int ssq_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SUNSHAPE_AMD_H */

@@ -1,0 +1,104 @@
+/*
+ * CPU restatement of SunShape's nearest-codeword encode -- TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
+ * this library, and only as the checker.  The product path never calls it.
+ *
+ * Follows sunshape/codec.py:362-385 (SunShapeBlockCodec.quantize):
+ *   keys.float() -> x[..., perm] -> per block b:
+ *     heavy (mixed mode): passthrough_values[:, b, :] = x_b, index 0
+ *     else: argmin_c torch.cdist(x_b @ E_b^T, C_b @ E_b^T)      (E = identity here)
+ * torch.cdist with >25 rows takes ATen's mm formulation (_euclidean_dist):
+ *   x1_ = [-2*x, |x|^2, 1],  x2_ = [c, 1, |c|^2],  d2 = x1_ @ x2_^T,
+ *   d = sqrt(clamp_min(d2, 0)),  argmin -> first minimum.
+ * |x|^2 is x.pow(2).sum(-1): each square rounded, summed left to right.
+ * The fp32 GEMM with K = bd + 2 accumulates k = 0..K-1 in order with fused
+ * multiply-adds, starting from the first product (checked bit-for-bit against
+ * torch's CPU matmul in tests/test_oracle_encode.py).
+ * sqrt is the correctly rounded IEEE square root (see that test for why).
+ */
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+/* |v|^2 as x.pow(2).sum(-1): left-to-right sum of rounded squares. */
+static float sq_norm(const float* v, int bd) {
+    float s = v[0] * v[0];
+    for (int d = 1; d < bd; ++d) {
+        float t = v[d] * v[d];
+        s = s + t;
+    }
+    return s;
+}
+
+/* Pre-sqrt distance of the mm formulation, k ascending, fused multiply-adds. */
+static float mm_dist2(const float* x, float xn, const float* c, float cn, int bd) {
+    float acc = (-2.0f * x[0]) * c[0];
+    for (int d = 1; d < bd; ++d) acc = fmaf(-2.0f * x[d], c[d], acc);
+    acc = fmaf(xn, 1.0f, acc);
+    acc = fmaf(1.0f, cn, acc);
+    return acc;
+}
+
+/* Distance matrix for one block: e2[i*nc+j] = pre-sqrt value, d[i*nc+j] = sqrt(clamp_min(., 0)). */
+void oracle_block_dist(const float* x, int64_t n, const float* c, int nc, int bd, float* e2, float* d) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float* xi = x + i * bd;
+        float xn = sq_norm(xi, bd);
+        for (int j = 0; j < nc; ++j) {
+            const float* cj = c + (int64_t)j * bd;
+            float v = mm_dist2(xi, xn, cj, sq_norm(cj, bd), bd);
+            if (e2) e2[i * nc + j] = v;
+            if (d) d[i * nc + j] = sqrtf(v > 0.0f ? v : 0.0f);
+        }
+    }
+}
+
+/*
+ * Encode n keys.
+ *   keys      fp32 [n, D] in the original basis (bf16 keys are upcast exactly by the caller)
+ *   perm      int64 [D]   forward permutation: x_perm[j] = x[perm[j]]
+ *   cent      fp32 [nb, nc, bd] codebook in the permuted basis
+ *   heavy     uint8 [nb] or NULL; nonzero = passthrough block (index 0, values copied)
+ *   codes     uint8 [n, nb] out
+ *   pt        fp32 [n, nb, bd] out or NULL; zeros on light blocks (dense, as the reference)
+ */
+void oracle_encode(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
+                   int nb, int nc, int bd, const uint8_t* heavy, uint8_t* codes, float* pt) {
+    float* cn = (float*)malloc(sizeof(float) * (size_t)nb * (size_t)nc);
+    float* xp = (float*)malloc(sizeof(float) * (size_t)D);
+    for (int b = 0; b < nb; ++b)
+        for (int j = 0; j < nc; ++j)
+            cn[b * nc + j] = sq_norm(cent + ((int64_t)b * nc + j) * bd, bd);
+    for (int64_t i = 0; i < n; ++i) {
+        const float* k = keys + i * D;
+        for (int j = 0; j < D; ++j) xp[j] = k[perm[j]];
+        for (int b = 0; b < nb; ++b) {
+            const float* xb = xp + b * bd;
+            if (heavy && heavy[b]) {
+                codes[i * nb + b] = 0;
+                if (pt)
+                    for (int d = 0; d < bd; ++d) pt[(i * nb + b) * bd + d] = xb[d];
+                continue;
+            }
+            if (pt)
+                for (int d = 0; d < bd; ++d) pt[(i * nb + b) * bd + d] = 0.0f;
+            const float* cb = cent + (int64_t)b * nc * bd;
+            float xn = sq_norm(xb, bd);
+            float best = INFINITY;
+            int best_j = 0;
+            for (int j = 0; j < nc; ++j) {
+                float v = mm_dist2(xb, xn, cb + (int64_t)j * bd, cn[b * nc + j], bd);
+                float dj = sqrtf(v > 0.0f ? v : 0.0f);
+                if (dj < best) { /* strict: the first minimum wins */
+                    best = dj;
+                    best_j = j;
+                }
+            }
+            codes[i * nb + b] = (uint8_t)best_j;
+        }
+    }
+    free(xp);
+    free(cn);
+}

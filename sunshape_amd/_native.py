@@ -1,0 +1,192 @@
+"""ctypes binding of the sunshape_amd C ABI (include/sunshape_amd.h).
+
+torch is imported before the library is loaded so that the library's
+``libamdhip64.so.7`` dependency resolves to the HIP runtime torch already
+mapped: one HIP runtime per process, so torch's streams and device pointers
+are valid in the library.
+
+There is no CPU fallback anywhere in this package: if the library is missing,
+every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must precede loading the HIP library)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libsunshape_amd.so")
+
+SSQ_OK = 0
+SSQ_ERR_INVALID = 1
+SSQ_ERR_HIP = 2
+SSQ_ERR_ABI = 3
+SSQ_ERR_UNSUPPORTED = 4
+
+SSQ_F32, SSQ_BF16, SSQ_F16 = 0, 1, 2
+SSQ_CONTIGUOUS, SSQ_PAGED = 0, 1
+
+DTYPE_CODE = {torch.float32: SSQ_F32, torch.bfloat16: SSQ_BF16, torch.float16: SSQ_F16}
+
+# every function include/sunshape_amd.h declares
+EXPORTED_SYMBOLS = (
+    "ssq_decode_workspace_size",
+    "ssq_decode",
+    "ssq_attention_scores",
+    "ssq_lut_build",
+    "ssq_encode",
+    "ssq_dequantize",
+    "ssq_last_error",
+    "ssq_abi_version",
+)
+
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_u32 = ctypes.c_uint32
+_f32 = ctypes.c_float
+
+
+class DecodeArgs(ctypes.Structure):
+    """Mirror of ``ssq_decode_args``."""
+
+    _fields_ = [
+        ("struct_size", _u32),
+        ("q", _vp), ("q_dtype", _i32), ("q_sb", _i64), ("q_sh", _i64), ("q_sl", _i64),
+        ("batch", _i32), ("num_q_heads", _i32), ("q_len", _i32), ("head_dim", _i32), ("num_kv_heads", _i32),
+        ("has_scale", _i32), ("scale", _f32),
+        ("perm", _vp), ("perm_sh", _i64),
+        ("cent", _vp), ("cent_sh", _i64),
+        ("block_dim", _i32), ("n_blocks", _i32), ("n_centroids", _i32),
+        ("heavy_mask", ctypes.c_uint64 * 2),
+        ("pt_dense", _i32), ("pt_dtype", _i32),
+        ("pt", _vp), ("pt_sb", _i64), ("pt_sh", _i64), ("pt_st", _i64),
+        ("layout", _i32), ("seq_len", _i32),
+        ("codes", _vp), ("c_sb", _i64), ("c_sh", _i64), ("c_st", _i64),
+        ("block_table", _vp), ("bt_sb", _i64), ("seq_lens", _vp), ("page_size", _i32),
+        ("v", _vp), ("v_dtype", _i32), ("value_dim", _i32),
+        ("v_sb", _i64), ("v_sh", _i64), ("v_st", _i64),
+        ("mask", _vp), ("m_sb", _i64), ("m_sh", _i64), ("m_sl", _i64), ("m_st", _i64),
+        ("out", _vp), ("o_sb", _i64), ("o_sh", _i64), ("o_sl", _i64),
+        ("lse", _vp),
+        ("scores", _vp), ("s_sb", _i64), ("s_sh", _i64), ("s_sl", _i64),
+        ("num_splits", _i32), ("kernel", _i32),
+    ]
+
+    def __init__(self, **kw):
+        super().__init__()
+        self.struct_size = ctypes.sizeof(DecodeArgs)
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
+class EncodeArgs(ctypes.Structure):
+    """Mirror of ``ssq_encode_args``."""
+
+    _fields_ = [
+        ("struct_size", _u32),
+        ("keys", _vp), ("k_dtype", _i32), ("k_sb", _i64), ("k_sh", _i64), ("k_ss", _i64),
+        ("batch", _i32), ("num_kv_heads", _i32), ("seq_len", _i32), ("head_dim", _i32),
+        ("perm", _vp), ("perm_sh", _i64),
+        ("cent", _vp), ("cent_sh", _i64),
+        ("block_dim", _i32), ("n_blocks", _i32), ("n_centroids", _i32),
+        ("heavy_mask", ctypes.c_uint64 * 2),
+        ("codes", _vp), ("c_sb", _i64), ("c_sh", _i64), ("c_st", _i64),
+        ("pt", _vp), ("pt_dtype", _i32), ("pt_dense", _i32), ("pt_sb", _i64), ("pt_sh", _i64), ("pt_st", _i64),
+        ("slot_mapping", _vp), ("sm_sb", _i64), ("page_size", _i32),
+        ("kernel", _i32),
+    ]
+
+    def __init__(self, **kw):
+        super().__init__()
+        self.struct_size = ctypes.sizeof(EncodeArgs)
+        for k, v in kw.items():
+            setattr(self, k, v)
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    P = ctypes.POINTER
+    lib.ssq_decode_workspace_size.argtypes = [P(DecodeArgs)]
+    lib.ssq_decode_workspace_size.restype = ctypes.c_size_t
+    lib.ssq_decode.argtypes = [P(DecodeArgs), _vp, ctypes.c_size_t, _vp]
+    lib.ssq_decode.restype = ctypes.c_int
+    lib.ssq_attention_scores.argtypes = [P(DecodeArgs), _vp]
+    lib.ssq_attention_scores.restype = ctypes.c_int
+    lib.ssq_lut_build.argtypes = [_vp, _i32, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _vp, _vp]
+    lib.ssq_lut_build.restype = ctypes.c_int
+    lib.ssq_encode.argtypes = [P(EncodeArgs), _vp]
+    lib.ssq_encode.restype = ctypes.c_int
+    lib.ssq_dequantize.argtypes = [_vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _i64,
+                                   _vp, _i64, _vp]
+    lib.ssq_dequantize.restype = ctypes.c_int
+    lib.ssq_last_error.argtypes = []
+    lib.ssq_last_error.restype = ctypes.c_char_p
+    lib.ssq_abi_version.argtypes = []
+    lib.ssq_abi_version.restype = ctypes.c_int
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library once; raise if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"sunshape_amd HIP library is not built ({LIB_PATH}); run `python -m sunshape_amd.build`"
+                )
+            handle = ctypes.CDLL(LIB_PATH)
+            _declare(handle)
+            if handle.ssq_abi_version() != 1:
+                raise RuntimeError("sunshape_amd library ABI version mismatch")
+            _lib = handle
+    return _lib
+
+
+class SunShapeKernelError(RuntimeError):
+    """A sunshape_amd entry point returned an error status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+def check(status: int) -> None:
+    if status != SSQ_OK:
+        msg = lib().ssq_last_error().decode("utf-8", "replace")
+        raise SunShapeKernelError(status, msg)
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None for None)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return DTYPE_CODE[dt]
+    except KeyError:
+        raise RuntimeError(f"unsupported dtype {dt}; expected float32, bfloat16 or float16") from None
+
+
+def heavy_mask_words(mask) -> tuple[int, int]:
+    """bool [nb] (tensor or sequence) -> two uint64 bit words."""
+    if mask is None:
+        return 0, 0
+    bits = [bool(x) for x in (mask.tolist() if hasattr(mask, "tolist") else mask)]
+    if len(bits) > 128:
+        raise RuntimeError("at most 128 blocks are supported")
+    w0 = sum(1 << i for i, x in enumerate(bits[:64]) if x)
+    w1 = sum(1 << i for i, x in enumerate(bits[64:]) if x)
+    return w0, w1

@@ -1,0 +1,83 @@
+// Shared device/host helpers for the sunshape_amd HIP kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sunshape_amd.h"
+
+#define SSQ_WAVE 64
+
+// ---------------------------------------------------------------------------
+// scalar conversions (bf16 / f16 stored as raw 16-bit words)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float ssq_bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// round-to-nearest-even, as torch's float -> bfloat16 conversion (finite inputs)
+__device__ __forceinline__ uint32_t ssq_f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+__device__ __forceinline__ float ssq_f16_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+__device__ __forceinline__ uint32_t ssq_f32_to_f16(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// load element i of a tensor of dtype `dt` as fp32
+__device__ __forceinline__ float ssq_load_elem(const void* p, int dt, int64_t i) {
+    if (dt == SSQ_F32) return reinterpret_cast<const float*>(p)[i];
+    uint32_t h = reinterpret_cast<const uint16_t*>(p)[i];
+    return dt == SSQ_BF16 ? ssq_bf16_to_f32(h) : ssq_f16_to_f32(h);
+}
+
+// round an fp32 value to dtype `dt` and return it as fp32 (query scaling semantics)
+__device__ __forceinline__ float ssq_round_to(float x, int dt) {
+    if (dt == SSQ_BF16) return ssq_bf16_to_f32(ssq_f32_to_bf16(x));
+    if (dt == SSQ_F16) return ssq_f16_to_f32(ssq_f32_to_f16(x));
+    return x;
+}
+
+__device__ __forceinline__ void ssq_store_elem(void* p, int dt, int64_t i, float x) {
+    if (dt == SSQ_F32) {
+        reinterpret_cast<float*>(p)[i] = x;
+    } else {
+        uint32_t h = dt == SSQ_BF16 ? ssq_f32_to_bf16(x) : ssq_f32_to_f16(x);
+        reinterpret_cast<uint16_t*>(p)[i] = (uint16_t)h;
+    }
+}
+
+__device__ __forceinline__ bool ssq_is_heavy(const uint64_t hm0, const uint64_t hm1, int blk) {
+    return blk < 64 ? ((hm0 >> blk) & 1ull) : ((hm1 >> (blk - 64)) & 1ull);
+}
+
+// wave64 reductions through ds_swizzle/bpermute (__shfl_xor)
+__device__ __forceinline__ float ssq_wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, SSQ_WAVE));
+    return v;
+}
+__device__ __forceinline__ float ssq_wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, SSQ_WAVE);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// host-side error plumbing
+// ---------------------------------------------------------------------------
+int ssq_fail(int code, const char* fmt, ...);
+int ssq_check_hip(hipError_t e, const char* what);
+
+#define SSQ_REQUIRE(cond, ...)                                  \
+    do {                                                        \
+        if (!(cond)) return ssq_fail(SSQ_ERR_INVALID, __VA_ARGS__); \
+    } while (0)
+#define SSQ_UNSUPPORTED(cond, ...)                                  \
+    do {                                                            \
+        if (!(cond)) return ssq_fail(SSQ_ERR_UNSUPPORTED, __VA_ARGS__); \
+    } while (0)

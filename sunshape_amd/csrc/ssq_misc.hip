@@ -1,0 +1,113 @@
+// Error plumbing, LUT build (test hook / standalone op) and dequantize.
+#include "ssq_common.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace {
+thread_local char g_err[512] = "";
+}
+
+int ssq_fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ssq_check_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return SSQ_OK;
+    return ssq_fail(SSQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+extern "C" const char* ssq_last_error(void) { return g_err; }
+extern "C" int ssq_abi_version(void) { return SSQ_ABI_VERSION; }
+
+namespace {
+
+// LUT[r, blk, c] = sum_d qp[r, blk*bd + d] * C[blk, c, d]  (fp32 FMA chain, dims ascending,
+// the same arithmetic as the decode kernel's in-LDS build)
+__global__ __launch_bounds__(256) void k_lut(const void* q, int q_dtype, int64_t q_sr, int head_dim,
+                                             const int64_t* perm, const float* cent, int bd, int nc,
+                                             int has_scale, float scale, float* lut) {
+    extern __shared__ float qp[];
+    const int r = blockIdx.y;
+    for (int j = threadIdx.x; j < head_dim; j += blockDim.x) {
+        float v = ssq_load_elem(q, q_dtype, (int64_t)r * q_sr + perm[j]);
+        if (has_scale) v = ssq_round_to(v * scale, q_dtype);
+        qp[j] = v;
+    }
+    __syncthreads();
+    const int nb = head_dim / bd;
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nb * nc) return;
+    const int blk = e / nc;
+    const float* c = cent + (int64_t)e * bd;
+    float acc = qp[blk * bd] * c[0];
+    for (int d = 1; d < bd; ++d) acc = fmaf(qp[blk * bd + d], c[d], acc);
+    lut[(int64_t)r * nb * nc + e] = acc;
+}
+
+// k_hat in the original basis: out[t, perm[i]] = k_perm[t, i]
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t* codes, int64_t c_st, int tokens,
+                                                 const int64_t* perm, const float* cent, int head_dim, int bd,
+                                                 int nc, uint64_t hm0, uint64_t hm1, int pt_dense,
+                                                 const void* pt, int pt_dtype, int64_t pt_st, float* out,
+                                                 int64_t o_st) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (int64_t)tokens * head_dim) return;
+    const int t = (int)(e / head_dim);
+    const int i = (int)(e - (int64_t)t * head_dim);
+    const int blk = i / bd, d = i - blk * bd;
+    float v;
+    if (ssq_is_heavy(hm0, hm1, blk)) {
+        int slot = blk;
+        if (!pt_dense)
+            slot = blk < 64 ? __popcll(hm0 & ((1ull << blk) - 1ull))
+                            : __popcll(hm0) + __popcll(hm1 & ((1ull << (blk - 64)) - 1ull));
+        v = ssq_load_elem(pt, pt_dtype, (int64_t)t * pt_st + slot * bd + d);
+    } else {
+        int c = codes[(int64_t)t * c_st + blk];
+        if (c >= nc) c = nc - 1;
+        v = cent[((int64_t)blk * nc + c) * bd + d];
+    }
+    out[(int64_t)t * o_st + perm[i]] = v;
+}
+
+}  // namespace
+
+extern "C" int ssq_lut_build(const void* q, int32_t q_dtype, int64_t q_sr, int32_t rows, int32_t head_dim,
+                             const int64_t* perm, const float* cent, int32_t block_dim, int32_t n_centroids,
+                             int32_t has_scale, float scale, float* lut, void* stream) {
+    SSQ_REQUIRE(q && perm && cent && lut, "NULL pointer argument");
+    SSQ_REQUIRE(rows >= 1 && rows <= 65535, "rows out of range");
+    SSQ_REQUIRE(block_dim >= 1 && head_dim % block_dim == 0 && head_dim <= 4096, "bad head_dim/block_dim");
+    SSQ_REQUIRE(n_centroids >= 1 && n_centroids <= 65536, "bad n_centroids");
+    SSQ_REQUIRE(q_dtype >= SSQ_F32 && q_dtype <= SSQ_F16, "bad q_dtype");
+    const int nb = head_dim / block_dim;
+    const int entries = nb * n_centroids;
+    dim3 grid((entries + 255) / 256, rows);
+    hipLaunchKernelGGL(k_lut, grid, dim3(256), head_dim * sizeof(float), (hipStream_t)stream, q, q_dtype, q_sr,
+                       head_dim, perm, cent, block_dim, n_centroids, has_scale, scale, lut);
+    return ssq_check_hip(hipGetLastError(), "k_lut launch");
+}
+
+extern "C" int ssq_dequantize(const uint8_t* codes, int64_t c_st, int32_t tokens, const int64_t* perm,
+                              const float* cent, int32_t head_dim, int32_t block_dim, int32_t n_centroids,
+                              const uint64_t* heavy_mask, int32_t pt_dense, const void* pt, int32_t pt_dtype,
+                              int64_t pt_st, float* out, int64_t o_st, void* stream) {
+    SSQ_REQUIRE(codes && perm && cent && out, "NULL pointer argument");
+    SSQ_REQUIRE(block_dim >= 1 && head_dim % block_dim == 0, "head_dim must be divisible by block_dim");
+    SSQ_REQUIRE(n_centroids >= 1 && n_centroids <= 256, "n_centroids must be in [1, 256]");
+    SSQ_REQUIRE(head_dim / block_dim <= 128, "n_blocks > 128");
+    SSQ_REQUIRE(tokens >= 0, "negative token count");
+    const uint64_t hm0 = heavy_mask ? heavy_mask[0] : 0, hm1 = heavy_mask ? heavy_mask[1] : 0;
+    SSQ_REQUIRE(!(hm0 || hm1) || pt, "Mixed-precision quantized keys are missing passthrough values.");
+    if (tokens == 0) return SSQ_OK;
+    const int64_t n = (int64_t)tokens * head_dim;
+    hipLaunchKernelGGL(k_dequant, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, codes, c_st,
+                       tokens, perm, cent, head_dim, block_dim, n_centroids, hm0, hm1, pt_dense, pt, pt_dtype, pt_st,
+                       out, o_st);
+    return ssq_check_hip(hipGetLastError(), "k_dequant launch");
+}

@@ -1,0 +1,354 @@
+"""Torch-tensor wrappers over the sunshape_amd C ABI.
+
+Every function takes device tensors, checks shapes/dtypes/strides on the host,
+launches on the tensors' current HIP stream and returns freshly allocated
+outputs (the caller's inputs are never written).  Codec arrays may be shared by
+all KV heads (the reference's per-layer codec: perm [D], centroids
+[nb, nc, bd]) or given per KV head (perm [Hkv, D], centroids [Hkv, nb, nc, bd]).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import torch
+
+from . import _native as N
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _on_gpu(name: str, t: torch.Tensor) -> None:
+    _require(t.is_cuda, f"{name} must be a HIP device tensor (got device {t.device}); this library has no CPU path")
+
+
+def _codec_arrays(perm: torch.Tensor, cent: torch.Tensor, head_dim: int, n_kv: Optional[int]):
+    """Validate codec arrays; return (perm, cent, perm_sh, cent_sh, bd, nb, nc)."""
+    _on_gpu("permutation", perm)
+    _on_gpu("centroids", cent)
+    _require(perm.dtype == torch.int64, "permutation must be int64")
+    _require(cent.dtype == torch.float32, "centroids must be float32")
+    perm = perm.contiguous()
+    cent = cent.contiguous()
+    if cent.ndim == 3:
+        nb, nc, bd = cent.shape
+        cent_sh = 0
+    elif cent.ndim == 4:
+        _, nb, nc, bd = cent.shape
+        _require(n_kv is None or cent.shape[0] == n_kv, f"centroids hold {cent.shape[0]} KV heads, expected {n_kv}")
+        cent_sh = nb * nc * bd
+    else:
+        raise RuntimeError(f"Expected codec.centroids.ndim == 3 (or 4 for per-KV-head codebooks), got {cent.ndim}.")
+    if perm.ndim == 1:
+        perm_sh = 0
+        _require(perm.shape[0] == head_dim, f"permutation length {perm.shape[0]} != head_dim {head_dim}")
+    else:
+        _require(perm.ndim == 2 and perm.shape[1] == head_dim, "permutation must be [D] or [Hkv, D]")
+        _require(n_kv is None or perm.shape[0] == n_kv, f"permutation holds {perm.shape[0]} KV heads, expected {n_kv}")
+        perm_sh = head_dim
+    _require(nb * bd == head_dim, f"centroids [{nb}, {nc}, {bd}] do not tile head_dim {head_dim}")
+    return perm, cent, perm_sh, cent_sh, bd, nb, nc
+
+
+def lut_build(q: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, scale: Optional[float] = None) -> torch.Tensor:
+    """LUT[r, b, c] = q_perm[r, b-block] . C[b, c]  (fp32 [R, nb, nc]).
+
+    Reference: sunshape/triton_kernels.py:381-408 (``_precompute_query_centroid_dots``).
+    """
+    _on_gpu("query", q)
+    _require(q.ndim == 2, f"Expected query.ndim == 2, got {q.ndim}.")
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    R, D = q.shape
+    perm, cent, _, _, bd, nb, nc = _codec_arrays(perm, cent, D, None)
+    _require(perm.ndim == 1 and cent.ndim == 3, "lut_build takes one codec (perm [D], centroids [nb, nc, bd])")
+    out = torch.empty((R, nb, nc), device=q.device, dtype=torch.float32)
+    if R == 0:
+        return out
+    rc = N.lib().ssq_lut_build(N.ptr(q), N.dtype_code(q.dtype), q.stride(0), R, D, N.ptr(perm), N.ptr(cent), bd, nc,
+                               1 if scale is not None else 0, float(scale or 0.0), N.ptr(out), N.stream_of(q.device))
+    N.check(rc)
+    return out
+
+
+def _pt_args(heavy: Optional[Sequence[bool]], pt: Optional[torch.Tensor], pt_dense: bool):
+    w0, w1 = N.heavy_mask_words(heavy)
+    if not (w0 or w1):
+        return (0, 0), None, 0, N.SSQ_F32
+    _require(pt is not None, "Mixed-precision quantized keys are missing passthrough values.")
+    _on_gpu("passthrough_values", pt)
+    _require(pt.stride(-1) == 1 and pt.stride(-2) == pt.shape[-1], "passthrough values must be contiguous per token")
+    return (w0, w1), pt, 1 if pt_dense else 0, N.dtype_code(pt.dtype)
+
+
+def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor,
+                     heavy: Optional[Sequence[bool]] = None, pt: Optional[torch.Tensor] = None,
+                     pt_dense: bool = True) -> torch.Tensor:
+    """scores[r, t] = q_r . k_hat_t in fp32 (q in the original basis, unscaled).
+
+    q [R, D]; codes uint8 [T, nb]; pt [T, nb, bd] (dense) or [T, n_heavy, bd].
+    Reference: sunshape/triton_kernels.py:570-609 and sunshape/codec.py:403-422.
+    """
+    _on_gpu("query", q)
+    _on_gpu("indices", codes)
+    _require(q.ndim == 2, f"Expected query.ndim == 2, got {q.ndim}.")
+    _require(codes.ndim == 2, f"Expected quantized_key.indices.ndim == 2, got {codes.ndim}.")
+    _require(codes.dtype == torch.uint8, f"indices must be uint8 codes (n_centroids <= 256), got {codes.dtype}")
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    codes = codes if codes.stride(-1) == 1 else codes.contiguous()
+    R, D = q.shape
+    T = codes.shape[0]
+    perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, None)
+    _require(perm.ndim == 1 and cent.ndim == 3, "attention_scores takes one codec (perm [D], centroids [nb, nc, bd])")
+    _require(codes.shape[1] == nb, "Quantized key block count does not match codec: "
+             f"indices.shape[1]={codes.shape[1]}, codec.n_blocks={nb}.")
+    out = torch.empty((R, T), device=q.device, dtype=torch.float32)
+    if R == 0 or T == 0:
+        return out
+    hm, pt, ptd, ptdt = _pt_args(heavy, pt, pt_dense)
+    a = N.DecodeArgs(
+        q=N.ptr(q), q_dtype=N.dtype_code(q.dtype), q_sb=0, q_sh=q.stride(0), q_sl=0,
+        batch=1, num_q_heads=R, q_len=1, head_dim=D, num_kv_heads=1, has_scale=0, scale=0.0,
+        perm=N.ptr(perm), perm_sh=0, cent=N.ptr(cent), cent_sh=0,
+        block_dim=bd, n_blocks=nb, n_centroids=nc,
+        pt_dense=ptd, pt_dtype=ptdt, pt=N.ptr(pt), pt_sb=0, pt_sh=0, pt_st=0 if pt is None else pt.stride(0),
+        layout=N.SSQ_CONTIGUOUS, seq_len=T, codes=N.ptr(codes), c_sb=0, c_sh=0, c_st=codes.stride(0),
+        scores=N.ptr(out), s_sb=0, s_sh=out.stride(0), s_sl=0,
+    )
+    a.heavy_mask[0], a.heavy_mask[1] = hm
+    N.check(N.lib().ssq_attention_scores(ctypes.byref(a), N.stream_of(q.device)))
+    return out
+
+
+def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
+               scale: Optional[float] = None, heavy: Optional[Sequence[bool]] = None,
+               pt: Optional[torch.Tensor] = None, pt_dense: bool = False) -> torch.Tensor:
+    """Raw scores for every (batch, query head) in one launch: fp32 [B, Hq, Lq, T].
+
+    q [B, Hq, Lq, D]; codes [B, Hkv, T, nb] uint8; query head h reads KV head
+    h // (Hq/Hkv).  With ``scale`` the query is scaled in its own dtype first
+    (sunshape/vllm_attn_backend.py:235-236) -- the logits the decode softmaxes.
+    """
+    for name, t in (("query", q), ("codes", codes)):
+        _on_gpu(name, t)
+    _require(q.ndim == 4 and codes.ndim == 4, "gqa_scores expects q [B, Hq, Lq, D] and codes [B, Hkv, T, nb]")
+    _require(codes.dtype == torch.uint8, "codes must be uint8")
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    codes = codes if codes.stride(-1) == 1 else codes.contiguous()
+    B, Hq, Lq, D = q.shape
+    Hkv, T = codes.shape[1], codes.shape[2]
+    _require(codes.shape[0] == B, "Quantized key batch size does not match query batch size.")
+    _require(Hq % Hkv == 0, "Query head count must be divisible by kv-head count.")
+    perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, Hkv)
+    _require(codes.shape[3] == nb, f"codes must be [.., {nb}]")
+    out = torch.empty((B, Hq, Lq, T), device=q.device, dtype=torch.float32)
+    if T == 0:
+        return out
+    hm, pt, ptd, ptdt = _pt_args(heavy, pt, pt_dense)
+    ps = (pt.stride(0), pt.stride(1), pt.stride(2)) if pt is not None else (0, 0, 0)
+    a = N.DecodeArgs(
+        q=N.ptr(q), q_dtype=N.dtype_code(q.dtype), q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
+        batch=B, num_q_heads=Hq, q_len=Lq, head_dim=D, num_kv_heads=Hkv,
+        has_scale=1 if scale is not None else 0, scale=float(scale or 0.0),
+        perm=N.ptr(perm), perm_sh=perm_sh, cent=N.ptr(cent), cent_sh=cent_sh,
+        block_dim=bd, n_blocks=nb, n_centroids=nc,
+        pt_dense=ptd, pt_dtype=ptdt, pt=N.ptr(pt), pt_sb=ps[0], pt_sh=ps[1], pt_st=ps[2],
+        layout=N.SSQ_CONTIGUOUS, seq_len=T, codes=N.ptr(codes), c_sb=codes.stride(0), c_sh=codes.stride(1),
+        c_st=codes.stride(2),
+        scores=N.ptr(out), s_sb=out.stride(0), s_sh=out.stride(1), s_sl=out.stride(2),
+    )
+    a.heavy_mask[0], a.heavy_mask[1] = hm
+    N.check(N.lib().ssq_attention_scores(ctypes.byref(a), N.stream_of(q.device)))
+    return out
+
+
+def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
+           scale: Optional[float] = None,
+           mask: Optional[torch.Tensor] = None,
+           heavy: Optional[Sequence[bool]] = None, pt: Optional[torch.Tensor] = None, pt_dense: bool = False,
+           block_table: Optional[torch.Tensor] = None, seq_lens: Optional[torch.Tensor] = None,
+           return_lse: bool = False, return_scores: bool = False,
+           num_splits: int = 0, kernel: int = 0):
+    """Fused VQ-key decode attention for all batches and KV heads in one launch.
+
+    q [B, Hq, Lq, D].  Contiguous layout: codes [B, Hkv, T, nb] uint8, v [B, Hkv, T, Dv],
+    pt [B, Hkv, T, slots, bd].  Paged layout (block_table given): codes [P, Hkv, page, nb],
+    v [P, Hkv, Dv, page] (vLLM's value layout), pt [P, Hkv, page, slots, bd],
+    block_table [B, max_pages] int32, seq_lens [B] int32.
+    mask: additive, broadcastable to [B, Hq, Lq, T] (converted to fp32).
+    Returns out [B, Hq, Lq, Dv] in v's dtype, plus lse [B, Hq, Lq] / raw scores [B, Hq, Lq, T]
+    (fp32) when requested.
+    Reference: sunshape/vllm_attn_backend.py:216-253.
+    """
+    for name, t in (("query", q), ("codes", codes), ("value", v)):
+        _on_gpu(name, t)
+    _require(q.ndim == 4, "Quantized attention expects query/value tensors with shape [batch, heads, seq, dim].")
+    _require(codes.dtype == torch.uint8, "codes must be uint8")
+    _require(q.stride(-1) == 1 and codes.stride(-1) == 1, "query and codes must be contiguous in the last dim")
+    B, Hq, Lq, D = q.shape
+    paged = block_table is not None
+    Hkv = codes.shape[1]
+    _require(Hq % Hkv == 0, "Query head count must be divisible by kv-head count.")
+    perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, Hkv)
+    _require(codes.ndim == 4 and codes.shape[-1] == nb, f"codes must be [.., {nb}] uint8")
+    if paged:
+        _on_gpu("block_table", block_table)
+        _require(seq_lens is not None, "paged decode needs seq_lens")
+        _on_gpu("seq_lens", seq_lens)
+        _require(block_table.dtype == torch.int32 and seq_lens.dtype == torch.int32, "block_table/seq_lens must be int32")
+        _require(block_table.ndim == 2 and block_table.shape[0] == B and block_table.stride(1) == 1, "block_table [B, max_pages]")
+        page = codes.shape[2]
+        _require(v.ndim == 4 and v.shape[0] == codes.shape[0] and v.shape[1] == Hkv and v.shape[3] == page,
+                 "paged V must be [P, Hkv, Dv, page]")
+        _require(v.stride(-1) == 1, "paged V pages must be contiguous over tokens")
+        Dv = v.shape[2]
+        T = block_table.shape[1] * page
+        layout = N.SSQ_PAGED
+        v_strides = (v.stride(0), v.stride(1), v.stride(2))
+    else:
+        _require(codes.shape[0] == B, "Quantized key batch size does not match query batch size.")
+        _require(v.ndim == 4 and v.shape[0] == B, "Quantized key batch size does not match value batch size.")
+        _require(v.shape[1] == Hkv, "Quantized key kv-head count does not match value kv-head count.")
+        _require(v.shape[2] == codes.shape[2], "Quantized key sequence length does not match value sequence length.")
+        _require(v.stride(-1) == 1, "value must be contiguous in the last dim")
+        T = codes.shape[2]
+        Dv = v.shape[3]
+        page = 0
+        layout = N.SSQ_CONTIGUOUS
+        v_strides = (v.stride(0), v.stride(1), v.stride(2))
+    out = torch.empty((B, Hq, Lq, Dv), device=q.device, dtype=v.dtype)
+    lse = torch.empty((B, Hq, Lq), device=q.device, dtype=torch.float32) if return_lse else None
+    scores = torch.empty((B, Hq, Lq, T), device=q.device, dtype=torch.float32) if return_scores else None
+    if mask is not None:
+        _on_gpu("attn_mask", mask)
+        mask = mask.to(torch.float32)
+        _require(mask.ndim == 4, "decode() takes a 4-D mask view broadcastable to [B, Hq, Lq, T]")
+        mask = mask.expand(B, Hq, Lq, T)
+    hm, pt, ptd, ptdt = _pt_args(heavy, pt, pt_dense)
+    if pt is not None:
+        pt_strides = (pt.stride(0), pt.stride(1), pt.stride(2))
+    else:
+        pt_strides = (0, 0, 0)
+    a = N.DecodeArgs(
+        q=N.ptr(q), q_dtype=N.dtype_code(q.dtype), q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
+        batch=B, num_q_heads=Hq, q_len=Lq, head_dim=D, num_kv_heads=Hkv,
+        has_scale=1 if scale is not None else 0, scale=float(scale or 0.0),
+        perm=N.ptr(perm), perm_sh=perm_sh, cent=N.ptr(cent), cent_sh=cent_sh,
+        block_dim=bd, n_blocks=nb, n_centroids=nc,
+        pt_dense=ptd, pt_dtype=ptdt, pt=N.ptr(pt), pt_sb=pt_strides[0], pt_sh=pt_strides[1], pt_st=pt_strides[2],
+        layout=layout, seq_len=T, codes=N.ptr(codes), c_sb=codes.stride(0), c_sh=codes.stride(1), c_st=codes.stride(2),
+        block_table=N.ptr(block_table), bt_sb=block_table.stride(0) if paged else 0,
+        seq_lens=N.ptr(seq_lens), page_size=page,
+        v=N.ptr(v), v_dtype=N.dtype_code(v.dtype), value_dim=Dv,
+        v_sb=v_strides[0], v_sh=v_strides[1], v_st=v_strides[2],
+        mask=N.ptr(mask),
+        m_sb=mask.stride(0) if mask is not None else 0, m_sh=mask.stride(1) if mask is not None else 0,
+        m_sl=mask.stride(2) if mask is not None else 0, m_st=mask.stride(3) if mask is not None else 0,
+        out=N.ptr(out), o_sb=out.stride(0), o_sh=out.stride(1), o_sl=out.stride(2),
+        lse=N.ptr(lse),
+        scores=N.ptr(scores), s_sb=scores.stride(0) if scores is not None else 0,
+        s_sh=scores.stride(1) if scores is not None else 0, s_sl=scores.stride(2) if scores is not None else 0,
+        num_splits=int(num_splits), kernel=int(kernel),
+    )
+    a.heavy_mask[0], a.heavy_mask[1] = hm
+    L = N.lib()
+    ws_bytes = L.ssq_decode_workspace_size(ctypes.byref(a))
+    ws = torch.empty((max(ws_bytes, 1),), device=q.device, dtype=torch.uint8) if ws_bytes else None
+    N.check(L.ssq_decode(ctypes.byref(a), N.ptr(ws), ws_bytes, N.stream_of(q.device)))
+    res = [out]
+    if return_lse:
+        res.append(lse)
+    if return_scores:
+        res.append(scores)
+    return res[0] if len(res) == 1 else tuple(res)
+
+
+def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
+           heavy: Optional[Sequence[bool]] = None, pt_dtype: Optional[torch.dtype] = None, pt_dense: bool = False,
+           codes_out: Optional[torch.Tensor] = None, pt_out: Optional[torch.Tensor] = None,
+           slot_mapping: Optional[torch.Tensor] = None, kernel: int = 0):
+    """Nearest-codeword encode of keys [B, Hkv, S, D] -> (codes uint8 [B, Hkv, S, nb], pt or None).
+
+    Passthrough values (heavy blocks) are [B, Hkv, S, n_heavy, bd] (compact) or
+    [B, Hkv, S, nb, bd] zero-filled (pt_dense, the reference's layout).  With
+    slot_mapping [B, S] (int64) the outputs go into caller-provided pages:
+    codes_out [P, Hkv, page, nb], pt_out [P, Hkv, page, slots, bd].
+    Reference: sunshape/codec.py:362-385, sunshape/vllm_attn_backend.py:101-123.
+    """
+    _on_gpu("key_states", keys)
+    _require(keys.ndim == 4, "quantize_key_states expects key_states with shape [batch, kv_heads, seq_len, head_dim].")
+    _require(keys.stride(-1) == 1, "keys must be contiguous in the last dim")
+    B, Hkv, S, D = keys.shape
+    perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, Hkv)
+    w0, w1 = N.heavy_mask_words(heavy)
+    n_heavy = bin(w0).count("1") + bin(w1).count("1")
+    pt_dtype = pt_dtype or keys.dtype
+    if slot_mapping is None:
+        codes = torch.empty((B, Hkv, S, nb), device=keys.device, dtype=torch.uint8)
+        pt = None
+        if n_heavy:
+            if pt_dense:
+                pt = torch.zeros((B, Hkv, S, nb, bd), device=keys.device, dtype=pt_dtype)
+            else:
+                pt = torch.empty((B, Hkv, S, n_heavy, bd), device=keys.device, dtype=pt_dtype)
+        c_str = (codes.stride(0), codes.stride(1), codes.stride(2))
+        p_str = (pt.stride(0), pt.stride(1), pt.stride(2)) if pt is not None else (0, 0, 0)
+        page = 0
+    else:
+        _on_gpu("slot_mapping", slot_mapping)
+        _require(slot_mapping.dtype == torch.int64 and slot_mapping.shape == (B, S) and slot_mapping.stride(1) == 1,
+                 "slot_mapping must be int64 [B, S]")
+        _require(codes_out is not None and codes_out.dtype == torch.uint8 and codes_out.ndim == 4
+                 and codes_out.shape[1] == Hkv and codes_out.shape[3] == nb and codes_out.stride(3) == 1,
+                 "paged encode needs codes_out [P, Hkv, page, nb] uint8")
+        codes = codes_out
+        page = codes_out.shape[2]
+        pt = pt_out
+        if n_heavy:
+            _require(pt is not None and pt.ndim == 5 and pt.shape[2] == page, "paged encode needs pt_out [P, Hkv, page, slots, bd]")
+            pt_dtype = pt.dtype
+        c_str = (codes.stride(0), codes.stride(1), codes.stride(2))
+        p_str = (pt.stride(0), pt.stride(1), pt.stride(2)) if pt is not None else (0, 0, 0)
+    a = N.EncodeArgs(
+        keys=N.ptr(keys), k_dtype=N.dtype_code(keys.dtype), k_sb=keys.stride(0), k_sh=keys.stride(1), k_ss=keys.stride(2),
+        batch=B, num_kv_heads=Hkv, seq_len=S, head_dim=D,
+        perm=N.ptr(perm), perm_sh=perm_sh, cent=N.ptr(cent), cent_sh=cent_sh,
+        block_dim=bd, n_blocks=nb, n_centroids=nc,
+        codes=N.ptr(codes), c_sb=c_str[0], c_sh=c_str[1], c_st=c_str[2],
+        pt=N.ptr(pt), pt_dtype=N.dtype_code(pt_dtype), pt_dense=1 if pt_dense else 0,
+        pt_sb=p_str[0], pt_sh=p_str[1], pt_st=p_str[2],
+        slot_mapping=N.ptr(slot_mapping), sm_sb=slot_mapping.stride(0) if slot_mapping is not None else 0,
+        page_size=page, kernel=int(kernel),
+    )
+    a.heavy_mask[0], a.heavy_mask[1] = w0, w1
+    N.check(N.lib().ssq_encode(ctypes.byref(a), N.stream_of(keys.device)))
+    return codes, pt
+
+
+def dequantize(codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
+               heavy: Optional[Sequence[bool]] = None, pt: Optional[torch.Tensor] = None,
+               pt_dense: bool = True) -> torch.Tensor:
+    """k_hat fp32 [T, D] in the original basis from codes uint8 [T, nb].
+
+    Reference: sunshape/codec.py:387-398.
+    """
+    _on_gpu("indices", codes)
+    _require(codes.ndim == 2 and codes.dtype == torch.uint8, "indices must be uint8 [T, nb]")
+    codes = codes if codes.stride(-1) == 1 else codes.contiguous()
+    _require(cent.ndim == 3 and perm.ndim == 1, "dequantize takes one codec (perm [D], centroids [nb, nc, bd])")
+    nb, nc, bd = cent.shape
+    D = nb * bd
+    perm, cent, _, _, bd, nb, nc = _codec_arrays(perm, cent, D, None)
+    _require(codes.shape[1] == nb, f"indices.shape[1]={codes.shape[1]} != n_blocks={nb}")
+    T = codes.shape[0]
+    out = torch.empty((T, D), device=codes.device, dtype=torch.float32)
+    (w0, w1), pt, ptd, ptdt = _pt_args(heavy, pt, pt_dense)
+    hm = (ctypes.c_uint64 * 2)(w0, w1)
+    N.check(N.lib().ssq_dequantize(N.ptr(codes), codes.stride(0), T, N.ptr(perm), N.ptr(cent), D, bd, nc,
+                                   ctypes.cast(hm, ctypes.c_void_p), ptd, N.ptr(pt), ptdt,
+                                   0 if pt is None else pt.stride(0), N.ptr(out), out.stride(0),
+                                   N.stream_of(codes.device)))
+    return out

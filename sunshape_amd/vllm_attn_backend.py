@@ -1,0 +1,391 @@
+"""SunShape attention backend shim (drop-in for ``sunshape.vllm_attn_backend``).
+
+Same surface as sunshape/vllm_attn_backend.py: mode toggles, handle/runtime
+registration globals, ``SunShapeQuantizedKeys``, ``quantize_key_states``,
+``SunShapeAttentionImpl.forward`` and the backend factory.  The quantized fast
+path is one fused HIP launch over every (batch, KV head) instead of the
+reference's Python loop (:230-252).
+
+Differences by design:
+* ``SunShapeQuantizedKeys`` may carry the batched code tensor it was built from
+  (``codes`` [B, Hkv, S, nb], ``passthrough`` [B, Hkv, S, slots, bd]); the
+  per-head tuple view ``quantized_heads`` is still provided.
+* A quantized payload that fails the fast-path gate raises
+  ``RuntimeError(reason)`` instead of being dequantized and re-routed
+  (sunshape/vllm_attn_backend.py:306-307); dense keys still go to the delegate
+  or SDPA exactly as in the reference (:307-345), after the codec round trip.
+"""
+
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+import torch.nn.functional as F
+
+from . import hip_ops
+from .codec import SunShapeQuantized
+from .integration.vllm import SunShapeVLLMConfig, SunShapeVLLMHandle, SunShapeVLLMRuntimeState, install_hooks
+
+MODE_ACTIVE = "active"
+MODE_CAPTURE = "capture"
+MODE_OFF = "off"
+
+_MODE = MODE_OFF
+_ACTIVE_HANDLE: SunShapeVLLMHandle | None = None
+_RUNTIME_STATE: SunShapeVLLMRuntimeState | None = None
+
+
+@dataclass(frozen=True)
+class SunShapeQuantizedKeys:
+    """Per-head quantized key cache payload (sunshape/vllm_attn_backend.py:38-53)."""
+
+    quantized_heads: tuple[Any, ...]
+    batch_size: int
+    num_kv_heads: int
+    seq_len: int
+    codes: torch.Tensor | None = None          # [B, Hkv, S, nb] uint8 backing store
+    passthrough: torch.Tensor | None = None    # [B, Hkv, S, slots, bd]
+    passthrough_dense: bool = False
+
+    def head(self, batch_idx: int, kv_head_idx: int) -> Any:
+        return self.quantized_heads[batch_idx * self.num_kv_heads + kv_head_idx]
+
+    def batched(self) -> tuple[torch.Tensor, torch.Tensor | None, bool]:
+        """(codes [B, Hkv, S, nb], passthrough or None, dense flag), stacking the heads if needed."""
+        if self.codes is not None:
+            return self.codes, self.passthrough, self.passthrough_dense
+        heads = self.quantized_heads
+        codes = torch.stack([h.indices for h in heads]).reshape(self.batch_size, self.num_kv_heads, self.seq_len, -1)
+        if codes.dtype != torch.uint8:
+            codes = codes.to(torch.uint8)
+        pt = None
+        if heads and getattr(heads[0], "passthrough_values", None) is not None:
+            pt = torch.stack([h.passthrough_values for h in heads])
+            pt = pt.reshape(self.batch_size, self.num_kv_heads, self.seq_len, *pt.shape[-2:])
+        return codes, pt, True
+
+
+def set_mode(mode: str):
+    global _MODE
+    _MODE = mode
+
+
+def get_mode() -> str:
+    return _MODE
+
+
+def register_handle(handle: SunShapeVLLMHandle) -> SunShapeVLLMHandle:
+    global _ACTIVE_HANDLE
+    _ACTIVE_HANDLE = handle
+    set_mode(MODE_ACTIVE)
+    return handle
+
+
+def register_runtime_state(state: SunShapeVLLMRuntimeState) -> SunShapeVLLMRuntimeState:
+    global _RUNTIME_STATE
+    _RUNTIME_STATE = state
+    set_mode(MODE_ACTIVE)
+    return state
+
+
+def clear_registered_handle() -> None:
+    global _ACTIVE_HANDLE
+    _ACTIVE_HANDLE = None
+    if _RUNTIME_STATE is None:
+        set_mode(MODE_OFF)
+
+
+def clear_registered_runtime() -> None:
+    global _RUNTIME_STATE
+    _RUNTIME_STATE = None
+    if _ACTIVE_HANDLE is None:
+        set_mode(MODE_OFF)
+
+
+def get_registered_handle() -> SunShapeVLLMHandle | None:
+    return _ACTIVE_HANDLE
+
+
+def get_registered_runtime() -> SunShapeVLLMRuntimeState | None:
+    return _RUNTIME_STATE
+
+
+def _codec_head_arrays(codec, num_kv_heads: int):
+    """(perm, centroids) for hip_ops: shared [D]/[nb,nc,bd] or per-KV-head [Hkv, ...]."""
+    perm = codec.effective_permutation() if hasattr(codec, "effective_permutation") else codec.permutation
+    cent = codec.centroids
+    if cent.ndim == 4 and cent.shape[0] != num_kv_heads:
+        raise RuntimeError(f"codec holds {cent.shape[0]} KV-head codebooks, keys have {num_kv_heads} KV heads")
+    return perm, cent
+
+
+def quantize_key_states(layer_idx: int, key_states: torch.Tensor) -> SunShapeQuantizedKeys:
+    """Encode [B, Hkv, S, D] keys in one HIP launch (sunshape/vllm_attn_backend.py:101-123)."""
+    runtime = get_registered_runtime()
+    if runtime is None:
+        raise RuntimeError("SunShape runtime state is not registered.")
+    codec = runtime.codec_for_layer(int(layer_idx))
+    if codec is None:
+        raise RuntimeError(f"No SunShape codec is registered for layer {layer_idx}.")
+    if key_states.ndim != 4:
+        raise RuntimeError(
+            "quantize_key_states expects key_states with shape [batch, kv_heads, seq_len, head_dim]."
+        )
+    reason = codec.unsupported_reason()
+    if reason is not None:
+        raise RuntimeError(reason)
+    batch_size, num_kv_heads, seq_len, _ = key_states.shape
+    perm, cent = _codec_head_arrays(codec, num_kv_heads)
+    heavy = codec.heavy_blocks()
+    keys = key_states.to(codec.device)
+    if keys.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        keys = keys.float()
+    codes, pt = hip_ops.encode(keys, perm, cent, heavy=heavy, pt_dtype=torch.float32, pt_dense=True)
+    mixed = codec.mode == "profileperm_mixed_precision"
+    pblocks = codec.mixed_high_precision_blocks.detach().clone() if mixed else None
+    heads = []
+    for b in range(batch_size):
+        for h in range(num_kv_heads):
+            heads.append(SunShapeQuantized(
+                indices=codes[b, h],
+                head_dim=codec.head_dim,
+                block_dim=codec.block_dim,
+                n_blocks=codec.n_blocks,
+                passthrough_blocks=pblocks,
+                passthrough_values=None if pt is None else pt[b, h],
+            ))
+    return SunShapeQuantizedKeys(
+        quantized_heads=tuple(heads),
+        batch_size=int(batch_size),
+        num_kv_heads=int(num_kv_heads),
+        seq_len=int(seq_len),
+        codes=codes,
+        passthrough=pt,
+        passthrough_dense=True,
+    )
+
+
+def _decode_keys_if_needed(layer_idx: int | None, key_states: torch.Tensor) -> torch.Tensor:
+    """Dense keys through the codec round trip (sunshape/vllm_attn_backend.py:126-137)."""
+    runtime = get_registered_runtime()
+    if runtime is None or layer_idx is None:
+        return key_states
+    codec = runtime.codec_for_layer(int(layer_idx))
+    if codec is None or key_states.ndim < 2:
+        return key_states
+    orig_shape = key_states.shape
+    orig_dtype = key_states.dtype
+    if codec.num_kv_heads is not None and key_states.ndim == 4:
+        heads = [codec(key_states[:, h].reshape(-1, orig_shape[-1]).float(), kv_head=h).reshape(orig_shape[0], 1, orig_shape[2], orig_shape[3])
+                 for h in range(orig_shape[1])]
+        return torch.cat(heads, dim=1).to(orig_dtype)
+    flat = key_states.reshape(-1, orig_shape[-1])
+    decoded = codec(flat.float())
+    return decoded.to(orig_dtype).reshape(orig_shape)
+
+
+def _quantized_fast_path_unavailable_reason(
+    *,
+    runtime_state: SunShapeVLLMRuntimeState | None,
+    layer_idx: int | None,
+    query: torch.Tensor,
+    key: Any,
+    value: torch.Tensor,
+    attn_mask: torch.Tensor | None,
+    is_causal: bool,
+) -> str | None:
+    """Same checks and messages as sunshape/vllm_attn_backend.py:159-194."""
+    if runtime_state is None or layer_idx is None:
+        return "No registered runtime state for quantized attention."
+    if not isinstance(key, SunShapeQuantizedKeys):
+        return "Key payload is not SunShapeQuantizedKeys."
+    codec = runtime_state.codec_for_layer(int(layer_idx))
+    if codec is None:
+        return f"No codec for layer {layer_idx}."
+    if query.ndim != 4 or value.ndim != 4:
+        return "Quantized attention expects query/value tensors with shape [batch, heads, seq, dim]."
+    if key.batch_size != int(query.shape[0]):
+        return "Quantized key batch size does not match query batch size."
+    if key.batch_size != int(value.shape[0]):
+        return "Quantized key batch size does not match value batch size."
+    if key.num_kv_heads != int(value.shape[1]):
+        return "Quantized key kv-head count does not match value kv-head count."
+    if key.seq_len != int(value.shape[2]):
+        return "Quantized key sequence length does not match value sequence length."
+    if int(query.shape[-1]) != int(codec.head_dim):
+        return "Query head_dim does not match codec head_dim."
+    if int(query.shape[1]) % int(key.num_kv_heads) != 0:
+        return "Query head count must be divisible by kv-head count."
+    if is_causal and int(query.shape[2]) != 1:
+        return "Causal quantized fast path currently targets decode (query_len == 1)."
+    if attn_mask is not None and attn_mask.ndim not in {2, 3, 4}:
+        return "Unsupported attention-mask rank for quantized fast path."
+    reason = codec.unsupported_reason() if hasattr(codec, "unsupported_reason") else None
+    if reason is not None:
+        return reason
+    return None
+
+
+def _mask_view(attn_mask: torch.Tensor | None, batch: int, hq: int, lq: int, seq: int) -> torch.Tensor | None:
+    """4-D view of the mask with the reference's per-(batch, head) slicing (vllm_attn_backend.py:197-213)."""
+    if attn_mask is None:
+        return None
+    m = attn_mask
+    if m.ndim == 2:                       # [Lq, S] for every batch and head
+        return m[None, None]
+    if m.ndim == 3:
+        if m.shape[0] == batch:           # [B, Lq, S]: same for every head of a batch
+            return m[:, None]
+        return m[None]                    # [Hq, Lq, S]: same for every batch
+    return m
+
+
+def _apply_quantized_attention(
+    *,
+    codec,
+    query: torch.Tensor,
+    key: SunShapeQuantizedKeys,
+    value: torch.Tensor,
+    attn_mask: torch.Tensor | None,
+    scale: float | None,
+) -> torch.Tensor:
+    """One fused HIP launch for sunshape/vllm_attn_backend.py:216-253."""
+    batch_size, num_query_heads, query_len, _ = query.shape
+    _, num_kv_heads, seq_len, _ = value.shape
+    codes, pt, dense = key.batched()
+    perm, cent = _codec_head_arrays(codec, num_kv_heads)
+    heavy = codec.heavy_blocks() if hasattr(codec, "heavy_blocks") else None
+    mask = _mask_view(attn_mask, batch_size, num_query_heads, query_len, seq_len)
+    q = query if query.stride(-1) == 1 else query.contiguous()
+    v = value if value.stride(-1) == 1 else value.contiguous()
+    return hip_ops.decode(q, codes, v, perm, cent, scale=scale, mask=mask, heavy=heavy, pt=pt, pt_dense=dense)
+
+
+class SunShapeAttentionImpl:
+    """Attention shim for vLLM integration (sunshape/vllm_attn_backend.py:256-347)."""
+
+    def __init__(self, *, delegate: Any = None, layer_idx: int | None = None, runtime_state: SunShapeVLLMRuntimeState | None = None):
+        self.delegate = delegate
+        self.layer_idx = layer_idx
+        self.runtime_state = runtime_state or get_registered_runtime()
+
+    def forward(
+        self,
+        query: torch.Tensor,
+        key: Any,
+        value: torch.Tensor,
+        *,
+        attn_mask: torch.Tensor | None = None,
+        is_causal: bool = False,
+        scale: float | None = None,
+        layer_idx: int | None = None,
+        **kwargs: Any,
+    ) -> torch.Tensor:
+        layer = self.layer_idx if layer_idx is None else layer_idx
+        runtime_state = self.runtime_state or get_registered_runtime()
+        reason = _quantized_fast_path_unavailable_reason(
+            runtime_state=runtime_state,
+            layer_idx=layer,
+            query=query,
+            key=key,
+            value=value,
+            attn_mask=attn_mask,
+            is_causal=is_causal,
+        )
+        if reason is None:
+            codec = runtime_state.codec_for_layer(int(layer)) if runtime_state is not None else None
+            if codec is None:
+                raise RuntimeError(f"No codec is registered for layer {layer}.")
+            return _apply_quantized_attention(
+                codec=codec, query=query, key=key, value=value, attn_mask=attn_mask, scale=scale,
+            )
+        if isinstance(key, SunShapeQuantizedKeys):
+            raise RuntimeError(reason)
+        key = _decode_keys_if_needed(layer, key)
+        delegate = self.delegate
+        if delegate is not None:
+            if hasattr(delegate, "forward"):
+                return delegate.forward(query, key, value, attn_mask=attn_mask, is_causal=is_causal,
+                                        scale=scale, layer_idx=layer, **kwargs)
+            if callable(delegate):
+                return delegate(query, key, value, attn_mask=attn_mask, is_causal=is_causal,
+                                scale=scale, layer_idx=layer, **kwargs)
+        if query.ndim != 4 or key.ndim != 4 or value.ndim != 4:
+            raise RuntimeError(
+                "SunShapeAttentionImpl fallback expects 4D [batch, heads, seq, dim] tensors "
+                "when no delegate backend is provided."
+            )
+        if scale is not None:
+            query = query * float(scale)
+        return F.scaled_dot_product_attention(query, key, value, attn_mask=attn_mask, is_causal=is_causal)
+
+    __call__ = forward
+
+
+class SunShapeAttentionBackend:
+    """Backend/factory surface (sunshape/vllm_attn_backend.py:350-366)."""
+
+    backend_name = "sunshape"
+
+    def __init__(self, *, delegate_backend: Any = None):
+        self.delegate_backend = delegate_backend
+
+    def make_impl(self, *, layer_idx: int | None = None, delegate: Any = None) -> SunShapeAttentionImpl:
+        return SunShapeAttentionImpl(
+            delegate=delegate if delegate is not None else self.delegate_backend,
+            layer_idx=layer_idx,
+            runtime_state=get_registered_runtime(),
+        )
+
+    def describe(self) -> dict[str, Any]:
+        return describe_backend()
+
+
+def get_backend_factory(*, delegate_backend: Any = None) -> SunShapeAttentionBackend:
+    return SunShapeAttentionBackend(delegate_backend=delegate_backend)
+
+
+def ensure_backend_registered() -> dict[str, Any]:
+    runtime = get_registered_runtime()
+    handle = get_registered_handle()
+    return {
+        "backend": "sunshape",
+        "mode": get_mode(),
+        "registered": handle is not None,
+        "runtime_loaded": runtime is not None,
+        "install_entrypoint": "sunshape_amd.vllm_attn_backend:install_sunshape_hooks",
+        "env_backend": os.environ.get("VLLM_ATTENTION_BACKEND"),
+    }
+
+
+def describe_backend() -> dict[str, Any]:
+    handle = get_registered_handle()
+    if handle is None:
+        return {"mode": get_mode(), "registered": False, "config": None, "runtime": None}
+    return {
+        "mode": get_mode(),
+        "registered": True,
+        "config": handle.config.to_dict(),
+        "hooks_installed": handle.hooks_installed,
+        "connector_registered": handle.connector_registered,
+        "runtime_patch_available": handle.runtime_patch_available,
+        "notes": list(handle.notes),
+        "runtime": _RUNTIME_STATE.to_dict() if _RUNTIME_STATE is not None else None,
+    }
+
+
+def install_sunshape_hooks(*args, **kwargs) -> SunShapeVLLMHandle:
+    return register_handle(install_hooks(*args, **kwargs))
+
+
+__all__ = [
+    "MODE_ACTIVE", "MODE_CAPTURE", "MODE_OFF",
+    "SunShapeVLLMConfig", "SunShapeVLLMHandle", "SunShapeVLLMRuntimeState",
+    "SunShapeAttentionBackend", "SunShapeAttentionImpl", "SunShapeQuantizedKeys",
+    "clear_registered_handle", "clear_registered_runtime", "describe_backend", "ensure_backend_registered",
+    "get_mode", "get_registered_handle", "get_registered_runtime", "get_backend_factory",
+    "install_sunshape_hooks", "quantize_key_states", "register_handle", "register_runtime_state", "set_mode",
+]

@@ -1,0 +1,105 @@
+"""Drop-in surfaces on the GPU: codec quantize/dequantize/forward/attention_scores,
+quantize_key_states + SunShapeAttentionImpl.forward, bundle round trip, per-KV-head codecs."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _util import BF16_TOL, SCORE_TOL, assert_rel, log, np_of
+from oracle import vq_oracle as O
+from sunshape_amd import synthetic
+from sunshape_amd import vllm_attn_backend as VB
+from sunshape_amd.codec import SunShapeBlockCodec
+from sunshape_amd.hf import SunShapeBundle
+from sunshape_amd.integration.vllm import load_runtime_state
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _mixed_codec(seed=31, D=64, bd=2):
+    cb = synthetic.make_codebook(1, D, bd, seed, shared_sigma=True)
+    heavy = synthetic.heavy_blocks_by_sigma(cb.sigma[0], cb.perm[0], bd, 4)
+    cent = cb.centroids[0].clone()
+    cent[heavy] = 0
+    codec = SunShapeBlockCodec.from_buffers(cb.perm[0], cent, mode="profileperm_mixed_precision",
+                                            mixed_high_precision_blocks=heavy, device=DEV)
+    return codec, cb.sigma[0]
+
+
+def test_codec_quantize_dequantize_forward_mixed():
+    log("codec mixed quantize/dequantize")
+    codec, sigma = _mixed_codec()
+    keys = (torch.randn(2000, 64) * sigma).to(torch.bfloat16)
+    qz = codec.quantize(keys.to(DEV))
+    assert qz.indices.dtype == torch.uint8 and qz.indices.shape == (2000, 32)
+    assert qz.passthrough_values.shape == (2000, 32, 2) and qz.passthrough_values.dtype == torch.float32
+    heavy = codec.mixed_high_precision_blocks.cpu().numpy()
+    rc, rpt = O.encode(keys.float().numpy(), codec.permutation.cpu().numpy(), codec.centroids.cpu().numpy(), heavy)
+    assert np.array_equal(np_of(qz.indices), rc)
+    assert np.array_equal(np_of(qz.passthrough_values), rpt)
+    k_hat = np_of(codec.dequantize(qz))
+    ref = O.dequantize(rc, codec.centroids.cpu().numpy(), codec.permutation.cpu().numpy(), heavy, rpt)
+    assert np.array_equal(k_hat, ref)
+    assert np.array_equal(np_of(codec(keys.to(DEV))), ref)
+    q = torch.randn(5, 64, device=DEV)
+    s = np_of(codec.attention_scores(q, qz))
+    assert_rel(s, np_of(q).astype(np.float64) @ ref.astype(np.float64).T, SCORE_TOL, "mixed scores")
+
+
+def test_codec_identity_mode_ignores_permutation_buffer():
+    log("codec identity mode")
+    cb = synthetic.make_codebook(1, 64, 8, 5)
+    codec = SunShapeBlockCodec.from_buffers(cb.perm[0], cb.centroids[0], mode="identity_baseline", device=DEV)
+    keys = torch.randn(300, 64)
+    rc, _ = O.encode(keys.numpy(), np.arange(64), cb.centroids[0].numpy())
+    assert np.array_equal(np_of(codec.quantize(keys.to(DEV)).indices), rc)
+
+
+def test_quantize_key_states_and_impl_forward_per_kv_head_codec():
+    log("backend per-kv-head end to end")
+    B, Hq, Hkv, S, D, bd = 2, 8, 2, 900, 128, 4
+    cb = synthetic.make_codebook(Hkv, D, bd, 41)
+    codec = SunShapeBlockCodec.from_buffers(cb.perm, cb.centroids, device=DEV)
+    bundle = SunShapeBundle("m", [0], 2.0, bd, "profileperm_baseline", 0, 0, 0, {0: codec})
+    from sunshape_amd.integration.vllm import SunShapeVLLMRuntimeState
+
+    rs = SunShapeVLLMRuntimeState("p", "m", "sunshape_base", 2.0, bd, [0], bundle, "cuda")
+    VB.register_runtime_state(rs)
+    try:
+        g = torch.Generator().manual_seed(42)
+        keys = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+        qk = VB.quantize_key_states(0, keys.to(DEV))
+        assert qk.batch_size == B and qk.num_kv_heads == Hkv and qk.seq_len == S
+        codes = np_of(qk.codes)
+        for b in range(B):
+            for h in range(Hkv):
+                rc, _ = O.encode(keys[b, h].float().numpy(), cb.perm[h].numpy(), cb.centroids[h].numpy())
+                assert np.array_equal(codes[b, h], rc)
+                assert torch.equal(qk.head(b, h).indices, qk.codes[b, h])
+        q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16).to(DEV)
+        v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16).to(DEV)
+        impl = VB.get_backend_factory().make_impl(layer_idx=0)
+        out = np_of(impl(q, qk, v, scale=1 / math.sqrt(D), is_causal=True))
+        ref = O.decode_attention(np_of(q), codes, np_of(v), cb.centroids.numpy(), cb.perm.numpy(), 1 / math.sqrt(D),
+                                 "bf16", "bf16")
+        assert_rel(out, ref, BF16_TOL, "impl.forward")
+        # payload rebuilt from the per-head tuple only (no batched backing store)
+        qk2 = VB.SunShapeQuantizedKeys(quantized_heads=qk.quantized_heads, batch_size=B, num_kv_heads=Hkv, seq_len=S)
+        assert np.array_equal(np_of(impl(q, qk2, v, scale=1 / math.sqrt(D))), out)
+    finally:
+        VB.clear_registered_runtime()
+
+
+def test_bundle_roundtrip_on_gpu_and_runtime_state(tmp_path):
+    log("bundle round trip")
+    codec, _ = _mixed_codec(seed=51)
+    b = SunShapeBundle("m", [2], 4.0, 2, "profileperm_mixed_precision", 0, 0, 0, {2: codec})
+    path = b.save(tmp_path / "b.pt")
+    rs = load_runtime_state(bundle_path=path, model_name="m", mode="sunshape_mixed", bits_per_dim=4.0, block_dim=2,
+                            layers=[2], device="cuda")
+    c2 = rs.codec_for_layer(2)
+    keys = torch.randn(100, 64, device=DEV)
+    assert torch.equal(c2.quantize(keys).indices, codec.quantize(keys).indices)

@@ -1,0 +1,131 @@
+"""HIP encode vs the oracle, bit-for-bit: golden fixture, block sizes, both kernels,
+constructed ties, torch.cdist on this host's CPU, paged slot mapping, config 5."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from _util import bf16_from_bits, log, np_of, torch_bf16_from_bits
+from oracle import vq_oracle as O
+from sunshape_amd import hip_ops, synthetic
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _gpu_encode(keys_np, perm, cent, heavy=None, kernel=0, dtype=torch.float32, pt_dense=True):
+    keys = torch.from_numpy(keys_np).to(DEV).to(dtype)
+    codes, pt = hip_ops.encode(keys[None, None], torch.from_numpy(perm).to(DEV), torch.from_numpy(cent).to(DEV),
+                               heavy=None if heavy is None else list(heavy), pt_dtype=torch.float32,
+                               pt_dense=pt_dense, kernel=kernel)
+    return np_of(codes[0, 0]), None if pt is None else np_of(pt[0, 0])
+
+
+@pytest.mark.parametrize("kernel", [1, 2])
+def test_encode_golden_fixture_bit_exact(kernel):
+    log(f"encode golden kernel={kernel}")
+    f = np.load(os.path.join(GOLD, "encode_mixed.npz"))
+    keys = torch_bf16_from_bits(f["keys_bf16_bits"], DEV)
+    codes, pt = hip_ops.encode(keys[None, None], torch.from_numpy(f["perm"]).to(DEV),
+                               torch.from_numpy(f["centroids"]).to(DEV), heavy=f["heavy"].tolist(),
+                               pt_dtype=torch.float32, pt_dense=True, kernel=kernel)
+    assert np.array_equal(np_of(codes[0, 0]), f["codes"])
+    assert np.array_equal(np_of(pt[0, 0]), f["passthrough"])
+
+
+@pytest.mark.parametrize("D,bd", [(64, 1), (64, 2), (48, 3), (128, 4), (64, 8), (128, 8), (64, 16)])
+def test_encode_kernels_vs_oracle_bit_exact(D, bd):
+    log(f"encode D={D} bd={bd}")
+    rng = np.random.default_rng(D * 31 + bd)
+    n = 3000
+    perm = rng.permutation(D)
+    sig = np.exp(rng.uniform(np.log(0.1), np.log(3), D)).astype(np.float32)
+    cent = (rng.standard_normal((D // bd, 256, bd)) * sig[perm].reshape(D // bd, 1, bd)).astype(np.float32)
+    keys = O.bf16_round((rng.standard_normal((n, D)) * sig).astype(np.float32))
+    ref, _ = O.encode(keys, perm, cent)
+    got_scan, _ = _gpu_encode(keys, perm, cent, kernel=1, dtype=torch.bfloat16)
+    assert np.array_equal(got_scan, ref), int((got_scan != ref).sum())
+    if bd <= 10:
+        got_mfma, _ = _gpu_encode(keys, perm, cent, kernel=2, dtype=torch.bfloat16)
+        assert np.array_equal(got_mfma, ref), int((got_mfma != ref).sum())
+
+
+def test_encode_constructed_ties_and_exact_rows():
+    log("encode constructed ties")
+    rng = np.random.default_rng(7)
+    D, bd = 32, 2
+    perm = rng.permutation(D)
+    cent = rng.standard_normal((16, 256, bd)).astype(np.float32)
+    cent[:, 200] = cent[:, 17]                                    # duplicates: lower index wins
+    cent[:, 201] = np.nextafter(cent[:, 40], np.float32(np.inf))  # one-ulp neighbours
+    cent[:, 9] = cent[:, 8] * np.float32(1 + 2 ** -22)
+    pick = rng.choice([17, 40, 201, 8, 9, 3], size=(400, 16))
+    xp = np.stack([np.concatenate([cent[b, pick[i, b]] for b in range(16)]) for i in range(400)])
+    xp[200:] += rng.standard_normal(xp[200:].shape).astype(np.float32) * 1e-3
+    keys = O.inverse_transform(xp, perm).astype(np.float32)
+    ref, _ = O.encode(keys, perm, cent)
+    assert not (ref == 200).any()
+    for kernel in (1, 2):
+        got, _ = _gpu_encode(keys, perm, cent, kernel=kernel)
+        assert np.array_equal(got, ref), (kernel, int((got != ref).sum()))
+
+
+def test_encode_vs_torch_cdist_on_this_host():
+    """torch.cdist on this host's CPU differs only on sqrt-rounding ties (counted)."""
+    log("encode vs torch.cdist")
+    rng = np.random.default_rng(8)
+    bd, n = 2, 50000
+    x = O.bf16_round(rng.standard_normal((n, bd)).astype(np.float32))
+    c = rng.standard_normal((256, bd)).astype(np.float32)
+    got, _ = _gpu_encode(x, np.arange(bd), c[None])
+    ref = torch.cdist(torch.from_numpy(x), torch.from_numpy(c)).argmin(-1).numpy()
+    bad = np.nonzero(got[:, 0] != ref)[0]
+    e2, _ = O.block_distances(x, c)
+    for i in bad:
+        a, b = e2[i, got[i, 0]], e2[i, ref[i]]
+        assert abs(a - b) <= 4 * np.spacing(np.float32(max(min(abs(a), abs(b)), 1e-30))), (i, a, b)
+    print(f"[info] rows differing from this host's torch.cdist (sqrt ties): {len(bad)} of {n}")
+
+
+def test_encode_paged_slot_mapping_matches_contiguous():
+    log("encode paged slot mapping")
+    p = synthetic.config5(DEV, B=2, S=96)
+    heavy = p["heavy"].tolist()
+    codes, pt = hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy)
+    page, Hkv, nb = 16, 2, 32
+    P = 2 * 96 // page + 3
+    g = torch.Generator().manual_seed(3)
+    table = torch.randperm(P, generator=g)[: 2 * 96 // page].view(2, -1)
+    slots = (table[:, :, None] * page + torch.arange(page)).reshape(2, 96).to(torch.int64).to(DEV)
+    cpages = torch.zeros(P, Hkv, page, nb, dtype=torch.uint8, device=DEV)
+    ppages = torch.zeros(P, Hkv, page, 4, 2, dtype=torch.bfloat16, device=DEV)
+    hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy, codes_out=cpages, pt_out=ppages,
+                   slot_mapping=slots)
+    t = table.to(DEV)
+    for b in range(2):
+        got_c = cpages[t[b]].permute(1, 0, 2, 3).reshape(Hkv, 96, nb)
+        got_p = ppages[t[b]].permute(1, 0, 2, 3, 4).reshape(Hkv, 96, 4, 2)
+        assert torch.equal(got_c, codes[b]) and torch.equal(got_p, pt[b])
+
+
+def test_config5_full_encode():
+    """Full config 5 (16 x 2 x 16384 keys): MFMA == exact scan on every row; oracle on a row sample."""
+    log("config5 full encode")
+    p = synthetic.config5(DEV)
+    heavy = p["heavy"].tolist()
+    c_mfma, pt = hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy, kernel=2)
+    c_scan, pt2 = hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy, kernel=1)
+    assert torch.equal(c_mfma, c_scan) and torch.equal(pt, pt2)
+    hv = p["heavy"].numpy()
+    keys = np_of(p["keys"])
+    perm, cent = np_of(p["perm"]), np_of(p["centroids"])
+    rng = np.random.default_rng(1)
+    got = np_of(c_mfma)
+    for b, kv in ((0, 0), (7, 1), (15, 1)):
+        rows = rng.choice(16384, 3000, replace=False)
+        ref, rpt = O.encode(keys[b, kv, rows], perm, cent[kv], hv)
+        assert np.array_equal(got[b, kv, rows], ref)
+        assert np.array_equal(np_of(pt[b, kv, rows]), rpt[:, hv])

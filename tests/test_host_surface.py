@@ -1,0 +1,211 @@
+"""Host-side behaviour of the drop-in Python surface (no GPU needed).
+
+Gate strings follow sunshape/triton_kernels.py:327-363 and
+sunshape/vllm_attn_backend.py:159-194; everything that would reach a kernel
+with CPU tensors must raise instead (no CPU path exists)."""
+
+import math
+
+import pytest
+import torch
+
+from sunshape_amd import hip_ops
+from sunshape_amd.codec import SunShapeBlockCodec, SunShapeQuantized, _invert_permutation
+from sunshape_amd.hf import SunShapeBundle, default_block_dim, resolve_mode_alias
+from sunshape_amd.integration.vllm import SunShapeVLLMRuntimeState
+from sunshape_amd.kernels import _triton_fast_path_unavailable_reason, require_triton_fast_path
+from sunshape_amd import synthetic
+from sunshape_amd import vllm_attn_backend as VB
+
+
+def _codec(nkv=None, mode="profileperm_baseline"):
+    g = torch.Generator().manual_seed(0)
+    D, bd = 64, 8
+    shape = (() if nkv is None else (nkv,)) + (D // bd, 256, bd)
+    cent = torch.randn(*shape, generator=g)
+    perm = torch.randperm(D, generator=g) if nkv is None else torch.stack([torch.randperm(D, generator=g) for _ in range(nkv)])
+    return SunShapeBlockCodec.from_buffers(perm, cent, mode=mode, device="cpu")
+
+
+def test_codec_buffers_match_reference_layout():
+    c = SunShapeBlockCodec(head_dim=64, block_dim=8, device="cpu")
+    sd = c.state_dict()
+    assert set(sd) == {"E", "E_inv", "centroids", "dsq_block_affinity", "dsq_active_blocks",
+                       "mixed_high_precision_blocks", "mixed_block_mass", "permutation", "inv_permutation", "rotation"}
+    assert sd["centroids"].shape == (8, 256, 8)
+    assert sd["permutation"].dtype == torch.long
+    with pytest.raises(ValueError):
+        SunShapeBlockCodec(head_dim=64, block_dim=7, device="cpu")
+
+
+def test_per_kv_head_codec_and_inverse_permutation():
+    c = _codec(nkv=3)
+    assert c.centroids.shape == (3, 8, 256, 8) and c.permutation.shape == (3, 64)
+    x = torch.randn(5, 64)
+    for h in range(3):
+        y = c._forward_transform(x, kv_head=h)
+        assert torch.equal(c._inverse_transform(y, kv_head=h), x)
+    assert torch.equal(_invert_permutation(c.permutation)[1][c.permutation[1]], torch.arange(64))
+
+
+def test_effective_permutation_identity_outside_profileperm_modes():
+    c = _codec(mode="identity_baseline")
+    assert torch.equal(c.effective_permutation(), torch.arange(64))
+    assert not torch.equal(_codec().effective_permutation(), torch.arange(64))
+
+
+def test_heavy_blocks_cached_and_refreshed():
+    c = _codec(mode="profileperm_mixed_precision")
+    assert c.heavy_blocks() is None
+    c.mixed_high_precision_blocks[2] = True
+    assert c.heavy_blocks()[2] is True and sum(c.heavy_blocks()) == 1
+    c.mixed_high_precision_blocks[2] = False
+    assert c.heavy_blocks() is None
+
+
+def test_unsupported_modes_raise_with_reason():
+    c = SunShapeBlockCodec(head_dim=64, block_dim=8, use_rotation=True, device="cpu")
+    assert "rotation" in c.unsupported_reason()
+    with pytest.raises(RuntimeError, match="rotation"):
+        c.quantize(torch.randn(4, 64))
+    pro = _codec(mode="profileperm_localmetric_dsq")
+    with pytest.raises(RuntimeError, match="metric"):
+        pro.quantize(torch.randn(4, 64))
+    with pytest.raises(NotImplementedError):
+        pro.fit(torch.randn(4, 64), torch.randn(4, 64))
+
+
+def test_scores_gate_reasons():
+    c = _codec()
+    q = torch.randn(4, 64)
+    qk = SunShapeQuantized(torch.zeros(10, 8, dtype=torch.uint8), 64, 8, 8)
+    assert "HIP device" in _triton_fast_path_unavailable_reason(c, q, qk)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        require_triton_fast_path(c, q, qk)
+    assert _triton_fast_path_unavailable_reason(c, q, object()) == "Quantized key must expose an .indices tensor."
+
+
+def test_ops_reject_cpu_tensors_before_any_launch():
+    c = _codec()
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        hip_ops.attention_scores(torch.randn(2, 64), torch.zeros(5, 8, dtype=torch.uint8), c.permutation, c.centroids)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        hip_ops.encode(torch.randn(1, 1, 5, 64), c.permutation, c.centroids)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        c.quantize(torch.randn(3, 64))
+
+
+def test_backend_gate_reasons():
+    c = _codec()
+    bundle = SunShapeBundle("m", [0], 1.0, 8, "profileperm_baseline", 0, 0, 0, {0: c})
+    rs = SunShapeVLLMRuntimeState("p", "m", "sunshape_base", 1.0, 8, [0], bundle, "cpu")
+    key = VB.SunShapeQuantizedKeys(quantized_heads=(), batch_size=2, num_kv_heads=2, seq_len=10)
+    q = torch.randn(2, 4, 1, 64)
+    v = torch.randn(2, 2, 10, 64)
+    R = VB._quantized_fast_path_unavailable_reason
+    kw = dict(runtime_state=rs, layer_idx=0, query=q, key=key, value=v, attn_mask=None, is_causal=False)
+    assert R(**kw) is None
+    assert R(**{**kw, "runtime_state": None}) == "No registered runtime state for quantized attention."
+    assert R(**{**kw, "key": torch.randn(2, 2, 10, 64)}) == "Key payload is not SunShapeQuantizedKeys."
+    assert R(**{**kw, "layer_idx": 5}) == "No codec for layer 5."
+    assert R(**{**kw, "query": torch.randn(3, 4, 1, 64)}) == "Quantized key batch size does not match query batch size."
+    assert R(**{**kw, "value": torch.randn(2, 2, 11, 64)}) == "Quantized key sequence length does not match value sequence length."
+    assert R(**{**kw, "query": torch.randn(2, 3, 1, 64)}) == "Query head count must be divisible by kv-head count."
+    assert R(**{**kw, "query": torch.randn(2, 4, 2, 64), "is_causal": True}) == \
+        "Causal quantized fast path currently targets decode (query_len == 1)."
+    assert R(**{**kw, "attn_mask": torch.zeros(10)}) == "Unsupported attention-mask rank for quantized fast path."
+    impl = VB.SunShapeAttentionImpl(layer_idx=0, runtime_state=rs)
+    bad = VB.SunShapeQuantizedKeys(quantized_heads=(), batch_size=3, num_kv_heads=2, seq_len=10)
+    with pytest.raises(RuntimeError, match="batch size"):
+        impl.forward(q, bad, v)
+
+
+def test_backend_dense_keys_go_to_delegate():
+    seen = {}
+
+    def delegate(q, k, v, **kw):
+        seen.update(kw)
+        return q + 1
+
+    impl = VB.SunShapeAttentionImpl(delegate=delegate, layer_idx=None)
+    VB.clear_registered_runtime()
+    q = torch.randn(1, 2, 1, 8)
+    out = impl.forward(q, torch.randn(1, 2, 4, 8), torch.randn(1, 2, 4, 8), scale=0.5)
+    assert torch.equal(out, q + 1) and seen["scale"] == 0.5
+
+
+def test_mask_view_matches_reference_slicing():
+    B, Hq, Lq, T = 2, 6, 1, 7
+    m2 = torch.randn(Lq, T)
+    m3b = torch.randn(B, Lq, T)
+    m3h = torch.randn(Hq, Lq, T)
+    m4 = torch.randn(B, Hq, Lq, T)
+    for m in (m2, m3b, m3h, m4):
+        view = VB._mask_view(m, B, Hq, Lq, T).expand(B, Hq, Lq, T)
+        for b in range(B):
+            for kv in range(2):
+                h0, h1 = kv * 3, kv * 3 + 3
+                # reference: sunshape/vllm_attn_backend.py:197-213
+                if m.ndim == 2:
+                    ref = m.unsqueeze(0)
+                elif m.ndim == 3:
+                    ref = m[b].unsqueeze(0) if m.shape[0] == B else m[h0:h1]
+                else:
+                    ref = m[b, h0:h1]
+                assert torch.equal(view[b, h0:h1], ref.expand(3, Lq, T))
+
+
+def test_mode_registration_globals():
+    VB.clear_registered_runtime()
+    VB.clear_registered_handle()
+    assert VB.get_mode() == VB.MODE_OFF
+    rs = SunShapeVLLMRuntimeState("p", "m", "x", 1.0, 8, [], SunShapeBundle("m", [], 1.0, 8, "x", 0, 0, 0, {}), "cpu")
+    VB.register_runtime_state(rs)
+    assert VB.get_mode() == VB.MODE_ACTIVE and VB.get_registered_runtime() is rs
+    assert VB.ensure_backend_registered()["runtime_loaded"]
+    VB.clear_registered_runtime()
+    assert VB.get_mode() == VB.MODE_OFF
+    keys = VB.SunShapeQuantizedKeys(quantized_heads=("a", "b", "c", "d"), batch_size=2, num_kv_heads=2, seq_len=1)
+    assert keys.head(1, 0) == "c"
+
+
+def test_bundle_roundtrip_and_extension(tmp_path):
+    c1 = _codec()
+    c2 = _codec(nkv=2, mode="profileperm_mixed_precision")
+    c2.mixed_high_precision_blocks[1] = True
+    b = SunShapeBundle("model", [0, 5], 1.0, 8, "profileperm_baseline", 4096, 3, 42, {0: c1, 5: c2}, {"k": 1})
+    path = b.save(tmp_path / "bundle.pt")
+    obj = torch.load(path, weights_only=True)
+    assert obj["format_version"] == 1 and "num_kv_heads" not in obj["codecs"]["0"]
+    assert obj["codecs"]["5"]["num_kv_heads"] == 2
+    b2 = SunShapeBundle.load(path, device="cpu")
+    assert b2.layers == [0, 5] and b2.trace_meta == {"k": 1}
+    for k, v in c2.state_dict().items():
+        assert torch.equal(b2.codecs[5].state_dict()[k], v)
+    assert b2.codecs[5].heavy_blocks()[1]
+    torch.save({"nope": 1}, tmp_path / "bad.pt")
+    with pytest.raises(ValueError):
+        SunShapeBundle.load(tmp_path / "bad.pt", device="cpu")
+
+
+def test_mode_aliases_and_block_dim():
+    assert resolve_mode_alias("sunshape_mixed") == "profileperm_mixed_precision"
+    assert default_block_dim(1.0) == 8 and default_block_dim(4.0) == 2
+    with pytest.raises(ValueError):
+        resolve_mode_alias("nope")
+
+
+def test_synthetic_configs_shapes():
+    p = synthetic.config1()
+    assert p["codes"].shape == (4096, 8) and p["centroids"].shape == (8, 256, 8)
+    p = synthetic.config2(B=2, T=64)
+    assert p["q"].shape == (2, 14, 1, 64) and p["q"].dtype == torch.bfloat16 and p["codes"].shape == (2, 2, 64, 8)
+    p = synthetic.config4(B=2, T=64)
+    assert p["code_pages"].shape == (8, 8, 16, 32) and p["v_pages"].shape == (8, 8, 128, 16)
+    assert sorted(p["block_table"].flatten().tolist()) == list(range(8))
+    p = synthetic.config5(B=1, S=32)
+    assert p["heavy"].sum() == 4 and not p["centroids"][:, p["heavy"]].any()
+    cb = synthetic.make_codebook(2, 64, 2, 0)
+    # codebook coordinates follow the permuted per-dim sigma
+    assert cb.centroids.shape == (2, 32, 256, 2)
+    assert math.isclose(float(cb.sigma.min()), 0.1, rel_tol=2.0) and float(cb.sigma.max()) <= 3.0

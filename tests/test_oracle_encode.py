@@ -1,0 +1,136 @@
+"""Pins the oracle's encode (oracle/vq_encode.c) against torch.cdist, the library
+call the reference's quantize makes (sunshape/codec.py:376-377).  CPU only.
+
+torch.cdist on these sizes computes sqrt(clamp_min([-2x, |x|^2, 1] @ [c, 1, |c|^2]^T, 0)).
+The pre-sqrt GEMM is reproduced bit-for-bit.  torch's CPU sqrt is not correctly
+rounded (its last bit depends on the host CPU: about 0.6% of inputs differ on this
+container's Xeon and ~17% on an EPYC host), so the oracle uses the IEEE sqrt, and
+the two argmins can differ only where two codewords' distances are within a few ulps
+(a sqrt-rounding tie).  The tests below check the GEMM bitwise, and check that every
+argmin difference against torch.cdist is such a tie.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import vq_oracle as O
+
+
+def _torch_mm_dist2(x: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """ATen's _euclidean_dist before clamp/sqrt, via the same torch calls."""
+    x1 = torch.from_numpy(x)
+    x2 = torch.from_numpy(c)
+    x1n = x1.pow(2).sum(-1, keepdim=True)
+    x2n = x2.pow(2).sum(-1, keepdim=True)
+    x1_ = torch.cat([x1.mul(-2), x1n, torch.ones_like(x1n)], -1)
+    x2_ = torch.cat([x2, torch.ones_like(x2n), x2n], -1)
+    return x1_.matmul(x2_.mT).numpy()
+
+
+def _data(seed, n, bd, nc=256, bf16=True):
+    rng = np.random.default_rng(seed)
+    sig = np.exp(rng.uniform(math.log(0.1), math.log(3), bd)).astype(np.float32)
+    x = (rng.standard_normal((n, bd)) * sig).astype(np.float32)
+    if bf16:
+        x = O.bf16_round(x)
+    c = (rng.standard_normal((nc, bd)) * sig).astype(np.float32)
+    return x, c
+
+
+@pytest.mark.parametrize("bd", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("n", [30, 1000, 6000])
+def test_presqrt_gemm_bit_exact_vs_torch(bd, n):
+    x, c = _data(100 + bd * 7 + n, n, bd)
+    e2, _ = O.block_distances(x, c)
+    ref = _torch_mm_dist2(x, c)
+    assert np.array_equal(e2.view(np.uint32), ref.view(np.uint32))
+
+
+def test_check_detects_unfused_accumulation():
+    """A plausible mistake (separately rounded products) is caught by the bitwise check."""
+    x, c = _data(7, 2000, 4)
+    ref = _torch_mm_dist2(x, c)
+    xn = (x * x).astype(np.float32)
+    xn = (((xn[:, 0] + xn[:, 1]).astype(np.float32) + xn[:, 2]).astype(np.float32) + xn[:, 3]).astype(np.float32)
+    cn = (c * c).astype(np.float32)
+    cn = (((cn[:, 0] + cn[:, 1]).astype(np.float32) + cn[:, 2]).astype(np.float32) + cn[:, 3]).astype(np.float32)
+    acc = ((-2 * x[:, None, 0]) * c[None, :, 0]).astype(np.float32)
+    for d in range(1, 4):
+        acc = (acc + ((-2 * x[:, None, d]) * c[None, :, d]).astype(np.float32)).astype(np.float32)
+    acc = ((acc + xn[:, None]).astype(np.float32) + cn[None, :]).astype(np.float32)
+    assert not np.array_equal(acc, ref)
+
+
+def test_post_sqrt_is_ieee_sqrt_of_clamped_gemm():
+    x, c = _data(8, 3000, 2)
+    e2, d = O.block_distances(x, c)
+    assert np.array_equal(d, np.sqrt(np.maximum(e2, np.float32(0))))
+
+
+def _assert_only_sqrt_ties(x, c, got, ref):
+    """Rows where two argmins differ must hold a tie of the pre-sqrt values within 4 ulps."""
+    e2 = _torch_mm_dist2(x, c)
+    bad = np.nonzero(got != ref)[0]
+    for i in bad:
+        a, b = e2[i, got[i]], e2[i, ref[i]]
+        lo = min(a, b)
+        assert abs(a - b) <= 4 * np.spacing(np.float32(max(abs(lo), 1e-30))), (i, a, b)
+    return len(bad)
+
+
+@pytest.mark.parametrize("bd", [2, 4, 8])
+def test_encode_argmin_matches_torch_cdist(bd):
+    n = 20000
+    x, c = _data(200 + bd, n, bd)
+    got, _ = O.encode(x, np.arange(bd), c[None])
+    ref = torch.cdist(torch.from_numpy(x), torch.from_numpy(c)).argmin(-1).numpy()
+    n_ties = _assert_only_sqrt_ties(x, c, got[:, 0], ref)
+    assert n_ties <= max(2, n // 10000)
+
+
+def test_encode_near_ties_constructed():
+    """Codewords duplicated or nudged by one ulp: first index on exact ties, smaller d otherwise."""
+    rng = np.random.default_rng(9)
+    bd = 2
+    c = rng.standard_normal((256, bd)).astype(np.float32)
+    c[200] = c[17]                      # exact duplicate: lower index must win
+    c[201] = np.nextafter(c[40], np.float32(np.inf))
+    x = np.concatenate([c[[17, 40, 201, 5]], rng.standard_normal((500, bd)).astype(np.float32)])
+    got, _ = O.encode(x, np.arange(bd), c[None])
+    ref = torch.cdist(torch.from_numpy(x), torch.from_numpy(c)).argmin(-1).numpy()
+    assert got[0, 0] == 17
+    _assert_only_sqrt_ties(x, c, got[:, 0], ref)
+
+
+def test_encode_exact_centroid_rows():
+    rng = np.random.default_rng(10)
+    D, bd = 16, 2
+    perm = rng.permutation(D)
+    cent = rng.standard_normal((D // bd, 256, bd)).astype(np.float32) * 3
+    pick = rng.integers(0, 256, (50, D // bd))
+    xp = np.stack([np.concatenate([cent[b, pick[i, b]] for b in range(D // bd)]) for i in range(50)])
+    keys = O.inverse_transform(xp, perm).astype(np.float32)
+    codes, _ = O.encode(keys, perm, cent)
+    assert np.array_equal(codes, pick.astype(np.uint8))
+
+
+def test_encode_heavy_blocks_passthrough():
+    rng = np.random.default_rng(11)
+    D, bd = 64, 2
+    perm = rng.permutation(D)
+    cent = rng.standard_normal((32, 256, bd)).astype(np.float32)
+    heavy = np.zeros(32, bool)
+    heavy[[0, 9, 20, 31]] = True
+    keys = O.bf16_round(rng.standard_normal((300, D)).astype(np.float32))
+    codes, pt = O.encode(keys, perm, cent, heavy)
+    xp = O.forward_transform(keys, perm).reshape(300, 32, bd)
+    assert not codes[:, heavy].any()
+    assert np.array_equal(pt[:, heavy], xp[:, heavy])
+    assert not pt[:, ~heavy].any()
+    # light blocks agree with per-block cdist argmin
+    for b in np.nonzero(~heavy)[0][:5]:
+        ref = torch.cdist(torch.from_numpy(xp[:, b].copy()), torch.from_numpy(cent[b])).argmin(-1).numpy()
+        _assert_only_sqrt_ties(xp[:, b].copy(), cent[b], codes[:, b], ref)
