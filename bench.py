@@ -40,7 +40,7 @@ def _args():
     ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5enc"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
 
 
@@ -201,7 +201,7 @@ def _cpu_baseline(unit_data, seconds):
 
     limit = threadpool_limits(limits=1) if threadpool_limits else contextlib.nullcontext()
     with limit:
-        while elapsed < seconds and units < 64:
+        while elapsed < seconds and units < 4096:
             b = int(rng.integers(p.meta["B"]))
             kv = int(rng.integers(p.meta["Hkv"]))
             if paged:

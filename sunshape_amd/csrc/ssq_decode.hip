@@ -543,6 +543,14 @@ int run_generic(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipS
 
 }  // namespace
 
+// Launches the split merge (shared with the MFMA decode kernel).
+int ssq_launch_merge(const ssq_decode_args& a, int n_splits, const float* ws_o, const float* ws_m,
+                     const float* ws_l, hipStream_t st) {
+    const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
+    hipLaunchKernelGGL(k_merge, dim3((unsigned)n_rows_all), dim3(128), 0, st, a, n_splits, ws_o, ws_m, ws_l);
+    return ssq_check_hip(hipGetLastError(), "k_merge launch");
+}
+
 int ssq_decode_mfma_supported(const ssq_decode_args* a);
 size_t ssq_decode_mfma_workspace(const ssq_decode_args* a);
 int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipStream_t st);

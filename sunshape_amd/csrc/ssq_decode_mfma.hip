@@ -1,9 +1,410 @@
-// MFMA paged decode kernel (vLLM page layout, P.V on matrix cores).
+// Fused VQ-key decode over vLLM-style pages with P.V on the matrix cores (gfx950).
+//
+// Same mathematics as the generic kernel (ssq_decode.hip): LUT scores
+// (triton_kernels.py:381-408, :174-196), online softmax, probabilities cast to
+// the value dtype before P.V (vllm_attn_backend.py:251-252).  Different mapping:
+//
+//   workgroup = 8 waves for one (batch, KV head, context split); LUT [nb][nc][RP]
+//   fp32 in LDS (<= ~144 KiB, so one workgroup per CU).
+//   wave      = streams 64-token tiles (4 pages of 16) independently with its own
+//               running (max, sum, O); waves merge through LDS at the end.
+//   scores    = one token per lane: nb ds_read_b128 LUT gathers give all RP rows.
+//   P.V       = v_mfma_f32_16x16x32_bf16 (or _f16): A = P [16 rows x 32 tokens]
+//               staged through a per-wave LDS strip; B = V [32 tokens x 16 dims]
+//               read straight from the page: vLLM's value page is dim-major
+//               ([Dv][page]), so the 8 consecutive tokens of one dim that a lane
+//               supplies to the B operand are one 16-byte load.
 #include "ssq_common.h"
 
-int ssq_decode_mfma_supported(const ssq_decode_args* a) { (void)a; return 0; }
-size_t ssq_decode_mfma_workspace(const ssq_decode_args* a) { (void)a; return 0; }
+#include <math.h>
+
+int ssq_launch_merge(const ssq_decode_args& a, int n_splits, const float* ws_o, const float* ws_m,
+                     const float* ws_l, hipStream_t st);
+
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * SSQ_WAVE;
+constexpr int kTileTok = 64;  // tokens per wave iteration (4 pages)
+constexpr int kPage = 16;
+constexpr size_t kMaxSmem = 160 * 1024;
+
+struct MfmaParams {
+    ssq_decode_args a;
+    int G, rows, split_len, n_splits;
+    float* ws_o;
+    float* ws_m;
+    float* ws_l;
+};
+
+// LDS carve-up (floats): lut [nb*nc*RP] | qp [RP*D] | pstrip [waves][RP][64] (16-bit, as floats/2)
+__host__ __device__ inline size_t lut_floats(const ssq_decode_args& a, int RP) {
+    return (size_t)a.n_blocks * a.n_centroids * RP;
+}
+__host__ __device__ inline size_t pstrip_offset(const ssq_decode_args& a, int RP) {
+    return (lut_floats(a, RP) + (size_t)RP * a.head_dim + 3) & ~(size_t)3;
+}
+inline size_t mfma_smem(const ssq_decode_args& a, int RP) {
+    const size_t main = pstrip_offset(a, RP) + (size_t)kWaves * RP * kTileTok / 2;
+    const size_t merge = (size_t)kWaves * RP * (a.value_dim + 2);
+    return (main > merge ? main : merge) * sizeof(float);
+}
+
+template <int VT>
+__device__ __forceinline__ uint32_t to_vt16(float x) {
+    return VT == SSQ_BF16 ? ssq_f32_to_bf16(x) : ssq_f32_to_f16(x);
+}
+
+template <int VT>
+__device__ __forceinline__ v4f mfma(const uint4& a, const uint4& b, v4f c) {
+    if (VT == SSQ_BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0,
+                                                       0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+}
+
+template <int RP, int DT, int VT>
+__global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
+    extern __shared__ __align__(16) float smem[];
+    const ssq_decode_args& a = p.a;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int bk = blockIdx.x;
+    const int split = blockIdx.y;
+    const int b = bk / a.num_kv_heads;
+    const int kv = bk - b * a.num_kv_heads;
+    const int nb = a.n_blocks, nc = a.n_centroids, D = a.head_dim, bd = a.block_dim;
+    const int nr = p.rows;  // <= RP
+    const int T = min(a.seq_lens[b], a.seq_len);
+    const int t_begin = split * p.split_len;
+    const int t_end = min(T, t_begin + p.split_len);
+
+    float* lut = smem;
+    float* qp = smem + lut_floats(a, RP);
+    uint16_t* pstrip = reinterpret_cast<uint16_t*>(smem + pstrip_offset(a, RP)) + wave * RP * kTileTok;
+
+    // ---- scaled, permuted query rows; LUT build
+    const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
+    for (int e = tid; e < RP * D; e += kThreads) {
+        const int r = e / D, j = e - r * D;
+        float v = 0.f;
+        if (r < nr) {
+            const int g = r / a.q_len, qi = r - g * a.q_len;
+            const int h = kv * p.G + g;
+            v = ssq_load_elem(a.q, a.q_dtype, (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl + perm[j]);
+            if (a.has_scale) v = ssq_round_to(v * a.scale, a.q_dtype);
+        }
+        qp[e] = v;
+    }
+    __syncthreads();
+    const float* cent = a.cent + (int64_t)kv * a.cent_sh;
+    for (int e = tid; e < nb * nc; e += kThreads) {
+        const int blk = e / nc;
+        const float* c = cent + (int64_t)e * bd;
+        float acc[RP];
+#pragma unroll
+        for (int r = 0; r < RP; ++r) acc[r] = qp[r * D + blk * bd] * c[0];
+        for (int d = 1; d < bd; ++d) {
+            const float cd = c[d];
+#pragma unroll
+            for (int r = 0; r < RP; ++r) acc[r] = fmaf(qp[r * D + blk * bd + d], cd, acc[r]);
+        }
+        if (RP % 4 == 0) {
+#pragma unroll
+            for (int r = 0; r < RP; r += 4)
+                *reinterpret_cast<float4*>(lut + (size_t)e * RP + r) = make_float4(acc[r], acc[r + 1], acc[r + 2], acc[r + 3]);
+        } else {
+#pragma unroll
+            for (int r = 0; r < RP; ++r) lut[(size_t)e * RP + r] = acc[r];
+        }
+    }
+    __syncthreads();
+
+    // ---- stream tiles
+    float m_run[RP], l_lane[RP];
+#pragma unroll
+    for (int r = 0; r < RP; ++r) { m_run[r] = -INFINITY; l_lane[r] = 0.f; }
+    v4f acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    const int32_t* btab = a.block_table + (int64_t)b * a.bt_sb;
+    const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)kv * a.v_sh + (int64_t)(lane & 15) * a.v_st;
+    const uint8_t* cbase = a.codes + (int64_t)kv * a.c_sh;
+    const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
+    const int arow = lane & 15;          // A-operand row (query row) this lane supplies
+    const int kchunk = 8 * (lane >> 4);  // first of the 8 tokens this lane supplies within a 32-token K group
+
+    for (int tile = wave; tile < n_tiles; tile += kWaves) {
+        const int t0 = t_begin + tile * kTileTok;
+        const int t = t0 + lane;
+        const bool valid = t < t_end;
+        // V fragments for the two 32-token K groups (issued first: the long-latency loads)
+        uint4 vf[2][DT];
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const int tk = t0 + 32 * g + kchunk;
+            if (tk < t_end) {
+                const int page = btab[tk >> 4];
+                const uint16_t* src = vbase + (int64_t)page * a.v_sb + (tk & 15);
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) vf[g][dt] = *reinterpret_cast<const uint4*>(src + (int64_t)(16 * dt) * a.v_st);
+                if (tk + 8 > t_end) {  // tail: zero values of tokens past the end (unwritten slots)
+                    const int keep = t_end - tk;
+#pragma unroll
+                    for (int dt = 0; dt < DT; ++dt) {
+                        uint32_t w[4] = {vf[g][dt].x, vf[g][dt].y, vf[g][dt].z, vf[g][dt].w};
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            if (j >= keep) w[j >> 1] &= (j & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+                        vf[g][dt] = make_uint4(w[0], w[1], w[2], w[3]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) vf[g][dt] = make_uint4(0, 0, 0, 0);
+            }
+        }
+        // scores: one token per lane
+        float s[RP];
+#pragma unroll
+        for (int r = 0; r < RP; ++r) s[r] = 0.f;
+        if (valid) {
+            const int page = btab[t >> 4];
+            const uint32_t* crow = reinterpret_cast<const uint32_t*>(cbase + (int64_t)page * a.c_sb + (int64_t)(t & 15) * a.c_st);
+            for (int w4 = 0; w4 < (nb >> 2); ++w4) {
+                const uint32_t word = crow[w4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const int blk = 4 * w4 + k;
+                    const int code = (word >> (8 * k)) & 0xFF;
+                    const int cc = code < nc ? code : nc - 1;
+                    const float* e = lut + ((size_t)blk * nc + cc) * RP;
+                    if (RP % 4 == 0) {
+#pragma unroll
+                        for (int r = 0; r < RP; r += 4) {
+                            const float4 v = *reinterpret_cast<const float4*>(e + r);
+                            s[r] += v.x; s[r + 1] += v.y; s[r + 2] += v.z; s[r + 3] += v.w;
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < RP; ++r) s[r] += e[r];
+                    }
+                }
+            }
+            if (a.scores) {
+#pragma unroll
+                for (int r = 0; r < RP; ++r) {
+                    if (r < nr) {
+                        const int g = r / a.q_len, qi = r - g * a.q_len;
+                        const int h = kv * p.G + g;
+                        a.scores[(int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)qi * a.s_sl + t] = s[r];
+                    }
+                }
+            }
+        }
+        // online softmax (wave-local)
+        float alpha[RP];
+        bool rescale = false;
+#pragma unroll
+        for (int r = 0; r < RP; ++r) {
+            const float tm = ssq_wave_max(valid ? s[r] : -INFINITY);
+            const float mn = fmaxf(m_run[r], tm);
+            alpha[r] = (mn == -INFINITY) ? 1.f : __expf(m_run[r] - mn);
+            rescale |= mn != m_run[r];
+            m_run[r] = mn;
+            const float pr = (valid && mn != -INFINITY) ? __expf(s[r] - mn) : 0.f;
+            l_lane[r] = l_lane[r] * alpha[r] + pr;
+            pstrip[r * kTileTok + lane] = (uint16_t)to_vt16<VT>(pr);
+        }
+        if (rescale) {  // wave-uniform
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 4 * (lane >> 4) + i;
+                float f = 1.f;
+#pragma unroll
+                for (int r = 0; r < RP; ++r)
+                    if (row == r) f = alpha[r];
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) acc[dt][i] *= f;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // A fragments: row arow, tokens 32g + kchunk .. +8 of this tile
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            uint4 af = make_uint4(0, 0, 0, 0);
+            if (arow < RP) af = *reinterpret_cast<const uint4*>(pstrip + arow * kTileTok + 32 * g + kchunk);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma<VT>(af, vf[g][dt], acc[dt]);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // ---- merge the waves' (m, l, O) through LDS (the LUT is no longer needed)
+    float l_w[RP];
+#pragma unroll
+    for (int r = 0; r < RP; ++r) l_w[r] = ssq_wave_sum(l_lane[r]);
+    __syncthreads();
+    float* mbuf = smem;                         // [waves][RP]
+    float* lbuf = mbuf + kWaves * RP;           // [waves][RP]
+    float* obuf = lbuf + kWaves * RP;           // [waves][RP][Dv]
+    const int Dv = DT * 16;
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RP; ++r) { mbuf[wave * RP + r] = m_run[r]; lbuf[wave * RP + r] = l_w[r]; }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = 4 * (lane >> 4) + i;
+        if (row < RP) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) obuf[((size_t)wave * RP + row) * Dv + 16 * dt + (lane & 15)] = acc[dt][i];
+        }
+    }
+    __syncthreads();
+    const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
+    for (int e = tid; e < nr * Dv; e += kThreads) {
+        const int r = e / Dv, dv = e - r * Dv;
+        float M = -INFINITY;
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mbuf[w * RP + r]);
+        float L = 0.f, o = 0.f;
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = mbuf[w * RP + r];
+            if (mw == -INFINITY) continue;
+            const float f = __expf(mw - M);
+            L += lbuf[w * RP + r] * f;
+            o += obuf[((size_t)w * RP + r) * Dv + dv] * f;
+        }
+        const int g = r / a.q_len, qi = r - g * a.q_len;
+        const int h = kv * p.G + g;
+        const int rid = (b * a.num_q_heads + h) * a.q_len + qi;
+        if (p.n_splits == 1) {
+            ssq_store_elem(a.out, a.v_dtype, (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)qi * a.o_sl + dv, o / L);
+            if (a.lse && dv == 0) a.lse[rid] = M + logf(L);
+        } else {
+            p.ws_o[((size_t)split * n_rows_all + rid) * Dv + dv] = o;
+            if (dv == 0) {
+                p.ws_m[(size_t)split * n_rows_all + rid] = M;
+                p.ws_l[(size_t)split * n_rows_all + rid] = L;
+            }
+        }
+    }
+}
+
+int pow2_at_least(int x) {
+    int q = 1;
+    while (q < x) q <<= 1;
+    return q;
+}
+
+struct MPlan {
+    int RP, DT, split_len, n_splits;
+    size_t smem, ws_bytes;
+};
+
+bool plan(const ssq_decode_args* a, MPlan& pl) {
+    if (a->layout != SSQ_PAGED || a->page_size != kPage) return false;
+    if (a->v == nullptr || (a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16)) return false;
+    if (a->mask != nullptr || a->heavy_mask[0] || a->heavy_mask[1]) return false;
+    if (a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;
+    if (a->n_blocks % 4 != 0 || a->c_st % 4 != 0 || a->c_sb % 4 != 0 || a->c_sh % 4 != 0 || (uintptr_t)a->codes % 4)
+        return false;
+    if ((uintptr_t)a->v % 16 || (a->v_sb * 2) % 16 || (a->v_sh * 2) % 16 || (a->v_st * 2) % 16) return false;
+    const int rows = (a->num_q_heads / a->num_kv_heads) * a->q_len;
+    if (rows > 16) return false;
+    pl.RP = pow2_at_least(rows);
+    pl.DT = a->value_dim / 16;
+    pl.smem = mfma_smem(*a, pl.RP);
+    if (pl.smem > kMaxSmem) return false;
+    const int units = a->batch * a->num_kv_heads;
+    const int tiles = (a->seq_len + kTileTok - 1) / kTileTok;
+    int splits = a->num_splits > 0 ? a->num_splits : (256 + units - 1) / units;
+    const int max_splits = (tiles + kWaves - 1) / kWaves;  // keep every wave busy
+    if (splits > max_splits) splits = max_splits;
+    if (splits < 1) splits = 1;
+    const int tiles_per_split = (tiles + splits - 1) / splits;
+    pl.split_len = tiles_per_split * kTileTok;
+    pl.n_splits = (a->seq_len + pl.split_len - 1) / pl.split_len;
+    if (pl.n_splits < 1) pl.n_splits = 1;
+    const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
+    pl.ws_bytes = pl.n_splits > 1 ? (size_t)pl.n_splits * n_rows_all * (a->value_dim + 2) * 4 : 0;
+    return true;
+}
+
+template <int RP, int DT, int VT>
+int launch(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
+    auto kern = k_decode_mfma<RP, DT, VT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxSmem);
+        if (e != hipSuccess) return ssq_check_hip(e, "hipFuncSetAttribute(decode_mfma)");
+        attr_set = true;
+    }
+    dim3 grid(mp.a.batch * mp.a.num_kv_heads, pl.n_splits);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), pl.smem, st, mp);
+    return ssq_check_hip(hipGetLastError(), "k_decode_mfma launch");
+}
+
+template <int RP, int VT>
+int launch_dt(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
+    switch (pl.DT) {
+        case 4: return launch<RP, 4, VT>(mp, pl, st);
+        case 8: return launch<RP, 8, VT>(mp, pl, st);
+        default: return launch<RP, 16, VT>(mp, pl, st);
+    }
+}
+
+template <int RP>
+int launch_vt(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
+    return mp.a.v_dtype == SSQ_BF16 ? launch_dt<RP, SSQ_BF16>(mp, pl, st) : launch_dt<RP, SSQ_F16>(mp, pl, st);
+}
+
+}  // namespace
+
+int ssq_decode_mfma_supported(const ssq_decode_args* a) {
+    MPlan pl;
+    return plan(a, pl) ? 1 : 0;
+}
+
+size_t ssq_decode_mfma_workspace(const ssq_decode_args* a) {
+    MPlan pl;
+    return plan(a, pl) ? pl.ws_bytes : 0;
+}
+
 int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipStream_t st) {
-    (void)a; (void)workspace; (void)ws_bytes; (void)st;
-    return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode kernel not built");
+    MPlan pl;
+    if (!plan(a, pl)) return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode kernel does not support this problem");
+    if (a->seq_len == 0) return ssq_fail(SSQ_ERR_INVALID, "seq_len == 0: softmax over an empty context");
+    SSQ_REQUIRE(ws_bytes >= pl.ws_bytes, "workspace too small: %zu < %zu bytes", ws_bytes, pl.ws_bytes);
+    SSQ_REQUIRE(pl.ws_bytes == 0 || workspace, "workspace is NULL");
+    MfmaParams mp;
+    mp.a = *a;
+    mp.G = a->num_q_heads / a->num_kv_heads;
+    mp.rows = mp.G * a->q_len;
+    mp.split_len = pl.split_len;
+    mp.n_splits = pl.n_splits;
+    const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
+    float* ws = reinterpret_cast<float*>(workspace);
+    mp.ws_o = ws;
+    mp.ws_m = ws ? ws + (size_t)pl.n_splits * n_rows_all * a->value_dim : nullptr;
+    mp.ws_l = ws ? mp.ws_m + (size_t)pl.n_splits * n_rows_all : nullptr;
+    int rc;
+    switch (pl.RP) {
+        case 1: rc = launch_vt<1>(mp, pl, st); break;
+        case 2: rc = launch_vt<2>(mp, pl, st); break;
+        case 4: rc = launch_vt<4>(mp, pl, st); break;
+        case 8: rc = launch_vt<8>(mp, pl, st); break;
+        default: rc = launch_vt<16>(mp, pl, st); break;
+    }
+    if (rc) return rc;
+    if (pl.n_splits > 1) rc = ssq_launch_merge(*a, pl.n_splits, mp.ws_o, mp.ws_m, mp.ws_l, st);
+    return rc;
 }

@@ -187,7 +187,8 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
         _on_gpu(name, t)
     _require(q.ndim == 4, "Quantized attention expects query/value tensors with shape [batch, heads, seq, dim].")
     _require(codes.dtype == torch.uint8, "codes must be uint8")
-    _require(q.stride(-1) == 1 and codes.stride(-1) == 1, "query and codes must be contiguous in the last dim")
+    q = q if q.stride(-1) == 1 else q.contiguous()
+    _require(codes.stride(-1) == 1, "codes must be contiguous in the last dim")
     B, Hq, Lq, D = q.shape
     paged = block_table is not None
     Hkv = codes.shape[1]
@@ -280,7 +281,7 @@ def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
     """
     _on_gpu("key_states", keys)
     _require(keys.ndim == 4, "quantize_key_states expects key_states with shape [batch, kv_heads, seq_len, head_dim].")
-    _require(keys.stride(-1) == 1, "keys must be contiguous in the last dim")
+    keys = keys if keys.stride(-1) == 1 else keys.contiguous()
     B, Hkv, S, D = keys.shape
     perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, Hkv)
     w0, w1 = N.heavy_mask_words(heavy)
