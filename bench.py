@@ -37,7 +37,7 @@ def _args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5enc"])
+    ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5enc", "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -178,6 +178,21 @@ def _encode_workload(dev, kernel):
     return step, n, algo, cfg, None, "ssq_encode"
 
 
+def _copy_workload(dev):
+    """A plain 1 GiB device-to-device copy: calibrates rocprofv3's FETCH_SIZE/WRITE_SIZE counters."""
+    import torch
+
+    n = 1 << 30
+    src = torch.ones(n // 2, device=dev, dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+
+    def step():
+        dst.copy_(src)
+
+    cfg = {"workload": "calibration copy, 1 GiB read + 1 GiB write", "bytes_read": n, "bytes_written": n}
+    return step, n // 2, 2 * n, cfg, None, "copy"
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 def _cpu_baseline(unit_data, seconds):
     """The oracle's eager restatement of the reference decode path, one (batch, KV head) at a time."""
@@ -235,6 +250,8 @@ def main():
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
         step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev)
+    elif args.workload == "copycal":
+        step, keys, algo_bytes, cfg, unit_data, kname = _copy_workload(dev)
     else:
         step, keys, algo_bytes, cfg, unit_data, kname = _encode_workload(dev, args.kernel)
 

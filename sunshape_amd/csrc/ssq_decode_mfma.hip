@@ -4,7 +4,7 @@
 // (triton_kernels.py:381-408, :174-196), online softmax, probabilities cast to
 // the value dtype before P.V (vllm_attn_backend.py:251-252).  Different mapping:
 //
-//   workgroup = 8 waves for one (batch, KV head, context split); LUT [nb][nc][RP]
+//   workgroup = 4 waves (one per SIMD) for one (batch, KV head, context split); LUT [nb][nc][RP]
 //   fp32 in LDS (<= ~144 KiB, so one workgroup per CU).
 //   wave      = streams 64-token tiles (4 pages of 16) independently with its own
 //               running (max, sum, O); waves merge through LDS at the end.
@@ -27,10 +27,14 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
-constexpr int kWaves = 8;
+#ifndef SSQ_DECODE_WAVES
+#define SSQ_DECODE_WAVES 4
+#endif
+constexpr int kWaves = SSQ_DECODE_WAVES;  // waves per workgroup
 constexpr int kThreads = kWaves * SSQ_WAVE;
 constexpr int kTileTok = 64;  // tokens per wave iteration (4 pages)
 constexpr int kPage = 16;
+constexpr int kNC = 256;      // codewords per block (uint8 codes)
 constexpr size_t kMaxSmem = 160 * 1024;
 
 struct MfmaParams {
@@ -41,15 +45,16 @@ struct MfmaParams {
     float* ws_l;
 };
 
-// LDS carve-up (floats): lut [nb*nc*RP] | qp [RP*D] | pstrip [waves][RP][64] (16-bit, as floats/2)
-__host__ __device__ inline size_t lut_floats(const ssq_decode_args& a, int RP) {
-    return (size_t)a.n_blocks * a.n_centroids * RP;
-}
+// LDS carve-up (floats): lut [nb*256*RP] | qp [RP*D] | pstrip [waves][RP][64] (16-bit) | pages [split_len/16] (int32)
+__host__ __device__ inline size_t lut_floats(const ssq_decode_args& a, int RP) { return (size_t)a.n_blocks * kNC * RP; }
 __host__ __device__ inline size_t pstrip_offset(const ssq_decode_args& a, int RP) {
     return (lut_floats(a, RP) + (size_t)RP * a.head_dim + 3) & ~(size_t)3;
 }
-inline size_t mfma_smem(const ssq_decode_args& a, int RP) {
-    const size_t main = pstrip_offset(a, RP) + (size_t)kWaves * RP * kTileTok / 2;
+__host__ __device__ inline size_t pages_offset(const ssq_decode_args& a, int RP) {
+    return pstrip_offset(a, RP) + (size_t)kWaves * RP * kTileTok / 2;
+}
+inline size_t mfma_smem(const ssq_decode_args& a, int RP, int split_len) {
+    const size_t main = pages_offset(a, RP) + (size_t)split_len / kPage;
     const size_t merge = (size_t)kWaves * RP * (a.value_dim + 2);
     return (main > merge ? main : merge) * sizeof(float);
 }
@@ -67,7 +72,174 @@ __device__ __forceinline__ v4f mfma(const uint4& a, const uint4& b, v4f c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
 }
 
-template <int RP, int DT, int VT>
+// wave-wide max / sum: DPP rotations inside each 16-lane row, then the four row results by readlane
+template <int CTL>
+__device__ __forceinline__ float dpp_ror(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_ror<0x121>(v));
+    v = fmaxf(v, dpp_ror<0x122>(v));
+    v = fmaxf(v, dpp_ror<0x124>(v));
+    v = fmaxf(v, dpp_ror<0x128>(v));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_ror<0x121>(v);
+    v += dpp_ror<0x122>(v);
+    v += dpp_ror<0x124>(v);
+    v += dpp_ror<0x128>(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// registers of one 64-token tile in flight
+template <int NB, int DT>
+struct TileRegs {
+    uint4 c[NB / 16 > 0 ? NB / 16 : 1];  // this lane's token codes (NB bytes)
+    uint2 c8;                            // NB == 8
+    uint4 v[2][DT];                      // B-operand V fragments of the two 32-token K groups
+};
+
+template <int NB, int DT>
+__device__ __forceinline__ void issue_tile(const ssq_decode_args& a, const int* pages, int t_begin, int t_end, int tile,
+                                           int lane, const uint8_t* cbase, const uint16_t* vbase, TileRegs<NB, DT>& R) {
+    const int rel = tile * kTileTok;  // tile start relative to the split
+    const int t = t_begin + rel + lane;
+    if (t < t_end) {
+        const int page = pages[(rel + lane) >> 4];
+        const uint8_t* crow = cbase + (int64_t)page * a.c_sb + (int64_t)(t & 15) * a.c_st;
+        if (NB >= 16) {
+#pragma unroll
+            for (int i = 0; i < NB / 16; ++i) R.c[i] = reinterpret_cast<const uint4*>(crow)[i];
+        } else {
+            R.c8 = *reinterpret_cast<const uint2*>(crow);
+        }
+    }
+    const int kchunk = 8 * (lane >> 4);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const int r = rel + 32 * g + kchunk;
+        if (t_begin + r < t_end) {
+            const uint16_t* src = vbase + (int64_t)pages[r >> 4] * a.v_sb + (r & 15);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) R.v[g][dt] = *reinterpret_cast<const uint4*>(src + (int64_t)(16 * dt) * a.v_st);
+        }
+    }
+}
+
+template <int RP, int DT, int VT, int NB>
+__device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* lut, uint16_t* pstrip, int b, int kv,
+                                             int t_begin, int t_end, int tile, int lane, TileRegs<NB, DT>& R,
+                                             float (&m_run)[RP], float (&l_lane)[RP], v4f (&acc)[DT]) {
+    const ssq_decode_args& a = p.a;
+    const int t0 = t_begin + tile * kTileTok;
+    const int t = t0 + lane;
+    const bool valid = t < t_end;
+    float s[RP];
+#pragma unroll
+    for (int r = 0; r < RP; ++r) s[r] = 0.f;
+    if (valid) {
+#pragma unroll
+        for (int wi = 0; wi < NB / 4; ++wi) {
+            uint32_t word;
+            if (NB >= 16) {
+                const uint4 c = R.c[wi >> 2];
+                word = (wi & 3) == 0 ? c.x : (wi & 3) == 1 ? c.y : (wi & 3) == 2 ? c.z : c.w;
+            } else {
+                word = (wi & 1) ? R.c8.y : R.c8.x;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int blk = 4 * wi + k;
+                const uint32_t code = (word >> (8 * k)) & 0xFFu;
+                const float* e = lut + ((size_t)blk * kNC + code) * RP;
+                if (RP >= 4) {
+#pragma unroll
+                    for (int r = 0; r < RP; r += 4) {
+                        const float4 v = *reinterpret_cast<const float4*>(e + r);
+                        s[r] += v.x; s[r + 1] += v.y; s[r + 2] += v.z; s[r + 3] += v.w;
+                    }
+                } else if (RP == 2) {
+                    const float2 v = *reinterpret_cast<const float2*>(e);
+                    s[0] += v.x; s[1] += v.y;
+                } else {
+                    s[0] += e[0];
+                }
+            }
+        }
+        if (a.scores) {
+#pragma unroll
+            for (int r = 0; r < RP; ++r) {
+                if (r < p.rows) {
+                    const int g = r / a.q_len, qi = r - g * a.q_len;
+                    const int h = kv * p.G + g;
+                    a.scores[(int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)qi * a.s_sl + t] = s[r];
+                }
+            }
+        }
+    }
+    // online softmax (wave-local)
+    float alpha[RP];
+    bool rescale = false;
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+        const float tm = wave_max(valid ? s[r] : -INFINITY);
+        const float mn = fmaxf(m_run[r], tm);
+        alpha[r] = (mn == -INFINITY) ? 1.f : __expf(m_run[r] - mn);
+        rescale |= mn != m_run[r];
+        m_run[r] = mn;
+        const float pr = (valid && mn != -INFINITY) ? __expf(s[r] - mn) : 0.f;
+        l_lane[r] = l_lane[r] * alpha[r] + pr;
+        pstrip[r * kTileTok + lane] = (uint16_t)to_vt16<VT>(pr);
+    }
+    if (rescale) {  // wave-uniform
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * (lane >> 4) + i;
+            float f = 1.f;
+#pragma unroll
+            for (int r = 0; r < RP; ++r)
+                if (row == r) f = alpha[r];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) acc[dt][i] *= f;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int arow = lane & 15;
+    const int kchunk = 8 * (lane >> 4);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const int tk = t0 + 32 * g + kchunk;
+        uint4 af = make_uint4(0, 0, 0, 0);
+        if (arow < RP) af = *reinterpret_cast<const uint4*>(pstrip + arow * kTileTok + 32 * g + kchunk);
+        if (tk + 8 > t_end) {  // tail: values of slots past the end are unwritten; zero them
+            const int keep = t_end - tk;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                uint32_t w[4] = {R.v[g][dt].x, R.v[g][dt].y, R.v[g][dt].z, R.v[g][dt].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (j >= keep) w[j >> 1] &= (j & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+                R.v[g][dt] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma<VT>(af, R.v[g][dt], acc[dt]);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+template <int RP, int DT, int VT, int NB>
 __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_decode_args& a = p.a;
@@ -78,7 +250,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     const int split = blockIdx.y;
     const int b = bk / a.num_kv_heads;
     const int kv = bk - b * a.num_kv_heads;
-    const int nb = a.n_blocks, nc = a.n_centroids, D = a.head_dim, bd = a.block_dim;
+    const int D = a.head_dim, bd = a.block_dim;
     const int nr = p.rows;  // <= RP
     const int T = min(a.seq_lens[b], a.seq_len);
     const int t_begin = split * p.split_len;
@@ -87,8 +259,12 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     float* lut = smem;
     float* qp = smem + lut_floats(a, RP);
     uint16_t* pstrip = reinterpret_cast<uint16_t*>(smem + pstrip_offset(a, RP)) + wave * RP * kTileTok;
+    int* pages = reinterpret_cast<int*>(smem + pages_offset(a, RP));
 
-    // ---- scaled, permuted query rows; LUT build
+    // ---- block-table slice, scaled permuted query rows, LUT
+    const int32_t* btab = a.block_table + (int64_t)b * a.bt_sb + t_begin / kPage;
+    const int n_pages = t_end > t_begin ? (t_end - t_begin + kPage - 1) / kPage : 0;
+    for (int i = tid; i < n_pages; i += kThreads) pages[i] = btab[i];
     const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
     for (int e = tid; e < RP * D; e += kThreads) {
         const int r = e / D, j = e - r * D;
@@ -103,8 +279,8 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     }
     __syncthreads();
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
-    for (int e = tid; e < nb * nc; e += kThreads) {
-        const int blk = e / nc;
+    for (int e = tid; e < NB * kNC; e += kThreads) {
+        const int blk = e / kNC;
         const float* c = cent + (int64_t)e * bd;
         float acc[RP];
 #pragma unroll
@@ -125,133 +301,33 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     }
     __syncthreads();
 
-    // ---- stream tiles
+    // ---- stream tiles, two in flight per wave (A/B register sets, no copies)
     float m_run[RP], l_lane[RP];
 #pragma unroll
     for (int r = 0; r < RP; ++r) { m_run[r] = -INFINITY; l_lane[r] = 0.f; }
     v4f acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
-
-    const int32_t* btab = a.block_table + (int64_t)b * a.bt_sb;
     const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)kv * a.v_sh + (int64_t)(lane & 15) * a.v_st;
     const uint8_t* cbase = a.codes + (int64_t)kv * a.c_sh;
     const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
-    const int arow = lane & 15;          // A-operand row (query row) this lane supplies
-    const int kchunk = 8 * (lane >> 4);  // first of the 8 tokens this lane supplies within a 32-token K group
-
-    for (int tile = wave; tile < n_tiles; tile += kWaves) {
-        const int t0 = t_begin + tile * kTileTok;
-        const int t = t0 + lane;
-        const bool valid = t < t_end;
-        // V fragments for the two 32-token K groups (issued first: the long-latency loads)
-        uint4 vf[2][DT];
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            const int tk = t0 + 32 * g + kchunk;
-            if (tk < t_end) {
-                const int page = btab[tk >> 4];
-                const uint16_t* src = vbase + (int64_t)page * a.v_sb + (tk & 15);
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) vf[g][dt] = *reinterpret_cast<const uint4*>(src + (int64_t)(16 * dt) * a.v_st);
-                if (tk + 8 > t_end) {  // tail: zero values of tokens past the end (unwritten slots)
-                    const int keep = t_end - tk;
-#pragma unroll
-                    for (int dt = 0; dt < DT; ++dt) {
-                        uint32_t w[4] = {vf[g][dt].x, vf[g][dt].y, vf[g][dt].z, vf[g][dt].w};
-#pragma unroll
-                        for (int j = 0; j < 8; ++j)
-                            if (j >= keep) w[j >> 1] &= (j & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-                        vf[g][dt] = make_uint4(w[0], w[1], w[2], w[3]);
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) vf[g][dt] = make_uint4(0, 0, 0, 0);
-            }
-        }
-        // scores: one token per lane
-        float s[RP];
-#pragma unroll
-        for (int r = 0; r < RP; ++r) s[r] = 0.f;
-        if (valid) {
-            const int page = btab[t >> 4];
-            const uint32_t* crow = reinterpret_cast<const uint32_t*>(cbase + (int64_t)page * a.c_sb + (int64_t)(t & 15) * a.c_st);
-            for (int w4 = 0; w4 < (nb >> 2); ++w4) {
-                const uint32_t word = crow[w4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const int blk = 4 * w4 + k;
-                    const int code = (word >> (8 * k)) & 0xFF;
-                    const int cc = code < nc ? code : nc - 1;
-                    const float* e = lut + ((size_t)blk * nc + cc) * RP;
-                    if (RP % 4 == 0) {
-#pragma unroll
-                        for (int r = 0; r < RP; r += 4) {
-                            const float4 v = *reinterpret_cast<const float4*>(e + r);
-                            s[r] += v.x; s[r + 1] += v.y; s[r + 2] += v.z; s[r + 3] += v.w;
-                        }
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < RP; ++r) s[r] += e[r];
-                    }
-                }
-            }
-            if (a.scores) {
-#pragma unroll
-                for (int r = 0; r < RP; ++r) {
-                    if (r < nr) {
-                        const int g = r / a.q_len, qi = r - g * a.q_len;
-                        const int h = kv * p.G + g;
-                        a.scores[(int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)qi * a.s_sl + t] = s[r];
-                    }
-                }
-            }
-        }
-        // online softmax (wave-local)
-        float alpha[RP];
-        bool rescale = false;
-#pragma unroll
-        for (int r = 0; r < RP; ++r) {
-            const float tm = ssq_wave_max(valid ? s[r] : -INFINITY);
-            const float mn = fmaxf(m_run[r], tm);
-            alpha[r] = (mn == -INFINITY) ? 1.f : __expf(m_run[r] - mn);
-            rescale |= mn != m_run[r];
-            m_run[r] = mn;
-            const float pr = (valid && mn != -INFINITY) ? __expf(s[r] - mn) : 0.f;
-            l_lane[r] = l_lane[r] * alpha[r] + pr;
-            pstrip[r * kTileTok + lane] = (uint16_t)to_vt16<VT>(pr);
-        }
-        if (rescale) {  // wave-uniform
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = 4 * (lane >> 4) + i;
-                float f = 1.f;
-#pragma unroll
-                for (int r = 0; r < RP; ++r)
-                    if (row == r) f = alpha[r];
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) acc[dt][i] *= f;
-            }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // A fragments: row arow, tokens 32g + kchunk .. +8 of this tile
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            uint4 af = make_uint4(0, 0, 0, 0);
-            if (arow < RP) af = *reinterpret_cast<const uint4*>(pstrip + arow * kTileTok + 32 * g + kchunk);
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma<VT>(af, vf[g][dt], acc[dt]);
-        }
-        __builtin_amdgcn_wave_barrier();
+    TileRegs<NB, DT> RA, RB;
+    int tile = wave;
+    if (tile < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile, lane, cbase, vbase, RA);
+    while (tile < n_tiles) {
+        if (tile + kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + kWaves, lane, cbase, vbase, RB);
+        compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane, acc);
+        tile += kWaves;
+        if (tile >= n_tiles) break;
+        if (tile + kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + kWaves, lane, cbase, vbase, RA);
+        compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RB, m_run, l_lane, acc);
+        tile += kWaves;
     }
 
     // ---- merge the waves' (m, l, O) through LDS (the LUT is no longer needed)
     float l_w[RP];
 #pragma unroll
-    for (int r = 0; r < RP; ++r) l_w[r] = ssq_wave_sum(l_lane[r]);
+    for (int r = 0; r < RP; ++r) l_w[r] = wave_sum(l_lane[r]);
     __syncthreads();
     float* mbuf = smem;                         // [waves][RP]
     float* lbuf = mbuf + kWaves * RP;           // [waves][RP]
@@ -315,15 +391,17 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     if (a->v == nullptr || (a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16)) return false;
     if (a->mask != nullptr || a->heavy_mask[0] || a->heavy_mask[1]) return false;
     if (a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;
-    if (a->n_blocks % 4 != 0 || a->c_st % 4 != 0 || a->c_sb % 4 != 0 || a->c_sh % 4 != 0 || (uintptr_t)a->codes % 4)
-        return false;
+    if (a->n_centroids != kNC) return false;
+    if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32) return false;
+    // code rows: 8-byte (nb 8) or 16-byte (nb >= 16) vector loads
+    const int cal = a->n_blocks >= 16 ? 16 : 8;
+    if (a->c_st % cal != 0 || a->c_sb % cal != 0 || a->c_sh % cal != 0 || (uintptr_t)a->codes % cal) return false;
     if ((uintptr_t)a->v % 16 || (a->v_sb * 2) % 16 || (a->v_sh * 2) % 16 || (a->v_st * 2) % 16) return false;
     const int rows = (a->num_q_heads / a->num_kv_heads) * a->q_len;
     if (rows > 16) return false;
     pl.RP = pow2_at_least(rows);
+    if (pl.RP * a->n_blocks > 128) return false;
     pl.DT = a->value_dim / 16;
-    pl.smem = mfma_smem(*a, pl.RP);
-    if (pl.smem > kMaxSmem) return false;
     const int units = a->batch * a->num_kv_heads;
     const int tiles = (a->seq_len + kTileTok - 1) / kTileTok;
     int splits = a->num_splits > 0 ? a->num_splits : (256 + units - 1) / units;
@@ -334,14 +412,16 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     pl.split_len = tiles_per_split * kTileTok;
     pl.n_splits = (a->seq_len + pl.split_len - 1) / pl.split_len;
     if (pl.n_splits < 1) pl.n_splits = 1;
+    pl.smem = mfma_smem(*a, pl.RP, pl.split_len);
+    if (pl.smem > kMaxSmem) return false;
     const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
     pl.ws_bytes = pl.n_splits > 1 ? (size_t)pl.n_splits * n_rows_all * (a->value_dim + 2) * 4 : 0;
     return true;
 }
 
-template <int RP, int DT, int VT>
+template <int RP, int DT, int VT, int NB>
 int launch(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
-    auto kern = k_decode_mfma<RP, DT, VT>;
+    auto kern = k_decode_mfma<RP, DT, VT, NB>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxSmem);
@@ -353,12 +433,22 @@ int launch(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
     return ssq_check_hip(hipGetLastError(), "k_decode_mfma launch");
 }
 
+template <int RP, int DT, int VT>
+int launch_nb(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
+    switch (mp.a.n_blocks) {
+        case 8: return launch<RP, DT, VT, 8>(mp, pl, st);
+        case 16: if constexpr (RP <= 8) return launch<RP, DT, VT, 16>(mp, pl, st); break;
+        default: if constexpr (RP <= 4) return launch<RP, DT, VT, 32>(mp, pl, st); break;
+    }
+    return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode: LUT of %d rows x %d blocks exceeds LDS", RP, mp.a.n_blocks);
+}
+
 template <int RP, int VT>
 int launch_dt(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
     switch (pl.DT) {
-        case 4: return launch<RP, 4, VT>(mp, pl, st);
-        case 8: return launch<RP, 8, VT>(mp, pl, st);
-        default: return launch<RP, 16, VT>(mp, pl, st);
+        case 4: return launch_nb<RP, 4, VT>(mp, pl, st);
+        case 8: return launch_nb<RP, 8, VT>(mp, pl, st);
+        default: return launch_nb<RP, 16, VT>(mp, pl, st);
     }
 }
 
