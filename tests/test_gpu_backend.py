@@ -103,3 +103,47 @@ def test_bundle_roundtrip_on_gpu_and_runtime_state(tmp_path):
     c2 = rs.codec_for_layer(2)
     keys = torch.randn(100, 64, device=DEV)
     assert torch.equal(c2.quantize(keys).indices, codec.quantize(keys).indices)
+
+
+@pytest.mark.parametrize("mixed", [False, True])
+def test_paged_cache_append_and_decode(mixed):
+    """Prefill + two single-token appends into pages for 3 sequences, then decode (F1)."""
+    from sunshape_amd.paged import PagedSunShapeCache
+
+    log(f"paged cache mixed={mixed}")
+    Hkv, Hq, D, bd = 2, 8, 64, 2
+    if mixed:
+        codec, sigma = _mixed_codec(seed=61)
+    else:
+        cb = synthetic.make_codebook(1, D, bd, 62)
+        codec, sigma = SunShapeBlockCodec.from_buffers(cb.perm[0], cb.centroids[0], device=DEV), cb.sigma[0]
+    cache = PagedSunShapeCache(codec, num_pages=64, num_kv_heads=Hkv, value_dim=D, device=DEV)
+    g = torch.Generator().manual_seed(63)
+    seqs = [5, 9, 2]
+    hist_k = {s: [] for s in seqs}
+    hist_v = {s: [] for s in seqs}
+    for S in (100, 1, 1):
+        k = (torch.randn(3, Hkv, S, D, generator=g) * sigma).to(torch.bfloat16)
+        v = torch.randn(3, Hkv, S, D, generator=g).to(torch.bfloat16)
+        cache.append(seqs, k.to(DEV), v.to(DEV))
+        for i, s in enumerate(seqs):
+            hist_k[s].append(k[i])
+            hist_v[s].append(v[i])
+    q = torch.randn(3, Hq, 1, D, generator=g).to(torch.bfloat16)
+    out = np_of(cache.decode(seqs, q.to(DEV), scale=1 / math.sqrt(D)))
+    heavy = None if codec.heavy_blocks() is None else np.array(codec.heavy_blocks())
+    perm, cent = codec.permutation.cpu().numpy(), codec.centroids.cpu().numpy()
+    for i, s in enumerate(seqs):
+        keys = torch.cat(hist_k[s], dim=1).float().numpy()   # [Hkv, 102, D]
+        vals = torch.cat(hist_v[s], dim=1).float().numpy()
+        codes, pts = [], []
+        for h in range(Hkv):
+            c, pt = O.encode(keys[h], perm, cent, heavy)
+            codes.append(c)
+            pts.append(pt)
+        pt_all = None if heavy is None else O.bf16_round(np.stack(pts))[None]
+        ref = O.decode_attention(q[i:i + 1].float().numpy(), np.stack(codes)[None], vals[None], cent, perm,
+                                 1 / math.sqrt(D), "bf16", "bf16", heavy=heavy, pt_values=pt_all)
+        assert_rel(out[i:i + 1], ref, BF16_TOL, f"seq {s}")
+    cache.free(9)
+    assert 9 not in cache.block_tables
