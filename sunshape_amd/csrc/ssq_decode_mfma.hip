@@ -100,6 +100,27 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// 16-byte load of streamed (read-once) data: non-temporal, so the single pass over
+// the values does not evict the codebooks and block tables other workgroups reuse
+#ifndef SSQ_STREAM_NT
+#define SSQ_STREAM_NT 1
+#endif
+#ifndef SSQ_PIPE_DEPTH
+#define SSQ_PIPE_DEPTH 2  // tiles in flight per wave
+#endif
+#ifndef SSQ_CODES_NT
+#define SSQ_CODES_NT 1
+#endif
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const uint16_t* p) {
+#if SSQ_STREAM_NT
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return *reinterpret_cast<const uint4*>(p);
+#endif
+}
+
 // registers of one 64-token tile in flight
 template <int NB, int DT>
 struct TileRegs {
@@ -118,7 +139,14 @@ __device__ __forceinline__ void issue_tile(const ssq_decode_args& a, const int* 
         const uint8_t* crow = cbase + (int64_t)page * a.c_sb + (int64_t)(t & 15) * a.c_st;
         if (NB >= 16) {
 #pragma unroll
-            for (int i = 0; i < NB / 16; ++i) R.c[i] = reinterpret_cast<const uint4*>(crow)[i];
+            for (int i = 0; i < NB / 16; ++i) {
+#if SSQ_CODES_NT
+                const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(crow) + i);
+                R.c[i] = make_uint4(v.x, v.y, v.z, v.w);
+#else
+                R.c[i] = reinterpret_cast<const uint4*>(crow)[i];
+#endif
+            }
         } else {
             R.c8 = *reinterpret_cast<const uint2*>(crow);
         }
@@ -130,7 +158,7 @@ __device__ __forceinline__ void issue_tile(const ssq_decode_args& a, const int* 
         if (t_begin + r < t_end) {
             const uint16_t* src = vbase + (int64_t)pages[r >> 4] * a.v_sb + (r & 15);
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) R.v[g][dt] = *reinterpret_cast<const uint4*>(src + (int64_t)(16 * dt) * a.v_st);
+            for (int dt = 0; dt < DT; ++dt) R.v[g][dt] = load_stream(src + (int64_t)(16 * dt) * a.v_st);
         }
     }
 }
@@ -278,25 +306,55 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
         qp[e] = v;
     }
     __syncthreads();
+    // the first tile's codes and values are independent of the LUT: put them in flight before building it
+    const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)kv * a.v_sh + (int64_t)(lane & 15) * a.v_st;
+    const uint8_t* cbase = a.codes + (int64_t)kv * a.c_sh;
+    const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
+    TileRegs<NB, DT> RA, RB;
+    int tile = wave;
+    if (tile < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile, lane, cbase, vbase, RA);
+    // LUT: each thread owns entries tid + k*kThreads; codewords are loaded a batch at a time so the
+    // loads overlap instead of each waiting out a full memory latency
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
-    for (int e = tid; e < NB * kNC; e += kThreads) {
-        const int blk = e / kNC;
-        const float* c = cent + (int64_t)e * bd;
-        float acc[RP];
+    constexpr int kBatch = 8;
+    for (int e0 = tid; e0 < NB * kNC; e0 += kBatch * kThreads) {
+        float cw[kBatch][4];
 #pragma unroll
-        for (int r = 0; r < RP; ++r) acc[r] = qp[r * D + blk * bd] * c[0];
-        for (int d = 1; d < bd; ++d) {
-            const float cd = c[d];
+        for (int k = 0; k < kBatch; ++k) {
+            const int e = e0 + k * kThreads;
+            if (e < NB * kNC) {
+                const float* c = cent + (int64_t)e * bd;
+                if (bd == 4) {
+                    const float4 v = *reinterpret_cast<const float4*>(c);
+                    cw[k][0] = v.x; cw[k][1] = v.y; cw[k][2] = v.z; cw[k][3] = v.w;
+                } else {
 #pragma unroll
-            for (int r = 0; r < RP; ++r) acc[r] = fmaf(qp[r * D + blk * bd + d], cd, acc[r]);
+                    for (int d = 0; d < 4; ++d) cw[k][d] = d < bd ? c[d] : 0.f;
+                }
+            }
         }
-        if (RP % 4 == 0) {
 #pragma unroll
-            for (int r = 0; r < RP; r += 4)
-                *reinterpret_cast<float4*>(lut + (size_t)e * RP + r) = make_float4(acc[r], acc[r + 1], acc[r + 2], acc[r + 3]);
-        } else {
+        for (int k = 0; k < kBatch; ++k) {
+            const int e = e0 + k * kThreads;
+            if (e >= NB * kNC) break;
+            const int blk = e / kNC;
+            const float* c = cent + (int64_t)e * bd;
+            float acc[RP];
 #pragma unroll
-            for (int r = 0; r < RP; ++r) lut[(size_t)e * RP + r] = acc[r];
+            for (int r = 0; r < RP; ++r) acc[r] = qp[r * D + blk * bd] * cw[k][0];
+            for (int d = 1; d < bd; ++d) {
+                const float cd = d < 4 ? cw[k][d] : c[d];
+#pragma unroll
+                for (int r = 0; r < RP; ++r) acc[r] = fmaf(qp[r * D + blk * bd + d], cd, acc[r]);
+            }
+            if (RP % 4 == 0) {
+#pragma unroll
+                for (int r = 0; r < RP; r += 4)
+                    *reinterpret_cast<float4*>(lut + (size_t)e * RP + r) = make_float4(acc[r], acc[r + 1], acc[r + 2], acc[r + 3]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < RP; ++r) lut[(size_t)e * RP + r] = acc[r];
+            }
         }
     }
     __syncthreads();
@@ -308,12 +366,23 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     v4f acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
-    const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)kv * a.v_sh + (int64_t)(lane & 15) * a.v_st;
-    const uint8_t* cbase = a.codes + (int64_t)kv * a.c_sh;
-    const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
-    TileRegs<NB, DT> RA, RB;
-    int tile = wave;
-    if (tile < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile, lane, cbase, vbase, RA);
+#if SSQ_PIPE_DEPTH == 3
+    TileRegs<NB, DT> RC;
+    if (tile + kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + kWaves, lane, cbase, vbase, RB);
+    while (tile < n_tiles) {
+        if (tile + 2 * kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + 2 * kWaves, lane, cbase, vbase, RC);
+        compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane, acc);
+        tile += kWaves;
+        if (tile >= n_tiles) break;
+        if (tile + 2 * kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + 2 * kWaves, lane, cbase, vbase, RA);
+        compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RB, m_run, l_lane, acc);
+        tile += kWaves;
+        if (tile >= n_tiles) break;
+        if (tile + 2 * kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + 2 * kWaves, lane, cbase, vbase, RB);
+        compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RC, m_run, l_lane, acc);
+        tile += kWaves;
+    }
+#else
     while (tile < n_tiles) {
         if (tile + kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + kWaves, lane, cbase, vbase, RB);
         compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane, acc);
@@ -323,6 +392,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
         compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RB, m_run, l_lane, acc);
         tile += kWaves;
     }
+#endif
 
     // ---- merge the waves' (m, l, O) through LDS (the LUT is no longer needed)
     float l_w[RP];
@@ -392,6 +462,7 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     if (a->mask != nullptr || a->heavy_mask[0] || a->heavy_mask[1]) return false;
     if (a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;
     if (a->n_centroids != kNC) return false;
+    if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;  // float4 codeword loads
     if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32) return false;
     // code rows: 8-byte (nb 8) or 16-byte (nb >= 16) vector loads
     const int cal = a->n_blocks >= 16 ? 16 : 8;

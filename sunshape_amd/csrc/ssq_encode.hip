@@ -138,95 +138,155 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
 // MFMA screen + exact certification
 // ---------------------------------------------------------------------------
 constexpr int kMfmaWaves = 4;
-constexpr int kRounds = 8;  // key groups of 16 per wave per workgroup
+constexpr int kRounds = 8;        // key groups of 16 per wave per workgroup
+constexpr int kMaxLight = 128;
+constexpr size_t kMfmaSmemCap = 80 * 1024;  // two workgroups per CU (160 KiB LDS)
+
+struct MfmaEncodeParams {
+    ssq_encode_args a;
+    int nbc;                  // light blocks per workgroup chunk
+    int n_light;
+    uint8_t light[kMaxLight]; // light (VQ-coded) block ids, ascending
+};
+
+template <int CTL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTL, 0xF, 0xF, false));
+}
+template <int CTL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTL, 0xF, 0xF, false);
+}
+// reductions over the 16 lanes of a row (every lane of the row receives the result)
+__device__ __forceinline__ float row_min_f(float v) {
+    v = fminf(v, dpp_f<0x121>(v)); v = fminf(v, dpp_f<0x122>(v));
+    v = fminf(v, dpp_f<0x124>(v)); v = fminf(v, dpp_f<0x128>(v));
+    return v;
+}
+__device__ __forceinline__ int row_min_i(int v) {
+    v = min(v, dpp_i<0x121>(v)); v = min(v, dpp_i<0x122>(v));
+    v = min(v, dpp_i<0x124>(v)); v = min(v, dpp_i<0x128>(v));
+    return v;
+}
+__device__ __forceinline__ int row_sum_i(int v) {
+    v += dpp_i<0x121>(v); v += dpp_i<0x122>(v);
+    v += dpp_i<0x124>(v); v += dpp_i<0x128>(v);
+    return v;
+}
+
+inline size_t mfma_enc_smem(const ssq_encode_args& a, int nbc, int KS) {
+    return ((size_t)nbc * KS * 1024 + a.head_dim + (size_t)kMfmaWaves * 16 * (a.head_dim + 1) +
+            (size_t)kMfmaWaves * 16 * nbc) * 4 + (size_t)kMfmaWaves * 16 * a.n_blocks + 64;
+}
 
 template <int KS>
-__global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE) void k_encode_mfma(const EncodeParams p) {
+__global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const MfmaEncodeParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_encode_args& a = p.a;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int bk = blockIdx.y;
     const int b = bk / a.num_kv_heads, kv = bk - b * a.num_kv_heads;
-    const int blk0 = blockIdx.z * p.nbc;
-    const int nbc = min(p.nbc, a.n_blocks - blk0);
+    const int chunk = blockIdx.z;
+    const int l0 = chunk * p.nbc;
+    const int nbc = min(p.nbc, p.n_light - l0);
     const int bd = a.block_dim, D = a.head_dim, nb = a.n_blocks;
-    const int XS = D + 1;  // padded row stride of the per-wave key scratch
+    const int XS = D + 1;
     const uint64_t hm0 = a.heavy_mask[0], hm1 = a.heavy_mask[1];
+    const bool do_heavy = chunk == 0 && (hm0 | hm1);
 
-    // LDS: bsw [nbc][KS][16][64] | cnmax [nbc] | xs [waves][16][XS] | xn [waves][16][nb] | codes [waves][16][nbc]
+    // LDS: bsw [nbc][KS][16][64] | perm [D] | xs [waves][16][XS] | xn [waves][16][nbc] | codes [waves][16][nb]
     float* bsw = smem;
-    float* cnmax = bsw + (size_t)nbc * KS * 16 * 64;
-    float* xs_all = cnmax + nbc;
-    float* xn_all = xs_all + kMfmaWaves * 16 * XS;
-    uint8_t* codes_all = reinterpret_cast<uint8_t*>(xn_all + kMfmaWaves * 16 * nb);
+    int* perm_l = reinterpret_cast<int*>(bsw + (size_t)nbc * KS * 1024);
+    float* xs = reinterpret_cast<float*>(perm_l + D) + wave * 16 * XS;
+    float* xn = reinterpret_cast<float*>(perm_l + D) + kMfmaWaves * 16 * XS + wave * 16 * nbc;
+    uint8_t* cs = reinterpret_cast<uint8_t*>(reinterpret_cast<float*>(perm_l + D) + kMfmaWaves * 16 * XS +
+                                             kMfmaWaves * 16 * nbc) + wave * 16 * nb;
 
-    // B operands in lane order: bsw[bl][s][nt][l] = Baug[k = 4s + l/16][n = 16nt + l%16]
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
-    for (int e = threadIdx.x; e < nbc * KS * 16 * 64; e += kMfmaWaves * SSQ_WAVE) {
+    const int64_t* perm_g = a.perm + (int64_t)kv * a.perm_sh;
+    for (int j = threadIdx.x; j < D; j += kMfmaWaves * SSQ_WAVE) perm_l[j] = (int)perm_g[j];
+    // B operands in lane order: bsw[bl][s][nt][l] = [c, 1, |c|^2, 0..][k = 4s + l/16] of codeword 16nt + l%16
+    for (int e = threadIdx.x; e < nbc * KS * 1024; e += kMfmaWaves * SSQ_WAVE) {
         const int l = e & 63;
         const int nt = (e >> 6) & 15;
         const int s = (e >> 10) % KS;
         const int bl = e / (KS * 1024);
-        const int blk = blk0 + bl;
+        const int blk = p.light[l0 + bl];
         const int k = 4 * s + (l >> 4);
-        const int n = 16 * nt + (l & 15);
-        const float* c = cent + ((int64_t)blk * 256 + n) * bd;
-        float v;
-        if (k < bd) v = c[k];
-        else if (k == bd) v = 1.0f;
-        else if (k == bd + 1) v = sq_norm(c, bd);
-        else v = 0.0f;
-        bsw[e] = v;
+        const float* c = cent + ((int64_t)blk * 256 + 16 * nt + (l & 15)) * bd;
+        bsw[e] = k < bd ? c[k] : k == bd ? 1.0f : k == bd + 1 ? sq_norm(c, bd) : 0.0f;
     }
     __syncthreads();
-    for (int bl = threadIdx.x; bl < nbc; bl += kMfmaWaves * SSQ_WAVE) {
-        float m = 0.f;
-        const float* c = cent + (int64_t)(blk0 + bl) * 256 * bd;
-        for (int n = 0; n < 256; ++n) m = fmaxf(m, sq_norm(c + n * bd, bd));
-        cnmax[bl] = m;
-    }
 
-    float* xs = xs_all + wave * 16 * XS;
-    float* xn = xn_all + wave * 16 * nb;
-    uint8_t* cs = codes_all + wave * 16 * nbc;
-    const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
+    // key rows: lane (m = l/4, quarter q = l%4) loads elements [q*D/4, (q+1)*D/4) of row m
+    const int esz = a.k_dtype == SSQ_F32 ? 4 : 2;
+    const bool vec = (D % 32 == 0) && ((a.k_ss * esz) % 16 == 0) && ((a.k_sh * esz) % 16 == 0) &&
+                     ((a.k_sb * esz) % 16 == 0) && ((uintptr_t)a.keys % 16 == 0) && esz == 2;
+    const int lm = lane >> 2, lq = lane & 3;
     const int s_wg = blockIdx.x * (kMfmaWaves * kRounds * 16);
+    const int64_t krow0 = (int64_t)b * a.k_sb + (int64_t)kv * a.k_sh;
+    uint4 pre[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    auto fetch = [&](int round) {  // vector path: 16 bf16 (D=64) or the first 32 of a longer row quarter
+        const int s = s_wg + (round * kMfmaWaves + wave) * 16 + lm;
+        if (vec && s < a.seq_len && D == 64) {
+            const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.keys) + krow0 +
+                                                              (int64_t)s * a.k_ss + lq * 16);
+            pre[0] = src[0];
+            pre[1] = src[1];
+        }
+    };
+    fetch(0);
+    const int lane16 = lane & 15;
+    const int mrow = 4 * (lane >> 4);
 
     for (int round = 0; round < kRounds; ++round) {
         const int s0 = s_wg + (round * kMfmaWaves + wave) * 16;
-        // stage 16 keys (permuted, fp32) and their block norms
-        for (int e = lane; e < 16 * D; e += 64) {
-            const int m = e / D, j = e - m * D;
-            const int s = s0 + m;
-            float v = 0.f;
-            if (s < a.seq_len)
-                v = ssq_load_elem(a.keys, a.k_dtype,
-                                  (int64_t)b * a.k_sb + (int64_t)kv * a.k_sh + (int64_t)s * a.k_ss + perm[j]);
-            xs[m * XS + j] = v;
+        if (s0 >= a.seq_len) break;  // wave-uniform
+        // stage this round's 16 rows (unpermuted, fp32) into xs
+        if (vec && D == 64) {
+            const uint32_t w[8] = {pre[0].x, pre[0].y, pre[0].z, pre[0].w, pre[1].x, pre[1].y, pre[1].z, pre[1].w};
+            float* dst = xs + lm * XS + lq * 16;
+            const bool ok = s0 + lm < a.seq_len;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float lo = a.k_dtype == SSQ_BF16 ? __uint_as_float(w[i] << 16) : ssq_f16_to_f32(w[i] & 0xFFFFu);
+                const float hi = a.k_dtype == SSQ_BF16 ? __uint_as_float(w[i] & 0xFFFF0000u) : ssq_f16_to_f32(w[i] >> 16);
+                dst[2 * i] = ok ? lo : 0.f;
+                dst[2 * i + 1] = ok ? hi : 0.f;
+            }
+            fetch(round + 1 < kRounds ? round + 1 : round);
+        } else {
+            for (int e = lane; e < 16 * D; e += 64) {
+                const int m = e / D, j = e - m * D;
+                const int s = s0 + m;
+                xs[m * XS + j] = s < a.seq_len ? ssq_load_elem(a.keys, a.k_dtype, krow0 + (int64_t)s * a.k_ss + j) : 0.f;
+            }
         }
-        __syncthreads();
-        for (int e = lane; e < 16 * nb; e += 64) {
-            const int m = e / nb, blk = e - m * nb;
-            xn[e] = sq_norm(xs + m * XS + blk * bd, bd);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // block norms of the permuted rows: xn[m][bl]
+        for (int e = lane; e < 16 * nbc; e += 64) {
+            const int m = e / nbc, bl = e - m * nbc;
+            const int blk = p.light[l0 + bl];
+            float x[16];
+            for (int d = 0; d < bd; ++d) x[d] = xs[m * XS + perm_l[blk * bd + d]];
+            xn[e] = sq_norm(x, bd);
         }
-        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
         for (int bl = 0; bl < nbc; ++bl) {
-            const int blk = blk0 + bl;
-            if (ssq_is_heavy(hm0, hm1, blk)) {
-                if (lane < 16) cs[lane * nbc + bl] = 0;
-                continue;
-            }
-            // A operand: lane (m = l%16, k = 4s + l/16) holds [-2x, xn, 1, 0...][k]
-            const int am = lane & 15;
+            const int blk = p.light[l0 + bl];
             float av[KS];
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
                 const int k = 4 * s + (lane >> 4);
                 float v;
-                if (k < bd) v = -2.0f * xs[am * XS + blk * bd + k];
-                else if (k == bd) v = xn[am * nb + blk];
+                if (k < bd) v = -2.0f * xs[lane16 * XS + perm_l[blk * bd + k]];
+                else if (k == bd) v = xn[lane16 * nbc + bl];
                 else if (k == bd + 1) v = 1.0f;
                 else v = 0.0f;
                 av[s] = v;
@@ -241,91 +301,120 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE) void k_encode_mfma(const Enc
                     c = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bb[(s * 16 + nt) * 64 + lane], c, 0, 0, 0);
                 acc[nt] = c;
             }
-            // lane holds d2[m = 4*(l/16) + i][n = 16*nt + l%16]
-            float mn[4];
+            // lane holds d2[key 4*(l/16)+i][codeword 16*nt + l%16]
+            float thr[4];
+            int first[4], cnt[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float v = acc[0][i];
 #pragma unroll
                 for (int nt = 1; nt < 16; ++nt) v = fminf(v, acc[nt][i]);
-#pragma unroll
-                for (int o = 1; o < 16; o <<= 1) v = fminf(v, __shfl_xor(v, o, 64));
-                mn[i] = v;
+                const float mn = row_min_f(v);
+                // Error bound (gamma = 2^-19 >= 2 * 12u covers any rounding order, even truncation, of the
+                // <= 12-term sum): |value_j - |x-c_j|^2| <= gamma * (|x| + |c_j|)^2 by Cauchy-Schwarz, and a
+                // codeword that can win has |c_j| <= |x| + sqrt(|x-c_j|^2) with |x-c_j|^2 <= max(mn,0) + 1,
+                // so every relevant error is <= err = 2^-16*|x|^2 + 2^-18*(max(mn,0) + 1) (with slack).
+                // The exact winner j* has d(j*) <= d(argmin) and sqrt merges values <= 2^-21 apart, hence
+                // value_j*(MFMA) <= max(mn,0)*(1 + 2^-21) + 4*err: every codeword under thr is a candidate.
+                const float xnv = xn[(mrow + i) * nbc + bl];
+                const float mp = fmaxf(mn, 0.f);
+                const float err = 0x1.04p-16f * xnv + 0x1.0p-18f * (mp + 1.0f);
+                thr[i] = mp * (1.0f + 0x1.0p-20f) + 5.0f * err + 0x1.0p-100f;
+                first[i] = 16;
+                cnt[i] = 0;
             }
-            // Any fp32 evaluation of the K <= 12 term sum (by the MFMA or the exact chain)
-            // is within 12*2u*(sum |terms|) <= 50u*(xn + cn) of the real value; eps uses 256u.
-            // The exact winner's MFMA value is <= min + 3 eps + 2^-21 (min + eps).
-            float thr[4];
-            const int mrow = 4 * (lane >> 4);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float eps = 0x1.0p-16f * (xn[(mrow + i) * nb + blk] + cnmax[bl]) + 0x1.0p-100f;
-                thr[i] = mn[i] + 4.0f * eps + 0x1.0p-20f * fabsf(mn[i]);
-            }
-            float bf[4];
-            int bn[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { bf[i] = INFINITY; bn[i] = 256; }
-#pragma unroll
-            for (int nt = 0; nt < 16; ++nt) {
+            for (int nt = 15; nt >= 0; --nt) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    if (acc[nt][i] <= thr[i]) {
-                        const int m = mrow + i;
-                        const int n = 16 * nt + (lane & 15);
-                        float x[12], c[12];
-                        for (int d = 0; d < bd; ++d) {
-                            x[d] = xs[m * XS + blk * bd + d];
-                            const int k = d;
-                            c[d] = bb[((k >> 2) * 16 + nt) * 64 + (k & 3) * 16 + (lane & 15)];
-                        }
-                        const int kc = bd + 1;
-                        const float cnv = bb[((kc >> 2) * 16 + nt) * 64 + (kc & 3) * 16 + (lane & 15)];
-                        const float f = dist_of(mm_dist2(x, xn[m * nb + blk], c, cnv, bd));
-                        if (f < bf[i] || (f == bf[i] && n < bn[i])) { bf[i] = f; bn[i] = n; }
-                    }
+                    const bool c = acc[nt][i] <= thr[i];
+                    first[i] = c ? nt : first[i];
+                    cnt[i] += c ? 1 : 0;
                 }
             }
+            int code[4];
+            bool slow = false;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                const int total = row_sum_i(cnt[i]);
+                code[i] = row_min_i(first[i] < 16 ? 16 * first[i] + lane16 : 4096);
+                slow |= total != 1;
+            }
+            if (__builtin_amdgcn_ballot_w64(slow)) {  // rare: several candidates -> exact arithmetic decides
 #pragma unroll
-                for (int o = 1; o < 16; o <<= 1) {
-                    const float of = __shfl_xor(bf[i], o, 64);
-                    const int on = __shfl_xor(bn[i], o, 64);
-                    if (of < bf[i] || (of == bf[i] && on < bn[i])) { bf[i] = of; bn[i] = on; }
+                for (int i = 0; i < 4; ++i) {
+                    const int total = row_sum_i(cnt[i]);
+                    float bf = INFINITY;
+                    int bn = 4096;
+                    if (total != 1) {
+                        const int m = mrow + i;
+                        float x[12], c[12];
+                        for (int d = 0; d < bd; ++d) x[d] = xs[m * XS + perm_l[blk * bd + d]];
+                        for (int nt = 0; nt < 16; ++nt) {
+                            if (acc[nt][i] <= thr[i]) {
+                                for (int d = 0; d < bd; ++d) c[d] = bb[((d >> 2) * 16 + nt) * 64 + (d & 3) * 16 + lane16];
+                                const int kc = bd + 1;
+                                const float cnv = bb[((kc >> 2) * 16 + nt) * 64 + (kc & 3) * 16 + lane16];
+                                const float f = dist_of(mm_dist2(x, xn[m * nbc + bl], c, cnv, bd));
+                                const int n = 16 * nt + lane16;
+                                if (f < bf || (f == bf && n < bn)) { bf = f; bn = n; }
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int o = 0; o < 4; ++o) {
+                        float of;
+                        int on;
+                        switch (o) {
+                            case 0: of = dpp_f<0x121>(bf); on = dpp_i<0x121>(bn); break;
+                            case 1: of = dpp_f<0x122>(bf); on = dpp_i<0x122>(bn); break;
+                            case 2: of = dpp_f<0x124>(bf); on = dpp_i<0x124>(bn); break;
+                            default: of = dpp_f<0x128>(bf); on = dpp_i<0x128>(bn); break;
+                        }
+                        if (of < bf || (of == bf && on < bn)) { bf = of; bn = on; }
+                    }
+                    if (total != 1) code[i] = bn;
                 }
             }
-            if ((lane & 15) == 0) {
+            if (lane16 == 0) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) cs[(mrow + i) * nbc + bl] = (uint8_t)bn[i];
+                for (int i = 0; i < 4; ++i) cs[(mrow + i) * nb + blk] = (uint8_t)code[i];
             }
         }
-        __syncthreads();
-        // write codes (and passthrough values) for the 16 keys of this round
-        for (int e = lane; e < 16 * nbc; e += 64) {
-            const int m = e / nbc, bl = e - m * nbc;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // write this round's codes (and, in chunk 0, the heavy blocks' code 0 + passthrough values)
+        for (int e = lane; e < 16 * nb; e += 64) {
+            const int m = e / nb, blk = e - m * nb;
             const int s = s0 + m;
             if (s >= a.seq_len) continue;
-            const int blk = blk0 + bl;
+            const bool heavy = ssq_is_heavy(hm0, hm1, blk);
+            bool mine = false;
+            if (heavy) {
+                mine = do_heavy;
+            } else {
+                for (int bl = 0; bl < nbc; ++bl) mine |= p.light[l0 + bl] == blk;
+            }
+            if (!mine) continue;
             int64_t crow, prow;
             out_rows(a, b, kv, s, crow, prow);
-            a.codes[crow + blk] = cs[e];
-            if (ssq_is_heavy(hm0, hm1, blk)) {
+            if (heavy) {
+                a.codes[crow + blk] = 0;
                 const int slot = a.pt_dense ? blk : heavy_ordinal(hm0, hm1, blk);
                 for (int d = 0; d < bd; ++d)
-                    ssq_store_elem(a.pt, a.pt_dtype, prow + (int64_t)slot * bd + d, xs[m * XS + blk * bd + d]);
+                    ssq_store_elem(a.pt, a.pt_dtype, prow + (int64_t)slot * bd + d, xs[m * XS + perm_l[blk * bd + d]]);
+            } else {
+                a.codes[crow + blk] = cs[e];
             }
         }
-        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
 constexpr size_t kMaxSmem = 160 * 1024;
-
-size_t mfma_smem(const ssq_encode_args& a, int nbc, int KS) {
-    return ((size_t)nbc * KS * 1024 + nbc + (size_t)kMfmaWaves * 16 * (a.head_dim + 1) +
-            (size_t)kMfmaWaves * 16 * a.n_blocks) * 4 + (size_t)kMfmaWaves * 16 * nbc + 16;
-}
 
 template <typename K>
 int set_smem_attr(K kern, bool& done) {
@@ -362,21 +451,33 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
     const int kernel = a->kernel == 0 ? (mfma_ok ? 2 : 1) : a->kernel;
     if (kernel == 2) {
         SSQ_UNSUPPORTED(mfma_ok, "MFMA encode needs n_centroids == 256 and block_dim <= 10");
-        int nbc = a->n_blocks;
-        while (nbc > 1 && mfma_smem(*a, nbc, KS) > kMaxSmem) --nbc;
-        SSQ_UNSUPPORTED(mfma_smem(*a, nbc, KS) <= kMaxSmem, "head_dim too large for the MFMA encode");
-        p.nbc = nbc;
+        MfmaEncodeParams mp;
+        mp.a = *a;
+        mp.n_light = 0;
+        for (int blk = 0; blk < a->n_blocks; ++blk) {
+            const bool heavy = blk < 64 ? ((a->heavy_mask[0] >> blk) & 1) : ((a->heavy_mask[1] >> (blk - 64)) & 1);
+            if (!heavy) mp.light[mp.n_light++] = (uint8_t)blk;
+        }
+        int nbc = mp.n_light > 0 ? mp.n_light : 1;
+        while (nbc > 1 && mfma_enc_smem(*a, nbc, KS) > kMfmaSmemCap) --nbc;
+        if (mp.n_light > 0) {  // balance the chunks
+            const int chunks0 = (mp.n_light + nbc - 1) / nbc;
+            nbc = (mp.n_light + chunks0 - 1) / chunks0;
+        }
+        SSQ_UNSUPPORTED(mfma_enc_smem(*a, nbc, KS) <= kMaxSmem, "head_dim too large for the MFMA encode");
+        mp.nbc = nbc;
+        const int chunks = mp.n_light > 0 ? (mp.n_light + nbc - 1) / nbc : 1;
         const int keys_wg = kMfmaWaves * kRounds * 16;
-        dim3 grid((a->seq_len + keys_wg - 1) / keys_wg, a->batch * a->num_kv_heads, (a->n_blocks + nbc - 1) / nbc);
-        const size_t smem = mfma_smem(*a, nbc, KS);
+        dim3 grid((a->seq_len + keys_wg - 1) / keys_wg, a->batch * a->num_kv_heads, chunks);
+        const size_t smem = mfma_enc_smem(*a, nbc, KS);
         int rc;
         switch (KS) {
             case 1: { static bool d = false; rc = set_smem_attr(k_encode_mfma<1>, d); if (rc) return rc;
-                      hipLaunchKernelGGL(k_encode_mfma<1>, grid, dim3(kMfmaWaves * SSQ_WAVE), smem, st, p); break; }
+                      hipLaunchKernelGGL(k_encode_mfma<1>, grid, dim3(kMfmaWaves * SSQ_WAVE), smem, st, mp); break; }
             case 2: { static bool d = false; rc = set_smem_attr(k_encode_mfma<2>, d); if (rc) return rc;
-                      hipLaunchKernelGGL(k_encode_mfma<2>, grid, dim3(kMfmaWaves * SSQ_WAVE), smem, st, p); break; }
+                      hipLaunchKernelGGL(k_encode_mfma<2>, grid, dim3(kMfmaWaves * SSQ_WAVE), smem, st, mp); break; }
             default: { static bool d = false; rc = set_smem_attr(k_encode_mfma<3>, d); if (rc) return rc;
-                       hipLaunchKernelGGL(k_encode_mfma<3>, grid, dim3(kMfmaWaves * SSQ_WAVE), smem, st, p); break; }
+                       hipLaunchKernelGGL(k_encode_mfma<3>, grid, dim3(kMfmaWaves * SSQ_WAVE), smem, st, mp); break; }
         }
         return ssq_check_hip(hipGetLastError(), "k_encode_mfma launch");
     }
