@@ -17,6 +17,7 @@
 #include "ssq_common.h"
 
 #include <math.h>
+#include <string.h>
 
 namespace {
 
@@ -137,6 +138,9 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
 // ---------------------------------------------------------------------------
 // MFMA screen + exact certification
 // ---------------------------------------------------------------------------
+#ifndef SSQ_ENC_PIPE
+#define SSQ_ENC_PIPE 0  // 1: MFMAs of the next block issued before the current block's reductions
+#endif
 constexpr int kMfmaWaves = 4;
 constexpr int kRounds = 8;        // key groups of 16 per wave per workgroup
 constexpr int kMaxLight = 128;
@@ -173,9 +177,122 @@ __device__ __forceinline__ int row_sum_i(int v) {
     v += dpp_i<0x124>(v); v += dpp_i<0x128>(v);
     return v;
 }
+// one step of a row-wide lexicographic (value, index) minimum
+template <int CTL>
+__device__ __forceinline__ void lexmin_step(float& bf, int& bn) {
+    const float of = dpp_f<CTL>(bf);
+    const int on = dpp_i<CTL>(bn);
+    if (of < bf || (of == bf && on < bn)) { bf = of; bn = on; }
+}
+
+
+// A/B operands of one light block and its 16 MFMA tiles: acc[nt] holds d2[key 4*(l/16)+i][codeword 16nt + l%16]
+template <int KS>
+__device__ __forceinline__ void issue_block(const float* bsw, const float* xs, const float* xn, const int* poff,
+                                            int bl, int nbc, int bd, int XS, int lane, int lane16, v4f (&acc)[16]) {
+    float av[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const int k = 4 * s + (lane >> 4);
+        float v;
+        if (k < bd) v = -2.0f * xs[lane16 * XS + poff[bl * bd + k]];
+        else if (k == bd) v = xn[lane16 * nbc + bl];
+        else if (k == bd + 1) v = 1.0f;
+        else v = 0.0f;
+        av[s] = v;
+    }
+    const float* bb = bsw + (size_t)bl * KS * 1024;
+#pragma unroll
+    for (int nt = 0; nt < 16; ++nt) {
+        v4f c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bb[(s * 16 + nt) * 64 + lane], c, 0, 0, 0);
+        acc[nt] = c;
+    }
+}
+
+// first-argmin of sqrt(max(d2,0)) for the 16 keys of the wave in one light block; codes -> cs[key][blk]
+template <int KS>
+__device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, const float* xn, const int* poff,
+                                             const int* lightL, int bl, int nbc, int nb, int bd, int XS,
+                                             int lane16, int mrow, const v4f (&acc)[16], uint8_t* cs) {
+    float thr[4];
+    int first[4], cnt[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float v = acc[0][i];
+#pragma unroll
+        for (int nt = 1; nt < 16; ++nt) v = fminf(v, acc[nt][i]);
+        const float mn = row_min_f(v);
+        // Error bound.  gamma = 2^-19 >= 2 * 12u covers any rounding order (even truncation) of the
+        // <= 12-term sum, so |value_j - |x-c_j|^2| <= gamma * (|x| + |c_j|)^2 (Cauchy-Schwarz), with
+        // |c_j| <= |x| + |x-c_j|.  Every codeword that can matter has |x-c_j|^2 <= Y =
+        // 1.01*max(mn,0) + 64*gamma*|x|^2 (self-consistent because 12*gamma << 0.01), so its error is
+        // <= err = 8*gamma*|x|^2 + 2*gamma*Y <= 2^-16*|x|^2*1.02 + 2^-18*max(mn,0)*1.02 (+ underflow).
+        // The exact winner j* has d(j*) <= d(argmin) and sqrt merges values <= 2^-21 apart, hence
+        // value_j*(MFMA) <= max(mn,0)*(1 + 2^-21) + 4*err: every codeword under thr is a candidate.
+        const float xnv = xn[(mrow + i) * nbc + bl];
+        const float mp = fmaxf(mn, 0.f);
+        const float err = 0x1.06p-16f * xnv + 0x1.06p-18f * mp;
+        thr[i] = mp * (1.0f + 0x1.0p-20f) + 5.0f * err + 0x1.0p-100f;
+        first[i] = 16;
+        cnt[i] = 0;
+    }
+#pragma unroll
+    for (int nt = 15; nt >= 0; --nt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool c = acc[nt][i] <= thr[i];
+            first[i] = c ? nt : first[i];
+            cnt[i] += c ? 1 : 0;
+        }
+    }
+    int code[4], total[4];
+    bool slow = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        total[i] = row_sum_i(cnt[i]);
+        code[i] = row_min_i(first[i] < 16 ? 16 * first[i] + lane16 : 4096);
+        slow |= total[i] != 1;
+    }
+    if (__builtin_amdgcn_ballot_w64(slow)) {  // rare: several candidates -> exact arithmetic decides
+        const float* bb = bsw + (size_t)bl * KS * 1024;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float bf = INFINITY;
+            int bn = 4096;
+            if (total[i] != 1) {
+                const int m = mrow + i;
+                float x[12], c[12];
+                for (int d = 0; d < bd; ++d) x[d] = xs[m * XS + poff[bl * bd + d]];
+                for (int nt = 0; nt < 16; ++nt) {
+                    if (acc[nt][i] <= thr[i]) {
+                        for (int d = 0; d < bd; ++d) c[d] = bb[((d >> 2) * 16 + nt) * 64 + (d & 3) * 16 + lane16];
+                        const int kc = bd + 1;
+                        const float cnv = bb[((kc >> 2) * 16 + nt) * 64 + (kc & 3) * 16 + lane16];
+                        const float f = dist_of(mm_dist2(x, xn[m * nbc + bl], c, cnv, bd));
+                        const int n = 16 * nt + lane16;
+                        if (f < bf || (f == bf && n < bn)) { bf = f; bn = n; }
+                    }
+                }
+            }
+            lexmin_step<0x121>(bf, bn);
+            lexmin_step<0x122>(bf, bn);
+            lexmin_step<0x124>(bf, bn);
+            lexmin_step<0x128>(bf, bn);
+            if (total[i] != 1) code[i] = bn;
+        }
+    }
+    if (lane16 == 0) {
+        const int blk = lightL[bl];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cs[(mrow + i) * nb + blk] = (uint8_t)code[i];
+    }
+}
 
 inline size_t mfma_enc_smem(const ssq_encode_args& a, int nbc, int KS) {
-    return ((size_t)nbc * KS * 1024 + a.head_dim + (size_t)kMfmaWaves * 16 * (a.head_dim + 1) +
+    return ((size_t)nbc * KS * 1024 + a.head_dim + (size_t)nbc * (a.block_dim + 1) + (size_t)kMfmaWaves * 16 * (a.head_dim + 1) +
             (size_t)kMfmaWaves * 16 * nbc) * 4 + (size_t)kMfmaWaves * 16 * a.n_blocks + 64;
 }
 
@@ -194,18 +311,33 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
     const int XS = D + 1;
     const uint64_t hm0 = a.heavy_mask[0], hm1 = a.heavy_mask[1];
     const bool do_heavy = chunk == 0 && (hm0 | hm1);
+    uint64_t cm0 = 0, cm1 = 0;  // light blocks of this chunk
+    for (int bl = 0; bl < nbc; ++bl) {
+        const int blk = p.light[l0 + bl];
+        if (blk < 64) cm0 |= 1ull << blk; else cm1 |= 1ull << (blk - 64);
+    }
+    const int lo_blk = nbc > 0 ? p.light[l0] : 0;
+    const int hi_blk = nbc > 0 ? p.light[l0 + nbc - 1] : -1;
 
-    // LDS: bsw [nbc][KS][16][64] | perm [D] | xs [waves][16][XS] | xn [waves][16][nbc] | codes [waves][16][nb]
+    // LDS: bsw [nbc][KS][16][64] | perm [D] | poff [nbc*bd] | lightL [nbc] | xs [waves][16][XS] |
+    //      xn [waves][16][nbc] | codes [waves][16][nb]
     float* bsw = smem;
     int* perm_l = reinterpret_cast<int*>(bsw + (size_t)nbc * KS * 1024);
-    float* xs = reinterpret_cast<float*>(perm_l + D) + wave * 16 * XS;
-    float* xn = reinterpret_cast<float*>(perm_l + D) + kMfmaWaves * 16 * XS + wave * 16 * nbc;
-    uint8_t* cs = reinterpret_cast<uint8_t*>(reinterpret_cast<float*>(perm_l + D) + kMfmaWaves * 16 * XS +
-                                             kMfmaWaves * 16 * nbc) + wave * 16 * nb;
+    int* poff = perm_l + D;         // poff[bl*bd + d] = perm[light[bl]*bd + d]: the block's dims in the key row
+    int* lightL = poff + nbc * bd;  // light block ids of this chunk
+    float* xs_all = reinterpret_cast<float*>(lightL + nbc);
+    float* xs = xs_all + wave * 16 * XS;
+    float* xn = xs_all + kMfmaWaves * 16 * XS + wave * 16 * nbc;
+    uint8_t* cs = reinterpret_cast<uint8_t*>(xs_all + kMfmaWaves * 16 * XS + kMfmaWaves * 16 * nbc) + wave * 16 * nb;
 
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
     const int64_t* perm_g = a.perm + (int64_t)kv * a.perm_sh;
     for (int j = threadIdx.x; j < D; j += kMfmaWaves * SSQ_WAVE) perm_l[j] = (int)perm_g[j];
+    for (int j = threadIdx.x; j < nbc * bd; j += kMfmaWaves * SSQ_WAVE) {
+        const int bl = j / bd, d = j - bl * bd;
+        poff[j] = (int)perm_g[p.light[l0 + bl] * bd + d];
+    }
+    for (int bl = threadIdx.x; bl < nbc; bl += kMfmaWaves * SSQ_WAVE) lightL[bl] = p.light[l0 + bl];
     // B operands in lane order: bsw[bl][s][nt][l] = [c, 1, |c|^2, 0..][k = 4s + l/16] of codeword 16nt + l%16
     for (int e = threadIdx.x; e < nbc * KS * 1024; e += kMfmaWaves * SSQ_WAVE) {
         const int l = e & 63;
@@ -266,146 +398,58 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // block norms of the permuted rows: xn[m][bl]
-        for (int e = lane; e < 16 * nbc; e += 64) {
-            const int m = e / nbc, bl = e - m * nbc;
-            const int blk = p.light[l0 + bl];
+        // block norms of the permuted rows: xn[m][bl]  (lane: key m = lane & 15, blocks lane/16 + 4k)
+        for (int bl = lane >> 4; bl < nbc; bl += 4) {
             float x[16];
-            for (int d = 0; d < bd; ++d) x[d] = xs[m * XS + perm_l[blk * bd + d]];
-            xn[e] = sq_norm(x, bd);
+            for (int d = 0; d < bd; ++d) x[d] = xs[lane16 * XS + poff[bl * bd + d]];
+            xn[lane16 * nbc + bl] = sq_norm(x, bd);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-        for (int bl = 0; bl < nbc; ++bl) {
-            const int blk = p.light[l0 + bl];
-            float av[KS];
-#pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                const int k = 4 * s + (lane >> 4);
-                float v;
-                if (k < bd) v = -2.0f * xs[lane16 * XS + perm_l[blk * bd + k]];
-                else if (k == bd) v = xn[lane16 * nbc + bl];
-                else if (k == bd + 1) v = 1.0f;
-                else v = 0.0f;
-                av[s] = v;
-            }
-            const float* bb = bsw + (size_t)bl * KS * 1024;
-            v4f acc[16];
-#pragma unroll
-            for (int nt = 0; nt < 16; ++nt) {
-                v4f c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int s = 0; s < KS; ++s)
-                    c = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bb[(s * 16 + nt) * 64 + lane], c, 0, 0, 0);
-                acc[nt] = c;
-            }
-            // lane holds d2[key 4*(l/16)+i][codeword 16*nt + l%16]
-            float thr[4];
-            int first[4], cnt[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float v = acc[0][i];
-#pragma unroll
-                for (int nt = 1; nt < 16; ++nt) v = fminf(v, acc[nt][i]);
-                const float mn = row_min_f(v);
-                // Error bound (gamma = 2^-19 >= 2 * 12u covers any rounding order, even truncation, of the
-                // <= 12-term sum): |value_j - |x-c_j|^2| <= gamma * (|x| + |c_j|)^2 by Cauchy-Schwarz, and a
-                // codeword that can win has |c_j| <= |x| + sqrt(|x-c_j|^2) with |x-c_j|^2 <= max(mn,0) + 1,
-                // so every relevant error is <= err = 2^-16*|x|^2 + 2^-18*(max(mn,0) + 1) (with slack).
-                // The exact winner j* has d(j*) <= d(argmin) and sqrt merges values <= 2^-21 apart, hence
-                // value_j*(MFMA) <= max(mn,0)*(1 + 2^-21) + 4*err: every codeword under thr is a candidate.
-                const float xnv = xn[(mrow + i) * nbc + bl];
-                const float mp = fmaxf(mn, 0.f);
-                const float err = 0x1.04p-16f * xnv + 0x1.0p-18f * (mp + 1.0f);
-                thr[i] = mp * (1.0f + 0x1.0p-20f) + 5.0f * err + 0x1.0p-100f;
-                first[i] = 16;
-                cnt[i] = 0;
-            }
-#pragma unroll
-            for (int nt = 15; nt >= 0; --nt) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bool c = acc[nt][i] <= thr[i];
-                    first[i] = c ? nt : first[i];
-                    cnt[i] += c ? 1 : 0;
-                }
-            }
-            int code[4];
-            bool slow = false;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int total = row_sum_i(cnt[i]);
-                code[i] = row_min_i(first[i] < 16 ? 16 * first[i] + lane16 : 4096);
-                slow |= total != 1;
-            }
-            if (__builtin_amdgcn_ballot_w64(slow)) {  // rare: several candidates -> exact arithmetic decides
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int total = row_sum_i(cnt[i]);
-                    float bf = INFINITY;
-                    int bn = 4096;
-                    if (total != 1) {
-                        const int m = mrow + i;
-                        float x[12], c[12];
-                        for (int d = 0; d < bd; ++d) x[d] = xs[m * XS + perm_l[blk * bd + d]];
-                        for (int nt = 0; nt < 16; ++nt) {
-                            if (acc[nt][i] <= thr[i]) {
-                                for (int d = 0; d < bd; ++d) c[d] = bb[((d >> 2) * 16 + nt) * 64 + (d & 3) * 16 + lane16];
-                                const int kc = bd + 1;
-                                const float cnv = bb[((kc >> 2) * 16 + nt) * 64 + (kc & 3) * 16 + lane16];
-                                const float f = dist_of(mm_dist2(x, xn[m * nbc + bl], c, cnv, bd));
-                                const int n = 16 * nt + lane16;
-                                if (f < bf || (f == bf && n < bn)) { bf = f; bn = n; }
-                            }
-                        }
-                    }
-#pragma unroll
-                    for (int o = 0; o < 4; ++o) {
-                        float of;
-                        int on;
-                        switch (o) {
-                            case 0: of = dpp_f<0x121>(bf); on = dpp_i<0x121>(bn); break;
-                            case 1: of = dpp_f<0x122>(bf); on = dpp_i<0x122>(bn); break;
-                            case 2: of = dpp_f<0x124>(bf); on = dpp_i<0x124>(bn); break;
-                            default: of = dpp_f<0x128>(bf); on = dpp_i<0x128>(bn); break;
-                        }
-                        if (of < bf || (of == bf && on < bn)) { bf = of; bn = on; }
-                    }
-                    if (total != 1) code[i] = bn;
-                }
-            }
-            if (lane16 == 0) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) cs[(mrow + i) * nb + blk] = (uint8_t)code[i];
-            }
+        // software pipeline over the chunk's blocks: the MFMAs of block bl+1 are issued before the
+        // VALU passes over block bl, so the matrix core works while the vector ALU reduces
+#if SSQ_ENC_PIPE
+        v4f accA[16], accB[16];
+        if (nbc > 0) issue_block<KS>(bsw, xs, xn, poff, 0, nbc, bd, XS, lane, lane16, accA);
+        for (int bl = 0; bl < nbc; bl += 2) {
+            issue_block<KS>(bsw, xs, xn, poff, min(bl + 1, nbc - 1), nbc, bd, XS, lane, lane16, accB);
+            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl, nbc, nb, bd, XS, lane16, mrow, accA, cs);
+            if (bl + 1 >= nbc) break;
+            issue_block<KS>(bsw, xs, xn, poff, min(bl + 2, nbc - 1), nbc, bd, XS, lane, lane16, accA);
+            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl + 1, nbc, nb, bd, XS, lane16, mrow, accB, cs);
         }
+#else
+        for (int bl = 0; bl < nbc; ++bl) {
+            v4f acc[16];
+            issue_block<KS>(bsw, xs, xn, poff, bl, nbc, bd, XS, lane, lane16, acc);
+            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl, nbc, nb, bd, XS, lane16, mrow, acc, cs);
+        }
+#endif
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // write this round's codes (and, in chunk 0, the heavy blocks' code 0 + passthrough values)
-        for (int e = lane; e < 16 * nb; e += 64) {
-            const int m = e / nb, blk = e - m * nb;
+        // write this round's codes: lane (key m = lane/4) writes blocks lane%4 + 4k of its key;
+        // chunk 0 also writes the heavy blocks' code 0 and passthrough values
+        {
+            const int m = lane >> 2;
             const int s = s0 + m;
-            if (s >= a.seq_len) continue;
-            const bool heavy = ssq_is_heavy(hm0, hm1, blk);
-            bool mine = false;
-            if (heavy) {
-                mine = do_heavy;
-            } else {
-                for (int bl = 0; bl < nbc; ++bl) mine |= p.light[l0 + bl] == blk;
-            }
-            if (!mine) continue;
-            int64_t crow, prow;
-            out_rows(a, b, kv, s, crow, prow);
-            if (heavy) {
-                a.codes[crow + blk] = 0;
-                const int slot = a.pt_dense ? blk : heavy_ordinal(hm0, hm1, blk);
-                for (int d = 0; d < bd; ++d)
-                    ssq_store_elem(a.pt, a.pt_dtype, prow + (int64_t)slot * bd + d, xs[m * XS + perm_l[blk * bd + d]]);
-            } else {
-                a.codes[crow + blk] = cs[e];
+            if (s < a.seq_len) {
+                int64_t crow, prow;
+                out_rows(a, b, kv, s, crow, prow);
+                for (int blk = lane & 3; blk < nb; blk += 4) {
+                    const bool heavy = ssq_is_heavy(hm0, hm1, blk);
+                    if (heavy) {
+                        if (!do_heavy) continue;
+                        a.codes[crow + blk] = 0;
+                        const int slot = a.pt_dense ? blk : heavy_ordinal(hm0, hm1, blk);
+                        for (int d = 0; d < bd; ++d)
+                            ssq_store_elem(a.pt, a.pt_dtype, prow + (int64_t)slot * bd + d, xs[m * XS + perm_l[blk * bd + d]]);
+                    } else if (blk >= lo_blk && blk <= hi_blk && ((blk < 64 ? (cm0 >> blk) : (cm1 >> (blk - 64))) & 1ull)) {
+                        a.codes[crow + blk] = cs[m * nb + blk];
+                    }
+                }
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -452,6 +496,7 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
     if (kernel == 2) {
         SSQ_UNSUPPORTED(mfma_ok, "MFMA encode needs n_centroids == 256 and block_dim <= 10");
         MfmaEncodeParams mp;
+        memset(&mp, 0, sizeof(mp));
         mp.a = *a;
         mp.n_light = 0;
         for (int blk = 0; blk < a->n_blocks; ++blk) {
