@@ -139,7 +139,10 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
 // MFMA screen + exact certification
 // ---------------------------------------------------------------------------
 #ifndef SSQ_ENC_PIPE
-#define SSQ_ENC_PIPE 0  // 1: MFMAs of the next block issued before the current block's reductions
+#define SSQ_ENC_PIPE 1  // 0: each block's MFMAs and reduction back to back
+#endif
+#ifndef SSQ_ENC_COUNT
+#define SSQ_ENC_COUNT 1
 #endif
 constexpr int kMfmaWaves = 4;
 constexpr int kRounds = 8;        // key groups of 16 per wave per workgroup
@@ -148,6 +151,7 @@ constexpr size_t kMfmaSmemCap = 80 * 1024;  // two workgroups per CU (160 KiB LD
 
 struct MfmaEncodeParams {
     ssq_encode_args a;
+    float e1, e2;             // certification error bound: err = e1*|x|^2 + e2*max(min, 0)
     int nbc;                  // light blocks per workgroup chunk
     int n_light;
     uint8_t light[kMaxLight]; // light (VQ-coded) block ids, ascending
@@ -161,20 +165,21 @@ template <int CTL>
 __device__ __forceinline__ int dpp_i(int v) {
     return __builtin_amdgcn_update_dpp(v, v, CTL, 0xF, 0xF, false);
 }
-// reductions over the 16 lanes of a row (every lane of the row receives the result)
-__device__ __forceinline__ float row_min_f(float v) {
-    v = fminf(v, dpp_f<0x121>(v)); v = fminf(v, dpp_f<0x122>(v));
-    v = fminf(v, dpp_f<0x124>(v)); v = fminf(v, dpp_f<0x128>(v));
+// minimum over the 16 lanes of a row (row rotations; every lane of the row receives the result).
+// Rotations stay inside the row, so every lane reads a valid source and bound_ctrl never applies;
+// the plain mov_dpp form lets the compiler fold each rotation into the v_min_i32 that consumes it.
+template <int CTL>
+__device__ __forceinline__ int rot_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ int row_sum_i(int v) {
+    v += rot_i<0x121>(v); v += rot_i<0x122>(v);
+    v += rot_i<0x124>(v); v += rot_i<0x128>(v);
     return v;
 }
 __device__ __forceinline__ int row_min_i(int v) {
-    v = min(v, dpp_i<0x121>(v)); v = min(v, dpp_i<0x122>(v));
-    v = min(v, dpp_i<0x124>(v)); v = min(v, dpp_i<0x128>(v));
-    return v;
-}
-__device__ __forceinline__ int row_sum_i(int v) {
-    v += dpp_i<0x121>(v); v += dpp_i<0x122>(v);
-    v += dpp_i<0x124>(v); v += dpp_i<0x128>(v);
+    v = min(v, rot_i<0x121>(v)); v = min(v, rot_i<0x122>(v));
+    v = min(v, rot_i<0x124>(v)); v = min(v, rot_i<0x128>(v));
     return v;
 }
 // one step of a row-wide lexicographic (value, index) minimum
@@ -213,75 +218,129 @@ __device__ __forceinline__ void issue_block(const float* bsw, const float* xs, c
 }
 
 // first-argmin of sqrt(max(d2,0)) for the 16 keys of the wave in one light block; codes -> cs[key][blk]
+//
+// Fast path, per key (4 per lane, the row's 16 lanes hold its 256 codewords):
+//  1. the minimum MFMA value with its codeword index packed into the low 8 mantissa bits.  For
+//     values >= 0 the float bit pattern orders like a signed int, and every negative value orders
+//     below them, so one integer min3 chain finds both (a 4-bit slot tag inside the lane, widened
+//     to the 8-bit codeword index for the row reduction);
+//  2. a threshold thr that provably contains the exact reference winner (bound below);
+//  3. the candidates (MFMA value <= thr) counted on the scalar unit from ballots: the key is
+//     decided when its row holds exactly one candidate, which is then the packed minimum.
+// Keys with several candidates re-evaluate just those candidates with the reference's fp32 chain
+// and a correctly rounded sqrt, in a compact loop (one candidate per lane per trip).
+//
+// Error bound.  The K = bd + 2 terms of a distance pass through at most K roundings (product and
+// sums, any order, even truncation), so |value_j - |x-c_j|^2| <= g*(|x| + |c_j|)^2 with
+// g = 1.001*K*2^-23 (Cauchy-Schwarz), the same for the MFMA and for the reference chain, and
+// |c_j| <= |x| + |x-c_j|.  Every codeword that can matter has |x-c_j|^2 <= Y = 1.01*max(mn,0) +
+// 64*g*|x|^2 (self-consistent because 12*g << 0.01), so its error is <= err = 8*g*|x|^2 + 2*g*Y
+// <= e1*|x|^2 + e2*max(mn,0) with e1 = 1.0234*8g, e2 = 1.0234*2g (+ underflow).  The exact winner
+// j* has d(j*) <= d(argmin) and sqrt merges values <= 2^-21 apart, hence value_j*(MFMA) <=
+// max(mn,0)*(1 + 2^-21) + 4*err.  mt, the minimum with its 8 low bits cleared, satisfies mt <= mn <
+// mt*(1 + 2^-15), so thr = max(mt,0)*(1 + 2^-14) + 5*err(mt) + 2^-100 still exceeds that bound:
+// every codeword under thr is a candidate, and so is the row minimum.
 template <int KS>
 __device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, const float* xn, const int* poff,
                                              const int* lightL, int bl, int nbc, int nb, int bd, int XS,
-                                             int lane16, int mrow, const v4f (&acc)[16], uint8_t* cs) {
+                                             int lane16, int mrow, float e1, float e2, const v4f (&acc)[16],
+                                             uint8_t* cs) {
+    int pm[4];
     float thr[4];
-    int first[4], cnt[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        float v = acc[0][i];
+        int v = __float_as_int(acc[0][i]) & -16;
 #pragma unroll
-        for (int nt = 1; nt < 16; ++nt) v = fminf(v, acc[nt][i]);
-        const float mn = row_min_f(v);
-        // Error bound.  gamma = 2^-19 >= 2 * 12u covers any rounding order (even truncation) of the
-        // <= 12-term sum, so |value_j - |x-c_j|^2| <= gamma * (|x| + |c_j|)^2 (Cauchy-Schwarz), with
-        // |c_j| <= |x| + |x-c_j|.  Every codeword that can matter has |x-c_j|^2 <= Y =
-        // 1.01*max(mn,0) + 64*gamma*|x|^2 (self-consistent because 12*gamma << 0.01), so its error is
-        // <= err = 8*gamma*|x|^2 + 2*gamma*Y <= 2^-16*|x|^2*1.02 + 2^-18*max(mn,0)*1.02 (+ underflow).
-        // The exact winner j* has d(j*) <= d(argmin) and sqrt merges values <= 2^-21 apart, hence
-        // value_j*(MFMA) <= max(mn,0)*(1 + 2^-21) + 4*err: every codeword under thr is a candidate.
+        for (int nt = 1; nt < 16; ++nt) v = min(v, (__float_as_int(acc[nt][i]) & -16) | nt);
+        pm[i] = row_min_i((v & -256) | ((v & 15) << 4) | lane16);
         const float xnv = xn[(mrow + i) * nbc + bl];
-        const float mp = fmaxf(mn, 0.f);
-        const float err = 0x1.06p-16f * xnv + 0x1.06p-18f * mp;
-        thr[i] = mp * (1.0f + 0x1.0p-20f) + 5.0f * err + 0x1.0p-100f;
-        first[i] = 16;
-        cnt[i] = 0;
+        const float mp = fmaxf(__int_as_float(pm[i] & -256), 0.f);
+        const float err = e1 * xnv + e2 * mp;
+        thr[i] = mp * (1.0f + 0x1.0p-14f) + 5.0f * err + 0x1.0p-100f;
     }
-#pragma unroll
-    for (int nt = 15; nt >= 0; --nt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const bool c = acc[nt][i] <= thr[i];
-            first[i] = c ? nt : first[i];
-            cnt[i] += c ? 1 : 0;
-        }
-    }
-    int code[4], total[4];
-    bool slow = false;
+    // candidate masks: field r (16 bits) of seen = lanes of row r with a candidate; dup = lanes
+    // with two.  The row's minimum is always a candidate, so no field of seen is zero and the
+    // per-field decrement below never borrows across fields.
+    uint64_t bad[4];
+    uint64_t any_bad = 0;
+#if SSQ_ENC_COUNT == 0
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        total[i] = row_sum_i(cnt[i]);
-        code[i] = row_min_i(first[i] < 16 ? 16 * first[i] + lane16 : 4096);
-        slow |= total[i] != 1;
+        uint64_t seen = __builtin_amdgcn_ballot_w64(acc[0][i] <= thr[i]);
+        uint64_t dup = 0;
+#pragma unroll
+        for (int nt = 1; nt < 16; ++nt) {
+            const uint64_t m = __builtin_amdgcn_ballot_w64(acc[nt][i] <= thr[i]);
+            dup |= seen & m;
+            seen |= m;
+        }
+        bad[i] = dup | (seen & (seen - 0x0001000100010001ull));
+        any_bad |= bad[i];
     }
-    if (__builtin_amdgcn_ballot_w64(slow)) {  // rare: several candidates -> exact arithmetic decides
-        const float* bb = bsw + (size_t)bl * KS * 1024;
+#else
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int cnt = 0;
+#pragma unroll
+        for (int nt = 0; nt < 16; ++nt) cnt += acc[nt][i] <= thr[i] ? 1 : 0;
+        cnt = row_sum_i(cnt);
+        bad[i] = __builtin_amdgcn_ballot_w64(cnt != 1);
+        any_bad |= bad[i];
+    }
+#endif
+    int code[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) code[i] = pm[i] & 255;
+    if (any_bad) {  // rare: several candidates -> exact arithmetic decides
+        const int rsh = mrow * 4;  // bit offset of this lane's row field
+        // this lane's candidates of undecided keys: bit 16*i + nt
+        uint64_t cand = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float bf = INFINITY;
-            int bn = 4096;
-            if (total[i] != 1) {
-                const int m = mrow + i;
-                float x[12], c[12];
-                for (int d = 0; d < bd; ++d) x[d] = xs[m * XS + poff[bl * bd + d]];
-                for (int nt = 0; nt < 16; ++nt) {
-                    if (acc[nt][i] <= thr[i]) {
-                        for (int d = 0; d < bd; ++d) c[d] = bb[((d >> 2) * 16 + nt) * 64 + (d & 3) * 16 + lane16];
-                        const int kc = bd + 1;
-                        const float cnv = bb[((kc >> 2) * 16 + nt) * 64 + (kc & 3) * 16 + lane16];
-                        const float f = dist_of(mm_dist2(x, xn[m * nbc + bl], c, cnv, bd));
-                        const int n = 16 * nt + lane16;
-                        if (f < bf || (f == bf && n < bn)) { bf = f; bn = n; }
-                    }
-                }
+            if (bad[i]) {  // wave-uniform
+                const bool slow = ((bad[i] >> rsh) & 0xFFFFull) != 0;
+                uint32_t bits = 0;
+#pragma unroll
+                for (int nt = 0; nt < 16; ++nt) bits |= (slow && acc[nt][i] <= thr[i]) ? (1u << nt) : 0u;
+                cand |= (uint64_t)bits << (16 * i);
             }
-            lexmin_step<0x121>(bf, bn);
-            lexmin_step<0x122>(bf, bn);
-            lexmin_step<0x124>(bf, bn);
-            lexmin_step<0x128>(bf, bn);
-            if (total[i] != 1) code[i] = bn;
+        }
+        const float* bb = bsw + (size_t)bl * KS * 1024;
+        const int kc = bd + 1;
+        const float* cnp = bb + (kc >> 2) * 1024 + (kc & 3) * 16 + lane16;  // |c|^2 row of the B operand
+        float bf[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+        int bn[4] = {4096, 4096, 4096, 4096};
+#pragma unroll 1
+        while (cand) {
+            const int pos = __builtin_ctzll(cand);
+            cand &= cand - 1;
+            const int i = pos >> 4, nt = pos & 15;
+            const int m = mrow + i;
+            const float* xr = xs + m * XS;
+            const int* po = poff + bl * bd;
+            const float* cb = bb + nt * 64 + lane16;
+            // the reference chain: k ascending FMA over [-2x, |x|^2, 1] . [c, 1, |c|^2]
+            float d2 = (-2.0f * xr[po[0]]) * cb[0];
+#pragma unroll 1
+            for (int d = 1; d < bd; ++d) d2 = __builtin_fmaf(-2.0f * xr[po[d]], cb[(d >> 2) * 1024 + (d & 3) * 16], d2);
+            d2 = __builtin_fmaf(xn[m * nbc + bl], 1.0f, d2);
+            d2 = __builtin_fmaf(1.0f, cnp[nt * 64], d2);
+            const float f = dist_of(d2);
+            const int n = 16 * nt + lane16;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (k == i && (f < bf[k] || (f == bf[k] && n < bn[k]))) { bf[k] = f; bn[k] = n; }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (bad[i]) {  // wave-uniform
+                lexmin_step<0x121>(bf[i], bn[i]);
+                lexmin_step<0x122>(bf[i], bn[i]);
+                lexmin_step<0x124>(bf[i], bn[i]);
+                lexmin_step<0x128>(bf[i], bn[i]);
+                if (((bad[i] >> rsh) & 0xFFFFull) != 0) code[i] = bn[i];
+            }
         }
     }
     if (lane16 == 0) {
@@ -408,23 +467,22 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-        // software pipeline over the chunk's blocks: the MFMAs of block bl+1 are issued before the
-        // VALU passes over block bl, so the matrix core works while the vector ALU reduces
 #if SSQ_ENC_PIPE
+        // software pipeline: the MFMAs of block bl+1 are in flight while the VALU reduces block bl
         v4f accA[16], accB[16];
         if (nbc > 0) issue_block<KS>(bsw, xs, xn, poff, 0, nbc, bd, XS, lane, lane16, accA);
         for (int bl = 0; bl < nbc; bl += 2) {
-            issue_block<KS>(bsw, xs, xn, poff, min(bl + 1, nbc - 1), nbc, bd, XS, lane, lane16, accB);
-            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl, nbc, nb, bd, XS, lane16, mrow, accA, cs);
+            if (bl + 1 < nbc) issue_block<KS>(bsw, xs, xn, poff, bl + 1, nbc, bd, XS, lane, lane16, accB);
+            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl, nbc, nb, bd, XS, lane16, mrow, p.e1, p.e2, accA, cs);
             if (bl + 1 >= nbc) break;
-            issue_block<KS>(bsw, xs, xn, poff, min(bl + 2, nbc - 1), nbc, bd, XS, lane, lane16, accA);
-            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl + 1, nbc, nb, bd, XS, lane16, mrow, accB, cs);
+            if (bl + 2 < nbc) issue_block<KS>(bsw, xs, xn, poff, bl + 2, nbc, bd, XS, lane, lane16, accA);
+            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl + 1, nbc, nb, bd, XS, lane16, mrow, p.e1, p.e2, accB, cs);
         }
 #else
         for (int bl = 0; bl < nbc; ++bl) {
             v4f acc[16];
             issue_block<KS>(bsw, xs, xn, poff, bl, nbc, bd, XS, lane, lane16, acc);
-            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl, nbc, nb, bd, XS, lane16, mrow, acc, cs);
+            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl, nbc, nb, bd, XS, lane16, mrow, p.e1, p.e2, acc, cs);
         }
 #endif
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -498,6 +556,13 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
         MfmaEncodeParams mp;
         memset(&mp, 0, sizeof(mp));
         mp.a = *a;
+        {
+            // g = 1.001 * K * 2^-23 for the K = bd + 2 terms of a distance; 1.0234 covers the
+            // bound's second-order terms (see reduce_block); rounded up by the 1.0005 factor
+            const double g = 1.001 * (a->block_dim + 2) * 0x1.0p-23;
+            mp.e1 = (float)(1.0234 * 8.0 * g * 1.0005);
+            mp.e2 = (float)(1.0234 * 2.0 * g * 1.0005);
+        }
         mp.n_light = 0;
         for (int blk = 0; blk < a->n_blocks; ++blk) {
             const bool heavy = blk < 64 ? ((a->heavy_mask[0] >> blk) & 1) : ((a->heavy_mask[1] >> (blk - 64)) & 1);
