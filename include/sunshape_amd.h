@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SSQ_ABI_VERSION 1
+#define SSQ_ABI_VERSION 2
 
 enum ssq_status {
     SSQ_OK = 0,
@@ -124,7 +124,11 @@ int ssq_lut_build(const void* q, int32_t q_dtype, int64_t q_sr, int32_t rows, in
 /*
  * Nearest-codeword encode of keys [B, Hkv, S, D] (k[b*k_sb + kv*k_sh + s*k_ss + d]).
  * codes[b, kv, s, blk] = argmin_c sqrt(max(0, |x_blk|^2 - 2 x_blk.c + |c|^2)) evaluated
- * with torch.cdist's mm formulation, lowest index on ties; heavy blocks get code 0 and
+ * with torch.cdist's mm formulation, lowest index on ties.  With a block metric
+ * (SunShape-Pro, metric != NULL: E [D, D] fp32 row-major at metric + kv*metric_sh, of which
+ * only the diagonal bd x bd blocks E_b are read, as codec.py:375-376 slices them) x_blk and
+ * every codeword c are first mapped to E_b x and E_b c (y_k = sum_j E_b[k][j] x_j, j
+ * ascending, first product rounded, then fused multiply-adds).  Heavy blocks get code 0 and
  * their values are copied to pt in pt_dtype (slot = ordinal among heavy blocks, or the
  * block index itself when pt_dense != 0: the reference's dense [.., nb, bd] layout, whose
  * light-block entries the caller pre-fills with zeros).
@@ -139,6 +143,7 @@ typedef struct ssq_encode_args {
     int32_t batch, num_kv_heads, seq_len, head_dim;
     const int64_t* perm; int64_t perm_sh;
     const float* cent; int64_t cent_sh;
+    const float* metric; int64_t metric_sh;   /* SunShape-Pro E [D, D] or NULL (identity) */
     int32_t block_dim, n_blocks, n_centroids;
     uint64_t heavy_mask[2];
     uint8_t* codes; int64_t c_sb, c_sh, c_st;

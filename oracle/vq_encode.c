@@ -7,7 +7,13 @@
  * Follows sunshape/codec.py:362-385 (SunShapeBlockCodec.quantize):
  *   keys.float() -> x[..., perm] -> per block b:
  *     heavy (mixed mode): passthrough_values[:, b, :] = x_b, index 0
- *     else: argmin_c torch.cdist(x_b @ E_b^T, C_b @ E_b^T)      (E = identity here)
+ *     else: argmin_c torch.cdist(x_b @ E_b^T, C_b @ E_b^T)
+ *           E_b = E[b*bd:(b+1)*bd, b*bd:(b+1)*bd], the block's diagonal block of the
+ *           [D, D] metric (identity outside SunShape-Pro, sunshape/codec.py:289-312).
+ *           y = x_b @ E_b^T is evaluated row by row as y_k = sum_j E_b[k][j] * x_j with
+ *           j ascending, first product rounded, then fused multiply-adds; C_b @ E_b^T
+ *           likewise.  (torch's matmul leaves its order unspecified; this is the
+ *           order the HIP kernels use, and an identity E reproduces x exactly.)
  * torch.cdist with >25 rows takes ATen's mm formulation (_euclidean_dist):
  *   x1_ = [-2*x, |x|^2, 1],  x2_ = [c, 1, |c|^2],  d2 = x1_ @ x2_^T,
  *   d = sqrt(clamp_min(d2, 0)),  argmin -> first minimum.
@@ -41,6 +47,15 @@ static float mm_dist2(const float* x, float xn, const float* c, float cn, int bd
     return acc;
 }
 
+/* y[k] = sum_j e[k*ld + j] * x[j], j ascending, first product rounded, then FMAs. */
+static void metric_apply(const float* e, int ld, const float* x, int bd, float* y) {
+    for (int k = 0; k < bd; ++k) {
+        float acc = e[(int64_t)k * ld] * x[0];
+        for (int j = 1; j < bd; ++j) acc = fmaf(e[(int64_t)k * ld + j], x[j], acc);
+        y[k] = acc;
+    }
+}
+
 /* Distance matrix for one block: e2[i*nc+j] = pre-sqrt value, d[i*nc+j] = sqrt(clamp_min(., 0)). */
 void oracle_block_dist(const float* x, int64_t n, const float* c, int nc, int bd, float* e2, float* d) {
     for (int64_t i = 0; i < n; ++i) {
@@ -64,10 +79,21 @@ void oracle_block_dist(const float* x, int64_t n, const float* c, int nc, int bd
  *   codes     uint8 [n, nb] out
  *   pt        fp32 [n, nb, bd] out or NULL; zeros on light blocks (dense, as the reference)
  */
-void oracle_encode(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
-                   int nb, int nc, int bd, const uint8_t* heavy, uint8_t* codes, float* pt) {
+void oracle_encode_metric(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
+                          const float* metric, int nb, int nc, int bd, const uint8_t* heavy, uint8_t* codes,
+                          float* pt) {
     float* cn = (float*)malloc(sizeof(float) * (size_t)nb * (size_t)nc);
     float* xp = (float*)malloc(sizeof(float) * (size_t)D);
+    float* cm = NULL; /* codebook in the metric space, C_b @ E_b^T */
+    float y[64];
+    if (metric) {
+        cm = (float*)malloc(sizeof(float) * (size_t)nb * (size_t)nc * (size_t)bd);
+        for (int b = 0; b < nb; ++b)
+            for (int j = 0; j < nc; ++j)
+                metric_apply(metric + (int64_t)b * bd * D + (int64_t)b * bd, D, cent + ((int64_t)b * nc + j) * bd, bd,
+                             cm + ((int64_t)b * nc + j) * bd);
+        cent = cm;
+    }
     for (int b = 0; b < nb; ++b)
         for (int j = 0; j < nc; ++j)
             cn[b * nc + j] = sq_norm(cent + ((int64_t)b * nc + j) * bd, bd);
@@ -85,6 +111,10 @@ void oracle_encode(const float* keys, int64_t n, int D, const int64_t* perm, con
             if (pt)
                 for (int d = 0; d < bd; ++d) pt[(i * nb + b) * bd + d] = 0.0f;
             const float* cb = cent + (int64_t)b * nc * bd;
+            if (metric) {
+                metric_apply(metric + (int64_t)b * bd * D + (int64_t)b * bd, D, xb, bd, y);
+                xb = y;
+            }
             float xn = sq_norm(xb, bd);
             float best = INFINITY;
             int best_j = 0;
@@ -101,4 +131,10 @@ void oracle_encode(const float* keys, int64_t n, int D, const int64_t* perm, con
     }
     free(xp);
     free(cn);
+    free(cm);
+}
+
+void oracle_encode(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
+                   int nb, int nc, int bd, const uint8_t* heavy, uint8_t* codes, float* pt) {
+    oracle_encode_metric(keys, n, D, perm, cent, NULL, nb, nc, bd, heavy, codes, pt);
 }

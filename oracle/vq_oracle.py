@@ -301,6 +301,9 @@ def _lib():
         lib.oracle_encode.argtypes = [vp, ctypes.c_int64, ctypes.c_int, vp, vp,
                                       ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, vp]
         lib.oracle_encode.restype = None
+        lib.oracle_encode_metric.argtypes = [vp, ctypes.c_int64, ctypes.c_int, vp, vp, vp,
+                                             ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, vp]
+        lib.oracle_encode_metric.restype = None
         lib.oracle_block_dist.argtypes = [vp, ctypes.c_int64, vp, ctypes.c_int, ctypes.c_int, vp, vp]
         lib.oracle_block_dist.restype = None
         _LIB = lib
@@ -312,11 +315,13 @@ def _ptr(a: Optional[np.ndarray]):
 
 
 def encode(keys: np.ndarray, perm: np.ndarray, centroids: np.ndarray,
-           heavy: Optional[np.ndarray] = None):
+           heavy: Optional[np.ndarray] = None, metric: Optional[np.ndarray] = None):
     """``codec.quantize(keys)``: codes uint8 [N, nb], passthrough fp32 [N, nb, bd] or None.
 
     sunshape/codec.py:362-385; exact arithmetic in oracle/vq_encode.c.
     keys: [N, D] values (bf16 keys pass as their exact fp32 upcast).
+    metric: the codec's E [D, D] (SunShape-Pro block metric; only its diagonal
+    bd x bd blocks are read, as codec.py:375-376 slices them), None = identity.
     """
     keys = np.ascontiguousarray(keys, dtype=np.float32)
     perm = np.ascontiguousarray(perm, dtype=np.int64)
@@ -329,7 +334,11 @@ def encode(keys: np.ndarray, perm: np.ndarray, centroids: np.ndarray,
     if heavy is not None and np.any(heavy):
         hv = np.ascontiguousarray(np.asarray(heavy, dtype=bool).astype(np.uint8))
         pt = np.empty((n, nb, bd), dtype=np.float32)
-    _lib().oracle_encode(_ptr(keys), n, D, _ptr(perm), _ptr(cen), nb, nc, bd, _ptr(hv), _ptr(codes), _ptr(pt))
+    met = None if metric is None else np.ascontiguousarray(metric, dtype=np.float32)
+    if met is not None and met.shape != (D, D):
+        raise ValueError(f"metric must be [{D}, {D}]")
+    _lib().oracle_encode_metric(_ptr(keys), n, D, _ptr(perm), _ptr(cen), _ptr(met), nb, nc, bd, _ptr(hv),
+                                _ptr(codes), _ptr(pt))
     return codes, pt
 
 

@@ -30,6 +30,8 @@ SSQ_CONTIGUOUS, SSQ_PAGED = 0, 1
 
 DTYPE_CODE = {torch.float32: SSQ_F32, torch.bfloat16: SSQ_BF16, torch.float16: SSQ_F16}
 
+ABI_VERSION = 2  # SSQ_ABI_VERSION in include/sunshape_amd.h
+
 # every function include/sunshape_amd.h declares
 EXPORTED_SYMBOLS = (
     "ssq_decode_workspace_size",
@@ -91,6 +93,7 @@ class EncodeArgs(ctypes.Structure):
         ("batch", _i32), ("num_kv_heads", _i32), ("seq_len", _i32), ("head_dim", _i32),
         ("perm", _vp), ("perm_sh", _i64),
         ("cent", _vp), ("cent_sh", _i64),
+        ("metric", _vp), ("metric_sh", _i64),
         ("block_dim", _i32), ("n_blocks", _i32), ("n_centroids", _i32),
         ("heavy_mask", ctypes.c_uint64 * 2),
         ("codes", _vp), ("c_sb", _i64), ("c_sh", _i64), ("c_st", _i64),
@@ -144,7 +147,7 @@ def lib() -> ctypes.CDLL:
                 )
             handle = ctypes.CDLL(LIB_PATH)
             _declare(handle)
-            if handle.ssq_abi_version() != 1:
+            if handle.ssq_abi_version() != ABI_VERSION:
                 raise RuntimeError("sunshape_amd library ABI version mismatch")
             _lib = handle
     return _lib

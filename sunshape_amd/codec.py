@@ -23,8 +23,10 @@ import torch
 from . import hip_ops
 
 PERMUTATION_MODES = frozenset({"profileperm_baseline", "profileperm_localmetric_dsq", "profileperm_mixed_precision"})
-# encode needs an identity block metric E (sunshape/codec.py:375-376); these modes have one
+# modes whose fitted E is the identity (sunshape/codec.py:279-312): encode takes no metric
 IDENTITY_METRIC_MODES = frozenset({"profileperm_baseline", "profileperm_mixed_precision", "identity_baseline"})
+# SunShape-Pro / legacy modes: encode compares E_b x with E_b c (sunshape/codec.py:375-376)
+METRIC_MODES = frozenset({"profileperm_localmetric_dsq", "legacy_strict"})
 
 
 class SunShapeQuantized(NamedTuple):
@@ -115,8 +117,13 @@ class SunShapeBlockCodec(torch.nn.Module):
     def from_buffers(cls, permutation: torch.Tensor, centroids: torch.Tensor, *,
                      mode: str = "profileperm_baseline",
                      mixed_high_precision_blocks: torch.Tensor | None = None,
+                     metric: torch.Tensor | None = None,
                      device: torch.device | None = None) -> "SunShapeBlockCodec":
-        """Codec from a fitted permutation ([D] or [Hkv, D]) and codebook ([nb, nc, bd] or [Hkv, nb, nc, bd])."""
+        """Codec from a fitted permutation ([D] or [Hkv, D]) and codebook ([nb, nc, bd] or [Hkv, nb, nc, bd]).
+
+        metric: the SunShape-Pro block metric E ([D, D], or [Hkv, D, D] per KV head); E_inv is
+        set to its pseudo-inverse as the reference's fit does (sunshape/codec.py:303-304).
+        """
         nkv = centroids.shape[0] if centroids.ndim == 4 else None
         nb, nc, bd = centroids.shape[-3:]
         dev = torch.device(device) if device is not None else centroids.device
@@ -129,6 +136,12 @@ class SunShapeBlockCodec(torch.nn.Module):
         codec.inv_permutation.copy_(_invert_permutation(codec.permutation))
         if mixed_high_precision_blocks is not None:
             codec.mixed_high_precision_blocks.copy_(mixed_high_precision_blocks.to(dev, torch.bool))
+        if metric is not None:
+            E = metric.to(dev, torch.float32).contiguous()
+            if E.shape[-2:] != (nb * bd, nb * bd) or E.ndim not in (2, 3):
+                raise ValueError(f"metric must be [{nb * bd}, {nb * bd}] or [Hkv, {nb * bd}, {nb * bd}]")
+            codec.E = E
+            codec.E_inv = torch.linalg.pinv(E.cpu()).to(dev)
         return codec
 
     def heavy_blocks(self) -> tuple[bool, ...] | None:
@@ -156,6 +169,19 @@ class SunShapeBlockCodec(torch.nn.Module):
         if kv_head is not None and perm.ndim == 2:
             perm = perm[kv_head]
         return perm
+
+    def encode_metric(self, kv_head: int | None = None) -> torch.Tensor | None:
+        """The block metric E the encode applies (SunShape-Pro), or None for identity-metric modes.
+
+        [D, D] (or [Hkv, D, D] for per-head metrics; kv_head selects one).  Only the diagonal
+        bd x bd blocks are read, as sunshape/codec.py:375-376 slices them.
+        """
+        if self.mode not in METRIC_MODES:
+            return None
+        E = self.E
+        if kv_head is not None and E.ndim == 3:
+            E = E[kv_head]
+        return E
 
     def codebook(self, kv_head: int | None = None) -> torch.Tensor:
         cent = self.centroids
@@ -211,8 +237,6 @@ class SunShapeBlockCodec(torch.nn.Module):
         [N, nb, bd] (zeros on light blocks).
         """
         reason = self.unsupported_reason()
-        if reason is None and self.mode not in IDENTITY_METRIC_MODES:
-            reason = f"mode {self.mode!r} encodes under a block metric E (SunShape-Pro), not implemented by the HIP encode."
         if reason is not None:
             raise RuntimeError(reason)
         perm, cent = self._select_head(kv_head)
@@ -220,8 +244,11 @@ class SunShapeBlockCodec(torch.nn.Module):
         if keys.dtype not in (torch.float32, torch.bfloat16, torch.float16):
             keys = keys.float()
         heavy = self.heavy_blocks()
+        metric = self.encode_metric(kv_head)
+        if metric is not None and metric.ndim == 3:
+            raise RuntimeError("per-KV-head metric: pass kv_head=")
         codes, pt = hip_ops.encode(keys.reshape(1, 1, -1, self.head_dim), perm, cent, heavy=heavy,
-                                   pt_dtype=torch.float32, pt_dense=True)
+                                   pt_dtype=torch.float32, pt_dense=True, metric=metric)
         mixed = self.mode == "profileperm_mixed_precision"
         return SunShapeQuantized(
             indices=codes.reshape(-1, self.n_blocks),

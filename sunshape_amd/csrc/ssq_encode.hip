@@ -43,6 +43,14 @@ __device__ __forceinline__ float mm_dist2(const float* x, float xn, const float*
     return acc;
 }
 
+// y_k = sum_j e[k*ld + j] * x[j] for one row k of a SunShape-Pro block metric E_b:
+// j ascending, first product rounded, then fused multiply-adds
+__device__ __forceinline__ float metric_row(const float* e, const float* x, int bd) {
+    float acc = e[0] * x[0];
+    for (int j = 1; j < bd; ++j) acc = __builtin_fmaf(e[j], x[j], acc);
+    return acc;
+}
+
 // correctly rounded sqrt of max(v, 0)
 __device__ __forceinline__ float dist_of(float v) { return __builtin_sqrtf(v > 0.f ? v : 0.f); }
 
@@ -87,7 +95,19 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
     float* cb = smem;                        // [nbc][nc][bd]
     float* cn = cb + (size_t)nbc * nc * bd;  // [nbc][nc]
     const float* cent = a.cent + (int64_t)kv * a.cent_sh + (int64_t)blk0 * nc * bd;
-    for (int e = threadIdx.x; e < nbc * nc * bd; e += kScanThreads) cb[e] = cent[e];
+    const float* met = a.metric ? a.metric + (int64_t)kv * a.metric_sh : nullptr;
+    const int D = a.head_dim;
+    if (met) {  // codebook in the metric space: c' = E_b c, one codeword per thread
+        for (int e = threadIdx.x; e < nbc * nc; e += kScanThreads) {
+            const int blk = blk0 + e / nc;
+            const float* eb = met + (int64_t)blk * bd * D + blk * bd;
+            float c[16];
+            for (int d = 0; d < bd; ++d) c[d] = cent[(size_t)e * bd + d];
+            for (int k = 0; k < bd; ++k) cb[(size_t)e * bd + k] = metric_row(eb + (int64_t)k * D, c, bd);
+        }
+    } else {
+        for (int e = threadIdx.x; e < nbc * nc * bd; e += kScanThreads) cb[e] = cent[e];
+    }
     __syncthreads();
     for (int e = threadIdx.x; e < nbc * nc; e += kScanThreads) cn[e] = sq_norm(cb + (size_t)e * bd, bd);
     __syncthreads();
@@ -114,6 +134,12 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
             for (int d = 0; d < bd; ++d) ssq_store_elem(a.pt, a.pt_dtype, prow + (int64_t)slot * bd + d, x[d]);
             continue;
         }
+        if (met) {
+            const float* eb = met + (int64_t)blk * bd * D + blk * bd;
+            float y[16];
+            for (int k = 0; k < bd; ++k) y[k] = metric_row(eb + (int64_t)k * D, x, bd);
+            for (int k = 0; k < bd; ++k) x[k] = y[k];
+        }
         const float xn = sq_norm(x, bd);
         // pass 1: smallest pre-sqrt value (first index)
         float emin = INFINITY;
@@ -139,7 +165,7 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
 // MFMA screen + exact certification
 // ---------------------------------------------------------------------------
 #ifndef SSQ_ENC_PIPE
-#define SSQ_ENC_PIPE 1  // 0: each block's MFMAs and reduction back to back
+#define SSQ_ENC_PIPE 1  // 0: each block's MFMAs and reduction back to back (always so with a metric)
 #endif
 #ifndef SSQ_ENC_COUNT
 #define SSQ_ENC_COUNT 1
@@ -152,6 +178,7 @@ constexpr size_t kMfmaSmemCap = 80 * 1024;  // two workgroups per CU (160 KiB LD
 struct MfmaEncodeParams {
     ssq_encode_args a;
     float e1, e2;             // certification error bound: err = e1*|x|^2 + e2*max(min, 0)
+    int ys_stride;            // row stride of the keys' metric images in LDS (block metric only)
     int nbc;                  // light blocks per workgroup chunk
     int n_light;
     uint8_t light[kMaxLight]; // light (VQ-coded) block ids, ascending
@@ -192,15 +219,24 @@ __device__ __forceinline__ void lexmin_step(float& bf, int& bn) {
 
 
 // A/B operands of one light block and its 16 MFMA tiles: acc[nt] holds d2[key 4*(l/16)+i][codeword 16nt + l%16]
-template <int KS>
-__device__ __forceinline__ void issue_block(const float* bsw, const float* xs, const float* xn, const int* poff,
-                                            int bl, int nbc, int bd, int XS, int lane, int lane16, v4f (&acc)[16]) {
+// key element k of light block bl for key row m: the permuted key (xs through poff) or, with a
+// block metric, its image E_b x staged in ys
+template <bool MET>
+__device__ __forceinline__ float key_elem(const float* xs, const float* ys, const int* poff, int XS, int YS, int m,
+                                          int bl, int bd, int k) {
+    return MET ? ys[m * YS + bl * bd + k] : xs[m * XS + poff[bl * bd + k]];
+}
+
+template <int KS, bool MET>
+__device__ __forceinline__ void issue_block(const float* bsw, const float* xs, const float* ys, const float* xn,
+                                            const int* poff, int bl, int nbc, int bd, int XS, int YS, int lane,
+                                            int lane16, v4f (&acc)[16]) {
     float av[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
         const int k = 4 * s + (lane >> 4);
         float v;
-        if (k < bd) v = -2.0f * xs[lane16 * XS + poff[bl * bd + k]];
+        if (k < bd) v = -2.0f * key_elem<MET>(xs, ys, poff, XS, YS, lane16, bl, bd, k);
         else if (k == bd) v = xn[lane16 * nbc + bl];
         else if (k == bd + 1) v = 1.0f;
         else v = 0.0f;
@@ -240,11 +276,11 @@ __device__ __forceinline__ void issue_block(const float* bsw, const float* xs, c
 // max(mn,0)*(1 + 2^-21) + 4*err.  mt, the minimum with its 8 low bits cleared, satisfies mt <= mn <
 // mt*(1 + 2^-15), so thr = max(mt,0)*(1 + 2^-14) + 5*err(mt) + 2^-100 still exceeds that bound:
 // every codeword under thr is a candidate, and so is the row minimum.
-template <int KS>
-__device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, const float* xn, const int* poff,
-                                             const int* lightL, int bl, int nbc, int nb, int bd, int XS,
-                                             int lane16, int mrow, float e1, float e2, const v4f (&acc)[16],
-                                             uint8_t* cs) {
+template <int KS, bool MET>
+__device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, const float* ys, const float* xn,
+                                             const int* poff, const int* lightL, int bl, int nbc, int nb, int bd,
+                                             int XS, int YS, int lane16, int mrow, float e1, float e2,
+                                             const v4f (&acc)[16], uint8_t* cs) {
     int pm[4];
     float thr[4];
 #pragma unroll
@@ -316,13 +352,13 @@ __device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, 
             cand &= cand - 1;
             const int i = pos >> 4, nt = pos & 15;
             const int m = mrow + i;
-            const float* xr = xs + m * XS;
-            const int* po = poff + bl * bd;
             const float* cb = bb + nt * 64 + lane16;
             // the reference chain: k ascending FMA over [-2x, |x|^2, 1] . [c, 1, |c|^2]
-            float d2 = (-2.0f * xr[po[0]]) * cb[0];
+            float d2 = (-2.0f * key_elem<MET>(xs, ys, poff, XS, YS, m, bl, bd, 0)) * cb[0];
 #pragma unroll 1
-            for (int d = 1; d < bd; ++d) d2 = __builtin_fmaf(-2.0f * xr[po[d]], cb[(d >> 2) * 1024 + (d & 3) * 16], d2);
+            for (int d = 1; d < bd; ++d)
+                d2 = __builtin_fmaf(-2.0f * key_elem<MET>(xs, ys, poff, XS, YS, m, bl, bd, d),
+                                    cb[(d >> 2) * 1024 + (d & 3) * 16], d2);
             d2 = __builtin_fmaf(xn[m * nbc + bl], 1.0f, d2);
             d2 = __builtin_fmaf(1.0f, cnp[nt * 64], d2);
             const float f = dist_of(d2);
@@ -350,12 +386,16 @@ __device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, 
     }
 }
 
+inline int mfma_ys_stride(const ssq_encode_args& a, int nbc) { return nbc * a.block_dim + 1; }
 inline size_t mfma_enc_smem(const ssq_encode_args& a, int nbc, int KS) {
-    return ((size_t)nbc * KS * 1024 + a.head_dim + (size_t)nbc * (a.block_dim + 1) + (size_t)kMfmaWaves * 16 * (a.head_dim + 1) +
-            (size_t)kMfmaWaves * 16 * nbc) * 4 + (size_t)kMfmaWaves * 16 * a.n_blocks + 64;
+    size_t words = (size_t)nbc * KS * 1024 + a.head_dim + (size_t)nbc * (a.block_dim + 1) +
+                   (size_t)kMfmaWaves * 16 * (a.head_dim + 1) + (size_t)kMfmaWaves * 16 * nbc;
+    if (a.metric)  // E_b blocks of the chunk + the keys' metric images
+        words += (size_t)nbc * a.block_dim * a.block_dim + (size_t)kMfmaWaves * 16 * mfma_ys_stride(a, nbc);
+    return words * 4 + (size_t)kMfmaWaves * 16 * a.n_blocks + 64;
 }
 
-template <int KS>
+template <int KS, bool MET>
 __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const MfmaEncodeParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_encode_args& a = p.a;
@@ -379,7 +419,7 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
     const int hi_blk = nbc > 0 ? p.light[l0 + nbc - 1] : -1;
 
     // LDS: bsw [nbc][KS][16][64] | perm [D] | poff [nbc*bd] | lightL [nbc] | xs [waves][16][XS] |
-    //      xn [waves][16][nbc] | codes [waves][16][nb]
+    //      xn [waves][16][nbc] | (MET: em [nbc][bd][bd] | ys [waves][16][YS]) | codes [waves][16][nb]
     float* bsw = smem;
     int* perm_l = reinterpret_cast<int*>(bsw + (size_t)nbc * KS * 1024);
     int* poff = perm_l + D;         // poff[bl*bd + d] = perm[light[bl]*bd + d]: the block's dims in the key row
@@ -387,7 +427,11 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
     float* xs_all = reinterpret_cast<float*>(lightL + nbc);
     float* xs = xs_all + wave * 16 * XS;
     float* xn = xs_all + kMfmaWaves * 16 * XS + wave * 16 * nbc;
-    uint8_t* cs = reinterpret_cast<uint8_t*>(xs_all + kMfmaWaves * 16 * XS + kMfmaWaves * 16 * nbc) + wave * 16 * nb;
+    float* tail = xs_all + kMfmaWaves * 16 * XS + kMfmaWaves * 16 * nbc;
+    const int YS = MET ? p.ys_stride : 0;
+    float* em = tail;                                  // em[bl][k][j] = E_b[k][j] (MET only)
+    float* ys = em + (MET ? nbc * bd * bd : 0) + wave * 16 * YS;
+    uint8_t* cs = reinterpret_cast<uint8_t*>(tail + (MET ? nbc * bd * bd + kMfmaWaves * 16 * YS : 0)) + wave * 16 * nb;
 
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
     const int64_t* perm_g = a.perm + (int64_t)kv * a.perm_sh;
@@ -397,7 +441,18 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
         poff[j] = (int)perm_g[p.light[l0 + bl] * bd + d];
     }
     for (int bl = threadIdx.x; bl < nbc; bl += kMfmaWaves * SSQ_WAVE) lightL[bl] = p.light[l0 + bl];
+    if (MET) {
+        const float* met = a.metric + (int64_t)kv * a.metric_sh;
+        for (int j = threadIdx.x; j < nbc * bd * bd; j += kMfmaWaves * SSQ_WAVE) {
+            const int bl = j / (bd * bd), r = j - bl * bd * bd;
+            const int k = r / bd, jj = r - k * bd;
+            const int blk = p.light[l0 + bl];
+            em[j] = met[(int64_t)(blk * bd + k) * D + blk * bd + jj];
+        }
+        __syncthreads();
+    }
     // B operands in lane order: bsw[bl][s][nt][l] = [c, 1, |c|^2, 0..][k = 4s + l/16] of codeword 16nt + l%16
+    // (with a block metric, c' = E_b c in place of c)
     for (int e = threadIdx.x; e < nbc * KS * 1024; e += kMfmaWaves * SSQ_WAVE) {
         const int l = e & 63;
         const int nt = (e >> 6) & 15;
@@ -406,7 +461,21 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
         const int blk = p.light[l0 + bl];
         const int k = 4 * s + (l >> 4);
         const float* c = cent + ((int64_t)blk * 256 + 16 * nt + (l & 15)) * bd;
-        bsw[e] = k < bd ? c[k] : k == bd ? 1.0f : k == bd + 1 ? sq_norm(c, bd) : 0.0f;
+        float v = 0.0f;
+        if (MET) {
+            if (k < bd) {
+                v = metric_row(em + (bl * bd + k) * bd, c, bd);
+            } else if (k == bd + 1) {
+                float cp[12];
+                for (int kk = 0; kk < bd; ++kk) cp[kk] = metric_row(em + (bl * bd + kk) * bd, c, bd);
+                v = sq_norm(cp, bd);
+            } else if (k == bd) {
+                v = 1.0f;
+            }
+        } else {
+            v = k < bd ? c[k] : k == bd ? 1.0f : k == bd + 1 ? sq_norm(c, bd) : 0.0f;
+        }
+        bsw[e] = v;
     }
     __syncthreads();
 
@@ -461,30 +530,38 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
         for (int bl = lane >> 4; bl < nbc; bl += 4) {
             float x[16];
             for (int d = 0; d < bd; ++d) x[d] = xs[lane16 * XS + poff[bl * bd + d]];
+            if (MET) {  // the key block's metric image y = E_b x
+                float y[12];
+                for (int k = 0; k < bd; ++k) y[k] = metric_row(em + (bl * bd + k) * bd, x, bd);
+                for (int k = 0; k < bd; ++k) {
+                    ys[lane16 * YS + bl * bd + k] = y[k];
+                    x[k] = y[k];
+                }
+            }
             xn[lane16 * nbc + bl] = sq_norm(x, bd);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-#if SSQ_ENC_PIPE
-        // software pipeline: the MFMAs of block bl+1 are in flight while the VALU reduces block bl
-        v4f accA[16], accB[16];
-        if (nbc > 0) issue_block<KS>(bsw, xs, xn, poff, 0, nbc, bd, XS, lane, lane16, accA);
-        for (int bl = 0; bl < nbc; bl += 2) {
-            if (bl + 1 < nbc) issue_block<KS>(bsw, xs, xn, poff, bl + 1, nbc, bd, XS, lane, lane16, accB);
-            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl, nbc, nb, bd, XS, lane16, mrow, p.e1, p.e2, accA, cs);
-            if (bl + 1 >= nbc) break;
-            if (bl + 2 < nbc) issue_block<KS>(bsw, xs, xn, poff, bl + 2, nbc, bd, XS, lane, lane16, accA);
-            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl + 1, nbc, nb, bd, XS, lane16, mrow, p.e1, p.e2, accB, cs);
+        if constexpr (SSQ_ENC_PIPE && !MET) {
+            // software pipeline: the MFMAs of block bl+1 are in flight while the VALU reduces block bl
+            v4f accA[16], accB[16];
+            if (nbc > 0) issue_block<KS, MET>(bsw, xs, ys, xn, poff, 0, nbc, bd, XS, YS, lane, lane16, accA);
+            for (int bl = 0; bl < nbc; bl += 2) {
+                if (bl + 1 < nbc) issue_block<KS, MET>(bsw, xs, ys, xn, poff, bl + 1, nbc, bd, XS, YS, lane, lane16, accB);
+                reduce_block<KS, MET>(bsw, xs, ys, xn, poff, lightL, bl, nbc, nb, bd, XS, YS, lane16, mrow, p.e1, p.e2, accA, cs);
+                if (bl + 1 >= nbc) break;
+                if (bl + 2 < nbc) issue_block<KS, MET>(bsw, xs, ys, xn, poff, bl + 2, nbc, bd, XS, YS, lane, lane16, accA);
+                reduce_block<KS, MET>(bsw, xs, ys, xn, poff, lightL, bl + 1, nbc, nb, bd, XS, YS, lane16, mrow, p.e1, p.e2, accB, cs);
+            }
+        } else {
+            for (int bl = 0; bl < nbc; ++bl) {
+                v4f acc[16];
+                issue_block<KS, MET>(bsw, xs, ys, xn, poff, bl, nbc, bd, XS, YS, lane, lane16, acc);
+                reduce_block<KS, MET>(bsw, xs, ys, xn, poff, lightL, bl, nbc, nb, bd, XS, YS, lane16, mrow, p.e1, p.e2, acc, cs);
+            }
         }
-#else
-        for (int bl = 0; bl < nbc; ++bl) {
-            v4f acc[16];
-            issue_block<KS>(bsw, xs, xn, poff, bl, nbc, bd, XS, lane, lane16, acc);
-            reduce_block<KS>(bsw, xs, xn, poff, lightL, bl, nbc, nb, bd, XS, lane16, mrow, p.e1, p.e2, acc, cs);
-        }
-#endif
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -576,18 +653,30 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
         }
         SSQ_UNSUPPORTED(mfma_enc_smem(*a, nbc, KS) <= kMaxSmem, "head_dim too large for the MFMA encode");
         mp.nbc = nbc;
+        mp.ys_stride = mfma_ys_stride(*a, nbc);
         const int chunks = mp.n_light > 0 ? (mp.n_light + nbc - 1) / nbc : 1;
         const int keys_wg = kMfmaWaves * kRounds * 16;
         dim3 grid((a->seq_len + keys_wg - 1) / keys_wg, a->batch * a->num_kv_heads, chunks);
         const size_t smem = mfma_enc_smem(*a, nbc, KS);
         int rc;
-        switch (KS) {
-            case 1: { static bool d = false; rc = set_smem_attr(k_encode_mfma<1>, d); if (rc) return rc;
-                      hipLaunchKernelGGL(k_encode_mfma<1>, grid, dim3(kMfmaWaves * SSQ_WAVE), smem, st, mp); break; }
-            case 2: { static bool d = false; rc = set_smem_attr(k_encode_mfma<2>, d); if (rc) return rc;
-                      hipLaunchKernelGGL(k_encode_mfma<2>, grid, dim3(kMfmaWaves * SSQ_WAVE), smem, st, mp); break; }
-            default: { static bool d = false; rc = set_smem_attr(k_encode_mfma<3>, d); if (rc) return rc;
-                       hipLaunchKernelGGL(k_encode_mfma<3>, grid, dim3(kMfmaWaves * SSQ_WAVE), smem, st, mp); break; }
+        const int sel = KS * 2 + (a->metric ? 1 : 0);
+        switch (sel) {
+#define SSQ_ENC_LAUNCH(KSV, MV)                                                                        \
+    case KSV * 2 + MV: {                                                                               \
+        static bool d = false;                                                                         \
+        rc = set_smem_attr(k_encode_mfma<KSV, MV>, d);                                                 \
+        if (rc) return rc;                                                                             \
+        hipLaunchKernelGGL((k_encode_mfma<KSV, MV>), grid, dim3(kMfmaWaves * SSQ_WAVE), smem, st, mp); \
+        break;                                                                                         \
+    }
+            SSQ_ENC_LAUNCH(1, false)
+            SSQ_ENC_LAUNCH(1, true)
+            SSQ_ENC_LAUNCH(2, false)
+            SSQ_ENC_LAUNCH(2, true)
+            SSQ_ENC_LAUNCH(3, false)
+            SSQ_ENC_LAUNCH(3, true)
+#undef SSQ_ENC_LAUNCH
+            default: return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA encode: unsupported block_dim");
         }
         return ssq_check_hip(hipGetLastError(), "k_encode_mfma launch");
     }

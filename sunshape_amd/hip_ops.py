@@ -270,13 +270,16 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
 def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
            heavy: Optional[Sequence[bool]] = None, pt_dtype: Optional[torch.dtype] = None, pt_dense: bool = False,
            codes_out: Optional[torch.Tensor] = None, pt_out: Optional[torch.Tensor] = None,
-           slot_mapping: Optional[torch.Tensor] = None, kernel: int = 0):
+           slot_mapping: Optional[torch.Tensor] = None, metric: Optional[torch.Tensor] = None, kernel: int = 0):
     """Nearest-codeword encode of keys [B, Hkv, S, D] -> (codes uint8 [B, Hkv, S, nb], pt or None).
 
     Passthrough values (heavy blocks) are [B, Hkv, S, n_heavy, bd] (compact) or
     [B, Hkv, S, nb, bd] zero-filled (pt_dense, the reference's layout).  With
     slot_mapping [B, S] (int64) the outputs go into caller-provided pages:
-    codes_out [P, Hkv, page, nb], pt_out [P, Hkv, page, slots, bd].
+    codes_out [P, Hkv, page, nb], pt_out [P, Hkv, page, slots, bd].  Without it, codes_out /
+    pt_out (compact) may be given as [B, Hkv, S, ...] views to write into instead of allocating.
+    metric: SunShape-Pro block metric E [D, D] or per KV head [Hkv, D, D] (fp32); distances are
+    taken between E_b x and E_b c (sunshape/codec.py:375-376).  None = identity.
     Reference: sunshape/codec.py:362-385, sunshape/vllm_attn_backend.py:101-123.
     """
     _on_gpu("key_states", keys)
@@ -287,11 +290,33 @@ def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
     w0, w1 = N.heavy_mask_words(heavy)
     n_heavy = bin(w0).count("1") + bin(w1).count("1")
     pt_dtype = pt_dtype or keys.dtype
+    metric_sh = 0
+    if metric is not None:
+        _on_gpu("metric", metric)
+        metric = metric.to(torch.float32).contiguous()
+        _require(metric.shape[-2:] == (D, D) and metric.ndim in (2, 3), f"metric must be [{D}, {D}] or [Hkv, {D}, {D}]")
+        if metric.ndim == 3:
+            _require(metric.shape[0] == Hkv, f"per-head metric holds {metric.shape[0]} heads, keys have {Hkv}")
+            metric_sh = D * D
     if slot_mapping is None:
-        codes = torch.empty((B, Hkv, S, nb), device=keys.device, dtype=torch.uint8)
+        if codes_out is not None:  # caller's buffer (e.g. a slice of a preallocated cache)
+            _on_gpu("codes_out", codes_out)
+            _require(codes_out.dtype == torch.uint8 and tuple(codes_out.shape) == (B, Hkv, S, nb)
+                     and codes_out.stride(3) == 1, f"codes_out must be uint8 [{B}, {Hkv}, {S}, {nb}] with unit last stride")
+            codes = codes_out
+        else:
+            codes = torch.empty((B, Hkv, S, nb), device=keys.device, dtype=torch.uint8)
         pt = None
         if n_heavy:
-            if pt_dense:
+            if pt_out is not None:
+                _on_gpu("pt_out", pt_out)
+                slots = nb if pt_dense else n_heavy
+                _require(tuple(pt_out.shape) == (B, Hkv, S, slots, bd) and pt_out.stride(4) == 1
+                         and pt_out.stride(3) == bd, f"pt_out must be [{B}, {Hkv}, {S}, {slots}, {bd}] with packed rows")
+                _require(not pt_dense, "pt_out takes the compact passthrough layout")
+                pt = pt_out
+                pt_dtype = pt.dtype
+            elif pt_dense:
                 pt = torch.zeros((B, Hkv, S, nb, bd), device=keys.device, dtype=pt_dtype)
             else:
                 pt = torch.empty((B, Hkv, S, n_heavy, bd), device=keys.device, dtype=pt_dtype)
@@ -317,6 +342,7 @@ def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
         keys=N.ptr(keys), k_dtype=N.dtype_code(keys.dtype), k_sb=keys.stride(0), k_sh=keys.stride(1), k_ss=keys.stride(2),
         batch=B, num_kv_heads=Hkv, seq_len=S, head_dim=D,
         perm=N.ptr(perm), perm_sh=perm_sh, cent=N.ptr(cent), cent_sh=cent_sh,
+        metric=N.ptr(metric), metric_sh=metric_sh,
         block_dim=bd, n_blocks=nb, n_centroids=nc,
         codes=N.ptr(codes), c_sb=c_str[0], c_sh=c_str[1], c_st=c_str[2],
         pt=N.ptr(pt), pt_dtype=N.dtype_code(pt_dtype), pt_dense=1 if pt_dense else 0,

@@ -143,7 +143,8 @@ def quantize_key_states(layer_idx: int, key_states: torch.Tensor) -> SunShapeQua
     keys = key_states.to(codec.device)
     if keys.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         keys = keys.float()
-    codes, pt = hip_ops.encode(keys, perm, cent, heavy=heavy, pt_dtype=torch.float32, pt_dense=True)
+    metric = codec.encode_metric() if hasattr(codec, "encode_metric") else None
+    codes, pt = hip_ops.encode(keys, perm, cent, heavy=heavy, pt_dtype=torch.float32, pt_dense=True, metric=metric)
     mixed = codec.mode == "profileperm_mixed_precision"
     pblocks = codec.mixed_high_precision_blocks.detach().clone() if mixed else None
     heads = []

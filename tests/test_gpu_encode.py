@@ -129,3 +129,79 @@ def test_config5_full_encode():
         ref, rpt = O.encode(keys[b, kv, rows], perm, cent[kv], hv)
         assert np.array_equal(got[b, kv, rows], ref)
         assert np.array_equal(np_of(pt[b, kv, rows]), rpt[:, hv])
+
+
+# ---------------------------------------------------------------------------
+# SunShape-Pro block metric (sunshape/codec.py:375-376)
+# ---------------------------------------------------------------------------
+
+def _pro_case(D, bd, seed, n=2500, near_identity=False):
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(D)
+    sig = np.exp(rng.uniform(np.log(0.1), np.log(3), D)).astype(np.float32)
+    cent = (rng.standard_normal((D // bd, 256, bd)) * sig[perm].reshape(D // bd, 1, bd)).astype(np.float32)
+    keys = O.bf16_round((rng.standard_normal((n, D)) * sig).astype(np.float32))
+    E = rng.standard_normal((D, D)).astype(np.float32)
+    if near_identity:
+        E = (np.eye(D) + 0.3 * E).astype(np.float32)
+    return keys, perm, cent, E
+
+
+@pytest.mark.parametrize("D,bd", [(64, 2), (64, 4), (64, 8), (48, 3), (64, 16)])
+def test_metric_encode_kernels_vs_oracle_bit_exact(D, bd):
+    log(f"metric encode D={D} bd={bd}")
+    keys, perm, cent, E = _pro_case(D, bd, D * 7 + bd)
+    ref, _ = O.encode(keys, perm, cent, metric=E)
+    kt = torch.from_numpy(keys).to(DEV).to(torch.bfloat16)[None, None]
+    args = (torch.from_numpy(perm).to(DEV), torch.from_numpy(cent).to(DEV))
+    Et = torch.from_numpy(E).to(DEV)
+    for kernel in ([1, 2] if bd <= 10 else [1]):
+        codes, _ = hip_ops.encode(kt, *args, metric=Et, kernel=kernel)
+        got = np_of(codes[0, 0])
+        assert np.array_equal(got, ref), (kernel, int((got != ref).sum()))
+
+
+def test_metric_encode_mixed_per_head_and_paged():
+    """Heavy blocks (raw values, not E_b x), per-KV-head metrics [Hkv, D, D], paged output."""
+    log("metric encode mixed/per-head/paged")
+    D, bd, Hkv, S = 64, 2, 2, 160
+    keys0, perm, cent0, E0 = _pro_case(D, bd, 91, n=S, near_identity=True)
+    keys1, _, cent1, E1 = _pro_case(D, bd, 92, n=S, near_identity=True)
+    heavy = np.zeros(D // bd, dtype=bool)
+    heavy[[1, 5, 17]] = True
+    keys = torch.from_numpy(np.stack([keys0, keys1])).to(DEV).to(torch.bfloat16)[None]
+    cent = torch.from_numpy(np.stack([cent0, cent1])).to(DEV)
+    Et = torch.from_numpy(np.stack([E0, E1])).to(DEV)
+    permt = torch.from_numpy(perm).to(DEV)
+    codes, pt = hip_ops.encode(keys, permt, cent, heavy=heavy.tolist(), metric=Et, pt_dtype=torch.float32,
+                               pt_dense=True)
+    for h, (k, c, E) in enumerate(((keys0, cent0, E0), (keys1, cent1, E1))):
+        ref, rpt = O.encode(k, perm, c, heavy, metric=E)
+        assert np.array_equal(np_of(codes[0, h]), ref)
+        assert np.array_equal(np_of(pt[0, h]), rpt)
+    page = 16
+    P = S // page + 2
+    slots = (torch.randperm(P, generator=torch.Generator().manual_seed(4))[: S // page][:, None] * page
+             + torch.arange(page)).reshape(1, S).to(torch.int64).to(DEV)
+    cp = torch.zeros(P, Hkv, page, D // bd, dtype=torch.uint8, device=DEV)
+    pp = torch.zeros(P, Hkv, page, 3, bd, dtype=torch.float32, device=DEV)
+    hip_ops.encode(keys, permt, cent, heavy=heavy.tolist(), metric=Et, codes_out=cp, pt_out=pp, slot_mapping=slots)
+    s = slots[0].cpu()
+    got = cp[s // page, :, s % page].permute(1, 0, 2)
+    assert torch.equal(got, codes[0])
+
+
+def test_pro_codec_quantize_matches_oracle():
+    from sunshape_amd.codec import SunShapeBlockCodec
+
+    log("pro codec quantize")
+    D, bd = 64, 4
+    keys, perm, cent, E = _pro_case(D, bd, 93, n=1500, near_identity=True)
+    codec = SunShapeBlockCodec.from_buffers(torch.from_numpy(perm), torch.from_numpy(cent),
+                                            mode="profileperm_localmetric_dsq", metric=torch.from_numpy(E), device=DEV)
+    qz = codec.quantize(torch.from_numpy(keys).to(DEV))
+    ref, _ = O.encode(keys, perm, cent, metric=E)
+    assert np.array_equal(np_of(qz.indices), ref)
+    # decode-side arithmetic ignores E: k_hat = C[b, idx] in the original basis
+    k_hat = np_of(codec.dequantize(qz))
+    assert np.array_equal(k_hat, O.dequantize(ref, cent, perm))

@@ -69,10 +69,27 @@ def test_unsupported_modes_raise_with_reason():
     with pytest.raises(RuntimeError, match="rotation"):
         c.quantize(torch.randn(4, 64))
     pro = _codec(mode="profileperm_localmetric_dsq")
-    with pytest.raises(RuntimeError, match="metric"):
-        pro.quantize(torch.randn(4, 64))
     with pytest.raises(NotImplementedError):
         pro.fit(torch.randn(4, 64), torch.randn(4, 64))
+    # no silent CPU path: a CPU tensor reaches the device check and raises
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        pro.quantize(torch.randn(4, 64))
+
+
+def test_encode_metric_selection():
+    """SunShape-Pro and legacy modes encode under E (sunshape/codec.py:375-376); the others do not."""
+    E = torch.randn(64, 64)
+    for mode, has in (("profileperm_localmetric_dsq", True), ("legacy_strict", True),
+                      ("profileperm_baseline", False), ("profileperm_mixed_precision", False),
+                      ("identity_baseline", False)):
+        cb = synthetic.make_codebook(1, 64, 8, 3)
+        c = SunShapeBlockCodec.from_buffers(cb.perm[0], cb.centroids[0], mode=mode, metric=E, device="cpu")
+        m = c.encode_metric()
+        assert (m is not None) == has, mode
+        if has:
+            assert torch.equal(m, E)
+    with pytest.raises(ValueError):
+        SunShapeBlockCodec.from_buffers(torch.arange(64), torch.zeros(8, 256, 8), metric=torch.eye(32), device="cpu")
 
 
 def test_scores_gate_reasons():

@@ -134,3 +134,87 @@ def test_encode_heavy_blocks_passthrough():
     for b in np.nonzero(~heavy)[0][:5]:
         ref = torch.cdist(torch.from_numpy(xp[:, b].copy()), torch.from_numpy(cent[b])).argmin(-1).numpy()
         _assert_only_sqrt_ties(xp[:, b].copy(), cent[b], codes[:, b], ref)
+
+
+# ---------------------------------------------------------------------------
+# SunShape-Pro block metric: argmin_c cdist(x_b @ E_b^T, C_b @ E_b^T) (sunshape/codec.py:375-376)
+# ---------------------------------------------------------------------------
+
+def _metric_case(seed, n=800, D=32, bd=4, nc=64):
+    rng = np.random.default_rng(seed)
+    keys = O.bf16_round(rng.standard_normal((n, D)).astype(np.float32))
+    perm = rng.permutation(D)
+    cent = rng.standard_normal((D // bd, nc, bd)).astype(np.float32)
+    E = rng.standard_normal((D, D)).astype(np.float32)  # not symmetric: a transpose would show
+    return keys, perm, cent, E
+
+
+def _gap_ok(dist, chosen, other, rel=1e-5):
+    """Two indices may differ only where their exact distances are within rounding of each other."""
+    a = dist[np.arange(len(chosen)), chosen]
+    b = dist[np.arange(len(other)), other]
+    return np.abs(a - b) <= rel * np.maximum(np.abs(a), np.abs(b)) + 1e-30
+
+
+def test_metric_identity_reproduces_plain_encode():
+    keys, perm, cent, _ = _metric_case(11)
+    c0, _ = O.encode(keys, perm, cent)
+    c1, _ = O.encode(keys, perm, cent, metric=np.eye(keys.shape[1], dtype=np.float32))
+    assert np.array_equal(c0, c1)
+
+
+def test_metric_vs_fp64_brute_force_and_torch_restatement():
+    keys, perm, cent, E = _metric_case(12)
+    D, bd = keys.shape[1], cent.shape[2]
+    codes, _ = O.encode(keys, perm, cent, metric=E)
+    xp = torch.from_numpy(keys[:, perm])
+    diffs = 0
+    for b in range(D // bd):
+        sl = slice(b * bd, (b + 1) * bd)
+        Eb = torch.from_numpy(E[sl, sl])
+        y64 = xp[:, sl].double() @ Eb.double().T
+        c64 = torch.from_numpy(cent[b]).double() @ Eb.double().T
+        dist = torch.cdist(y64, c64).pow(2).numpy()
+        brute = dist.argmin(1)
+        ref = torch.cdist(xp[:, sl] @ Eb.T, torch.from_numpy(cent[b]) @ Eb.T).argmin(-1).numpy()
+        for other in (brute, ref):
+            neq = codes[:, b] != other
+            diffs += int(neq.sum())
+            assert _gap_ok(dist, codes[:, b], other)[neq].all()
+    assert diffs <= 0.01 * keys.shape[0] * (D // bd)
+
+
+def test_metric_transposed_is_detected():
+    """Applying E_b instead of E_b^T (a plausible slip) changes many codes."""
+    keys, perm, cent, E = _metric_case(13)
+    good, _ = O.encode(keys, perm, cent, metric=E)
+    bad, _ = O.encode(keys, perm, cent, metric=np.ascontiguousarray(E.T))
+    assert (good != bad).mean() > 0.2
+
+
+def test_metric_power_of_two_scale_and_off_block_entries_invariant():
+    """2E scales every fp32 step exactly (same codes); entries outside the diagonal blocks are never read."""
+    keys, perm, cent, E = _metric_case(14)
+    bd = cent.shape[2]
+    base, _ = O.encode(keys, perm, cent, metric=E)
+    scaled, _ = O.encode(keys, perm, cent, metric=2.0 * E)
+    assert np.array_equal(base, scaled)
+    E2 = E.copy()
+    mask = np.kron(np.eye(E.shape[0] // bd), np.ones((bd, bd))).astype(bool)
+    E2[~mask] = 123.0
+    off, _ = O.encode(keys, perm, cent, metric=E2)
+    assert np.array_equal(base, off)
+
+
+def test_metric_keys_on_codewords():
+    """x = a codeword: that codeword's index (well-separated codebook, any invertible E_b)."""
+    rng = np.random.default_rng(15)
+    D, bd, nc = 16, 2, 32
+    grid = np.stack(np.meshgrid(np.arange(8), np.arange(4)), -1).reshape(-1, 2).astype(np.float32) * 4.0
+    cent = np.stack([grid[rng.permutation(nc)] for _ in range(D // bd)])
+    idx = rng.integers(0, nc, size=(50, D // bd))
+    xp = np.concatenate([cent[b][idx[:, b]] for b in range(D // bd)], axis=1)
+    perm = np.arange(D)
+    E = (np.eye(D) + 0.1 * rng.standard_normal((D, D))).astype(np.float32)
+    codes, _ = O.encode(xp.astype(np.float32), perm, cent, metric=E)
+    assert np.array_equal(codes, idx.astype(np.uint8))
