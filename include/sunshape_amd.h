@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SSQ_ABI_VERSION 2
+#define SSQ_ABI_VERSION 3
 
 enum ssq_status {
     SSQ_OK = 0,
@@ -100,6 +100,11 @@ typedef struct ssq_decode_args {
     /* tuning: 0 = library heuristic */
     int32_t num_splits;
     int32_t kernel;      /* 0 auto, 1 generic LUT/VALU kernel, 2 MFMA paged kernel */
+    /* code storage: 0 = one uint8 per block (c_* strides in bytes); 1..8 = packing in
+     * uint32 words, vpe = 32 / code_bits codes per word, block blk = p*vpe + v at bits
+     * [v*code_bits, (v+1)*code_bits) of word p (the layout of sunshape/triton_kernels.py:213-283);
+     * c_* strides then count words.  Packed codes take the generic kernel. */
+    int32_t code_bits;
 } ssq_decode_args;
 
 /* Bytes of device workspace ssq_decode / ssq_attention_scores need (0 if none). */
@@ -162,6 +167,16 @@ int ssq_dequantize(const uint8_t* codes, int64_t c_st, int32_t tokens,
                    int32_t n_centroids, const uint64_t* heavy_mask, int32_t pt_dense,
                    const void* pt, int32_t pt_dtype, int64_t pt_st,
                    float* out, int64_t o_st, void* stream);
+
+/* Pack uint8 codes [rows, n_blocks] (row stride c_st bytes) into uint32 words
+ * [rows, ceil(n_blocks / (32 / bits))] (row stride o_st words) in the code_bits layout above.
+ * Precondition: every code < 2^bits (bits above are dropped); unused high bits of a word are 0.
+ * The reference has the reader of this layout (sunshape/triton_kernels.py:213-283) but no writer. */
+int ssq_pack_codes(const uint8_t* codes, int64_t c_st, int64_t rows, int32_t n_blocks, int32_t bits,
+                   uint32_t* out, int64_t o_st, void* stream);
+/* Inverse of ssq_pack_codes. */
+int ssq_unpack_codes(const uint32_t* packed, int64_t p_st, int64_t rows, int32_t n_blocks, int32_t bits,
+                     uint8_t* out, int64_t o_st, void* stream);
 
 const char* ssq_last_error(void);
 int ssq_abi_version(void);

@@ -265,6 +265,39 @@ def decode_attention(q: np.ndarray, codes: np.ndarray, v: np.ndarray,
 
 
 # ----------------------------------------------------------------------------
+# sub-byte packed codes (sunshape/triton_kernels.py:250-266 reads this layout)
+# ----------------------------------------------------------------------------
+
+def pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
+    """uint8 [..., nb] -> int32 [..., ceil(nb / vpe)], vpe = 32 // bits.
+
+    Block b = p*vpe + v sits in bits [v*bits, (v+1)*bits) of word p, so that the
+    reference's reader ``(packed[t, p] >> (v * bits)) & ((1 << bits) - 1)``
+    (sunshape/triton_kernels.py:251-266) returns it.
+    """
+    codes = np.asarray(codes, dtype=np.uint8)
+    nb = codes.shape[-1]
+    vpe = 32 // bits
+    nw = (nb + vpe - 1) // vpe
+    words = np.zeros(codes.shape[:-1] + (nw,), dtype=np.uint64)
+    for b in range(nb):
+        p, v = divmod(b, vpe)
+        words[..., p] |= (codes[..., b].astype(np.uint64) & ((1 << bits) - 1)) << np.uint64(v * bits)
+    return words.astype(np.uint32).view(np.int32)
+
+
+def unpack_codes(words: np.ndarray, nb: int, bits: int) -> np.ndarray:
+    """The reference reader (sunshape/triton_kernels.py:251-266) applied to every block."""
+    w = np.asarray(words).view(np.uint32).astype(np.uint64)
+    vpe = 32 // bits
+    out = np.empty(w.shape[:-1] + (nb,), dtype=np.uint8)
+    for b in range(nb):
+        p, v = divmod(b, vpe)
+        out[..., b] = (w[..., p] >> np.uint64(v * bits)) & np.uint64((1 << bits) - 1)
+    return out
+
+
+# ----------------------------------------------------------------------------
 # paged layout (vLLM-style pages; no counterpart in the reference)
 # ----------------------------------------------------------------------------
 

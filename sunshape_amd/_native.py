@@ -30,7 +30,7 @@ SSQ_CONTIGUOUS, SSQ_PAGED = 0, 1
 
 DTYPE_CODE = {torch.float32: SSQ_F32, torch.bfloat16: SSQ_BF16, torch.float16: SSQ_F16}
 
-ABI_VERSION = 2  # SSQ_ABI_VERSION in include/sunshape_amd.h
+ABI_VERSION = 3  # SSQ_ABI_VERSION in include/sunshape_amd.h
 
 # every function include/sunshape_amd.h declares
 EXPORTED_SYMBOLS = (
@@ -40,6 +40,8 @@ EXPORTED_SYMBOLS = (
     "ssq_lut_build",
     "ssq_encode",
     "ssq_dequantize",
+    "ssq_pack_codes",
+    "ssq_unpack_codes",
     "ssq_last_error",
     "ssq_abi_version",
 )
@@ -75,6 +77,7 @@ class DecodeArgs(ctypes.Structure):
         ("lse", _vp),
         ("scores", _vp), ("s_sb", _i64), ("s_sh", _i64), ("s_sl", _i64),
         ("num_splits", _i32), ("kernel", _i32),
+        ("code_bits", _i32),
     ]
 
     def __init__(self, **kw):
@@ -128,6 +131,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ssq_dequantize.argtypes = [_vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _i64,
                                    _vp, _i64, _vp]
     lib.ssq_dequantize.restype = ctypes.c_int
+    lib.ssq_pack_codes.argtypes = [_vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]
+    lib.ssq_pack_codes.restype = ctypes.c_int
+    lib.ssq_unpack_codes.argtypes = [_vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]
+    lib.ssq_unpack_codes.restype = ctypes.c_int
     lib.ssq_last_error.argtypes = []
     lib.ssq_last_error.restype = ctypes.c_char_p
     lib.ssq_abi_version.argtypes = []

@@ -165,17 +165,17 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
 #pragma unroll
         for (int r = 0; r < RP; ++r) s[r] = 0.f;
         if (valid) {
-            const uint8_t* crow;
-            int64_t pt_base = 0;
+            int64_t cofs, pt_base;  // code row offset (bytes, or words when packed)
             if (PAGED) {
                 const int page = a.block_table[(int64_t)b * a.bt_sb + t / a.page_size];
                 const int off = t - (t / a.page_size) * a.page_size;
-                crow = a.codes + (int64_t)page * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)off * a.c_st;
+                cofs = (int64_t)page * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)off * a.c_st;
                 pt_base = (int64_t)page * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)off * a.pt_st;
             } else {
-                crow = a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)t * a.c_st;
+                cofs = (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)t * a.c_st;
                 pt_base = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)t * a.pt_st;
             }
+            const uint8_t* crow = a.codes + cofs;
             auto add_block = [&](int blk, uint32_t code) {
                 if (ssq_is_heavy(a.heavy_mask[0], a.heavy_mask[1], blk)) {
                     const int64_t po = pt_base + (int64_t)heavy_slot(a, blk) * bd;
@@ -205,7 +205,15 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
                     }
                 }
             };
-            if (p.word_codes) {
+            if (a.code_bits) {  // sub-byte codes packed into uint32 words
+                const uint32_t* w = reinterpret_cast<const uint32_t*>(a.codes) + cofs;
+                const int bits = a.code_bits, vpe = 32 / bits;
+                const uint32_t msk = (1u << bits) - 1u;
+                for (int pi = 0, blk = 0; blk < nb; ++pi) {
+                    const uint32_t word = w[pi];
+                    for (int v = 0; v < vpe && blk < nb; ++v, ++blk) add_block(blk, (word >> (v * bits)) & msk);
+                }
+            } else if (p.word_codes) {
                 const uint32_t* w = reinterpret_cast<const uint32_t*>(crow);
                 for (int wi = 0; wi < (nb >> 2); ++wi) {
                     const uint32_t word = w[wi];
@@ -444,6 +452,12 @@ int validate(const ssq_decode_args* a, bool need_v) {
     SSQ_REQUIRE(a->head_dim <= 1024, "head_dim > 1024");
     SSQ_REQUIRE(a->n_centroids >= 1 && a->n_centroids <= 256, "n_centroids must be in [1, 256] for uint8 codes");
     SSQ_REQUIRE(a->n_blocks <= 128, "n_blocks > 128");
+    SSQ_REQUIRE(a->code_bits >= 0 && a->code_bits <= 8, "code_bits must be 0 (uint8) or 1..8 (packed)");
+    if (a->code_bits) {
+        SSQ_REQUIRE(a->n_centroids <= (1 << a->code_bits), "n_centroids=%d needs more than %d-bit codes",
+                    a->n_centroids, a->code_bits);
+        SSQ_REQUIRE((uintptr_t)a->codes % 4 == 0, "packed codes must be 4-byte aligned");
+    }
     SSQ_REQUIRE(a->q_dtype >= SSQ_F32 && a->q_dtype <= SSQ_F16, "bad q_dtype");
     SSQ_REQUIRE(a->seq_len >= 0, "negative seq_len");
     const bool any_heavy = a->heavy_mask[0] || a->heavy_mask[1];
@@ -511,8 +525,8 @@ int run_generic(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipS
     dp.R = pl.R;
     dp.split_len = pl.split_len;
     dp.n_splits = pl.n_splits;
-    const bool aligned = ((uintptr_t)a->codes % 4 == 0) && a->n_blocks % 4 == 0 && a->c_st % 4 == 0 &&
-                         a->c_sh % 4 == 0 && a->c_sb % 4 == 0;
+    const bool aligned = a->code_bits == 0 && ((uintptr_t)a->codes % 4 == 0) && a->n_blocks % 4 == 0 &&
+                         a->c_st % 4 == 0 && a->c_sh % 4 == 0 && a->c_sb % 4 == 0;
     dp.word_codes = aligned ? 1 : 0;
     const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
     float* ws = reinterpret_cast<float*>(workspace);

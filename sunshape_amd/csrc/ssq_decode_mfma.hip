@@ -457,7 +457,7 @@ struct MPlan {
 };
 
 bool plan(const ssq_decode_args* a, MPlan& pl) {
-    if (a->layout != SSQ_PAGED || a->page_size != kPage) return false;
+    if (a->layout != SSQ_PAGED || a->page_size != kPage || a->code_bits != 0) return false;
     if (a->v == nullptr || (a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16)) return false;
     if (a->mask != nullptr || a->heavy_mask[0] || a->heavy_mask[1]) return false;
     if (a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;

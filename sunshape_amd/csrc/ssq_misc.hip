@@ -111,3 +111,73 @@ extern "C" int ssq_dequantize(const uint8_t* codes, int64_t c_st, int32_t tokens
                        out, o_st);
     return ssq_check_hip(hipGetLastError(), "k_dequant launch");
 }
+
+// ---------------------------------------------------------------------------
+// sub-byte code packing: word p of a row holds blocks p*vpe .. p*vpe+vpe-1, vpe = 32 / bits,
+// block p*vpe + v at bits [v*bits, (v+1)*bits)  (the layout sunshape/triton_kernels.py:250-266 reads)
+// ---------------------------------------------------------------------------
+namespace {
+
+__global__ __launch_bounds__(256) void k_pack(const uint8_t* codes, int64_t c_st, int64_t rows, int nb, int bits,
+                                              uint32_t* out, int64_t o_st) {
+    const int vpe = 32 / bits;
+    const int nw = (nb + vpe - 1) / vpe;
+    const uint32_t msk = (1u << bits) - 1u;
+    const int64_t total = rows * nw;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / nw;
+        const int w = (int)(i - r * nw);
+        uint32_t word = 0;
+        for (int v = 0; v < vpe; ++v) {
+            const int blk = w * vpe + v;
+            if (blk < nb) word |= ((uint32_t)codes[r * c_st + blk] & msk) << (v * bits);
+        }
+        out[r * o_st + w] = word;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_unpack(const uint32_t* packed, int64_t p_st, int64_t rows, int nb, int bits,
+                                                uint8_t* out, int64_t o_st) {
+    const int vpe = 32 / bits;
+    const uint32_t msk = (1u << bits) - 1u;
+    const int64_t total = rows * nb;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / nb;
+        const int blk = (int)(i - r * nb);
+        const int w = blk / vpe, v = blk - w * vpe;
+        out[r * o_st + blk] = (uint8_t)((packed[r * p_st + w] >> (v * bits)) & msk);
+    }
+}
+
+int grid_for(int64_t work) {
+    const int64_t blocks = (work + 255) / 256;
+    return (int)(blocks < 65536 ? (blocks > 0 ? blocks : 1) : 65536);
+}
+
+}  // namespace
+
+extern "C" int ssq_pack_codes(const uint8_t* codes, int64_t c_st, int64_t rows, int32_t n_blocks, int32_t bits,
+                              uint32_t* out, int64_t o_st, void* stream) {
+    SSQ_REQUIRE(bits >= 1 && bits <= 8, "bits must be in [1, 8] for uint8 codes");
+    SSQ_REQUIRE(rows >= 0 && n_blocks >= 1, "bad rows / n_blocks");
+    const int nw = (n_blocks + 32 / bits - 1) / (32 / bits);
+    SSQ_REQUIRE(c_st >= n_blocks && o_st >= nw, "row strides too small");
+    if (rows == 0) return SSQ_OK;
+    SSQ_REQUIRE(codes && out, "codes and out must be non-NULL");
+    hipLaunchKernelGGL(k_pack, dim3(grid_for(rows * nw)), dim3(256), 0, (hipStream_t)stream, codes, c_st, rows,
+                       n_blocks, bits, out, o_st);
+    return ssq_check_hip(hipGetLastError(), "k_pack launch");
+}
+
+extern "C" int ssq_unpack_codes(const uint32_t* packed, int64_t p_st, int64_t rows, int32_t n_blocks, int32_t bits,
+                                uint8_t* out, int64_t o_st, void* stream) {
+    SSQ_REQUIRE(bits >= 1 && bits <= 8, "bits must be in [1, 8] for uint8 codes");
+    SSQ_REQUIRE(rows >= 0 && n_blocks >= 1, "bad rows / n_blocks");
+    const int nw = (n_blocks + 32 / bits - 1) / (32 / bits);
+    SSQ_REQUIRE(p_st >= nw && o_st >= n_blocks, "row strides too small");
+    if (rows == 0) return SSQ_OK;
+    SSQ_REQUIRE(packed && out, "packed and out must be non-NULL");
+    hipLaunchKernelGGL(k_unpack, dim3(grid_for(rows * n_blocks)), dim3(256), 0, (hipStream_t)stream, packed, p_st,
+                       rows, n_blocks, bits, out, o_st);
+    return ssq_check_hip(hipGetLastError(), "k_unpack launch");
+}

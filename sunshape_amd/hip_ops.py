@@ -74,6 +74,57 @@ def lut_build(q: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, scale: Op
     return out
 
 
+def words_per_row(n_blocks: int, bits: int) -> int:
+    """uint32 words of one packed code row: ceil(nb / (32 // bits))."""
+    vpe = 32 // bits
+    return (n_blocks + vpe - 1) // vpe
+
+
+def _check_codes(codes: torch.Tensor, nb: int, code_bits: int) -> None:
+    if code_bits == 0:
+        _require(codes.dtype == torch.uint8, f"codes must be uint8 (n_centroids <= 256), got {codes.dtype}")
+        _require(codes.shape[-1] == nb, f"codes must be [.., {nb}] uint8")
+    else:
+        _require(1 <= code_bits <= 8, "code_bits must be 0 (uint8) or 1..8 (packed words)")
+        nw = words_per_row(nb, code_bits)
+        _require(codes.dtype == torch.int32, f"packed codes must be int32 words, got {codes.dtype}")
+        _require(codes.shape[-1] == nw, f"packed codes must be [.., {nw}] int32 for nb={nb}, bits={code_bits}")
+
+
+def pack_codes(codes: torch.Tensor, bits: int, *, check: bool = True) -> torch.Tensor:
+    """uint8 codes [..., nb] -> int32 words [..., ceil(nb / (32 // bits))].
+
+    Word p holds blocks p*vpe .. p*vpe + vpe - 1 (vpe = 32 // bits), block p*vpe + v in bits
+    [v*bits, (v+1)*bits): the layout sunshape/triton_kernels.py:250-266 unpacks.  With ``check``
+    (a device reduction and one sync) codes >= 2**bits raise instead of losing their high bits.
+    """
+    _on_gpu("codes", codes)
+    _require(codes.dtype == torch.uint8 and codes.ndim >= 1, "pack_codes takes uint8 codes [..., nb]")
+    _require(1 <= bits <= 8, "bits must be in [1, 8]")
+    if check and codes.numel() and bits < 8:
+        _require(int(codes.max()) < (1 << bits), f"codes do not fit in {bits} bits")
+    nb = codes.shape[-1]
+    flat = codes.reshape(-1, nb)
+    flat = flat if flat.stride(-1) == 1 else flat.contiguous()
+    out = torch.empty((flat.shape[0], words_per_row(nb, bits)), device=codes.device, dtype=torch.int32)
+    N.check(N.lib().ssq_pack_codes(N.ptr(flat), flat.stride(0), flat.shape[0], nb, bits, N.ptr(out), out.stride(0),
+                                   N.stream_of(codes.device)))
+    return out.view(*codes.shape[:-1], out.shape[-1])
+
+
+def unpack_codes(packed: torch.Tensor, n_blocks: int, bits: int) -> torch.Tensor:
+    """Inverse of pack_codes: int32 words [..., nw] -> uint8 codes [..., n_blocks]."""
+    _on_gpu("packed", packed)
+    _check_codes(packed, n_blocks, bits)
+    nw = packed.shape[-1]
+    flat = packed.reshape(-1, nw)
+    flat = flat if flat.stride(-1) == 1 else flat.contiguous()
+    out = torch.empty((flat.shape[0], n_blocks), device=packed.device, dtype=torch.uint8)
+    N.check(N.lib().ssq_unpack_codes(N.ptr(flat), flat.stride(0), flat.shape[0], n_blocks, bits, N.ptr(out),
+                                     out.stride(0), N.stream_of(packed.device)))
+    return out.view(*packed.shape[:-1], n_blocks)
+
+
 def _pt_args(heavy: Optional[Sequence[bool]], pt: Optional[torch.Tensor], pt_dense: bool):
     w0, w1 = N.heavy_mask_words(heavy)
     if not (w0 or w1):
@@ -86,25 +137,28 @@ def _pt_args(heavy: Optional[Sequence[bool]], pt: Optional[torch.Tensor], pt_den
 
 def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor,
                      heavy: Optional[Sequence[bool]] = None, pt: Optional[torch.Tensor] = None,
-                     pt_dense: bool = True) -> torch.Tensor:
+                     pt_dense: bool = True, code_bits: int = 0) -> torch.Tensor:
     """scores[r, t] = q_r . k_hat_t in fp32 (q in the original basis, unscaled).
 
-    q [R, D]; codes uint8 [T, nb]; pt [T, nb, bd] (dense) or [T, n_heavy, bd].
+    q [R, D]; codes uint8 [T, nb] (or int32 packed words [T, nw] with code_bits);
+    pt [T, nb, bd] (dense) or [T, n_heavy, bd].
     Reference: sunshape/triton_kernels.py:570-609 and sunshape/codec.py:403-422.
     """
     _on_gpu("query", q)
     _on_gpu("indices", codes)
     _require(q.ndim == 2, f"Expected query.ndim == 2, got {q.ndim}.")
     _require(codes.ndim == 2, f"Expected quantized_key.indices.ndim == 2, got {codes.ndim}.")
-    _require(codes.dtype == torch.uint8, f"indices must be uint8 codes (n_centroids <= 256), got {codes.dtype}")
     q = q if q.stride(-1) == 1 else q.contiguous()
     codes = codes if codes.stride(-1) == 1 else codes.contiguous()
     R, D = q.shape
     T = codes.shape[0]
     perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, None)
     _require(perm.ndim == 1 and cent.ndim == 3, "attention_scores takes one codec (perm [D], centroids [nb, nc, bd])")
-    _require(codes.shape[1] == nb, "Quantized key block count does not match codec: "
-             f"indices.shape[1]={codes.shape[1]}, codec.n_blocks={nb}.")
+    if code_bits == 0:
+        _require(codes.dtype == torch.uint8, f"indices must be uint8 codes (n_centroids <= 256), got {codes.dtype}")
+        _require(codes.shape[1] == nb, "Quantized key block count does not match codec: "
+                 f"indices.shape[1]={codes.shape[1]}, codec.n_blocks={nb}.")
+    _check_codes(codes, nb, code_bits)
     out = torch.empty((R, T), device=q.device, dtype=torch.float32)
     if R == 0 or T == 0:
         return out
@@ -116,7 +170,7 @@ def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, c
         block_dim=bd, n_blocks=nb, n_centroids=nc,
         pt_dense=ptd, pt_dtype=ptdt, pt=N.ptr(pt), pt_sb=0, pt_sh=0, pt_st=0 if pt is None else pt.stride(0),
         layout=N.SSQ_CONTIGUOUS, seq_len=T, codes=N.ptr(codes), c_sb=0, c_sh=0, c_st=codes.stride(0),
-        scores=N.ptr(out), s_sb=0, s_sh=out.stride(0), s_sl=0,
+        scores=N.ptr(out), s_sb=0, s_sh=out.stride(0), s_sl=0, code_bits=int(code_bits),
     )
     a.heavy_mask[0], a.heavy_mask[1] = hm
     N.check(N.lib().ssq_attention_scores(ctypes.byref(a), N.stream_of(q.device)))
@@ -125,7 +179,7 @@ def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, c
 
 def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
                scale: Optional[float] = None, heavy: Optional[Sequence[bool]] = None,
-               pt: Optional[torch.Tensor] = None, pt_dense: bool = False) -> torch.Tensor:
+               pt: Optional[torch.Tensor] = None, pt_dense: bool = False, code_bits: int = 0) -> torch.Tensor:
     """Raw scores for every (batch, query head) in one launch: fp32 [B, Hq, Lq, T].
 
     q [B, Hq, Lq, D]; codes [B, Hkv, T, nb] uint8; query head h reads KV head
@@ -135,7 +189,6 @@ def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: t
     for name, t in (("query", q), ("codes", codes)):
         _on_gpu(name, t)
     _require(q.ndim == 4 and codes.ndim == 4, "gqa_scores expects q [B, Hq, Lq, D] and codes [B, Hkv, T, nb]")
-    _require(codes.dtype == torch.uint8, "codes must be uint8")
     q = q if q.stride(-1) == 1 else q.contiguous()
     codes = codes if codes.stride(-1) == 1 else codes.contiguous()
     B, Hq, Lq, D = q.shape
@@ -143,7 +196,7 @@ def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: t
     _require(codes.shape[0] == B, "Quantized key batch size does not match query batch size.")
     _require(Hq % Hkv == 0, "Query head count must be divisible by kv-head count.")
     perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, Hkv)
-    _require(codes.shape[3] == nb, f"codes must be [.., {nb}]")
+    _check_codes(codes, nb, code_bits)
     out = torch.empty((B, Hq, Lq, T), device=q.device, dtype=torch.float32)
     if T == 0:
         return out
@@ -158,7 +211,7 @@ def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: t
         pt_dense=ptd, pt_dtype=ptdt, pt=N.ptr(pt), pt_sb=ps[0], pt_sh=ps[1], pt_st=ps[2],
         layout=N.SSQ_CONTIGUOUS, seq_len=T, codes=N.ptr(codes), c_sb=codes.stride(0), c_sh=codes.stride(1),
         c_st=codes.stride(2),
-        scores=N.ptr(out), s_sb=out.stride(0), s_sh=out.stride(1), s_sl=out.stride(2),
+        scores=N.ptr(out), s_sb=out.stride(0), s_sh=out.stride(1), s_sl=out.stride(2), code_bits=int(code_bits),
     )
     a.heavy_mask[0], a.heavy_mask[1] = hm
     N.check(N.lib().ssq_attention_scores(ctypes.byref(a), N.stream_of(q.device)))
@@ -171,7 +224,7 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
            heavy: Optional[Sequence[bool]] = None, pt: Optional[torch.Tensor] = None, pt_dense: bool = False,
            block_table: Optional[torch.Tensor] = None, seq_lens: Optional[torch.Tensor] = None,
            return_lse: bool = False, return_scores: bool = False,
-           num_splits: int = 0, kernel: int = 0):
+           num_splits: int = 0, kernel: int = 0, code_bits: int = 0):
     """Fused VQ-key decode attention for all batches and KV heads in one launch.
 
     q [B, Hq, Lq, D].  Contiguous layout: codes [B, Hkv, T, nb] uint8, v [B, Hkv, T, Dv],
@@ -179,6 +232,7 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
     v [P, Hkv, Dv, page] (vLLM's value layout), pt [P, Hkv, page, slots, bd],
     block_table [B, max_pages] int32, seq_lens [B] int32.
     mask: additive, broadcastable to [B, Hq, Lq, T] (converted to fp32).
+    code_bits: 0 for uint8 codes, 1..8 for int32 words from pack_codes (last dim nw).
     Returns out [B, Hq, Lq, Dv] in v's dtype, plus lse [B, Hq, Lq] / raw scores [B, Hq, Lq, T]
     (fp32) when requested.
     Reference: sunshape/vllm_attn_backend.py:216-253.
@@ -186,7 +240,6 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
     for name, t in (("query", q), ("codes", codes), ("value", v)):
         _on_gpu(name, t)
     _require(q.ndim == 4, "Quantized attention expects query/value tensors with shape [batch, heads, seq, dim].")
-    _require(codes.dtype == torch.uint8, "codes must be uint8")
     q = q if q.stride(-1) == 1 else q.contiguous()
     _require(codes.stride(-1) == 1, "codes must be contiguous in the last dim")
     B, Hq, Lq, D = q.shape
@@ -194,7 +247,8 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
     Hkv = codes.shape[1]
     _require(Hq % Hkv == 0, "Query head count must be divisible by kv-head count.")
     perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, Hkv)
-    _require(codes.ndim == 4 and codes.shape[-1] == nb, f"codes must be [.., {nb}] uint8")
+    _require(codes.ndim == 4, f"codes must be 4-D [.., {nb}]")
+    _check_codes(codes, nb, code_bits)
     if paged:
         _on_gpu("block_table", block_table)
         _require(seq_lens is not None, "paged decode needs seq_lens")
@@ -252,7 +306,7 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
         lse=N.ptr(lse),
         scores=N.ptr(scores), s_sb=scores.stride(0) if scores is not None else 0,
         s_sh=scores.stride(1) if scores is not None else 0, s_sl=scores.stride(2) if scores is not None else 0,
-        num_splits=int(num_splits), kernel=int(kernel),
+        num_splits=int(num_splits), kernel=int(kernel), code_bits=int(code_bits),
     )
     a.heavy_mask[0], a.heavy_mask[1] = hm
     L = N.lib()

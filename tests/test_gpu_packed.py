@@ -1,0 +1,89 @@
+"""Sub-byte packed codes on the GPU: pack/unpack kernels against the oracle, and scores /
+decode over packed words equal to the same kernel over uint8 codes, bit for bit."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _util import SCORE_TOL, BF16_TOL, assert_rel, log, np_of
+from oracle import vq_oracle as O
+from sunshape_amd import hip_ops, synthetic
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+@pytest.mark.parametrize("bits,nb", [(1, 33), (3, 11), (4, 32), (6, 32), (6, 8), (7, 9), (8, 16)])
+def test_pack_unpack_kernels_vs_oracle(bits, nb):
+    log(f"pack bits={bits} nb={nb}")
+    rng = np.random.default_rng(bits * 10 + nb)
+    c = rng.integers(0, 1 << bits, size=(3, 101, nb), dtype=np.uint8)
+    ct = torch.from_numpy(c).to(DEV)
+    w = hip_ops.pack_codes(ct, bits)
+    assert np.array_equal(np_of(w), O.pack_codes(c, bits))
+    assert torch.equal(hip_ops.unpack_codes(w, nb, bits), ct)
+    if bits < 8:
+        with pytest.raises(RuntimeError, match="fit"):
+            hip_ops.pack_codes(torch.full((2, nb), 1 << bits, dtype=torch.uint8, device=DEV), bits)
+
+
+def _case(nc=64, bd=2, D=64, B=2, Hkv=2, Hq=8, T=700, seed=21):
+    cb = synthetic.make_codebook(Hkv, D, bd, seed, n_centroids=nc)
+    g = torch.Generator().manual_seed(seed)
+    codes = torch.randint(0, nc, (B, Hkv, T, D // bd), generator=g, dtype=torch.uint8)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+    return cb, codes, q, v
+
+
+def test_scores_over_packed_codes_equal_uint8():
+    log("packed scores")
+    cb, codes, q, _ = _case()
+    perm, cent = cb.perm[0].to(DEV), cb.centroids[0].to(DEV)
+    c2 = codes[0, 0].to(DEV)
+    w = hip_ops.pack_codes(c2, 6)
+    qq = q[0, :, 0].float().to(DEV)
+    s8 = hip_ops.attention_scores(qq, c2, perm, cent)
+    s6 = hip_ops.attention_scores(qq, w, perm, cent, code_bits=6)
+    assert torch.equal(s8, s6)
+    ref = O.attention_scores(np_of(qq), np_of(c2), cb.centroids[0].numpy(), cb.perm[0].numpy())
+    assert_rel(np_of(s6), ref, SCORE_TOL, "packed scores vs oracle")
+    with pytest.raises(RuntimeError, match="n_centroids"):
+        hip_ops.attention_scores(qq, hip_ops.pack_codes(c2 & 31, 5), perm, cent, code_bits=5)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_decode_over_packed_codes_equals_uint8(paged):
+    log(f"packed decode paged={paged}")
+    cb, codes, q, v = _case(T=640)
+    B, Hkv, T, nb = codes.shape
+    perm, cent = cb.perm.to(DEV), cb.centroids.to(DEV)
+    scale = 1 / math.sqrt(64)
+    if not paged:
+        c8 = codes.to(DEV)
+        w = hip_ops.pack_codes(c8, 6)
+        o8, l8 = hip_ops.decode(q.to(DEV), c8, v.to(DEV), perm, cent, scale=scale, return_lse=True, kernel=1)
+        o6, l6 = hip_ops.decode(q.to(DEV), w, v.to(DEV), perm, cent, scale=scale, return_lse=True, code_bits=6)
+    else:
+        page = 16
+        n = T // page
+        P = B * n + 5
+        table = torch.randperm(P, generator=torch.Generator().manual_seed(2))[: B * n].view(B, n).to(torch.int32)
+        cp = torch.zeros(P, Hkv, page, nb, dtype=torch.uint8)
+        vp = torch.zeros(P, Hkv, 64, page, dtype=torch.bfloat16)
+        for b in range(B):
+            cp[table[b].long()] = codes[b].view(Hkv, n, page, nb).permute(1, 0, 2, 3)
+            vp[table[b].long()] = v[b].view(Hkv, n, page, 64).permute(1, 0, 3, 2)
+        lens = torch.full((B,), T, dtype=torch.int32).to(DEV)
+        cpd, vpd, tbl = cp.to(DEV), vp.to(DEV), table.to(DEV)
+        w = hip_ops.pack_codes(cpd, 6)
+        o8, l8 = hip_ops.decode(q.to(DEV), cpd, vpd, perm, cent, scale=scale, block_table=tbl, seq_lens=lens,
+                                return_lse=True, kernel=1)
+        o6, l6 = hip_ops.decode(q.to(DEV), w, vpd, perm, cent, scale=scale, block_table=tbl, seq_lens=lens,
+                                return_lse=True, code_bits=6)
+    assert torch.equal(o8, o6) and torch.equal(l8, l6)
+    ref = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
+                             cb.perm.numpy(), scale, "bf16", "bf16")
+    assert_rel(np_of(o6), ref, BF16_TOL, "packed decode vs oracle")

@@ -300,3 +300,34 @@ def test_lse_merge_equals_full_softmax():
     out, lse = O.lse_merge(np.stack(ms), np.stack(ls), np.stack(os_))
     np.testing.assert_allclose(out, ref, rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(lse, np.log(np.exp(s).sum(-1)), rtol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# packed codes (sunshape/triton_kernels.py:250-266)
+# ---------------------------------------------------------------------------
+
+def test_pack_codes_hand_example():
+    """6-bit codes, 5 per word: word0 = 1 | 2<<6 | 3<<12 | 4<<18 | 5<<24, word1 = 6 (order within a word pinned)."""
+    w = O.pack_codes(np.array([[1, 2, 3, 4, 5, 6]], dtype=np.uint8), 6)
+    assert w.shape == (1, 2)
+    assert int(w[0, 0]) == 1 | 2 << 6 | 3 << 12 | 4 << 18 | 5 << 24 and int(w[0, 1]) == 6
+
+
+def test_pack_codes_8bit_is_little_endian_byte_view():
+    rng = np.random.default_rng(0)
+    c = rng.integers(0, 256, size=(7, 32), dtype=np.uint8)
+    assert np.array_equal(O.pack_codes(c, 8), c.view("<i4"))
+
+
+@pytest.mark.parametrize("bits,nb", [(1, 33), (2, 16), (3, 11), (4, 32), (5, 7), (6, 32), (7, 9), (8, 3)])
+def test_pack_unpack_round_trip(bits, nb):
+    rng = np.random.default_rng(bits * 100 + nb)
+    c = rng.integers(0, 1 << bits, size=(2, 5, nb), dtype=np.uint8)
+    w = O.pack_codes(c, bits)
+    vpe = 32 // bits
+    assert w.shape == (2, 5, (nb + vpe - 1) // vpe) and w.dtype == np.int32
+    assert np.array_equal(O.unpack_codes(w, nb, bits), c)
+    # unused high bits of each word are zero
+    used = vpe * bits
+    if used < 32:
+        assert not (w.view(np.uint32) >> np.uint32(used)).any()
