@@ -105,9 +105,6 @@ __device__ __forceinline__ float wave_sum(float v) {
 #ifndef SSQ_STREAM_NT
 #define SSQ_STREAM_NT 1
 #endif
-#ifndef SSQ_PIPE_DEPTH
-#define SSQ_PIPE_DEPTH 2  // tiles in flight per wave
-#endif
 #ifndef SSQ_CODES_NT
 #define SSQ_CODES_NT 1
 #endif
@@ -132,34 +129,35 @@ struct TileRegs {
 template <int NB, int DT>
 __device__ __forceinline__ void issue_tile(const ssq_decode_args& a, const int* pages, int t_begin, int t_end, int tile,
                                            int lane, const uint8_t* cbase, const uint16_t* vbase, TileRegs<NB, DT>& R) {
+    // Every load is issued unconditionally (straight-line code keeps the compiler's vmcnt
+    // bookkeeping exact, so waiting for this tile never drains the next one).  Lanes past the
+    // split's end read their split's last token / 8-token chunk instead: a valid address whose
+    // data compute_tile masks (scores by `valid`, V chunks by the tail zeroing).
     const int rel = tile * kTileTok;  // tile start relative to the split
-    const int t = t_begin + rel + lane;
-    if (t < t_end) {
-        const int page = pages[(rel + lane) >> 4];
-        const uint8_t* crow = cbase + (int64_t)page * a.c_sb + (int64_t)(t & 15) * a.c_st;
-        if (NB >= 16) {
+    const int last = t_end - 1 - t_begin;
+    const int tr = min(rel + lane, last);
+    const int page = pages[tr >> 4];
+    const uint8_t* crow = cbase + (int64_t)page * a.c_sb + (int64_t)((t_begin + tr) & 15) * a.c_st;
+    if (NB >= 16) {
 #pragma unroll
-            for (int i = 0; i < NB / 16; ++i) {
+        for (int i = 0; i < NB / 16; ++i) {
 #if SSQ_CODES_NT
-                const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(crow) + i);
-                R.c[i] = make_uint4(v.x, v.y, v.z, v.w);
+            const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(crow) + i);
+            R.c[i] = make_uint4(v.x, v.y, v.z, v.w);
 #else
-                R.c[i] = reinterpret_cast<const uint4*>(crow)[i];
+            R.c[i] = reinterpret_cast<const uint4*>(crow)[i];
 #endif
-            }
-        } else {
-            R.c8 = *reinterpret_cast<const uint2*>(crow);
         }
+    } else {
+        R.c8 = *reinterpret_cast<const uint2*>(crow);
     }
     const int kchunk = 8 * (lane >> 4);
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-        const int r = rel + 32 * g + kchunk;
-        if (t_begin + r < t_end) {
-            const uint16_t* src = vbase + (int64_t)pages[r >> 4] * a.v_sb + (r & 15);
+        const int r = min(rel + 32 * g + kchunk, last & ~7);
+        const uint16_t* src = vbase + (int64_t)pages[r >> 4] * a.v_sb + (r & 15);
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) R.v[g][dt] = load_stream(src + (int64_t)(16 * dt) * a.v_st);
-        }
+        for (int dt = 0; dt < DT; ++dt) R.v[g][dt] = load_stream(src + (int64_t)(16 * dt) * a.v_st);
     }
 }
 
@@ -174,35 +172,56 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
     float s[RP];
 #pragma unroll
     for (int r = 0; r < RP; ++r) s[r] = 0.f;
-    if (valid) {
+    {
+        // LUT gathers a batch of KB blocks at a time: all KB reads are issued before the first
+        // is consumed (one wave per SIMD hides no LDS latency otherwise); the sums still run in
+        // block order from 0.  Lanes past the end gather too (their codes are a valid token's)
+        // and are dropped by `valid` below.
+        constexpr int KB = RP >= 8 ? 4 : 8;
+        constexpr int NV = RP >= 4 ? RP / 4 : 1;  // float4 (or one float2 / float) per block
 #pragma unroll
-        for (int wi = 0; wi < NB / 4; ++wi) {
-            uint32_t word;
-            if (NB >= 16) {
-                const uint4 c = R.c[wi >> 2];
-                word = (wi & 3) == 0 ? c.x : (wi & 3) == 1 ? c.y : (wi & 3) == 2 ? c.z : c.w;
-            } else {
-                word = (wi & 1) ? R.c8.y : R.c8.x;
-            }
+        for (int b0 = 0; b0 < NB; b0 += KB) {
+            float4 ev[KB][NV];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int blk = 4 * wi + k;
-                const uint32_t code = (word >> (8 * k)) & 0xFFu;
+            for (int k = 0; k < KB; ++k) {
+                const int blk = b0 + k;
+                const int wi = blk >> 2;
+                uint32_t word;
+                if (NB >= 16) {
+                    const uint4 c = R.c[wi >> 2];
+                    word = (wi & 3) == 0 ? c.x : (wi & 3) == 1 ? c.y : (wi & 3) == 2 ? c.z : c.w;
+                } else {
+                    word = (wi & 1) ? R.c8.y : R.c8.x;
+                }
+                const uint32_t code = (word >> (8 * (blk & 3))) & 0xFFu;
                 const float* e = lut + ((size_t)blk * kNC + code) * RP;
                 if (RP >= 4) {
 #pragma unroll
-                    for (int r = 0; r < RP; r += 4) {
-                        const float4 v = *reinterpret_cast<const float4*>(e + r);
-                        s[r] += v.x; s[r + 1] += v.y; s[r + 2] += v.z; s[r + 3] += v.w;
-                    }
+                    for (int j = 0; j < NV; ++j) ev[k][j] = *reinterpret_cast<const float4*>(e + 4 * j);
                 } else if (RP == 2) {
                     const float2 v = *reinterpret_cast<const float2*>(e);
-                    s[0] += v.x; s[1] += v.y;
+                    ev[k][0] = make_float4(v.x, v.y, 0.f, 0.f);
                 } else {
-                    s[0] += e[0];
+                    ev[k][0] = make_float4(e[0], 0.f, 0.f, 0.f);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
+                if (RP >= 4) {
+#pragma unroll
+                    for (int j = 0; j < NV; ++j) {
+                        s[4 * j] += ev[k][j].x; s[4 * j + 1] += ev[k][j].y;
+                        s[4 * j + 2] += ev[k][j].z; s[4 * j + 3] += ev[k][j].w;
+                    }
+                } else if (RP == 2) {
+                    s[0] += ev[k][0].x; s[1] += ev[k][0].y;
+                } else {
+                    s[0] += ev[k][0].x;
                 }
             }
         }
+    }
+    if (valid) {
         if (a.scores) {
 #pragma unroll
             for (int r = 0; r < RP; ++r) {
@@ -267,6 +286,87 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
     __builtin_amdgcn_wave_barrier();
 }
 
+// vector of N floats from memory (N = 1, 2, 4 or a multiple of 4; 4N-byte aligned)
+template <int N>
+__device__ __forceinline__ void load_vec(const float* __restrict__ src, float (&dst)[N]) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(src + i);
+            dst[i] = v.x; dst[i + 1] = v.y; dst[i + 2] = v.z; dst[i + 3] = v.w;
+        }
+    } else if constexpr (N == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(src);
+        dst[0] = v.x; dst[1] = v.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) dst[i] = src[i];
+    }
+}
+
+// LUT[e][r] = sum_d qp[r][blk*BD + d] * C[e][d] for this thread's entries e = tid + k*kThreads
+// (blk = e / 256): FMA chain over d from the first product (triton_kernels.py:381-408).  A batch
+// of entries loads its codewords and query sub-vectors as vectors before any arithmetic, so the
+// build costs a few memory / LDS latencies instead of one per element.
+template <int RP, int NB, int BD>
+__device__ __forceinline__ void build_lut(const float* __restrict__ cent, const float* __restrict__ qp,
+                                          float* __restrict__ lut, int D, int tid) {
+    constexpr int kPer = NB * kNC / kThreads;
+    constexpr int kB = kPer < 128 / BD ? kPer : 128 / BD;  // up to 128 codeword floats in flight
+#pragma unroll
+    for (int k0 = 0; k0 < kPer; k0 += kB) {
+        float c[kB][BD];
+#pragma unroll
+        for (int kk = 0; kk < kB; ++kk) {
+            if (k0 + kk < kPer) load_vec<BD>(cent + (int64_t)(tid + (k0 + kk) * kThreads) * BD, c[kk]);
+        }
+#pragma unroll
+        for (int kk = 0; kk < kB; ++kk) {
+            if (k0 + kk >= kPer) break;
+            const int e = tid + (k0 + kk) * kThreads;
+            const float* qb = qp + (e / kNC) * BD;
+            float acc[RP];
+#pragma unroll
+            for (int r = 0; r < RP; ++r) {
+                float qv[BD];
+                load_vec<BD>(qb + r * D, qv);
+                float t = qv[0] * c[kk][0];
+#pragma unroll
+                for (int d = 1; d < BD; ++d) t = fmaf(qv[d], c[kk][d], t);
+                acc[r] = t;
+            }
+            if constexpr (RP % 4 == 0) {
+#pragma unroll
+                for (int r = 0; r < RP; r += 4)
+                    *reinterpret_cast<float4*>(lut + (size_t)e * RP + r) = make_float4(acc[r], acc[r + 1], acc[r + 2], acc[r + 3]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < RP; ++r) lut[(size_t)e * RP + r] = acc[r];
+            }
+        }
+    }
+}
+
+// any block_dim: one element at a time
+template <int RP, int NB>
+__device__ void build_lut_any(const float* __restrict__ cent, const float* __restrict__ qp, float* __restrict__ lut,
+                              int D, int bd, int tid) {
+    for (int e = tid; e < NB * kNC; e += kThreads) {
+        const float* c = cent + (int64_t)e * bd;
+        const float* qb = qp + (e / kNC) * bd;
+        float acc[RP];
+#pragma unroll
+        for (int r = 0; r < RP; ++r) acc[r] = qb[r * D] * c[0];
+        for (int d = 1; d < bd; ++d) {
+            const float cd = c[d];
+#pragma unroll
+            for (int r = 0; r < RP; ++r) acc[r] = fmaf(qb[r * D + d], cd, acc[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < RP; ++r) lut[(size_t)e * RP + r] = acc[r];
+    }
+}
+
 template <int RP, int DT, int VT, int NB>
 __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     extern __shared__ __align__(16) float smem[];
@@ -289,21 +389,52 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     uint16_t* pstrip = reinterpret_cast<uint16_t*>(smem + pstrip_offset(a, RP)) + wave * RP * kTileTok;
     int* pages = reinterpret_cast<int*>(smem + pages_offset(a, RP));
 
-    // ---- block-table slice, scaled permuted query rows, LUT
+    // ---- prologue: block-table slice, scaled permuted query rows, LUT (the loads of each
+    // stage are all issued before any is consumed)
     const int32_t* btab = a.block_table + (int64_t)b * a.bt_sb + t_begin / kPage;
     const int n_pages = t_end > t_begin ? (t_end - t_begin + kPage - 1) / kPage : 0;
-    for (int i = tid; i < n_pages; i += kThreads) pages[i] = btab[i];
-    const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
-    for (int e = tid; e < RP * D; e += kThreads) {
-        const int r = e / D, j = e - r * D;
-        float v = 0.f;
-        if (r < nr) {
-            const int g = r / a.q_len, qi = r - g * a.q_len;
-            const int h = kv * p.G + g;
-            v = ssq_load_elem(a.q, a.q_dtype, (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl + perm[j]);
-            if (a.has_scale) v = ssq_round_to(v * a.scale, a.q_dtype);
+    const float* cent = a.cent + (int64_t)kv * a.cent_sh;
+    // block-table slice: kBT entries per thread per pass, all loads issued before the stores
+    constexpr int kBT = 8;
+    for (int base = 0; base < n_pages; base += kBT * kThreads) {
+        int ent[kBT];
+#pragma unroll
+        for (int k = 0; k < kBT; ++k) {
+            const int i = base + k * kThreads + tid;
+            ent[k] = i < n_pages ? btab[i] : 0;
         }
-        qp[e] = v;
+#pragma unroll
+        for (int k = 0; k < kBT; ++k) {
+            const int i = base + k * kThreads + tid;
+            if (i < n_pages) pages[i] = ent[k];
+        }
+    }
+    // scaled, permuted query rows: the permutation entries first, then the gathers
+    const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
+    constexpr int kQP = (RP * 256 + kThreads - 1) / kThreads;  // head_dim <= 256 on this kernel
+    {
+        int64_t src[kQP];
+#pragma unroll
+        for (int k = 0; k < kQP; ++k) {
+            const int e = tid + k * kThreads;
+            src[k] = -1;
+            if (e < RP * D) {
+                const int r = e / D, j = e - r * D;
+                if (r < nr) {
+                    const int g = r / a.q_len, qi = r - g * a.q_len;
+                    const int h = kv * p.G + g;
+                    src[k] = (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl + perm[j];
+                }
+            }
+        }
+        float qv[kQP];
+#pragma unroll
+        for (int k = 0; k < kQP; ++k) qv[k] = src[k] >= 0 ? ssq_load_elem(a.q, a.q_dtype, src[k]) : 0.f;
+#pragma unroll
+        for (int k = 0; k < kQP; ++k) {
+            const int e = tid + k * kThreads;
+            if (e < RP * D) qp[e] = (src[k] >= 0 && a.has_scale) ? ssq_round_to(qv[k] * a.scale, a.q_dtype) : qv[k];
+        }
     }
     __syncthreads();
     // the first tile's codes and values are independent of the LUT: put them in flight before building it
@@ -312,50 +443,17 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
     TileRegs<NB, DT> RA, RB;
     int tile = wave;
-    if (tile < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile, lane, cbase, vbase, RA);
-    // LUT: each thread owns entries tid + k*kThreads; codewords are loaded a batch at a time so the
-    // loads overlap instead of each waiting out a full memory latency
-    const float* cent = a.cent + (int64_t)kv * a.cent_sh;
-    constexpr int kBatch = 8;
-    for (int e0 = tid; e0 < NB * kNC; e0 += kBatch * kThreads) {
-        float cw[kBatch][4];
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-            const int e = e0 + k * kThreads;
-            if (e < NB * kNC) {
-                const float* c = cent + (int64_t)e * bd;
-                if (bd == 4) {
-                    const float4 v = *reinterpret_cast<const float4*>(c);
-                    cw[k][0] = v.x; cw[k][1] = v.y; cw[k][2] = v.z; cw[k][3] = v.w;
-                } else {
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) cw[k][d] = d < bd ? c[d] : 0.f;
-                }
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < kBatch; ++k) {
-            const int e = e0 + k * kThreads;
-            if (e >= NB * kNC) break;
-            const int blk = e / kNC;
-            const float* c = cent + (int64_t)e * bd;
-            float acc[RP];
-#pragma unroll
-            for (int r = 0; r < RP; ++r) acc[r] = qp[r * D + blk * bd] * cw[k][0];
-            for (int d = 1; d < bd; ++d) {
-                const float cd = d < 4 ? cw[k][d] : c[d];
-#pragma unroll
-                for (int r = 0; r < RP; ++r) acc[r] = fmaf(qp[r * D + blk * bd + d], cd, acc[r]);
-            }
-            if (RP % 4 == 0) {
-#pragma unroll
-                for (int r = 0; r < RP; r += 4)
-                    *reinterpret_cast<float4*>(lut + (size_t)e * RP + r) = make_float4(acc[r], acc[r + 1], acc[r + 2], acc[r + 3]);
-            } else {
-#pragma unroll
-                for (int r = 0; r < RP; ++r) lut[(size_t)e * RP + r] = acc[r];
-            }
-        }
+    // Tile loads are issued unconditionally (a wave past the last tile re-reads tile n_tiles-1,
+    // mostly from L2): every path then carries the same queue of outstanding loads, so the
+    // compiler's vmcnt waits for the tile being computed never drain the tile behind it.
+    const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
+    if (n_tiles > 0) issue_tile<NB, DT>(a, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, RA);
+    switch (bd) {
+        case 1: build_lut<RP, NB, 1>(cent, qp, lut, D, tid); break;
+        case 2: build_lut<RP, NB, 2>(cent, qp, lut, D, tid); break;
+        case 4: build_lut<RP, NB, 4>(cent, qp, lut, D, tid); break;
+        case 8: build_lut<RP, NB, 8>(cent, qp, lut, D, tid); break;
+        default: build_lut_any<RP, NB>(cent, qp, lut, D, bd, tid); break;
     }
     __syncthreads();
 
@@ -366,33 +464,15 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     v4f acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
-#if SSQ_PIPE_DEPTH == 3
-    TileRegs<NB, DT> RC;
-    if (tile + kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + kWaves, lane, cbase, vbase, RB);
     while (tile < n_tiles) {
-        if (tile + 2 * kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + 2 * kWaves, lane, cbase, vbase, RC);
+        issue_tile<NB, DT>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RB);
         compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane, acc);
         tile += kWaves;
         if (tile >= n_tiles) break;
-        if (tile + 2 * kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + 2 * kWaves, lane, cbase, vbase, RA);
-        compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RB, m_run, l_lane, acc);
-        tile += kWaves;
-        if (tile >= n_tiles) break;
-        if (tile + 2 * kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + 2 * kWaves, lane, cbase, vbase, RB);
-        compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RC, m_run, l_lane, acc);
-        tile += kWaves;
-    }
-#else
-    while (tile < n_tiles) {
-        if (tile + kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + kWaves, lane, cbase, vbase, RB);
-        compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane, acc);
-        tile += kWaves;
-        if (tile >= n_tiles) break;
-        if (tile + kWaves < n_tiles) issue_tile<NB, DT>(a, pages, t_begin, t_end, tile + kWaves, lane, cbase, vbase, RA);
+        issue_tile<NB, DT>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RA);
         compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RB, m_run, l_lane, acc);
         tile += kWaves;
     }
-#endif
 
     // ---- merge the waves' (m, l, O) through LDS (the LUT is no longer needed)
     float l_w[RP];
@@ -464,6 +544,7 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     if (a->n_centroids != kNC) return false;
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;  // float4 codeword loads
     if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32) return false;
+    if (a->head_dim > 256) return false;  // query staging covers at most 256 dims per row
     // code rows: 8-byte (nb 8) or 16-byte (nb >= 16) vector loads
     const int cal = a->n_blocks >= 16 ? 16 : 8;
     if (a->c_st % cal != 0 || a->c_sb % cal != 0 || a->c_sh % cal != 0 || (uintptr_t)a->codes % cal) return false;
