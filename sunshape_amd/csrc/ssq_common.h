@@ -73,6 +73,9 @@ __device__ __forceinline__ float ssq_wave_sum(float v) {
 int ssq_fail(int code, const char* fmt, ...);
 int ssq_check_hip(hipError_t e, const char* what);
 
+// compute units of the current device (cached per device; 256 on MI355X)
+int ssq_device_cus();
+
 #define SSQ_REQUIRE(cond, ...)                                  \
     do {                                                        \
         if (!(cond)) return ssq_fail(SSQ_ERR_INVALID, __VA_ARGS__); \

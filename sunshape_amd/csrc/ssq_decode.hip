@@ -27,6 +27,7 @@ struct DecodeParams {
     int split_len;  // tokens per split (multiple of kTile)
     int n_splits;
     int word_codes; // 1: code rows are 4-byte aligned with nb % 4 == 0
+    int vec_cent;   // 1: codebook 16-byte aligned (per head too), head_dim % 4 == 0, nb*nc % 4 == 0
     float* ws_o;    // [n_splits, B*Hq*Lq, Dv]
     float* ws_m;    // [n_splits, B*Hq*Lq]
     float* ws_l;
@@ -67,6 +68,70 @@ __device__ __forceinline__ void load_v8(const void* base, int64_t elem_off, floa
     }
 }
 
+// vector of N floats (N = 1, 2 or a multiple of 4; 4N-byte aligned)
+template <int N>
+__device__ __forceinline__ void load_vec(const float* __restrict__ src, float (&dst)[N]) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(src + i);
+            dst[i] = v.x; dst[i + 1] = v.y; dst[i + 2] = v.z; dst[i + 3] = v.w;
+        }
+    } else if constexpr (N == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(src);
+        dst[0] = v.x; dst[1] = v.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) dst[i] = src[i];
+    }
+}
+
+// LUT[e][r] = sum_d qp[r][blk*BD + d] * C[e][d], e = blk*nc + c: FMA chain over d from the first
+// product (triton_kernels.py:381-408).  Each thread loads a batch of kB codewords as vectors, and
+// each entry's query sub-vectors as vectors, before the arithmetic: the build then costs a few
+// memory / LDS latencies rather than one per element.  Heavy (passthrough) blocks are skipped.
+template <int RP, int BD>
+__device__ __forceinline__ void build_lut_vec(const ssq_decode_args& a, const float* __restrict__ cent,
+                                              const float* __restrict__ qp, float* __restrict__ lut, int tid) {
+    constexpr int kB = 64 / BD < 16 ? 64 / BD : 16;
+    const int nc = a.n_centroids, D = a.head_dim;
+    const int total = a.n_blocks * nc;
+    for (int e0 = tid; e0 < total; e0 += kB * kThreads) {
+        float c[kB][BD];
+#pragma unroll
+        for (int kk = 0; kk < kB; ++kk) {
+            const int e = e0 + kk * kThreads;
+            if (e < total) load_vec<BD>(cent + (int64_t)e * BD, c[kk]);
+        }
+#pragma unroll
+        for (int kk = 0; kk < kB; ++kk) {
+            const int e = e0 + kk * kThreads;
+            if (e >= total) break;
+            const int blk = e / nc;
+            if (ssq_is_heavy(a.heavy_mask[0], a.heavy_mask[1], blk)) continue;
+            const float* qb = qp + blk * BD;
+            float acc[RP];
+#pragma unroll
+            for (int r = 0; r < RP; ++r) {
+                float qv[BD];
+                load_vec<BD>(qb + r * D, qv);
+                float t = qv[0] * c[kk][0];
+#pragma unroll
+                for (int d = 1; d < BD; ++d) t = fmaf(qv[d], c[kk][d], t);
+                acc[r] = t;
+            }
+            if constexpr (RP % 4 == 0) {
+#pragma unroll
+                for (int r = 0; r < RP; r += 4)
+                    *reinterpret_cast<float4*>(lut + (size_t)e * RP + r) = make_float4(acc[r], acc[r + 1], acc[r + 2], acc[r + 3]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < RP; ++r) lut[(size_t)e * RP + r] = acc[r];
+            }
+        }
+    }
+}
+
 // float offset of the reduction scratch; identical on host and device
 __host__ __device__ inline size_t red_offset(const ssq_decode_args& a, int RP, bool has_v) {
     size_t main = (size_t)a.n_blocks * a.n_centroids * RP + (size_t)RP * a.head_dim + (has_v ? (size_t)RP * kTile : 0);
@@ -91,6 +156,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
     const int b = bk / a.num_kv_heads;
     const int kv = bk - b * a.num_kv_heads;
     const int nb = a.n_blocks, nc = a.n_centroids, D = a.head_dim, bd = a.block_dim;
+    const bool any_heavy = (a.heavy_mask[0] | a.heavy_mask[1]) != 0;
     const int r0 = grp * p.R;
     const int nr = min(p.R, p.rows - r0);
     const int T = PAGED ? min(a.seq_lens[b], a.seq_len) : a.seq_len;
@@ -122,7 +188,14 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
 
     // ---- 2. LUT build (fp32 FMA chain over the block's dims, dims ascending)
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
-    for (int e = tid; e < nb * nc; e += kThreads) {
+    // vector codeword / query loads need a 16-byte aligned codebook (host-checked: vec_cent)
+    // and a 4-aligned head_dim
+    const int vb = p.vec_cent ? bd : 0;
+    if (vb == 1) build_lut_vec<RP, 1>(a, cent, qp, lut, tid);
+    else if (vb == 2) build_lut_vec<RP, 2>(a, cent, qp, lut, tid);
+    else if (vb == 4) build_lut_vec<RP, 4>(a, cent, qp, lut, tid);
+    else if (vb == 8) build_lut_vec<RP, 8>(a, cent, qp, lut, tid);
+    else for (int e = tid; e < nb * nc; e += kThreads) {
         const int blk = e / nc;
         if (ssq_is_heavy(a.heavy_mask[0], a.heavy_mask[1], blk)) continue;
         const float* c = cent + (int64_t)e * bd;
@@ -158,9 +231,54 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
 #pragma unroll
         for (int j = 0; j < kAccW; ++j) acc[r][j] = 0.f;
 
+    // ---- contiguous layout: the next tile's inputs are loaded into registers while the current
+    // tile computes -- this thread's token code words (word-aligned uint8 codes, nb <= 32, no
+    // passthrough blocks) and,
+    // with 16-bit V (Dv <= 128), the V chunks of its P.V slots.  The loads are unconditional
+    // (addresses clamped to the split's last token; those tokens get p = 0), so the compiler's
+    // vmcnt waits for the current tile never drain the next one.
+    constexpr int kCW = 8, kVC = 16;
+    const bool pf_codes = !PAGED && p.word_codes && nb <= 4 * kCW && !any_heavy;
+    const bool pf_v = !PAGED && HAS_V && VT != SSQ_F32 && Dv <= 8 * kVC && pv_active;  // nvc <= kVC then
+    const int nvc = (kTile + tpar - 1) / tpar;  // P.V slots per thread per tile (token pv_t + k*tpar < kTile)
+    uint32_t cwn[kCW];
+    uint4 vvn[kVC];
+#pragma unroll
+    for (int i = 0; i < kCW; ++i) cwn[i] = 0u;
+#pragma unroll
+    for (int k = 0; k < kVC; ++k) vvn[k] = make_uint4(0u, 0u, 0u, 0u);
+    auto prefetch = [&](int t0n) {
+        if (pf_codes) {
+            const int tc = min(t0n + tid, t_end - 1);
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(
+                a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st);
+#pragma unroll
+            for (int i = 0; i < kCW; ++i)
+                if (i < (nb >> 2)) cwn[i] = w[i];
+        }
+        if (pf_v) {
+            const uint16_t* vb = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kv * a.v_sh + pv_d * 8;
+#pragma unroll
+            for (int k = 0; k < kVC; ++k)
+                if (k < nvc && pv_t + k * tpar < kTile) {
+                    const int tv = min(t0n + pv_t + k * tpar, t_end - 1);
+                    vvn[k] = *reinterpret_cast<const uint4*>(vb + (int64_t)tv * a.v_st);
+                }
+        }
+    };
+    const int last_t0 = t_end > t_begin ? t_begin + (t_end - 1 - t_begin) / kTile * kTile : t_begin;
+    if (t_end > t_begin) prefetch(t_begin);
+
     for (int t0 = t_begin; t0 < t_end; t0 += kTile) {
         const int t = t0 + tid;
         const bool valid = t < t_end;
+        uint32_t cw[kCW];
+        uint4 vv[kVC];
+#pragma unroll
+        for (int i = 0; i < kCW; ++i) cw[i] = cwn[i];
+#pragma unroll
+        for (int k = 0; k < kVC; ++k) vv[k] = vvn[k];
+        prefetch(min(t0 + kTile, last_t0));
         float s[RP];
 #pragma unroll
         for (int r = 0; r < RP; ++r) s[r] = 0.f;
@@ -212,6 +330,50 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
                 for (int pi = 0, blk = 0; blk < nb; ++pi) {
                     const uint32_t word = w[pi];
                     for (int v = 0; v < vpe && blk < nb; ++v, ++blk) add_block(blk, (word >> (v * bits)) & msk);
+                }
+            } else if (pf_codes) {
+                // LUT gathers 8 blocks at a time, summed in block order
+#pragma unroll
+                for (int w0 = 0; w0 < kCW; w0 += 2) {
+                    if (w0 < (nb >> 2)) {
+                        constexpr int NV = RP >= 4 ? RP / 4 : 1;
+                        float4 ev[8][NV];
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) {
+                            const int blk = 4 * w0 + k;
+                            const uint32_t word = cw[w0 + (k >> 2)];
+                            const int code = (int)((word >> (8 * (k & 3))) & 0xFFu);
+                            const int cc = code < nc ? code : nc - 1;
+                            const float* e = lut + ((size_t)blk * nc + cc) * RP;
+                            if (blk < nb) {
+                                if (RP >= 4) {
+#pragma unroll
+                                    for (int j = 0; j < NV; ++j) ev[k][j] = *reinterpret_cast<const float4*>(e + 4 * j);
+                                } else if (RP == 2) {
+                                    const float2 v2 = *reinterpret_cast<const float2*>(e);
+                                    ev[k][0] = make_float4(v2.x, v2.y, 0.f, 0.f);
+                                } else {
+                                    ev[k][0] = make_float4(e[0], 0.f, 0.f, 0.f);
+                                }
+                            }
+                        }
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) {
+                            if (4 * w0 + k < nb) {
+                                if (RP >= 4) {
+#pragma unroll
+                                    for (int j = 0; j < NV; ++j) {
+                                        s[4 * j] += ev[k][j].x; s[4 * j + 1] += ev[k][j].y;
+                                        s[4 * j + 2] += ev[k][j].z; s[4 * j + 3] += ev[k][j].w;
+                                    }
+                                } else if (RP == 2) {
+                                    s[0] += ev[k][0].x; s[1] += ev[k][0].y;
+                                } else {
+                                    s[0] += ev[k][0].x;
+                                }
+                            }
+                        }
+                    }
                 }
             } else if (p.word_codes) {
                 const uint32_t* w = reinterpret_cast<const uint32_t*>(crow);
@@ -279,7 +441,22 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
 #pragma unroll
             for (int j = 0; j < kAccW; ++j) acc[r][j] *= alpha[r];
         if (pv_active) {
-            if (!PAGED) {
+            if (pf_v) {
+#pragma unroll
+                for (int k = 0; k < kVC; ++k) {
+                    const int tt = pv_t + k * tpar;
+                    if (k < nvc && tt < kTile) {
+                        float v[8];
+                        unpack8<VT>(vv[k], v);
+#pragma unroll
+                        for (int r = 0; r < RP; ++r) {
+                            const float pr = ptile[r * kTile + tt];
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) acc[r][j] = fmaf(pr, v[j], acc[r][j]);
+                        }
+                    }
+                }
+            } else if (!PAGED) {
                 const int64_t vbase = (int64_t)b * a.v_sb + (int64_t)kv * a.v_sh + pv_d * 8;
                 for (int tt = pv_t; tt < nt; tt += tpar) {
                     float v[8];
@@ -428,7 +605,11 @@ int make_plan(const ssq_decode_args& a, Plan& pl) {
     pl.smem = smem_bytes(a, pl.RP, pl.has_v);
     const int units = a.batch * a.num_kv_heads * pl.n_groups;
     const int tiles = (a.seq_len + kTile - 1) / kTile;
-    int splits = a.num_splits > 0 ? a.num_splits : (512 + units - 1) / units;
+    // one round of workgroups: as many as the device runs at once at this LDS footprint
+    // (each split rebuilds the LUT, so a second round costs more than it hides)
+    const int per_cu = pl.smem > 0 ? (int)(kMaxSmem / pl.smem) : 1;
+    const int slots = ssq_device_cus() * (per_cu < 1 ? 1 : per_cu > 2 ? 2 : per_cu);
+    int splits = a.num_splits > 0 ? a.num_splits : (slots + units - 1) / units;
     if (splits > tiles) splits = tiles;
     if (splits < 1) splits = 1;
     const int tiles_per_split = (tiles + splits - 1) / splits;
@@ -528,6 +709,8 @@ int run_generic(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipS
     const bool aligned = a->code_bits == 0 && ((uintptr_t)a->codes % 4 == 0) && a->n_blocks % 4 == 0 &&
                          a->c_st % 4 == 0 && a->c_sh % 4 == 0 && a->c_sb % 4 == 0;
     dp.word_codes = aligned ? 1 : 0;
+    dp.vec_cent = ((uintptr_t)a->cent % 16 == 0 && (a->cent_sh * 4) % 16 == 0 && a->head_dim % 4 == 0 &&
+                   (a->n_blocks * a->n_centroids) % 4 == 0) ? 1 : 0;  // qp (after the LUT) 16-byte aligned
     const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
     float* ws = reinterpret_cast<float*>(workspace);
     dp.ws_o = ws;

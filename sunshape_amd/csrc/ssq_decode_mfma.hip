@@ -556,7 +556,8 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     pl.DT = a->value_dim / 16;
     const int units = a->batch * a->num_kv_heads;
     const int tiles = (a->seq_len + kTileTok - 1) / kTileTok;
-    int splits = a->num_splits > 0 ? a->num_splits : (256 + units - 1) / units;
+    const int cus = ssq_device_cus();  // one workgroup per CU (the LUT fills the LDS)
+    int splits = a->num_splits > 0 ? a->num_splits : (cus + units - 1) / units;
     const int max_splits = (tiles + kWaves - 1) / kWaves;  // keep every wave busy
     if (splits > max_splits) splits = max_splits;
     if (splits < 1) splits = 1;

@@ -22,6 +22,18 @@ int ssq_check_hip(hipError_t e, const char* what) {
 }
 
 extern "C" const char* ssq_last_error(void) { return g_err; }
+
+int ssq_device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
 extern "C" int ssq_abi_version(void) { return SSQ_ABI_VERSION; }
 
 namespace {

@@ -179,7 +179,8 @@ def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, c
 
 def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
                scale: Optional[float] = None, heavy: Optional[Sequence[bool]] = None,
-               pt: Optional[torch.Tensor] = None, pt_dense: bool = False, code_bits: int = 0) -> torch.Tensor:
+               pt: Optional[torch.Tensor] = None, pt_dense: bool = False, code_bits: int = 0,
+               num_splits: int = 0) -> torch.Tensor:
     """Raw scores for every (batch, query head) in one launch: fp32 [B, Hq, Lq, T].
 
     q [B, Hq, Lq, D]; codes [B, Hkv, T, nb] uint8; query head h reads KV head
@@ -212,6 +213,7 @@ def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: t
         layout=N.SSQ_CONTIGUOUS, seq_len=T, codes=N.ptr(codes), c_sb=codes.stride(0), c_sh=codes.stride(1),
         c_st=codes.stride(2),
         scores=N.ptr(out), s_sb=out.stride(0), s_sh=out.stride(1), s_sl=out.stride(2), code_bits=int(code_bits),
+        num_splits=int(num_splits),
     )
     a.heavy_mask[0], a.heavy_mask[1] = hm
     N.check(N.lib().ssq_attention_scores(ctypes.byref(a), N.stream_of(q.device)))
