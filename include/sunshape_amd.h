@@ -99,7 +99,7 @@ typedef struct ssq_decode_args {
     float* scores; int64_t s_sb, s_sh, s_sl;  /* raw logits [B, Hq, Lq, T] fp32 (t contiguous) or NULL */
     /* tuning: 0 = library heuristic */
     int32_t num_splits;
-    int32_t kernel;      /* 0 auto, 1 generic LUT/VALU kernel, 2 MFMA paged kernel */
+    int32_t kernel;      /* 0 auto, 1 generic LUT/VALU kernel, 2 MFMA paged kernel, 3 MFMA contiguous kernel */
     /* code storage: 0 = one uint8 per block (c_* strides in bytes); 1..8 = packing in
      * uint32 words, vpe = 32 / code_bits codes per word, block blk = p*vpe + v at bits
      * [v*code_bits, (v+1)*code_bits) of word p (the layout of sunshape/triton_kernels.py:213-283);

@@ -751,10 +751,32 @@ int ssq_launch_merge(const ssq_decode_args& a, int n_splits, const float* ws_o, 
 int ssq_decode_mfma_supported(const ssq_decode_args* a);
 size_t ssq_decode_mfma_workspace(const ssq_decode_args* a);
 int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipStream_t st);
+int ssq_decode_contig_supported(const ssq_decode_args* a);
+size_t ssq_decode_contig_workspace(const ssq_decode_args* a);
+int ssq_decode_contig(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipStream_t st);
+
+namespace {
+// kernel choice: 2 = MFMA paged, 3 = MFMA contiguous, 1 = generic; 0 picks the first that serves
+int pick_kernel(const ssq_decode_args* a) {
+    if (a->kernel != 0) return a->kernel;
+    if (a->v && ssq_decode_mfma_supported(a)) return 2;
+    if (!a->v) {
+        // scores only: the LUT kernel is the faster one while every query row fits one LUT of <= 64 KiB
+        const int rows = (a->num_q_heads / a->num_kv_heads) * a->q_len;
+        int rp = 1;
+        while (rp < rows) rp <<= 1;
+        if (rows <= kMaxRows && (size_t)a->n_blocks * a->n_centroids * rp * 4 <= 64 * 1024) return 1;
+    }
+    if (ssq_decode_contig_supported(a)) return 3;
+    return 1;
+}
+}  // namespace
 
 extern "C" size_t ssq_decode_workspace_size(const ssq_decode_args* a) {
     if (validate(a, a && a->v != nullptr) != SSQ_OK) return 0;
-    if (a->v && a->kernel != 1 && ssq_decode_mfma_supported(a)) return ssq_decode_mfma_workspace(a);
+    const int k = pick_kernel(a);
+    if (k == 2 && a->v && ssq_decode_mfma_supported(a)) return ssq_decode_mfma_workspace(a);
+    if (k == 3 && ssq_decode_contig_supported(a)) return ssq_decode_contig_workspace(a);
     Plan pl;
     if (make_plan(*a, pl) != SSQ_OK) return 0;
     return pl.ws_bytes;
@@ -763,9 +785,14 @@ extern "C" size_t ssq_decode_workspace_size(const ssq_decode_args* a) {
 extern "C" int ssq_decode(const ssq_decode_args* a, void* workspace, size_t workspace_bytes, void* stream) {
     int rc = validate(a, true);
     if (rc) return rc;
-    if (a->kernel == 2 || (a->kernel == 0 && ssq_decode_mfma_supported(a))) {
+    const int k = pick_kernel(a);
+    if (k == 2) {
         SSQ_UNSUPPORTED(ssq_decode_mfma_supported(a), "MFMA decode kernel does not support this problem");
         return ssq_decode_mfma(a, workspace, workspace_bytes, (hipStream_t)stream);
+    }
+    if (k == 3) {
+        SSQ_UNSUPPORTED(ssq_decode_contig_supported(a), "contiguous MFMA kernel does not support this problem");
+        return ssq_decode_contig(a, workspace, workspace_bytes, (hipStream_t)stream);
     }
     return run_generic(a, workspace, workspace_bytes, (hipStream_t)stream);
 }
@@ -775,5 +802,11 @@ extern "C" int ssq_attention_scores(const ssq_decode_args* a, void* stream) {
     if (rc) return rc;
     SSQ_REQUIRE(a->v == nullptr && a->scores != nullptr, "scores-only call needs v == NULL and scores != NULL");
     if (a->seq_len == 0) return SSQ_OK;
+    const int k = pick_kernel(a);
+    SSQ_UNSUPPORTED(k != 2, "the MFMA paged kernel computes decode, not scores only");
+    if (k == 3) {
+        SSQ_UNSUPPORTED(ssq_decode_contig_supported(a), "contiguous MFMA kernel does not support this problem");
+        return ssq_decode_contig(a, nullptr, 0, (hipStream_t)stream);
+    }
     return run_generic(a, nullptr, 0, (hipStream_t)stream);
 }

@@ -1,0 +1,500 @@
+// Fused VQ-key decode (and scores) over the reference's contiguous layout on the matrix cores.
+//
+// Same mathematics as the other decode kernels (q scaled in its own dtype, softmax in fp32, the
+// probabilities cast to the value dtype before P.V: vllm_attn_backend.py:232-252), mapped for
+// contiguous token-major values [B, Hkv, T, Dv] and head_dim 64:
+//
+//   scores = v_mfma_f32_16x16x4f32 over Qp [16 rows x 64] . K_hat^T: the permuted, scaled query
+//            rows are a fixed A operand held in registers; each lane gathers its B element
+//            K_hat[token][dim] = C[blk][code][d] from the codebook staged in LDS.  No LUT is built,
+//            so up to 16 query rows share one pass over the keys.  fp32 products and sums; the
+//            order differs from the LUT kernels' (block by block), within fp32 rounding.
+//   P.V    = v_mfma_f32_16x16x32_bf16 (_f16): A = P [16 rows x 32 tokens] from a per-wave LDS strip;
+//            B = V [32 tokens x 16 dims].  V tiles are copied to LDS with coalesced 16-byte loads
+//            and read back transposed with ds_read_b64_tr_b16: within each 16-lane group, lane l
+//            addresses V[t0 + l/4][n0 + 4*(l%4) .. +3] and receives V[t0 .. t0+3][n0 + l], so two
+//            reads give a lane its 8 consecutive tokens of one dim.
+//
+// workgroup = 4 waves for one (batch, KV head, context split); each wave streams 64-token tiles with
+// its own running (max, sum, O), the next tile's loads in flight; waves merge through LDS at the end.
+#include "ssq_common.h"
+
+#include <math.h>
+
+int ssq_launch_merge(const ssq_decode_args& a, int n_splits, const float* ws_o, const float* ws_m,
+                     const float* ws_l, hipStream_t st);
+
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * SSQ_WAVE;
+constexpr int kTile = 64;  // tokens per wave iteration
+constexpr int kD = 64;     // head_dim served
+constexpr size_t kMaxSmem = 160 * 1024;
+
+struct ContigParams {
+    ssq_decode_args a;
+    int G, rows, split_len, n_splits;
+    float* ws_o;
+    float* ws_m;
+    float* ws_l;
+};
+
+// per-wave LDS region (bytes): V tile [64][Dv] (16-bit) | codes [64][NB] | P strip [16][64] (16-bit)
+__host__ __device__ constexpr int wave_v_bytes(int DT) { return kTile * DT * 16 * 2; }
+__host__ __device__ constexpr int wave_bytes(int NB, int DT) { return wave_v_bytes(DT) + kTile * NB + 16 * kTile * 2; }
+inline size_t contig_smem(const ssq_decode_args& a, int DT) {
+    const size_t cb = (size_t)a.n_blocks * a.n_centroids * a.block_dim * 4;
+    const size_t main = cb + (size_t)kWaves * wave_bytes(a.n_blocks, DT);
+    const size_t merge = (size_t)kWaves * 16 * (16 * DT + 2) * 4;
+    return main > merge ? main : merge;
+}
+
+__device__ __forceinline__ uint4 ld16(const void* p) {
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <int VT>
+__device__ __forceinline__ uint32_t to_vt16(float x) {
+    return VT == SSQ_BF16 ? ssq_f32_to_bf16(x) : ssq_f32_to_f16(x);
+}
+
+template <int VT>
+__device__ __forceinline__ v4f mfma_pv(const uint4& a, const uint4& b, v4f c) {
+    if (VT == SSQ_BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0,
+                                                       0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+}
+
+template <int CTL>
+__device__ __forceinline__ float dpp_ror(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTL, 0xF, 0xF, false));
+}
+// max / sum over the 16 lanes of a row (every lane of the row receives the result)
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dpp_ror<0x121>(v)); v = fmaxf(v, dpp_ror<0x122>(v));
+    v = fmaxf(v, dpp_ror<0x124>(v)); v = fmaxf(v, dpp_ror<0x128>(v));
+    return v;
+}
+__device__ __forceinline__ float row_sum(float v) {
+    v += dpp_ror<0x121>(v); v += dpp_ror<0x122>(v);
+    v += dpp_ror<0x124>(v); v += dpp_ror<0x128>(v);
+    return v;
+}
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// registers of one 64-token tile in flight: this lane's 16-byte V chunks and its token's code row
+template <int NB, int DT>
+struct Tile {
+    uint4 v[2 * DT];
+    uint4 c[NB >= 16 ? NB / 16 : 1];
+    uint2 c8;
+};
+
+// Loads are unconditional; chunks of tokens past the split's end re-read the last token's row
+// (valid memory; such tokens get p = 0 and are never scored).
+template <int NB, int DT, bool HAS_V>
+__device__ __forceinline__ void issue_tile(const ssq_decode_args& a, int b, int kv, int t0, int t_end, int lane,
+                                           Tile<NB, DT>& R) {
+    const int tc = min(t0 + lane, t_end - 1);
+    const uint8_t* crow = a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st;
+    if constexpr (NB >= 16) {
+#pragma unroll
+        for (int i = 0; i < NB / 16; ++i) R.c[i] = ld16(crow + 16 * i);
+    } else {
+        R.c8 = *reinterpret_cast<const uint2*>(crow);
+    }
+    if constexpr (HAS_V) {
+        const uint16_t* vb = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kv * a.v_sh;
+        constexpr int kRowChunks = 2 * DT;  // 16-byte chunks per token row (Dv = 16 * DT)
+#pragma unroll
+        for (int i = 0; i < 2 * DT; ++i) {
+            const int chunk = i * SSQ_WAVE + lane;  // chunk of the tile, row-major
+            const int tok = min(t0 + chunk / kRowChunks, t_end - 1);
+            R.v[i] = ld16(vb + (int64_t)tok * a.v_st + (chunk % kRowChunks) * 8);
+        }
+    }
+}
+
+template <int BD, int DT, int VT, bool HAS_V>
+__global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p) {
+    constexpr int NB = kD / BD;
+    constexpr int NBW = NB / 4;  // code row dwords
+    constexpr int KS = kD / 4;   // score k-steps
+    constexpr int Dv = 16 * DT;
+    extern __shared__ __align__(16) float smem[];
+    const ssq_decode_args& a = p.a;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int bk = blockIdx.x;
+    const int split = blockIdx.y;
+    const int b = bk / a.num_kv_heads;
+    const int kv = bk - b * a.num_kv_heads;
+    const int nc = a.n_centroids;
+    const int nr = p.rows;
+    const int t_begin = split * p.split_len;
+    const int t_end = min(a.seq_len, t_begin + p.split_len);
+
+    float* cb = smem;  // codebook [NB][nc][BD] fp32
+    uint8_t* wreg = reinterpret_cast<uint8_t*>(smem + (size_t)NB * nc * BD) + wave * wave_bytes(NB, DT);
+    uint16_t* vt = reinterpret_cast<uint16_t*>(wreg);                            // [64][Dv]
+    uint8_t* ct = wreg + wave_v_bytes(DT);                                       // [64][NB]
+    uint16_t* ps = reinterpret_cast<uint16_t*>(wreg + wave_v_bytes(DT) + kTile * NB);  // [16][64]
+
+    // the first two tiles' loads go out before the prologue (two register sets in flight: a set is
+    // free again once its tile is in LDS, and then loads the tile two rounds ahead)
+    const int n_tiles = (t_end - t_begin + kTile - 1) / kTile;
+    const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
+    Tile<NB, DT> ra, rb;
+    if (n_tiles > 0) {
+        issue_tile<NB, DT, HAS_V>(a, b, kv, t_begin + min(wave, last_tile) * kTile, t_end, lane, ra);
+        issue_tile<NB, DT, HAS_V>(a, b, kv, t_begin + min(wave + kWaves, last_tile) * kTile, t_end, lane, rb);
+    }
+
+    // ---- prologue: codebook to LDS; this lane's query A-operand values Qp[row l16][4s + lg]
+    // (all of a thread's loads are issued before its first store: one memory latency, not 16)
+    const float* cent = a.cent + (int64_t)kv * a.cent_sh;
+    {
+        constexpr int kPer = kD * 256 / 4 / kThreads;  // float4s per thread at nc = 256
+        const int n4 = NB * nc * BD / 4;
+        float4 st[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < n4) st[k] = *reinterpret_cast<const float4*>(cent + 4 * i);
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < n4) *reinterpret_cast<float4*>(cb + 4 * i) = st[k];
+        }
+    }
+    float qa[KS];
+    {
+        const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
+        int64_t pj[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) pj[s] = perm[4 * s + lg];
+        int64_t qrow = -1;
+        if (l16 < nr) {
+            const int g = l16 / a.q_len, qi = l16 - g * a.q_len;
+            const int h = kv * p.G + g;
+            qrow = (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl;
+        }
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            float v = qrow >= 0 ? ssq_load_elem(a.q, a.q_dtype, qrow + pj[s]) : 0.f;
+            if (qrow >= 0 && a.has_scale) v = ssq_round_to(v * a.scale, a.q_dtype);
+            qa[s] = v;
+        }
+    }
+    __syncthreads();
+
+    // Codebook gather of step s: this lane supplies head dim j = 4s + lg, i.e. dim j % BD of block
+    // j / BD.  For BD in {1, 2, 4, 8} the block's LDS byte offset and its code's bit position in the
+    // step's code word split into a per-step (uniform) part and a per-lane part, so no per-step
+    // tables are kept:  offset = lane_off + step_off(s) + code * BD * 4,  bit = lane_sh + step_sh(s).
+    constexpr int kLogBD = BD == 1 ? 0 : BD == 2 ? 1 : BD == 4 ? 2 : 3;
+    const uint8_t* cbb = reinterpret_cast<const uint8_t*>(cb);
+    const uint32_t ncm1 = (uint32_t)(nc - 1);
+    const uint32_t lane_off = BD <= 4 ? (uint32_t)(((lg >> kLogBD) * nc * BD) + (lg & (BD - 1))) * 4u : 4u * lg;
+    const uint32_t lane_sh = BD == 1 ? 8u * lg : BD == 2 ? 8u * (lg >> 1) : 0u;
+    float m_run[4], l_run[4];
+    v4f acc[DT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { m_run[i] = -INFINITY; l_run[i] = 0.f; }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+    // one tile: its registers -> the wave's LDS region, the set reloaded two rounds ahead, compute
+    auto step = [&](Tile<NB, DT>& R, int tile) {
+        const int t0 = t_begin + tile * kTile;
+        wave_sync();
+        if constexpr (NB >= 16) {
+#pragma unroll
+            for (int i = 0; i < NB / 16; ++i) *reinterpret_cast<uint4*>(ct + lane * NB + 16 * i) = R.c[i];
+        } else {
+            *reinterpret_cast<uint2*>(ct + lane * NB) = R.c8;
+        }
+        if constexpr (HAS_V) {
+#pragma unroll
+            for (int i = 0; i < 2 * DT; ++i) *reinterpret_cast<uint4*>(vt + (i * SSQ_WAVE + lane) * 8) = R.v[i];
+        }
+        wave_sync();
+        issue_tile<NB, DT, HAS_V>(a, b, kv, t_begin + min(tile + 2 * kWaves, last_tile) * kTile, t_end, lane, R);
+
+        // ---- scores: S[row 4*lg+i][token 16g + l16] for the tile's 4 groups of 16 tokens
+        v4f sc[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            uint32_t cw[NBW];
+            const uint8_t* crow = ct + (16 * g + l16) * NB;
+            if constexpr (NB >= 16) {
+#pragma unroll
+                for (int i = 0; i < NB / 16; ++i) {
+                    const uint4 w = *reinterpret_cast<const uint4*>(crow + 16 * i);
+                    cw[4 * i] = w.x; cw[4 * i + 1] = w.y; cw[4 * i + 2] = w.z; cw[4 * i + 3] = w.w;
+                }
+            } else {
+                const uint2 w = *reinterpret_cast<const uint2*>(crow);
+                cw[0] = w.x; cw[1] = w.y;
+            }
+            v4f c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                // the word holding this step's block code is the same for every lg (BD in {1,2,4,8})
+                const uint32_t word = cw[((4 * s) / BD) >> 2];
+                const uint32_t step_sh = BD == 1 ? 0u : BD == 2 ? 16u * (s & 1) : BD == 4 ? 8u * (s & 3) : 8u * ((s >> 1) & 3);
+                const uint32_t step_off = BD <= 4 ? (uint32_t)s * 16u * (uint32_t)nc
+                                                  : (uint32_t)(s >> 1) * 32u * (uint32_t)nc + 16u * (s & 1);
+                const uint32_t code = min(__builtin_amdgcn_ubfe(word, lane_sh + step_sh, 8), ncm1);
+                const float kval = *reinterpret_cast<const float*>(cbb + lane_off + step_off + (code << (2 + kLogBD)));
+                c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kval, c, 0, 0, 0);
+            }
+            sc[g] = c;
+        }
+        // additive mask, raw-score output
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int t = t0 + 16 * g + l16;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 4 * lg + i;
+                if (r < nr && t < t_end) {
+                    const int gq = r / a.q_len, qi = r - gq * a.q_len;
+                    const int h = kv * p.G + gq;
+                    if (a.mask)
+                        sc[g][i] += a.mask[(int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qi * a.m_sl +
+                                           (int64_t)t * a.m_st];
+                    if (a.scores) a.scores[(int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)qi * a.s_sl + t] = sc[g][i];
+                }
+            }
+        }
+        if constexpr (!HAS_V) return;
+
+        // ---- online softmax (rows 4*lg + i live in this lane's row of 16 lanes)
+        float alpha[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                if (t0 + 16 * g + l16 < t_end) mx = fmaxf(mx, sc[g][i]);
+            mx = row_max(mx);
+            const float mn = fmaxf(m_run[i], mx);
+            alpha[i] = (mn == -INFINITY) ? 1.f : __expf(m_run[i] - mn);
+            m_run[i] = mn;
+            float lsum = 0.f;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const bool valid = t0 + 16 * g + l16 < t_end;
+                const float pr = (valid && mn != -INFINITY) ? __expf(sc[g][i] - mn) : 0.f;
+                lsum += pr;
+                ps[(4 * lg + i) * kTile + 16 * g + l16] = (uint16_t)to_vt16<VT>(pr);
+            }
+            l_run[i] = l_run[i] * alpha[i] + lsum;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) acc[dt][i] *= alpha[i];
+        }
+        wave_sync();
+
+        // ---- P.V
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            const uint4 af = *reinterpret_cast<const uint4*>(ps + l16 * kTile + 32 * kh + 8 * lg);
+            const int tr_tok = 32 * kh + 8 * lg + (l16 >> 2);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const uint16_t* src = vt + tr_tok * Dv + 16 * dt + 4 * (l16 & 3);
+                const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) v4s*)(src));
+                const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) v4s*)(src + 4 * Dv));
+                const uint2 l2 = __builtin_bit_cast(uint2, lo);
+                const uint2 h2 = __builtin_bit_cast(uint2, hi);
+                acc[dt] = mfma_pv<VT>(af, make_uint4(l2.x, l2.y, h2.x, h2.y), acc[dt]);
+            }
+        }
+    };
+    for (int tile = wave; tile < n_tiles;) {
+        step(ra, tile);
+        tile += kWaves;
+        if (tile >= n_tiles) break;
+        step(rb, tile);
+        tile += kWaves;
+    }
+    if constexpr (!HAS_V) return;
+
+    // ---- merge the waves' (m, l, O) through LDS (the codebook is no longer needed)
+    float l_w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) l_w[i] = row_sum(l_run[i]);
+    __syncthreads();
+    float* mbuf = smem;               // [waves][16]
+    float* lbuf = mbuf + kWaves * 16;  // [waves][16]
+    float* obuf = lbuf + kWaves * 16;  // [waves][16][Dv]
+    if (l16 == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { mbuf[wave * 16 + 4 * lg + i] = m_run[i]; lbuf[wave * 16 + 4 * lg + i] = l_w[i]; }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) obuf[((size_t)wave * 16 + 4 * lg + i) * Dv + 16 * dt + l16] = acc[dt][i];
+    __syncthreads();
+    const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
+    for (int e = tid; e < nr * Dv; e += kThreads) {
+        const int r = e / Dv, dv = e - r * Dv;
+        float M = -INFINITY;
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mbuf[w * 16 + r]);
+        float L = 0.f, o = 0.f;
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = mbuf[w * 16 + r];
+            if (mw == -INFINITY) continue;
+            const float f = __expf(mw - M);
+            L += lbuf[w * 16 + r] * f;
+            o += obuf[((size_t)w * 16 + r) * Dv + dv] * f;
+        }
+        const int gq = r / a.q_len, qi = r - gq * a.q_len;
+        const int h = kv * p.G + gq;
+        const int rid = (b * a.num_q_heads + h) * a.q_len + qi;
+        if (p.n_splits == 1) {
+            ssq_store_elem(a.out, a.v_dtype, (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)qi * a.o_sl + dv, o / L);
+            if (a.lse && dv == 0) a.lse[rid] = M + logf(L);
+        } else {
+            p.ws_o[((size_t)split * n_rows_all + rid) * Dv + dv] = o;
+            if (dv == 0) {
+                p.ws_m[(size_t)split * n_rows_all + rid] = M;
+                p.ws_l[(size_t)split * n_rows_all + rid] = L;
+            }
+        }
+    }
+}
+
+struct CPlan {
+    int DT, split_len, n_splits;
+    size_t smem, ws_bytes;
+};
+
+bool plan(const ssq_decode_args* a, bool has_v, CPlan& pl) {
+    if (a->layout != SSQ_CONTIGUOUS || a->code_bits != 0 || a->heavy_mask[0] || a->heavy_mask[1]) return false;
+    if (a->head_dim != kD) return false;
+    const int bd = a->block_dim;
+    if (bd != 1 && bd != 2 && bd != 4 && bd != 8) return false;
+    if (a->n_centroids > 256) return false;
+    const int rows = (a->num_q_heads / a->num_kv_heads) * a->q_len;
+    if (rows > 16) return false;
+    if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;
+    const int nb = a->n_blocks;
+    const int cal = nb >= 16 ? 16 : 8;  // code row loads of 16 (or 8) bytes
+    if ((uintptr_t)a->codes % cal || a->c_st % cal || a->c_sh % cal || a->c_sb % cal) return false;
+    pl.DT = 4;
+    if (has_v) {
+        if (a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16) return false;
+        if (a->value_dim != 64 && a->value_dim != 128) return false;
+        if ((uintptr_t)a->v % 16 || (a->v_sb * 2) % 16 || (a->v_sh * 2) % 16 || (a->v_st * 2) % 16) return false;
+        pl.DT = a->value_dim / 16;
+    }
+    pl.smem = contig_smem(*a, pl.DT);
+    if (pl.smem > kMaxSmem) return false;
+    const int units = a->batch * a->num_kv_heads;
+    const int tiles = (a->seq_len + kTile - 1) / kTile;
+    const int cus = ssq_device_cus();
+    int splits = a->num_splits > 0 ? a->num_splits : (cus + units - 1) / units;
+    const int max_splits = (tiles + kWaves - 1) / kWaves;
+    if (splits > max_splits) splits = max_splits;
+    if (splits < 1) splits = 1;
+    const int tiles_per_split = (tiles + splits - 1) / splits;
+    pl.split_len = tiles_per_split * kTile;
+    pl.n_splits = (a->seq_len + pl.split_len - 1) / pl.split_len;
+    if (pl.n_splits < 1) pl.n_splits = 1;
+    const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
+    pl.ws_bytes = (has_v && pl.n_splits > 1) ? (size_t)pl.n_splits * n_rows_all * (a->value_dim + 2) * 4 : 0;
+    return true;
+}
+
+template <int BD, int DT, int VT, bool HAS_V>
+int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
+    auto kern = k_decode_contig<BD, DT, VT, HAS_V>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxSmem);
+        if (e != hipSuccess) return ssq_check_hip(e, "hipFuncSetAttribute(decode_contig)");
+        attr_set = true;
+    }
+    dim3 grid(cp.a.batch * cp.a.num_kv_heads, pl.n_splits);
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), pl.smem, st, cp);
+    return ssq_check_hip(hipGetLastError(), "k_decode_contig launch");
+}
+
+template <int DT, int VT, bool HAS_V>
+int launch_bd(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
+    switch (cp.a.block_dim) {
+        case 1: return launch<1, DT, VT, HAS_V>(cp, pl, st);
+        case 2: return launch<2, DT, VT, HAS_V>(cp, pl, st);
+        case 4: return launch<4, DT, VT, HAS_V>(cp, pl, st);
+        default: return launch<8, DT, VT, HAS_V>(cp, pl, st);
+    }
+}
+
+}  // namespace
+
+int ssq_decode_contig_supported(const ssq_decode_args* a) {
+    CPlan pl;
+    return plan(a, a->v != nullptr, pl) ? 1 : 0;
+}
+
+size_t ssq_decode_contig_workspace(const ssq_decode_args* a) {
+    CPlan pl;
+    return plan(a, a->v != nullptr, pl) ? pl.ws_bytes : 0;
+}
+
+// decode (a->v != NULL) or scores only (a->v == NULL, a->scores != NULL)
+int ssq_decode_contig(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipStream_t st) {
+    const bool has_v = a->v != nullptr;
+    CPlan pl;
+    if (!plan(a, has_v, pl)) return ssq_fail(SSQ_ERR_UNSUPPORTED, "contiguous MFMA kernel does not support this problem");
+    if (a->seq_len == 0) {
+        if (!has_v) return SSQ_OK;
+        return ssq_fail(SSQ_ERR_INVALID, "seq_len == 0: softmax over an empty context");
+    }
+    SSQ_REQUIRE(ws_bytes >= pl.ws_bytes, "workspace too small: %zu < %zu bytes", ws_bytes, pl.ws_bytes);
+    SSQ_REQUIRE(pl.ws_bytes == 0 || workspace, "workspace is NULL");
+    ContigParams cp;
+    cp.a = *a;
+    cp.G = a->num_q_heads / a->num_kv_heads;
+    cp.rows = cp.G * a->q_len;
+    cp.split_len = pl.split_len;
+    cp.n_splits = pl.n_splits;
+    const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
+    float* ws = reinterpret_cast<float*>(workspace);
+    cp.ws_o = ws;
+    cp.ws_m = ws ? ws + (size_t)pl.n_splits * n_rows_all * a->value_dim : nullptr;
+    cp.ws_l = ws ? cp.ws_m + (size_t)pl.n_splits * n_rows_all : nullptr;
+    int rc;
+    if (!has_v) {
+        rc = launch_bd<4, SSQ_BF16, false>(cp, pl, st);
+    } else if (a->v_dtype == SSQ_BF16) {
+        rc = pl.DT == 4 ? launch_bd<4, SSQ_BF16, true>(cp, pl, st) : launch_bd<8, SSQ_BF16, true>(cp, pl, st);
+    } else {
+        rc = pl.DT == 4 ? launch_bd<4, SSQ_F16, true>(cp, pl, st) : launch_bd<8, SSQ_F16, true>(cp, pl, st);
+    }
+    if (rc) return rc;
+    if (has_v && pl.n_splits > 1) return ssq_launch_merge(*a, pl.n_splits, cp.ws_o, cp.ws_m, cp.ws_l, st);
+    return SSQ_OK;
+}

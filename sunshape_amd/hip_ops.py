@@ -137,7 +137,7 @@ def _pt_args(heavy: Optional[Sequence[bool]], pt: Optional[torch.Tensor], pt_den
 
 def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor,
                      heavy: Optional[Sequence[bool]] = None, pt: Optional[torch.Tensor] = None,
-                     pt_dense: bool = True, code_bits: int = 0) -> torch.Tensor:
+                     pt_dense: bool = True, code_bits: int = 0, kernel: int = 0) -> torch.Tensor:
     """scores[r, t] = q_r . k_hat_t in fp32 (q in the original basis, unscaled).
 
     q [R, D]; codes uint8 [T, nb] (or int32 packed words [T, nw] with code_bits);
@@ -170,7 +170,7 @@ def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, c
         block_dim=bd, n_blocks=nb, n_centroids=nc,
         pt_dense=ptd, pt_dtype=ptdt, pt=N.ptr(pt), pt_sb=0, pt_sh=0, pt_st=0 if pt is None else pt.stride(0),
         layout=N.SSQ_CONTIGUOUS, seq_len=T, codes=N.ptr(codes), c_sb=0, c_sh=0, c_st=codes.stride(0),
-        scores=N.ptr(out), s_sb=0, s_sh=out.stride(0), s_sl=0, code_bits=int(code_bits),
+        scores=N.ptr(out), s_sb=0, s_sh=out.stride(0), s_sl=0, code_bits=int(code_bits), kernel=int(kernel),
     )
     a.heavy_mask[0], a.heavy_mask[1] = hm
     N.check(N.lib().ssq_attention_scores(ctypes.byref(a), N.stream_of(q.device)))
@@ -180,7 +180,7 @@ def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, c
 def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
                scale: Optional[float] = None, heavy: Optional[Sequence[bool]] = None,
                pt: Optional[torch.Tensor] = None, pt_dense: bool = False, code_bits: int = 0,
-               num_splits: int = 0) -> torch.Tensor:
+               num_splits: int = 0, kernel: int = 0) -> torch.Tensor:
     """Raw scores for every (batch, query head) in one launch: fp32 [B, Hq, Lq, T].
 
     q [B, Hq, Lq, D]; codes [B, Hkv, T, nb] uint8; query head h reads KV head
@@ -213,7 +213,7 @@ def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: t
         layout=N.SSQ_CONTIGUOUS, seq_len=T, codes=N.ptr(codes), c_sb=codes.stride(0), c_sh=codes.stride(1),
         c_st=codes.stride(2),
         scores=N.ptr(out), s_sb=out.stride(0), s_sh=out.stride(1), s_sl=out.stride(2), code_bits=int(code_bits),
-        num_splits=int(num_splits),
+        num_splits=int(num_splits), kernel=int(kernel),
     )
     a.heavy_mask[0], a.heavy_mask[1] = hm
     N.check(N.lib().ssq_attention_scores(ctypes.byref(a), N.stream_of(q.device)))

@@ -200,3 +200,63 @@ def test_mixed_passthrough_decode_config5_shape():
                                      heavy=hv, pt=rpt)
             assert_rel(o[b, kv * 7:(kv + 1) * 7], ro, BF16_TOL, f"mixed out b={b} kv={kv}")
             assert_rel(s[b, kv * 7:(kv + 1) * 7], rs, SCORE_TOL, f"mixed scores b={b} kv={kv}")
+
+
+# ---------------------------------------------------------------------------
+# contiguous-layout MFMA kernel (kernel 3): every block_dim, value width and dtype, with mask,
+# lse, raw scores and split counts; its scores sum in MFMA order, so they agree with the LUT
+# kernels within fp32 rounding (SCORE_TOL), not bit for bit
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("bd,Dv,vdt", [(1, 64, torch.bfloat16), (2, 64, torch.bfloat16), (4, 128, torch.bfloat16),
+                                       (8, 64, torch.float16), (2, 128, torch.float16)])
+def test_contiguous_mfma_kernel_vs_oracle(bd, Dv, vdt):
+    log(f"contig mfma bd={bd} Dv={Dv} vdt={vdt}")
+    B, Hkv, Hq, T, D = 2, 2, 14, 777, 64
+    cb = synthetic.make_codebook(Hkv, D, bd, 70 + bd)
+    g = torch.Generator().manual_seed(71 + bd)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    codes = torch.randint(0, 256, (B, Hkv, T, D // bd), generator=g, dtype=torch.uint8)
+    v = torch.randn(B, Hkv, T, Dv, generator=g).to(vdt)
+    mask = torch.zeros(B, Hq, 1, T)
+    mask[0, :, :, :37] = float("-inf")
+    mask[1, 3:9, :, 500:] = -2.5
+    scale = 1 / math.sqrt(D)
+    args = (q.to(DEV), codes.to(DEV), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+    out, lse, scores = hip_ops.decode(*args, scale=scale, mask=mask.to(DEV), return_lse=True, return_scores=True,
+                                      kernel=3)
+    vname = "bf16" if vdt == torch.bfloat16 else "f16"
+    ro, rs, rl = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
+                                    cb.perm.numpy(), scale, "bf16", vname, mask=mask.numpy(), return_scores=True)
+    assert_rel(np_of(out), ro, BF16_TOL, "out")
+    fin = np.isfinite(rs)
+    assert np.array_equal(np.isfinite(np_of(scores)), fin)
+    assert_rel(np_of(scores)[fin], rs[fin], SCORE_TOL, "scores")
+    assert_rel(np_of(lse), rl, SCORE_TOL, "lse")
+    # split counts agree, and the LUT kernel agrees within rounding
+    o1 = np_of(hip_ops.decode(*args, scale=scale, mask=mask.to(DEV), kernel=3, num_splits=1))
+    o5 = np_of(hip_ops.decode(*args, scale=scale, mask=mask.to(DEV), kernel=3, num_splits=5))
+    assert_rel(o5, o1, 1e-2, "5 vs 1 splits")
+    og = np_of(hip_ops.decode(*args, scale=scale, mask=mask.to(DEV), kernel=1))
+    assert_rel(np_of(out), og, BF16_TOL, "vs LUT kernel")
+
+
+@pytest.mark.parametrize("bd", [2, 8])
+def test_contiguous_mfma_scores_only_vs_oracle(bd):
+    log(f"contig mfma scores bd={bd}")
+    B, Hkv, Hq, T, D = 2, 2, 14, 1000, 64
+    cb = synthetic.make_codebook(Hkv, D, bd, 80 + bd)
+    g = torch.Generator().manual_seed(81 + bd)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    codes = torch.randint(0, 256, (B, Hkv, T, D // bd), generator=g, dtype=torch.uint8)
+    s3 = np_of(hip_ops.gqa_scores(q.to(DEV), codes.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV), scale=0.125,
+                                  kernel=3))
+    s1 = np_of(hip_ops.gqa_scores(q.to(DEV), codes.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV), scale=0.125,
+                                  kernel=1))
+    assert_rel(s3, s1, SCORE_TOL, "MFMA vs LUT scores")
+    G = Hq // Hkv
+    for b in range(B):
+        for kv in range(Hkv):
+            qs = O.query_scale(q[b, kv * G:(kv + 1) * G, 0].float().numpy(), 0.125, "bf16")
+            ref = O.attention_scores(qs, codes[b, kv].numpy(), cb.centroids[kv].numpy(), cb.perm[kv].numpy())
+            assert_rel(s3[b, kv * G:(kv + 1) * G, 0], ref, SCORE_TOL, f"b={b} kv={kv}")

@@ -45,8 +45,9 @@ def test_scores_over_packed_codes_equal_uint8():
     c2 = codes[0, 0].to(DEV)
     w = hip_ops.pack_codes(c2, 6)
     qq = q[0, :, 0].float().to(DEV)
-    s8 = hip_ops.attention_scores(qq, c2, perm, cent)
-    s6 = hip_ops.attention_scores(qq, w, perm, cent, code_bits=6)
+    # the same (generic LUT) kernel reads both forms
+    s8 = hip_ops.attention_scores(qq, c2, perm, cent, kernel=1)
+    s6 = hip_ops.attention_scores(qq, w, perm, cent, code_bits=6, kernel=1)
     assert torch.equal(s8, s6)
     ref = O.attention_scores(np_of(qq), np_of(c2), cb.centroids[0].numpy(), cb.perm[0].numpy())
     assert_rel(np_of(s6), ref, SCORE_TOL, "packed scores vs oracle")
