@@ -10,7 +10,7 @@ Prints ONE JSON line: keys scored/s (B*Hkv*T per step / time), achieved HBM GB/s
 algorithmic bytes and its fraction of the 8 TB/s peak, the kernel's average launch time
 from HIP events on its own stream, and a bounded CPU-oracle baseline timed on the host.
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5enc] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -37,7 +37,7 @@ def _args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5enc", "copycal"])
+    ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -60,10 +60,21 @@ def _decode_workload(name, dev, kernel):
     from sunshape_amd import _native as N
     from sunshape_amd import hip_ops, synthetic
 
+    heavy, pt = None, None
     if name == "c4":
         p = synthetic.config4(dev)
         B, Hq, Hkv, T, D, bd = 64, 32, 8, 32768, 128, 4
         paged = True
+    elif name == "c5":
+        # SunShape-Mixed: the config-5 keys encoded once (28 VQ blocks + 4 bf16 passthrough blocks)
+        p = synthetic.config5(dev)
+        B, Hq, Hkv, T, D, bd = 16, 14, 2, 16384, 64, 2
+        paged = False
+        heavy = p["heavy"].tolist()
+        codes5, pt = hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy)
+        p.tensors["codes"], p.tensors["pt"] = codes5, pt
+        p.tensors["perm"] = p["perm"][None].expand(Hkv, D)
+        p.meta["T"] = T
     else:
         p = synthetic.config3(dev)
         B, Hq, Hkv, T, D, bd = 16, 14, 2, 8192, 64, 2
@@ -81,7 +92,7 @@ def _decode_workload(name, dev, kernel):
         ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], block_table=bt, seq_lens=sl, kernel=kernel)
     else:
         codes, v = p["codes"], p["v"]
-        ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], kernel=kernel)
+        ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], heavy=heavy, pt=pt, kernel=kernel)
     a = N.DecodeArgs(
         q=q.data_ptr(), q_dtype=N.SSQ_BF16, q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
         batch=B, num_q_heads=Hq, q_len=1, head_dim=D, num_kv_heads=Hkv, has_scale=1, scale=p.meta["scale"],
@@ -94,6 +105,10 @@ def _decode_workload(name, dev, kernel):
         v=v.data_ptr(), v_dtype=N.SSQ_BF16, value_dim=Dv, v_sb=v.stride(0), v_sh=v.stride(1), v_st=v.stride(2),
         out=out.data_ptr(), o_sb=out.stride(0), o_sh=out.stride(1), o_sl=out.stride(2), kernel=kernel,
     )
+    if heavy is not None:
+        a.heavy_mask[0], a.heavy_mask[1] = N.heavy_mask_words(heavy)
+        a.pt, a.pt_dtype, a.pt_dense = pt.data_ptr(), N.SSQ_BF16, 0
+        a.pt_sb, a.pt_sh, a.pt_st = pt.stride(0), pt.stride(1), pt.stride(2)
     L = N.lib()
     ws_bytes = L.ssq_decode_workspace_size(ctypes.byref(a))
     ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
@@ -114,9 +129,11 @@ def _decode_workload(name, dev, kernel):
                   + B * Hq * Dv * 2                # bf16 out
                   + Hkv * nb * 256 * bd * 4        # fp32 codebooks
                   + Hkv * D * 8                    # int64 permutations
-                  + (B * (T // 16) * 4 if paged else 0))  # int32 block table
-    cfg = {"workload": "C4 paged fused decode (Llama-3-8B layer, 2 bits/dim)" if paged else
-           "C3 contiguous fused decode (Qwen2.5-0.5B layer, 4 bits/dim)",
+                  + (B * (T // 16) * 4 if paged else 0)  # int32 block table
+                  + (pt.numel() * 2 if pt is not None else 0))  # bf16 passthrough values
+    cfg = {"workload": {"c4": "C4 paged fused decode (Llama-3-8B layer, 2 bits/dim)",
+                        "c3": "C3 contiguous fused decode (Qwen2.5-0.5B layer, 4 bits/dim)",
+                        "c5": "C5 SunShape-Mixed fused decode (config-5 keys: 28 VQ + 4 bf16 blocks of dim 2)"}[name],
            "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "context": T, "block_dim": bd,
            "bits_per_dim": 8 / bd, "n_centroids": 256, "layout": "paged16" if paged else "contiguous",
            "kernel": kernel}
@@ -226,10 +243,16 @@ def _cpu_baseline(unit_data, seconds):
             else:
                 codes = p["codes"][b, kv].cpu().numpy()
                 v = p["v"][b, kv].float().cpu().numpy()
+            hv, ptv = None, None
+            if "pt" in p.tensors:  # SunShape-Mixed: dense passthrough values for the oracle
+                hv = np.asarray(p["heavy"].tolist())
+                ptv = np.zeros(codes.shape + (cent.shape[-1],), np.float32)
+                ptv[:, hv] = p["pt"][b, kv].float().cpu().numpy()
+                ptv = ptv[None, None]
             qu = q[b, kv * G:(kv + 1) * G][None]
             t0 = time.perf_counter()
             O.decode_attention(qu, codes[None, None], v[None, None], cent[kv][None], perm[kv][None], p.meta["scale"],
-                               "bf16", "bf16")
+                               "bf16", "bf16", heavy=hv, pt_values=ptv)
             elapsed += time.perf_counter() - t0
             units += 1
     return {"value": units * T / elapsed, "unit": "keys/s", "cores": 1, "kind": "port",
@@ -246,7 +269,7 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.workload in ("c4", "c3"):
+    if args.workload in ("c4", "c3", "c5"):
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
         step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev)

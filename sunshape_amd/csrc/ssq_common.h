@@ -35,6 +35,38 @@ __device__ __forceinline__ float ssq_load_elem(const void* p, int dt, int64_t i)
     return dt == SSQ_BF16 ? ssq_bf16_to_f32(h) : ssq_f16_to_f32(h);
 }
 
+// Load N elements of a tensor of dtype `dt` as fp32.  One uniform branch on the dtype surrounds
+// the whole batch, so all N loads are in flight together (a branch per element makes the compiler
+// wait for each load before the next one).  Every idx[i] must be a valid element offset.
+template <int N>
+__device__ __forceinline__ void ssq_load_elems(const void* p, int dt, const int64_t (&idx)[N], float (&out)[N]) {
+    if (dt == SSQ_F32) {
+        const float* f = reinterpret_cast<const float*>(p);
+#pragma unroll
+        for (int i = 0; i < N; ++i) out[i] = f[idx[i]];
+    } else {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+        uint32_t r[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) r[i] = h[idx[i]];
+        if (dt == SSQ_BF16) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) out[i] = ssq_bf16_to_f32(r[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < N; ++i) out[i] = ssq_f16_to_f32(r[i]);
+        }
+    }
+}
+
+// raw bits of element i (fp32 bits, or the 16-bit pattern zero-extended); ssq_bits_to_f32 converts
+__device__ __forceinline__ uint32_t ssq_load_bits(const void* p, int dt, int64_t i) {
+    return dt == SSQ_F32 ? reinterpret_cast<const uint32_t*>(p)[i] : (uint32_t)reinterpret_cast<const uint16_t*>(p)[i];
+}
+__device__ __forceinline__ float ssq_bits_to_f32(uint32_t u, int dt) {
+    return dt == SSQ_F32 ? __uint_as_float(u) : dt == SSQ_BF16 ? ssq_bf16_to_f32(u) : ssq_f16_to_f32(u);
+}
+
 // round an fp32 value to dtype `dt` and return it as fp32 (query scaling semantics)
 __device__ __forceinline__ float ssq_round_to(float x, int dt) {
     if (dt == SSQ_BF16) return ssq_bf16_to_f32(ssq_f32_to_bf16(x));

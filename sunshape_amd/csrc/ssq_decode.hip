@@ -170,19 +170,36 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
     float* ptile = qp + RP * D;
     float* red = smem + red_offset(a, RP, HAS_V);
 
-    // ---- 1. scaled, permuted query rows
+    // ---- 1. scaled, permuted query rows (4 elements per thread per pass, their permutation
+    // entries and gathers each issued together; indexes clamped so no load sits behind a branch)
     const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
-    for (int e = tid; e < RP * D; e += kThreads) {
-        const int r = e / D, j = e - r * D;
-        float v = 0.f;
-        if (r < nr) {
-            const int row = r0 + r;
-            const int g = row / a.q_len, qi = row - g * a.q_len;
-            const int h = kv * p.G + g;
-            v = ssq_load_elem(a.q, a.q_dtype, (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl + perm[j]);
-            if (a.has_scale) v = ssq_round_to(v * a.scale, a.q_dtype);
+    for (int e0 = 0; e0 < RP * D; e0 += 4 * kThreads) {
+        int64_t src[4];
+        bool ok[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int e = e0 + k * kThreads + tid;
+            src[k] = perm[e < RP * D ? e % D : 0];
         }
-        qp[e] = v;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int e = e0 + k * kThreads + tid;
+            const int r = e / D;
+            ok[k] = e < RP * D && r < nr;
+            if (ok[k]) {
+                const int row = r0 + r;
+                const int g = row / a.q_len, qi = row - g * a.q_len;
+                const int h = kv * p.G + g;
+                src[k] += (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl;
+            }
+        }
+        float v[4];
+        ssq_load_elems(a.q, a.q_dtype, src, v);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int e = e0 + k * kThreads + tid;
+            if (e < RP * D) qp[e] = !ok[k] ? 0.f : a.has_scale ? ssq_round_to(v[k] * a.scale, a.q_dtype) : v[k];
+        }
     }
     __syncthreads();
 
@@ -543,29 +560,85 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
 }
 
 // Combine split partials: out = sum_s o_s e^{m_s-M} / sum_s l_s e^{m_s-M}, lse = M + log L.
-__global__ __launch_bounds__(128) void k_merge(const ssq_decode_args a, int n_splits, const float* ws_o,
-                                               const float* ws_m, const float* ws_l) {
+// One workgroup per query row.  M and L are reduced over the splits by the whole workgroup (its
+// loads side by side, not one latency per split); the split weights e^{m_s-M} go to LDS in chunks,
+// and each thread sums its value dims over a chunk with 8 independent loads in flight.
+constexpr int kMergeThreads = 128;
+constexpr int kMergeChunk = 256;
+
+__device__ __forceinline__ float merge_block_reduce(float v, bool is_max, float* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float w = __shfl_xor(v, o);
+        v = is_max ? fmaxf(v, w) : v + w;
+    }
+    __syncthreads();  // red may still be read from the previous reduction
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return is_max ? fmaxf(red[0], red[1]) : red[0] + red[1];
+}
+
+__global__ __launch_bounds__(kMergeThreads) void k_merge(const ssq_decode_args a, int n_splits, const float* ws_o,
+                                                         const float* ws_m, const float* ws_l) {
+    __shared__ float wt[kMergeChunk];
+    __shared__ float red[2];
     const int rid = blockIdx.x;
+    const int tid = threadIdx.x;
     const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
     const int qi = rid % a.q_len;
     const int h = (rid / a.q_len) % a.num_q_heads;
     const int b = rid / (a.q_len * a.num_q_heads);
     float M = -INFINITY;
-    for (int s = 0; s < n_splits; ++s) M = fmaxf(M, ws_m[(size_t)s * n_rows_all + rid]);
+    for (int s = tid; s < n_splits; s += kMergeThreads) M = fmaxf(M, ws_m[(size_t)s * n_rows_all + rid]);
+    M = merge_block_reduce(M, true, red);
     float L = 0.f;
-    for (int s = 0; s < n_splits; ++s) {
+    for (int s = tid; s < n_splits; s += kMergeThreads) {
         const float ms = ws_m[(size_t)s * n_rows_all + rid];
         if (ms != -INFINITY) L += ws_l[(size_t)s * n_rows_all + rid] * __expf(ms - M);
     }
-    for (int dv = threadIdx.x; dv < a.value_dim; dv += blockDim.x) {
-        float o = 0.f;
-        for (int s = 0; s < n_splits; ++s) {
-            const float ms = ws_m[(size_t)s * n_rows_all + rid];
-            if (ms != -INFINITY) o += ws_o[((size_t)s * n_rows_all + rid) * a.value_dim + dv] * __expf(ms - M);
+    L = merge_block_reduce(L, false, red);
+    const int Dv = a.value_dim;
+    constexpr int kDvPer = 2;  // value dims per thread (Dv <= 256); more take further passes
+    for (int d0 = 0; d0 < Dv; d0 += kDvPer * kMergeThreads) {
+        float o[kDvPer];
+#pragma unroll
+        for (int k = 0; k < kDvPer; ++k) o[k] = 0.f;
+        for (int c0 = 0; c0 < n_splits; c0 += kMergeChunk) {
+            const int nch = min(kMergeChunk, n_splits - c0);
+            __syncthreads();
+            for (int i = tid; i < nch; i += kMergeThreads) {
+                const float ms = ws_m[(size_t)(c0 + i) * n_rows_all + rid];
+                wt[i] = ms != -INFINITY ? __expf(ms - M) : 0.f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < kDvPer; ++k) {
+                const int dv = d0 + k * kMergeThreads + tid;
+                if (dv >= Dv) continue;
+                const float* src = ws_o + ((size_t)c0 * n_rows_all + rid) * Dv + dv;
+                const size_t step = (size_t)n_rows_all * Dv;
+                float acc = o[k];
+                int i = 0;
+                for (; i + 8 <= nch; i += 8) {
+                    float x[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) x[u] = src[(size_t)(i + u) * step];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) acc += x[u] * wt[i + u];
+                }
+                for (; i < nch; ++i) acc += src[(size_t)i * step] * wt[i];
+                o[k] = acc;
+            }
         }
-        ssq_store_elem(a.out, a.v_dtype, (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)qi * a.o_sl + dv, o / L);
+#pragma unroll
+        for (int k = 0; k < kDvPer; ++k) {
+            const int dv = d0 + k * kMergeThreads + tid;
+            if (dv < Dv)
+                ssq_store_elem(a.out, a.v_dtype, (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)qi * a.o_sl + dv,
+                               o[k] / L);
+        }
     }
-    if (a.lse && threadIdx.x == 0) a.lse[rid] = M + logf(L);
+    if (a.lse && tid == 0) a.lse[rid] = M + logf(L);
 }
 
 // --------------------------------------------------------------------------
@@ -731,7 +804,7 @@ int run_generic(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipS
     }
     if (rc) return rc;
     if (pl.has_v && pl.n_splits > 1) {
-        hipLaunchKernelGGL(k_merge, dim3((unsigned)n_rows_all), dim3(128), 0, st, *a, pl.n_splits, dp.ws_o, dp.ws_m,
+        hipLaunchKernelGGL(k_merge, dim3((unsigned)n_rows_all), dim3(kMergeThreads), 0, st, *a, pl.n_splits, dp.ws_o, dp.ws_m,
                            dp.ws_l);
         rc = ssq_check_hip(hipGetLastError(), "k_merge launch");
     }
@@ -744,7 +817,7 @@ int run_generic(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipS
 int ssq_launch_merge(const ssq_decode_args& a, int n_splits, const float* ws_o, const float* ws_m,
                      const float* ws_l, hipStream_t st) {
     const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)n_rows_all), dim3(128), 0, st, a, n_splits, ws_o, ws_m, ws_l);
+    hipLaunchKernelGGL(k_merge, dim3((unsigned)n_rows_all), dim3(kMergeThreads), 0, st, a, n_splits, ws_o, ws_m, ws_l);
     return ssq_check_hip(hipGetLastError(), "k_merge launch");
 }
 

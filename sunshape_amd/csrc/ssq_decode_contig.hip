@@ -36,6 +36,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * SSQ_WAVE;
 constexpr int kTile = 64;  // tokens per wave iteration
 constexpr int kD = 64;     // head_dim served
+constexpr int kHP = 16;    // passthrough (heavy-block) dims per token, padded to whole MFMA steps
 constexpr size_t kMaxSmem = 160 * 1024;
 
 struct ContigParams {
@@ -44,14 +45,25 @@ struct ContigParams {
     float* ws_o;
     float* ws_m;
     float* ws_l;
+    // passthrough dims (SunShape-Mixed): the token record element and the permuted head dim of
+    // heavy dim idx (blocks ascending, then d); n_hd of them
+    int n_hd;
+    int hoff[kHP];
+    int hdim[kHP];
 };
 
 // per-wave LDS region (bytes): V tile [64][Dv] (16-bit) | codes [64][NB] | P strip [16][64] (16-bit)
+//                               | passthrough values [64][kHP] fp32 (heavy blocks only)
 __host__ __device__ constexpr int wave_v_bytes(int DT) { return kTile * DT * 16 * 2; }
-__host__ __device__ constexpr int wave_bytes(int NB, int DT) { return wave_v_bytes(DT) + kTile * NB + 16 * kTile * 2; }
+__host__ __device__ constexpr int wave_bytes(int NB, int DT, bool HV) {
+    return wave_v_bytes(DT) + kTile * NB + 16 * kTile * 2 + (HV ? kTile * kHP * 4 : 0);
+}
+// codebook region: [NB][nc][BD] fp32, padded to whole 1 KB chunks (one direct-to-LDS wave load each)
+__host__ __device__ constexpr int cb_floats(int nc) { return (16 * nc + 63) / 64 * 256; }
 inline size_t contig_smem(const ssq_decode_args& a, int DT) {
-    const size_t cb = (size_t)a.n_blocks * a.n_centroids * a.block_dim * 4;
-    const size_t main = cb + (size_t)kWaves * wave_bytes(a.n_blocks, DT);
+    const bool hv = (a.heavy_mask[0] | a.heavy_mask[1]) != 0;
+    const size_t cb = (size_t)cb_floats(a.n_centroids) * 4;
+    const size_t main = cb + (size_t)kWaves * wave_bytes(a.n_blocks, DT, hv);
     const size_t merge = (size_t)kWaves * 16 * (16 * DT + 2) * 4;
     return main > merge ? main : merge;
 }
@@ -96,20 +108,28 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// registers of one 64-token tile in flight: this lane's 16-byte V chunks and its token's code row
-template <int NB, int DT>
+// registers of one 64-token tile in flight: this lane's 16-byte V chunks, its token's code row
+// and (heavy blocks) its token's passthrough values
+template <int NB, int DT, bool HV>
 struct Tile {
     uint4 v[2 * DT];
     uint4 c[NB >= 16 ? NB / 16 : 1];
     uint2 c8;
+    uint32_t h[HV ? kHP : 1];  // raw bits (ssq_load_bits); converted when the tile goes to LDS
 };
 
 // Loads are unconditional; chunks of tokens past the split's end re-read the last token's row
 // (valid memory; such tokens get p = 0 and are never scored).
-template <int NB, int DT, bool HAS_V>
-__device__ __forceinline__ void issue_tile(const ssq_decode_args& a, int b, int kv, int t0, int t_end, int lane,
-                                           Tile<NB, DT>& R) {
+template <int NB, int DT, bool HAS_V, bool HV>
+__device__ __forceinline__ void issue_tile(const ContigParams& p, int b, int kv, int t0, int t_end, int lane,
+                                           Tile<NB, DT, HV>& R) {
+    const ssq_decode_args& a = p.a;
     const int tc = min(t0 + lane, t_end - 1);
+    if constexpr (HV) {
+        const int64_t pb = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)tc * a.pt_st;
+#pragma unroll
+        for (int i = 0; i < kHP; ++i) R.h[i] = ssq_load_bits(a.pt, a.pt_dtype, pb + p.hoff[i]);  // hoff clamped
+    }
     const uint8_t* crow = a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st;
     if constexpr (NB >= 16) {
 #pragma unroll
@@ -129,7 +149,7 @@ __device__ __forceinline__ void issue_tile(const ssq_decode_args& a, int b, int 
     }
 }
 
-template <int BD, int DT, int VT, bool HAS_V>
+template <int BD, int DT, int VT, bool HAS_V, bool HV>
 __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p) {
     constexpr int NB = kD / BD;
     constexpr int NBW = NB / 4;  // code row dwords
@@ -151,58 +171,83 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
     const int t_end = min(a.seq_len, t_begin + p.split_len);
 
     float* cb = smem;  // codebook [NB][nc][BD] fp32
-    uint8_t* wreg = reinterpret_cast<uint8_t*>(smem + (size_t)NB * nc * BD) + wave * wave_bytes(NB, DT);
+    uint8_t* wreg = reinterpret_cast<uint8_t*>(smem + cb_floats(nc)) + wave * wave_bytes(NB, DT, HV);
     uint16_t* vt = reinterpret_cast<uint16_t*>(wreg);                            // [64][Dv]
     uint8_t* ct = wreg + wave_v_bytes(DT);                                       // [64][NB]
     uint16_t* ps = reinterpret_cast<uint16_t*>(wreg + wave_v_bytes(DT) + kTile * NB);  // [16][64]
+    float* ph = reinterpret_cast<float*>(wreg + wave_v_bytes(DT) + kTile * NB + 16 * kTile * 2);  // [64][kHP]
 
-    // the first two tiles' loads go out before the prologue (two register sets in flight: a set is
-    // free again once its tile is in LDS, and then loads the tile two rounds ahead)
+    // ---- prologue.  Issue order: this lane's permutation entries, the first two tiles (two register
+    // sets in flight: a set is free again once its tile is in LDS, and then loads the tile two rounds
+    // ahead), the codebook, and the query rows unpermuted (lane j loads dim j of each row, so no load
+    // waits for the permutation): one memory latency in all.  The scaled rows then go through the
+    // wave's V-tile region (free until the first tile) to be permuted into the A operand.
+    const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
+    int64_t pj[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) pj[s] = perm[4 * s + lg];
+    int64_t pjh[HV ? kHP / 4 : 1];  // passthrough pass: permuted head dim of heavy dim 4s + lg
+    if constexpr (HV) {
+#pragma unroll
+        for (int s = 0; s < kHP / 4; ++s) pjh[s] = perm[p.hdim[4 * s + lg]];  // hdim is 0 past n_hd
+    }
+
     const int n_tiles = (t_end - t_begin + kTile - 1) / kTile;
     const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
-    Tile<NB, DT> ra, rb;
+    Tile<NB, DT, HV> ra, rb;
     if (n_tiles > 0) {
-        issue_tile<NB, DT, HAS_V>(a, b, kv, t_begin + min(wave, last_tile) * kTile, t_end, lane, ra);
-        issue_tile<NB, DT, HAS_V>(a, b, kv, t_begin + min(wave + kWaves, last_tile) * kTile, t_end, lane, rb);
+        issue_tile<NB, DT, HAS_V, HV>(p, b, kv, t_begin + min(wave, last_tile) * kTile, t_end, lane, ra);
+        issue_tile<NB, DT, HAS_V, HV>(p, b, kv, t_begin + min(wave + kWaves, last_tile) * kTile, t_end, lane, rb);
     }
 
-    // ---- prologue: codebook to LDS; this lane's query A-operand values Qp[row l16][4s + lg]
-    // (all of a thread's loads are issued before its first store: one memory latency, not 16)
-    const float* cent = a.cent + (int64_t)kv * a.cent_sh;
+    // the codebook goes global -> LDS directly (no registers): 1 KB chunks, lane l's 16 bytes at
+    // chunk + 16 l; the tail chunk's lanes past the end re-read the last float4 into the padding
     {
-        constexpr int kPer = kD * 256 / 4 / kThreads;  // float4s per thread at nc = 256
-        const int n4 = NB * nc * BD / 4;
-        float4 st[kPer];
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            const int i = tid + k * kThreads;
-            if (i < n4) st[k] = *reinterpret_cast<const float4*>(cent + 4 * i);
-        }
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            const int i = tid + k * kThreads;
-            if (i < n4) *reinterpret_cast<float4*>(cb + 4 * i) = st[k];
+        const float* cent = a.cent + (int64_t)kv * a.cent_sh;
+        const int n4 = 16 * nc;  // float4s: NB * nc * BD = 64 nc floats
+        const int n_chunks = (n4 + 63) / 64;
+        for (int c = wave; c < n_chunks; c += kWaves) {
+            const int i = min(c * 64 + lane, n4 - 1);
+            __builtin_amdgcn_global_load_lds(cent + 4 * i, (__attribute__((address_space(3))) void*)(cb + 256 * c), 16, 0,
+                                             0);
         }
     }
+
     float qa[KS];
+    float qh[HV ? kHP / 4 : 1];  // A operand of the passthrough pass: Qp[row l16][heavy dim 4s + lg]
     {
-        const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
-        int64_t pj[KS];
+        constexpr int kRows = 16;  // A-operand rows (nr <= 16)
+        int64_t src[kRows];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) pj[s] = perm[4 * s + lg];
-        int64_t qrow = -1;
-        if (l16 < nr) {
-            const int g = l16 / a.q_len, qi = l16 - g * a.q_len;
-            const int h = kv * p.G + g;
-            qrow = (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl;
+        for (int r = 0; r < kRows; ++r) {
+            src[r] = lane;  // rows past nr read row 0 and are zeroed
+            if (r < nr) {
+                const int g = r / a.q_len, qi = r - g * a.q_len;
+                const int h = kv * p.G + g;
+                src[r] += (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl;
+            }
         }
+        float qv[kRows];
+        ssq_load_elems(a.q, a.q_dtype, src, qv);
+        float* qs = reinterpret_cast<float*>(vt);  // [16][64] scaled query rows, head dims unpermuted
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-            float v = qrow >= 0 ? ssq_load_elem(a.q, a.q_dtype, qrow + pj[s]) : 0.f;
-            if (qrow >= 0 && a.has_scale) v = ssq_round_to(v * a.scale, a.q_dtype);
-            qa[s] = v;
+        for (int r = 0; r < kRows; ++r)
+            qs[r * kD + lane] = r >= nr ? 0.f : a.has_scale ? ssq_round_to(qv[r] * a.scale, a.q_dtype) : qv[r];
+        wave_sync();
+        const float* qrow = qs + l16 * kD;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qa[s] = qrow[min((uint64_t)pj[s], (uint64_t)(kD - 1))];
+        if constexpr (HV) {
+#pragma unroll
+            for (int s = 0; s < kHP / 4; ++s)  // heavy dims past n_hd are zero
+                qh[s] = 4 * s + lg < p.n_hd ? qrow[min((uint64_t)pjh[s], (uint64_t)(kD - 1))] : 0.f;
+            // passthrough blocks contribute through their stored values (second pass), not the codebook
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+                if ((a.heavy_mask[0] >> ((4 * s + lg) / BD)) & 1ull) qa[s] = 0.f;
         }
     }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's direct-to-LDS codebook loads have landed
     __syncthreads();
 
     // Codebook gather of step s: this lane supplies head dim j = 4s + lg, i.e. dim j % BD of block
@@ -222,7 +267,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
     for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
 
     // one tile: its registers -> the wave's LDS region, the set reloaded two rounds ahead, compute
-    auto step = [&](Tile<NB, DT>& R, int tile) {
+    auto step = [&](Tile<NB, DT, HV>& R, int tile) {
         const int t0 = t_begin + tile * kTile;
         wave_sync();
         if constexpr (NB >= 16) {
@@ -235,8 +280,17 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
 #pragma unroll
             for (int i = 0; i < 2 * DT; ++i) *reinterpret_cast<uint4*>(vt + (i * SSQ_WAVE + lane) * 8) = R.v[i];
         }
+        if constexpr (HV) {
+#pragma unroll
+            for (int i = 0; i < kHP; i += 4) {
+                float x[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) x[u] = i + u < p.n_hd ? ssq_bits_to_f32(R.h[i + u], a.pt_dtype) : 0.f;
+                *reinterpret_cast<float4*>(ph + lane * kHP + i) = make_float4(x[0], x[1], x[2], x[3]);
+            }
+        }
         wave_sync();
-        issue_tile<NB, DT, HAS_V>(a, b, kv, t_begin + min(tile + 2 * kWaves, last_tile) * kTile, t_end, lane, R);
+        issue_tile<NB, DT, HAS_V, HV>(p, b, kv, t_begin + min(tile + 2 * kWaves, last_tile) * kTile, t_end, lane, R);
 
         // ---- scores: S[row 4*lg+i][token 16g + l16] for the tile's 4 groups of 16 tokens
         v4f sc[4];
@@ -265,6 +319,15 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
                 const uint32_t code = min(__builtin_amdgcn_ubfe(word, lane_sh + step_sh, 8), ncm1);
                 const float kval = *reinterpret_cast<const float*>(cbb + lane_off + step_off + (code << (2 + kLogBD)));
                 c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kval, c, 0, 0, 0);
+            }
+            if constexpr (HV) {  // passthrough pass: B = the tokens' stored heavy-block values
+#pragma unroll
+                for (int s = 0; s < kHP / 4; ++s) {
+                    if (4 * s < p.n_hd) {
+                        const float kval = ph[(16 * g + l16) * kHP + 4 * s + lg];
+                        c = __builtin_amdgcn_mfma_f32_16x16x4f32(qh[s], kval, c, 0, 0, 0);
+                    }
+                }
             }
             sc[g] = c;
         }
@@ -392,7 +455,12 @@ struct CPlan {
 };
 
 bool plan(const ssq_decode_args* a, bool has_v, CPlan& pl) {
-    if (a->layout != SSQ_CONTIGUOUS || a->code_bits != 0 || a->heavy_mask[0] || a->heavy_mask[1]) return false;
+    if (a->layout != SSQ_CONTIGUOUS || a->code_bits != 0) return false;
+    if (a->heavy_mask[1]) return false;
+    if (a->heavy_mask[0]) {
+        const int n_hd = __builtin_popcountll(a->heavy_mask[0]) * a->block_dim;
+        if (n_hd > kHP || !a->pt || a->pt_dtype < SSQ_F32 || a->pt_dtype > SSQ_F16) return false;
+    }
     if (a->head_dim != kD) return false;
     const int bd = a->block_dim;
     if (bd != 1 && bd != 2 && bd != 4 && bd != 8) return false;
@@ -428,9 +496,9 @@ bool plan(const ssq_decode_args* a, bool has_v, CPlan& pl) {
     return true;
 }
 
-template <int BD, int DT, int VT, bool HAS_V>
+template <int BD, int DT, int VT, bool HAS_V, bool HV>
 int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
-    auto kern = k_decode_contig<BD, DT, VT, HAS_V>;
+    auto kern = k_decode_contig<BD, DT, VT, HAS_V, HV>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxSmem);
@@ -442,14 +510,18 @@ int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     return ssq_check_hip(hipGetLastError(), "k_decode_contig launch");
 }
 
-template <int DT, int VT, bool HAS_V>
+template <int DT, int VT, bool HAS_V, bool HV>
 int launch_bd(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     switch (cp.a.block_dim) {
-        case 1: return launch<1, DT, VT, HAS_V>(cp, pl, st);
-        case 2: return launch<2, DT, VT, HAS_V>(cp, pl, st);
-        case 4: return launch<4, DT, VT, HAS_V>(cp, pl, st);
-        default: return launch<8, DT, VT, HAS_V>(cp, pl, st);
+        case 1: return launch<1, DT, VT, HAS_V, HV>(cp, pl, st);
+        case 2: return launch<2, DT, VT, HAS_V, HV>(cp, pl, st);
+        case 4: return launch<4, DT, VT, HAS_V, HV>(cp, pl, st);
+        default: return launch<8, DT, VT, HAS_V, HV>(cp, pl, st);
     }
+}
+template <int DT, int VT, bool HAS_V>
+int launch_hv(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
+    return cp.n_hd > 0 ? launch_bd<DT, VT, HAS_V, true>(cp, pl, st) : launch_bd<DT, VT, HAS_V, false>(cp, pl, st);
 }
 
 }  // namespace
@@ -486,13 +558,27 @@ int ssq_decode_contig(const ssq_decode_args* a, void* workspace, size_t ws_bytes
     cp.ws_o = ws;
     cp.ws_m = ws ? ws + (size_t)pl.n_splits * n_rows_all * a->value_dim : nullptr;
     cp.ws_l = ws ? cp.ws_m + (size_t)pl.n_splits * n_rows_all : nullptr;
+    // passthrough dims: heavy blocks ascending, then d; record slot = block (dense) or ordinal
+    cp.n_hd = 0;
+    for (int i = 0; i < kHP; ++i) { cp.hoff[i] = 0; cp.hdim[i] = 0; }
+    for (int blk = 0, h = 0; blk < a->n_blocks && blk < 64; ++blk) {
+        if (!((a->heavy_mask[0] >> blk) & 1ull)) continue;
+        const int slot = a->pt_dense ? blk : h;
+        for (int d = 0; d < a->block_dim && cp.n_hd < kHP; ++d) {
+            cp.hoff[cp.n_hd] = slot * a->block_dim + d;
+            cp.hdim[cp.n_hd] = blk * a->block_dim + d;
+            ++cp.n_hd;
+        }
+        ++h;
+    }
+    for (int i = cp.n_hd; i < kHP; ++i) cp.hoff[i] = cp.hoff[0];  // loaded, then zeroed in the kernel
     int rc;
     if (!has_v) {
-        rc = launch_bd<4, SSQ_BF16, false>(cp, pl, st);
+        rc = launch_hv<4, SSQ_BF16, false>(cp, pl, st);
     } else if (a->v_dtype == SSQ_BF16) {
-        rc = pl.DT == 4 ? launch_bd<4, SSQ_BF16, true>(cp, pl, st) : launch_bd<8, SSQ_BF16, true>(cp, pl, st);
+        rc = pl.DT == 4 ? launch_hv<4, SSQ_BF16, true>(cp, pl, st) : launch_hv<8, SSQ_BF16, true>(cp, pl, st);
     } else {
-        rc = pl.DT == 4 ? launch_bd<4, SSQ_F16, true>(cp, pl, st) : launch_bd<8, SSQ_F16, true>(cp, pl, st);
+        rc = pl.DT == 4 ? launch_hv<4, SSQ_F16, true>(cp, pl, st) : launch_hv<8, SSQ_F16, true>(cp, pl, st);
     }
     if (rc) return rc;
     if (has_v && pl.n_splits > 1) return ssq_launch_merge(*a, pl.n_splits, cp.ws_o, cp.ws_m, cp.ws_l, st);

@@ -389,14 +389,48 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     uint16_t* pstrip = reinterpret_cast<uint16_t*>(smem + pstrip_offset(a, RP)) + wave * RP * kTileTok;
     int* pages = reinterpret_cast<int*>(smem + pages_offset(a, RP));
 
-    // ---- prologue: block-table slice, scaled permuted query rows, LUT (the loads of each
-    // stage are all issued before any is consumed)
+    // ---- prologue.  The query rows are loaded unpermuted (coalesced, independent of the
+    // permutation) together with this thread's permutation entries and the first block-table
+    // pass: one memory latency.  The rows are scaled into the LUT region (free until the LUT is
+    // built), then permuted LDS-to-LDS into qp.
     const int32_t* btab = a.block_table + (int64_t)b * a.bt_sb + t_begin / kPage;
     const int n_pages = t_end > t_begin ? (t_end - t_begin + kPage - 1) / kPage : 0;
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
-    // block-table slice: kBT entries per thread per pass, all loads issued before the stores
-    constexpr int kBT = 8;
-    for (int base = 0; base < n_pages; base += kBT * kThreads) {
+    const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
+    constexpr int kQP = (RP * 256 + kThreads - 1) / kThreads;  // head_dim <= 256 on this kernel
+    constexpr int kBT = 8;                                      // block-table entries per thread per pass
+    float qv[kQP];
+    bool ok[kQP];
+    int64_t pv[kQP];
+    {
+        int64_t src[kQP];
+#pragma unroll
+        for (int k = 0; k < kQP; ++k) {
+            const int e = tid + k * kThreads;
+            const int r = e / D, j = e - r * D;
+            pv[k] = perm[e < RP * D ? j : 0];
+            ok[k] = e < RP * D && r < nr;
+            src[k] = 0;  // rows past nr read element 0 and are zeroed
+            if (ok[k]) {
+                const int g = r / a.q_len, qi = r - g * a.q_len;
+                const int h = kv * p.G + g;
+                src[k] = (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl + j;
+            }
+        }
+        int ent[kBT];
+#pragma unroll
+        for (int k = 0; k < kBT; ++k) {
+            const int i = k * kThreads + tid;
+            ent[k] = i < n_pages ? btab[i] : 0;
+        }
+        ssq_load_elems(a.q, a.q_dtype, src, qv);
+#pragma unroll
+        for (int k = 0; k < kBT; ++k) {
+            const int i = k * kThreads + tid;
+            if (i < n_pages) pages[i] = ent[k];
+        }
+    }
+    for (int base = kBT * kThreads; base < n_pages; base += kBT * kThreads) {  // longer splits
         int ent[kBT];
 #pragma unroll
         for (int k = 0; k < kBT; ++k) {
@@ -409,32 +443,18 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
             if (i < n_pages) pages[i] = ent[k];
         }
     }
-    // scaled, permuted query rows: the permutation entries first, then the gathers
-    const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
-    constexpr int kQP = (RP * 256 + kThreads - 1) / kThreads;  // head_dim <= 256 on this kernel
-    {
-        int64_t src[kQP];
+    float* qraw = lut;  // [RP][D], scaled
 #pragma unroll
-        for (int k = 0; k < kQP; ++k) {
-            const int e = tid + k * kThreads;
-            src[k] = -1;
-            if (e < RP * D) {
-                const int r = e / D, j = e - r * D;
-                if (r < nr) {
-                    const int g = r / a.q_len, qi = r - g * a.q_len;
-                    const int h = kv * p.G + g;
-                    src[k] = (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl + perm[j];
-                }
-            }
-        }
-        float qv[kQP];
+    for (int k = 0; k < kQP; ++k) {
+        const int e = tid + k * kThreads;
+        if (e < RP * D) qraw[e] = !ok[k] ? 0.f : a.has_scale ? ssq_round_to(qv[k] * a.scale, a.q_dtype) : qv[k];
+    }
+    __syncthreads();
 #pragma unroll
-        for (int k = 0; k < kQP; ++k) qv[k] = src[k] >= 0 ? ssq_load_elem(a.q, a.q_dtype, src[k]) : 0.f;
-#pragma unroll
-        for (int k = 0; k < kQP; ++k) {
-            const int e = tid + k * kThreads;
-            if (e < RP * D) qp[e] = (src[k] >= 0 && a.has_scale) ? ssq_round_to(qv[k] * a.scale, a.q_dtype) : qv[k];
-        }
+    for (int k = 0; k < kQP; ++k) {
+        const int e = tid + k * kThreads;
+        const int r = e / D;
+        if (e < RP * D) qp[e] = qraw[r * D + (int)min((uint64_t)pv[k], (uint64_t)(D - 1))];
     }
     __syncthreads();
     // the first tile's codes and values are independent of the LUT: put them in flight before building it

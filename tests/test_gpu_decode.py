@@ -241,6 +241,63 @@ def test_contiguous_mfma_kernel_vs_oracle(bd, Dv, vdt):
     assert_rel(np_of(out), og, BF16_TOL, "vs LUT kernel")
 
 
+@pytest.mark.parametrize("bd,n_heavy,dense,pdt", [(1, 13, False, torch.bfloat16), (2, 4, False, torch.bfloat16),
+                                                  (4, 3, True, torch.float32), (8, 2, False, torch.float16)])
+def test_contiguous_mfma_kernel_mixed_passthrough(bd, n_heavy, dense, pdt):
+    """Passthrough (SunShape-Mixed) blocks on kernel 3: their score terms come from the stored
+    values (dense or compact slots, any pt dtype), the codebook supplies the rest."""
+    log(f"contig mfma mixed bd={bd} n_heavy={n_heavy} dense={dense} pdt={pdt}")
+    B, Hkv, Hq, T, D = 2, 2, 14, 555, 64
+    nb = D // bd
+    cb = synthetic.make_codebook(Hkv, D, bd, 90 + bd)
+    g = torch.Generator().manual_seed(91 + bd)
+    hidx = sorted(torch.randperm(nb, generator=g)[:n_heavy].tolist())
+    heavy = [i in hidx for i in range(nb)]
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    codes = torch.randint(0, 256, (B, Hkv, T, nb), generator=g, dtype=torch.uint8)
+    v = torch.randn(B, Hkv, T, 64, generator=g).to(torch.bfloat16)
+    ptd = torch.zeros(B, Hkv, T, nb, bd)
+    ptd[:, :, :, hidx] = torch.randn(B, Hkv, T, n_heavy, bd, generator=g)
+    ptd = ptd.to(pdt)
+    pt = ptd if dense else ptd[:, :, :, hidx].contiguous()
+    mask = torch.zeros(B, Hq, 1, T)
+    mask[1, :, :, 400:] = float("-inf")
+    scale = 1 / math.sqrt(D)
+    args = (q.to(DEV), codes.to(DEV), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+    kw = dict(scale=scale, mask=mask.to(DEV), heavy=heavy, pt=pt.to(DEV), pt_dense=dense)
+    out, lse, scores = hip_ops.decode(*args, **kw, return_lse=True, return_scores=True, kernel=3)
+    ro, rs, rl = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
+                                    cb.perm.numpy(), scale, "bf16", "bf16", mask=mask.numpy(), heavy=np.array(heavy),
+                                    pt_values=ptd.float().numpy(), return_scores=True)
+    assert_rel(np_of(out), ro, BF16_TOL, "out")
+    fin = np.isfinite(rs)
+    assert np.array_equal(np.isfinite(np_of(scores)), fin)
+    assert_rel(np_of(scores)[fin], rs[fin], SCORE_TOL, "scores")
+    assert_rel(np_of(lse), rl, SCORE_TOL, "lse")
+    og = np_of(hip_ops.decode(*args, **kw, kernel=1))
+    assert_rel(np_of(out), og, BF16_TOL, "vs LUT kernel")
+
+
+def test_contiguous_mfma_kernel_rejects_wide_passthrough():
+    """More than 16 passthrough dims do not fit the kernel's passthrough pass: an explicit
+    kernel 3 request is refused, and auto dispatch serves the call on the LUT kernel."""
+    log("contig mfma wide passthrough")
+    B, Hkv, Hq, T, D, bd = 1, 2, 8, 130, 64, 4
+    cb = synthetic.make_codebook(Hkv, D, bd, 95)
+    g = torch.Generator().manual_seed(96)
+    heavy = [i in (0, 3, 5, 9, 12) for i in range(D // bd)]  # 20 passthrough dims
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16).to(DEV)
+    codes = torch.randint(0, 256, (B, Hkv, T, D // bd), generator=g, dtype=torch.uint8).to(DEV)
+    v = torch.randn(B, Hkv, T, 64, generator=g).to(torch.bfloat16).to(DEV)
+    pt = torch.randn(B, Hkv, T, sum(heavy), bd, generator=g).to(torch.bfloat16).to(DEV)
+    args = (q, codes, v, cb.perm.to(DEV), cb.centroids.to(DEV))
+    with pytest.raises(RuntimeError):
+        hip_ops.decode(*args, scale=0.125, heavy=heavy, pt=pt, kernel=3)
+    oa = hip_ops.decode(*args, scale=0.125, heavy=heavy, pt=pt)
+    o1 = hip_ops.decode(*args, scale=0.125, heavy=heavy, pt=pt, kernel=1)
+    assert torch.equal(oa, o1)
+
+
 @pytest.mark.parametrize("bd", [2, 8])
 def test_contiguous_mfma_scores_only_vs_oracle(bd):
     log(f"contig mfma scores bd={bd}")
