@@ -167,9 +167,6 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
 #ifndef SSQ_ENC_PIPE
 #define SSQ_ENC_PIPE 1  // 0: each block's MFMAs and reduction back to back (always so with a metric)
 #endif
-#ifndef SSQ_ENC_COUNT
-#define SSQ_ENC_COUNT 1
-#endif
 constexpr int kMfmaWaves = 4;
 constexpr int kRounds = 8;        // key groups of 16 per wave per workgroup
 constexpr int kMaxLight = 128;
@@ -184,41 +181,53 @@ struct MfmaEncodeParams {
     uint8_t light[kMaxLight]; // light (VQ-coded) block ids, ascending
 };
 
-template <int CTL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTL, 0xF, 0xF, false));
+// Exchange with the lane 16 (32) apart through the gfx950 permlane swaps: the two results are this
+// lane's value and its partner's, in an order that differs between partners, so only symmetric
+// combinations (min, sum, lexicographic min) are taken of them.
+__device__ __forceinline__ void xchg16(int v, int& a, int& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    a = (int)r[0];
+    b = (int)r[1];
 }
-template <int CTL>
-__device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(v, v, CTL, 0xF, 0xF, false);
+__device__ __forceinline__ void xchg32(int v, int& a, int& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    a = (int)r[0];
+    b = (int)r[1];
 }
-// minimum over the 16 lanes of a row (row rotations; every lane of the row receives the result).
-// Rotations stay inside the row, so every lane reads a valid source and bound_ctrl never applies;
-// the plain mov_dpp form lets the compiler fold each rotation into the v_min_i32 that consumes it.
-template <int CTL>
-__device__ __forceinline__ int rot_i(int v) {
-    return __builtin_amdgcn_mov_dpp(v, CTL, 0xF, 0xF, true);
+// median of three signed ints (v_med3_i32; no builtin exposes the integer form)
+__device__ __forceinline__ int med3_i(int a, int b, int c) {
+    int r;
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
 }
-__device__ __forceinline__ int row_sum_i(int v) {
-    v += rot_i<0x121>(v); v += rot_i<0x122>(v);
-    v += rot_i<0x124>(v); v += rot_i<0x128>(v);
-    return v;
+// minimum / sum over the 4 lanes l % 16 + 16 g (one key's lanes)
+__device__ __forceinline__ int key_min_i(int v) {
+    int a, b;
+    xchg16(v, a, b); v = min(a, b);
+    xchg32(v, a, b); return min(a, b);
 }
-__device__ __forceinline__ int row_min_i(int v) {
-    v = min(v, rot_i<0x121>(v)); v = min(v, rot_i<0x122>(v));
-    v = min(v, rot_i<0x124>(v)); v = min(v, rot_i<0x128>(v));
-    return v;
+__device__ __forceinline__ int key_sum_i(int v) {
+    int a, b;
+    xchg16(v, a, b); v = a + b;
+    xchg32(v, a, b); return a + b;
 }
-// one step of a row-wide lexicographic (value, index) minimum
-template <int CTL>
-__device__ __forceinline__ void lexmin_step(float& bf, int& bn) {
-    const float of = dpp_f<CTL>(bf);
-    const int on = dpp_i<CTL>(bn);
-    if (of < bf || (of == bf && on < bn)) { bf = of; bn = on; }
+// lexicographic (value, index) minimum over the key's 4 lanes
+__device__ __forceinline__ void key_lexmin(float& bf, int& bn) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+        int fa, fb, na, nb2;
+        if (st == 0) { xchg16(__float_as_int(bf), fa, fb); xchg16(bn, na, nb2); }
+        else { xchg32(__float_as_int(bf), fa, fb); xchg32(bn, na, nb2); }
+        const float af = __int_as_float(fa), bfv = __int_as_float(fb);
+        const bool take_a = af < bfv || (af == bfv && na < nb2);
+        bf = take_a ? af : bfv;
+        bn = take_a ? na : nb2;
+    }
 }
 
-
-// A/B operands of one light block and its 16 MFMA tiles: acc[nt] holds d2[key 4*(l/16)+i][codeword 16nt + l%16]
+// Distances of one light block for the wave's 16 keys.  Codewords are the MFMA's row operand and
+// keys its column operand, so acc[nt][i] = d2[key l%16][codeword 16nt + 4(l/16) + i]: each lane
+// holds 64 of its key's 256 distances, and a key's 4 lanes sit 16 apart.
 // key element k of light block bl for key row m: the permuted key (xs through poff) or, with a
 // block metric, its image E_b x staged in ys
 template <bool MET>
@@ -231,7 +240,7 @@ template <int KS, bool MET>
 __device__ __forceinline__ void issue_block(const float* bsw, const float* xs, const float* ys, const float* xn,
                                             const int* poff, int bl, int nbc, int bd, int XS, int YS, int lane,
                                             int lane16, v4f (&acc)[16]) {
-    float av[KS];
+    float av[KS];  // column operand: [-2x, |x|^2, 1, 0..][k = 4s + l/16] of key l%16
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
         const int k = 4 * s + (lane >> 4);
@@ -248,21 +257,22 @@ __device__ __forceinline__ void issue_block(const float* bsw, const float* xs, c
         v4f c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < KS; ++s)
-            c = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s], bb[(s * 16 + nt) * 64 + lane], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(bb[(s * 16 + nt) * 64 + lane], av[s], c, 0, 0, 0);
         acc[nt] = c;
     }
 }
 
 // first-argmin of sqrt(max(d2,0)) for the 16 keys of the wave in one light block; codes -> cs[key][blk]
 //
-// Fast path, per key (4 per lane, the row's 16 lanes hold its 256 codewords):
-//  1. the minimum MFMA value with its codeword index packed into the low 8 mantissa bits.  For
-//     values >= 0 the float bit pattern orders like a signed int, and every negative value orders
-//     below them, so one integer min3 chain finds both (a 4-bit slot tag inside the lane, widened
-//     to the 8-bit codeword index for the row reduction);
-//  2. a threshold thr that provably contains the exact reference winner (bound below);
-//  3. the candidates (MFMA value <= thr) counted on the scalar unit from ballots: the key is
-//     decided when its row holds exactly one candidate, which is then the packed minimum.
+// Fast path (lane: one key, 64 of its codewords):
+//  1. the lane's minimum m1 and second minimum m2 of its MFMA values with a 6-bit slot tag in the
+//     low mantissa bits (one min and one med3 per value), compared as signed ints: for values >= 0
+//     the float bit pattern orders like a signed int, and every negative value orders below them;
+//  2. the key's minimum over its 4 lanes with the 8-bit codeword index in place of the tag, and
+//     from it a threshold thr that provably contains the exact reference winner (bound below);
+//  3. the key is decided when exactly one of its lanes has m1 <= thr and none has m2 <= thr (both
+//     with their 8 low bits cleared, which never raises a value that is >= 0 and keeps a negative
+//     one negative).  A decided key has exactly one MFMA value <= thr, and that is the minimum.
 // Keys with several candidates re-evaluate just those candidates with the reference's fp32 chain
 // and a correctly rounded sqrt, in a compact loop (one candidate per lane per trip).
 //
@@ -275,115 +285,74 @@ __device__ __forceinline__ void issue_block(const float* bsw, const float* xs, c
 // j* has d(j*) <= d(argmin) and sqrt merges values <= 2^-21 apart, hence value_j*(MFMA) <=
 // max(mn,0)*(1 + 2^-21) + 4*err.  mt, the minimum with its 8 low bits cleared, satisfies mt <= mn <
 // mt*(1 + 2^-15), so thr = max(mt,0)*(1 + 2^-14) + 5*err(mt) + 2^-100 still exceeds that bound:
-// every codeword under thr is a candidate, and so is the row minimum.
+// every codeword under thr is a candidate, and so is the key's minimum.
 template <int KS, bool MET>
 __device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, const float* ys, const float* xn,
                                              const int* poff, const int* lightL, int bl, int nbc, int nb, int bd,
                                              int XS, int YS, int lane16, int mrow, float e1, float e2,
                                              const v4f (&acc)[16], uint8_t* cs) {
-    int pm[4];
-    float thr[4];
+    const int grp = mrow >> 2;  // this lane's codeword quarter within each tile of 16
+    // 1. lane minimum and second minimum (packed: value bits, slot tag 4nt + i in the low 6 bits)
+    int m1 = __float_as_int(acc[0][0]) & -64;
+    int m2 = 0x7FFFFFFF;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int v = __float_as_int(acc[0][i]) & -16;
-#pragma unroll
-        for (int nt = 1; nt < 16; ++nt) v = min(v, (__float_as_int(acc[nt][i]) & -16) | nt);
-        pm[i] = row_min_i((v & -256) | ((v & 15) << 4) | lane16);
-        const float xnv = xn[(mrow + i) * nbc + bl];
-        const float mp = fmaxf(__int_as_float(pm[i] & -256), 0.f);
-        const float err = e1 * xnv + e2 * mp;
-        thr[i] = mp * (1.0f + 0x1.0p-14f) + 5.0f * err + 0x1.0p-100f;
-    }
-    // candidate masks: field r (16 bits) of seen = lanes of row r with a candidate; dup = lanes
-    // with two.  The row's minimum is always a candidate, so no field of seen is zero and the
-    // per-field decrement below never borrows across fields.
-    uint64_t bad[4];
-    uint64_t any_bad = 0;
-#if SSQ_ENC_COUNT == 0
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint64_t seen = __builtin_amdgcn_ballot_w64(acc[0][i] <= thr[i]);
-        uint64_t dup = 0;
-#pragma unroll
-        for (int nt = 1; nt < 16; ++nt) {
-            const uint64_t m = __builtin_amdgcn_ballot_w64(acc[nt][i] <= thr[i]);
-            dup |= seen & m;
-            seen |= m;
-        }
-        bad[i] = dup | (seen & (seen - 0x0001000100010001ull));
-        any_bad |= bad[i];
-    }
-#else
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int cnt = 0;
-#pragma unroll
-        for (int nt = 0; nt < 16; ++nt) cnt += acc[nt][i] <= thr[i] ? 1 : 0;
-        cnt = row_sum_i(cnt);
-        bad[i] = __builtin_amdgcn_ballot_w64(cnt != 1);
-        any_bad |= bad[i];
-    }
-#endif
-    int code[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) code[i] = pm[i] & 255;
-    if (any_bad) {  // rare: several candidates -> exact arithmetic decides
-        const int rsh = mrow * 4;  // bit offset of this lane's row field
-        // this lane's candidates of undecided keys: bit 16*i + nt
-        uint64_t cand = 0;
+    for (int nt = 0; nt < 16; ++nt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            if (bad[i]) {  // wave-uniform
-                const bool slow = ((bad[i] >> rsh) & 0xFFFFull) != 0;
-                uint32_t bits = 0;
+            if (nt == 0 && i == 0) continue;
+            const int v = (__float_as_int(acc[nt][i]) & -64) | (4 * nt + i);
+            m2 = med3_i(m1, m2, v);  // m1 <= m2: the second minimum of {m1, m2, v}
+            m1 = min(m1, v);
+        }
+    }
+    // 2. key minimum with the codeword index 16nt + 4grp + i in the low 8 bits
+    const int t1 = m1;
+    const int pk = key_min_i((t1 & -256) | ((t1 & 60) << 2) | (grp << 2) | (t1 & 3));
+    const float xnv = xn[lane16 * nbc + bl];
+    const float mp = fmaxf(__int_as_float(pk & -256), 0.f);
+    const float thr = mp * (1.0f + 0x1.0p-14f) + 5.0f * (e1 * xnv + e2 * mp) + 0x1.0p-100f;
+    // 3. decided keys: one lane's minimum under thr, no lane's second minimum under thr
+    const int flag = (__int_as_float(t1 & -256) <= thr ? 1 : 0) + (__int_as_float(m2 & -256) <= thr ? 2 : 0);
+    const bool undecided = key_sum_i(flag) != 1;
+    int code = pk & 255;
+    if (__builtin_amdgcn_ballot_w64(undecided)) {  // rare: several candidates -> exact arithmetic decides
+        // this lane's candidates of an undecided key: bit 4nt + i
+        uint64_t cand = 0;
+        if (undecided) {
 #pragma unroll
-                for (int nt = 0; nt < 16; ++nt) bits |= (slow && acc[nt][i] <= thr[i]) ? (1u << nt) : 0u;
-                cand |= (uint64_t)bits << (16 * i);
-            }
+            for (int nt = 0; nt < 16; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    cand |= acc[nt][i] <= thr ? (1ull << (4 * nt + i)) : 0ull;
         }
         const float* bb = bsw + (size_t)bl * KS * 1024;
         const int kc = bd + 1;
-        const float* cnp = bb + (kc >> 2) * 1024 + (kc & 3) * 16 + lane16;  // |c|^2 row of the B operand
-        float bf[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
-        int bn[4] = {4096, 4096, 4096, 4096};
+        const float* cnp = bb + (kc >> 2) * 1024 + (kc & 3) * 16;  // |c|^2 row of the codeword operand
+        float bf = INFINITY;
+        int bn = 4096;
 #pragma unroll 1
         while (cand) {
             const int pos = __builtin_ctzll(cand);
             cand &= cand - 1;
-            const int i = pos >> 4, nt = pos & 15;
-            const int m = mrow + i;
-            const float* cb = bb + nt * 64 + lane16;
+            const int r = 4 * grp + (pos & 3);  // codeword 16nt + r
+            const int nt = pos >> 2;
+            const float* cb = bb + nt * 64 + r;
             // the reference chain: k ascending FMA over [-2x, |x|^2, 1] . [c, 1, |c|^2]
-            float d2 = (-2.0f * key_elem<MET>(xs, ys, poff, XS, YS, m, bl, bd, 0)) * cb[0];
+            float d2 = (-2.0f * key_elem<MET>(xs, ys, poff, XS, YS, lane16, bl, bd, 0)) * cb[0];
 #pragma unroll 1
             for (int d = 1; d < bd; ++d)
-                d2 = __builtin_fmaf(-2.0f * key_elem<MET>(xs, ys, poff, XS, YS, m, bl, bd, d),
+                d2 = __builtin_fmaf(-2.0f * key_elem<MET>(xs, ys, poff, XS, YS, lane16, bl, bd, d),
                                     cb[(d >> 2) * 1024 + (d & 3) * 16], d2);
-            d2 = __builtin_fmaf(xn[m * nbc + bl], 1.0f, d2);
-            d2 = __builtin_fmaf(1.0f, cnp[nt * 64], d2);
+            d2 = __builtin_fmaf(xnv, 1.0f, d2);
+            d2 = __builtin_fmaf(1.0f, cnp[nt * 64 + r], d2);
             const float f = dist_of(d2);
-            const int n = 16 * nt + lane16;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                if (k == i && (f < bf[k] || (f == bf[k] && n < bn[k]))) { bf[k] = f; bn[k] = n; }
-            }
+            const int n = 16 * nt + r;
+            if (f < bf || (f == bf && n < bn)) { bf = f; bn = n; }
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (bad[i]) {  // wave-uniform
-                lexmin_step<0x121>(bf[i], bn[i]);
-                lexmin_step<0x122>(bf[i], bn[i]);
-                lexmin_step<0x124>(bf[i], bn[i]);
-                lexmin_step<0x128>(bf[i], bn[i]);
-                if (((bad[i] >> rsh) & 0xFFFFull) != 0) code[i] = bn[i];
-            }
-        }
+        key_lexmin(bf, bn);
+        if (undecided) code = bn;
     }
-    if (lane16 == 0) {
-        const int blk = lightL[bl];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) cs[(mrow + i) * nb + blk] = (uint8_t)code[i];
-    }
+    if (mrow == 0) cs[lane16 * nb + lightL[bl]] = (uint8_t)code;
 }
 
 inline int mfma_ys_stride(const ssq_encode_args& a, int nbc) { return nbc * a.block_dim + 1; }
