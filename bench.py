@@ -315,10 +315,13 @@ def main():
         "pct_hbm_peak": 100.0 * achieved_gbps / HBM_PEAK_GBPS,
         "kernel_avg_ms": avg_ms,
         "kernel_min_ms": min(launch_ms),
+        "kernel_median_ms": sorted(launch_ms)[len(launch_ms) // 2],
         "roofline": {"bound": "hbm", "achieved": achieved_gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved_gbps / HBM_PEAK_GBPS, "traffic": traffic,
                      "kernel": kname, "algorithmic_bytes_per_launch": algo_bytes},
     }
+    if "q_heads" in cfg:  # every query head scores every key: q.k scores/s = keys/s x G
+        line["qk_scores_per_s"] = line["value"] * (cfg["q_heads"] // cfg["kv_heads"])
     if args.workload == "c5enc":
         flop = keys * 28 * 256 * 2 * 4
         tf = flop / (avg_ms * 1e-3) / 1e12

@@ -51,6 +51,26 @@ __device__ __forceinline__ float metric_row(const float* e, const float* x, int 
     return acc;
 }
 
+// the same two, for register arrays of N >= bd entries (unrolled, static indexes)
+template <int N>
+__device__ __forceinline__ float sq_norm_n(const float (&v)[N], int bd) {
+    float s = v[0] * v[0];
+#pragma unroll
+    for (int d = 1; d < N; ++d) {
+        const float t = v[d] * v[d];
+        if (d < bd) s = s + t;
+    }
+    return s;
+}
+template <int N>
+__device__ __forceinline__ float metric_row_n(const float* e, const float (&x)[N], int bd) {
+    float acc = e[0] * x[0];
+#pragma unroll
+    for (int j = 1; j < N; ++j)
+        if (j < bd) acc = __builtin_fmaf(e[j], x[j], acc);
+    return acc;
+}
+
 // correctly rounded sqrt of max(v, 0)
 __device__ __forceinline__ float dist_of(float v) { return __builtin_sqrtf(v > 0.f ? v : 0.f); }
 
@@ -236,11 +256,10 @@ __device__ __forceinline__ float key_elem(const float* xs, const float* ys, cons
     return MET ? ys[m * YS + bl * bd + k] : xs[m * XS + poff[bl * bd + k]];
 }
 
+// column operand of light block bl: [-2x, |x|^2, 1, 0..][k = 4s + l/16] of key l%16
 template <int KS, bool MET>
-__device__ __forceinline__ void issue_block(const float* bsw, const float* xs, const float* ys, const float* xn,
-                                            const int* poff, int bl, int nbc, int bd, int XS, int YS, int lane,
-                                            int lane16, v4f (&acc)[16]) {
-    float av[KS];  // column operand: [-2x, |x|^2, 1, 0..][k = 4s + l/16] of key l%16
+__device__ __forceinline__ void col_operand(const float* xs, const float* ys, const float* xn, const int* poff, int bl,
+                                            int nbc, int bd, int XS, int YS, int lane, int lane16, float (&av)[KS]) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
         const int k = 4 * s + (lane >> 4);
@@ -251,6 +270,14 @@ __device__ __forceinline__ void issue_block(const float* bsw, const float* xs, c
         else v = 0.0f;
         av[s] = v;
     }
+}
+
+template <int KS, bool MET>
+__device__ __forceinline__ void issue_block(const float* bsw, const float* xs, const float* ys, const float* xn,
+                                            const int* poff, int bl, int nbc, int bd, int XS, int YS, int lane,
+                                            int lane16, v4f (&acc)[16]) {
+    float av[KS];
+    col_operand<KS, MET>(xs, ys, xn, poff, bl, nbc, bd, XS, YS, lane, lane16, av);
     const float* bb = bsw + (size_t)bl * KS * 1024;
 #pragma unroll
     for (int nt = 0; nt < 16; ++nt) {
@@ -418,33 +445,45 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
             const int blk = p.light[l0 + bl];
             em[j] = met[(int64_t)(blk * bd + k) * D + blk * bd + jj];
         }
-        __syncthreads();
     }
+    __syncthreads();
     // B operands in lane order: bsw[bl][s][nt][l] = [c, 1, |c|^2, 0..][k = 4s + l/16] of codeword 16nt + l%16
-    // (with a block metric, c' = E_b c in place of c)
-    for (int e = threadIdx.x; e < nbc * KS * 1024; e += kMfmaWaves * SSQ_WAVE) {
-        const int l = e & 63;
-        const int nt = (e >> 6) & 15;
-        const int s = (e >> 10) % KS;
-        const int bl = e / (KS * 1024);
-        const int blk = p.light[l0 + bl];
-        const int k = 4 * s + (l >> 4);
-        const float* c = cent + ((int64_t)blk * 256 + 16 * nt + (l & 15)) * bd;
-        float v = 0.0f;
-        if (MET) {
-            if (k < bd) {
-                v = metric_row(em + (bl * bd + k) * bd, c, bd);
-            } else if (k == bd + 1) {
-                float cp[12];
-                for (int kk = 0; kk < bd; ++kk) cp[kk] = metric_row(em + (bl * bd + kk) * bd, c, bd);
-                v = sq_norm(cp, bd);
-            } else if (k == bd) {
-                v = 1.0f;
+    // (with a block metric, c' = E_b c in place of c).  One codeword row per thread per pass, the
+    // loads of a pass's kRB rows issued together (indexes clamped: no load behind a branch).
+    {
+        constexpr int kCB = 4 * KS - 2;  // >= bd
+        constexpr int kRB = 8;
+        constexpr int kThr = kMfmaWaves * SSQ_WAVE;
+        const int n_rows = nbc * 256;
+        for (int r0 = 0; r0 < n_rows; r0 += kRB * kThr) {
+            float cv[kRB][kCB];
+#pragma unroll
+            for (int u = 0; u < kRB; ++u) {
+                const int r = min(r0 + u * kThr + (int)threadIdx.x, n_rows - 1);
+                const float* c = cent + ((int64_t)lightL[r >> 8] * 256 + (r & 255)) * bd;
+#pragma unroll
+                for (int d = 0; d < kCB; ++d) cv[u][d] = c[min(d, bd - 1)];
             }
-        } else {
-            v = k < bd ? c[k] : k == bd ? 1.0f : k == bd + 1 ? sq_norm(c, bd) : 0.0f;
+#pragma unroll
+            for (int u = 0; u < kRB; ++u) {
+                const int r = r0 + u * kThr + (int)threadIdx.x;
+                if (r >= n_rows) break;
+                const int bl = r >> 8, j = r & 255;
+                float cp[kCB];
+#pragma unroll
+                for (int d = 0; d < kCB; ++d) cp[d] = cv[u][d];
+                if (MET) {
+#pragma unroll
+                    for (int k = 0; k < kCB; ++k)
+                        if (k < bd) cp[k] = metric_row_n(em + (bl * bd + k) * bd, cv[u], bd);
+                }
+                const float cn = sq_norm_n(cp, bd);
+                float* dst = bsw + (size_t)bl * KS * 1024 + (j >> 4) * 64 + (j & 15);
+#pragma unroll
+                for (int k = 0; k < 4 * KS; ++k)
+                    dst[(k >> 2) * 1024 + (k & 3) * 16] = k < bd ? cp[k] : k == bd ? 1.0f : k == bd + 1 ? cn : 0.0f;
+            }
         }
-        bsw[e] = v;
     }
     __syncthreads();
 
@@ -514,7 +553,7 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
         if constexpr (SSQ_ENC_PIPE && !MET) {
-            // software pipeline: the MFMAs of block bl+1 are in flight while the VALU reduces block bl
+            // software pipeline: the MFMAs of block bl+1 run while the VALU reduces block bl
             v4f accA[16], accB[16];
             if (nbc > 0) issue_block<KS, MET>(bsw, xs, ys, xn, poff, 0, nbc, bd, XS, YS, lane, lane16, accA);
             for (int bl = 0; bl < nbc; bl += 2) {
