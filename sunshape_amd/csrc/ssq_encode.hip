@@ -343,18 +343,29 @@ __device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, 
     const bool undecided = key_sum_i(flag) != 1;
     int code = pk & 255;
     if (__builtin_amdgcn_ballot_w64(undecided)) {  // rare: several candidates -> exact arithmetic decides
-        // this lane's candidates of an undecided key: bit 4nt + i
+        // This lane's candidates of an undecided key (bit 4nt + i).  While its second minimum is
+        // over thr the lane holds at most one value <= thr, and then it is the minimum's slot;
+        // only a lane with two candidates scans all 64 values.
         uint64_t cand = 0;
         if (undecided) {
+            if (flag & 2) {
 #pragma unroll
-            for (int nt = 0; nt < 16; ++nt)
+                for (int nt = 0; nt < 16; ++nt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    cand |= acc[nt][i] <= thr ? (1ull << (4 * nt + i)) : 0ull;
+                    for (int i = 0; i < 4; ++i)
+                        cand |= acc[nt][i] <= thr ? (1ull << (4 * nt + i)) : 0ull;
+            } else if (flag & 1) {
+                cand = 1ull << (t1 & 63);
+            }
         }
         const float* bb = bsw + (size_t)bl * KS * 1024;
         const int kc = bd + 1;
         const float* cnp = bb + (kc >> 2) * 1024 + (kc & 3) * 16;  // |c|^2 row of the codeword operand
+        constexpr int kCB = 4 * KS - 2;  // >= bd
+        float xk[kCB];                   // -2x of this lane's key block (loop invariant)
+#pragma unroll
+        for (int d = 0; d < kCB; ++d)
+            xk[d] = -2.0f * key_elem<MET>(xs, ys, poff, XS, YS, lane16, bl, bd, min(d, bd - 1));
         float bf = INFINITY;
         int bn = 4096;
 #pragma unroll 1
@@ -364,14 +375,17 @@ __device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, 
             const int r = 4 * grp + (pos & 3);  // codeword 16nt + r
             const int nt = pos >> 2;
             const float* cb = bb + nt * 64 + r;
+            float cv[kCB];
+#pragma unroll
+            for (int d = 0; d < kCB; ++d) cv[d] = cb[(min(d, bd - 1) >> 2) * 1024 + (min(d, bd - 1) & 3) * 16];
+            const float cnv = cnp[nt * 64 + r];
             // the reference chain: k ascending FMA over [-2x, |x|^2, 1] . [c, 1, |c|^2]
-            float d2 = (-2.0f * key_elem<MET>(xs, ys, poff, XS, YS, lane16, bl, bd, 0)) * cb[0];
-#pragma unroll 1
-            for (int d = 1; d < bd; ++d)
-                d2 = __builtin_fmaf(-2.0f * key_elem<MET>(xs, ys, poff, XS, YS, lane16, bl, bd, d),
-                                    cb[(d >> 2) * 1024 + (d & 3) * 16], d2);
+            float d2 = xk[0] * cv[0];
+#pragma unroll
+            for (int d = 1; d < kCB; ++d)
+                if (d < bd) d2 = __builtin_fmaf(xk[d], cv[d], d2);
             d2 = __builtin_fmaf(xnv, 1.0f, d2);
-            d2 = __builtin_fmaf(1.0f, cnp[nt * 64 + r], d2);
+            d2 = __builtin_fmaf(1.0f, cnv, d2);
             const float f = dist_of(d2);
             const int n = 16 * nt + r;
             if (f < bf || (f == bf && n < bn)) { bf = f; bn = n; }
