@@ -187,15 +187,16 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
 #ifndef SSQ_ENC_PIPE
 #define SSQ_ENC_PIPE 1  // 0: each block's MFMAs and reduction back to back (always so with a metric)
 #endif
-constexpr int kMfmaWaves = 4;
+constexpr int kMfmaWaves = 8;
 constexpr int kRounds = 8;        // key groups of 16 per wave per workgroup
 constexpr int kMaxLight = 128;
-constexpr size_t kMfmaSmemCap = 80 * 1024;  // two workgroups per CU (160 KiB LDS)
+constexpr size_t kMfmaSmemCap = 160 * 1024;  // one workgroup of 8 waves per CU
 
 struct MfmaEncodeParams {
     ssq_encode_args a;
     float e1, e2;             // certification error bound: err = e1*|x|^2 + e2*max(min, 0)
     int ys_stride;            // row stride of the keys' metric images in LDS (block metric only)
+    int row_codes;            // 1: one chunk holds every light block and code rows take 16-byte stores
     int nbc;                  // light blocks per workgroup chunk
     int n_light;
     uint8_t light[kMaxLight]; // light (VQ-coded) block ids, ascending
@@ -256,28 +257,41 @@ __device__ __forceinline__ float key_elem(const float* xs, const float* ys, cons
     return MET ? ys[m * YS + bl * bd + k] : xs[m * XS + poff[bl * bd + k]];
 }
 
+// |x|^2 of key row m's light block bl (of its metric image with a block metric): the squares
+// of the block's elements rounded and summed left to right
+template <int KS, bool MET>
+__device__ __forceinline__ float key_norm(const float* xs, const float* ys, const int* poff, int XS, int YS, int m,
+                                          int bl, int bd) {
+    constexpr int kCB = 4 * KS - 2;  // >= bd
+    float x[kCB];
+#pragma unroll
+    for (int d = 0; d < kCB; ++d) x[d] = key_elem<MET>(xs, ys, poff, XS, YS, m, bl, bd, min(d, bd - 1));
+    return sq_norm_n(x, bd);
+}
+
 // column operand of light block bl: [-2x, |x|^2, 1, 0..][k = 4s + l/16] of key l%16
 template <int KS, bool MET>
-__device__ __forceinline__ void col_operand(const float* xs, const float* ys, const float* xn, const int* poff, int bl,
-                                            int nbc, int bd, int XS, int YS, int lane, int lane16, float (&av)[KS]) {
+__device__ __forceinline__ void col_operand(const float* xs, const float* ys, float xnv, const int* poff, int bl,
+                                            int bd, int XS, int YS, int lane, int lane16, float (&av)[KS]) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
         const int k = 4 * s + (lane >> 4);
         float v;
         if (k < bd) v = -2.0f * key_elem<MET>(xs, ys, poff, XS, YS, lane16, bl, bd, k);
-        else if (k == bd) v = xn[lane16 * nbc + bl];
+        else if (k == bd) v = xnv;
         else if (k == bd + 1) v = 1.0f;
         else v = 0.0f;
         av[s] = v;
     }
 }
 
+// the block's MFMAs into acc; xnv = |x|^2 of this lane's key block (also needed by the reduction)
 template <int KS, bool MET>
-__device__ __forceinline__ void issue_block(const float* bsw, const float* xs, const float* ys, const float* xn,
-                                            const int* poff, int bl, int nbc, int bd, int XS, int YS, int lane,
-                                            int lane16, v4f (&acc)[16]) {
+__device__ __forceinline__ void issue_block(const float* bsw, const float* xs, const float* ys, const int* poff, int bl,
+                                            int bd, int XS, int YS, int lane, int lane16, v4f (&acc)[16], float& xnv) {
     float av[KS];
-    col_operand<KS, MET>(xs, ys, xn, poff, bl, nbc, bd, XS, YS, lane, lane16, av);
+    xnv = key_norm<KS, MET>(xs, ys, poff, XS, YS, lane16, bl, bd);
+    col_operand<KS, MET>(xs, ys, xnv, poff, bl, bd, XS, YS, lane, lane16, av);
     const float* bb = bsw + (size_t)bl * KS * 1024;
 #pragma unroll
     for (int nt = 0; nt < 16; ++nt) {
@@ -314,8 +328,8 @@ __device__ __forceinline__ void issue_block(const float* bsw, const float* xs, c
 // mt*(1 + 2^-15), so thr = max(mt,0)*(1 + 2^-14) + 5*err(mt) + 2^-100 still exceeds that bound:
 // every codeword under thr is a candidate, and so is the key's minimum.
 template <int KS, bool MET>
-__device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, const float* ys, const float* xn,
-                                             const int* poff, const int* lightL, int bl, int nbc, int nb, int bd,
+__device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, const float* ys, float xnv,
+                                             const int* poff, const int* lightL, int bl, int nb, int bd,
                                              int XS, int YS, int lane16, int mrow, float e1, float e2,
                                              const v4f (&acc)[16], uint8_t* cs) {
     const int grp = mrow >> 2;  // this lane's codeword quarter within each tile of 16
@@ -335,7 +349,6 @@ __device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, 
     // 2. key minimum with the codeword index 16nt + 4grp + i in the low 8 bits
     const int t1 = m1;
     const int pk = key_min_i((t1 & -256) | ((t1 & 60) << 2) | (grp << 2) | (t1 & 3));
-    const float xnv = xn[lane16 * nbc + bl];
     const float mp = fmaxf(__int_as_float(pk & -256), 0.f);
     const float thr = mp * (1.0f + 0x1.0p-14f) + 5.0f * (e1 * xnv + e2 * mp) + 0x1.0p-100f;
     // 3. decided keys: one lane's minimum under thr, no lane's second minimum under thr
@@ -399,14 +412,14 @@ __device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, 
 inline int mfma_ys_stride(const ssq_encode_args& a, int nbc) { return nbc * a.block_dim + 1; }
 inline size_t mfma_enc_smem(const ssq_encode_args& a, int nbc, int KS) {
     size_t words = (size_t)nbc * KS * 1024 + a.head_dim + (size_t)nbc * (a.block_dim + 1) +
-                   (size_t)kMfmaWaves * 16 * (a.head_dim + 1) + (size_t)kMfmaWaves * 16 * nbc;
+                   (size_t)kMfmaWaves * 16 * (a.head_dim + 1);
     if (a.metric)  // E_b blocks of the chunk + the keys' metric images
         words += (size_t)nbc * a.block_dim * a.block_dim + (size_t)kMfmaWaves * 16 * mfma_ys_stride(a, nbc);
     return words * 4 + (size_t)kMfmaWaves * 16 * a.n_blocks + 64;
 }
 
 template <int KS, bool MET>
-__global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const MfmaEncodeParams p) {
+__global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const MfmaEncodeParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_encode_args& a = p.a;
     const int lane = threadIdx.x & 63;
@@ -429,19 +442,21 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
     const int hi_blk = nbc > 0 ? p.light[l0 + nbc - 1] : -1;
 
     // LDS: bsw [nbc][KS][16][64] | perm [D] | poff [nbc*bd] | lightL [nbc] | xs [waves][16][XS] |
-    //      xn [waves][16][nbc] | (MET: em [nbc][bd][bd] | ys [waves][16][YS]) | codes [waves][16][nb]
+    //      (MET: em [nbc][bd][bd] | ys [waves][16][YS]) | codes [waves][16][nb]
     float* bsw = smem;
     int* perm_l = reinterpret_cast<int*>(bsw + (size_t)nbc * KS * 1024);
     int* poff = perm_l + D;         // poff[bl*bd + d] = perm[light[bl]*bd + d]: the block's dims in the key row
     int* lightL = poff + nbc * bd;  // light block ids of this chunk
     float* xs_all = reinterpret_cast<float*>(lightL + nbc);
     float* xs = xs_all + wave * 16 * XS;
-    float* xn = xs_all + kMfmaWaves * 16 * XS + wave * 16 * nbc;
-    float* tail = xs_all + kMfmaWaves * 16 * XS + kMfmaWaves * 16 * nbc;
+    float* tail = xs_all + kMfmaWaves * 16 * XS;
     const int YS = MET ? p.ys_stride : 0;
     float* em = tail;                                  // em[bl][k][j] = E_b[k][j] (MET only)
     float* ys = em + (MET ? nbc * bd * bd : 0) + wave * 16 * YS;
     uint8_t* cs = reinterpret_cast<uint8_t*>(tail + (MET ? nbc * bd * bd + kMfmaWaves * 16 * YS : 0)) + wave * 16 * nb;
+    if (p.row_codes) {  // heavy blocks keep code 0 in the whole-row writes
+        for (int i = lane; i < 4 * nb; i += 64) reinterpret_cast<uint32_t*>(cs)[i] = 0u;
+    }
 
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
     const int64_t* perm_g = a.perm + (int64_t)kv * a.perm_sh;
@@ -548,48 +563,69 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 2) void k_encode_mfma(const 
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // block norms of the permuted rows: xn[m][bl]  (lane: key m = lane & 15, blocks lane/16 + 4k)
-        for (int bl = lane >> 4; bl < nbc; bl += 4) {
-            float x[16];
-            for (int d = 0; d < bd; ++d) x[d] = xs[lane16 * XS + poff[bl * bd + d]];
-            if (MET) {  // the key block's metric image y = E_b x
-                float y[12];
-                for (int k = 0; k < bd; ++k) y[k] = metric_row(em + (bl * bd + k) * bd, x, bd);
-                for (int k = 0; k < bd; ++k) {
-                    ys[lane16 * YS + bl * bd + k] = y[k];
-                    x[k] = y[k];
-                }
+        if constexpr (MET) {  // the key blocks' metric images y = E_b x  (lane: key m = lane & 15, blocks lane/16 + 4k)
+            for (int bl = lane >> 4; bl < nbc; bl += 4) {
+                float x[16];
+                for (int d = 0; d < bd; ++d) x[d] = xs[lane16 * XS + poff[bl * bd + d]];
+                for (int k = 0; k < bd; ++k) ys[lane16 * YS + bl * bd + k] = metric_row(em + (bl * bd + k) * bd, x, bd);
             }
-            xn[lane16 * nbc + bl] = sq_norm(x, bd);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
         if constexpr (SSQ_ENC_PIPE && !MET) {
             // software pipeline: the MFMAs of block bl+1 run while the VALU reduces block bl
             v4f accA[16], accB[16];
-            if (nbc > 0) issue_block<KS, MET>(bsw, xs, ys, xn, poff, 0, nbc, bd, XS, YS, lane, lane16, accA);
+            float xnA = 0.f, xnB = 0.f;
+            if (nbc > 0) issue_block<KS, MET>(bsw, xs, ys, poff, 0, bd, XS, YS, lane, lane16, accA, xnA);
             for (int bl = 0; bl < nbc; bl += 2) {
-                if (bl + 1 < nbc) issue_block<KS, MET>(bsw, xs, ys, xn, poff, bl + 1, nbc, bd, XS, YS, lane, lane16, accB);
-                reduce_block<KS, MET>(bsw, xs, ys, xn, poff, lightL, bl, nbc, nb, bd, XS, YS, lane16, mrow, p.e1, p.e2, accA, cs);
+                if (bl + 1 < nbc) issue_block<KS, MET>(bsw, xs, ys, poff, bl + 1, bd, XS, YS, lane, lane16, accB, xnB);
+                reduce_block<KS, MET>(bsw, xs, ys, xnA, poff, lightL, bl, nb, bd, XS, YS, lane16, mrow, p.e1, p.e2, accA, cs);
                 if (bl + 1 >= nbc) break;
-                if (bl + 2 < nbc) issue_block<KS, MET>(bsw, xs, ys, xn, poff, bl + 2, nbc, bd, XS, YS, lane, lane16, accA);
-                reduce_block<KS, MET>(bsw, xs, ys, xn, poff, lightL, bl + 1, nbc, nb, bd, XS, YS, lane16, mrow, p.e1, p.e2, accB, cs);
+                if (bl + 2 < nbc) issue_block<KS, MET>(bsw, xs, ys, poff, bl + 2, bd, XS, YS, lane, lane16, accA, xnA);
+                reduce_block<KS, MET>(bsw, xs, ys, xnB, poff, lightL, bl + 1, nb, bd, XS, YS, lane16, mrow, p.e1, p.e2, accB, cs);
             }
         } else {
             for (int bl = 0; bl < nbc; ++bl) {
                 v4f acc[16];
-                issue_block<KS, MET>(bsw, xs, ys, xn, poff, bl, nbc, bd, XS, YS, lane, lane16, acc);
-                reduce_block<KS, MET>(bsw, xs, ys, xn, poff, lightL, bl, nbc, nb, bd, XS, YS, lane16, mrow, p.e1, p.e2, acc, cs);
+                float xnv;
+                issue_block<KS, MET>(bsw, xs, ys, poff, bl, bd, XS, YS, lane, lane16, acc, xnv);
+                reduce_block<KS, MET>(bsw, xs, ys, xnv, poff, lightL, bl, nb, bd, XS, YS, lane16, mrow, p.e1, p.e2, acc, cs);
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // write this round's codes: lane (key m = lane/4) writes blocks lane%4 + 4k of its key;
-        // chunk 0 also writes the heavy blocks' code 0 and passthrough values
-        {
+        // write this round's codes.  Whole rows: the wave's code rows, complete in cs (heavy
+        // entries hold 0), go out in 16-byte pieces, then the passthrough values.  Otherwise lane
+        // (key m = lane/4) writes blocks lane%4 + 4k of its key, and chunk 0 also writes the heavy
+        // blocks' code 0 and passthrough values.
+        if (p.row_codes) {
+            const int pieces = nb >> 4;
+            for (int e = lane; e < 16 * pieces; e += 64) {
+                const int m = e / pieces, q = e - m * pieces;
+                const int s = s0 + m;
+                if (s < a.seq_len) {
+                    int64_t crow, prow;
+                    out_rows(a, b, kv, s, crow, prow);
+                    const uint32_t* src = reinterpret_cast<const uint32_t*>(cs + m * nb + 16 * q);
+                    *reinterpret_cast<uint4*>(a.codes + crow + 16 * q) = make_uint4(src[0], src[1], src[2], src[3]);
+                }
+            }
+            const int m = lane >> 2;
+            const int s = s0 + m;
+            if (do_heavy && s < a.seq_len) {
+                int64_t crow, prow;
+                out_rows(a, b, kv, s, crow, prow);
+                for (int blk = lane & 3; blk < nb; blk += 4) {
+                    if (!ssq_is_heavy(hm0, hm1, blk)) continue;
+                    const int slot = a.pt_dense ? blk : heavy_ordinal(hm0, hm1, blk);
+                    for (int d = 0; d < bd; ++d)
+                        ssq_store_elem(a.pt, a.pt_dtype, prow + (int64_t)slot * bd + d, xs[m * XS + perm_l[blk * bd + d]]);
+                }
+            }
+        } else {
             const int m = lane >> 2;
             const int s = s0 + m;
             if (s < a.seq_len) {
@@ -677,6 +713,8 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
         mp.nbc = nbc;
         mp.ys_stride = mfma_ys_stride(*a, nbc);
         const int chunks = mp.n_light > 0 ? (mp.n_light + nbc - 1) / nbc : 1;
+        mp.row_codes = chunks == 1 && a->n_blocks % 16 == 0 && (uintptr_t)a->codes % 16 == 0 && a->c_sb % 16 == 0 &&
+                       a->c_sh % 16 == 0 && a->c_st % 16 == 0;
         const int keys_wg = kMfmaWaves * kRounds * 16;
         dim3 grid((a->seq_len + keys_wg - 1) / keys_wg, a->batch * a->num_kv_heads, chunks);
         const size_t smem = mfma_enc_smem(*a, nbc, KS);
