@@ -149,7 +149,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
     const ssq_decode_args& a = p.a;
     const int tid = threadIdx.x;
     const int lane = tid & (SSQ_WAVE - 1);
-    const int wave = tid / SSQ_WAVE;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / SSQ_WAVE);  // wave-uniform: scalar loop control
     const int split = blockIdx.x;
     const int grp = blockIdx.y;
     const int bk = blockIdx.z;

@@ -110,21 +110,37 @@ __device__ __forceinline__ void wave_sync() {
 
 // registers of one 64-token tile in flight: this lane's 16-byte V chunks, its token's code row
 // and (heavy blocks) its token's passthrough values
-template <int NB, int DT, bool HV>
+template <int NB, int DT, bool HV, bool MK>
 struct Tile {
     uint4 v[2 * DT];
     uint4 c[NB >= 16 ? NB / 16 : 1];
     uint2 c8;
     uint32_t h[HV ? kHP : 1];  // raw bits (ssq_load_bits); converted when the tile goes to LDS
+    float mk[MK ? 16 : 1];     // additive mask at [row 4*lg + i][token 16g + l16], index 4g + i
 };
 
 // Loads are unconditional; chunks of tokens past the split's end re-read the last token's row
 // (valid memory; such tokens get p = 0 and are never scored).
-template <int NB, int DT, bool HAS_V, bool HV>
+template <int NB, int DT, bool HAS_V, bool HV, bool MK>
 __device__ __forceinline__ void issue_tile(const ContigParams& p, int b, int kv, int t0, int t_end, int lane,
-                                           Tile<NB, DT, HV>& R) {
+                                           Tile<NB, DT, HV, MK>& R) {
     const ssq_decode_args& a = p.a;
     const int tc = min(t0 + lane, t_end - 1);
+    if constexpr (MK) {  // clamped offsets; entries of invalid (row, token) pairs are never added
+        const int l16 = lane & 15, lg = lane >> 4;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int t = min(t0 + 16 * g + l16, t_end - 1);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = min(4 * lg + i, p.rows - 1);
+                const int gq = r / a.q_len, qi = r - gq * a.q_len;
+                const int h = kv * p.G + gq;
+                R.mk[4 * g + i] =
+                    a.mask[(int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qi * a.m_sl + (int64_t)t * a.m_st];
+            }
+        }
+    }
     if constexpr (HV) {
         const int64_t pb = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)tc * a.pt_st;
 #pragma unroll
@@ -149,7 +165,7 @@ __device__ __forceinline__ void issue_tile(const ContigParams& p, int b, int kv,
     }
 }
 
-template <int BD, int DT, int VT, bool HAS_V, bool HV>
+template <int BD, int DT, int VT, bool HAS_V, bool HV, bool MK>
 __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p) {
     constexpr int NB = kD / BD;
     constexpr int NBW = NB / 4;  // code row dwords
@@ -159,7 +175,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
     const ssq_decode_args& a = p.a;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
     const int l16 = lane & 15, lg = lane >> 4;
     const int bk = blockIdx.x;
     const int split = blockIdx.y;
@@ -194,10 +210,10 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
 
     const int n_tiles = (t_end - t_begin + kTile - 1) / kTile;
     const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
-    Tile<NB, DT, HV> ra, rb;
+    Tile<NB, DT, HV, MK> ra, rb;
     if (n_tiles > 0) {
-        issue_tile<NB, DT, HAS_V, HV>(p, b, kv, t_begin + min(wave, last_tile) * kTile, t_end, lane, ra);
-        issue_tile<NB, DT, HAS_V, HV>(p, b, kv, t_begin + min(wave + kWaves, last_tile) * kTile, t_end, lane, rb);
+        issue_tile<NB, DT, HAS_V, HV, MK>(p, b, kv, t_begin + min(wave, last_tile) * kTile, t_end, lane, ra);
+        issue_tile<NB, DT, HAS_V, HV, MK>(p, b, kv, t_begin + min(wave + kWaves, last_tile) * kTile, t_end, lane, rb);
     }
 
     // the codebook goes global -> LDS directly (no registers): 1 KB chunks, lane l's 16 bytes at
@@ -267,7 +283,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
     for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
 
     // one tile: its registers -> the wave's LDS region, the set reloaded two rounds ahead, compute
-    auto step = [&](Tile<NB, DT, HV>& R, int tile) {
+    auto step = [&](Tile<NB, DT, HV, MK>& R, int tile) {
         const int t0 = t_begin + tile * kTile;
         wave_sync();
         if constexpr (NB >= 16) {
@@ -290,7 +306,10 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
             }
         }
         wave_sync();
-        issue_tile<NB, DT, HAS_V, HV>(p, b, kv, t_begin + min(tile + 2 * kWaves, last_tile) * kTile, t_end, lane, R);
+        float mk[MK ? 16 : 1];  // this tile's mask values, taken before R is reloaded
+#pragma unroll
+        for (int k = 0; k < (MK ? 16 : 1); ++k) mk[k] = MK ? R.mk[k] : 0.f;
+        issue_tile<NB, DT, HAS_V, HV, MK>(p, b, kv, t_begin + min(tile + 2 * kWaves, last_tile) * kTile, t_end, lane, R);
 
         // ---- scores: S[row 4*lg+i][token 16g + l16] for the tile's 4 groups of 16 tokens
         v4f sc[4];
@@ -331,20 +350,26 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
             }
             sc[g] = c;
         }
-        // additive mask, raw-score output
+        // additive mask (loaded with the tile), raw-score output
+        if constexpr (MK) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int t = t0 + 16 * g + l16;
+            for (int g = 0; g < 4; ++g)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 4 * lg + i;
-                if (r < nr && t < t_end) {
-                    const int gq = r / a.q_len, qi = r - gq * a.q_len;
-                    const int h = kv * p.G + gq;
-                    if (a.mask)
-                        sc[g][i] += a.mask[(int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qi * a.m_sl +
-                                           (int64_t)t * a.m_st];
-                    if (a.scores) a.scores[(int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)qi * a.s_sl + t] = sc[g][i];
+                for (int i = 0; i < 4; ++i)
+                    if (4 * lg + i < nr && t0 + 16 * g + l16 < t_end) sc[g][i] += mk[4 * g + i];
+        }
+        if (a.scores) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int t = t0 + 16 * g + l16;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * lg + i;
+                    if (r < nr && t < t_end) {
+                        const int gq = r / a.q_len, qi = r - gq * a.q_len;
+                        const int h = kv * p.G + gq;
+                        a.scores[(int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)qi * a.s_sl + t] = sc[g][i];
+                    }
                 }
             }
         }
@@ -394,12 +419,13 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
             }
         }
     };
-    for (int tile = wave; tile < n_tiles;) {
+    // Two steps per trip and a single exit: a break between the steps made the compiler's
+    // load-counter waits at the loop head drain both register sets, i.e. no tile ahead stayed in
+    // flight.  A step past the last tile is harmless: its tokens are all past t_end, so they get
+    // probability 0 and no score or mask access.
+    for (int tile = wave; tile < n_tiles; tile += 2 * kWaves) {
         step(ra, tile);
-        tile += kWaves;
-        if (tile >= n_tiles) break;
-        step(rb, tile);
-        tile += kWaves;
+        step(rb, tile + kWaves);
     }
     if constexpr (!HAS_V) return;
 
@@ -496,9 +522,9 @@ bool plan(const ssq_decode_args* a, bool has_v, CPlan& pl) {
     return true;
 }
 
-template <int BD, int DT, int VT, bool HAS_V, bool HV>
+template <int BD, int DT, int VT, bool HAS_V, bool HV, bool MK>
 int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
-    auto kern = k_decode_contig<BD, DT, VT, HAS_V, HV>;
+    auto kern = k_decode_contig<BD, DT, VT, HAS_V, HV, MK>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxSmem);
@@ -510,18 +536,22 @@ int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     return ssq_check_hip(hipGetLastError(), "k_decode_contig launch");
 }
 
-template <int DT, int VT, bool HAS_V, bool HV>
+template <int DT, int VT, bool HAS_V, bool HV, bool MK>
 int launch_bd(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     switch (cp.a.block_dim) {
-        case 1: return launch<1, DT, VT, HAS_V, HV>(cp, pl, st);
-        case 2: return launch<2, DT, VT, HAS_V, HV>(cp, pl, st);
-        case 4: return launch<4, DT, VT, HAS_V, HV>(cp, pl, st);
-        default: return launch<8, DT, VT, HAS_V, HV>(cp, pl, st);
+        case 1: return launch<1, DT, VT, HAS_V, HV, MK>(cp, pl, st);
+        case 2: return launch<2, DT, VT, HAS_V, HV, MK>(cp, pl, st);
+        case 4: return launch<4, DT, VT, HAS_V, HV, MK>(cp, pl, st);
+        default: return launch<8, DT, VT, HAS_V, HV, MK>(cp, pl, st);
     }
+}
+template <int DT, int VT, bool HAS_V, bool HV>
+int launch_mk(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
+    return cp.a.mask ? launch_bd<DT, VT, HAS_V, HV, true>(cp, pl, st) : launch_bd<DT, VT, HAS_V, HV, false>(cp, pl, st);
 }
 template <int DT, int VT, bool HAS_V>
 int launch_hv(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
-    return cp.n_hd > 0 ? launch_bd<DT, VT, HAS_V, true>(cp, pl, st) : launch_bd<DT, VT, HAS_V, false>(cp, pl, st);
+    return cp.n_hd > 0 ? launch_mk<DT, VT, HAS_V, true>(cp, pl, st) : launch_mk<DT, VT, HAS_V, false>(cp, pl, st);
 }
 
 }  // namespace

@@ -373,7 +373,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     const ssq_decode_args& a = p.a;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
     const int bk = blockIdx.x;
     const int split = blockIdx.y;
     const int b = bk / a.num_kv_heads;

@@ -423,7 +423,7 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
     extern __shared__ __align__(16) float smem[];
     const ssq_encode_args& a = p.a;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
     const int bk = blockIdx.y;
     const int b = bk / a.num_kv_heads, kv = bk - b * a.num_kv_heads;
     const int chunk = blockIdx.z;
