@@ -404,16 +404,18 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
             } else {
                 for (int blk = 0; blk < nb; ++blk) add_block(blk, crow[blk]);
             }
-            if (a.mask) {
+            if (a.mask) {  // every row's load issued before any is added (rows past nr read row 0)
+                float mk[RP];
 #pragma unroll
                 for (int r = 0; r < RP; ++r) {
-                    if (r < nr) {
-                        const int row = r0 + r;
-                        const int g = row / a.q_len, qi = row - g * a.q_len;
-                        const int h = kv * p.G + g;
-                        s[r] += a.mask[(int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qi * a.m_sl + (int64_t)t * a.m_st];
-                    }
+                    const int row = r0 + (r < nr ? r : 0);
+                    const int g = row / a.q_len, qi = row - g * a.q_len;
+                    const int h = kv * p.G + g;
+                    mk[r] = a.mask[(int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qi * a.m_sl + (int64_t)t * a.m_st];
                 }
+#pragma unroll
+                for (int r = 0; r < RP; ++r)
+                    if (r < nr) s[r] += mk[r];
             }
             if (a.scores) {
 #pragma unroll

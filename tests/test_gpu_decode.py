@@ -278,6 +278,34 @@ def test_contiguous_mfma_kernel_mixed_passthrough(bd, n_heavy, dense, pdt):
     assert_rel(np_of(out), og, BF16_TOL, "vs LUT kernel")
 
 
+@pytest.mark.parametrize("T,splits", [(1, 0), (37, 0), (64, 1), (65, 1), (300, 1), (300, 3), (511, 7), (1333, 2)])
+def test_contiguous_mfma_kernel_edge_lengths(T, splits):
+    """Contexts shorter than a tile, tile boundaries, and split counts that leave each wave an
+    odd number of tiles (the kernel's loop then runs one step past the last tile), with q_len 2
+    and a mask; the LUT kernel on the same inputs (masked) must agree too."""
+    log(f"contig edge T={T} splits={splits}")
+    B, Hkv, Hq, Lq, D, bd = 2, 2, 14, 2, 64, 2
+    cb = synthetic.make_codebook(Hkv, D, bd, 100 + T)
+    g = torch.Generator().manual_seed(101 + T)
+    q = torch.randn(B, Hq, Lq, D, generator=g).to(torch.bfloat16)
+    codes = torch.randint(0, 256, (B, Hkv, T, D // bd), generator=g, dtype=torch.uint8)
+    v = torch.randn(B, Hkv, T, 64, generator=g).to(torch.bfloat16)
+    mask = torch.where(torch.rand(B, Hq, Lq, T, generator=g) < 0.2, float("-inf"), 0.0)
+    mask[..., 0] = 0.0  # every row keeps a key
+    scale = 1 / math.sqrt(D)
+    args = (q.to(DEV), codes.to(DEV), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+    for m in (None, mask):
+        md = None if m is None else m.to(DEV)
+        out, lse = hip_ops.decode(*args, scale=scale, mask=md, return_lse=True, kernel=3, num_splits=splits)
+        ro, _, rl = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
+                                       cb.perm.numpy(), scale, "bf16", "bf16", mask=None if m is None else m.numpy(),
+                                       return_scores=True)
+        assert_rel(np_of(out), ro, BF16_TOL, f"out mask={m is not None}")
+        assert_rel(np_of(lse), rl, SCORE_TOL, f"lse mask={m is not None}")
+        og = np_of(hip_ops.decode(*args, scale=scale, mask=md, kernel=1))
+        assert_rel(og, ro, BF16_TOL, f"LUT kernel mask={m is not None}")
+
+
 def test_contiguous_mfma_kernel_rejects_wide_passthrough():
     """More than 16 passthrough dims do not fit the kernel's passthrough pass: an explicit
     kernel 3 request is refused, and auto dispatch serves the call on the LUT kernel."""
