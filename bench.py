@@ -184,15 +184,29 @@ def _encode_workload(dev, kernel):
     heavy = p["heavy"].tolist()
     keys_t = p["keys"]
     B, Hkv, S, D = keys_t.shape
+    # the search grid is built once per codebook (as a codec caches it); kernel 2 times the
+    # exhaustive MFMA screen instead
+    grid, grid_ms = None, None
+    if kernel in (0, 3):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        grid = hip_ops.encode_grid(p["centroids"])
+        torch.cuda.synchronize()
+        grid_ms = (time.perf_counter() - t0) * 1e3
+        ref, _ = hip_ops.encode(keys_t, p["perm"], p["centroids"], heavy=heavy, kernel=2)
+        got, _ = hip_ops.encode(keys_t, p["perm"], p["centroids"], heavy=heavy, kernel=kernel, grid=grid)
+        assert torch.equal(got, ref), "grid encode differs from the MFMA encode"
 
     def step():
-        hip_ops.encode(keys_t, p["perm"], p["centroids"], heavy=heavy, kernel=kernel)
+        hip_ops.encode(keys_t, p["perm"], p["centroids"], heavy=heavy, kernel=kernel, grid=grid)
 
     n = B * Hkv * S
     algo = n * D * 2 + n * 32 + n * 4 * 2 * 2 + Hkv * 32 * 256 * 2 * 4
     cfg = {"workload": "C5 encode (16 x 2 x 16384 bf16 keys, 28 VQ + 4 bf16 blocks of dim 2)", "keys": n,
-           "head_dim": D, "block_dim": 2, "heavy_blocks": 4, "kernel": kernel}
-    return step, n, algo, cfg, None, "ssq_encode"
+           "head_dim": D, "block_dim": 2, "heavy_blocks": 4, "kernel": kernel,
+           "search": "grid" if grid is not None else "exhaustive", "grid_build_ms": grid_ms,
+           "grid_bytes": None if grid is None else grid.numel()}
+    return step, n, algo, cfg, None, "ssq_encode" if grid is None else "ssq_encode_grid"
 
 
 def _copy_workload(dev):

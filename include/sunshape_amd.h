@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SSQ_ABI_VERSION 3
+#define SSQ_ABI_VERSION 4
 
 enum ssq_status {
     SSQ_OK = 0,
@@ -154,10 +154,26 @@ typedef struct ssq_encode_args {
     uint8_t* codes; int64_t c_sb, c_sh, c_st;
     void* pt; int32_t pt_dtype; int32_t pt_dense; int64_t pt_sb, pt_sh, pt_st;
     const int64_t* slot_mapping; int64_t sm_sb; int32_t page_size;
-    int32_t kernel;      /* 0 auto, 1 VALU exact scan, 2 MFMA screen + exact certification */
+    int32_t kernel;      /* 0 auto, 1 VALU exact scan, 2 MFMA screen + exact certification, 3 grid search */
+    const void* grid; uint64_t grid_bytes;  /* optional search grid from ssq_encode_grid_build (or NULL) */
 } ssq_encode_args;
 
 int ssq_encode(const ssq_encode_args* a, void* stream);
+
+/*
+ * Search grid for the encode (block_dim 2, no block metric; no counterpart in the reference: a
+ * search structure of this library, built once per codebook and reused by every encode with
+ * that codebook).  For each codebook (one, or one per KV head) and block, a 128 x 128 grid of
+ * cells covers twice the codewords' bounding box; each cell lists, ascending, every codeword
+ * that can be the reference's first minimum for a key in the cell (rounding of the reference's
+ * fp32 evaluation included), up to 31 (more, or a key outside the grid, falls back to scanning
+ * all codewords).  ssq_encode then evaluates only those candidates, with the reference's exact
+ * arithmetic, so its codes equal kernels 1 and 2 bit for bit.
+ * The grid depends only on perm-independent codebook values (cent, cent_sh, n_blocks,
+ * n_centroids, num_kv_heads when cent_sh != 0); rebuild it when the codebook changes.
+ */
+uint64_t ssq_encode_grid_bytes(const ssq_encode_args* a);
+int ssq_encode_grid_build(const ssq_encode_args* a, void* grid, uint64_t grid_bytes, void* stream);
 
 /* k_hat[t, j] (original basis, fp32 [T, D] with row stride o_st) from codes [T, nb]
  * (row stride c_st) and optional passthrough pt (dense [T, nb, bd] fp32 when pt_dense,

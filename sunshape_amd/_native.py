@@ -30,7 +30,7 @@ SSQ_CONTIGUOUS, SSQ_PAGED = 0, 1
 
 DTYPE_CODE = {torch.float32: SSQ_F32, torch.bfloat16: SSQ_BF16, torch.float16: SSQ_F16}
 
-ABI_VERSION = 3  # SSQ_ABI_VERSION in include/sunshape_amd.h
+ABI_VERSION = 4  # SSQ_ABI_VERSION in include/sunshape_amd.h
 
 # every function include/sunshape_amd.h declares
 EXPORTED_SYMBOLS = (
@@ -39,6 +39,8 @@ EXPORTED_SYMBOLS = (
     "ssq_attention_scores",
     "ssq_lut_build",
     "ssq_encode",
+    "ssq_encode_grid_bytes",
+    "ssq_encode_grid_build",
     "ssq_dequantize",
     "ssq_pack_codes",
     "ssq_unpack_codes",
@@ -103,6 +105,7 @@ class EncodeArgs(ctypes.Structure):
         ("pt", _vp), ("pt_dtype", _i32), ("pt_dense", _i32), ("pt_sb", _i64), ("pt_sh", _i64), ("pt_st", _i64),
         ("slot_mapping", _vp), ("sm_sb", _i64), ("page_size", _i32),
         ("kernel", _i32),
+        ("grid", _vp), ("grid_bytes", ctypes.c_uint64),
     ]
 
     def __init__(self, **kw):
@@ -128,6 +131,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ssq_lut_build.restype = ctypes.c_int
     lib.ssq_encode.argtypes = [P(EncodeArgs), _vp]
     lib.ssq_encode.restype = ctypes.c_int
+    lib.ssq_encode_grid_bytes.argtypes = [P(EncodeArgs)]
+    lib.ssq_encode_grid_bytes.restype = ctypes.c_uint64
+    lib.ssq_encode_grid_build.argtypes = [P(EncodeArgs), _vp, ctypes.c_uint64, _vp]
+    lib.ssq_encode_grid_build.restype = ctypes.c_int
     lib.ssq_dequantize.argtypes = [_vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _i64,
                                    _vp, _i64, _vp]
     lib.ssq_dequantize.restype = ctypes.c_int

@@ -107,6 +107,9 @@ int ssq_check_hip(hipError_t e, const char* what);
 
 // compute units of the current device (cached per device; 256 on MI355X)
 int ssq_device_cus();
+// grid-search encode (ssq_encode_grid.hip)
+bool ssq_encode_grid_supported(const ssq_encode_args* a);
+int ssq_encode_grid_run(const ssq_encode_args* a, hipStream_t st);
 
 #define SSQ_REQUIRE(cond, ...)                                  \
     do {                                                        \

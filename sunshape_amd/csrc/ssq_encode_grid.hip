@@ -1,0 +1,548 @@
+// Grid-search encode for block_dim 2 (no block metric): exact nearest codeword with the
+// reference's rounding, evaluating only the codewords a cell grid certifies as possible winners.
+//
+// Reference semantics (sunshape/codec.py:362-385): code = first argmin_c sqrt(clamp_min(
+// [-2x, |x|^2, 1] . [c, 1, |c|^2], 0)), the dot product a k-ascending FMA chain from the first
+// product and the norms left-to-right sums of rounded squares (torch.cdist's mm formulation).
+//
+//  * k_grid_header / k_grid_cells (built once per codebook, ssq_encode_grid_build): per block, a
+//    kG x kG grid of cells over twice the codewords' bounding box.  Cell C lists, ascending, every
+//    codeword j with dmin(C, c_j)^2 <= min_k dmax(C, c_k)^2 + M_C, where M_C bounds the rounding
+//    terms below; more than 31 such codewords mark the cell "scan all".
+//  * k_encode_grid: lane = key.  Per light block: the key's two permuted elements, its cell, the
+//    cell's record (32 bytes from the grid), then the reference chain on each listed candidate in
+//    ascending order, keeping the first minimum of the correctly rounded sqrt.  Keys outside the
+//    grid and "scan all" cells evaluate every codeword.
+//
+// Why the list holds the winner.  Let r_j be the reference's value for codeword j, D_j the exact
+// value of the same expression on the same (rounded) norms, d_j = |x - c_j|.  Then |r_j - D_j| <=
+// e_j = g (|x| + |c_j|)^2 (1 + 2.001u) with g = 1.001 K 2^-23, K = bd + 2 (any rounding order),
+// and D_j = d_j^2 + alpha + beta_j with |alpha| <= 2.001u|x|^2, |beta_j| <= 2.001u|c_j|^2, u = 2^-24.
+// The winner j* has sqrt(max(r_j*, 0)) <= sqrt(max(r_k, 0)) for every k, so max(r_j*, 0) <=
+// max(r_k, 0)(1 + 2^-21) (correctly rounded sqrt).  Chaining the bounds, for every k:
+//   d_j*^2 <= d_k^2 + 2|alpha| + |beta_j*| + |beta_k| + e_j* + e_k + (d_k^2 + |alpha| + |beta_k| + e_k) 2^-21.
+// For x in C (R = max |x| over C, Rc = max |c|): d_j*^2 >= dmin(C, c_j*)^2 and, for the k that
+// minimises dmax(C, c_k), d_k^2 <= dmax(C, c_k)^2 =: dmm, giving dmin(C, c_j*)^2 <= dmm + M_C with
+//   M_C = 1.01 (4.002u (R^2 + Rc^2) + 2.0002 g (R + Rc)^2 + (dmm + 2.001u (R^2 + Rc^2) + g (R + Rc)^2) 2^-21).
+// Cells are widened by 0.001 of a cell on each side, far more than the fp32 rounding of the
+// search kernel's cell index, so a key always lies in the cell it is looked up in.  The build
+// runs in fp64.
+#include "ssq_common.h"
+
+#include <math.h>
+#include <string.h>
+
+namespace {
+
+constexpr int kG = 128;        // cells per dimension
+constexpr int kRec = 32;       // bytes per cell record: count (255 = scan all), then indices
+constexpr int kMaxCand = kRec - 1;
+constexpr int kHdr = 8;        // floats per block header: lo0, lo1, inv_h0, inv_h1, Rc, valid
+constexpr int kThreads = 256;
+
+inline int grid_heads(const ssq_encode_args& a) { return a.cent_sh == 0 ? 1 : a.num_kv_heads; }
+inline size_t grid_hdr_bytes(const ssq_encode_args& a) {
+    return ((size_t)grid_heads(a) * a.n_blocks * kHdr * 4 + 255) & ~(size_t)255;
+}
+inline size_t grid_total_bytes(const ssq_encode_args& a) {
+    return grid_hdr_bytes(a) + (size_t)grid_heads(a) * a.n_blocks * kG * kG * kRec;
+}
+
+// ---------------------------------------------------------------------------
+// build
+// ---------------------------------------------------------------------------
+// one workgroup per (block, codebook head): bounding box, max |c|, grid origin and pitch
+__global__ __launch_bounds__(kThreads) void k_grid_header(const float* cent, int64_t cent_sh, int nb, int nc,
+                                                          float* hdr) {
+    __shared__ float red[5][kThreads];
+    const int blk = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+    const float* c = cent + (int64_t)h * cent_sh + (int64_t)blk * nc * 2;
+    float mn0 = INFINITY, mx0 = -INFINITY, mn1 = INFINITY, mx1 = -INFINITY, nrm = 0.f;
+    for (int j = tid; j < nc; j += kThreads) {
+        const float v0 = c[2 * j], v1 = c[2 * j + 1];
+        mn0 = fminf(mn0, v0); mx0 = fmaxf(mx0, v0);
+        mn1 = fminf(mn1, v1); mx1 = fmaxf(mx1, v1);
+        nrm = fmaxf(nrm, (float)((double)v0 * v0 + (double)v1 * v1));
+        if (!isfinite(v0) || !isfinite(v1)) nrm = INFINITY;
+    }
+    red[0][tid] = mn0; red[1][tid] = mx0; red[2][tid] = mn1; red[3][tid] = mx1; red[4][tid] = nrm;
+    __syncthreads();
+    for (int o = kThreads / 2; o > 0; o >>= 1) {
+        if (tid < o) {
+            red[0][tid] = fminf(red[0][tid], red[0][tid + o]);
+            red[1][tid] = fmaxf(red[1][tid], red[1][tid + o]);
+            red[2][tid] = fminf(red[2][tid], red[2][tid + o]);
+            red[3][tid] = fmaxf(red[3][tid], red[3][tid + o]);
+            red[4][tid] = fmaxf(red[4][tid], red[4][tid + o]);
+        }
+        __syncthreads();
+    }
+    if (tid != 0) return;
+    float* out = hdr + ((int64_t)h * nb + blk) * kHdr;
+    const double lo[2] = {red[0][0], red[2][0]}, hi[2] = {red[1][0], red[3][0]};
+    bool valid = isfinite(red[4][0]);
+    float org[2], inv[2];
+    for (int d = 0; d < 2; ++d) {
+        const double mid = 0.5 * (lo[d] + hi[d]);
+        double half = (hi[d] - lo[d]);  // twice the box's half-width
+        if (!(half > fabs(mid) * 0x1.0p-20)) half = fmax(fabs(mid) * 0x1.0p-20, 0x1.0p-60);
+        org[d] = (float)(mid - half);
+        const double pitch = 2.0 * half / kG;
+        inv[d] = (float)(1.0 / pitch);
+        valid = valid && isfinite(org[d]) && isfinite(inv[d]) && inv[d] > 0.f;
+    }
+    out[0] = org[0]; out[1] = org[1]; out[2] = inv[0]; out[3] = inv[1];
+    out[4] = (float)(sqrt((double)red[4][0]) * (1.0 + 0x1.0p-20));
+    out[5] = valid ? 1.f : 0.f;
+    out[6] = 0.f; out[7] = 0.f;
+}
+
+// one thread per cell
+__global__ __launch_bounds__(kThreads) void k_grid_cells(const float* cent, int64_t cent_sh, int nb, int nc,
+                                                         const float* hdr, uint8_t* cells) {
+    __shared__ double cw[256][2];
+    const int blk = blockIdx.y, h = blockIdx.z, tid = threadIdx.x;
+    const int cell = blockIdx.x * kThreads + tid;
+    const float* c = cent + (int64_t)h * cent_sh + (int64_t)blk * nc * 2;
+    for (int j = tid; j < nc; j += kThreads) { cw[j][0] = c[2 * j]; cw[j][1] = c[2 * j + 1]; }
+    __syncthreads();
+    const float* hd = hdr + ((int64_t)h * nb + blk) * kHdr;
+    uint8_t rec[kRec];
+#pragma unroll
+    for (int i = 0; i < kRec; ++i) rec[i] = 0;
+    if (hd[5] == 0.f) {
+        rec[0] = 255;
+    } else {
+        const int i0 = cell / kG, i1 = cell - (cell / kG) * kG;
+        const double a0 = (double)hd[0] + ((double)i0 - 0.001) / (double)hd[2];
+        const double b0 = (double)hd[0] + ((double)i0 + 1.001) / (double)hd[2];
+        const double a1 = (double)hd[1] + ((double)i1 - 0.001) / (double)hd[3];
+        const double b1 = (double)hd[1] + ((double)i1 + 1.001) / (double)hd[3];
+        const double R2 = fmax(a0 * a0, b0 * b0) + fmax(a1 * a1, b1 * b1);
+        const double R = sqrt(R2), Rc = hd[4];
+        double dmm = INFINITY;
+        for (int j = 0; j < nc; ++j) {
+            const double dx = fmax(fabs(a0 - cw[j][0]), fabs(b0 - cw[j][0]));
+            const double dy = fmax(fabs(a1 - cw[j][1]), fabs(b1 - cw[j][1]));
+            dmm = fmin(dmm, dx * dx + dy * dy);
+        }
+        const double u = 0x1.0p-24, g = 1.001 * 4 * 0x1.0p-23;  // K = bd + 2 = 4
+        const double S = (R + Rc) * (R + Rc), N2 = R2 + Rc * Rc;
+        const double M = 1.01 * (4.002 * u * N2 + 2.0002 * g * S + (dmm + 2.001 * u * N2 + g * S) * 0x1.0p-21);
+        const double bound = dmm + M;
+        int cnt = 0;
+        for (int j = 0; j < nc; ++j) {
+            const double dx = fmax(fmax(a0 - cw[j][0], cw[j][0] - b0), 0.0);
+            const double dy = fmax(fmax(a1 - cw[j][1], cw[j][1] - b1), 0.0);
+            if (dx * dx + dy * dy <= bound) {
+                if (cnt < kMaxCand) rec[1 + cnt] = (uint8_t)j;
+                ++cnt;
+            }
+        }
+        rec[0] = cnt <= kMaxCand ? (uint8_t)cnt : 255;
+    }
+    uint4* dst = reinterpret_cast<uint4*>(cells + (((int64_t)h * nb + blk) * kG * kG + cell) * kRec);
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(rec);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// ---------------------------------------------------------------------------
+// search
+// ---------------------------------------------------------------------------
+constexpr int kMaxLight = 128;
+
+struct GridParams {
+    ssq_encode_args a;
+    const float* hdr;
+    const uint8_t* cells;
+    int n_light;
+    int row_codes;             // whole code rows in 16-byte stores
+    int row_q;                 // 16-byte pieces of a key row when rows are read whole (else 0)
+    uint8_t light[kMaxLight];  // light block ids, ascending
+};
+
+// LDS layout (bytes): cb [nl][256] float2 | cn [nl][256] float | hd [nl] float4 | poff [nl][4] int |
+// codes [waves][64][nb]
+inline size_t grid_smem(int nl, int nb, int waves) {
+    return (size_t)nl * 256 * 12 + (size_t)nl * 16 + (size_t)nl * 16 + (size_t)waves * 64 * nb;
+}
+
+struct Cand {  // running first minimum of sqrt(max(d2, 0)) over ascending codeword indices
+    float bd;  // clamped pre-sqrt value of the best so far
+    int bj;
+};
+
+// the reference's chain for codeword (c, |c|^2) of index j, then the first-minimum update
+// (ok = false leaves the state alone)
+__device__ __forceinline__ void eval_val(float2 c, float cq, int j, float m0, float m1, float xn, bool ok,
+                                         Cand& st) {
+    float d2 = m0 * c.x;                     // (-2 x0) c0, rounded
+    d2 = __builtin_fmaf(m1, c.y, d2);        // + (-2 x1) c1
+    d2 = __builtin_fmaf(xn, 1.0f, d2);       // + |x|^2 . 1
+    d2 = __builtin_fmaf(1.0f, cq, d2);       // + 1 . |c|^2
+    const float dc = d2 > 0.f ? d2 : 0.f;
+    // dc < bd (1 - 2^-20) gives a strictly smaller correctly rounded sqrt; values within
+    // (1 +- 2^-20) of bd compare their square roots; anything larger loses
+    // (bitwise operators, a wave-uniform test and an opaque statement: one rarely taken branch,
+    // which the compiler would otherwise flatten into two correctly rounded square roots per
+    // candidate)
+    bool take = (st.bj < 0) | (dc < st.bd * (1.0f - 0x1.0p-20f));
+    const bool near = ok & !take & (dc <= st.bd * (1.0f + 0x1.0p-20f));
+    if (__builtin_amdgcn_ballot_w64(near)) {
+        __asm__ volatile("" ::: "memory");  // keeps the branch: not speculated
+        const bool lt = __builtin_sqrtf(dc) < __builtin_sqrtf(st.bd);
+        take = near ? lt : take;
+    }
+    take &= ok;
+    st.bd = take ? dc : st.bd;
+    st.bj = take ? j : st.bj;
+}
+
+__device__ __forceinline__ void eval_cand(const float2* cb, const float* cn, int j, float m0, float m1, float xn,
+                                          Cand& st) {
+    eval_val(cb[j], cn[j], j, m0, m1, xn, true, st);
+}
+
+template <bool ROWREG>
+__global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
+    extern __shared__ __align__(16) float smem[];
+    const ssq_encode_args& a = p.a;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int waves = blockDim.x >> 6;
+    const int bk = blockIdx.y;
+    const int b = bk / a.num_kv_heads, kv = bk - b * a.num_kv_heads;
+    const int nl = p.n_light, nb = a.n_blocks, nc = a.n_centroids;
+    const int hsel = a.cent_sh == 0 ? 0 : kv;
+
+    float2* cb = reinterpret_cast<float2*>(smem);                          // [nl][256]
+    float* cn = reinterpret_cast<float*>(cb + nl * 256);                   // [nl][256]
+    float4* hd = reinterpret_cast<float4*>(cn + nl * 256);                 // [nl]: lo0, lo1, inv_h0, inv_h1
+    int* poff = reinterpret_cast<int*>(hd + nl);                           // [nl]: perm0, perm1, block id, 0
+    uint8_t* cs = reinterpret_cast<uint8_t*>(poff + 4 * nl) + wave * 64 * nb;  // this wave's code rows
+
+    // ---- stage the light blocks' codewords, |c|^2 (rounded squares summed left to right), headers
+    const float* cent = a.cent + (int64_t)kv * a.cent_sh;
+    const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
+    for (int e = threadIdx.x; e < nl * 256; e += blockDim.x) {
+        const int li = e >> 8, j = e & 255;
+        if (j < nc) {
+            const float* c = cent + ((int64_t)p.light[li] * nc + j) * 2;
+            const float c0 = c[0], c1 = c[1];
+            cb[e] = make_float2(c0, c1);
+            const float t0 = c0 * c0, t1 = c1 * c1;
+            cn[e] = t0 + t1;
+        }
+    }
+    for (int li = threadIdx.x; li < nl; li += blockDim.x) {
+        const float* h = p.hdr + ((int64_t)hsel * nb + p.light[li]) * kHdr;
+        hd[li] = h[5] != 0.f ? make_float4(h[0], h[1], h[2], h[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+        poff[4 * li] = (int)perm[p.light[li] * 2];
+        poff[4 * li + 1] = (int)perm[p.light[li] * 2 + 1];
+        poff[4 * li + 2] = p.light[li];  // kept in LDS: a kernel-argument array indexed in the loop
+        poff[4 * li + 3] = 0;            // would be a memory load that waits for every pending load
+    }
+    for (int i = lane; i < 16 * nb; i += 64) reinterpret_cast<uint32_t*>(cs)[i] = 0u;  // heavy blocks: code 0
+    __syncthreads();
+
+    const uint64_t hm0 = a.heavy_mask[0], hm1 = a.heavy_mask[1];
+    const int64_t krow0 = (int64_t)b * a.k_sb + (int64_t)kv * a.k_sh;
+    const uint8_t* cells = p.cells + (int64_t)hsel * nb * kG * kG * kRec;
+    const int keys_wg = waves * 64;
+    const int s = blockIdx.x * keys_wg + wave * 64 + lane;
+    const bool live = s < a.seq_len;
+    const int64_t krow = krow0 + (int64_t)(live ? s : a.seq_len - 1) * a.k_ss;
+
+    const int kdt = a.k_dtype;
+    // ---- the key's permuted elements.  ROWREG: the whole row (at most 128 bytes, 16-byte
+    // aligned) is loaded once with 16-byte loads into registers, and each block's two elements
+    // are picked out by a wave-uniform register index: one memory access per 16 bytes of key
+    // instead of one per element.  Otherwise each element is a load of its own, issued one
+    // block ahead of its use.
+    uint32_t row[32];
+    if constexpr (ROWREG) {
+        const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.keys) +
+                                                          krow * (kdt == SSQ_F32 ? 4 : 2));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint4 v = i < p.row_q ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+            row[4 * i] = v.x; row[4 * i + 1] = v.y; row[4 * i + 2] = v.z; row[4 * i + 3] = v.w;
+        }
+    }
+    // element e (wave-uniform) of the register row, as raw bits
+    auto row_bits = [&](int e) -> uint32_t {
+        if (kdt == SSQ_F32) return row[e & 31];
+        const uint32_t w = row[(e >> 1) & 31];
+        return (e & 1) ? (w >> 16) : (w & 0xffffu);
+    };
+    // light block li's permuted element positions and block id, wave-uniform
+    auto block_info = [&](int li, int& e0, int& e1, int& blk) {
+        const int4 v = reinterpret_cast<const int4*>(poff)[li];
+        e0 = __builtin_amdgcn_readfirstlane(v.x);
+        e1 = __builtin_amdgcn_readfirstlane(v.y);
+        blk = __builtin_amdgcn_readfirstlane(v.z);
+    };
+    // the byte offset of (x0, x1)'s cell record in block blk of this head's table; inside =
+    // false means "scan all" (the offset is then cell (0, 0)'s, a valid record)
+    auto cell_off = [&](int li, int blk, float x0, float x1, bool& inside) -> uint32_t {
+        const float4 h = hd[li];
+        const float f0 = floorf((x0 - h.x) * h.z), f1 = floorf((x1 - h.y) * h.w);
+        inside = h.z > 0.f && f0 >= 0.f && f0 < (float)kG && f1 >= 0.f && f1 < (float)kG;
+        const int c0 = inside ? (int)f0 : 0, c1 = inside ? (int)f1 : 0;
+        return (uint32_t)((blk * kG * kG + c0 * kG + c1) * kRec);
+    };
+    auto rec_lo = [&](uint32_t off) { return *reinterpret_cast<const uint4*>(cells + off); };
+    auto rec_hi = [&](uint32_t off) { return *reinterpret_cast<const uint4*>(cells + off + 16); };
+    // lists of 16 to 31 candidates continue in the record's second 16 bytes
+    auto needs_hi = [](const uint4& r, bool inside) {
+        const uint32_t c = r.x & 255u;
+        return inside && c > 15u && c != 255u;
+    };
+    const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
+
+    // Software pipeline over the light blocks, one block apart: at trip li the loads of trip
+    // li - 1 have landed; the trip issues the second half of block li + 1's record (lanes
+    // with long lists only) and the first half of block li + 2's, then evaluates block li.
+    // Indices past the last block are clamped to it.  Stage names: *0 = block li, *1 = li + 1.
+    float xa0 = 0.f, xb0 = 0.f, xa1 = 0.f, xb1 = 0.f;
+    uint4 lo0 = zero4, lo1 = zero4, hi0 = zero4;
+    uint32_t off1 = 0;
+    bool in0 = false, in1 = false;
+    uint32_t ua = 0, ub = 0;  // element path: raw bits of block li + 2
+    auto elems = [&](int li, float& x0, float& x1, int& blk) {
+        int e0, e1;
+        block_info(li, e0, e1, blk);
+        if constexpr (ROWREG) {
+            x0 = ssq_bits_to_f32(row_bits(e0), kdt);
+            x1 = ssq_bits_to_f32(row_bits(e1), kdt);
+        } else {
+            x0 = ssq_load_elem(a.keys, kdt, krow + e0);
+            x1 = ssq_load_elem(a.keys, kdt, krow + e1);
+        }
+    };
+    auto issue_bits = [&](int li) {
+        if constexpr (!ROWREG) {
+            const int4 v = reinterpret_cast<const int4*>(poff)[li];
+            ua = ssq_load_bits(a.keys, kdt, krow + __builtin_amdgcn_readfirstlane(v.x));
+            ub = ssq_load_bits(a.keys, kdt, krow + __builtin_amdgcn_readfirstlane(v.y));
+        }
+    };
+    if (nl > 0) {
+        int blk;
+        elems(0, xa0, xb0, blk);
+        const uint32_t off0 = cell_off(0, blk, xa0, xb0, in0);
+        lo0 = rec_lo(off0);
+        elems(min(1, nl - 1), xa1, xb1, blk);
+        off1 = cell_off(min(1, nl - 1), blk, xa1, xb1, in1);
+        lo1 = rec_lo(off1);
+        issue_bits(min(2, nl - 1));
+        if (needs_hi(lo0, in0)) hi0 = rec_hi(off0);
+    }
+    for (int li = 0; li < nl; ++li) {
+        // ---- block li + 1: the record's second half where the list needs it
+        uint4 hi1 = zero4;
+        if (needs_hi(lo1, in1)) hi1 = rec_hi(off1);
+        // ---- block li + 2: key elements, cell, the record's first half
+        const int l2 = min(li + 2, nl - 1);
+        float xa2, xb2;
+        int blk2;
+        if constexpr (ROWREG) {
+            elems(l2, xa2, xb2, blk2);
+        } else {
+            int e0, e1;
+            block_info(l2, e0, e1, blk2);
+            xa2 = ssq_bits_to_f32(ua, kdt);
+            xb2 = ssq_bits_to_f32(ub, kdt);
+            issue_bits(min(li + 3, nl - 1));
+        }
+        bool in2;
+        const uint32_t off2 = cell_off(l2, blk2, xa2, xb2, in2);
+        const uint4 lo2 = rec_lo(off2);
+
+        // ---- candidates of block li
+        const float m0 = -2.0f * xa0, m1 = -2.0f * xb0;
+        const float xn = xa0 * xa0 + xb0 * xb0;
+        const float2* cbl = cb + li * 256;
+        const float* cnl = cn + li * 256;
+        const uint32_t w[8] = {lo0.x, lo0.y, lo0.z, lo0.w, hi0.x, hi0.y, hi0.z, hi0.w};
+        const int cnt = (int)(w[0] & 255u);
+        const bool full = !in0 || cnt == 255;
+        const int lcnt = full ? 0 : cnt;
+        Cand st{INFINITY, -1};
+        // Record word g holds bytes 4g .. 4g+3, candidates 4g-1 .. 4g+2 (byte 0 is the count).
+        // The codewords of word g + 1 are read while word g is evaluated, so each word costs one
+        // LDS latency, not four.  Bytes past a lane's count index real codewords (zero padding,
+        // or the first 31 of a "scan all" cell) and are read but not used.
+        float2 cc[4];
+        float cq[4];
+        auto fetch = [&](uint32_t wd, int i0, float2 (&c)[4], float (&q)[4]) {
+#pragma unroll
+            for (int i = i0; i < 4; ++i) {
+                const int j = (int)((wd >> (8 * i)) & 255u);
+                c[i] = cbl[j];
+                q[i] = cnl[j];
+            }
+        };
+        fetch(w[0], 1, cc, cq);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            if (!__builtin_amdgcn_ballot_w64((g == 0 ? 0 : 4 * g - 1) < lcnt)) break;  // the wave's lists are done
+            float2 nc2[4];
+            float nq[4];
+            if (g < 7) fetch(w[g + 1], 0, nc2, nq);
+#pragma unroll
+            for (int i = (g == 0 ? 1 : 0); i < 4; ++i)
+                eval_val(cc[i], cq[i], (int)((w[g] >> (8 * i)) & 255u), m0, m1, xn, 4 * g + i - 1 < lcnt, st);
+            if (g < 7) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) { cc[i] = nc2[i]; cq[i] = nq[i]; }
+            }
+        }
+        if (__builtin_amdgcn_ballot_w64(full)) {  // rare: every codeword
+            for (int j = 0; j < nc; ++j)
+                if (full) eval_cand(cbl, cnl, j, m0, m1, xn, st);
+        }
+        cs[lane * nb + __builtin_amdgcn_readfirstlane(poff[4 * li + 2])] = (uint8_t)(st.bj < 0 ? 0 : st.bj);
+
+        // ---- rotate the stages
+        xa0 = xa1; xb0 = xb1; lo0 = lo1; hi0 = hi1; in0 = in1;
+        xa1 = xa2; xb1 = xb2; lo1 = lo2; off1 = off2; in1 = in2;
+    }
+
+    // ---- outputs: code rows, heavy blocks' passthrough values
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    auto out_rows = [&](int ss, int64_t& crow, int64_t& prow) {
+        if (a.slot_mapping) {
+            const int64_t slot = a.slot_mapping[(int64_t)b * a.sm_sb + ss];
+            const int64_t page = slot / a.page_size, off = slot - page * a.page_size;
+            crow = page * a.c_sb + (int64_t)kv * a.c_sh + off * a.c_st;
+            prow = page * a.pt_sb + (int64_t)kv * a.pt_sh + off * a.pt_st;
+        } else {
+            crow = (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)ss * a.c_st;
+            prow = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)ss * a.pt_st;
+        }
+    };
+    const int s_wave = blockIdx.x * keys_wg + wave * 64;
+    if (p.row_codes) {
+        const int pieces = nb >> 4;
+        for (int e = lane; e < 64 * pieces; e += 64) {
+            const int m = e / pieces, q = e - m * pieces;
+            const int ss = s_wave + m;
+            if (ss < a.seq_len) {
+                int64_t crow, prow;
+                out_rows(ss, crow, prow);
+                const uint32_t* src = reinterpret_cast<const uint32_t*>(cs + m * nb + 16 * q);
+                *reinterpret_cast<uint4*>(a.codes + crow + 16 * q) = make_uint4(src[0], src[1], src[2], src[3]);
+            }
+        }
+    } else if (live) {
+        int64_t crow, prow;
+        out_rows(s, crow, prow);
+        for (int blk = 0; blk < nb; ++blk) a.codes[crow + blk] = cs[lane * nb + blk];
+    }
+    if ((hm0 | hm1) && live) {
+        int64_t crow, prow;
+        out_rows(s, crow, prow);
+        for (int blk = 0, hh = 0; blk < nb; ++blk) {
+            if (!ssq_is_heavy(hm0, hm1, blk)) continue;
+            const int slot = a.pt_dense ? blk : hh;
+            ++hh;
+            for (int d = 0; d < 2; ++d)
+                ssq_store_elem(a.pt, a.pt_dtype, prow + (int64_t)slot * 2 + d,
+                               ssq_load_elem(a.keys, a.k_dtype, krow + perm[blk * 2 + d]));
+        }
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+bool ssq_encode_grid_supported(const ssq_encode_args* a) {
+    return a->block_dim == 2 && !a->metric && a->n_centroids >= 1 && a->n_centroids <= 256 && a->n_blocks <= 128;
+}
+
+extern "C" uint64_t ssq_encode_grid_bytes(const ssq_encode_args* a) {
+    if (!a || a->struct_size != sizeof(ssq_encode_args) || !ssq_encode_grid_supported(a) || a->n_blocks < 1 ||
+        a->num_kv_heads < 1)
+        return 0;
+    return grid_total_bytes(*a);
+}
+
+extern "C" int ssq_encode_grid_build(const ssq_encode_args* a, void* grid, uint64_t grid_bytes, void* stream) {
+    if (!a) return ssq_fail(SSQ_ERR_INVALID, "args is NULL");
+    if (a->struct_size != sizeof(ssq_encode_args))
+        return ssq_fail(SSQ_ERR_ABI, "ssq_encode_args size %u != library's %zu", a->struct_size, sizeof(ssq_encode_args));
+    SSQ_REQUIRE(a->cent && grid, "cent and grid must be non-NULL");
+    SSQ_REQUIRE(a->n_blocks >= 1 && a->num_kv_heads >= 1, "bad n_blocks/num_kv_heads");
+    SSQ_UNSUPPORTED(ssq_encode_grid_supported(a), "the encode grid serves block_dim 2 without a block metric");
+    SSQ_REQUIRE(grid_bytes >= grid_total_bytes(*a), "grid buffer too small (%llu < %zu bytes)",
+                (unsigned long long)grid_bytes, grid_total_bytes(*a));
+    hipStream_t st = (hipStream_t)stream;
+    const int nh = grid_heads(*a), nb = a->n_blocks, nc = a->n_centroids;
+    float* hdr = reinterpret_cast<float*>(grid);
+    uint8_t* cells = reinterpret_cast<uint8_t*>(grid) + grid_hdr_bytes(*a);
+    hipLaunchKernelGGL(k_grid_header, dim3(nb, nh), dim3(kThreads), 0, st, a->cent, a->cent_sh, nb, nc, hdr);
+    int rc = ssq_check_hip(hipGetLastError(), "k_grid_header launch");
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_grid_cells, dim3(kG * kG / kThreads, nb, nh), dim3(kThreads), 0, st, a->cent, a->cent_sh, nb,
+                       nc, (const float*)hdr, cells);
+    return ssq_check_hip(hipGetLastError(), "k_grid_cells launch");
+}
+
+// called by ssq_encode (arguments already validated); SSQ_ERR_UNSUPPORTED when the grid path
+// cannot serve the call
+int ssq_encode_grid_run(const ssq_encode_args* a, hipStream_t st) {
+    SSQ_UNSUPPORTED(ssq_encode_grid_supported(a), "the grid encode serves block_dim 2 without a block metric");
+    SSQ_REQUIRE(a->grid, "the grid encode needs a grid from ssq_encode_grid_build");
+    SSQ_REQUIRE(a->grid_bytes >= grid_total_bytes(*a), "grid too small for this codebook (%llu < %zu bytes)",
+                (unsigned long long)a->grid_bytes, grid_total_bytes(*a));
+    GridParams gp;
+    memset(&gp, 0, sizeof(gp));
+    gp.a = *a;
+    gp.hdr = reinterpret_cast<const float*>(a->grid);
+    gp.cells = reinterpret_cast<const uint8_t*>(a->grid) + grid_hdr_bytes(*a);
+    for (int blk = 0; blk < a->n_blocks; ++blk) {
+        const bool heavy = blk < 64 ? ((a->heavy_mask[0] >> blk) & 1) : ((a->heavy_mask[1] >> (blk - 64)) & 1);
+        if (!heavy) gp.light[gp.n_light++] = (uint8_t)blk;
+    }
+    int waves = 16;
+    while (waves > 4 && grid_smem(gp.n_light, a->n_blocks, waves) > 160 * 1024) waves >>= 1;
+    const size_t smem = grid_smem(gp.n_light, a->n_blocks, waves);
+    SSQ_UNSUPPORTED(smem <= 160 * 1024, "too many blocks for the grid encode's LDS");
+    gp.row_codes = a->n_blocks % 16 == 0 && (uintptr_t)a->codes % 16 == 0 && a->c_sb % 16 == 0 &&
+                   a->c_sh % 16 == 0 && a->c_st % 16 == 0;
+    // key rows of at most 128 bytes at 16-byte aligned addresses are read whole, into registers
+    const int esz = a->k_dtype == SSQ_F32 ? 4 : 2;
+    const int64_t row_bytes = (int64_t)a->head_dim * esz;
+    const bool rowreg = row_bytes % 16 == 0 && row_bytes <= 128 && (uintptr_t)a->keys % 16 == 0 &&
+                        (a->k_sb * esz) % 16 == 0 && (a->k_sh * esz) % 16 == 0 && (a->k_ss * esz) % 16 == 0;
+    gp.row_q = rowreg ? (int)(row_bytes / 16) : 0;
+    const void* fn = rowreg ? reinterpret_cast<const void*>(k_encode_grid<true>)
+                            : reinterpret_cast<const void*>(k_encode_grid<false>);
+    int dev = 0;
+    int rc = ssq_check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    static bool attr[2][64] = {};  // per kernel and device: dynamic LDS above the default
+    if (dev < 64 && !attr[rowreg][dev]) {
+        rc = ssq_check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
+                           "hipFuncSetAttribute(k_encode_grid)");
+        if (rc) return rc;
+        attr[rowreg][dev] = true;
+    } else if (dev >= 64) {
+        rc = ssq_check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
+                           "hipFuncSetAttribute(k_encode_grid)");
+        if (rc) return rc;
+    }
+    const int keys_wg = waves * 64;
+    dim3 grid((a->seq_len + keys_wg - 1) / keys_wg, a->batch * a->num_kv_heads);
+    if (rowreg)
+        hipLaunchKernelGGL(k_encode_grid<true>, grid, dim3(waves * 64), smem, st, gp);
+    else
+        hipLaunchKernelGGL(k_encode_grid<false>, grid, dim3(waves * 64), smem, st, gp);
+    return ssq_check_hip(hipGetLastError(), "k_encode_grid launch");
+}

@@ -326,7 +326,8 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
 def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
            heavy: Optional[Sequence[bool]] = None, pt_dtype: Optional[torch.dtype] = None, pt_dense: bool = False,
            codes_out: Optional[torch.Tensor] = None, pt_out: Optional[torch.Tensor] = None,
-           slot_mapping: Optional[torch.Tensor] = None, metric: Optional[torch.Tensor] = None, kernel: int = 0):
+           slot_mapping: Optional[torch.Tensor] = None, metric: Optional[torch.Tensor] = None, kernel: int = 0,
+           grid: Optional[torch.Tensor] = None):
     """Nearest-codeword encode of keys [B, Hkv, S, D] -> (codes uint8 [B, Hkv, S, nb], pt or None).
 
     Passthrough values (heavy blocks) are [B, Hkv, S, n_heavy, bd] (compact) or
@@ -336,6 +337,9 @@ def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
     pt_out (compact) may be given as [B, Hkv, S, ...] views to write into instead of allocating.
     metric: SunShape-Pro block metric E [D, D] or per KV head [Hkv, D, D] (fp32); distances are
     taken between E_b x and E_b c (sunshape/codec.py:375-376).  None = identity.
+    grid: search grid from encode_grid(cent) (block_dim 2, no metric); with it the encode
+    evaluates only each key's certified candidates (same codes).  kernel: 0 auto, 1 exact scan,
+    2 MFMA screen, 3 grid search.
     Reference: sunshape/codec.py:362-385, sunshape/vllm_attn_backend.py:101-123.
     """
     _on_gpu("key_states", keys)
@@ -406,9 +410,37 @@ def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
         slot_mapping=N.ptr(slot_mapping), sm_sb=slot_mapping.stride(0) if slot_mapping is not None else 0,
         page_size=page, kernel=int(kernel),
     )
+    if grid is not None:
+        _on_gpu("grid", grid)
+        _require(grid.dtype == torch.uint8 and grid.is_contiguous(), "grid must be the uint8 tensor from encode_grid")
+        a.grid, a.grid_bytes = N.ptr(grid), grid.numel()
     a.heavy_mask[0], a.heavy_mask[1] = w0, w1
     N.check(N.lib().ssq_encode(ctypes.byref(a), N.stream_of(keys.device)))
     return codes, pt
+
+
+def encode_grid(cent: torch.Tensor, num_kv_heads: int = 1) -> torch.Tensor:
+    """Search grid for encode(..., grid=) from codebooks [nb, nc, 2] or [Hkv, nb, nc, 2] (fp32).
+
+    Built once per codebook (a uint8 buffer of about 0.5 MiB per block and head); rebuild it
+    whenever the codebook changes.  No counterpart in the reference: a search structure of this
+    library, whose encode results equal the exhaustive ones bit for bit.
+    """
+    _on_gpu("centroids", cent)
+    cent = cent.to(torch.float32).contiguous()
+    _require(cent.ndim in (3, 4) and cent.shape[-1] == 2, "the encode grid serves block_dim 2 codebooks")
+    if cent.ndim == 4:
+        num_kv_heads = cent.shape[0]
+    nb, nc = cent.shape[-3], cent.shape[-2]
+    a = N.EncodeArgs(num_kv_heads=int(num_kv_heads), cent=N.ptr(cent),
+                     cent_sh=nb * nc * 2 if cent.ndim == 4 else 0,
+                     block_dim=2, n_blocks=nb, n_centroids=nc, head_dim=2 * nb)
+    lib = N.lib()
+    size = lib.ssq_encode_grid_bytes(ctypes.byref(a))
+    _require(size > 0, "the encode grid serves block_dim 2 codebooks with at most 128 blocks of 256 codewords")
+    grid = torch.empty(size, device=cent.device, dtype=torch.uint8)
+    N.check(lib.ssq_encode_grid_build(ctypes.byref(a), N.ptr(grid), size, N.stream_of(cent.device)))
+    return grid
 
 
 def dequantize(codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,

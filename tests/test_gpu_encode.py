@@ -24,14 +24,16 @@ def _gpu_encode(keys_np, perm, cent, heavy=None, kernel=0, dtype=torch.float32, 
     return np_of(codes[0, 0]), None if pt is None else np_of(pt[0, 0])
 
 
-@pytest.mark.parametrize("kernel", [1, 2])
+@pytest.mark.parametrize("kernel", [1, 2, 3])
 def test_encode_golden_fixture_bit_exact(kernel):
     log(f"encode golden kernel={kernel}")
     f = np.load(os.path.join(GOLD, "encode_mixed.npz"))
     keys = torch_bf16_from_bits(f["keys_bf16_bits"], DEV)
-    codes, pt = hip_ops.encode(keys[None, None], torch.from_numpy(f["perm"]).to(DEV),
-                               torch.from_numpy(f["centroids"]).to(DEV), heavy=f["heavy"].tolist(),
-                               pt_dtype=torch.float32, pt_dense=True, kernel=kernel)
+    cent = torch.from_numpy(f["centroids"]).to(DEV)
+    grid = hip_ops.encode_grid(cent) if kernel == 3 else None
+    codes, pt = hip_ops.encode(keys[None, None], torch.from_numpy(f["perm"]).to(DEV), cent,
+                               heavy=f["heavy"].tolist(), pt_dtype=torch.float32, pt_dense=True, kernel=kernel,
+                               grid=grid)
     assert np.array_equal(np_of(codes[0, 0]), f["codes"])
     assert np.array_equal(np_of(pt[0, 0]), f["passthrough"])
 
@@ -119,6 +121,9 @@ def test_config5_full_encode():
     c_mfma, pt = hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy, kernel=2)
     c_scan, pt2 = hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy, kernel=1)
     assert torch.equal(c_mfma, c_scan) and torch.equal(pt, pt2)
+    grid = hip_ops.encode_grid(p["centroids"])
+    c_grid, pt3 = hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy, kernel=3, grid=grid)
+    assert torch.equal(c_grid, c_scan) and torch.equal(pt3, pt2)
     hv = p["heavy"].numpy()
     keys = np_of(p["keys"])
     perm, cent = np_of(p["perm"]), np_of(p["centroids"])
@@ -205,3 +210,135 @@ def test_pro_codec_quantize_matches_oracle():
     # decode-side arithmetic ignores E: k_hat = C[b, idx] in the original basis
     k_hat = np_of(codec.dequantize(qz))
     assert np.array_equal(k_hat, O.dequantize(ref, cent, perm))
+
+
+# ---------------------------------------------------------------------------
+# grid-search encode (kernel 3, block_dim 2): certified candidate lists from encode_grid
+# ---------------------------------------------------------------------------
+
+def _grid_case(D, nc, n, seed, spread=1.0):
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(D)
+    sig = np.exp(rng.uniform(np.log(0.1), np.log(3), D)).astype(np.float32)
+    cent = (rng.standard_normal((D // 2, nc, 2)) * sig[perm].reshape(D // 2, 1, 2)).astype(np.float32)
+    keys = O.bf16_round((rng.standard_normal((n, D)) * sig * spread).astype(np.float32))
+    return keys, perm, cent
+
+
+@pytest.mark.parametrize("D,nc,n,spread", [(64, 256, 3000, 1.0), (40, 64, 777, 1.0), (64, 256, 1500, 25.0),
+                                           (32, 256, 65, 0.2)])
+def test_grid_encode_vs_oracle_bit_exact(D, nc, n, spread):
+    """Grid encode == oracle == MFMA encode, bit for bit.  spread 25 puts most keys outside the
+    grid (every codeword scanned); spread 0.2 crowds them into the central cells; D 40 gives
+    code rows that are not whole 16-byte pieces; 64 codewords exercise nc < 256."""
+    log(f"grid encode D={D} nc={nc} n={n} spread={spread}")
+    keys, perm, cent = _grid_case(D, nc, n, D * 7 + nc + int(spread * 10), spread)
+    ref, _ = O.encode(keys, perm, cent)
+    c = torch.from_numpy(cent).to(DEV)
+    grid = hip_ops.encode_grid(c)
+    k = torch.from_numpy(keys).to(DEV).to(torch.bfloat16)[None, None]
+    codes, _ = hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, kernel=3, grid=grid)
+    got = np_of(codes[0, 0])
+    assert np.array_equal(got, ref), int((got != ref).sum())
+    if nc == 256:
+        m, _ = hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, kernel=2)
+        assert torch.equal(m, codes)
+    # auto dispatch takes the grid when one is given
+    a, _ = hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, grid=grid)
+    assert torch.equal(a, codes)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("odd_stride", [False, True])
+def test_grid_encode_key_paths(dtype, D, odd_stride):
+    """Both ways the grid search reads keys: rows of at most 128 bytes on 16-byte boundaries are
+    read whole into registers (fp16/bf16 up to D 64, fp32 up to D 32); wider rows and rows at
+    odd strides read each element on its own.  Each must equal the oracle bit for bit."""
+    log(f"grid encode key path dtype={dtype} D={D} odd_stride={odd_stride}")
+    keys, perm, cent = _grid_case(D, 256, 700, 300 + D + int(odd_stride), 1.0)
+    kt = torch.from_numpy(keys).to(dtype)
+    ref, _ = O.encode(kt.float().numpy(), perm, cent)
+    if odd_stride:  # rows 3 elements apart beyond D: not 16-byte aligned
+        buf = torch.zeros(keys.shape[0], D + 3, dtype=dtype)
+        buf[:, :D] = kt
+        k = buf.to(DEV)[:, :D][None, None]
+        assert k.stride(2) == D + 3
+    else:
+        k = kt.to(DEV)[None, None]
+    c = torch.from_numpy(cent).to(DEV)
+    codes, _ = hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, kernel=3, grid=hip_ops.encode_grid(c))
+    got = np_of(codes[0, 0])
+    assert np.array_equal(got, ref), int((got != ref).sum())
+
+
+def test_grid_encode_constructed_ties_duplicates_and_heavy():
+    """Duplicated codewords (lower index wins), one-ulp neighbours, keys on codewords, keys on cell
+    boundaries, and passthrough blocks in both layouts."""
+    log("grid encode constructed")
+    rng = np.random.default_rng(11)
+    D = 32
+    perm = rng.permutation(D)
+    cent = rng.standard_normal((16, 256, 2)).astype(np.float32)
+    cent[:, 200] = cent[:, 17]
+    cent[:, 201] = np.nextafter(cent[:, 40], np.float32(np.inf))
+    cent[:, 9] = cent[:, 8] * np.float32(1 + 2 ** -22)
+    pick = rng.choice([17, 40, 201, 8, 9, 3], size=(600, 16))
+    xp = np.stack([np.concatenate([cent[b, pick[i, b]] for b in range(16)]) for i in range(600)])
+    xp[200:400] += rng.standard_normal(xp[200:400].shape).astype(np.float32) * 1e-3
+    # keys on grid-cell boundaries of each block (origin + i / inv_pitch, as the grid computes them)
+    c = torch.from_numpy(cent).to(DEV)
+    grid = hip_ops.encode_grid(c)
+    hdr = np_of(grid[: 16 * 8 * 4].view(torch.float32)).reshape(16, 8)
+    for r in range(400, 600):
+        for b in range(16):
+            i0, i1 = rng.integers(0, 128, 2)
+            xp[r, 2 * b] = np.float32(hdr[b, 0] + np.float32(i0) / hdr[b, 2])
+            xp[r, 2 * b + 1] = np.float32(hdr[b, 1] + np.float32(i1) / hdr[b, 3])
+    keys = O.inverse_transform(xp, perm).astype(np.float32)
+    heavy = np.zeros(16, dtype=bool)
+    heavy[[2, 11]] = True
+    ref, rpt = O.encode(keys, perm, cent, heavy)
+    k = torch.from_numpy(keys).to(DEV)[None, None]
+    for dense in (True, False):
+        codes, pt = hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, heavy=heavy.tolist(), pt_dtype=torch.float32,
+                                   pt_dense=dense, kernel=3, grid=grid)
+        assert np.array_equal(np_of(codes[0, 0]), ref)
+        want = rpt if dense else rpt[:, heavy]
+        assert np.array_equal(np_of(pt[0, 0]), want)
+
+
+def test_grid_encode_paged_matches_contiguous():
+    log("grid encode paged")
+    p = synthetic.config5(DEV, B=2, S=96)
+    heavy = p["heavy"].tolist()
+    grid = hip_ops.encode_grid(p["centroids"])
+    codes, pt = hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy, kernel=2)
+    page, Hkv, nb = 16, 2, 32
+    P = 2 * 96 // page + 3
+    g = torch.Generator().manual_seed(4)
+    table = torch.randperm(P, generator=g)[: 2 * 96 // page].view(2, -1)
+    slots = (table[:, :, None] * page + torch.arange(page)).reshape(2, 96).to(torch.int64).to(DEV)
+    cpages = torch.zeros(P, Hkv, page, nb, dtype=torch.uint8, device=DEV)
+    ppages = torch.zeros(P, Hkv, page, 4, 2, dtype=torch.bfloat16, device=DEV)
+    hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy, codes_out=cpages, pt_out=ppages,
+                   slot_mapping=slots, kernel=3, grid=grid)
+    t = table.to(DEV)
+    for b in range(2):
+        got_c = cpages[t[b]].permute(1, 0, 2, 3).reshape(Hkv, 96, nb)
+        got_p = ppages[t[b]].permute(1, 0, 2, 3, 4).reshape(Hkv, 96, 4, 2)
+        assert torch.equal(got_c, codes[b]) and torch.equal(got_p, pt[b])
+
+
+def test_grid_encode_rejections():
+    log("grid encode rejections")
+    cent = torch.randn(8, 256, 4, device=DEV)
+    with pytest.raises(RuntimeError, match="block_dim 2"):
+        hip_ops.encode_grid(cent)
+    keys, perm, cent2 = _grid_case(16, 256, 20, 5)
+    k = torch.from_numpy(keys).to(DEV)[None, None]
+    with pytest.raises(RuntimeError, match="grid"):
+        hip_ops.encode(k, torch.from_numpy(perm).to(DEV), torch.from_numpy(cent2).to(DEV), kernel=3)
+    small = torch.zeros(16, dtype=torch.uint8, device=DEV)
+    with pytest.raises(RuntimeError, match="too small"):
+        hip_ops.encode(k, torch.from_numpy(perm).to(DEV), torch.from_numpy(cent2).to(DEV), kernel=3, grid=small)
