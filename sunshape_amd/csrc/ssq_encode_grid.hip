@@ -35,7 +35,7 @@
 namespace {
 
 constexpr int kG = 128;        // cells per dimension
-constexpr int kRec = 32;       // bytes per cell record: count (255 = scan all), then indices
+constexpr int kRec = 32;       // bytes per cell record: count (255 = scan all), then indices, padded
 constexpr int kMaxCand = kRec - 1;
 constexpr int kHdr = 8;        // floats per block header: lo0, lo1, inv_h0, inv_h1, Rc, valid
 constexpr int kThreads = 256;
@@ -139,7 +139,14 @@ __global__ __launch_bounds__(kThreads) void k_grid_cells(const float* cent, int6
                 ++cnt;
             }
         }
-        rec[0] = cnt <= kMaxCand ? (uint8_t)cnt : 255;
+        // count 0 (non-finite values) or more than 31: scan all.  Bytes past the list repeat
+        // its last index, so evaluating them again cannot change the search's result.
+        if (cnt == 0 || cnt > kMaxCand) {
+            rec[0] = 255;
+        } else {
+            rec[0] = (uint8_t)cnt;
+            for (int i = 1 + cnt; i < kRec; ++i) rec[i] = rec[cnt];
+        }
     }
     uint4* dst = reinterpret_cast<uint4*>(cells + (((int64_t)h * nb + blk) * kG * kG + cell) * kRec);
     const uint32_t* w = reinterpret_cast<const uint32_t*>(rec);
@@ -202,6 +209,35 @@ __device__ __forceinline__ void eval_val(float2 c, float cq, int j, float m0, fl
 __device__ __forceinline__ void eval_cand(const float2* cb, const float* cn, int j, float m0, float m1, float xn,
                                           Cand& st) {
     eval_val(cb[j], cn[j], j, m0, m1, xn, true, st);
+}
+
+// the reference's value for codeword (c, |c|^2), clamped at 0
+__device__ __forceinline__ float chain_val(float2 c, float cq, float m0, float m1, float xn) {
+    float d2 = m0 * c.x;
+    d2 = __builtin_fmaf(m1, c.y, d2);
+    d2 = __builtin_fmaf(xn, 1.0f, d2);
+    d2 = __builtin_fmaf(1.0f, cq, d2);
+    return d2 > 0.f ? d2 : 0.f;
+}
+
+// A later candidate of a cell list: taken iff its correctly rounded sqrt is strictly smaller.
+// Both values are non-negative floats, so their bit patterns order like the values.  A gap
+// of more than 32 units in the last place of the smaller one makes the ratio exceed
+// 1 + 33 2^-24, the square roots' ratio 1 + 16 2^-24, and so the correctly rounded roots
+// differ; a smaller value within 32 units compares the roots; an equal or larger one loses.
+// Re-evaluating a codeword already seen (the record's padding) always loses.
+__device__ __forceinline__ void next_val(float2 c, float cq, int j, float m0, float m1, float xn, Cand& st) {
+    const float dc = chain_val(c, cq, m0, m1, xn);
+    const int diff = (int)__float_as_uint(st.bd) - (int)__float_as_uint(dc);
+    bool take = diff > 32;
+    const bool near = (uint32_t)(diff - 1) < 32u;
+    if (__builtin_amdgcn_ballot_w64(near)) {
+        __asm__ volatile("" ::: "memory");  // keeps the branch: not speculated
+        const bool lt = __builtin_sqrtf(dc) < __builtin_sqrtf(st.bd);
+        take = near ? lt : take;
+    }
+    st.bd = take ? dc : st.bd;
+    st.bj = take ? j : st.bj;
 }
 
 template <bool ROWREG>
@@ -337,12 +373,22 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
         off1 = cell_off(min(1, nl - 1), blk, xa1, xb1, in1);
         lo1 = rec_lo(off1);
         issue_bits(min(2, nl - 1));
-        if (needs_hi(lo0, in0)) hi0 = rec_hi(off0);
+        if (needs_hi(lo0, in0)) {
+            hi0 = rec_hi(off0);
+        } else {
+            const uint32_t pad = (lo0.w >> 24) * 0x01010101u;
+            hi0 = make_uint4(pad, pad, pad, pad);
+        }
     }
     for (int li = 0; li < nl; ++li) {
         // ---- block li + 1: the record's second half where the list needs it
-        uint4 hi1 = zero4;
-        if (needs_hi(lo1, in1)) hi1 = rec_hi(off1);
+        uint4 hi1;
+        if (needs_hi(lo1, in1)) {
+            hi1 = rec_hi(off1);
+        } else {  // the list ends in the first half: its padding continues
+            const uint32_t pad = (lo1.w >> 24) * 0x01010101u;
+            hi1 = make_uint4(pad, pad, pad, pad);
+        }
         // ---- block li + 2: key elements, cell, the record's first half
         const int l2 = min(li + 2, nl - 1);
         float xa2, xb2;
@@ -372,8 +418,9 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
         Cand st{INFINITY, -1};
         // Record word g holds bytes 4g .. 4g+3, candidates 4g-1 .. 4g+2 (byte 0 is the count).
         // The codewords of word g + 1 are read while word g is evaluated, so each word costs one
-        // LDS latency, not four.  Bytes past a lane's count index real codewords (zero padding,
-        // or the first 31 of a "scan all" cell) and are read but not used.
+        // LDS latency, not four.  The first candidate starts the running minimum; bytes past a
+        // lane's count repeat its last candidate and cannot win.  Lanes that scan all codewords
+        // start over below.
         float2 cc[4];
         float cq[4];
         auto fetch = [&](uint32_t wd, int i0, float2 (&c)[4], float (&q)[4]) {
@@ -392,14 +439,22 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
             float nq[4];
             if (g < 7) fetch(w[g + 1], 0, nc2, nq);
 #pragma unroll
-            for (int i = (g == 0 ? 1 : 0); i < 4; ++i)
-                eval_val(cc[i], cq[i], (int)((w[g] >> (8 * i)) & 255u), m0, m1, xn, 4 * g + i - 1 < lcnt, st);
+            for (int i = (g == 0 ? 1 : 0); i < 4; ++i) {
+                const int j = (int)((w[g] >> (8 * i)) & 255u);
+                if (g == 0 && i == 1) {
+                    st.bd = chain_val(cc[i], cq[i], m0, m1, xn);
+                    st.bj = j;
+                } else {
+                    next_val(cc[i], cq[i], j, m0, m1, xn, st);
+                }
+            }
             if (g < 7) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) { cc[i] = nc2[i]; cq[i] = nq[i]; }
             }
         }
         if (__builtin_amdgcn_ballot_w64(full)) {  // rare: every codeword
+            if (full) st = Cand{INFINITY, -1};
             for (int j = 0; j < nc; ++j)
                 if (full) eval_cand(cbl, cnl, j, m0, m1, xn, st);
         }
