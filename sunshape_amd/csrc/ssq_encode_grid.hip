@@ -6,13 +6,14 @@
 // product and the norms left-to-right sums of rounded squares (torch.cdist's mm formulation).
 //
 //  * k_grid_header / k_grid_cells (built once per codebook, ssq_encode_grid_build): per block, a
-//    kG x kG grid of cells over twice the codewords' bounding box.  Cell C lists, ascending, every
-//    codeword j with dmin(C, c_j)^2 <= min_k dmax(C, c_k)^2 + M_C, where M_C bounds the rounding
-//    terms below; more than 31 such codewords mark the cell "scan all".
+//    kG x kG grid of cells under a per-dimension map that is finest where the codewords crowd and
+//    whose end cells reach to infinity (cell_edge).  Cell C lists, ascending, every codeword j
+//    with dmin(C, c_j)^2 <= min_k dmax(C, c_k)^2 + M_C, where M_C bounds the rounding terms
+//    below; more than 31 such codewords (or an unbounded cell) mark the cell "scan all".
 //  * k_encode_grid: lane = key.  Per light block: the key's two permuted elements, its cell, the
-//    cell's record (32 bytes from the grid), then the reference chain on each listed candidate in
-//    ascending order, keeping the first minimum of the correctly rounded sqrt.  Keys outside the
-//    grid and "scan all" cells evaluate every codeword.
+//    cell's record (16 or 32 bytes from the grid), then the reference chain on each listed
+//    candidate in ascending order, keeping the first minimum of the correctly rounded sqrt.
+//    Non-finite keys and "scan all" cells evaluate every codeword.
 //
 // Why the list holds the winner.  Let r_j be the reference's value for codeword j, D_j the exact
 // value of the same expression on the same (rounded) norms, d_j = |x - c_j|.  Then |r_j - D_j| <=
@@ -25,7 +26,7 @@
 // minimises dmax(C, c_k), d_k^2 <= dmax(C, c_k)^2 =: dmm, giving dmin(C, c_j*)^2 <= dmm + M_C with
 //   M_C = 1.01 (4.002u (R^2 + Rc^2) + 2.0002 g (R + Rc)^2 + (dmm + 2.001u (R^2 + Rc^2) + g (R + Rc)^2) 2^-21).
 // Cells are widened by 0.001 of a cell on each side, far more than the fp32 rounding of the
-// search kernel's cell index, so a key always lies in the cell it is looked up in.  The build
+// search kernel's cell map, so a key always lies in the cell it is looked up in.  The build
 // runs in fp64.
 #include "ssq_common.h"
 
@@ -37,7 +38,7 @@ namespace {
 constexpr int kG = 128;        // cells per dimension
 constexpr int kRec = 32;       // bytes per cell record: count (255 = scan all), then indices, padded
 constexpr int kMaxCand = kRec - 1;
-constexpr int kHdr = 8;        // floats per block header: lo0, lo1, inv_h0, inv_h1, Rc, valid
+constexpr int kHdr = 8;        // floats per block header: mid0, mid1, inv0, inv1, Rc, valid
 constexpr int kThreads = 256;
 
 inline int grid_heads(const ssq_encode_args& a) { return a.cent_sh == 0 ? 1 : a.num_kv_heads; }
@@ -51,50 +52,55 @@ inline size_t grid_total_bytes(const ssq_encode_args& a) {
 // ---------------------------------------------------------------------------
 // build
 // ---------------------------------------------------------------------------
-// one workgroup per (block, codebook head): bounding box, max |c|, grid origin and pitch
-__global__ __launch_bounds__(kThreads) void k_grid_header(const float* cent, int64_t cent_sh, int nb, int nc,
-                                                          float* hdr) {
-    __shared__ float red[5][kThreads];
-    const int blk = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+// one lane per (block, codebook head), in fp64: the cell map's centre (the codewords' bounding-box
+// centre) and scale (their RMS spread about the mean) per dimension, and max |c|
+__global__ __launch_bounds__(64) void k_grid_header(const float* cent, int64_t cent_sh, int nb, int nc, float* hdr) {
+    if (threadIdx.x != 0) return;
+    const int blk = blockIdx.x, h = blockIdx.y;
     const float* c = cent + (int64_t)h * cent_sh + (int64_t)blk * nc * 2;
-    float mn0 = INFINITY, mx0 = -INFINITY, mn1 = INFINITY, mx1 = -INFINITY, nrm = 0.f;
-    for (int j = tid; j < nc; j += kThreads) {
-        const float v0 = c[2 * j], v1 = c[2 * j + 1];
-        mn0 = fminf(mn0, v0); mx0 = fmaxf(mx0, v0);
-        mn1 = fminf(mn1, v1); mx1 = fmaxf(mx1, v1);
-        nrm = fmaxf(nrm, (float)((double)v0 * v0 + (double)v1 * v1));
-        if (!isfinite(v0) || !isfinite(v1)) nrm = INFINITY;
-    }
-    red[0][tid] = mn0; red[1][tid] = mx0; red[2][tid] = mn1; red[3][tid] = mx1; red[4][tid] = nrm;
-    __syncthreads();
-    for (int o = kThreads / 2; o > 0; o >>= 1) {
-        if (tid < o) {
-            red[0][tid] = fminf(red[0][tid], red[0][tid + o]);
-            red[1][tid] = fmaxf(red[1][tid], red[1][tid + o]);
-            red[2][tid] = fminf(red[2][tid], red[2][tid + o]);
-            red[3][tid] = fmaxf(red[3][tid], red[3][tid + o]);
-            red[4][tid] = fmaxf(red[4][tid], red[4][tid + o]);
+    double lo[2] = {INFINITY, INFINITY}, hi[2] = {-INFINITY, -INFINITY}, sum[2] = {0.0, 0.0};
+    double nrm = 0.0;
+    bool finite = true;
+    for (int j = 0; j < nc; ++j) {
+        for (int d = 0; d < 2; ++d) {
+            const double v = c[2 * j + d];
+            lo[d] = fmin(lo[d], v); hi[d] = fmax(hi[d], v); sum[d] += v;
+            finite = finite && isfinite(v);
         }
-        __syncthreads();
+        nrm = fmax(nrm, (double)(float)((double)c[2 * j] * c[2 * j] + (double)c[2 * j + 1] * c[2 * j + 1]));
     }
-    if (tid != 0) return;
-    float* out = hdr + ((int64_t)h * nb + blk) * kHdr;
-    const double lo[2] = {red[0][0], red[2][0]}, hi[2] = {red[1][0], red[3][0]};
-    bool valid = isfinite(red[4][0]);
-    float org[2], inv[2];
+    float mid[2], inv[2];
+    bool valid = finite;
     for (int d = 0; d < 2; ++d) {
-        const double mid = 0.5 * (lo[d] + hi[d]);
-        double half = (hi[d] - lo[d]);  // twice the box's half-width
-        if (!(half > fabs(mid) * 0x1.0p-20)) half = fmax(fabs(mid) * 0x1.0p-20, 0x1.0p-60);
-        org[d] = (float)(mid - half);
-        const double pitch = 2.0 * half / kG;
-        inv[d] = (float)(1.0 / pitch);
-        valid = valid && isfinite(org[d]) && isfinite(inv[d]) && inv[d] > 0.f;
+        const double mean = sum[d] / nc;
+        double var = 0.0;
+        for (int j = 0; j < nc; ++j) {
+            const double e = (double)c[2 * j + d] - mean;
+            var += e * e;
+        }
+        const double m = 0.5 * (lo[d] + hi[d]);
+        double sc = sqrt(var / nc);
+        if (!(sc > fabs(m) * 0x1.0p-20)) sc = fmax(fabs(m) * 0x1.0p-20, 0x1.0p-60);
+        mid[d] = (float)m;
+        inv[d] = (float)(1.0 / sc);
+        valid = valid && isfinite(mid[d]) && isfinite(inv[d]) && inv[d] > 0.f;
     }
-    out[0] = org[0]; out[1] = org[1]; out[2] = inv[0]; out[3] = inv[1];
-    out[4] = (float)(sqrt((double)red[4][0]) * (1.0 + 0x1.0p-20));
+    float* out = hdr + ((int64_t)h * nb + blk) * kHdr;
+    out[0] = mid[0]; out[1] = mid[1]; out[2] = inv[0]; out[3] = inv[1];
+    out[4] = finite ? (float)(sqrt(nrm) * (1.0 + 0x1.0p-20)) : INFINITY;
     out[5] = valid ? 1.f : 0.f;
     out[6] = 0.f; out[7] = 0.f;
+}
+
+// The cell map, per dimension: u = (x - mid) inv, t = u / (1 + |u|) in (-1, 1), cell
+// floor((t + 1) kG / 2) clamped to [0, kG).  Cells are finest at the centre, where keys and
+// codewords crowd, and the two end cells reach to infinity, so every finite key has a cell.
+// The search computes t in fp32 with an approximate reciprocal, within 1e-6 of t; each cell is
+// widened by 0.001 of its width in t, far more.
+__device__ __forceinline__ double cell_edge(double t, double mid, double scale) {
+    if (t <= -1.0) return -INFINITY;
+    if (t >= 1.0) return INFINITY;
+    return mid + scale * (t / (1.0 - fabs(t)));
 }
 
 // one thread per cell
@@ -114,10 +120,11 @@ __global__ __launch_bounds__(kThreads) void k_grid_cells(const float* cent, int6
         rec[0] = 255;
     } else {
         const int i0 = cell / kG, i1 = cell - (cell / kG) * kG;
-        const double a0 = (double)hd[0] + ((double)i0 - 0.001) / (double)hd[2];
-        const double b0 = (double)hd[0] + ((double)i0 + 1.001) / (double)hd[2];
-        const double a1 = (double)hd[1] + ((double)i1 - 0.001) / (double)hd[3];
-        const double b1 = (double)hd[1] + ((double)i1 + 1.001) / (double)hd[3];
+        const double w = 2.0 / kG, sc0 = 1.0 / (double)hd[2], sc1 = 1.0 / (double)hd[3];
+        const double a0 = cell_edge(-1.0 + w * (i0 - 0.001), hd[0], sc0);
+        const double b0 = cell_edge(-1.0 + w * (i0 + 1.001), hd[0], sc0);
+        const double a1 = cell_edge(-1.0 + w * (i1 - 0.001), hd[1], sc1);
+        const double b1 = cell_edge(-1.0 + w * (i1 + 1.001), hd[1], sc1);
         const double R2 = fmax(a0 * a0, b0 * b0) + fmax(a1 * a1, b1 * b1);
         const double R = sqrt(R2), Rc = hd[4];
         double dmm = INFINITY;
@@ -322,10 +329,15 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
     // the byte offset of (x0, x1)'s cell record in block blk of this head's table; inside =
     // false means "scan all" (the offset is then cell (0, 0)'s, a valid record)
     auto cell_off = [&](int li, int blk, float x0, float x1, bool& inside) -> uint32_t {
-        const float4 h = hd[li];
-        const float f0 = floorf((x0 - h.x) * h.z), f1 = floorf((x1 - h.y) * h.w);
-        inside = h.z > 0.f && f0 >= 0.f && f0 < (float)kG && f1 >= 0.f && f1 < (float)kG;
-        const int c0 = inside ? (int)f0 : 0, c1 = inside ? (int)f1 : 0;
+        const float4 h = hd[li];  // mid0, mid1, inv0, inv1 (inv 0: no grid)
+        const float u0 = (x0 - h.x) * h.z, u1 = (x1 - h.y) * h.w;
+        const float t0 = u0 * __builtin_amdgcn_rcpf(1.0f + fabsf(u0));
+        const float t1 = u1 * __builtin_amdgcn_rcpf(1.0f + fabsf(u1));
+        const float f0 = floorf((t0 + 1.0f) * (0.5f * kG)), f1 = floorf((t1 + 1.0f) * (0.5f * kG));
+        // t within rounding of +-1 may land one past the ends: the end cells take it.  NaN
+        // (a non-finite key element) has no cell
+        inside = h.z > 0.f && f0 >= -1.f && f0 <= (float)kG && f1 >= -1.f && f1 <= (float)kG;
+        const int c0 = inside ? min(max((int)f0, 0), kG - 1) : 0, c1 = inside ? min(max((int)f1, 0), kG - 1) : 0;
         return (uint32_t)((blk * kG * kG + c0 * kG + c1) * kRec);
     };
     auto rec_lo = [&](uint32_t off) { return *reinterpret_cast<const uint4*>(cells + off); };
@@ -541,7 +553,7 @@ extern "C" int ssq_encode_grid_build(const ssq_encode_args* a, void* grid, uint6
     const int nh = grid_heads(*a), nb = a->n_blocks, nc = a->n_centroids;
     float* hdr = reinterpret_cast<float*>(grid);
     uint8_t* cells = reinterpret_cast<uint8_t*>(grid) + grid_hdr_bytes(*a);
-    hipLaunchKernelGGL(k_grid_header, dim3(nb, nh), dim3(kThreads), 0, st, a->cent, a->cent_sh, nb, nc, hdr);
+    hipLaunchKernelGGL(k_grid_header, dim3(nb, nh), dim3(64), 0, st, a->cent, a->cent_sh, nb, nc, hdr);
     int rc = ssq_check_hip(hipGetLastError(), "k_grid_header launch");
     if (rc) return rc;
     hipLaunchKernelGGL(k_grid_cells, dim3(kG * kG / kThreads, nb, nh), dim3(kThreads), 0, st, a->cent, a->cent_sh, nb,

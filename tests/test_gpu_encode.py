@@ -228,8 +228,8 @@ def _grid_case(D, nc, n, seed, spread=1.0):
 @pytest.mark.parametrize("D,nc,n,spread", [(64, 256, 3000, 1.0), (40, 64, 777, 1.0), (64, 256, 1500, 25.0),
                                            (32, 256, 65, 0.2)])
 def test_grid_encode_vs_oracle_bit_exact(D, nc, n, spread):
-    """Grid encode == oracle == MFMA encode, bit for bit.  spread 25 puts most keys outside the
-    grid (every codeword scanned); spread 0.2 crowds them into the central cells; D 40 gives
+    """Grid encode == oracle == MFMA encode, bit for bit.  spread 25 puts most keys in the far,
+    wide cells (long lists or every codeword scanned); spread 0.2 crowds them into the central cells; D 40 gives
     code rows that are not whole 16-byte pieces; 64 codewords exercise nc < 256."""
     log(f"grid encode D={D} nc={nc} n={n} spread={spread}")
     keys, perm, cent = _grid_case(D, nc, n, D * 7 + nc + int(spread * 10), spread)
@@ -286,15 +286,21 @@ def test_grid_encode_constructed_ties_duplicates_and_heavy():
     pick = rng.choice([17, 40, 201, 8, 9, 3], size=(600, 16))
     xp = np.stack([np.concatenate([cent[b, pick[i, b]] for b in range(16)]) for i in range(600)])
     xp[200:400] += rng.standard_normal(xp[200:400].shape).astype(np.float32) * 1e-3
-    # keys on grid-cell boundaries of each block (origin + i / inv_pitch, as the grid computes them)
+    # keys on grid-cell boundaries of each block: header (mid, inv) per dimension; cell edge i at
+    # t = -1 + 2i/128 of the map t = u / (1 + |u|), u = (x - mid) inv
     c = torch.from_numpy(cent).to(DEV)
     grid = hip_ops.encode_grid(c)
     hdr = np_of(grid[: 16 * 8 * 4].view(torch.float32)).reshape(16, 8)
+
+    def edge(i, mid, inv):
+        t = -1.0 + 2.0 * i / 128
+        return np.float32(mid + (t / (1.0 - abs(t))) / inv)
+
     for r in range(400, 600):
         for b in range(16):
-            i0, i1 = rng.integers(0, 128, 2)
-            xp[r, 2 * b] = np.float32(hdr[b, 0] + np.float32(i0) / hdr[b, 2])
-            xp[r, 2 * b + 1] = np.float32(hdr[b, 1] + np.float32(i1) / hdr[b, 3])
+            i0, i1 = rng.integers(1, 128, 2)
+            xp[r, 2 * b] = edge(i0, hdr[b, 0], hdr[b, 2])
+            xp[r, 2 * b + 1] = edge(i1, hdr[b, 1], hdr[b, 3])
     keys = O.inverse_transform(xp, perm).astype(np.float32)
     heavy = np.zeros(16, dtype=bool)
     heavy[[2, 11]] = True
