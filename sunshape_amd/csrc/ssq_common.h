@@ -109,6 +109,7 @@ int ssq_check_hip(hipError_t e, const char* what);
 int ssq_device_cus();
 // grid-search encode (ssq_encode_grid.hip)
 bool ssq_encode_grid_supported(const ssq_encode_args* a);
+bool ssq_encode_grid_fits(const ssq_encode_args* a);
 int ssq_encode_grid_run(const ssq_encode_args* a, hipStream_t st);
 
 #define SSQ_REQUIRE(cond, ...)                                  \

@@ -681,7 +681,8 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
     if (a->slot_mapping) SSQ_REQUIRE(a->page_size >= 1, "paged output needs page_size >= 1");
     if (a->batch == 0 || a->seq_len == 0) return SSQ_OK;
     hipStream_t st = (hipStream_t)stream;
-    if (a->kernel == 3 || (a->kernel == 0 && a->grid && ssq_encode_grid_supported(a))) return ssq_encode_grid_run(a, st);
+    if (a->kernel == 3 || (a->kernel == 0 && a->grid && ssq_encode_grid_supported(a) && ssq_encode_grid_fits(a)))
+        return ssq_encode_grid_run(a, st);
     EncodeParams p;
     p.a = *a;
     const int KS = (a->block_dim + 2 + 3) / 4;

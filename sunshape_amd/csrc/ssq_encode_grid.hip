@@ -533,6 +533,14 @@ bool ssq_encode_grid_supported(const ssq_encode_args* a) {
     return a->block_dim == 2 && !a->metric && a->n_centroids >= 1 && a->n_centroids <= 256 && a->n_blocks <= 128;
 }
 
+// the search kernel holds every light block's codewords in LDS
+bool ssq_encode_grid_fits(const ssq_encode_args* a) {
+    int n_light = 0;
+    for (int blk = 0; blk < a->n_blocks; ++blk)
+        n_light += blk < 64 ? !((a->heavy_mask[0] >> blk) & 1) : !((a->heavy_mask[1] >> (blk - 64)) & 1);
+    return grid_smem(n_light, a->n_blocks, 4) <= 160 * 1024;
+}
+
 extern "C" uint64_t ssq_encode_grid_bytes(const ssq_encode_args* a) {
     if (!a || a->struct_size != sizeof(ssq_encode_args) || !ssq_encode_grid_supported(a) || a->n_blocks < 1 ||
         a->num_kv_heads < 1)

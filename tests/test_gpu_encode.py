@@ -336,6 +336,21 @@ def test_grid_encode_paged_matches_contiguous():
         assert torch.equal(got_c, codes[b]) and torch.equal(got_p, pt[b])
 
 
+def test_grid_encode_too_many_blocks_falls_back():
+    """64 light blocks do not fit the search kernel's LDS: with kernel 0 a passed grid is
+    ignored (the exhaustive encode runs), kernel 3 reports it unsupported."""
+    log("grid encode fallback at 64 light blocks")
+    keys, perm, cent = _grid_case(128, 256, 300, 17)
+    ref, _ = O.encode(keys, perm, cent)
+    c = torch.from_numpy(cent).to(DEV)
+    grid = hip_ops.encode_grid(c)
+    k = torch.from_numpy(keys).to(DEV).to(torch.bfloat16)[None, None]
+    codes, _ = hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, grid=grid)
+    assert np.array_equal(np_of(codes[0, 0]), ref)
+    with pytest.raises(RuntimeError, match="LDS"):
+        hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, kernel=3, grid=grid)
+
+
 def test_grid_encode_rejections():
     log("grid encode rejections")
     cent = torch.randn(8, 256, 4, device=DEV)
