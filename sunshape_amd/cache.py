@@ -164,7 +164,8 @@ class SunShapeCodeLayer(DynamicLayer):
         lo, hi = self._len, self._len + S
         perm, cent = _per_head_arrays(self.codec)
         hip_ops.encode(key_states, perm, cent, heavy=self.heavy, codes_out=self._codes[:, :, lo:hi],
-                       pt_out=None if self._pt is None else self._pt[:, :, lo:hi], metric=self.codec.encode_metric())
+                       pt_out=None if self._pt is None else self._pt[:, :, lo:hi], metric=self.codec.encode_metric(),
+                       grid=self.codec.encode_search_grid(cent))
         self._vals[:, :, lo:hi] = value_states
         self._len = hi
         return self._views()

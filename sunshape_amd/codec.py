@@ -111,6 +111,10 @@ class SunShapeBlockCodec(torch.nn.Module):
         self.register_buffer("inv_permutation", identity.clone())
         self.register_buffer("rotation", torch.eye(head_dim, device=dev))
         self._heavy_cache: tuple[int, tuple[bool, ...]] | None = None
+        # encode search grids (this library's extension, no reference counterpart), per
+        # codebook tensor passed to the encode; see encode_search_grid
+        self.use_encode_grid = True
+        self._grid_cache: dict = {}
 
     # ------------------------------------------------------------------ helpers
     @classmethod
@@ -183,6 +187,28 @@ class SunShapeBlockCodec(torch.nn.Module):
             E = E[kv_head]
         return E
 
+    def encode_search_grid(self, cent: torch.Tensor) -> torch.Tensor | None:
+        """The search grid for ``hip_ops.encode(..., grid=)`` over ``cent`` (this codec's
+        codebook, or one KV head of it), or None where the grid does not apply (block_dim other
+        than 2, a block metric, or ``use_encode_grid = False``).
+
+        No counterpart in the reference: a search structure whose encode results equal the
+        exhaustive search bit for bit.  Built on first use and rebuilt when the centroid buffer
+        changes (new storage or an in-place write, seen through its version counter).
+        """
+        if not self.use_encode_grid or self.block_dim != 2 or self.mode in METRIC_MODES:
+            return None
+        if cent.shape[-2] > 256 or cent.shape[-3] > 128:
+            return None
+        buf = self.centroids
+        slot = (cent.data_ptr(), tuple(cent.shape))
+        key = (buf.data_ptr(), buf._version)
+        hit = self._grid_cache.get(slot)
+        if hit is None or hit[0] != key:
+            hit = (key, hip_ops.encode_grid(cent))
+            self._grid_cache[slot] = hit
+        return hit[1]
+
     def codebook(self, kv_head: int | None = None) -> torch.Tensor:
         cent = self.centroids
         if kv_head is not None and cent.ndim == 4:
@@ -248,7 +274,8 @@ class SunShapeBlockCodec(torch.nn.Module):
         if metric is not None and metric.ndim == 3:
             raise RuntimeError("per-KV-head metric: pass kv_head=")
         codes, pt = hip_ops.encode(keys.reshape(1, 1, -1, self.head_dim), perm, cent, heavy=heavy,
-                                   pt_dtype=torch.float32, pt_dense=True, metric=metric)
+                                   pt_dtype=torch.float32, pt_dense=True, metric=metric,
+                                   grid=self.encode_search_grid(cent))
         mixed = self.mode == "profileperm_mixed_precision"
         return SunShapeQuantized(
             indices=codes.reshape(-1, self.n_blocks),
@@ -309,3 +336,4 @@ class SunShapeBlockCodec(torch.nn.Module):
     def _load_from_state_dict(self, *args, **kwargs):
         super()._load_from_state_dict(*args, **kwargs)
         self._heavy_cache = None
+        self._grid_cache = {}

@@ -82,7 +82,7 @@ class PagedSunShapeCache:
         perm = self.codec.effective_permutation()
         hip_ops.encode(key_states.to(self.device), perm, self.codec.centroids, heavy=self.heavy,
                        codes_out=self.code_pages, pt_out=self.pt_pages, slot_mapping=slots,
-                       metric=self.codec.encode_metric())
+                       metric=self.codec.encode_metric(), grid=self.codec.encode_search_grid(self.codec.centroids))
         flat = slots.reshape(-1)
         page, off = flat // self.page_size, flat % self.page_size
         vals = value_states.to(self.device, self.v_pages.dtype).permute(0, 2, 1, 3).reshape(B * S, Hkv, self.value_dim)

@@ -144,7 +144,9 @@ def quantize_key_states(layer_idx: int, key_states: torch.Tensor) -> SunShapeQua
     if keys.dtype not in (torch.float32, torch.bfloat16, torch.float16):
         keys = keys.float()
     metric = codec.encode_metric() if hasattr(codec, "encode_metric") else None
-    codes, pt = hip_ops.encode(keys, perm, cent, heavy=heavy, pt_dtype=torch.float32, pt_dense=True, metric=metric)
+    grid = codec.encode_search_grid(cent) if hasattr(codec, "encode_search_grid") else None
+    codes, pt = hip_ops.encode(keys, perm, cent, heavy=heavy, pt_dtype=torch.float32, pt_dense=True, metric=metric,
+                               grid=grid)
     mixed = codec.mode == "profileperm_mixed_precision"
     pblocks = codec.mixed_high_precision_blocks.detach().clone() if mixed else None
     heads = []

@@ -49,6 +49,29 @@ def test_codec_quantize_dequantize_forward_mixed():
     assert_rel(s, np_of(q).astype(np.float64) @ ref.astype(np.float64).T, SCORE_TOL, "mixed scores")
 
 
+def test_codec_encode_grid_cached_and_rebuilt_on_codebook_change():
+    """codec.quantize runs the grid search for block_dim 2 (the codec builds and caches the
+    grid); the codes equal the exhaustive encode's, and an in-place codebook write rebuilds it."""
+    log("codec encode grid cache")
+    codec, sigma = _mixed_codec(seed=41)
+    keys = (torch.randn(3000, 64) * sigma).to(torch.bfloat16).to(DEV)
+    qz = codec.quantize(keys)
+    assert len(codec._grid_cache) == 1
+    grid = next(iter(codec._grid_cache.values()))[1]
+    codec.use_encode_grid = False
+    assert np.array_equal(np_of(codec.quantize(keys).indices), np_of(qz.indices))
+    codec.use_encode_grid = True
+    assert codec.quantize(keys).indices.equal(qz.indices)
+    assert next(iter(codec._grid_cache.values()))[1] is grid  # reused
+    with torch.no_grad():
+        codec.centroids.mul_(1.5)
+    qz2 = codec.quantize(keys)
+    assert next(iter(codec._grid_cache.values()))[1] is not grid  # rebuilt
+    heavy = codec.mixed_high_precision_blocks.cpu().numpy()
+    rc, _ = O.encode(keys.float().cpu().numpy(), codec.permutation.cpu().numpy(), codec.centroids.cpu().numpy(), heavy)
+    assert np.array_equal(np_of(qz2.indices), rc)
+
+
 def test_codec_identity_mode_ignores_permutation_buffer():
     log("codec identity mode")
     cb = synthetic.make_codebook(1, 64, 8, 5)
