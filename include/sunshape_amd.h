@@ -170,7 +170,9 @@ int ssq_encode(const ssq_encode_args* a, void* stream);
  * all codewords).  ssq_encode then evaluates only those candidates, with the reference's exact
  * arithmetic, so its codes equal kernels 1 and 2 bit for bit.
  * The grid depends only on perm-independent codebook values (cent, cent_sh, n_blocks,
- * n_centroids, num_kv_heads when cent_sh != 0); rebuild it when the codebook changes.
+ * n_centroids, num_kv_heads when cent_sh != 0); rebuild it when the codebook changes.  Each
+ * block's header holds a fingerprint of its codebook: ssq_encode scans every codeword of a
+ * block whose codebook no longer matches, so a stale grid is slow, not wrong.
  */
 uint64_t ssq_encode_grid_bytes(const ssq_encode_args* a);
 int ssq_encode_grid_build(const ssq_encode_args* a, void* grid, uint64_t grid_bytes, void* stream);

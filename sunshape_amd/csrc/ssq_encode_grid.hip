@@ -38,7 +38,7 @@ namespace {
 constexpr int kG = 128;        // cells per dimension
 constexpr int kRec = 32;       // bytes per cell record: count (255 = scan all), then indices, padded
 constexpr int kMaxCand = kRec - 1;
-constexpr int kHdr = 8;        // floats per block header: mid0, mid1, inv0, inv1, Rc, valid
+constexpr int kHdr = 8;        // floats per block header: mid0, mid1, inv0, inv1, Rc, valid, fingerprint
 constexpr int kThreads = 256;
 
 inline int grid_heads(const ssq_encode_args& a) { return a.cent_sh == 0 ? 1 : a.num_kv_heads; }
@@ -52,6 +52,20 @@ inline size_t grid_total_bytes(const ssq_encode_args& a) {
 // ---------------------------------------------------------------------------
 // build
 // ---------------------------------------------------------------------------
+// Order-free fingerprint of one block's codebook (fp32 bit patterns, indices, count).  The
+// builder stores it in the block's header; the search recomputes it from the codebook it is
+// given and scans every codeword of a block whose fingerprint differs, so a grid built for
+// another codebook costs time, never correctness (barring a 32-bit collision).
+__device__ __forceinline__ uint32_t cw_mix(float c0, float c1, int j) {
+    const uint32_t a = __float_as_uint(c0), b = __float_as_uint(c1);
+    uint32_t h = ((a << 7) | (a >> 25)) ^ (b * 0x9E3779B1u) ^ ((uint32_t)j * 0x85EBCA77u);
+    h ^= h >> 15;
+    h *= 0x2C1B3C6Du;
+    h ^= h >> 12;
+    return h;
+}
+__device__ __forceinline__ uint32_t cw_count_mix(int nc) { return (uint32_t)nc * 0xC2B2AE35u; }
+
 // one lane per (block, codebook head), in fp64: the cell map's centre (the codewords' bounding-box
 // centre) and scale (their RMS spread about the mean) per dimension, and max |c|
 __global__ __launch_bounds__(64) void k_grid_header(const float* cent, int64_t cent_sh, int nb, int nc, float* hdr) {
@@ -87,9 +101,12 @@ __global__ __launch_bounds__(64) void k_grid_header(const float* cent, int64_t c
     }
     float* out = hdr + ((int64_t)h * nb + blk) * kHdr;
     out[0] = mid[0]; out[1] = mid[1]; out[2] = inv[0]; out[3] = inv[1];
+    uint32_t fp = cw_count_mix(nc);
+    for (int j = 0; j < nc; ++j) fp ^= cw_mix(c[2 * j], c[2 * j + 1], j);
     out[4] = finite ? (float)(sqrt(nrm) * (1.0 + 0x1.0p-20)) : INFINITY;
     out[5] = valid ? 1.f : 0.f;
-    out[6] = 0.f; out[7] = 0.f;
+    out[6] = __uint_as_float(fp);
+    out[7] = 0.f;
 }
 
 // The cell map, per dimension: u = (x - mid) inv, t = u / (1 + |u|) in (-1, 1), cell
@@ -265,26 +282,43 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
     int* poff = reinterpret_cast<int*>(hd + nl);                           // [nl]: perm0, perm1, block id, 0
     uint8_t* cs = reinterpret_cast<uint8_t*>(poff + 4 * nl) + wave * 64 * nb;  // this wave's code rows
 
-    // ---- stage the light blocks' codewords, |c|^2 (rounded squares summed left to right), headers
+    // ---- stage the light blocks, one wave per block: codewords, |c|^2 (rounded squares summed
+    // left to right), the header, and the codebook fingerprint check (a grid built for another
+    // codebook leaves the block without cells: every key scans all codewords)
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
     const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
-    for (int e = threadIdx.x; e < nl * 256; e += blockDim.x) {
-        const int li = e >> 8, j = e & 255;
-        if (j < nc) {
-            const float* c = cent + ((int64_t)p.light[li] * nc + j) * 2;
-            const float c0 = c[0], c1 = c[1];
-            cb[e] = make_float2(c0, c1);
-            const float t0 = c0 * c0, t1 = c1 * c1;
-            cn[e] = t0 + t1;
+    for (int li = wave; li < nl; li += waves) {
+        const int blk = p.light[li];
+        const float* c = cent + (int64_t)blk * nc * 2;
+        float v0[4], v1[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {  // loads first, then arithmetic
+            const int j = lane + 64 * q;
+            v0[q] = j < nc ? c[2 * j] : 0.f;
+            v1[q] = j < nc ? c[2 * j + 1] : 0.f;
         }
-    }
-    for (int li = threadIdx.x; li < nl; li += blockDim.x) {
-        const float* h = p.hdr + ((int64_t)hsel * nb + p.light[li]) * kHdr;
-        hd[li] = h[5] != 0.f ? make_float4(h[0], h[1], h[2], h[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
-        poff[4 * li] = (int)perm[p.light[li] * 2];
-        poff[4 * li + 1] = (int)perm[p.light[li] * 2 + 1];
-        poff[4 * li + 2] = p.light[li];  // kept in LDS: a kernel-argument array indexed in the loop
-        poff[4 * li + 3] = 0;            // would be a memory load that waits for every pending load
+        uint32_t f = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int j = lane + 64 * q;
+            if (j < nc) {
+                cb[li * 256 + j] = make_float2(v0[q], v1[q]);
+                const float t0 = v0[q] * v0[q], t1 = v1[q] * v1[q];
+                cn[li * 256 + j] = t0 + t1;
+                f ^= cw_mix(v0[q], v1[q], j);
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) f ^= __shfl_xor(f, o);
+        if (lane == 0) {
+            const float* h = p.hdr + ((int64_t)hsel * nb + blk) * kHdr;
+            const bool ok = h[5] != 0.f && (f ^ cw_count_mix(nc)) == __float_as_uint(h[6]);
+            hd[li] = ok ? make_float4(h[0], h[1], h[2], h[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+            poff[4 * li] = (int)perm[blk * 2];
+            poff[4 * li + 1] = (int)perm[blk * 2 + 1];
+            poff[4 * li + 2] = blk;  // kept in LDS: a kernel-argument array indexed in the loop
+            poff[4 * li + 3] = 0;    // would be a memory load that waits for every pending load
+        }
     }
     for (int i = lane; i < 16 * nb; i += 64) reinterpret_cast<uint32_t*>(cs)[i] = 0u;  // heavy blocks: code 0
     __syncthreads();

@@ -336,6 +336,25 @@ def test_grid_encode_paged_matches_contiguous():
         assert torch.equal(got_c, codes[b]) and torch.equal(got_p, pt[b])
 
 
+def test_grid_built_for_another_codebook_still_gives_exact_codes():
+    """A grid is only a search aid: used with a codebook it was not built for (here one block
+    changed by one ulp, and a wholly different codebook), the blocks whose fingerprint differs
+    scan every codeword, so the codes still equal the oracle's."""
+    log("grid encode with a stale grid")
+    keys, perm, cent = _grid_case(64, 256, 1200, 23)
+    c = torch.from_numpy(cent).to(DEV)
+    grid = hip_ops.encode_grid(c)
+    k = torch.from_numpy(keys).to(DEV).to(torch.bfloat16)[None, None]
+    tp = torch.from_numpy(perm).to(DEV)
+    cent2 = cent.copy()
+    cent2[5, 77, 1] = np.nextafter(cent2[5, 77, 1], np.float32(np.inf))
+    other = _grid_case(64, 256, 10, 99)[2]
+    for cb in (cent2, other):
+        ref, _ = O.encode(keys, perm, cb)
+        codes, _ = hip_ops.encode(k, tp, torch.from_numpy(cb).to(DEV), kernel=3, grid=grid)
+        assert np.array_equal(np_of(codes[0, 0]), ref)
+
+
 def test_grid_encode_too_many_blocks_falls_back():
     """64 light blocks do not fit the search kernel's LDS: with kernel 0 a passed grid is
     ignored (the exhaustive encode runs), kernel 3 reports it unsupported."""
