@@ -10,7 +10,7 @@ Prints ONE JSON line: keys scored/s (B*Hkv*T per step / time), achieved HBM GB/s
 algorithmic bytes and its fraction of the 8 TB/s peak, the kernel's average launch time
 from HIP events on its own stream, and a bounded CPU-oracle baseline timed on the host.
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -37,7 +37,7 @@ def _args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "copycal"])
+    ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -197,8 +197,17 @@ def _encode_workload(dev, kernel):
         got, _ = hip_ops.encode(keys_t, p["perm"], p["centroids"], heavy=heavy, kernel=kernel, grid=grid)
         assert torch.equal(got, ref), "grid encode differs from the MFMA encode"
 
-    def step():
-        hip_ops.encode(keys_t, p["perm"], p["centroids"], heavy=heavy, kernel=kernel, grid=grid)
+    from sunshape_amd import _native as N
+
+    a, codes_k, pt_k, keep = hip_ops.encode_args(keys_t, p["perm"], p["centroids"], heavy=heavy, kernel=kernel,
+                                                 grid=grid)
+    L = N.lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def step(_alive=(keep, codes_k, pt_k)):  # one prebuilt C-ABI call (outputs rewritten in place)
+        rc = L.ssq_encode(ctypes.byref(a), stream)
+        if rc:
+            N.check(rc)
 
     n = B * Hkv * S
     algo = n * D * 2 + n * 32 + n * 4 * 2 * 2 + Hkv * 32 * 256 * 2 * 4
@@ -207,6 +216,72 @@ def _encode_workload(dev, kernel):
            "search": "grid" if grid is not None else "exhaustive", "grid_build_ms": grid_ms,
            "grid_bytes": None if grid is None else grid.numel()}
     return step, n, algo, cfg, None, "ssq_encode" if grid is None else "ssq_encode_grid"
+
+
+def _append_workload(name, dev, kernel):
+    """One serving step's append: the new key of every (sequence, KV head) encoded into its slot of
+    the 16-token pages.  c4append: the config-4 codec (64 x 8 keys, 32 blocks of dim 4, per-head
+    codebooks, the MFMA encode); c5append: the config-5 codec (16 x 2 keys, 28 VQ blocks of dim 2 +
+    4 passthrough, the grid search with the codec's grid)."""
+    import torch
+
+    from sunshape_amd import hip_ops, synthetic
+
+    page = 16
+    g = torch.Generator(device=dev).manual_seed(44)
+    heavy, grid, pt_pages = None, None, None
+    if name == "c4append":
+        p = synthetic.config4(dev, T=256)
+        B, Hkv, D, bd, T = 64, 8, 128, 4, 256
+        bt = p["block_table"]
+        perm, cent = p["perm"], p["centroids"]
+        sigma = synthetic.make_codebook(Hkv, D, bd, 4).sigma.to(dev)  # config 4's codec (seed 4)
+        keys_t = (torch.randn(B, Hkv, 1, D, generator=g, device=dev) * sigma[:, None, :]).to(torch.bfloat16)
+    else:
+        p = synthetic.config5(dev, B=16, S=page)
+        B, Hkv, D, bd, T = 16, 2, 64, 2, 256
+        keys_t = p["keys"][:, :, -1:].contiguous()  # keys drawn as the codec was fitted
+        heavy = p["heavy"].tolist()
+        bt = torch.randperm(B * T // page, device=dev).to(torch.int32).view(B, T // page)
+        perm, cent = p["perm"], p["centroids"]
+        if kernel in (0, 3):
+            grid = hip_ops.encode_grid(cent)
+        pt_pages = torch.zeros(B * T // page, Hkv, page, sum(heavy), bd, device=dev, dtype=torch.bfloat16)
+    nb = D // bd
+    code_pages = torch.zeros(B * T // page, Hkv, page, nb, device=dev, dtype=torch.uint8)
+    pos = T - 1  # the step's token lands in the last slot of each sequence's last page
+    slots = (bt[:, pos // page].to(torch.int64) * page + pos % page).view(B, 1).contiguous()
+    ref, _ = hip_ops.encode(keys_t, perm, cent, heavy=heavy, kernel=2 if bd == 4 else 1)
+
+    # the timed loop replays one prebuilt C-ABI call: at a few microseconds per launch, the
+    # Python wrapper's checks would otherwise be what the events measure
+    from sunshape_amd import _native as N
+
+    a, _, _, keep = hip_ops.encode_args(keys_t, perm, cent, heavy=heavy, codes_out=code_pages, pt_out=pt_pages,
+                                        slot_mapping=slots, kernel=kernel, grid=grid)
+    L = N.lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def step(_alive=(keep, code_pages, pt_pages)):  # the args point into these
+        rc = L.ssq_encode(ctypes.byref(a), stream)
+        if rc:
+            N.check(rc)
+
+    step()
+    torch.cuda.synchronize()
+    pages = bt[:, pos // page].long()
+    got = code_pages[pages, :, pos % page]  # [B, Hkv, nb]
+    assert torch.equal(got, ref[:, :, 0]), "paged append differs from the contiguous encode"
+    n = B * Hkv
+    nlight = nb - (sum(heavy) if heavy else 0)
+    algo = n * D * 2 + n * nb + Hkv * nlight * 256 * bd * 4 + Hkv * D * 8 + B * 8 + n * (nb - nlight) * bd * 2
+    cfg = {"workload": {"c4append": "F1 paged append, one decode step at the config-4 shape "
+                                    "(64 x 8 keys, 32 blocks of dim 4)",
+                        "c5append": "F1 paged append, one decode step with the config-5 codec "
+                                    "(16 x 2 keys, 28 VQ blocks of dim 2 + 4 bf16 passthrough)"}[name],
+           "keys": n, "head_dim": D, "block_dim": bd, "page_size": page, "kernel": kernel,
+           "search": "grid" if grid is not None else "exhaustive"}
+    return step, n, algo, cfg, None, "ssq_encode"
 
 
 def _copy_workload(dev):
@@ -287,6 +362,8 @@ def main():
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
         step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev)
+    elif args.workload in ("c4append", "c5append"):
+        step, keys, algo_bytes, cfg, unit_data, kname = _append_workload(args.workload, dev, args.kernel)
     elif args.workload == "copycal":
         step, keys, algo_bytes, cfg, unit_data, kname = _copy_workload(dev)
     else:

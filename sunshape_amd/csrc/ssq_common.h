@@ -83,6 +83,39 @@ __device__ __forceinline__ void ssq_store_elem(void* p, int dt, int64_t i, float
     }
 }
 
+// The keys of an encode launch.  Short sequences are folded: all sequences of one KV head share
+// one key index range, i = b * seq_len + s, and gridDim.y counts KV heads, so a decode step's
+// one key per sequence fills workgroups instead of giving each its own.  Otherwise gridDim.y
+// counts (batch, KV head) pairs and i = s.
+struct SsqKeyMap {
+    int fold, b_blk, kv, n_keys;
+    __device__ __forceinline__ SsqKeyMap(const ssq_encode_args& a, int fold_) : fold(fold_) {
+        const int y = blockIdx.y;
+        kv = fold ? y : y % a.num_kv_heads;
+        b_blk = fold ? 0 : y / a.num_kv_heads;
+        n_keys = fold ? a.batch * a.seq_len : a.seq_len;
+    }
+    __device__ __forceinline__ void bs(const ssq_encode_args& a, int i, int& b, int& s) const {
+        if (fold) {
+            b = i / a.seq_len;
+            s = i - b * a.seq_len;
+        } else {
+            b = b_blk;
+            s = i;
+        }
+    }
+    // element offset of key i's row
+    __device__ __forceinline__ int64_t krow(const ssq_encode_args& a, int i) const {
+        int b, s;
+        bs(a, i, b, s);
+        return (int64_t)b * a.k_sb + (int64_t)kv * a.k_sh + (int64_t)s * a.k_ss;
+    }
+};
+// folding applies when a sequence is shorter than one workgroup's keys
+inline bool ssq_encode_fold(const ssq_encode_args* a, int keys_per_wg) {
+    return a->seq_len < keys_per_wg && (int64_t)a->batch * a->seq_len <= 0x7fffffff;
+}
+
 __device__ __forceinline__ bool ssq_is_heavy(const uint64_t hm0, const uint64_t hm1, int blk) {
     return blk < 64 ? ((hm0 >> blk) & 1ull) : ((hm1 >> (blk - 64)) & 1ull);
 }
@@ -109,7 +142,6 @@ int ssq_check_hip(hipError_t e, const char* what);
 int ssq_device_cus();
 // grid-search encode (ssq_encode_grid.hip)
 bool ssq_encode_grid_supported(const ssq_encode_args* a);
-bool ssq_encode_grid_fits(const ssq_encode_args* a);
 int ssq_encode_grid_run(const ssq_encode_args* a, hipStream_t st);
 
 #define SSQ_REQUIRE(cond, ...)                                  \

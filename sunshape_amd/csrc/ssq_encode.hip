@@ -77,6 +77,8 @@ __device__ __forceinline__ float dist_of(float v) { return __builtin_sqrtf(v > 0
 struct EncodeParams {
     ssq_encode_args a;
     int nbc;           // blocks per workgroup chunk
+    int fold;          // short sequences: all sequences of a KV head share one key range (SsqKeyMap)
+    int passes;        // key passes per workgroup (scan)
 };
 
 __device__ __forceinline__ int heavy_ordinal(uint64_t hm0, uint64_t hm1, int blk) {
@@ -107,8 +109,8 @@ constexpr int kScanPasses = 16;  // key passes per workgroup (amortises the code
 __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_encode_args& a = p.a;
-    const int bk = blockIdx.y;
-    const int b = bk / a.num_kv_heads, kv = bk - b * a.num_kv_heads;
+    const SsqKeyMap km(a, p.fold);
+    const int kv = km.kv;
     const int blk0 = blockIdx.z * p.nbc;
     const int nbc = min(p.nbc, a.n_blocks - blk0);
     const int bd = a.block_dim, nc = a.n_centroids;
@@ -140,9 +142,11 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
     const bool heavy = ssq_is_heavy(a.heavy_mask[0], a.heavy_mask[1], blk);
     const float* cbb = cb + (size_t)bl * nc * bd;
     const float* cnb = cn + (size_t)bl * nc;
-    for (int pass = 0; pass < kScanPasses; ++pass) {
-        const int s = (blockIdx.x * kScanPasses + pass) * keys_per_pass + kk;
-        if (s >= a.seq_len) return;
+    for (int pass = 0; pass < p.passes; ++pass) {
+        const int i = (blockIdx.x * p.passes + pass) * keys_per_pass + kk;
+        if (i >= km.n_keys) return;
+        int b, s;
+        km.bs(a, i, b, s);
         const int64_t kbase = (int64_t)b * a.k_sb + (int64_t)kv * a.k_sh + (int64_t)s * a.k_ss;
         float x[16];
         for (int d = 0; d < bd; ++d) x[d] = ssq_load_elem(a.keys, a.k_dtype, kbase + perm[blk * bd + d]);
@@ -199,6 +203,7 @@ struct MfmaEncodeParams {
     int row_codes;            // 1: one chunk holds every light block and code rows take 16-byte stores
     int nbc;                  // light blocks per workgroup chunk
     int n_light;
+    int fold;                 // short sequences: all sequences of a KV head share one key range (SsqKeyMap)
     uint8_t light[kMaxLight]; // light (VQ-coded) block ids, ascending
 };
 
@@ -424,8 +429,8 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
     const ssq_encode_args& a = p.a;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
-    const int bk = blockIdx.y;
-    const int b = bk / a.num_kv_heads, kv = bk - b * a.num_kv_heads;
+    const SsqKeyMap km(a, p.fold);
+    const int kv = km.kv, n_keys = km.n_keys;
     const int chunk = blockIdx.z;
     const int l0 = chunk * p.nbc;
     const int nbc = min(p.nbc, p.n_light - l0);
@@ -521,14 +526,13 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
     const bool vec = (D % 32 == 0) && ((a.k_ss * esz) % 16 == 0) && ((a.k_sh * esz) % 16 == 0) &&
                      ((a.k_sb * esz) % 16 == 0) && ((uintptr_t)a.keys % 16 == 0) && esz == 2;
     const int lm = lane >> 2, lq = lane & 3;
-    const int s_wg = blockIdx.x * (kMfmaWaves * kRounds * 16);
-    const int64_t krow0 = (int64_t)b * a.k_sb + (int64_t)kv * a.k_sh;
+    const int s_wg = blockIdx.x * (kMfmaWaves * kRounds * 16);  // first key index of the workgroup
     uint4 pre[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
     auto fetch = [&](int round) {  // vector path: 16 bf16 (D=64) or the first 32 of a longer row quarter
         const int s = s_wg + (round * kMfmaWaves + wave) * 16 + lm;
-        if (vec && s < a.seq_len && D == 64) {
-            const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.keys) + krow0 +
-                                                              (int64_t)s * a.k_ss + lq * 16);
+        if (vec && s < n_keys && D == 64) {
+            const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.keys) +
+                                                              km.krow(a, s) + lq * 16);
             pre[0] = src[0];
             pre[1] = src[1];
         }
@@ -539,12 +543,12 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
 
     for (int round = 0; round < kRounds; ++round) {
         const int s0 = s_wg + (round * kMfmaWaves + wave) * 16;
-        if (s0 >= a.seq_len) break;  // wave-uniform
+        if (s0 >= n_keys) break;  // wave-uniform
         // stage this round's 16 rows (unpermuted, fp32) into xs
         if (vec && D == 64) {
             const uint32_t w[8] = {pre[0].x, pre[0].y, pre[0].z, pre[0].w, pre[1].x, pre[1].y, pre[1].z, pre[1].w};
             float* dst = xs + lm * XS + lq * 16;
-            const bool ok = s0 + lm < a.seq_len;
+            const bool ok = s0 + lm < n_keys;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float lo = a.k_dtype == SSQ_BF16 ? __uint_as_float(w[i] << 16) : ssq_f16_to_f32(w[i] & 0xFFFFu);
@@ -557,7 +561,7 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
             for (int e = lane; e < 16 * D; e += 64) {
                 const int m = e / D, j = e - m * D;
                 const int s = s0 + m;
-                xs[m * XS + j] = s < a.seq_len ? ssq_load_elem(a.keys, a.k_dtype, krow0 + (int64_t)s * a.k_ss + j) : 0.f;
+                xs[m * XS + j] = s < n_keys ? ssq_load_elem(a.keys, a.k_dtype, km.krow(a, s) + j) : 0.f;
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -605,18 +609,22 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
             const int pieces = nb >> 4;
             for (int e = lane; e < 16 * pieces; e += 64) {
                 const int m = e / pieces, q = e - m * pieces;
-                const int s = s0 + m;
-                if (s < a.seq_len) {
+                const int i = s0 + m;
+                if (i < n_keys) {
                     int64_t crow, prow;
+                    int b, s;
+                    km.bs(a, i, b, s);
                     out_rows(a, b, kv, s, crow, prow);
                     const uint32_t* src = reinterpret_cast<const uint32_t*>(cs + m * nb + 16 * q);
                     *reinterpret_cast<uint4*>(a.codes + crow + 16 * q) = make_uint4(src[0], src[1], src[2], src[3]);
                 }
             }
             const int m = lane >> 2;
-            const int s = s0 + m;
-            if (do_heavy && s < a.seq_len) {
+            const int i = s0 + m;
+            if (do_heavy && i < n_keys) {
                 int64_t crow, prow;
+                int b, s;
+                km.bs(a, i, b, s);
                 out_rows(a, b, kv, s, crow, prow);
                 for (int blk = lane & 3; blk < nb; blk += 4) {
                     if (!ssq_is_heavy(hm0, hm1, blk)) continue;
@@ -627,9 +635,11 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
             }
         } else {
             const int m = lane >> 2;
-            const int s = s0 + m;
-            if (s < a.seq_len) {
+            const int i = s0 + m;
+            if (i < n_keys) {
                 int64_t crow, prow;
+                int b, s;
+                km.bs(a, i, b, s);
                 out_rows(a, b, kv, s, crow, prow);
                 for (int blk = lane & 3; blk < nb; blk += 4) {
                     const bool heavy = ssq_is_heavy(hm0, hm1, blk);
@@ -681,8 +691,7 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
     if (a->slot_mapping) SSQ_REQUIRE(a->page_size >= 1, "paged output needs page_size >= 1");
     if (a->batch == 0 || a->seq_len == 0) return SSQ_OK;
     hipStream_t st = (hipStream_t)stream;
-    if (a->kernel == 3 || (a->kernel == 0 && a->grid && ssq_encode_grid_supported(a) && ssq_encode_grid_fits(a)))
-        return ssq_encode_grid_run(a, st);
+    if (a->kernel == 3 || (a->kernel == 0 && a->grid && ssq_encode_grid_supported(a))) return ssq_encode_grid_run(a, st);
     EncodeParams p;
     p.a = *a;
     const int KS = (a->block_dim + 2 + 3) / 4;
@@ -712,13 +721,23 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
             nbc = (mp.n_light + chunks0 - 1) / chunks0;
         }
         SSQ_UNSUPPORTED(mfma_enc_smem(*a, nbc, KS) <= kMaxSmem, "head_dim too large for the MFMA encode");
+        const int keys_wg = kMfmaWaves * kRounds * 16;
+        mp.fold = ssq_encode_fold(a, keys_wg);
+        const int64_t n_keys = mp.fold ? (int64_t)a->batch * a->seq_len : a->seq_len;
+        const int64_t groups = ((n_keys + keys_wg - 1) / keys_wg) * (mp.fold ? a->num_kv_heads : a->batch * a->num_kv_heads);
+        if (mp.n_light > 0 && groups * ((mp.n_light + nbc - 1) / nbc) < ssq_device_cus()) {
+            // a small launch (a decode step's append): more, smaller block chunks fill the chip
+            const int64_t want = (ssq_device_cus() + groups - 1) / groups;
+            const int chunks1 = (int)(want < mp.n_light ? want : mp.n_light);
+            nbc = (mp.n_light + chunks1 - 1) / chunks1;
+        }
         mp.nbc = nbc;
         mp.ys_stride = mfma_ys_stride(*a, nbc);
         const int chunks = mp.n_light > 0 ? (mp.n_light + nbc - 1) / nbc : 1;
         mp.row_codes = chunks == 1 && a->n_blocks % 16 == 0 && (uintptr_t)a->codes % 16 == 0 && a->c_sb % 16 == 0 &&
                        a->c_sh % 16 == 0 && a->c_st % 16 == 0;
-        const int keys_wg = kMfmaWaves * kRounds * 16;
-        dim3 grid((a->seq_len + keys_wg - 1) / keys_wg, a->batch * a->num_kv_heads, chunks);
+        dim3 grid((unsigned)((n_keys + keys_wg - 1) / keys_wg), mp.fold ? a->num_kv_heads : a->batch * a->num_kv_heads,
+                  chunks);
         const size_t smem = mfma_enc_smem(*a, nbc, KS);
         int rc;
         const int sel = KS * 2 + (a->metric ? 1 : 0);
@@ -746,8 +765,12 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
     int nbc = a->n_blocks < kScanThreads ? a->n_blocks : kScanThreads;
     while (nbc > 1 && (size_t)nbc * a->n_centroids * (a->block_dim + 1) * 4 > 96 * 1024) --nbc;
     p.nbc = nbc;
-    const int keys_per_wg = (kScanThreads / nbc) * kScanPasses;
-    dim3 grid((a->seq_len + keys_per_wg - 1) / keys_per_wg, a->batch * a->num_kv_heads,
+    // folded (short sequences): one pass per workgroup, so the few keys spread over workgroups
+    p.fold = ssq_encode_fold(a, (kScanThreads / nbc) * kScanPasses);
+    p.passes = p.fold ? 1 : kScanPasses;
+    const int keys_per_wg = (kScanThreads / nbc) * p.passes;
+    const int64_t n_keys = p.fold ? (int64_t)a->batch * a->seq_len : a->seq_len;
+    dim3 grid((unsigned)((n_keys + keys_per_wg - 1) / keys_per_wg), p.fold ? a->num_kv_heads : a->batch * a->num_kv_heads,
               (a->n_blocks + nbc - 1) / nbc);
     const size_t smem = (size_t)nbc * a->n_centroids * (a->block_dim + 1) * 4;
     static bool done = false;

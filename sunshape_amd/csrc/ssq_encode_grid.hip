@@ -190,6 +190,8 @@ struct GridParams {
     int n_light;
     int row_codes;             // whole code rows in 16-byte stores
     int row_q;                 // 16-byte pieces of a key row when rows are read whole (else 0)
+    int fold;                  // short sequences: all sequences of a KV head share one key range (SsqKeyMap)
+    int nlc;                   // light blocks per workgroup chunk (blockIdx.z picks the chunk)
     uint8_t light[kMaxLight];  // light block ids, ascending
 };
 
@@ -230,10 +232,6 @@ __device__ __forceinline__ void eval_val(float2 c, float cq, int j, float m0, fl
     st.bj = take ? j : st.bj;
 }
 
-__device__ __forceinline__ void eval_cand(const float2* cb, const float* cn, int j, float m0, float m1, float xn,
-                                          Cand& st) {
-    eval_val(cb[j], cn[j], j, m0, m1, xn, true, st);
-}
 
 // the reference's value for codeword (c, |c|^2), clamped at 0
 __device__ __forceinline__ float chain_val(float2 c, float cq, float m0, float m1, float xn) {
@@ -271,9 +269,10 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int waves = blockDim.x >> 6;
-    const int bk = blockIdx.y;
-    const int b = bk / a.num_kv_heads, kv = bk - b * a.num_kv_heads;
-    const int nl = p.n_light, nb = a.n_blocks, nc = a.n_centroids;
+    const SsqKeyMap km(a, p.fold);
+    const int kv = km.kv;
+    const int l0 = blockIdx.z * p.nlc;  // this chunk's first light block
+    const int nl = min(p.nlc, p.n_light - l0), nb = a.n_blocks, nc = a.n_centroids;
     const int hsel = a.cent_sh == 0 ? 0 : kv;
 
     float2* cb = reinterpret_cast<float2*>(smem);                          // [nl][256]
@@ -288,7 +287,7 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
     const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
     for (int li = wave; li < nl; li += waves) {
-        const int blk = p.light[li];
+        const int blk = p.light[l0 + li];
         const float* c = cent + (int64_t)blk * nc * 2;
         float v0[4], v1[4];
 #pragma unroll
@@ -324,12 +323,11 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
     __syncthreads();
 
     const uint64_t hm0 = a.heavy_mask[0], hm1 = a.heavy_mask[1];
-    const int64_t krow0 = (int64_t)b * a.k_sb + (int64_t)kv * a.k_sh;
     const uint8_t* cells = p.cells + (int64_t)hsel * nb * kG * kG * kRec;
     const int keys_wg = waves * 64;
-    const int s = blockIdx.x * keys_wg + wave * 64 + lane;
-    const bool live = s < a.seq_len;
-    const int64_t krow = krow0 + (int64_t)(live ? s : a.seq_len - 1) * a.k_ss;
+    const int key = blockIdx.x * keys_wg + wave * 64 + lane;  // this lane's key index
+    const bool live = key < km.n_keys;
+    const int64_t krow = km.krow(a, live ? key : km.n_keys - 1);
 
     const int kdt = a.k_dtype;
     // ---- the key's permuted elements.  ROWREG: the whole row (at most 128 bytes, 16-byte
@@ -499,10 +497,20 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
                 for (int i = 0; i < 4; ++i) { cc[i] = nc2[i]; cq[i] = nq[i]; }
             }
         }
-        if (__builtin_amdgcn_ballot_w64(full)) {  // rare: every codeword
+        if (__builtin_amdgcn_ballot_w64(full)) {  // rare: every codeword, 8 read ahead of their use
             if (full) st = Cand{INFINITY, -1};
-            for (int j = 0; j < nc; ++j)
-                if (full) eval_cand(cbl, cnl, j, m0, m1, xn, st);
+            for (int j0 = 0; j0 < nc; j0 += 8) {
+                float2 c8[8];
+                float q8[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int j = min(j0 + u, nc - 1);
+                    c8[u] = cbl[j];
+                    q8[u] = cnl[j];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) eval_val(c8[u], q8[u], j0 + u, m0, m1, xn, full && j0 + u < nc, st);
+            }
         }
         cs[lane * nb + __builtin_amdgcn_readfirstlane(poff[4 * li + 2])] = (uint8_t)(st.bj < 0 ? 0 : st.bj);
 
@@ -515,7 +523,9 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    auto out_rows = [&](int ss, int64_t& crow, int64_t& prow) {
+    auto out_rows = [&](int i, int64_t& crow, int64_t& prow) {  // key index i's output rows
+        int b, ss;
+        km.bs(a, i, b, ss);
         if (a.slot_mapping) {
             const int64_t slot = a.slot_mapping[(int64_t)b * a.sm_sb + ss];
             const int64_t page = slot / a.page_size, off = slot - page * a.page_size;
@@ -531,22 +541,32 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
         const int pieces = nb >> 4;
         for (int e = lane; e < 64 * pieces; e += 64) {
             const int m = e / pieces, q = e - m * pieces;
-            const int ss = s_wave + m;
-            if (ss < a.seq_len) {
+            const int i = s_wave + m;
+            if (i < km.n_keys) {
                 int64_t crow, prow;
-                out_rows(ss, crow, prow);
+                out_rows(i, crow, prow);
                 const uint32_t* src = reinterpret_cast<const uint32_t*>(cs + m * nb + 16 * q);
                 *reinterpret_cast<uint4*>(a.codes + crow + 16 * q) = make_uint4(src[0], src[1], src[2], src[3]);
             }
         }
-    } else if (live) {
+    } else if (live && gridDim.z == 1) {  // every block's code (heavy blocks' 0 included)
         int64_t crow, prow;
-        out_rows(s, crow, prow);
+        out_rows(key, crow, prow);
         for (int blk = 0; blk < nb; ++blk) a.codes[crow + blk] = cs[lane * nb + blk];
-    }
-    if ((hm0 | hm1) && live) {
+    } else if (live) {  // one chunk of several: its blocks' codes; chunk 0 also the heavy blocks' 0
         int64_t crow, prow;
-        out_rows(s, crow, prow);
+        out_rows(key, crow, prow);
+        for (int li = 0; li < nl; ++li) {
+            const int blk = __builtin_amdgcn_readfirstlane(poff[4 * li + 2]);
+            a.codes[crow + blk] = cs[lane * nb + blk];
+        }
+        if (blockIdx.z == 0)
+            for (int blk = 0; blk < nb; ++blk)
+                if (ssq_is_heavy(hm0, hm1, blk)) a.codes[crow + blk] = 0;
+    }
+    if ((hm0 | hm1) && live && blockIdx.z == 0) {
+        int64_t crow, prow;
+        out_rows(key, crow, prow);
         for (int blk = 0, hh = 0; blk < nb; ++blk) {
             if (!ssq_is_heavy(hm0, hm1, blk)) continue;
             const int slot = a.pt_dense ? blk : hh;
@@ -567,13 +587,6 @@ bool ssq_encode_grid_supported(const ssq_encode_args* a) {
     return a->block_dim == 2 && !a->metric && a->n_centroids >= 1 && a->n_centroids <= 256 && a->n_blocks <= 128;
 }
 
-// the search kernel holds every light block's codewords in LDS
-bool ssq_encode_grid_fits(const ssq_encode_args* a) {
-    int n_light = 0;
-    for (int blk = 0; blk < a->n_blocks; ++blk)
-        n_light += blk < 64 ? !((a->heavy_mask[0] >> blk) & 1) : !((a->heavy_mask[1] >> (blk - 64)) & 1);
-    return grid_smem(n_light, a->n_blocks, 4) <= 160 * 1024;
-}
 
 extern "C" uint64_t ssq_encode_grid_bytes(const ssq_encode_args* a) {
     if (!a || a->struct_size != sizeof(ssq_encode_args) || !ssq_encode_grid_supported(a) || a->n_blocks < 1 ||
@@ -619,11 +632,28 @@ int ssq_encode_grid_run(const ssq_encode_args* a, hipStream_t st) {
         const bool heavy = blk < 64 ? ((a->heavy_mask[0] >> blk) & 1) : ((a->heavy_mask[1] >> (blk - 64)) & 1);
         if (!heavy) gp.light[gp.n_light++] = (uint8_t)blk;
     }
-    int waves = 16;
-    while (waves > 4 && grid_smem(gp.n_light, a->n_blocks, waves) > 160 * 1024) waves >>= 1;
-    const size_t smem = grid_smem(gp.n_light, a->n_blocks, waves);
+    // Launch shape.  Short sequences fold into one key range per KV head; a short launch runs only
+    // the waves that have keys, and splits the light blocks into chunks (blockIdx.z) until the
+    // workgroups fill the chip.  Chunks also keep a workgroup's codewords within the LDS.
+    const int nl = gp.n_light, nb = a->n_blocks;
+    gp.fold = ssq_encode_fold(a, 16 * 64);
+    const int64_t n_keys = gp.fold ? (int64_t)a->batch * a->seq_len : a->seq_len;
+    const int64_t gy = gp.fold ? a->num_kv_heads : (int64_t)a->batch * a->num_kv_heads;
+    const int waves = n_keys < 16 * 64 ? (int)((n_keys + 63) / 64) : 16;
+    const int keys_wg = waves * 64;
+    const int64_t groups = ((n_keys + keys_wg - 1) / keys_wg) * gy;
+    int nlc = nl > 0 ? nl : 1;
+    if (nl > 1 && groups < ssq_device_cus()) {
+        const int64_t want = (ssq_device_cus() + groups - 1) / groups;
+        const int64_t chunks0 = want < nl ? want : nl;
+        nlc = (int)((nl + chunks0 - 1) / chunks0);
+    }
+    while (nlc > 1 && grid_smem(nlc, nb, waves) > 160 * 1024) --nlc;
+    const size_t smem = grid_smem(nlc, nb, waves);
     SSQ_UNSUPPORTED(smem <= 160 * 1024, "too many blocks for the grid encode's LDS");
-    gp.row_codes = a->n_blocks % 16 == 0 && (uintptr_t)a->codes % 16 == 0 && a->c_sb % 16 == 0 &&
+    const int chunks = nl > 0 ? (nl + nlc - 1) / nlc : 1;
+    gp.nlc = nlc;
+    gp.row_codes = chunks == 1 && nb % 16 == 0 && (uintptr_t)a->codes % 16 == 0 && a->c_sb % 16 == 0 &&
                    a->c_sh % 16 == 0 && a->c_st % 16 == 0;
     // key rows of at most 128 bytes at 16-byte aligned addresses are read whole, into registers
     const int esz = a->k_dtype == SSQ_F32 ? 4 : 2;
@@ -647,8 +677,7 @@ int ssq_encode_grid_run(const ssq_encode_args* a, hipStream_t st) {
                            "hipFuncSetAttribute(k_encode_grid)");
         if (rc) return rc;
     }
-    const int keys_wg = waves * 64;
-    dim3 grid((a->seq_len + keys_wg - 1) / keys_wg, a->batch * a->num_kv_heads);
+    dim3 grid((unsigned)((n_keys + keys_wg - 1) / keys_wg), (unsigned)gy, chunks);
     if (rowreg)
         hipLaunchKernelGGL(k_encode_grid<true>, grid, dim3(waves * 64), smem, st, gp);
     else

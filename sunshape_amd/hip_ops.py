@@ -323,12 +323,15 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
     return res[0] if len(res) == 1 else tuple(res)
 
 
-def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
+def encode_args(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
            heavy: Optional[Sequence[bool]] = None, pt_dtype: Optional[torch.dtype] = None, pt_dense: bool = False,
            codes_out: Optional[torch.Tensor] = None, pt_out: Optional[torch.Tensor] = None,
            slot_mapping: Optional[torch.Tensor] = None, metric: Optional[torch.Tensor] = None, kernel: int = 0,
            grid: Optional[torch.Tensor] = None):
-    """Nearest-codeword encode of keys [B, Hkv, S, D] -> (codes uint8 [B, Hkv, S, nb], pt or None).
+    """Validated ssq_encode arguments for encode(): (args, codes, pt, tensors the args point into).
+
+    For callers that replay one launch many times through the C ABI (a benchmark, a serving
+    loop); keep the returned tensors alive while the args are in use.
 
     Passthrough values (heavy blocks) are [B, Hkv, S, n_heavy, bd] (compact) or
     [B, Hkv, S, nb, bd] zero-filled (pt_dense, the reference's layout).  With
@@ -394,7 +397,11 @@ def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
         page = codes_out.shape[2]
         pt = pt_out
         if n_heavy:
-            _require(pt is not None and pt.ndim == 5 and pt.shape[2] == page, "paged encode needs pt_out [P, Hkv, page, slots, bd]")
+            slots = nb if pt_dense else n_heavy
+            _require(pt is not None and pt.ndim == 5 and pt.shape[1] == Hkv and pt.shape[2] == page
+                     and pt.shape[3] == slots and pt.shape[4] == bd and pt.stride(4) == 1 and pt.stride(3) == bd,
+                     f"paged encode needs pt_out [P, Hkv, {page}, {slots}, {bd}] with packed rows")
+            _on_gpu("pt_out", pt)
             pt_dtype = pt.dtype
         c_str = (codes.stride(0), codes.stride(1), codes.stride(2))
         p_str = (pt.stride(0), pt.stride(1), pt.stride(2)) if pt is not None else (0, 0, 0)
@@ -415,6 +422,31 @@ def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
         _require(grid.dtype == torch.uint8 and grid.is_contiguous(), "grid must be the uint8 tensor from encode_grid")
         a.grid, a.grid_bytes = N.ptr(grid), grid.numel()
     a.heavy_mask[0], a.heavy_mask[1] = w0, w1
+    return a, codes, pt, (keys, perm, cent, metric, grid, slot_mapping)
+
+
+def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
+           heavy: Optional[Sequence[bool]] = None, pt_dtype: Optional[torch.dtype] = None, pt_dense: bool = False,
+           codes_out: Optional[torch.Tensor] = None, pt_out: Optional[torch.Tensor] = None,
+           slot_mapping: Optional[torch.Tensor] = None, metric: Optional[torch.Tensor] = None, kernel: int = 0,
+           grid: Optional[torch.Tensor] = None):
+    """Nearest-codeword encode of keys [B, Hkv, S, D] -> (codes uint8 [B, Hkv, S, nb], pt or None).
+
+    Passthrough values (heavy blocks) are [B, Hkv, S, n_heavy, bd] (compact) or
+    [B, Hkv, S, nb, bd] zero-filled (pt_dense, the reference's layout).  With
+    slot_mapping [B, S] (int64) the outputs go into caller-provided pages:
+    codes_out [P, Hkv, page, nb], pt_out [P, Hkv, page, slots, bd].  Without it, codes_out /
+    pt_out (compact) may be given as [B, Hkv, S, ...] views to write into instead of allocating.
+    metric: SunShape-Pro block metric E [D, D] or per KV head [Hkv, D, D] (fp32); distances are
+    taken between E_b x and E_b c (sunshape/codec.py:375-376).  None = identity.
+    grid: search grid from encode_grid(cent) (block_dim 2, no metric); with it the encode
+    evaluates only each key's certified candidates (same codes).  kernel: 0 auto, 1 exact scan,
+    2 MFMA screen, 3 grid search.
+    Reference: sunshape/codec.py:362-385, sunshape/vllm_attn_backend.py:101-123.
+    """
+    a, codes, pt, _keep = encode_args(keys, perm, cent, heavy=heavy, pt_dtype=pt_dtype, pt_dense=pt_dense,
+                                      codes_out=codes_out, pt_out=pt_out, slot_mapping=slot_mapping, metric=metric,
+                                      kernel=kernel, grid=grid)
     N.check(N.lib().ssq_encode(ctypes.byref(a), N.stream_of(keys.device)))
     return codes, pt
 

@@ -314,6 +314,36 @@ def test_grid_encode_constructed_ties_duplicates_and_heavy():
         assert np.array_equal(np_of(pt[0, 0]), want)
 
 
+@pytest.mark.parametrize("kernel,bd,B,S", [(1, 4, 64, 1), (2, 4, 64, 1), (2, 4, 5, 300), (1, 2, 33, 3),
+                                           (2, 2, 33, 3), (3, 2, 33, 3), (3, 2, 64, 1)])
+def test_short_sequences_fold_batches(kernel, bd, B, S):
+    """A decode step's append (one or a few keys per sequence): launches put every sequence of a
+    KV head in one key range.  Codes into contiguous rows and into shuffled pages must equal the
+    oracle's, per (sequence, KV head)."""
+    log(f"folded encode kernel={kernel} bd={bd} B={B} S={S}")
+    Hkv, D, page = 8 if bd == 4 else 2, 128 if bd == 4 else 64, 16
+    cb = synthetic.make_codebook(Hkv, D, bd, 70 + bd)
+    g = torch.Generator().manual_seed(71)
+    keys = (torch.randn(B, Hkv, S, D, generator=g) * cb.sigma[:, None, :]).to(torch.bfloat16)
+    perm, cent = cb.perm.to(DEV), cb.centroids.to(DEV)
+    grid = hip_ops.encode_grid(cent) if kernel == 3 else None
+    codes, _ = hip_ops.encode(keys.to(DEV), perm, cent, kernel=kernel, grid=grid)
+    got = np_of(codes)
+    for b in range(B):
+        for h in range(Hkv):
+            ref, _ = O.encode(keys[b, h].float().numpy(), cb.perm[h].numpy(), cb.centroids[h].numpy())
+            assert np.array_equal(got[b, h], ref), (b, h)
+    n_pages = B * ((S + page - 1) // page) + 2
+    order = torch.randperm(n_pages, generator=g)
+    slots = torch.stack([order[b * ((S + page - 1) // page) + torch.arange(S) // page] * page + torch.arange(S) % page
+                         for b in range(B)]).to(torch.int64).to(DEV)
+    pages = torch.zeros(n_pages, Hkv, page, D // bd, dtype=torch.uint8, device=DEV)
+    hip_ops.encode(keys.to(DEV), perm, cent, codes_out=pages, slot_mapping=slots, kernel=kernel, grid=grid)
+    flat = pages.permute(0, 2, 1, 3).reshape(n_pages * page, Hkv, D // bd)
+    back = flat[slots.reshape(-1)].reshape(B, S, Hkv, D // bd).permute(0, 2, 1, 3)
+    assert torch.equal(back, codes)
+
+
 def test_grid_encode_paged_matches_contiguous():
     log("grid encode paged")
     p = synthetic.config5(DEV, B=2, S=96)
@@ -355,19 +385,34 @@ def test_grid_built_for_another_codebook_still_gives_exact_codes():
         assert np.array_equal(np_of(codes[0, 0]), ref)
 
 
-def test_grid_encode_too_many_blocks_falls_back():
-    """64 light blocks do not fit the search kernel's LDS: with kernel 0 a passed grid is
-    ignored (the exhaustive encode runs), kernel 3 reports it unsupported."""
-    log("grid encode fallback at 64 light blocks")
-    keys, perm, cent = _grid_case(128, 256, 300, 17)
+def test_grid_encode_many_blocks_in_chunks():
+    """64 light blocks exceed one workgroup's LDS: the search splits them into block chunks
+    (one workgroup per chunk), and the codes still equal the oracle's."""
+    log("grid encode at 64 light blocks")
+    keys, perm, cent = _grid_case(128, 256, 1500, 17)
     ref, _ = O.encode(keys, perm, cent)
     c = torch.from_numpy(cent).to(DEV)
     grid = hip_ops.encode_grid(c)
     k = torch.from_numpy(keys).to(DEV).to(torch.bfloat16)[None, None]
-    codes, _ = hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, grid=grid)
-    assert np.array_equal(np_of(codes[0, 0]), ref)
-    with pytest.raises(RuntimeError, match="LDS"):
-        hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, kernel=3, grid=grid)
+    for kernel in (0, 3):
+        codes, _ = hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, kernel=kernel, grid=grid)
+        assert np.array_equal(np_of(codes[0, 0]), ref)
+
+
+def test_paged_encode_rejects_mis_shaped_passthrough_pages():
+    """Paged outputs are written through the slot mapping; a passthrough page buffer whose slot
+    count, block_dim or row packing does not match is refused before any launch."""
+    log("paged encode pt_out validation")
+    p = synthetic.config5(DEV, B=1, S=16)
+    heavy = p["heavy"].tolist()
+    slots = torch.arange(16, dtype=torch.int64, device=DEV).view(1, 16)
+    cpages = torch.zeros(2, 2, 16, 32, dtype=torch.uint8, device=DEV)
+    for bad in (torch.zeros(2, 2, 16, 32, 2, device=DEV),          # dense slots for the compact layout
+                torch.zeros(2, 2, 16, 4, 3, device=DEV),           # wrong block_dim
+                torch.zeros(2, 2, 16, 2, 4, device=DEV).transpose(3, 4)):  # rows not packed
+        with pytest.raises(RuntimeError, match="pt_out"):
+            hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy, codes_out=cpages, pt_out=bad,
+                           slot_mapping=slots)
 
 
 def test_grid_encode_rejections():
