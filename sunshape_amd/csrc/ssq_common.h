@@ -137,6 +137,8 @@ __device__ __forceinline__ float ssq_wave_sum(float v) {
 // ---------------------------------------------------------------------------
 int ssq_fail(int code, const char* fmt, ...);
 int ssq_check_hip(hipError_t e, const char* what);
+// allow `bytes` of dynamic LDS for kernel `fn` on the current device (set once per kernel and device)
+int ssq_allow_lds(const void* fn, int bytes, const char* what);
 
 // compute units of the current device (cached per device; 256 on MI355X)
 int ssq_device_cus();

@@ -739,12 +739,8 @@ int validate(const ssq_decode_args* a, bool need_v) {
 template <int RP, bool PAGED, bool HAS_V, int VT>
 int launch_t(const DecodeParams& dp, const Plan& pl, hipStream_t st) {
     auto kern = k_decode_generic<RP, PAGED, HAS_V, VT>;
-    static bool attr_set = false;  // once per instantiation: allow the full 160 KiB of LDS
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxSmem);
-        if (e != hipSuccess) return ssq_check_hip(e, "hipFuncSetAttribute(decode)");
-        attr_set = true;
-    }
+    int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode)");
+    if (rc) return rc;
     dim3 grid(pl.n_splits, pl.n_groups, dp.a.batch * dp.a.num_kv_heads);
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), pl.smem, st, dp);
     return ssq_check_hip(hipGetLastError(), "k_decode_generic launch");

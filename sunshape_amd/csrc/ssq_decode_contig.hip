@@ -525,12 +525,8 @@ bool plan(const ssq_decode_args* a, bool has_v, CPlan& pl) {
 template <int BD, int DT, int VT, bool HAS_V, bool HV, bool MK>
 int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     auto kern = k_decode_contig<BD, DT, VT, HAS_V, HV, MK>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxSmem);
-        if (e != hipSuccess) return ssq_check_hip(e, "hipFuncSetAttribute(decode_contig)");
-        attr_set = true;
-    }
+    int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_contig)");
+    if (rc) return rc;
     dim3 grid(cp.a.batch * cp.a.num_kv_heads, pl.n_splits);
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), pl.smem, st, cp);
     return ssq_check_hip(hipGetLastError(), "k_decode_contig launch");

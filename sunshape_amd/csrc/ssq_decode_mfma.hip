@@ -595,12 +595,8 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
 template <int RP, int DT, int VT, int NB>
 int launch(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
     auto kern = k_decode_mfma<RP, DT, VT, NB>;
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxSmem);
-        if (e != hipSuccess) return ssq_check_hip(e, "hipFuncSetAttribute(decode_mfma)");
-        attr_set = true;
-    }
+    int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_mfma)");
+    if (rc) return rc;
     dim3 grid(mp.a.batch * mp.a.num_kv_heads, pl.n_splits);
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), pl.smem, st, mp);
     return ssq_check_hip(hipGetLastError(), "k_decode_mfma launch");

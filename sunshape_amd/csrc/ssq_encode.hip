@@ -663,14 +663,6 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
 
 constexpr size_t kMaxSmem = 160 * 1024;
 
-template <typename K>
-int set_smem_attr(K kern, bool& done) {
-    if (done) return SSQ_OK;
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxSmem);
-    if (e != hipSuccess) return ssq_check_hip(e, "hipFuncSetAttribute(encode)");
-    done = true;
-    return SSQ_OK;
-}
 
 }  // namespace
 
@@ -744,8 +736,7 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
         switch (sel) {
 #define SSQ_ENC_LAUNCH(KSV, MV)                                                                        \
     case KSV * 2 + MV: {                                                                               \
-        static bool d = false;                                                                         \
-        rc = set_smem_attr(k_encode_mfma<KSV, MV>, d);                                                 \
+        rc = ssq_allow_lds((const void*)k_encode_mfma<KSV, MV>, (int)kMaxSmem, "hipFuncSetAttribute(encode)"); \
         if (rc) return rc;                                                                             \
         hipLaunchKernelGGL((k_encode_mfma<KSV, MV>), grid, dim3(kMfmaWaves * SSQ_WAVE), smem, st, mp); \
         break;                                                                                         \
@@ -773,8 +764,7 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
     dim3 grid((unsigned)((n_keys + keys_per_wg - 1) / keys_per_wg), p.fold ? a->num_kv_heads : a->batch * a->num_kv_heads,
               (a->n_blocks + nbc - 1) / nbc);
     const size_t smem = (size_t)nbc * a->n_centroids * (a->block_dim + 1) * 4;
-    static bool done = false;
-    int rc = set_smem_attr(k_encode_scan, done);
+    int rc = ssq_allow_lds((const void*)k_encode_scan, (int)kMaxSmem, "hipFuncSetAttribute(encode)");
     if (rc) return rc;
     hipLaunchKernelGGL(k_encode_scan, grid, dim3(kScanThreads), smem, st, p);
     return ssq_check_hip(hipGetLastError(), "k_encode_scan launch");

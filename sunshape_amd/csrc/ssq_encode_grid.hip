@@ -663,20 +663,8 @@ int ssq_encode_grid_run(const ssq_encode_args* a, hipStream_t st) {
     gp.row_q = rowreg ? (int)(row_bytes / 16) : 0;
     const void* fn = rowreg ? reinterpret_cast<const void*>(k_encode_grid<true>)
                             : reinterpret_cast<const void*>(k_encode_grid<false>);
-    int dev = 0;
-    int rc = ssq_check_hip(hipGetDevice(&dev), "hipGetDevice");
+    const int rc = ssq_allow_lds(fn, 160 * 1024, "hipFuncSetAttribute(k_encode_grid)");
     if (rc) return rc;
-    static bool attr[2][64] = {};  // per kernel and device: dynamic LDS above the default
-    if (dev < 64 && !attr[rowreg][dev]) {
-        rc = ssq_check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
-                           "hipFuncSetAttribute(k_encode_grid)");
-        if (rc) return rc;
-        attr[rowreg][dev] = true;
-    } else if (dev >= 64) {
-        rc = ssq_check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
-                           "hipFuncSetAttribute(k_encode_grid)");
-        if (rc) return rc;
-    }
     dim3 grid((unsigned)((n_keys + keys_wg - 1) / keys_wg), (unsigned)gy, chunks);
     if (rowreg)
         hipLaunchKernelGGL(k_encode_grid<true>, grid, dim3(waves * 64), smem, st, gp);

@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 namespace {
 thread_local char g_err[512] = "";
 }
@@ -22,6 +24,26 @@ int ssq_check_hip(hipError_t e, const char* what) {
 }
 
 extern "C" const char* ssq_last_error(void) { return g_err; }
+
+// hipFuncSetAttribute applies per device: remember each (kernel, device) pair it was set for
+int ssq_allow_lds(const void* fn, int bytes, const char* what) {
+    static std::mutex mu;
+    static struct {
+        const void* fn;
+        int dev, bytes;
+    } done[512];
+    static int n_done = 0;
+    int dev = 0;
+    int rc = ssq_check_hip(hipGetDevice(&dev), "hipGetDevice");
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < n_done; ++i)
+        if (done[i].fn == fn && done[i].dev == dev && done[i].bytes >= bytes) return SSQ_OK;
+    rc = ssq_check_hip(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes), what);
+    if (rc) return rc;
+    if (n_done < 512) done[n_done++] = {fn, dev, bytes};
+    return SSQ_OK;
+}
 
 int ssq_device_cus() {
     static int cached[64] = {0};
