@@ -32,8 +32,7 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef short v4s __attribute__((ext_vector_type(4)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * SSQ_WAVE;
+constexpr int kMaxWaves = 8;  // waves per workgroup: 8 where the LDS and registers allow, else 4
 constexpr int kTile = 64;  // tokens per wave iteration
 constexpr int kD = 64;     // head_dim served
 constexpr int kHP = 16;    // passthrough (heavy-block) dims per token, padded to whole MFMA steps
@@ -60,11 +59,11 @@ __host__ __device__ constexpr int wave_bytes(int NB, int DT, bool HV) {
 }
 // codebook region: [NB][nc][BD] fp32, padded to whole 1 KB chunks (one direct-to-LDS wave load each)
 __host__ __device__ constexpr int cb_floats(int nc) { return (16 * nc + 63) / 64 * 256; }
-inline size_t contig_smem(const ssq_decode_args& a, int DT) {
+inline size_t contig_smem(const ssq_decode_args& a, int DT, int waves) {
     const bool hv = (a.heavy_mask[0] | a.heavy_mask[1]) != 0;
     const size_t cb = (size_t)cb_floats(a.n_centroids) * 4;
-    const size_t main = cb + (size_t)kWaves * wave_bytes(a.n_blocks, DT, hv);
-    const size_t merge = (size_t)kWaves * 16 * (16 * DT + 2) * 4;
+    const size_t main = cb + (size_t)waves * wave_bytes(a.n_blocks, DT, hv);
+    const size_t merge = (size_t)waves * 16 * (16 * DT + 2) * 4;
     return main > merge ? main : merge;
 }
 
@@ -165,8 +164,13 @@ __device__ __forceinline__ void issue_tile(const ContigParams& p, int b, int kv,
     }
 }
 
+// 8-wave workgroups need two waves' registers per SIMD, which the variants without passthrough,
+// mask or 128-dim values fit; the others keep 4 waves
+__host__ __device__ constexpr bool contig_wide(int dt, bool hv, bool mk) { return !hv && !mk && dt <= 4; }
+
 template <int BD, int DT, int VT, bool HAS_V, bool HV, bool MK>
-__global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p) {
+__global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 * SSQ_WAVE) void k_decode_contig(
+    const ContigParams p) {
     constexpr int NB = kD / BD;
     constexpr int NBW = NB / 4;  // code row dwords
     constexpr int KS = kD / 4;   // score k-steps
@@ -176,6 +180,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar loop control
+    const int W = blockDim.x >> 6;                              // waves in the workgroup
     const int l16 = lane & 15, lg = lane >> 4;
     const int bk = blockIdx.x;
     const int split = blockIdx.y;
@@ -213,7 +218,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
     Tile<NB, DT, HV, MK> ra, rb;
     if (n_tiles > 0) {
         issue_tile<NB, DT, HAS_V, HV, MK>(p, b, kv, t_begin + min(wave, last_tile) * kTile, t_end, lane, ra);
-        issue_tile<NB, DT, HAS_V, HV, MK>(p, b, kv, t_begin + min(wave + kWaves, last_tile) * kTile, t_end, lane, rb);
+        issue_tile<NB, DT, HAS_V, HV, MK>(p, b, kv, t_begin + min(wave + W, last_tile) * kTile, t_end, lane, rb);
     }
 
     // the codebook goes global -> LDS directly (no registers): 1 KB chunks, lane l's 16 bytes at
@@ -222,7 +227,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
         const float* cent = a.cent + (int64_t)kv * a.cent_sh;
         const int n4 = 16 * nc;  // float4s: NB * nc * BD = 64 nc floats
         const int n_chunks = (n4 + 63) / 64;
-        for (int c = wave; c < n_chunks; c += kWaves) {
+        for (int c = wave; c < n_chunks; c += W) {
             const int i = min(c * 64 + lane, n4 - 1);
             __builtin_amdgcn_global_load_lds(cent + 4 * i, (__attribute__((address_space(3))) void*)(cb + 256 * c), 16, 0,
                                              0);
@@ -309,7 +314,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
         float mk[MK ? 16 : 1];  // this tile's mask values, taken before R is reloaded
 #pragma unroll
         for (int k = 0; k < (MK ? 16 : 1); ++k) mk[k] = MK ? R.mk[k] : 0.f;
-        issue_tile<NB, DT, HAS_V, HV, MK>(p, b, kv, t_begin + min(tile + 2 * kWaves, last_tile) * kTile, t_end, lane, R);
+        issue_tile<NB, DT, HAS_V, HV, MK>(p, b, kv, t_begin + min(tile + 2 * W, last_tile) * kTile, t_end, lane, R);
 
         // ---- scores: S[row 4*lg+i][token 16g + l16] for the tile's 4 groups of 16 tokens
         v4f sc[4];
@@ -423,9 +428,9 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
     // load-counter waits at the loop head drain both register sets, i.e. no tile ahead stayed in
     // flight.  A step past the last tile is harmless: its tokens are all past t_end, so they get
     // probability 0 and no score or mask access.
-    for (int tile = wave; tile < n_tiles; tile += 2 * kWaves) {
+    for (int tile = wave; tile < n_tiles; tile += 2 * W) {
         step(ra, tile);
-        step(rb, tile + kWaves);
+        step(rb, tile + W);
     }
     if constexpr (!HAS_V) return;
 
@@ -435,8 +440,8 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
     for (int i = 0; i < 4; ++i) l_w[i] = row_sum(l_run[i]);
     __syncthreads();
     float* mbuf = smem;               // [waves][16]
-    float* lbuf = mbuf + kWaves * 16;  // [waves][16]
-    float* obuf = lbuf + kWaves * 16;  // [waves][16][Dv]
+    float* lbuf = mbuf + W * 16;  // [waves][16]
+    float* obuf = lbuf + W * 16;  // [waves][16][Dv]
     if (l16 == 0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) { mbuf[wave * 16 + 4 * lg + i] = m_run[i]; lbuf[wave * 16 + 4 * lg + i] = l_w[i]; }
@@ -447,12 +452,12 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
         for (int dt = 0; dt < DT; ++dt) obuf[((size_t)wave * 16 + 4 * lg + i) * Dv + 16 * dt + l16] = acc[dt][i];
     __syncthreads();
     const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
-    for (int e = tid; e < nr * Dv; e += kThreads) {
+    for (int e = tid; e < nr * Dv; e += blockDim.x) {
         const int r = e / Dv, dv = e - r * Dv;
         float M = -INFINITY;
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mbuf[w * 16 + r]);
+        for (int w = 0; w < W; ++w) M = fmaxf(M, mbuf[w * 16 + r]);
         float L = 0.f, o = 0.f;
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < W; ++w) {
             const float mw = mbuf[w * 16 + r];
             if (mw == -INFINITY) continue;
             const float f = __expf(mw - M);
@@ -476,7 +481,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_contig(const ContigParams p
 }
 
 struct CPlan {
-    int DT, split_len, n_splits;
+    int DT, split_len, n_splits, waves;
     size_t smem, ws_bytes;
 };
 
@@ -504,13 +509,17 @@ bool plan(const ssq_decode_args* a, bool has_v, CPlan& pl) {
         if ((uintptr_t)a->v % 16 || (a->v_sb * 2) % 16 || (a->v_sh * 2) % 16 || (a->v_st * 2) % 16) return false;
         pl.DT = a->value_dim / 16;
     }
-    pl.smem = contig_smem(*a, pl.DT);
+    // 8 waves share the codebook where the LDS holds their tiles (two waves per SIMD hide each
+    // other's gather and MFMA latency); the passthrough variant's registers allow only 4
+    const bool hv = (a->heavy_mask[0] | a->heavy_mask[1]) != 0;
+    pl.waves = contig_wide(pl.DT, hv, a->mask != nullptr) && contig_smem(*a, pl.DT, kMaxWaves) <= kMaxSmem ? kMaxWaves : 4;
+    pl.smem = contig_smem(*a, pl.DT, pl.waves);
     if (pl.smem > kMaxSmem) return false;
     const int units = a->batch * a->num_kv_heads;
     const int tiles = (a->seq_len + kTile - 1) / kTile;
     const int cus = ssq_device_cus();
     int splits = a->num_splits > 0 ? a->num_splits : (cus + units - 1) / units;
-    const int max_splits = (tiles + kWaves - 1) / kWaves;
+    const int max_splits = (tiles + pl.waves - 1) / pl.waves;
     if (splits > max_splits) splits = max_splits;
     if (splits < 1) splits = 1;
     const int tiles_per_split = (tiles + splits - 1) / splits;
@@ -528,7 +537,7 @@ int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_contig)");
     if (rc) return rc;
     dim3 grid(cp.a.batch * cp.a.num_kv_heads, pl.n_splits);
-    hipLaunchKernelGGL(kern, grid, dim3(kThreads), pl.smem, st, cp);
+    hipLaunchKernelGGL(kern, grid, dim3(pl.waves * SSQ_WAVE), pl.smem, st, cp);
     return ssq_check_hip(hipGetLastError(), "k_decode_contig launch");
 }
 
