@@ -10,7 +10,7 @@ Prints ONE JSON line: keys scored/s (B*Hkv*T per step / time), achieved HBM GB/s
 algorithmic bytes and its fraction of the 8 TB/s peak, the kernel's average launch time
 from HIP events on its own stream, and a bounded CPU-oracle baseline timed on the host.
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -37,7 +37,7 @@ def _args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "copycal"])
+    ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "c4g8", "c4bd2", "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -61,9 +61,13 @@ def _decode_workload(name, dev, kernel):
     from sunshape_amd import hip_ops, synthetic
 
     heavy, pt = None, None
-    if name == "c4":
-        p = synthetic.config4(dev)
-        B, Hq, Hkv, T, D, bd = 64, 32, 8, 32768, 128, 4
+    if name in ("c4", "c4g8", "c4bd2"):
+        # c4g8 / c4bd2: the config-4 layer with 64 query heads (8 per KV head) or at 4 bits/dim
+        # (64 blocks of dim 2); their LUTs exceed the LDS, so the kernel runs two row groups
+        Hq = 64 if name == "c4g8" else 32
+        bd = 2 if name == "c4bd2" else 4
+        p = synthetic.config4(dev, Hq=Hq, bd=bd)
+        B, Hkv, T, D = 64, 8, 32768, 128
         paged = True
     elif name == "c5":
         # SunShape-Mixed: the config-5 keys encoded once (28 VQ blocks + 4 bf16 passthrough blocks)
@@ -132,6 +136,8 @@ def _decode_workload(name, dev, kernel):
                   + (B * (T // 16) * 4 if paged else 0)  # int32 block table
                   + (pt.numel() * 2 if pt is not None else 0))  # bf16 passthrough values
     cfg = {"workload": {"c4": "C4 paged fused decode (Llama-3-8B layer, 2 bits/dim)",
+                        "c4g8": "C4 layer with 64 query heads (8 per KV head), paged, 2 bits/dim",
+                        "c4bd2": "C4 layer at 4 bits/dim (64 blocks of dim 2), paged",
                         "c3": "C3 contiguous fused decode (Qwen2.5-0.5B layer, 4 bits/dim)",
                         "c5": "C5 SunShape-Mixed fused decode (config-5 keys: 28 VQ + 4 bf16 blocks of dim 2)"}[name],
            "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "context": T, "block_dim": bd,
@@ -358,7 +364,7 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.workload in ("c4", "c3", "c5"):
+    if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2"):
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
         step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev)

@@ -40,6 +40,7 @@ constexpr size_t kMaxSmem = 160 * 1024;
 struct MfmaParams {
     ssq_decode_args a;
     int G, rows, split_len, n_splits;
+    int rg;  // query rows per row group (blockIdx.z): a group's LUT fits the LDS, V streams once per group
     float* ws_o;
     float* ws_m;
     float* ws_l;
@@ -223,10 +224,11 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
     }
     if (valid) {
         if (a.scores) {
+            const int row0 = blockIdx.z * p.rg, nr = min(p.rg, p.rows - row0);
 #pragma unroll
             for (int r = 0; r < RP; ++r) {
-                if (r < p.rows) {
-                    const int g = r / a.q_len, qi = r - g * a.q_len;
+                if (r < nr) {
+                    const int g = (row0 + r) / a.q_len, qi = row0 + r - g * a.q_len;
                     const int h = kv * p.G + g;
                     a.scores[(int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)qi * a.s_sl + t] = s[r];
                 }
@@ -379,7 +381,8 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     const int b = bk / a.num_kv_heads;
     const int kv = bk - b * a.num_kv_heads;
     const int D = a.head_dim, bd = a.block_dim;
-    const int nr = p.rows;  // <= RP
+    const int row0 = blockIdx.z * p.rg;          // this workgroup's query rows: row0 .. row0 + nr - 1
+    const int nr = min(p.rg, p.rows - row0);     // <= RP
     const int T = min(a.seq_lens[b], a.seq_len);
     const int t_begin = split * p.split_len;
     const int t_end = min(T, t_begin + p.split_len);
@@ -412,7 +415,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
             ok[k] = e < RP * D && r < nr;
             src[k] = 0;  // rows past nr read element 0 and are zeroed
             if (ok[k]) {
-                const int g = r / a.q_len, qi = r - g * a.q_len;
+                const int g = (row0 + r) / a.q_len, qi = row0 + r - g * a.q_len;
                 const int h = kv * p.G + g;
                 src[k] = (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl + j;
             }
@@ -529,7 +532,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
             L += lbuf[w * RP + r] * f;
             o += obuf[((size_t)w * RP + r) * Dv + dv] * f;
         }
-        const int g = r / a.q_len, qi = r - g * a.q_len;
+        const int g = (row0 + r) / a.q_len, qi = row0 + r - g * a.q_len;
         const int h = kv * p.G + g;
         const int rid = (b * a.num_q_heads + h) * a.q_len + qi;
         if (p.n_splits == 1) {
@@ -553,6 +556,7 @@ int pow2_at_least(int x) {
 
 struct MPlan {
     int RP, DT, split_len, n_splits;
+    int rg, n_groups;  // query rows per row group, row groups
     size_t smem, ws_bytes;
 };
 
@@ -563,18 +567,24 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     if (a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;
     if (a->n_centroids != kNC) return false;
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;  // float4 codeword loads
-    if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32) return false;
+    if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32 && a->n_blocks != 64) return false;
     if (a->head_dim > 256) return false;  // query staging covers at most 256 dims per row
     // code rows: 8-byte (nb 8) or 16-byte (nb >= 16) vector loads
     const int cal = a->n_blocks >= 16 ? 16 : 8;
     if (a->c_st % cal != 0 || a->c_sb % cal != 0 || a->c_sh % cal != 0 || (uintptr_t)a->codes % cal) return false;
     if ((uintptr_t)a->v % 16 || (a->v_sb * 2) % 16 || (a->v_sh * 2) % 16 || (a->v_st * 2) % 16) return false;
+    // Query rows of one (batch, KV head) share a LUT of n_blocks x 256 x RP fp32 (<= 128 KiB).
+    // More rows than one LUT holds split into row groups, each streaming the codes and values
+    // again: twice the bytes at 8 query heads per KV head with 32 blocks, far less than the
+    // LUT-less generic kernel costs.
     const int rows = (a->num_q_heads / a->num_kv_heads) * a->q_len;
-    if (rows > 16) return false;
-    pl.RP = pow2_at_least(rows);
-    if (pl.RP * a->n_blocks > 128) return false;
+    if (rows > 64) return false;
+    const int cap = 128 / a->n_blocks < 16 ? 128 / a->n_blocks : 16;  // a power of two
+    pl.rg = rows < cap ? rows : cap;
+    pl.n_groups = (rows + pl.rg - 1) / pl.rg;
+    pl.RP = pow2_at_least(pl.rg);
     pl.DT = a->value_dim / 16;
-    const int units = a->batch * a->num_kv_heads;
+    const int units = a->batch * a->num_kv_heads * pl.n_groups;
     const int tiles = (a->seq_len + kTileTok - 1) / kTileTok;
     const int cus = ssq_device_cus();  // one workgroup per CU (the LUT fills the LDS)
     int splits = a->num_splits > 0 ? a->num_splits : (cus + units - 1) / units;
@@ -597,7 +607,7 @@ int launch(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
     auto kern = k_decode_mfma<RP, DT, VT, NB>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_mfma)");
     if (rc) return rc;
-    dim3 grid(mp.a.batch * mp.a.num_kv_heads, pl.n_splits);
+    dim3 grid(mp.a.batch * mp.a.num_kv_heads, pl.n_splits, pl.n_groups);
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), pl.smem, st, mp);
     return ssq_check_hip(hipGetLastError(), "k_decode_mfma launch");
 }
@@ -607,7 +617,8 @@ int launch_nb(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
     switch (mp.a.n_blocks) {
         case 8: return launch<RP, DT, VT, 8>(mp, pl, st);
         case 16: if constexpr (RP <= 8) return launch<RP, DT, VT, 16>(mp, pl, st); break;
-        default: if constexpr (RP <= 4) return launch<RP, DT, VT, 32>(mp, pl, st); break;
+        case 32: if constexpr (RP <= 4) return launch<RP, DT, VT, 32>(mp, pl, st); break;
+        default: if constexpr (RP <= 2) return launch<RP, DT, VT, 64>(mp, pl, st); break;
     }
     return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode: LUT of %d rows x %d blocks exceeds LDS", RP, mp.a.n_blocks);
 }
@@ -648,6 +659,7 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
     mp.a = *a;
     mp.G = a->num_q_heads / a->num_kv_heads;
     mp.rows = mp.G * a->q_len;
+    mp.rg = pl.rg;
     mp.split_len = pl.split_len;
     mp.n_splits = pl.n_splits;
     const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;

@@ -156,6 +156,31 @@ def test_config4_paged_small_vs_oracle(kernel):
     _paged_oracle_check(p, np_of(out), np_of(lse), np_of(scores), [(b, kv) for b in range(3) for kv in range(8)])
 
 
+@pytest.mark.parametrize("Hq,bd,lq", [(64, 4, 1), (128, 4, 1), (32, 2, 1), (64, 8, 2), (32, 2, 2)])
+def test_paged_mfma_row_groups_vs_oracle(Hq, bd, lq):
+    """More query rows per KV head than one LUT holds (8 or 16 heads at 32 blocks, 64 blocks of
+    dim 2 at head_dim 128, two query tokens): the MFMA kernel runs row groups, each streaming the
+    pages again.  Outputs, lse and raw scores against the oracle, per (sequence, KV head)."""
+    log(f"paged MFMA row groups Hq={Hq} bd={bd} q_len={lq}")
+    p = synthetic.config4(DEV, B=2, T=1024, Hq=Hq, bd=bd)
+    if lq > 1:
+        g = torch.Generator().manual_seed(9)
+        p.tensors["q"] = torch.randn(2, Hq, lq, 128, generator=g).to(torch.bfloat16).to(DEV)
+    out, lse, scores = hip_ops.decode(p["q"], p["code_pages"], p["v_pages"], p["perm"], p["centroids"],
+                                      scale=p.meta["scale"], block_table=p["block_table"], seq_lens=p["seq_lens"],
+                                      return_lse=True, return_scores=True, kernel=2)
+    o, l, sc = np_of(out), np_of(lse), np_of(scores)
+    if lq == 1:
+        _paged_oracle_check(p, o, l, sc, [(b, kv) for b in range(2) for kv in (0, 3, 7)])
+        return
+    # two query tokens: each is its own row of the kernel's group; check token by token
+    for qi in range(lq):
+        pq = synthetic.Problem(p.name, dict(p.tensors), dict(p.meta))
+        pq.tensors["q"] = p["q"][:, :, qi:qi + 1]
+        _paged_oracle_check(pq, o[:, :, qi:qi + 1], l[:, :, qi:qi + 1], sc[:, :, qi:qi + 1],
+                            [(b, kv) for b in range(2) for kv in (1, 6)])
+
+
 def test_paged_ragged_sequence_lengths():
     log("paged ragged seq_lens")
     p = synthetic.config4(DEV, B=4, T=1024)
