@@ -156,16 +156,18 @@ def test_config4_paged_small_vs_oracle(kernel):
     _paged_oracle_check(p, np_of(out), np_of(lse), np_of(scores), [(b, kv) for b in range(3) for kv in range(8)])
 
 
-@pytest.mark.parametrize("Hq,bd,lq", [(64, 4, 1), (128, 4, 1), (32, 2, 1), (64, 8, 2), (32, 2, 2)])
-def test_paged_mfma_row_groups_vs_oracle(Hq, bd, lq):
+@pytest.mark.parametrize("Hq,bd,lq,D", [(64, 4, 1, 128), (128, 4, 1, 128), (32, 2, 1, 128), (64, 8, 2, 128),
+                                        (32, 2, 2, 128), (128, 4, 2, 128), (64, 2, 1, 64), (64, 8, 1, 256)])
+def test_paged_mfma_row_groups_vs_oracle(Hq, bd, lq, D):
     """More query rows per KV head than one LUT holds (8 or 16 heads at 32 blocks, 64 blocks of
-    dim 2 at head_dim 128, two query tokens): the MFMA kernel runs row groups, each streaming the
-    pages again.  Outputs, lse and raw scores against the oracle, per (sequence, KV head)."""
-    log(f"paged MFMA row groups Hq={Hq} bd={bd} q_len={lq}")
-    p = synthetic.config4(DEV, B=2, T=1024, Hq=Hq, bd=bd)
+    dim 2 at head_dim 128, two query tokens): head_dim 64 and 128 take the MFMA-scores kernel (16
+    rows per pass, row groups beyond), head_dim 256 the LUT kernel in row groups.  Outputs, lse
+    and raw scores against the oracle, per (sequence, KV head)."""
+    log(f"paged MFMA row groups Hq={Hq} bd={bd} q_len={lq} D={D}")
+    p = synthetic.config4(DEV, B=2, T=1024 if D <= 128 else 256, Hq=Hq, bd=bd, D=D)
     if lq > 1:
         g = torch.Generator().manual_seed(9)
-        p.tensors["q"] = torch.randn(2, Hq, lq, 128, generator=g).to(torch.bfloat16).to(DEV)
+        p.tensors["q"] = torch.randn(2, Hq, lq, D, generator=g).to(torch.bfloat16).to(DEV)
     out, lse, scores = hip_ops.decode(p["q"], p["code_pages"], p["v_pages"], p["perm"], p["centroids"],
                                       scale=p.meta["scale"], block_table=p["block_table"], seq_lens=p["seq_lens"],
                                       return_lse=True, return_scores=True, kernel=2)
