@@ -226,3 +226,33 @@ def test_synthetic_configs_shapes():
     # codebook coordinates follow the permuted per-dim sigma
     assert cb.centroids.shape == (2, 32, 256, 2)
     assert math.isclose(float(cb.sigma.min()), 0.1, rel_tol=2.0) and float(cb.sigma.max()) <= 3.0
+
+
+def test_encode_search_grid_applies_only_where_it_is_exact_and_needs_a_device():
+    """The codec's search grid serves block_dim 2 without a block metric; elsewhere (and when
+    disabled) it is None, so the exhaustive encode runs.  Building one needs a device codebook."""
+    g = torch.Generator().manual_seed(3)
+    assert _codec().encode_search_grid(_codec().centroids) is None  # block_dim 8
+    c2 = SunShapeBlockCodec.from_buffers(torch.randperm(64, generator=g), torch.randn(32, 256, 2, generator=g),
+                                         device="cpu")
+    c2.use_encode_grid = False
+    assert c2.encode_search_grid(c2.centroids) is None
+    c2.use_encode_grid = True
+    with pytest.raises(RuntimeError, match="HIP device tensor"):
+        c2.encode_search_grid(c2.centroids)
+    pro = SunShapeBlockCodec.from_buffers(torch.randperm(64, generator=g), torch.randn(32, 256, 2, generator=g),
+                                          mode="profileperm_localmetric_dsq", metric=torch.eye(64), device="cpu")
+    assert pro.encode_search_grid(pro.centroids) is None  # a block metric changes the distances
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus above 1 exits with a message before touching a device."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode != 0
+    assert "one GPU" in (r.stderr + r.stdout)
