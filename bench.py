@@ -10,7 +10,7 @@ Prints ONE JSON line: keys scored/s (B*Hkv*T per step / time), achieved HBM GB/s
 algorithmic bytes and its fraction of the 8 TB/s peak, the kernel's average launch time
 from HIP events on its own stream, and a bounded CPU-oracle baseline timed on the host.
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -37,7 +37,8 @@ def _args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "c4g8", "c4bd2", "copycal"])
+    ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "c4g8", "c4bd2", "c3p6",
+                                                     "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -61,9 +62,10 @@ def _decode_workload(name, dev, kernel):
     from sunshape_amd import hip_ops, synthetic
 
     heavy, pt = None, None
+    nc, code_bits = 256, 0
     if name in ("c4", "c4g8", "c4bd2"):
         # c4g8 / c4bd2: the config-4 layer with 64 query heads (8 per KV head) or at 4 bits/dim
-        # (64 blocks of dim 2); their LUTs exceed the LDS, so the kernel runs two row groups
+        # (64 blocks of dim 2); their LUTs exceed the LDS, so they run the MFMA-scores kernel
         Hq = 64 if name == "c4g8" else 32
         bd = 2 if name == "c4bd2" else 4
         p = synthetic.config4(dev, Hq=Hq, bd=bd)
@@ -79,6 +81,20 @@ def _decode_workload(name, dev, kernel):
         p.tensors["codes"], p.tensors["pt"] = codes5, pt
         p.tensors["perm"] = p["perm"][None].expand(Hkv, D)
         p.meta["T"] = T
+    elif name == "c3p6":
+        # the config-3 layer at 3 bits/dim: 64 codewords per block, 6-bit codes packed five to an
+        # int32 word (the layout sunshape/triton_kernels.py:250-266 reads)
+        B, Hq, Hkv, T, D, bd = 16, 14, 2, 8192, 64, 2
+        nc, code_bits = 64, 6
+        cb = synthetic.make_codebook(Hkv, D, bd, 3, n_centroids=nc)
+        g = torch.Generator().manual_seed(103)
+        q3 = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16).to(dev)
+        c8 = torch.randint(0, nc, (B, Hkv, T, D // bd), generator=g, dtype=torch.uint8).to(dev)
+        v3 = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16).to(dev)
+        p = synthetic.Problem("C3p6", {"q": q3, "codes": hip_ops.pack_codes(c8, code_bits), "codes_u8": c8,
+                                       "v": v3, "perm": cb.perm.to(dev), "centroids": cb.centroids.to(dev)},
+                              {"scale": 1.0 / math.sqrt(D), "B": B, "Hq": Hq, "Hkv": Hkv, "T": T})
+        paged = False
     else:
         p = synthetic.config3(dev)
         B, Hq, Hkv, T, D, bd = 16, 14, 2, 8192, 64, 2
@@ -96,12 +112,13 @@ def _decode_workload(name, dev, kernel):
         ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], block_table=bt, seq_lens=sl, kernel=kernel)
     else:
         codes, v = p["codes"], p["v"]
-        ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], heavy=heavy, pt=pt, kernel=kernel)
+        ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], heavy=heavy, pt=pt, kernel=kernel,
+                             code_bits=code_bits)
     a = N.DecodeArgs(
         q=q.data_ptr(), q_dtype=N.SSQ_BF16, q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
         batch=B, num_q_heads=Hq, q_len=1, head_dim=D, num_kv_heads=Hkv, has_scale=1, scale=p.meta["scale"],
-        perm=perm.data_ptr(), perm_sh=D, cent=cent.data_ptr(), cent_sh=nb * 256 * bd,
-        block_dim=bd, n_blocks=nb, n_centroids=256,
+        perm=perm.data_ptr(), perm_sh=D, cent=cent.data_ptr(), cent_sh=nb * nc * bd,
+        block_dim=bd, n_blocks=nb, n_centroids=nc, code_bits=code_bits,
         layout=N.SSQ_PAGED if paged else N.SSQ_CONTIGUOUS, seq_len=T,
         codes=codes.data_ptr(), c_sb=codes.stride(0), c_sh=codes.stride(1), c_st=codes.stride(2),
         block_table=bt.data_ptr() if paged else None, bt_sb=bt.stride(0) if paged else 0,
@@ -127,11 +144,12 @@ def _decode_workload(name, dev, kernel):
     torch.cuda.synchronize()
     assert torch.equal(out, ref), "timed launch differs from the checked Python-surface launch"
     keys = B * Hkv * T
-    algo_bytes = (B * Hkv * T * nb                 # uint8 codes
+    code_bytes = codes.numel() * codes.element_size() if code_bits else B * Hkv * T * nb
+    algo_bytes = (code_bytes                       # uint8 codes (or packed words)
                   + B * Hkv * T * Dv * 2           # bf16 V
                   + B * Hq * D * 2                 # bf16 q
                   + B * Hq * Dv * 2                # bf16 out
-                  + Hkv * nb * 256 * bd * 4        # fp32 codebooks
+                  + Hkv * nb * nc * bd * 4         # fp32 codebooks
                   + Hkv * D * 8                    # int64 permutations
                   + (B * (T // 16) * 4 if paged else 0)  # int32 block table
                   + (pt.numel() * 2 if pt is not None else 0))  # bf16 passthrough values
@@ -139,10 +157,13 @@ def _decode_workload(name, dev, kernel):
                         "c4g8": "C4 layer with 64 query heads (8 per KV head), paged, 2 bits/dim",
                         "c4bd2": "C4 layer at 4 bits/dim (64 blocks of dim 2), paged",
                         "c3": "C3 contiguous fused decode (Qwen2.5-0.5B layer, 4 bits/dim)",
-                        "c5": "C5 SunShape-Mixed fused decode (config-5 keys: 28 VQ + 4 bf16 blocks of dim 2)"}[name],
+                        "c5": "C5 SunShape-Mixed fused decode (config-5 keys: 28 VQ + 4 bf16 blocks of dim 2)",
+                        "c3p6": "C3 layer at 3 bits/dim: 64 codewords, 6-bit codes packed in int32 words"}[name],
            "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "context": T, "block_dim": bd,
-           "bits_per_dim": 8 / bd, "n_centroids": 256, "layout": "paged16" if paged else "contiguous",
-           "kernel": kernel}
+           "bits_per_dim": (code_bits or 8) / bd, "n_centroids": nc,
+           "layout": "paged16" if paged else "contiguous", "kernel": kernel}
+    if code_bits:
+        cfg["code_bits"] = code_bits
     unit_data = (p, paged)
     return step, keys, algo_bytes, cfg, unit_data, "ssq_decode"
 
@@ -336,7 +357,7 @@ def _cpu_baseline(unit_data, seconds):
                 codes = p["code_pages"][pages][:, kv].reshape(-1, p["code_pages"].shape[-1]).cpu().numpy()
                 v = p["v_pages"][pages][:, kv].permute(0, 2, 1).reshape(-1, p["v_pages"].shape[2]).float().cpu().numpy()
             else:
-                codes = p["codes"][b, kv].cpu().numpy()
+                codes = p.tensors.get("codes_u8", p["codes"])[b, kv].cpu().numpy()  # unpacked for the oracle
                 v = p["v"][b, kv].float().cpu().numpy()
             hv, ptv = None, None
             if "pt" in p.tensors:  # SunShape-Mixed: dense passthrough values for the oracle
@@ -364,7 +385,7 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2"):
+    if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2", "c3p6"):
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
         step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev)

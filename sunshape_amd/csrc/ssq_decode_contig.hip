@@ -15,6 +15,10 @@
 //            addresses V[t0 + l/4][n0 + 4*(l%4) .. +3] and receives V[t0 .. t0+3][n0 + l], so two
 //            reads give a lane its 8 consecutive tokens of one dim.
 //
+// Codes arrive as byte rows or as 4- / 6-bit codes packed into int32 words
+// (sunshape/triton_kernels.py:250-266); packed rows are loaded as words and unpacked to bytes when
+// the tile is copied to LDS, so the score loop is the same for both.
+//
 // workgroup = 4 waves for one (batch, KV head, context split); each wave streams 64-token tiles with
 // its own running (max, sum, O), the next tile's loads in flight; waves merge through LDS at the end.
 #include "ssq_common.h"
@@ -107,22 +111,27 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// packed code rows (PB bits per code, 32 / PB codes per little-endian int32 word, the low bits
+// first; sunshape/triton_kernels.py:250-266): int32 words per row
+__host__ __device__ constexpr int pk_words(int NB, int PB) { return PB ? (NB + 32 / PB - 1) / (32 / PB) : 1; }
+
 // registers of one 64-token tile in flight: this lane's 16-byte V chunks, its token's code row
-// and (heavy blocks) its token's passthrough values
-template <int NB, int DT, bool HV, bool MK>
+// (bytes, or PB-bit codes in words) and (heavy blocks) its token's passthrough values
+template <int NB, int DT, bool HV, bool MK, int PB>
 struct Tile {
     uint4 v[2 * DT];
     uint4 c[NB >= 16 ? NB / 16 : 1];
     uint2 c8;
+    uint32_t pk[pk_words(NB, PB)];
     uint32_t h[HV ? kHP : 1];  // raw bits (ssq_load_bits); converted when the tile goes to LDS
     float mk[MK ? 16 : 1];     // additive mask at [row 4*lg + i][token 16g + l16], index 4g + i
 };
 
 // Loads are unconditional; chunks of tokens past the split's end re-read the last token's row
 // (valid memory; such tokens get p = 0 and are never scored).
-template <int NB, int DT, bool HAS_V, bool HV, bool MK>
+template <int NB, int DT, bool HAS_V, bool HV, bool MK, int PB>
 __device__ __forceinline__ void issue_tile(const ContigParams& p, int b, int kv, int t0, int t_end, int lane,
-                                           Tile<NB, DT, HV, MK>& R) {
+                                           Tile<NB, DT, HV, MK, PB>& R) {
     const ssq_decode_args& a = p.a;
     const int tc = min(t0 + lane, t_end - 1);
     if constexpr (MK) {  // clamped offsets; entries of invalid (row, token) pairs are never added
@@ -145,11 +154,17 @@ __device__ __forceinline__ void issue_tile(const ContigParams& p, int b, int kv,
 #pragma unroll
         for (int i = 0; i < kHP; ++i) R.h[i] = ssq_load_bits(a.pt, a.pt_dtype, pb + p.hoff[i]);  // hoff clamped
     }
-    const uint8_t* crow = a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st;
-    if constexpr (NB >= 16) {
+    if constexpr (PB) {  // packed rows: strides count int32 words
+        const uint32_t* prow = reinterpret_cast<const uint32_t*>(a.codes) + (int64_t)b * a.c_sb +
+                               (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st;
+#pragma unroll
+        for (int i = 0; i < pk_words(NB, PB); ++i) R.pk[i] = __builtin_nontemporal_load(prow + i);
+    } else if constexpr (NB >= 16) {
+        const uint8_t* crow = a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st;
 #pragma unroll
         for (int i = 0; i < NB / 16; ++i) R.c[i] = ld16(crow + 16 * i);
     } else {
+        const uint8_t* crow = a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st;
         R.c8 = *reinterpret_cast<const uint2*>(crow);
     }
     if constexpr (HAS_V) {
@@ -168,7 +183,7 @@ __device__ __forceinline__ void issue_tile(const ContigParams& p, int b, int kv,
 // mask or 128-dim values fit; the others keep 4 waves
 __host__ __device__ constexpr bool contig_wide(int dt, bool hv, bool mk) { return !hv && !mk && dt <= 4; }
 
-template <int BD, int DT, int VT, bool HAS_V, bool HV, bool MK>
+template <int BD, int DT, int VT, bool HAS_V, bool HV, bool MK, int PB>
 __global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 * SSQ_WAVE) void k_decode_contig(
     const ContigParams p) {
     constexpr int NB = kD / BD;
@@ -215,10 +230,10 @@ __global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 
 
     const int n_tiles = (t_end - t_begin + kTile - 1) / kTile;
     const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
-    Tile<NB, DT, HV, MK> ra, rb;
+    Tile<NB, DT, HV, MK, PB> ra, rb;
     if (n_tiles > 0) {
-        issue_tile<NB, DT, HAS_V, HV, MK>(p, b, kv, t_begin + min(wave, last_tile) * kTile, t_end, lane, ra);
-        issue_tile<NB, DT, HAS_V, HV, MK>(p, b, kv, t_begin + min(wave + W, last_tile) * kTile, t_end, lane, rb);
+        issue_tile<NB, DT, HAS_V, HV, MK, PB>(p, b, kv, t_begin + min(wave, last_tile) * kTile, t_end, lane, ra);
+        issue_tile<NB, DT, HAS_V, HV, MK, PB>(p, b, kv, t_begin + min(wave + W, last_tile) * kTile, t_end, lane, rb);
     }
 
     // the codebook goes global -> LDS directly (no registers): 1 KB chunks, lane l's 16 bytes at
@@ -288,10 +303,26 @@ __global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 
     for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
 
     // one tile: its registers -> the wave's LDS region, the set reloaded two rounds ahead, compute
-    auto step = [&](Tile<NB, DT, HV, MK>& R, int tile) {
+    auto step = [&](Tile<NB, DT, HV, MK, PB>& R, int tile) {
         const int t0 = t_begin + tile * kTile;
         wave_sync();
-        if constexpr (NB >= 16) {
+        if constexpr (PB) {  // unpack to one byte per code: the score loop reads byte rows either way
+            constexpr int kVpe = 32 / PB;
+            constexpr uint32_t kMsk = (1u << PB) - 1u;
+            uint32_t u[NB / 4];
+#pragma unroll
+            for (int j = 0; j < NB / 4; ++j) u[j] = 0u;
+#pragma unroll
+            for (int i = 0; i < NB; ++i) u[i >> 2] |= ((R.pk[i / kVpe] >> ((i % kVpe) * PB)) & kMsk) << (8 * (i & 3));
+            if constexpr (NB >= 16) {
+#pragma unroll
+                for (int i = 0; i < NB / 16; ++i)
+                    *reinterpret_cast<uint4*>(ct + lane * NB + 16 * i) =
+                        make_uint4(u[4 * i], u[4 * i + 1], u[4 * i + 2], u[4 * i + 3]);
+            } else {
+                *reinterpret_cast<uint2*>(ct + lane * NB) = make_uint2(u[0], u[1]);
+            }
+        } else if constexpr (NB >= 16) {
 #pragma unroll
             for (int i = 0; i < NB / 16; ++i) *reinterpret_cast<uint4*>(ct + lane * NB + 16 * i) = R.c[i];
         } else {
@@ -314,7 +345,7 @@ __global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 
         float mk[MK ? 16 : 1];  // this tile's mask values, taken before R is reloaded
 #pragma unroll
         for (int k = 0; k < (MK ? 16 : 1); ++k) mk[k] = MK ? R.mk[k] : 0.f;
-        issue_tile<NB, DT, HAS_V, HV, MK>(p, b, kv, t_begin + min(tile + 2 * W, last_tile) * kTile, t_end, lane, R);
+        issue_tile<NB, DT, HAS_V, HV, MK, PB>(p, b, kv, t_begin + min(tile + 2 * W, last_tile) * kTile, t_end, lane, R);
 
         // ---- scores: S[row 4*lg+i][token 16g + l16] for the tile's 4 groups of 16 tokens
         v4f sc[4];
@@ -486,7 +517,12 @@ struct CPlan {
 };
 
 bool plan(const ssq_decode_args* a, bool has_v, CPlan& pl) {
-    if (a->layout != SSQ_CONTIGUOUS || a->code_bits != 0) return false;
+    if (a->layout != SSQ_CONTIGUOUS) return false;
+    // packed codes: 4- and 6-bit words are unpacked in the kernel (without passthrough or mask);
+    // 8-bit words are byte rows (strides scaled to bytes); other widths take the generic kernel
+    const int cbits = a->code_bits;
+    if (cbits != 0 && cbits != 4 && cbits != 6 && cbits != 8) return false;
+    if ((cbits == 4 || cbits == 6) && (a->heavy_mask[0] || a->mask)) return false;
     if (a->heavy_mask[1]) return false;
     if (a->heavy_mask[0]) {
         const int n_hd = __builtin_popcountll(a->heavy_mask[0]) * a->block_dim;
@@ -500,8 +536,14 @@ bool plan(const ssq_decode_args* a, bool has_v, CPlan& pl) {
     if (rows > 16) return false;
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;
     const int nb = a->n_blocks;
-    const int cal = nb >= 16 ? 16 : 8;  // code row loads of 16 (or 8) bytes
-    if ((uintptr_t)a->codes % cal || a->c_st % cal || a->c_sh % cal || a->c_sb % cal) return false;
+    if (cbits == 4 || cbits == 6) {  // word loads
+        if ((uintptr_t)a->codes % 4) return false;
+    } else {
+        const int cal = nb >= 16 ? 16 : 8;  // code row loads of 16 (or 8) bytes
+        const int64_t cs = cbits == 8 ? 4 : 1;  // stride unit in bytes
+        if ((uintptr_t)a->codes % cal || (a->c_st * cs) % cal || (a->c_sh * cs) % cal || (a->c_sb * cs) % cal)
+            return false;
+    }
     pl.DT = 4;
     if (has_v) {
         if (a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16) return false;
@@ -531,9 +573,9 @@ bool plan(const ssq_decode_args* a, bool has_v, CPlan& pl) {
     return true;
 }
 
-template <int BD, int DT, int VT, bool HAS_V, bool HV, bool MK>
+template <int BD, int DT, int VT, bool HAS_V, bool HV, bool MK, int PB>
 int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
-    auto kern = k_decode_contig<BD, DT, VT, HAS_V, HV, MK>;
+    auto kern = k_decode_contig<BD, DT, VT, HAS_V, HV, MK, PB>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_contig)");
     if (rc) return rc;
     dim3 grid(cp.a.batch * cp.a.num_kv_heads, pl.n_splits);
@@ -541,13 +583,13 @@ int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     return ssq_check_hip(hipGetLastError(), "k_decode_contig launch");
 }
 
-template <int DT, int VT, bool HAS_V, bool HV, bool MK>
+template <int DT, int VT, bool HAS_V, bool HV, bool MK, int PB = 0>
 int launch_bd(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     switch (cp.a.block_dim) {
-        case 1: return launch<1, DT, VT, HAS_V, HV, MK>(cp, pl, st);
-        case 2: return launch<2, DT, VT, HAS_V, HV, MK>(cp, pl, st);
-        case 4: return launch<4, DT, VT, HAS_V, HV, MK>(cp, pl, st);
-        default: return launch<8, DT, VT, HAS_V, HV, MK>(cp, pl, st);
+        case 1: return launch<1, DT, VT, HAS_V, HV, MK, PB>(cp, pl, st);
+        case 2: return launch<2, DT, VT, HAS_V, HV, MK, PB>(cp, pl, st);
+        case 4: return launch<4, DT, VT, HAS_V, HV, MK, PB>(cp, pl, st);
+        default: return launch<8, DT, VT, HAS_V, HV, MK, PB>(cp, pl, st);
     }
 }
 template <int DT, int VT, bool HAS_V, bool HV>
@@ -556,6 +598,8 @@ int launch_mk(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
 }
 template <int DT, int VT, bool HAS_V>
 int launch_hv(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
+    if (cp.a.code_bits == 4) return launch_bd<DT, VT, HAS_V, false, false, 4>(cp, pl, st);
+    if (cp.a.code_bits == 6) return launch_bd<DT, VT, HAS_V, false, false, 6>(cp, pl, st);
     return cp.n_hd > 0 ? launch_mk<DT, VT, HAS_V, true>(cp, pl, st) : launch_mk<DT, VT, HAS_V, false>(cp, pl, st);
 }
 
@@ -584,6 +628,10 @@ int ssq_decode_contig(const ssq_decode_args* a, void* workspace, size_t ws_bytes
     SSQ_REQUIRE(pl.ws_bytes == 0 || workspace, "workspace is NULL");
     ContigParams cp;
     cp.a = *a;
+    if (a->code_bits == 8) {  // 8-bit words are the byte rows: byte strides, the byte-code path
+        cp.a.c_sb *= 4; cp.a.c_sh *= 4; cp.a.c_st *= 4;
+        cp.a.code_bits = 0;
+    }
     cp.G = a->num_q_heads / a->num_kv_heads;
     cp.rows = cp.G * a->q_len;
     cp.split_len = pl.split_len;

@@ -66,7 +66,8 @@ def test_decode_over_packed_codes_equals_uint8(paged):
         c8 = codes.to(DEV)
         w = hip_ops.pack_codes(c8, 6)
         o8, l8 = hip_ops.decode(q.to(DEV), c8, v.to(DEV), perm, cent, scale=scale, return_lse=True, kernel=1)
-        o6, l6 = hip_ops.decode(q.to(DEV), w, v.to(DEV), perm, cent, scale=scale, return_lse=True, code_bits=6)
+        o6, l6 = hip_ops.decode(q.to(DEV), w, v.to(DEV), perm, cent, scale=scale, return_lse=True, code_bits=6,
+                                kernel=1)
     else:
         page = 16
         n = T // page
@@ -88,3 +89,30 @@ def test_decode_over_packed_codes_equals_uint8(paged):
     ref = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
                              cb.perm.numpy(), scale, "bf16", "bf16")
     assert_rel(np_of(o6), ref, BF16_TOL, "packed decode vs oracle")
+
+
+@pytest.mark.parametrize("bits,bd,nc,Hq,T", [(6, 2, 64, 14, 700), (4, 2, 16, 8, 640), (6, 1, 64, 4, 333),
+                                             (4, 4, 16, 16, 1000), (6, 8, 64, 2, 129), (8, 2, 256, 14, 700)])
+def test_contig_mfma_decode_over_packed_codes_equals_uint8(bits, bd, nc, Hq, T):
+    """The contiguous MFMA kernel unpacks 4- and 6-bit words when the tile goes to LDS (8-bit words
+    are read as byte rows): output, LSE and raw scores equal its own uint8-code launch bit for bit."""
+    log(f"packed contig decode bits={bits} bd={bd} nc={nc} Hq={Hq} T={T}")
+    cb, codes, q, v = _case(nc=nc, bd=bd, Hq=Hq, T=T, seed=40 + bits + bd)
+    perm, cent = cb.perm.to(DEV), cb.centroids.to(DEV)
+    scale = 1 / math.sqrt(64)
+    c8 = codes.to(DEV)
+    w = hip_ops.pack_codes(c8, bits)
+    qd, vd = q.to(DEV), v.to(DEV)
+    o8, l8, s8 = hip_ops.decode(qd, c8, vd, perm, cent, scale=scale, return_lse=True, return_scores=True, kernel=3)
+    o6, l6, s6 = hip_ops.decode(qd, w, vd, perm, cent, scale=scale, return_lse=True, return_scores=True,
+                                code_bits=bits, kernel=3)
+    assert torch.equal(o8, o6) and torch.equal(l8, l6) and torch.equal(s8, s6)
+    # the default choice takes the same kernel; the scores-only launch reads packed words too
+    assert torch.equal(hip_ops.decode(qd, w, vd, perm, cent, scale=scale, code_bits=bits), o6)
+    g8 = hip_ops.gqa_scores(qd, c8, perm, cent, scale=scale, kernel=3)
+    assert torch.equal(hip_ops.gqa_scores(qd, w, perm, cent, scale=scale, code_bits=bits, kernel=3), g8)
+    assert torch.equal(g8, s8)
+    ref, ref_s, _ = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
+                                       cb.perm.numpy(), scale, "bf16", "bf16", return_scores=True)
+    assert_rel(np_of(o6), ref, BF16_TOL, "packed contig decode vs oracle")
+    assert_rel(np_of(s6), ref_s, SCORE_TOL, "packed contig scores vs oracle")
