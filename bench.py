@@ -8,7 +8,8 @@ batch with inputs resident in HBM.
 
 Prints ONE JSON line: keys scored/s (B*Hkv*T per step / time), achieved HBM GB/s on the
 algorithmic bytes and its fraction of the 8 TB/s peak, the kernel's average launch time
-from HIP events on its own stream, and a bounded CPU-oracle baseline timed on the host.
+from HIP events on its own stream, the same launch's time with cold caches (a 1 GiB flush
+before each), and a bounded CPU-oracle baseline timed on the host.
 
   python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6] [--no-cpu]
 """
@@ -42,6 +43,8 @@ def _args():
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cold-steps", type=int, default=20,
+                    help="extra launches timed after a cache flush each (0 skips them)")
     return ap.parse_args()
 
 
@@ -376,6 +379,29 @@ def _cpu_baseline(unit_data, seconds):
                       f"softmax, bf16 cast, P.V), single thread, {elapsed:.1f} s"}
 
 
+def _cold_launches(step, n, algo_bytes, dev):
+    """The same launch with cold caches: before each event-timed launch, a 1 GiB read-modify-write
+    pass (stream-ordered before it) evicts the inputs from L2 and the 256 MB Infinity Cache, so every
+    input byte comes from HBM.  The main timed loop is warm: a workload smaller than the Infinity
+    Cache (configs 2, 3, 5) can be served from it on repeated launches."""
+    import torch
+
+    flush = torch.zeros(1 << 28, device=dev, dtype=torch.int32)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    for i in range(n):
+        flush.add_(1)
+        starts[i].record()
+        step()
+        ends[i].record()
+    torch.cuda.synchronize()
+    ms = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    med = ms[len(ms) // 2]
+    del flush
+    return {"launches": n, "kernel_median_ms": med, "kernel_min_ms": ms[0],
+            "hbm_GBps": algo_bytes / (med * 1e-3) / 1e9, "flush_bytes": 1 << 30}
+
+
 # ----------------------------------------------------------------------------- main
 def main():
     args = _args()
@@ -454,6 +480,8 @@ def main():
             line["roofline"] = {"bound": "mfma", "achieved": tf, "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
                                 "frac": tf / MFMA_F32_PEAK_TFLOPS, "traffic": traffic, "kernel": kname,
                                 "algorithmic_flop_per_launch": flop}
+    if args.workload != "copycal" and args.cold_steps > 0:
+        line["cold"] = _cold_launches(step, args.cold_steps, algo_bytes, dev)
     if not args.no_cpu and unit_data is not None:
         line["cpu_baseline"] = _cpu_baseline(unit_data, args.cpu_seconds)
     else:
