@@ -11,7 +11,7 @@ algorithmic bytes and its fraction of the 8 TB/s peak, the kernel's average laun
 from HIP events on its own stream, the same launch's time with cold caches (a 1 GiB flush
 before each), and a bounded CPU-oracle baseline timed on the host.
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -39,7 +39,7 @@ def _args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "c4g8", "c4bd2", "c3p6",
-                                                     "copycal"])
+                                                     "c4p6", "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -66,12 +66,18 @@ def _decode_workload(name, dev, kernel):
 
     heavy, pt = None, None
     nc, code_bits = 256, 0
-    if name in ("c4", "c4g8", "c4bd2"):
+    if name in ("c4", "c4g8", "c4bd2", "c4p6"):
         # c4g8 / c4bd2: the config-4 layer with 64 query heads (8 per KV head) or at 4 bits/dim
-        # (64 blocks of dim 2); their LUTs exceed the LDS, so they run the MFMA-scores kernel
+        # (64 blocks of dim 2); their LUTs exceed the LDS, so they run the MFMA-scores kernel.
+        # c4p6: the layer at 3 bits/dim (64 blocks of dim 2, 64 codewords), 6-bit codes packed
+        # five to an int32 word in the pages
         Hq = 64 if name == "c4g8" else 32
-        bd = 2 if name == "c4bd2" else 4
-        p = synthetic.config4(dev, Hq=Hq, bd=bd)
+        bd = 2 if name in ("c4bd2", "c4p6") else 4
+        if name == "c4p6":
+            nc, code_bits = 64, 6
+        p = synthetic.config4(dev, Hq=Hq, bd=bd, n_centroids=nc)
+        if code_bits:
+            p.tensors["code_words"] = hip_ops.pack_codes(p["code_pages"], code_bits)
         B, Hkv, T, D = 64, 8, 32768, 128
         paged = True
     elif name == "c5":
@@ -110,9 +116,10 @@ def _decode_workload(name, dev, kernel):
     perm, cent = p["perm"].contiguous(), p["centroids"].contiguous()
     q = p["q"]
     if paged:
-        codes, v = p["code_pages"], p["v_pages"]
+        codes, v = p.tensors.get("code_words", p["code_pages"]), p["v_pages"]
         bt, sl = p["block_table"], p["seq_lens"]
-        ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], block_table=bt, seq_lens=sl, kernel=kernel)
+        ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], block_table=bt, seq_lens=sl, kernel=kernel,
+                             code_bits=code_bits)
     else:
         codes, v = p["codes"], p["v"]
         ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], heavy=heavy, pt=pt, kernel=kernel,
@@ -159,6 +166,7 @@ def _decode_workload(name, dev, kernel):
     cfg = {"workload": {"c4": "C4 paged fused decode (Llama-3-8B layer, 2 bits/dim)",
                         "c4g8": "C4 layer with 64 query heads (8 per KV head), paged, 2 bits/dim",
                         "c4bd2": "C4 layer at 4 bits/dim (64 blocks of dim 2), paged",
+                        "c4p6": "C4 layer at 3 bits/dim: 64 codewords, 6-bit codes packed in int32 words, paged",
                         "c3": "C3 contiguous fused decode (Qwen2.5-0.5B layer, 4 bits/dim)",
                         "c5": "C5 SunShape-Mixed fused decode (config-5 keys: 28 VQ + 4 bf16 blocks of dim 2)",
                         "c3p6": "C3 layer at 3 bits/dim: 64 codewords, 6-bit codes packed in int32 words"}[name],
@@ -411,7 +419,7 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2", "c3p6"):
+    if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2", "c3p6", "c4p6"):
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
         step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev)

@@ -119,17 +119,24 @@ __device__ __forceinline__ uint4 load_stream(const uint16_t* p) {
 #endif
 }
 
+// packed code rows (PB bits per code, 32 / PB codes per little-endian int32 word, the low bits
+// first; sunshape/triton_kernels.py:250-266): int32 words per row
+__host__ __device__ constexpr int pk_words(int NB, int PB) { return PB ? (NB + 32 / PB - 1) / (32 / PB) : 1; }
+
 // registers of one 64-token tile in flight
-template <int NB, int DT>
+template <int NB, int DT, int PB = 0>
 struct TileRegs {
     uint4 c[NB / 16 > 0 ? NB / 16 : 1];  // this lane's token codes (NB bytes)
     uint2 c8;                            // NB == 8
+    uint32_t pk[pk_words(NB, PB)];       // PB-bit codes in words (PB > 0)
     uint4 v[2][DT];                      // B-operand V fragments of the two 32-token K groups
 };
 
-template <int NB, int DT>
+// cbase: the KV head's codes (bytes; with PB > 0 int32 words, strides counting words)
+template <int NB, int DT, int PB = 0>
 __device__ __forceinline__ void issue_tile(const ssq_decode_args& a, const int* pages, int t_begin, int t_end, int tile,
-                                           int lane, const uint8_t* cbase, const uint16_t* vbase, TileRegs<NB, DT>& R) {
+                                           int lane, const uint8_t* cbase, const uint16_t* vbase,
+                                           TileRegs<NB, DT, PB>& R) {
     // Every load is issued unconditionally (straight-line code keeps the compiler's vmcnt
     // bookkeeping exact, so waiting for this tile never drains the next one).  Lanes past the
     // split's end read their split's last token / 8-token chunk instead: a valid address whose
@@ -139,7 +146,12 @@ __device__ __forceinline__ void issue_tile(const ssq_decode_args& a, const int* 
     const int tr = min(rel + lane, last);
     const int page = pages[tr >> 4];
     const uint8_t* crow = cbase + (int64_t)page * a.c_sb + (int64_t)((t_begin + tr) & 15) * a.c_st;
-    if (NB >= 16) {
+    if constexpr (PB > 0) {
+        const uint32_t* prow = reinterpret_cast<const uint32_t*>(cbase) + (int64_t)page * a.c_sb +
+                               (int64_t)((t_begin + tr) & 15) * a.c_st;
+#pragma unroll
+        for (int i = 0; i < pk_words(NB, PB); ++i) R.pk[i] = __builtin_nontemporal_load(prow + i);
+    } else if (NB >= 16) {
 #pragma unroll
         for (int i = 0; i < NB / 16; ++i) {
 #if SSQ_CODES_NT
@@ -550,12 +562,14 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
 
 // ---------------------------------------------------------------------------
 // k_decode_paged_mx: the same paged decode with the scores on the matrix cores, for shapes whose
-// LUT would need row groups (more query rows per KV head than a LUT of <= 128 KiB holds).
+// LUT would need row groups (more query rows per KV head than a LUT of <= 128 KiB holds), whose
+// codebook has fewer than 256 codewords, or whose codes are 4- / 6-bit words (PB; unpacked to
+// bytes as the tile's codes are copied to LDS).
 //
 //   scores = v_mfma_f32_16x16x4f32 over Qp [16 rows x KD] . K_hat^T: the permuted, scaled query
 //            rows are a fixed A operand in registers; each lane gathers its B element
-//            K_hat[token][dim] = C[blk][code][d] from the codebook staged in LDS (KD x 256 fp32,
-//            128 KiB at head_dim 128 whatever the block size).  No LUT, so up to 16 query rows
+//            K_hat[token][dim] = C[blk][code][d] from the codebook staged in LDS (KD x nc fp32,
+//            128 KiB at head_dim 128 and 256 codewords, whatever the block size).  No LUT, so up to 16 query rows
 //            share one pass over the pages.  fp32 products and sums in MFMA order, so scores
 //            match the LUT kernels within fp32 rounding.
 //   P.V    = as k_decode_mfma: P through a per-wave LDS strip, V fragments straight from the page.
@@ -588,7 +602,7 @@ __device__ __forceinline__ float row_sum16(float v) {
     return v;
 }
 
-template <int KD, int BD, int DT, int VT>
+template <int KD, int BD, int DT, int VT, int PB>
 __global__ __launch_bounds__(kThreads) void k_decode_paged_mx(const MfmaParams p) {
     constexpr int NB = KD / BD;
     constexpr int NBW = NB / 4;  // code row dwords
@@ -663,13 +677,15 @@ __global__ __launch_bounds__(kThreads) void k_decode_paged_mx(const MfmaParams p
     __syncthreads();  // every wave has its A operand: the per-wave regions are free
 
     const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)kv * a.v_sh + (int64_t)(lane & 15) * a.v_st;
-    const uint8_t* cbase = a.codes + (int64_t)kv * a.c_sh;
+    const uint8_t* cbase = PB > 0 ? reinterpret_cast<const uint8_t*>(reinterpret_cast<const uint32_t*>(a.codes) +
+                                                                     (int64_t)kv * a.c_sh)
+                                  : a.codes + (int64_t)kv * a.c_sh;
     const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
     const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
-    TileRegs<NB, DT> RA, RB;
+    TileRegs<NB, DT, PB> RA, RB;
     if (n_tiles > 0) {
-        issue_tile<NB, DT>(a, pages, t_begin, t_end, min(wave, last_tile), lane, cbase, vbase, RA);
-        issue_tile<NB, DT>(a, pages, t_begin, t_end, min(wave + kWaves, last_tile), lane, cbase, vbase, RB);
+        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(wave, last_tile), lane, cbase, vbase, RA);
+        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(wave + kWaves, last_tile), lane, cbase, vbase, RB);
     }
     // the codebook goes global -> LDS directly: 1 KB chunks, lane l's 16 bytes at chunk + 16 l;
     // the tail chunk's lanes past the end re-read the last float4 into the padding
@@ -700,12 +716,28 @@ __global__ __launch_bounds__(kThreads) void k_decode_paged_mx(const MfmaParams p
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-    auto step = [&](TileRegs<NB, DT>& R, int tile) {
+    auto step = [&](TileRegs<NB, DT, PB>& R, int tile) {
         const int t0 = t_begin + tile * kTileTok;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if constexpr (NB >= 16) {
+        if constexpr (PB > 0) {  // unpack to one byte per code: the score loop reads byte rows either way
+            constexpr int kVpe = 32 / PB;
+            constexpr uint32_t kMsk = (1u << PB) - 1u;
+            uint32_t u[NB / 4];
+#pragma unroll
+            for (int j = 0; j < NB / 4; ++j) u[j] = 0u;
+#pragma unroll
+            for (int i = 0; i < NB; ++i) u[i >> 2] |= ((R.pk[i / kVpe] >> ((i % kVpe) * PB)) & kMsk) << (8 * (i & 3));
+            if constexpr (NB >= 16) {
+#pragma unroll
+                for (int i = 0; i < NB / 16; ++i)
+                    *reinterpret_cast<uint4*>(ct + lane * NB + 16 * i) =
+                        make_uint4(u[4 * i], u[4 * i + 1], u[4 * i + 2], u[4 * i + 3]);
+            } else {
+                *reinterpret_cast<uint2*>(ct + lane * NB) = make_uint2(u[0], u[1]);
+            }
+        } else if constexpr (NB >= 16) {
 #pragma unroll
             for (int i = 0; i < NB / 16; ++i) *reinterpret_cast<uint4*>(ct + lane * NB + 16 * i) = R.c[i];
         } else {
@@ -809,7 +841,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_paged_mx(const MfmaParams p
             for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma<VT>(af, R.v[g][dt], acc[dt]);
         }
         // this set is consumed: load the tile two rounds ahead into it
-        issue_tile<NB, DT>(a, pages, t_begin, t_end, min(tile + 2 * kWaves, last_tile), lane, cbase, vbase, R);
+        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + 2 * kWaves, last_tile), lane, cbase, vbase, R);
     };
     // two steps per trip and a single exit (a break between the steps would let the loop-head
     // waits drain both register sets); a step past the last tile sees only tokens past the end
@@ -888,17 +920,29 @@ bool mx_shape(const ssq_decode_args* a) {
 }
 
 bool plan(const ssq_decode_args* a, MPlan& pl) {
-    if (a->layout != SSQ_PAGED || a->page_size != kPage || a->code_bits != 0) return false;
+    if (a->layout != SSQ_PAGED || a->page_size != kPage) return false;
+    // Codes: bytes, 8-bit words (the byte rows, strides scaled to bytes), or 4- / 6-bit words,
+    // which the MFMA-scores kernel unpacks; so does a codebook of fewer than 256 codewords (the
+    // LUT kernel's table is laid out for 256).  Other widths take the generic kernel.
+    const int cbits = a->code_bits;
+    if (cbits != 0 && cbits != 4 && cbits != 6 && cbits != 8) return false;
+    const bool need_mx = cbits == 4 || cbits == 6 || a->n_centroids != kNC;
+    if (need_mx && !mx_shape(a)) return false;
+    if (a->n_centroids > kNC) return false;
     if (a->v == nullptr || (a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16)) return false;
     if (a->mask != nullptr || a->heavy_mask[0] || a->heavy_mask[1]) return false;
     if (a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;
-    if (a->n_centroids != kNC) return false;
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;  // float4 codeword loads
     if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32 && a->n_blocks != 64) return false;
     if (a->head_dim > 256) return false;  // query staging covers at most 256 dims per row
-    // code rows: 8-byte (nb 8) or 16-byte (nb >= 16) vector loads
-    const int cal = a->n_blocks >= 16 ? 16 : 8;
-    if (a->c_st % cal != 0 || a->c_sb % cal != 0 || a->c_sh % cal != 0 || (uintptr_t)a->codes % cal) return false;
+    if (cbits == 4 || cbits == 6) {  // word loads
+        if ((uintptr_t)a->codes % 4) return false;
+    } else {  // code rows: 8-byte (nb 8) or 16-byte (nb >= 16) vector loads
+        const int cal = a->n_blocks >= 16 ? 16 : 8;
+        const int64_t cs = cbits == 8 ? 4 : 1;  // stride unit in bytes
+        if ((a->c_st * cs) % cal || (a->c_sb * cs) % cal || (a->c_sh * cs) % cal || (uintptr_t)a->codes % cal)
+            return false;
+    }
     if ((uintptr_t)a->v % 16 || (a->v_sb * 2) % 16 || (a->v_sh * 2) % 16 || (a->v_st * 2) % 16) return false;
     // Query rows of one (batch, KV head) share a LUT of n_blocks x 256 x RP fp32 (<= 128 KiB).
     // More rows than one LUT holds split into row groups, each streaming the codes and values
@@ -912,7 +956,7 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     pl.RP = pow2_at_least(pl.rg);
     // Where the LUT needs row groups, the MFMA-scores kernel serves up to 16 rows per pass over
     // the pages instead (its codebook is head_dim x 256 fp32 whatever the block size)
-    pl.mx = pl.n_groups > 1 && mx_shape(a);
+    pl.mx = need_mx || (pl.n_groups > 1 && mx_shape(a));
     if (pl.mx) {
         pl.rg = rows < 16 ? rows : 16;
         pl.n_groups = (rows + 15) / 16;
@@ -943,30 +987,38 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     return true;
 }
 
-template <int KD, int BD, int DT, int VT>
+template <int KD, int BD, int DT, int VT, int PB>
 int launch_mx(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
-    auto kern = k_decode_paged_mx<KD, BD, DT, VT>;
+    auto kern = k_decode_paged_mx<KD, BD, DT, VT, PB>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_paged_mx)");
     if (rc) return rc;
     dim3 grid(mp.a.batch * mp.a.num_kv_heads, pl.n_splits, pl.n_groups);
     hipLaunchKernelGGL(kern, grid, dim3(kThreads), pl.smem, st, mp);
     return ssq_check_hip(hipGetLastError(), "k_decode_paged_mx launch");
 }
-template <int KD, int DT, int VT>
+template <int KD, int DT, int VT, int PB>
 int launch_mx_bd(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
     switch (mp.a.block_dim) {
-        case 1: if constexpr (KD <= 64) return launch_mx<KD, 1, DT, VT>(mp, pl, st); break;
-        case 2: return launch_mx<KD, 2, DT, VT>(mp, pl, st);
-        case 4: return launch_mx<KD, 4, DT, VT>(mp, pl, st);
-        default: return launch_mx<KD, 8, DT, VT>(mp, pl, st);
+        case 1: if constexpr (KD <= 64) return launch_mx<KD, 1, DT, VT, PB>(mp, pl, st); break;
+        case 2: return launch_mx<KD, 2, DT, VT, PB>(mp, pl, st);
+        case 4: return launch_mx<KD, 4, DT, VT, PB>(mp, pl, st);
+        default: return launch_mx<KD, 8, DT, VT, PB>(mp, pl, st);
     }
     return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA-scores decode: more than 64 blocks");
+}
+template <int KD, int DT, int VT>
+int launch_mx_pb(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
+    switch (mp.a.code_bits) {
+        case 4: return launch_mx_bd<KD, DT, VT, 4>(mp, pl, st);
+        case 6: return launch_mx_bd<KD, DT, VT, 6>(mp, pl, st);
+        default: return launch_mx_bd<KD, DT, VT, 0>(mp, pl, st);
+    }
 }
 template <int VT>
 int launch_mx_vt(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
     if (mp.a.head_dim == 64)
-        return pl.DT == 4 ? launch_mx_bd<64, 4, VT>(mp, pl, st) : launch_mx_bd<64, 8, VT>(mp, pl, st);
-    return pl.DT == 4 ? launch_mx_bd<128, 4, VT>(mp, pl, st) : launch_mx_bd<128, 8, VT>(mp, pl, st);
+        return pl.DT == 4 ? launch_mx_pb<64, 4, VT>(mp, pl, st) : launch_mx_pb<64, 8, VT>(mp, pl, st);
+    return pl.DT == 4 ? launch_mx_pb<128, 4, VT>(mp, pl, st) : launch_mx_pb<128, 8, VT>(mp, pl, st);
 }
 
 template <int RP, int DT, int VT, int NB>
@@ -1024,6 +1076,10 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
     SSQ_REQUIRE(pl.ws_bytes == 0 || workspace, "workspace is NULL");
     MfmaParams mp;
     mp.a = *a;
+    if (a->code_bits == 8) {  // 8-bit words are the byte rows: byte strides, the byte-code path
+        mp.a.c_sb *= 4; mp.a.c_sh *= 4; mp.a.c_st *= 4;
+        mp.a.code_bits = 0;
+    }
     mp.G = a->num_q_heads / a->num_kv_heads;
     mp.rows = mp.G * a->q_len;
     mp.rg = pl.rg;

@@ -236,7 +236,8 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
     mask: additive, broadcastable to [B, Hq, Lq, T] (converted to fp32).
     code_bits: 0 for uint8 codes, 1..8 for int32 words from pack_codes (last dim nw).
     Returns out [B, Hq, Lq, Dv] in v's dtype, plus lse [B, Hq, Lq] / raw scores [B, Hq, Lq, T]
-    (fp32) when requested.
+    (fp32) when requested; paged, T = max_pages * page and a sequence's slots past its length
+    hold -inf.
     Reference: sunshape/vllm_attn_backend.py:216-253.
     """
     for name, t in (("query", q), ("codes", codes), ("value", v)):
@@ -278,7 +279,10 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
         v_strides = (v.stride(0), v.stride(1), v.stride(2))
     out = torch.empty((B, Hq, Lq, Dv), device=q.device, dtype=v.dtype)
     lse = torch.empty((B, Hq, Lq), device=q.device, dtype=torch.float32) if return_lse else None
-    scores = torch.empty((B, Hq, Lq, T), device=q.device, dtype=torch.float32) if return_scores else None
+    scores = None
+    if return_scores:  # paged: slots past a sequence's length are never scored and read -inf
+        scores = (torch.full((B, Hq, Lq, T), float("-inf"), device=q.device, dtype=torch.float32) if paged
+                  else torch.empty((B, Hq, Lq, T), device=q.device, dtype=torch.float32))
     if mask is not None:
         _on_gpu("attn_mask", mask)
         mask = mask.to(torch.float32)

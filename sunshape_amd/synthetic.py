@@ -94,7 +94,7 @@ def config3(device="cpu", seed: int = 3, *, B: int = 16, T: int = 8192) -> Probl
 
 
 def config4(device="cpu", seed: int = 4, *, B: int = 64, T: int = 32768, page: int = 16,
-            Hq: int = 32, Hkv: int = 8, D: int = 128, bd: int = 4) -> Problem:
+            Hq: int = 32, Hkv: int = 8, D: int = 128, bd: int = 4, n_centroids: int = N_CENTROIDS) -> Problem:
     """Llama-3-8B-shaped paged decode at 2 bits/dim.
 
     Pages hold every KV head (vLLM-style): code pages [P, Hkv, page, nb] uint8,
@@ -102,13 +102,13 @@ def config4(device="cpu", seed: int = 4, *, B: int = 64, T: int = 32768, page: i
     table [B, T/page] int32 is a seeded permutation of all P = B*T/page pages.
     """
     dev = torch.device(device)
-    cb = make_codebook(Hkv, D, bd, seed)
+    cb = make_codebook(Hkv, D, bd, seed, n_centroids=n_centroids)
     g = torch.Generator().manual_seed(seed + 100)
     q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
     P = B * T // page
     table = torch.randperm(P, generator=g).to(torch.int32).view(B, T // page)
     gd = torch.Generator(device=dev).manual_seed(seed + 200)
-    code_pages = torch.randint(0, 256, (P, Hkv, page, D // bd), generator=gd, device=dev, dtype=torch.uint8)
+    code_pages = torch.randint(0, n_centroids, (P, Hkv, page, D // bd), generator=gd, device=dev, dtype=torch.uint8)
     v_pages = torch.randn(P, Hkv, D, page, generator=gd, device=dev, dtype=torch.bfloat16)
     t = {"q": q.to(dev), "code_pages": code_pages, "v_pages": v_pages, "block_table": table.to(dev),
          "seq_lens": torch.full((B,), T, dtype=torch.int32, device=dev),

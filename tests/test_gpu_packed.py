@@ -84,7 +84,7 @@ def test_decode_over_packed_codes_equals_uint8(paged):
         o8, l8 = hip_ops.decode(q.to(DEV), cpd, vpd, perm, cent, scale=scale, block_table=tbl, seq_lens=lens,
                                 return_lse=True, kernel=1)
         o6, l6 = hip_ops.decode(q.to(DEV), w, vpd, perm, cent, scale=scale, block_table=tbl, seq_lens=lens,
-                                return_lse=True, code_bits=6)
+                                return_lse=True, code_bits=6, kernel=1)
     assert torch.equal(o8, o6) and torch.equal(l8, l6)
     ref = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
                              cb.perm.numpy(), scale, "bf16", "bf16")
@@ -116,3 +116,50 @@ def test_contig_mfma_decode_over_packed_codes_equals_uint8(bits, bd, nc, Hq, T):
                                        cb.perm.numpy(), scale, "bf16", "bf16", return_scores=True)
     assert_rel(np_of(o6), ref, BF16_TOL, "packed contig decode vs oracle")
     assert_rel(np_of(s6), ref_s, SCORE_TOL, "packed contig scores vs oracle")
+
+
+def _pages(codes, v, seed):
+    """Scatter [B, Hkv, T, nb] codes and [B, Hkv, T, Dv] values into shuffled 16-token pages
+    (the last page of each sequence zero-padded): codes [P, Hkv, 16, nb], values [P, Hkv, Dv, 16]."""
+    B, Hkv, T, nb = codes.shape
+    Dv = v.shape[-1]
+    page = 16
+    n = (T + page - 1) // page
+    P = B * n + 3
+    table = torch.randperm(P, generator=torch.Generator().manual_seed(seed))[: B * n].view(B, n).to(torch.int32)
+    cp = torch.zeros(P, Hkv, page, nb, dtype=torch.uint8)
+    vp = torch.zeros(P, Hkv, Dv, page, dtype=v.dtype)
+    pad = n * page - T
+    for b in range(B):
+        cb_ = torch.cat([codes[b], torch.zeros(Hkv, pad, nb, dtype=codes.dtype)], 1)
+        vb_ = torch.cat([v[b], torch.zeros(Hkv, pad, Dv, dtype=v.dtype)], 1)
+        cp[table[b].long()] = cb_.view(Hkv, n, page, nb).permute(1, 0, 2, 3)
+        vp[table[b].long()] = vb_.view(Hkv, n, page, Dv).permute(1, 0, 3, 2)
+    return cp.to(DEV), vp.to(DEV), table.to(DEV), torch.full((B,), T, dtype=torch.int32, device=DEV)
+
+
+@pytest.mark.parametrize("bits,bd,nc,Hq,D,T", [(6, 2, 64, 8, 64, 640), (4, 2, 16, 32, 64, 300), (6, 4, 64, 4, 128, 1000),
+                                               (6, 1, 64, 2, 64, 77), (8, 2, 256, 8, 64, 500), (0, 2, 64, 8, 64, 640)])
+def test_paged_mfma_decode_over_packed_codes(bits, bd, nc, Hq, D, T):
+    """Paged decode of 4- / 6-bit packed codes and of codebooks under 256 codewords runs on the
+    MFMA-scores kernel, which unpacks words when the tile goes to LDS: equal to its own uint8-code
+    launch bit for bit (8-bit words are read as the byte rows), and to the oracle."""
+    log(f"packed paged decode bits={bits} bd={bd} nc={nc} Hq={Hq} D={D} T={T}")
+    cb, codes, q, v = _case(nc=nc, bd=bd, D=D, Hq=Hq, T=T, seed=60 + bits + bd)
+    perm, cent = cb.perm.to(DEV), cb.centroids.to(DEV)
+    scale = 1 / math.sqrt(D)
+    cpd, vpd, tbl, lens = _pages(codes, v, seed=bits + 7)
+    qd = q.to(DEV)
+    kw = dict(scale=scale, block_table=tbl, seq_lens=lens, return_lse=True, return_scores=True, kernel=2)
+    o8, l8, s8 = hip_ops.decode(qd, cpd, vpd, perm, cent, **kw)
+    if bits:
+        w = hip_ops.pack_codes(cpd, bits)
+        o6, l6, s6 = hip_ops.decode(qd, w, vpd, perm, cent, code_bits=bits, **kw)
+        assert torch.equal(o8, o6) and torch.equal(l8, l6) and torch.equal(s8, s6)
+        kw.pop("kernel")
+        assert torch.equal(hip_ops.decode(qd, w, vpd, perm, cent, code_bits=bits, **kw)[0], o6)
+    assert s8.shape[-1] == (T + 15) // 16 * 16 and bool((s8[..., T:] == float("-inf")).all())
+    ref, ref_s, _ = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
+                                       cb.perm.numpy(), scale, "bf16", "bf16", return_scores=True)
+    assert_rel(np_of(o8), ref, BF16_TOL, "paged packed decode vs oracle")
+    assert_rel(np_of(s8[..., :T]), ref_s, SCORE_TOL, "paged packed scores vs oracle")
