@@ -46,8 +46,12 @@ struct MfmaParams {
     float* ws_l;
 };
 
-// LDS carve-up (floats): lut [nb*256*RP] | qp [RP*D] | pstrip [waves][RP][64] (16-bit) | pages [split_len/16] (int32)
-__host__ __device__ inline size_t lut_floats(const ssq_decode_args& a, int RP) { return (size_t)a.n_blocks * kNC * RP; }
+// LUT codewords per block: 256, or 64 for 64-codeword codebooks (a table a quarter the size)
+__host__ __device__ inline int lut_nc(const ssq_decode_args& a) { return a.n_centroids == 64 ? 64 : kNC; }
+// LDS carve-up (floats): lut [nb*nc*RP] | qp [RP*D] | pstrip [waves][RP][64] (16-bit) | pages [split_len/16] (int32)
+__host__ __device__ inline size_t lut_floats(const ssq_decode_args& a, int RP) {
+    return (size_t)a.n_blocks * lut_nc(a) * RP;
+}
 __host__ __device__ inline size_t pstrip_offset(const ssq_decode_args& a, int RP) {
     return (lut_floats(a, RP) + (size_t)RP * a.head_dim + 3) & ~(size_t)3;
 }
@@ -174,9 +178,9 @@ __device__ __forceinline__ void issue_tile(const ssq_decode_args& a, const int* 
     }
 }
 
-template <int RP, int DT, int VT, int NB>
+template <int RP, int DT, int VT, int NB, int NC, int PB>
 __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* lut, uint16_t* pstrip, int b, int kv,
-                                             int t_begin, int t_end, int tile, int lane, TileRegs<NB, DT>& R,
+                                             int t_begin, int t_end, int tile, int lane, TileRegs<NB, DT, PB>& R,
                                              float (&m_run)[RP], float (&l_lane)[RP], v4f (&acc)[DT]) {
     const ssq_decode_args& a = p.a;
     const int t0 = t_begin + tile * kTileTok;
@@ -198,16 +202,23 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
 #pragma unroll
             for (int k = 0; k < KB; ++k) {
                 const int blk = b0 + k;
-                const int wi = blk >> 2;
-                uint32_t word;
-                if (NB >= 16) {
-                    const uint4 c = R.c[wi >> 2];
-                    word = (wi & 3) == 0 ? c.x : (wi & 3) == 1 ? c.y : (wi & 3) == 2 ? c.z : c.w;
+                uint32_t code;
+                if constexpr (PB > 0) {  // PB-bit codes, 32 / PB to a word, low bits first
+                    constexpr int kVpe = 32 / PB;
+                    code = (R.pk[blk / kVpe] >> ((blk % kVpe) * PB)) & ((1u << PB) - 1u);
                 } else {
-                    word = (wi & 1) ? R.c8.y : R.c8.x;
+                    const int wi = blk >> 2;
+                    uint32_t word;
+                    if (NB >= 16) {
+                        const uint4 c = R.c[wi >> 2];
+                        word = (wi & 3) == 0 ? c.x : (wi & 3) == 1 ? c.y : (wi & 3) == 2 ? c.z : c.w;
+                    } else {
+                        word = (wi & 1) ? R.c8.y : R.c8.x;
+                    }
+                    code = (word >> (8 * (blk & 3))) & 0xFFu;
                 }
-                const uint32_t code = (word >> (8 * (blk & 3))) & 0xFFu;
-                const float* e = lut + ((size_t)blk * kNC + code) * RP;
+                if constexpr (NC < 256) code = min(code, (uint32_t)(NC - 1));  // codes past the codebook
+                const float* e = lut + ((size_t)blk * NC + code) * RP;
                 if (RP >= 4) {
 #pragma unroll
                     for (int j = 0; j < NV; ++j) ev[k][j] = *reinterpret_cast<const float4*>(e + 4 * j);
@@ -319,13 +330,13 @@ __device__ __forceinline__ void load_vec(const float* __restrict__ src, float (&
 }
 
 // LUT[e][r] = sum_d qp[r][blk*BD + d] * C[e][d] for this thread's entries e = tid + k*kThreads
-// (blk = e / 256): FMA chain over d from the first product (triton_kernels.py:381-408).  A batch
+// (blk = e / NC): FMA chain over d from the first product (triton_kernels.py:381-408).  A batch
 // of entries loads its codewords and query sub-vectors as vectors before any arithmetic, so the
 // build costs a few memory / LDS latencies instead of one per element.
-template <int RP, int NB, int BD>
+template <int RP, int NB, int BD, int NC>
 __device__ __forceinline__ void build_lut(const float* __restrict__ cent, const float* __restrict__ qp,
                                           float* __restrict__ lut, int D, int tid) {
-    constexpr int kPer = NB * kNC / kThreads;
+    constexpr int kPer = NB * NC / kThreads;
     constexpr int kB = kPer < 128 / BD ? kPer : 128 / BD;  // up to 128 codeword floats in flight
 #pragma unroll
     for (int k0 = 0; k0 < kPer; k0 += kB) {
@@ -338,7 +349,7 @@ __device__ __forceinline__ void build_lut(const float* __restrict__ cent, const 
         for (int kk = 0; kk < kB; ++kk) {
             if (k0 + kk >= kPer) break;
             const int e = tid + (k0 + kk) * kThreads;
-            const float* qb = qp + (e / kNC) * BD;
+            const float* qb = qp + (e / NC) * BD;
             float acc[RP];
 #pragma unroll
             for (int r = 0; r < RP; ++r) {
@@ -362,12 +373,12 @@ __device__ __forceinline__ void build_lut(const float* __restrict__ cent, const 
 }
 
 // any block_dim: one element at a time
-template <int RP, int NB>
+template <int RP, int NB, int NC>
 __device__ void build_lut_any(const float* __restrict__ cent, const float* __restrict__ qp, float* __restrict__ lut,
                               int D, int bd, int tid) {
-    for (int e = tid; e < NB * kNC; e += kThreads) {
+    for (int e = tid; e < NB * NC; e += kThreads) {
         const float* c = cent + (int64_t)e * bd;
-        const float* qb = qp + (e / kNC) * bd;
+        const float* qb = qp + (e / NC) * bd;
         float acc[RP];
 #pragma unroll
         for (int r = 0; r < RP; ++r) acc[r] = qb[r * D] * c[0];
@@ -381,7 +392,8 @@ __device__ void build_lut_any(const float* __restrict__ cent, const float* __res
     }
 }
 
-template <int RP, int DT, int VT, int NB>
+// NC: LUT codewords per block (256, or 64); PB: packed code bits (0 = byte codes)
+template <int RP, int DT, int VT, int NB, int NC, int PB>
 __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_decode_args& a = p.a;
@@ -474,21 +486,23 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     __syncthreads();
     // the first tile's codes and values are independent of the LUT: put them in flight before building it
     const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)kv * a.v_sh + (int64_t)(lane & 15) * a.v_st;
-    const uint8_t* cbase = a.codes + (int64_t)kv * a.c_sh;
+    const uint8_t* cbase = PB > 0 ? reinterpret_cast<const uint8_t*>(reinterpret_cast<const uint32_t*>(a.codes) +
+                                                                     (int64_t)kv * a.c_sh)
+                                  : a.codes + (int64_t)kv * a.c_sh;
     const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
-    TileRegs<NB, DT> RA, RB;
+    TileRegs<NB, DT, PB> RA, RB;
     int tile = wave;
     // Tile loads are issued unconditionally (a wave past the last tile re-reads tile n_tiles-1,
     // mostly from L2): every path then carries the same queue of outstanding loads, so the
     // compiler's vmcnt waits for the tile being computed never drain the tile behind it.
     const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
-    if (n_tiles > 0) issue_tile<NB, DT>(a, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, RA);
+    if (n_tiles > 0) issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, RA);
     switch (bd) {
-        case 1: build_lut<RP, NB, 1>(cent, qp, lut, D, tid); break;
-        case 2: build_lut<RP, NB, 2>(cent, qp, lut, D, tid); break;
-        case 4: build_lut<RP, NB, 4>(cent, qp, lut, D, tid); break;
-        case 8: build_lut<RP, NB, 8>(cent, qp, lut, D, tid); break;
-        default: build_lut_any<RP, NB>(cent, qp, lut, D, bd, tid); break;
+        case 1: build_lut<RP, NB, 1, NC>(cent, qp, lut, D, tid); break;
+        case 2: build_lut<RP, NB, 2, NC>(cent, qp, lut, D, tid); break;
+        case 4: build_lut<RP, NB, 4, NC>(cent, qp, lut, D, tid); break;
+        case 8: build_lut<RP, NB, 8, NC>(cent, qp, lut, D, tid); break;
+        default: build_lut_any<RP, NB, NC>(cent, qp, lut, D, bd, tid); break;
     }
     __syncthreads();
 
@@ -500,12 +514,12 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
     while (tile < n_tiles) {
-        issue_tile<NB, DT>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RB);
-        compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane, acc);
+        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RB);
+        compute_tile<RP, DT, VT, NB, NC, PB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane, acc);
         tile += kWaves;
         if (tile >= n_tiles) break;
-        issue_tile<NB, DT>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RA);
-        compute_tile<RP, DT, VT, NB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RB, m_run, l_lane, acc);
+        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RA);
+        compute_tile<RP, DT, VT, NB, NC, PB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RB, m_run, l_lane, acc);
         tile += kWaves;
     }
 
@@ -919,15 +933,20 @@ bool mx_shape(const ssq_decode_args* a) {
     return a->value_dim == 64 || a->value_dim == 128;
 }
 
+// the 64-codeword LUT kernel's instantiations
+bool lut64_shape(const ssq_decode_args& a, int RP, int DT) {
+    return a.v_dtype == SSQ_BF16 && (DT == 4 || DT == 8) && (RP == 2 || RP == 4 || RP == 8) &&
+           (a.n_blocks == 16 || a.n_blocks == 32 || a.n_blocks == 64);
+}
+
 bool plan(const ssq_decode_args* a, MPlan& pl) {
     if (a->layout != SSQ_PAGED || a->page_size != kPage) return false;
-    // Codes: bytes, 8-bit words (the byte rows, strides scaled to bytes), or 4- / 6-bit words,
-    // which the MFMA-scores kernel unpacks; so does a codebook of fewer than 256 codewords (the
-    // LUT kernel's table is laid out for 256).  Other widths take the generic kernel.
+    // Codes: bytes, 8-bit words (the byte rows, strides scaled to bytes), or 4- / 6-bit words.
+    // The LUT kernel serves 256-codeword codebooks with byte codes, and 64-codeword codebooks
+    // with byte or 6-bit codes (bf16 V, 2-8 rows, 16-64 blocks: lut64_shape); the MFMA-scores
+    // kernel serves the rest of its shapes.  Other widths take the generic kernel.
     const int cbits = a->code_bits;
     if (cbits != 0 && cbits != 4 && cbits != 6 && cbits != 8) return false;
-    const bool need_mx = cbits == 4 || cbits == 6 || a->n_centroids != kNC;
-    if (need_mx && !mx_shape(a)) return false;
     if (a->n_centroids > kNC) return false;
     if (a->v == nullptr || (a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16)) return false;
     if (a->mask != nullptr || a->heavy_mask[0] || a->heavy_mask[1]) return false;
@@ -944,25 +963,30 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
             return false;
     }
     if ((uintptr_t)a->v % 16 || (a->v_sb * 2) % 16 || (a->v_sh * 2) % 16 || (a->v_st * 2) % 16) return false;
-    // Query rows of one (batch, KV head) share a LUT of n_blocks x 256 x RP fp32 (<= 128 KiB).
+    // Query rows of one (batch, KV head) share a LUT of n_blocks x nc x RP fp32 (<= 128 KiB).
     // More rows than one LUT holds split into row groups, each streaming the codes and values
     // again: twice the bytes at 8 query heads per KV head with 32 blocks, far less than the
     // LUT-less generic kernel costs.
     const int rows = (a->num_q_heads / a->num_kv_heads) * a->q_len;
     if (rows > 64) return false;
-    const int cap = 128 / a->n_blocks < 16 ? 128 / a->n_blocks : 16;  // a power of two
+    const int lcap = 32768 / (a->n_blocks * lut_nc(*a));  // rows per 128 KiB LUT, a power of two
+    const int cap = lcap < 16 ? lcap : 16;
     pl.rg = rows < cap ? rows : cap;
     pl.n_groups = (rows + pl.rg - 1) / pl.rg;
     pl.RP = pow2_at_least(pl.rg);
-    // Where the LUT needs row groups, the MFMA-scores kernel serves up to 16 rows per pass over
-    // the pages instead (its codebook is head_dim x 256 fp32 whatever the block size)
-    pl.mx = need_mx || (pl.n_groups > 1 && mx_shape(a));
+    pl.DT = a->value_dim / 16;
+    const bool lut_ok = a->n_centroids == kNC ? cbits == 0 || cbits == 8
+                                              : a->n_centroids == 64 && cbits != 4 && lut64_shape(*a, pl.RP, pl.DT);
+    // Where the LUT needs row groups (or cannot serve the codes), the MFMA-scores kernel serves
+    // up to 16 rows per pass over the pages instead (its codebook is head_dim x nc fp32 whatever
+    // the block size)
+    if (!lut_ok && !mx_shape(a)) return false;
+    pl.mx = !lut_ok || (pl.n_groups > 1 && mx_shape(a));
     if (pl.mx) {
         pl.rg = rows < 16 ? rows : 16;
         pl.n_groups = (rows + 15) / 16;
         pl.RP = 16;
     }
-    pl.DT = a->value_dim / 16;
     const int units = a->batch * a->num_kv_heads * pl.n_groups;
     const int tiles = (a->seq_len + kTileTok - 1) / kTileTok;
     const int cus = ssq_device_cus();  // one workgroup per CU (the LUT fills the LDS)
@@ -1021,9 +1045,9 @@ int launch_mx_vt(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
     return pl.DT == 4 ? launch_mx_pb<128, 4, VT>(mp, pl, st) : launch_mx_pb<128, 8, VT>(mp, pl, st);
 }
 
-template <int RP, int DT, int VT, int NB>
+template <int RP, int DT, int VT, int NB, int NC = kNC, int PB = 0>
 int launch(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
-    auto kern = k_decode_mfma<RP, DT, VT, NB>;
+    auto kern = k_decode_mfma<RP, DT, VT, NB, NC, PB>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_mfma)");
     if (rc) return rc;
     dim3 grid(mp.a.batch * mp.a.num_kv_heads, pl.n_splits, pl.n_groups);
@@ -1054,6 +1078,24 @@ int launch_dt(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
 template <int RP>
 int launch_vt(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
     return mp.a.v_dtype == SSQ_BF16 ? launch_dt<RP, SSQ_BF16>(mp, pl, st) : launch_dt<RP, SSQ_F16>(mp, pl, st);
+}
+
+// 64-codeword LUT kernel (lut64_shape): bf16 V, byte or 6-bit codes
+template <int RP, int DT, int PB>
+int lut64_nb(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
+    switch (mp.a.n_blocks) {
+        case 16: return launch<RP, DT, SSQ_BF16, 16, 64, PB>(mp, pl, st);
+        case 32: return launch<RP, DT, SSQ_BF16, 32, 64, PB>(mp, pl, st);
+        default: return launch<RP, DT, SSQ_BF16, 64, 64, PB>(mp, pl, st);
+    }
+}
+template <int PB>
+int lut64_rp(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
+    switch (pl.RP) {
+        case 2: return pl.DT == 4 ? lut64_nb<2, 4, PB>(mp, pl, st) : lut64_nb<2, 8, PB>(mp, pl, st);
+        case 4: return pl.DT == 4 ? lut64_nb<4, 4, PB>(mp, pl, st) : lut64_nb<4, 8, PB>(mp, pl, st);
+        default: return pl.DT == 4 ? lut64_nb<8, 4, PB>(mp, pl, st) : lut64_nb<8, 8, PB>(mp, pl, st);
+    }
 }
 
 }  // namespace
@@ -1093,6 +1135,12 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
     int rc;
     if (pl.mx) {
         rc = mp.a.v_dtype == SSQ_BF16 ? launch_mx_vt<SSQ_BF16>(mp, pl, st) : launch_mx_vt<SSQ_F16>(mp, pl, st);
+        if (rc) return rc;
+        if (pl.n_splits > 1) rc = ssq_launch_merge(*a, pl.n_splits, mp.ws_o, mp.ws_m, mp.ws_l, st);
+        return rc;
+    }
+    if (mp.a.n_centroids == 64) {
+        rc = mp.a.code_bits == 6 ? lut64_rp<6>(mp, pl, st) : lut64_rp<0>(mp, pl, st);
         if (rc) return rc;
         if (pl.n_splits > 1) rc = ssq_launch_merge(*a, pl.n_splits, mp.ws_o, mp.ws_m, mp.ws_l, st);
         return rc;

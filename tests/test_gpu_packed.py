@@ -141,9 +141,11 @@ def _pages(codes, v, seed):
 @pytest.mark.parametrize("bits,bd,nc,Hq,D,T", [(6, 2, 64, 8, 64, 640), (4, 2, 16, 32, 64, 300), (6, 4, 64, 4, 128, 1000),
                                                (6, 1, 64, 2, 64, 77), (8, 2, 256, 8, 64, 500), (0, 2, 64, 8, 64, 640)])
 def test_paged_mfma_decode_over_packed_codes(bits, bd, nc, Hq, D, T):
-    """Paged decode of 4- / 6-bit packed codes and of codebooks under 256 codewords runs on the
-    MFMA-scores kernel, which unpacks words when the tile goes to LDS: equal to its own uint8-code
-    launch bit for bit (8-bit words are read as the byte rows), and to the oracle."""
+    """Paged decode of 4- / 6-bit packed codes and of codebooks under 256 codewords: 64-codeword
+    codebooks with 2-8 rows run the LUT kernel (a 64-entry table per block, codes unpacked from
+    the words in registers), the others the MFMA-scores kernel (words unpacked as the tile goes to
+    LDS).  Equal to the same kernel's uint8-code launch bit for bit (8-bit words are read as the
+    byte rows), and to the oracle."""
     log(f"packed paged decode bits={bits} bd={bd} nc={nc} Hq={Hq} D={D} T={T}")
     cb, codes, q, v = _case(nc=nc, bd=bd, D=D, Hq=Hq, T=T, seed=60 + bits + bd)
     perm, cent = cb.perm.to(DEV), cb.centroids.to(DEV)
