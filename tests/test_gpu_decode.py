@@ -208,6 +208,24 @@ def test_config4_full_size_sampled_units():
     _paged_oracle_check(p, o, l, None, units)
 
 
+def test_config4_layer_3bit_packed_full_size():
+    """The config-4 layer at 3 bits/dim (64 codewords, bd 2) at full size: 6-bit words and byte
+    codes give the same output bit for bit (64-codeword LUT kernel), and sampled units match the
+    oracle."""
+    log("config4 3-bit packed full size")
+    p = synthetic.config4(DEV, bd=2, n_centroids=64)
+    kw = dict(scale=p.meta["scale"], block_table=p["block_table"], seq_lens=p["seq_lens"], return_lse=True)
+    out8, lse8 = hip_ops.decode(p["q"], p["code_pages"], p["v_pages"], p["perm"], p["centroids"], **kw)
+    words = hip_ops.pack_codes(p["code_pages"], 6)
+    out6, lse6 = hip_ops.decode(p["q"], words, p["v_pages"], p["perm"], p["centroids"], code_bits=6, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out8, out6) and torch.equal(lse8, lse6)
+    del words
+    rng = np.random.default_rng(3)
+    units = [(int(rng.integers(64)), int(rng.integers(8))) for _ in range(3)] + [(63, 7)]
+    _paged_oracle_check(p, np_of(out6), np_of(lse6), None, units)
+
+
 def test_mixed_passthrough_decode_config5_shape():
     log("mixed passthrough decode")
     p = synthetic.config5(DEV, B=2, S=1200)
