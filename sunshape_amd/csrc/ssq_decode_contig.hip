@@ -51,6 +51,7 @@ struct ContigParams {
     // passthrough dims (SunShape-Mixed): the token record element and the permuted head dim of
     // heavy dim idx (blocks ascending, then d); n_hd of them
     int n_hd;
+    int pt_vec;  // 1: the 8 passthrough values are contiguous 16-bit elements from slot 0, 16-byte aligned
     int hoff[kHP];
     int hdim[kHP];
 };
@@ -117,19 +118,21 @@ __host__ __device__ constexpr int pk_words(int NB, int PB) { return PB ? (NB + 3
 
 // registers of one 64-token tile in flight: this lane's 16-byte V chunks, its token's code row
 // (bytes, or PB-bit codes in words) and (heavy blocks) its token's passthrough values
-template <int NB, int DT, bool HV, bool MK, int PB>
+// HV: passthrough values per token: 0 none; 1 up to kHP values, one load each (any dtype and
+// slot layout); 2 exactly 8 contiguous 16-bit values from slot 0, one 16-byte load
+template <int NB, int DT, int HV, bool MK, int PB>
 struct Tile {
     uint4 v[2 * DT];
     uint4 c[NB >= 16 ? NB / 16 : 1];
     uint2 c8;
     uint32_t pk[pk_words(NB, PB)];
-    uint32_t h[HV ? kHP : 1];  // raw bits (ssq_load_bits); converted when the tile goes to LDS
+    uint32_t h[HV == 1 ? kHP : HV == 2 ? 4 : 1];  // raw bits; converted when the tile goes to LDS
     float mk[MK ? 16 : 1];     // additive mask at [row 4*lg + i][token 16g + l16], index 4g + i
 };
 
 // Loads are unconditional; chunks of tokens past the split's end re-read the last token's row
 // (valid memory; such tokens get p = 0 and are never scored).
-template <int NB, int DT, bool HAS_V, bool HV, bool MK, int PB>
+template <int NB, int DT, bool HAS_V, int HV, bool MK, int PB>
 __device__ __forceinline__ void issue_tile(const ContigParams& p, int b, int kv, int t0, int t_end, int lane,
                                            Tile<NB, DT, HV, MK, PB>& R) {
     const ssq_decode_args& a = p.a;
@@ -149,10 +152,14 @@ __device__ __forceinline__ void issue_tile(const ContigParams& p, int b, int kv,
             }
         }
     }
-    if constexpr (HV) {
+    if constexpr (HV == 1) {
         const int64_t pb = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)tc * a.pt_st;
 #pragma unroll
         for (int i = 0; i < kHP; ++i) R.h[i] = ssq_load_bits(a.pt, a.pt_dtype, pb + p.hoff[i]);  // hoff clamped
+    } else if constexpr (HV == 2) {
+        const int64_t pb = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)tc * a.pt_st;
+        const uint4 w = ld16(reinterpret_cast<const uint16_t*>(a.pt) + pb);
+        R.h[0] = w.x; R.h[1] = w.y; R.h[2] = w.z; R.h[3] = w.w;
     }
     if constexpr (PB) {  // packed rows: strides count int32 words
         const uint32_t* prow = reinterpret_cast<const uint32_t*>(a.codes) + (int64_t)b * a.c_sb +
@@ -183,8 +190,8 @@ __device__ __forceinline__ void issue_tile(const ContigParams& p, int b, int kv,
 // mask or 128-dim values fit; the others keep 4 waves
 __host__ __device__ constexpr bool contig_wide(int dt, bool hv, bool mk) { return !hv && !mk && dt <= 4; }
 
-template <int BD, int DT, int VT, bool HAS_V, bool HV, bool MK, int PB>
-__global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 * SSQ_WAVE) void k_decode_contig(
+template <int BD, int DT, int VT, bool HAS_V, int HV, bool MK, int PB>
+__global__ __launch_bounds__(contig_wide(DT, HV != 0, MK) ? kMaxWaves * SSQ_WAVE : 4 * SSQ_WAVE) void k_decode_contig(
     const ContigParams p) {
     constexpr int NB = kD / BD;
     constexpr int NBW = NB / 4;  // code row dwords
@@ -207,7 +214,7 @@ __global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 
     const int t_end = min(a.seq_len, t_begin + p.split_len);
 
     float* cb = smem;  // codebook [NB][nc][BD] fp32
-    uint8_t* wreg = reinterpret_cast<uint8_t*>(smem + cb_floats(nc)) + wave * wave_bytes(NB, DT, HV);
+    uint8_t* wreg = reinterpret_cast<uint8_t*>(smem + cb_floats(nc)) + wave * wave_bytes(NB, DT, HV != 0);
     uint16_t* vt = reinterpret_cast<uint16_t*>(wreg);                            // [64][Dv]
     uint8_t* ct = wreg + wave_v_bytes(DT);                                       // [64][NB]
     uint16_t* ps = reinterpret_cast<uint16_t*>(wreg + wave_v_bytes(DT) + kTile * NB);  // [16][64]
@@ -222,8 +229,8 @@ __global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 
     int64_t pj[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) pj[s] = perm[4 * s + lg];
-    int64_t pjh[HV ? kHP / 4 : 1];  // passthrough pass: permuted head dim of heavy dim 4s + lg
-    if constexpr (HV) {
+    int64_t pjh[HV != 0 ? kHP / 4 : 1];  // passthrough pass: permuted head dim of heavy dim 4s + lg
+    if constexpr (HV != 0) {
 #pragma unroll
         for (int s = 0; s < kHP / 4; ++s) pjh[s] = perm[p.hdim[4 * s + lg]];  // hdim is 0 past n_hd
     }
@@ -250,7 +257,7 @@ __global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 
     }
 
     float qa[KS];
-    float qh[HV ? kHP / 4 : 1];  // A operand of the passthrough pass: Qp[row l16][heavy dim 4s + lg]
+    float qh[HV != 0 ? kHP / 4 : 1];  // A operand of the passthrough pass: Qp[row l16][heavy dim 4s + lg]
     {
         constexpr int kRows = 16;  // A-operand rows (nr <= 16)
         int64_t src[kRows];
@@ -273,7 +280,7 @@ __global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 
         const float* qrow = qs + l16 * kD;
 #pragma unroll
         for (int s = 0; s < KS; ++s) qa[s] = qrow[min((uint64_t)pj[s], (uint64_t)(kD - 1))];
-        if constexpr (HV) {
+        if constexpr (HV != 0) {
 #pragma unroll
             for (int s = 0; s < kHP / 4; ++s)  // heavy dims past n_hd are zero
                 qh[s] = 4 * s + lg < p.n_hd ? qrow[min((uint64_t)pjh[s], (uint64_t)(kD - 1))] : 0.f;
@@ -332,7 +339,7 @@ __global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 
 #pragma unroll
             for (int i = 0; i < 2 * DT; ++i) *reinterpret_cast<uint4*>(vt + (i * SSQ_WAVE + lane) * 8) = R.v[i];
         }
-        if constexpr (HV) {
+        if constexpr (HV == 1) {
 #pragma unroll
             for (int i = 0; i < kHP; i += 4) {
                 float x[4];
@@ -340,6 +347,17 @@ __global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 
                 for (int u = 0; u < 4; ++u) x[u] = i + u < p.n_hd ? ssq_bits_to_f32(R.h[i + u], a.pt_dtype) : 0.f;
                 *reinterpret_cast<float4*>(ph + lane * kHP + i) = make_float4(x[0], x[1], x[2], x[3]);
             }
+        } else if constexpr (HV == 2) {  // 8 values, two per word (low half first); dims 8..15 are zero
+#pragma unroll
+            for (int i = 0; i < 8; i += 4) {
+                float x[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    x[u] = ssq_bits_to_f32((R.h[(i + u) >> 1] >> (16 * ((i + u) & 1))) & 0xFFFFu, a.pt_dtype);
+                *reinterpret_cast<float4*>(ph + lane * kHP + i) = make_float4(x[0], x[1], x[2], x[3]);
+            }
+            *reinterpret_cast<float4*>(ph + lane * kHP + 8) = make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<float4*>(ph + lane * kHP + 12) = make_float4(0.f, 0.f, 0.f, 0.f);
         }
         wave_sync();
         float mk[MK ? 16 : 1];  // this tile's mask values, taken before R is reloaded
@@ -375,7 +393,7 @@ __global__ __launch_bounds__(contig_wide(DT, HV, MK) ? kMaxWaves * SSQ_WAVE : 4 
                 const float kval = *reinterpret_cast<const float*>(cbb + lane_off + step_off + (code << (2 + kLogBD)));
                 c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kval, c, 0, 0, 0);
             }
-            if constexpr (HV) {  // passthrough pass: B = the tokens' stored heavy-block values
+            if constexpr (HV != 0) {  // passthrough pass: B = the tokens' stored heavy-block values
 #pragma unroll
                 for (int s = 0; s < kHP / 4; ++s) {
                     if (4 * s < p.n_hd) {
@@ -573,7 +591,7 @@ bool plan(const ssq_decode_args* a, bool has_v, CPlan& pl) {
     return true;
 }
 
-template <int BD, int DT, int VT, bool HAS_V, bool HV, bool MK, int PB>
+template <int BD, int DT, int VT, bool HAS_V, int HV, bool MK, int PB>
 int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     auto kern = k_decode_contig<BD, DT, VT, HAS_V, HV, MK, PB>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_contig)");
@@ -583,7 +601,7 @@ int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     return ssq_check_hip(hipGetLastError(), "k_decode_contig launch");
 }
 
-template <int DT, int VT, bool HAS_V, bool HV, bool MK, int PB = 0>
+template <int DT, int VT, bool HAS_V, int HV, bool MK, int PB = 0>
 int launch_bd(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     switch (cp.a.block_dim) {
         case 1: return launch<1, DT, VT, HAS_V, HV, MK, PB>(cp, pl, st);
@@ -592,15 +610,16 @@ int launch_bd(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
         default: return launch<8, DT, VT, HAS_V, HV, MK, PB>(cp, pl, st);
     }
 }
-template <int DT, int VT, bool HAS_V, bool HV>
+template <int DT, int VT, bool HAS_V, int HV>
 int launch_mk(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     return cp.a.mask ? launch_bd<DT, VT, HAS_V, HV, true>(cp, pl, st) : launch_bd<DT, VT, HAS_V, HV, false>(cp, pl, st);
 }
 template <int DT, int VT, bool HAS_V>
 int launch_hv(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
-    if (cp.a.code_bits == 4) return launch_bd<DT, VT, HAS_V, false, false, 4>(cp, pl, st);
-    if (cp.a.code_bits == 6) return launch_bd<DT, VT, HAS_V, false, false, 6>(cp, pl, st);
-    return cp.n_hd > 0 ? launch_mk<DT, VT, HAS_V, true>(cp, pl, st) : launch_mk<DT, VT, HAS_V, false>(cp, pl, st);
+    if (cp.a.code_bits == 4) return launch_bd<DT, VT, HAS_V, 0, false, 4>(cp, pl, st);
+    if (cp.a.code_bits == 6) return launch_bd<DT, VT, HAS_V, 0, false, 6>(cp, pl, st);
+    if (cp.pt_vec && !cp.a.mask) return launch_bd<DT, VT, HAS_V, 2, false>(cp, pl, st);
+    return cp.n_hd > 0 ? launch_mk<DT, VT, HAS_V, 1>(cp, pl, st) : launch_mk<DT, VT, HAS_V, 0>(cp, pl, st);
 }
 
 }  // namespace
@@ -655,6 +674,12 @@ int ssq_decode_contig(const ssq_decode_args* a, void* workspace, size_t ws_bytes
         ++h;
     }
     for (int i = cp.n_hd; i < kHP; ++i) cp.hoff[i] = cp.hoff[0];  // loaded, then zeroed in the kernel
+    cp.pt_vec = 0;
+    if (cp.n_hd == 8 && (a->pt_dtype == SSQ_BF16 || a->pt_dtype == SSQ_F16) && (uintptr_t)a->pt % 16 == 0 &&
+        (a->pt_sb * 2) % 16 == 0 && (a->pt_sh * 2) % 16 == 0 && (a->pt_st * 2) % 16 == 0) {
+        cp.pt_vec = 1;
+        for (int i = 0; i < 8; ++i) cp.pt_vec &= cp.hoff[i] == i ? 1 : 0;
+    }
     int rc;
     if (!has_v) {
         rc = launch_hv<4, SSQ_BF16, false>(cp, pl, st);
