@@ -186,12 +186,14 @@ __device__ __forceinline__ void issue_tile(const ContigParams& p, int b, int kv,
     }
 }
 
-// 8-wave workgroups need two waves' registers per SIMD, which the variants without passthrough,
-// mask or 128-dim values fit; the others keep 4 waves
-__host__ __device__ constexpr bool contig_wide(int dt, bool hv, bool mk) { return !hv && !mk && dt <= 4; }
+// Waves per workgroup.  8 need two waves' registers per SIMD, which the variants without
+// passthrough, mask or 128-dim values fit; the others keep 4.  (The passthrough variants' tiles
+// leave LDS for only 6 waves beside a 64 KiB codebook; 6 waves put two on only two of the four
+// SIMDs and measured slower than 4.)
+__host__ __device__ constexpr int contig_waves(int dt, int hv, bool mk) { return !mk && dt <= 4 && hv == 0 ? 8 : 4; }
 
 template <int BD, int DT, int VT, bool HAS_V, int HV, bool MK, int PB>
-__global__ __launch_bounds__(contig_wide(DT, HV != 0, MK) ? kMaxWaves * SSQ_WAVE : 4 * SSQ_WAVE) void k_decode_contig(
+__global__ __launch_bounds__(contig_waves(DT, HV, MK) * SSQ_WAVE) void k_decode_contig(
     const ContigParams p) {
     constexpr int NB = kD / BD;
     constexpr int NBW = NB / 4;  // code row dwords
@@ -529,6 +531,38 @@ __global__ __launch_bounds__(contig_wide(DT, HV != 0, MK) ? kMaxWaves * SSQ_WAVE
     }
 }
 
+// passthrough dims of the heavy blocks, blocks ascending then d: the token record element and
+// the permuted head dim of each (n_hd of them), and whether they are 8 contiguous 16-bit
+// elements from slot 0 in 16-byte aligned rows (the one-load variant)
+struct PtLayout {
+    int n_hd = 0, vec = 0;
+    int hoff[kHP] = {}, hdim[kHP] = {};
+};
+PtLayout pt_layout(const ssq_decode_args& a) {
+    PtLayout L;
+    for (int blk = 0, h = 0; blk < a.n_blocks && blk < 64; ++blk) {
+        if (!((a.heavy_mask[0] >> blk) & 1ull)) continue;
+        const int slot = a.pt_dense ? blk : h;  // record slot = block (dense) or ordinal
+        for (int d = 0; d < a.block_dim && L.n_hd < kHP; ++d) {
+            L.hoff[L.n_hd] = slot * a.block_dim + d;
+            L.hdim[L.n_hd] = blk * a.block_dim + d;
+            ++L.n_hd;
+        }
+        ++h;
+    }
+    for (int i = L.n_hd; i < kHP; ++i) L.hoff[i] = L.hoff[0];  // loaded, then zeroed in the kernel
+    if (L.n_hd == 8 && (a.pt_dtype == SSQ_BF16 || a.pt_dtype == SSQ_F16) && (uintptr_t)a.pt % 16 == 0 &&
+        (a.pt_sb * 2) % 16 == 0 && (a.pt_sh * 2) % 16 == 0 && (a.pt_st * 2) % 16 == 0) {
+        L.vec = 1;
+        for (int i = 0; i < 8; ++i) L.vec &= L.hoff[i] == i ? 1 : 0;
+    }
+    return L;
+}
+// the kernel's passthrough variant: 0 none, 1 one load per value, 2 one 16-byte load (no mask)
+int hv_kind(const ssq_decode_args& a, const PtLayout& L) {
+    return L.n_hd == 0 ? 0 : L.vec && !a.mask ? 2 : 1;
+}
+
 struct CPlan {
     int DT, split_len, n_splits, waves;
     size_t smem, ws_bytes;
@@ -570,9 +604,9 @@ bool plan(const ssq_decode_args* a, bool has_v, CPlan& pl) {
         pl.DT = a->value_dim / 16;
     }
     // 8 waves share the codebook where the LDS holds their tiles (two waves per SIMD hide each
-    // other's gather and MFMA latency); the passthrough variant's registers allow only 4
-    const bool hv = (a->heavy_mask[0] | a->heavy_mask[1]) != 0;
-    pl.waves = contig_wide(pl.DT, hv, a->mask != nullptr) && contig_smem(*a, pl.DT, kMaxWaves) <= kMaxSmem ? kMaxWaves : 4;
+    // other's gather and MFMA latency) and the registers allow; otherwise 4
+    pl.waves = contig_waves(pl.DT, hv_kind(*a, pt_layout(*a)), a->mask != nullptr);
+    if (contig_smem(*a, pl.DT, pl.waves) > kMaxSmem) pl.waves = 4;
     pl.smem = contig_smem(*a, pl.DT, pl.waves);
     if (pl.smem > kMaxSmem) return false;
     const int units = a->batch * a->num_kv_heads;
@@ -597,6 +631,8 @@ int launch(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_contig)");
     if (rc) return rc;
     dim3 grid(cp.a.batch * cp.a.num_kv_heads, pl.n_splits);
+    SSQ_REQUIRE(pl.waves <= contig_waves(DT, HV, MK), "decode_contig: %d waves exceed the variant's %d", pl.waves,
+                contig_waves(DT, HV, MK));
     hipLaunchKernelGGL(kern, grid, dim3(pl.waves * SSQ_WAVE), pl.smem, st, cp);
     return ssq_check_hip(hipGetLastError(), "k_decode_contig launch");
 }
@@ -618,7 +654,7 @@ template <int DT, int VT, bool HAS_V>
 int launch_hv(const ContigParams& cp, const CPlan& pl, hipStream_t st) {
     if (cp.a.code_bits == 4) return launch_bd<DT, VT, HAS_V, 0, false, 4>(cp, pl, st);
     if (cp.a.code_bits == 6) return launch_bd<DT, VT, HAS_V, 0, false, 6>(cp, pl, st);
-    if (cp.pt_vec && !cp.a.mask) return launch_bd<DT, VT, HAS_V, 2, false>(cp, pl, st);
+    if (hv_kind(cp.a, PtLayout{cp.n_hd, cp.pt_vec}) == 2) return launch_bd<DT, VT, HAS_V, 2, false>(cp, pl, st);
     return cp.n_hd > 0 ? launch_mk<DT, VT, HAS_V, 1>(cp, pl, st) : launch_mk<DT, VT, HAS_V, 0>(cp, pl, st);
 }
 
@@ -661,25 +697,10 @@ int ssq_decode_contig(const ssq_decode_args* a, void* workspace, size_t ws_bytes
     cp.ws_m = ws ? ws + (size_t)pl.n_splits * n_rows_all * a->value_dim : nullptr;
     cp.ws_l = ws ? cp.ws_m + (size_t)pl.n_splits * n_rows_all : nullptr;
     // passthrough dims: heavy blocks ascending, then d; record slot = block (dense) or ordinal
-    cp.n_hd = 0;
-    for (int i = 0; i < kHP; ++i) { cp.hoff[i] = 0; cp.hdim[i] = 0; }
-    for (int blk = 0, h = 0; blk < a->n_blocks && blk < 64; ++blk) {
-        if (!((a->heavy_mask[0] >> blk) & 1ull)) continue;
-        const int slot = a->pt_dense ? blk : h;
-        for (int d = 0; d < a->block_dim && cp.n_hd < kHP; ++d) {
-            cp.hoff[cp.n_hd] = slot * a->block_dim + d;
-            cp.hdim[cp.n_hd] = blk * a->block_dim + d;
-            ++cp.n_hd;
-        }
-        ++h;
-    }
-    for (int i = cp.n_hd; i < kHP; ++i) cp.hoff[i] = cp.hoff[0];  // loaded, then zeroed in the kernel
-    cp.pt_vec = 0;
-    if (cp.n_hd == 8 && (a->pt_dtype == SSQ_BF16 || a->pt_dtype == SSQ_F16) && (uintptr_t)a->pt % 16 == 0 &&
-        (a->pt_sb * 2) % 16 == 0 && (a->pt_sh * 2) % 16 == 0 && (a->pt_st * 2) % 16 == 0) {
-        cp.pt_vec = 1;
-        for (int i = 0; i < 8; ++i) cp.pt_vec &= cp.hoff[i] == i ? 1 : 0;
-    }
+    const PtLayout L = pt_layout(*a);
+    cp.n_hd = L.n_hd;
+    cp.pt_vec = L.vec;
+    for (int i = 0; i < kHP; ++i) { cp.hoff[i] = L.hoff[i]; cp.hdim[i] = L.hdim[i]; }
     int rc;
     if (!has_v) {
         rc = launch_hv<4, SSQ_BF16, false>(cp, pl, st);
