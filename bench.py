@@ -11,7 +11,7 @@ algorithmic bytes and its fraction of the 8 TB/s peak, the kernel's average laun
 from HIP events on its own stream, the same launch's time with cold caches (a 1 GiB flush
 before each), and a bounded CPU-oracle baseline timed on the host.
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c5encpro] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -39,7 +39,7 @@ def _args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "c4g8", "c4bd2", "c3p6",
-                                                     "c4p6", "copycal"])
+                                                     "c4p6", "c5encpro", "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -213,7 +213,10 @@ def _scores_workload(dev):
     return step, keys, algo, cfg, None, "ssq_attention_scores"
 
 
-def _encode_workload(dev, kernel):
+def _encode_workload(dev, kernel, pro=False):
+    """c5enc: the config-5 encode (grid search by default).  c5encpro: the same keys under a
+    SunShape-Pro block metric E [D, D] (sunshape/codec.py:375-376), seeded near the identity;
+    the metric encode runs the MFMA screen on E x and E c."""
     import torch
 
     from sunshape_amd import hip_ops, synthetic
@@ -222,10 +225,17 @@ def _encode_workload(dev, kernel):
     heavy = p["heavy"].tolist()
     keys_t = p["keys"]
     B, Hkv, S, D = keys_t.shape
+    metric = None
+    if pro:
+        g = torch.Generator().manual_seed(55)
+        metric = (torch.eye(D) + 0.3 * torch.randn(D, D, generator=g)).to(dev)
+        ref, _ = hip_ops.encode(keys_t, p["perm"], p["centroids"], heavy=heavy, metric=metric, kernel=1)
+        got, _ = hip_ops.encode(keys_t, p["perm"], p["centroids"], heavy=heavy, metric=metric, kernel=kernel)
+        assert torch.equal(got, ref), "metric encode differs from the exact scan"
     # the search grid is built once per codebook (as a codec caches it); kernel 2 times the
     # exhaustive MFMA screen instead
     grid, grid_ms = None, None
-    if kernel in (0, 3):
+    if kernel in (0, 3) and not pro:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         grid = hip_ops.encode_grid(p["centroids"])
@@ -238,7 +248,7 @@ def _encode_workload(dev, kernel):
     from sunshape_amd import _native as N
 
     a, codes_k, pt_k, keep = hip_ops.encode_args(keys_t, p["perm"], p["centroids"], heavy=heavy, kernel=kernel,
-                                                 grid=grid)
+                                                 grid=grid, metric=metric)
     L = N.lib()
     stream = torch.cuda.current_stream(dev).cuda_stream
 
@@ -248,10 +258,11 @@ def _encode_workload(dev, kernel):
             N.check(rc)
 
     n = B * Hkv * S
-    algo = n * D * 2 + n * 32 + n * 4 * 2 * 2 + Hkv * 32 * 256 * 2 * 4
-    cfg = {"workload": "C5 encode (16 x 2 x 16384 bf16 keys, 28 VQ + 4 bf16 blocks of dim 2)", "keys": n,
+    algo = n * D * 2 + n * 32 + n * 4 * 2 * 2 + Hkv * 32 * 256 * 2 * 4 + (D * D * 4 if pro else 0)
+    cfg = {"workload": ("C5 encode (16 x 2 x 16384 bf16 keys, 28 VQ + 4 bf16 blocks of dim 2)" +
+                        (" under a SunShape-Pro block metric" if pro else "")), "keys": n,
            "head_dim": D, "block_dim": 2, "heavy_blocks": 4, "kernel": kernel,
-           "search": "grid" if grid is not None else "exhaustive", "grid_build_ms": grid_ms,
+           "search": "grid" if grid is not None else "exhaustive", "grid_build_ms": grid_ms, "metric": pro,
            "grid_bytes": None if grid is None else grid.numel()}
     return step, n, algo, cfg, None, "ssq_encode" if grid is None else "ssq_encode_grid"
 
@@ -428,7 +439,7 @@ def main():
     elif args.workload == "copycal":
         step, keys, algo_bytes, cfg, unit_data, kname = _copy_workload(dev)
     else:
-        step, keys, algo_bytes, cfg, unit_data, kname = _encode_workload(dev, args.kernel)
+        step, keys, algo_bytes, cfg, unit_data, kname = _encode_workload(dev, args.kernel, args.workload == "c5encpro")
 
     for _ in range(args.warmup):
         step()
@@ -474,12 +485,12 @@ def main():
     }
     if "q_heads" in cfg:  # every query head scores every key: q.k scores/s = keys/s x G
         line["qk_scores_per_s"] = line["value"] * (cfg["q_heads"] // cfg["kv_heads"])
-    if args.workload == "c5enc":
+    if args.workload in ("c5enc", "c5encpro"):
         # the exhaustive search's distance work (28 light blocks x 256 codewords x the 4-term
         # augmented dot product [-2x, |x|^2, 1] . [c, 1, |c|^2], a multiply-add per term); the grid
         # search evaluates a few codewords per block instead, so its roofline is HBM on the
         # algorithmic bytes and this figure is only a comparison
-        flop = keys * 28 * 256 * 2 * 4
+        flop = keys * 28 * 256 * 2 * 4 + (keys * 28 * 2 * 2 * 2 if cfg["metric"] else 0)  # + E_b x (2x2) per block
         tf = flop / (avg_ms * 1e-3) / 1e12
         line["unit"] = "keys/s"
         line["metric"] = "VQ encode: keys encoded/sec/GPU"
