@@ -1,7 +1,8 @@
 """vLLM-style paged KV cache for SunShape-compressed keys.
 
-No counterpart in the reference (it has no paged layout, SURVEY §0 trap 5); this
-is the caller on the write side of the decode kernel:
+No counterpart in the reference: its quantized keys are one contiguous [T, nb] code
+tensor per (batch, KV head) (sunshape/vllm_attn_backend.py:99-123), and it has no paged
+layout.  This is the caller on the write side of the decode kernel:
 
 * key pages   [P, Hkv, page, nb] uint8 codes, filled by the encode kernel through
   a slot mapping (token slot = page * page_size + offset), no dense key tensor;
