@@ -96,14 +96,18 @@ typedef struct ssq_decode_args {
     /* outputs */
     void* out; int64_t o_sb, o_sh, o_sl;      /* [B, Hq, Lq, Dv] in v_dtype; NULL for scores-only */
     float* lse;                                /* [B, Hq, Lq] fp32 contiguous or NULL */
-    float* scores; int64_t s_sb, s_sh, s_sl;  /* raw logits [B, Hq, Lq, T] fp32 (t contiguous) or NULL */
+    float* scores; int64_t s_sb, s_sh, s_sl;  /* raw logits [B, Hq, Lq, T] fp32 (t contiguous) or NULL;
+                                                 paged: entries t >= seq_lens[b] are not written */
     /* tuning: 0 = library heuristic */
     int32_t num_splits;
     int32_t kernel;      /* 0 auto, 1 generic LUT/VALU kernel, 2 MFMA paged kernel, 3 MFMA contiguous kernel */
     /* code storage: 0 = one uint8 per block (c_* strides in bytes); 1..8 = packing in
      * uint32 words, vpe = 32 / code_bits codes per word, block blk = p*vpe + v at bits
      * [v*code_bits, (v+1)*code_bits) of word p (the layout of sunshape/triton_kernels.py:213-283);
-     * c_* strides then count words.  Packed codes take the generic kernel. */
+     * c_* strides then count words.  8-bit words are read as byte rows; 6-bit words run on
+     * every MFMA decode kernel and 4-bit words on the contiguous and paged MFMA-scores ones
+     * (without mask or passthrough); other widths take the generic kernel.  Results equal the
+     * same kernel's launch over uint8 codes bit for bit. */
     int32_t code_bits;
 } ssq_decode_args;
 
