@@ -165,3 +165,26 @@ def test_paged_mfma_decode_over_packed_codes(bits, bd, nc, Hq, D, T):
                                        cb.perm.numpy(), scale, "bf16", "bf16", return_scores=True)
     assert_rel(np_of(o8), ref, BF16_TOL, "paged packed decode vs oracle")
     assert_rel(np_of(s8[..., :T]), ref_s, SCORE_TOL, "paged packed scores vs oracle")
+
+
+@pytest.mark.parametrize("Hq", [8, 2])
+def test_codes_past_the_codebook_read_its_last_codeword(Hq):
+    """Byte codes >= n_centroids (invalid input) read the last codeword in every decode kernel:
+    generic and contiguous MFMA over the contiguous layout, generic and paged (64-codeword LUT at
+    4 rows per KV head, MFMA scores at 1) over pages.  Checked against the oracle on clamped codes."""
+    log(f"codes past the codebook Hq={Hq}")
+    nc = 64
+    cb, codes, q, v = _case(nc=nc, bd=2, Hq=Hq, T=320, seed=77)
+    codes = torch.randint(0, 256, codes.shape, generator=torch.Generator().manual_seed(78), dtype=torch.uint8)
+    perm, cent = cb.perm.to(DEV), cb.centroids.to(DEV)
+    scale = 1 / math.sqrt(64)
+    ref = O.decode_attention(q.float().numpy(), np.minimum(codes.numpy(), nc - 1), v.float().numpy(),
+                             cb.centroids.numpy(), cb.perm.numpy(), scale, "bf16", "bf16")
+    qd = q.to(DEV)
+    for kernel in (1, 3):
+        o = hip_ops.decode(qd, codes.to(DEV), v.to(DEV), perm, cent, scale=scale, kernel=kernel)
+        assert_rel(np_of(o), ref, BF16_TOL, f"contiguous kernel {kernel}")
+    cpd, vpd, tbl, lens = _pages(codes, v, seed=79)
+    for kernel in (1, 2):
+        o = hip_ops.decode(qd, cpd, vpd, perm, cent, scale=scale, block_table=tbl, seq_lens=lens, kernel=kernel)
+        assert_rel(np_of(o), ref, BF16_TOL, f"paged kernel {kernel}")
