@@ -119,6 +119,17 @@ size_t ssq_decode_workspace_size(const ssq_decode_args* a);
  * softmax and cast :251, P.V :252) for all batches and KV heads in one call. */
 int ssq_decode(const ssq_decode_args* a, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ssq_decode without device allocation.  No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops that forbid
+ * hipMalloc).  The caller passes inputs and outputs only; the split workspace ssq_decode would
+ * take from the caller lives in a library-owned scratch array of SSQ_NOALLOC_SCRATCH_BYTES per
+ * device (held until the process ends).  A problem whose ssq_decode_workspace_size exceeds it
+ * fails with SSQ_ERR_UNSUPPORTED before anything is launched.  Calls and results are otherwise
+ * those of ssq_decode (same kernels).  Every call on one device shares that device's array:
+ * calls that overlap on one device race and must be serialised by the caller. */
+#define SSQ_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int ssq_decode_noalloc(const ssq_decode_args* a, void* stream);
+
 /* Scores only (a->v == NULL, a->scores != NULL): scores[r, t] = q_r . k_hat_t (unscaled
  * unless has_scale).  Replaces sunshape/triton_kernels.py:570-609 and codec.py:403-422. */
 int ssq_attention_scores(const ssq_decode_args* a, void* stream);

@@ -31,11 +31,13 @@ SSQ_CONTIGUOUS, SSQ_PAGED = 0, 1
 DTYPE_CODE = {torch.float32: SSQ_F32, torch.bfloat16: SSQ_BF16, torch.float16: SSQ_F16}
 
 ABI_VERSION = 4  # SSQ_ABI_VERSION in include/sunshape_amd.h
+NOALLOC_SCRATCH_BYTES = 32 << 20  # SSQ_NOALLOC_SCRATCH_BYTES
 
 # every function include/sunshape_amd.h declares
 EXPORTED_SYMBOLS = (
     "ssq_decode_workspace_size",
     "ssq_decode",
+    "ssq_decode_noalloc",
     "ssq_attention_scores",
     "ssq_lut_build",
     "ssq_encode",
@@ -125,6 +127,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ssq_decode_workspace_size.restype = ctypes.c_size_t
     lib.ssq_decode.argtypes = [P(DecodeArgs), _vp, ctypes.c_size_t, _vp]
     lib.ssq_decode.restype = ctypes.c_int
+    lib.ssq_decode_noalloc.argtypes = [P(DecodeArgs), _vp]
+    lib.ssq_decode_noalloc.restype = ctypes.c_int
     lib.ssq_attention_scores.argtypes = [P(DecodeArgs), _vp]
     lib.ssq_attention_scores.restype = ctypes.c_int
     lib.ssq_lut_build.argtypes = [_vp, _i32, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _vp, _vp]

@@ -226,7 +226,7 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
            heavy: Optional[Sequence[bool]] = None, pt: Optional[torch.Tensor] = None, pt_dense: bool = False,
            block_table: Optional[torch.Tensor] = None, seq_lens: Optional[torch.Tensor] = None,
            return_lse: bool = False, return_scores: bool = False,
-           num_splits: int = 0, kernel: int = 0, code_bits: int = 0):
+           num_splits: int = 0, kernel: int = 0, code_bits: int = 0, no_alloc: bool = False):
     """Fused VQ-key decode attention for all batches and KV heads in one launch.
 
     q [B, Hq, Lq, D].  Contiguous layout: codes [B, Hkv, T, nb] uint8, v [B, Hkv, T, Dv],
@@ -238,6 +238,8 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
     Returns out [B, Hq, Lq, Dv] in v's dtype, plus lse [B, Hq, Lq] / raw scores [B, Hq, Lq, T]
     (fp32) when requested; paged, T = max_pages * page and a sequence's slots past its length
     hold -inf.
+    no_alloc: run through ssq_decode_noalloc (split workspace in the library's per-device scratch
+    instead of a torch allocation; calls that overlap on one device race).
     Reference: sunshape/vllm_attn_backend.py:216-253.
     """
     for name, t in (("query", q), ("codes", codes), ("value", v)):
@@ -316,9 +318,12 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
     )
     a.heavy_mask[0], a.heavy_mask[1] = hm
     L = N.lib()
-    ws_bytes = L.ssq_decode_workspace_size(ctypes.byref(a))
-    ws = torch.empty((max(ws_bytes, 1),), device=q.device, dtype=torch.uint8) if ws_bytes else None
-    N.check(L.ssq_decode(ctypes.byref(a), N.ptr(ws), ws_bytes, N.stream_of(q.device)))
+    if no_alloc:
+        N.check(L.ssq_decode_noalloc(ctypes.byref(a), N.stream_of(q.device)))
+    else:
+        ws_bytes = L.ssq_decode_workspace_size(ctypes.byref(a))
+        ws = torch.empty((max(ws_bytes, 1),), device=q.device, dtype=torch.uint8) if ws_bytes else None
+        N.check(L.ssq_decode(ctypes.byref(a), N.ptr(ws), ws_bytes, N.stream_of(q.device)))
     res = [out]
     if return_lse:
         res.append(lse)
