@@ -56,15 +56,36 @@ def _compile(hipcc: str, src: str, obj: str) -> None:
         sys.stderr.write(err + "\n")
 
 
-def build(verbose: bool = False) -> str:
-    """Compile all HIP sources and link the shared library; returns its path."""
+def _stale(src: str, obj: str, dep_mtime: float) -> bool:
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    return t < os.path.getmtime(src) or t < dep_mtime
+
+
+def build(verbose: bool = False, incremental: bool = False) -> str:
+    """Compile all HIP sources and link the shared library; returns its path.
+
+    incremental: recompile only sources whose object is older than the source or than any
+    header under csrc/ or include/ (a development shortcut; the default rebuilds everything).
+    """
     hipcc = _hipcc()
     obj_dir = os.path.join(OUT_DIR, "obj")
     os.makedirs(obj_dir, exist_ok=True)
     srcs = sources()
     objs = [os.path.join(obj_dir, os.path.basename(s)[:-4] + ".o") for s in srcs]
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        list(ex.map(lambda so: _compile(hipcc, *so), zip(srcs, objs)))
+    work = list(zip(srcs, objs))
+    if incremental:
+        inc = os.path.join(os.path.dirname(HERE), "include")
+        hdrs = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+        hdrs += [os.path.join(inc, f) for f in os.listdir(inc) if f.endswith(".h")]
+        dep = max((os.path.getmtime(h) for h in hdrs), default=0.0)
+        work = [(s, o) for s, o in work if _stale(s, o, dep)]
+        if verbose:
+            print("compiling:", " ".join(os.path.basename(s) for s, _ in work) or "(nothing)")
+    if work:
+        with cf.ThreadPoolExecutor(max_workers=min(8, len(work))) as ex:
+            list(ex.map(lambda so: _compile(hipcc, *so), work))
     tmp = LIB_PATH + ".tmp"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -77,4 +98,4 @@ def build(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv[1:])
