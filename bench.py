@@ -9,7 +9,8 @@ batch with inputs resident in HBM.
 Prints ONE JSON line: keys scored/s (B*Hkv*T per step / time), achieved HBM GB/s on the
 algorithmic bytes and its fraction of the 8 TB/s peak, the kernel's average launch time
 from HIP events on its own stream, the same launch's time with cold caches (a 1 GiB flush
-before each), and a bounded CPU-oracle baseline timed on the host.
+before each), and a bounded CPU baseline: the reference's eager torch decode path on the
+host's cores (oracle/torch_eager.py).
 
   python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c5encpro] [--no-cpu]
 """
@@ -349,53 +350,67 @@ def _copy_workload(dev):
 
 
 # ----------------------------------------------------------------------------- CPU baseline
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def _cpu_baseline(unit_data, seconds):
-    """The oracle's eager restatement of the reference decode path, one (batch, KV head) at a time."""
+    """The reference's eager PyTorch decode path on the host's cores (oracle/torch_eager.py).
+
+    One (batch, KV head) unit at a time, as sunshape/vllm_attn_backend.py:228-252 loops: per-block
+    dequantize, fp32 q . k_hat^T, softmax, cast to the value dtype, P.V.  Units are drawn at random
+    from the workload until about ``seconds`` of CPU work is timed; only the torch calls are timed
+    (the unit's codes and values are copied to the host outside the timed region).  keys/s is the
+    sample's rate, i.e. the whole batch's rate extrapolated from the sampled units.
+    """
     import numpy as np
     import torch
 
-    from oracle import vq_oracle as O
+    from oracle import torch_eager as TE
 
-    try:
-        from threadpoolctl import threadpool_limits
-    except Exception:  # pragma: no cover
-        threadpool_limits = None
     p, paged = unit_data
     G = p.meta["Hq"] // p.meta["Hkv"] if "Hq" in p.meta else 7
     T = p.meta["T"]
-    perm, cent = p["perm"].cpu().numpy(), p["centroids"].cpu().numpy()
-    q = p["q"].float().cpu().numpy()
+    perm, cent = p["perm"].cpu(), p["centroids"].cpu()
+    inv = torch.argsort(perm, dim=-1)
+    q = p["q"].cpu()
+    threads = torch.get_num_threads()
     rng = np.random.default_rng(0)
     units, elapsed = 0, 0.0
-    import contextlib
-
-    limit = threadpool_limits(limits=1) if threadpool_limits else contextlib.nullcontext()
-    with limit:
-        while elapsed < seconds and units < 4096:
-            b = int(rng.integers(p.meta["B"]))
-            kv = int(rng.integers(p.meta["Hkv"]))
-            if paged:
-                pages = p["block_table"][b].long()
-                codes = p["code_pages"][pages][:, kv].reshape(-1, p["code_pages"].shape[-1]).cpu().numpy()
-                v = p["v_pages"][pages][:, kv].permute(0, 2, 1).reshape(-1, p["v_pages"].shape[2]).float().cpu().numpy()
-            else:
-                codes = p.tensors.get("codes_u8", p["codes"])[b, kv].cpu().numpy()  # unpacked for the oracle
-                v = p["v"][b, kv].float().cpu().numpy()
-            hv, ptv = None, None
-            if "pt" in p.tensors:  # SunShape-Mixed: dense passthrough values for the oracle
-                hv = np.asarray(p["heavy"].tolist())
-                ptv = np.zeros(codes.shape + (cent.shape[-1],), np.float32)
-                ptv[:, hv] = p["pt"][b, kv].float().cpu().numpy()
-                ptv = ptv[None, None]
-            qu = q[b, kv * G:(kv + 1) * G][None]
-            t0 = time.perf_counter()
-            O.decode_attention(qu, codes[None, None], v[None, None], cent[kv][None], perm[kv][None], p.meta["scale"],
-                               "bf16", "bf16", heavy=hv, pt_values=ptv)
-            elapsed += time.perf_counter() - t0
-            units += 1
-    return {"value": units * T / elapsed, "unit": "keys/s", "cores": 1, "kind": "port",
-            "sample": f"{units} (batch, KV head) units x {T} keys, numpy oracle (dequantize, LUT scores, fp32 "
-                      f"softmax, bf16 cast, P.V), single thread, {elapsed:.1f} s"}
+    n_units = p.meta["B"] * p.meta["Hkv"]
+    wall0 = time.perf_counter()
+    while elapsed < seconds and units < 4096 and time.perf_counter() - wall0 < 4 * seconds:
+        b = int(rng.integers(p.meta["B"]))
+        kv = int(rng.integers(p.meta["Hkv"]))
+        if paged:
+            pages = p["block_table"][b].long()
+            codes = p["code_pages"][pages][:, kv].reshape(-1, p["code_pages"].shape[-1]).cpu()
+            v = p["v_pages"][pages][:, kv].permute(0, 2, 1).reshape(-1, p["v_pages"].shape[2]).cpu()
+        else:
+            codes = p.tensors.get("codes_u8", p["codes"])[b, kv].cpu()  # byte codes (unpacked)
+            v = p["v"][b, kv].cpu()
+        heavy, ptv = None, None
+        if "pt" in p.tensors:  # SunShape-Mixed: the reference's dense fp32 passthrough layout
+            heavy = [bool(x) for x in p["heavy"].tolist()]
+            ptv = torch.zeros(codes.shape + (cent.shape[-1],), dtype=torch.float32)
+            ptv[:, torch.tensor(heavy)] = p["pt"][b, kv].float().cpu()
+        qu = q[b, kv * G:(kv + 1) * G]
+        t0 = time.perf_counter()
+        TE.decode_unit(qu, codes, v, cent[kv], inv[kv], p.meta["scale"], heavy, ptv)
+        elapsed += time.perf_counter() - t0
+        units += 1
+    return {"value": units * T / elapsed, "unit": "keys/s", "cores": threads, "kind": "port",
+            "host_cpus": os.cpu_count(), "cpu_model": _cpu_model(),
+            "sample": f"{units} (batch, KV head) units drawn with replacement from the workload's {n_units}, x {T} keys each, eager torch restatement of the "
+                      f"reference decode path (per-block dequantize, fp32 q.k_hat^T, softmax, bf16 cast, P.V; "
+                      f"sunshape/vllm_attn_backend.py:228-252) on {threads} torch threads, {elapsed:.1f} s timed; "
+                      f"keys/s extrapolates the sampled units' rate to the batch"}
 
 
 def _cold_launches(step, n, algo_bytes, dev):

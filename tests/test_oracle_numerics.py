@@ -262,6 +262,25 @@ def test_decode_matches_torch_call_sequence():
     assert np.mean(got[0] == ref) > 0.9
 
 
+def test_torch_eager_baseline_matches_oracle():
+    """oracle/torch_eager.py (bench.py's CPU baseline) computes what the oracle computes."""
+    from oracle import torch_eager as TE
+
+    rng = _rng(16)
+    q, codes, v, cents, perms = _decode_problem(rng, B=1, Hq=6, Hkv=2, T=900)
+    ref = O.decode_attention(q, codes, v, cents, perms, 1 / math.sqrt(64), "bf16", "bf16")
+    for kv in range(2):
+        inv = torch.from_numpy(O.invert_permutation(perms[kv]))
+        k_hat = TE.dequantize(torch.from_numpy(codes[0, kv]), torch.from_numpy(cents[kv]), inv)
+        assert np.array_equal(k_hat.numpy(), O.dequantize(codes[0, kv], cents[kv], perms[kv]))
+        got = TE.decode_unit(torch.from_numpy(q[0, 3 * kv:3 * kv + 3]).to(torch.bfloat16),
+                             torch.from_numpy(codes[0, kv]), torch.from_numpy(v[0, kv]).to(torch.bfloat16),
+                             torch.from_numpy(cents[kv]), inv, 1 / math.sqrt(64)).float().numpy()
+        r = ref[0, 3 * kv:3 * kv + 3]
+        assert np.abs(got - r).max() <= 2e-2 * np.abs(r).max()
+        assert np.mean(got == r) > 0.9
+
+
 # ----------------------------------------------------------------------------- paging, merging
 def test_page_gather_inverts_page_scatter():
     rng = _rng(16)
