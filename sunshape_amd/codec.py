@@ -333,7 +333,14 @@ class SunShapeBlockCodec(torch.nn.Module):
         qd = torch.softmax((q_test @ k_hat.T) / scale, dim=-1)
         return (p * (torch.log(p + 1e-9) - torch.log(qd + 1e-9))).sum(dim=-1).mean().item()
 
-    def _load_from_state_dict(self, *args, **kwargs):
-        super()._load_from_state_dict(*args, **kwargs)
+    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        # a per-KV-head SunShape-Pro metric is stored as [Hkv, D, D] (from_buffers); size E / E_inv
+        # from the payload so such a codec reloads (the reference's layout is [D, D])
+        for name in ("E", "E_inv"):
+            t = state_dict.get(prefix + name)
+            cur = getattr(self, name)
+            if t is not None and t.ndim == 3 and t.shape[-2:] == cur.shape[-2:] and tuple(t.shape) != tuple(cur.shape):
+                setattr(self, name, torch.empty(tuple(t.shape), device=cur.device, dtype=cur.dtype))
+        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
         self._heavy_cache = None
         self._grid_cache = {}

@@ -205,6 +205,27 @@ def test_bundle_roundtrip_and_extension(tmp_path):
         SunShapeBundle.load(tmp_path / "bad.pt", device="cpu")
 
 
+def test_bundle_roundtrip_per_kv_head_metric(tmp_path):
+    """A SunShape-Pro codec with one block metric per KV head ([Hkv, D, D]) saves and reloads."""
+    g = torch.Generator().manual_seed(3)
+    cent = torch.randn(2, 8, 256, 8, generator=g)
+    perm = torch.stack([torch.randperm(64, generator=g) for _ in range(2)])
+    E = torch.eye(64).expand(2, 64, 64) + 0.1 * torch.randn(2, 64, 64, generator=g)
+    c = SunShapeBlockCodec.from_buffers(perm, cent, mode="profileperm_localmetric_dsq", metric=E, device="cpu")
+    assert c.E.shape == (2, 64, 64) and c.E_inv.shape == (2, 64, 64)
+    b = SunShapeBundle("model", [3], 1.0, 8, "profileperm_localmetric_dsq", 1, 0, 0, {3: c})
+    b2 = SunShapeBundle.load(b.save(tmp_path / "pro.pt"), device="cpu")
+    c2 = b2.codecs[3]
+    for k, v in c.state_dict().items():
+        assert torch.equal(c2.state_dict()[k], v), k
+    assert torch.equal(c2.encode_metric(1), E[1])
+    # the reference's one-metric-per-layer layout still loads into [D, D]
+    c1 = SunShapeBlockCodec.from_buffers(perm[0], cent[0], mode="profileperm_localmetric_dsq", metric=E[0], device="cpu")
+    b3 = SunShapeBundle.load(SunShapeBundle("m", [0], 1.0, 8, "x", 1, 0, 0, {0: c1}).save(tmp_path / "one.pt"),
+                             device="cpu")
+    assert b3.codecs[0].E.shape == (64, 64) and torch.equal(b3.codecs[0].E, E[0])
+
+
 def test_mode_aliases_and_block_dim():
     assert resolve_mode_alias("sunshape_mixed") == "profileperm_mixed_precision"
     assert default_block_dim(1.0) == 8 and default_block_dim(4.0) == 2
