@@ -20,6 +20,7 @@
  *   ssq_encode            <- sunshape/codec.py:362-385 SunShapeBlockCodec.quantize and
  *                            sunshape/vllm_attn_backend.py:101-123 quantize_key_states
  *   ssq_dequantize        <- sunshape/codec.py:387-398 SunShapeBlockCodec.dequantize
+ *   ssq_transform_rows    <- sunshape/codec.py:247-259 _forward/_inverse_transform (rotated mode)
  */
 #ifndef SUNSHAPE_AMD_H
 #define SUNSHAPE_AMD_H
@@ -31,7 +32,7 @@
 extern "C" {
 #endif
 
-#define SSQ_ABI_VERSION 4
+#define SSQ_ABI_VERSION 5
 
 enum ssq_status {
     SSQ_OK = 0,
@@ -144,7 +145,7 @@ int ssq_lut_build(const void* q, int32_t q_dtype, int64_t q_sr, int32_t rows, in
 /*
  * Nearest-codeword encode of keys [B, Hkv, S, D] (k[b*k_sb + kv*k_sh + s*k_ss + d]).
  * codes[b, kv, s, blk] = argmin_c sqrt(max(0, |x_blk|^2 - 2 x_blk.c + |c|^2)) evaluated
- * with torch.cdist's mm formulation, lowest index on ties.  With a block metric
+ * with torch.cdist's mm formulation (or its direct one, direct_dist), lowest index on ties.  With a block metric
  * (SunShape-Pro, metric != NULL: E [D, D] fp32 row-major at metric + kv*metric_sh, of which
  * only the diagonal bd x bd blocks E_b are read, as codec.py:375-376 slices them) x_blk and
  * every codeword c are first mapped to E_b x and E_b c (y_k = sum_j E_b[k][j] x_j, j
@@ -171,6 +172,11 @@ typedef struct ssq_encode_args {
     const int64_t* slot_mapping; int64_t sm_sb; int32_t page_size;
     int32_t kernel;      /* 0 auto, 1 VALU exact scan, 2 MFMA screen + exact certification, 3 grid search */
     const void* grid; uint64_t grid_bytes;  /* optional search grid from ssq_encode_grid_build (or NULL) */
+    /* 1: torch.cdist's direct evaluation, sqrt(sum_k (x_k - c_k)^2) with the rounded squares summed
+     * in k order, which torch takes in place of the mm formulation when both of its inputs have at
+     * most 25 rows (the reference quantizing <= 25 keys per call with <= 25 codewords).  Runs on
+     * the exact scan (kernel 0 or 1; 2 and 3 are refused). */
+    int32_t direct_dist;
 } ssq_encode_args;
 
 int ssq_encode(const ssq_encode_args* a, void* stream);
@@ -191,6 +197,17 @@ int ssq_encode(const ssq_encode_args* a, void* stream);
  */
 uint64_t ssq_encode_grid_bytes(const ssq_encode_args* a);
 int ssq_encode_grid_build(const ssq_encode_args* a, void* grid, uint64_t grid_bytes, void* stream);
+
+/* Dense transform of rows, fp32 out [rows, dim] (row stride o_sr):
+ *   out[r, j] = sum_k xs[r, k] * M[j, k]   (transpose 0: x @ M^T)   or   sum_k xs[r, k] * M[k, j]
+ *   (transpose 1: x @ M), k ascending, the first product rounded, then fused multiply-adds;
+ * xs = x (x_dtype, row stride x_sr), or round_to_x_dtype(x * scale) when has_scale (ssq_decode's
+ * query scaling).  M: [dim, dim] fp32 row-major.
+ * Replaces the rotated mode of sunshape/codec.py:247-259: _forward_transform (x @ rotation.T)
+ * before scoring and encoding, _inverse_transform (x @ rotation) after dequantizing. */
+int ssq_transform_rows(const void* x, int32_t x_dtype, int64_t x_sr, int64_t rows, int32_t dim,
+                       int32_t has_scale, float scale, const float* mat, int32_t transpose,
+                       float* out, int64_t o_sr, void* stream);
 
 /* k_hat[t, j] (original basis, fp32 [T, D] with row stride o_st) from codes [T, nb]
  * (row stride c_st) and optional passthrough pt (dense [T, nb, bd] fp32 when pt_dense,

@@ -22,6 +22,11 @@
  * multiply-adds, starting from the first product (checked bit-for-bit against
  * torch's CPU matmul in tests/test_oracle_encode.py).
  * sqrt is the correctly rounded IEEE square root (see that test for why).
+ * When both of cdist's inputs have at most 25 rows, ATen evaluates the distance directly
+ * (the cdist_impl branch that skips _euclidean_dist): sqrt(sum_k (x_k - c_k)^2), each square
+ * rounded and summed in k order -- the `direct` flag (checked in tests/test_oracle_encode.py
+ * against torch's scalar CPU kernel bit for bit).
+ * Rotated mode (sunshape/codec.py:247-259, x @ rotation.T): oracle_transform_rows below.
  */
 #include <math.h>
 #include <stddef.h>
@@ -47,6 +52,18 @@ static float mm_dist2(const float* x, float xn, const float* c, float cn, int bd
     return acc;
 }
 
+/* Direct pre-sqrt distance: rounded squares of the differences, summed in k order. */
+static float direct_dist2(const float* x, const float* c, int bd) {
+    float d = x[0] - c[0];
+    float s = d * d;
+    for (int k = 1; k < bd; ++k) {
+        d = x[k] - c[k];
+        float t = d * d;
+        s = s + t;
+    }
+    return s;
+}
+
 /* y[k] = sum_j e[k*ld + j] * x[j], j ascending, first product rounded, then FMAs. */
 static void metric_apply(const float* e, int ld, const float* x, int bd, float* y) {
     for (int k = 0; k < bd; ++k) {
@@ -56,18 +73,23 @@ static void metric_apply(const float* e, int ld, const float* x, int bd, float* 
     }
 }
 
-/* Distance matrix for one block: e2[i*nc+j] = pre-sqrt value, d[i*nc+j] = sqrt(clamp_min(., 0)). */
-void oracle_block_dist(const float* x, int64_t n, const float* c, int nc, int bd, float* e2, float* d) {
+/* Distance matrix for one block: e2[i*nc+j] = pre-sqrt value, d[i*nc+j] = sqrt(clamp_min(., 0)).
+ * direct != 0: the direct evaluation in place of the mm formulation. */
+void oracle_block_dist_ex(const float* x, int64_t n, const float* c, int nc, int bd, int direct, float* e2, float* d) {
     for (int64_t i = 0; i < n; ++i) {
         const float* xi = x + i * bd;
         float xn = sq_norm(xi, bd);
         for (int j = 0; j < nc; ++j) {
             const float* cj = c + (int64_t)j * bd;
-            float v = mm_dist2(xi, xn, cj, sq_norm(cj, bd), bd);
+            float v = direct ? direct_dist2(xi, cj, bd) : mm_dist2(xi, xn, cj, sq_norm(cj, bd), bd);
             if (e2) e2[i * nc + j] = v;
             if (d) d[i * nc + j] = sqrtf(v > 0.0f ? v : 0.0f);
         }
     }
+}
+
+void oracle_block_dist(const float* x, int64_t n, const float* c, int nc, int bd, float* e2, float* d) {
+    oracle_block_dist_ex(x, n, c, nc, bd, 0, e2, d);
 }
 
 /*
@@ -79,9 +101,30 @@ void oracle_block_dist(const float* x, int64_t n, const float* c, int nc, int bd
  *   codes     uint8 [n, nb] out
  *   pt        fp32 [n, nb, bd] out or NULL; zeros on light blocks (dense, as the reference)
  */
-void oracle_encode_metric(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
-                          const float* metric, int nb, int nc, int bd, const uint8_t* heavy, uint8_t* codes,
-                          float* pt) {
+/*
+ * Rows through a dense D x D matrix: out[r, j] = sum_k x[r, k] * m_jk, m_jk = M[j*D + k]
+ * (transpose 0: x @ M^T, the rotated mode's _forward_transform) or M[k*D + j] (transpose 1:
+ * x @ M, its _inverse_transform); k ascending, the first product rounded, then fused
+ * multiply-adds (torch's matmul leaves its order unspecified; this is the order the HIP
+ * transform uses).
+ */
+void oracle_transform_rows(const float* x, int64_t n, int D, const float* M, int transpose, float* out) {
+    for (int64_t r = 0; r < n; ++r) {
+        const float* xr = x + r * D;
+        for (int j = 0; j < D; ++j) {
+            float acc = 0.0f;
+            for (int k = 0; k < D; ++k) {
+                const float m = transpose ? M[(int64_t)k * D + j] : M[(int64_t)j * D + k];
+                acc = k == 0 ? xr[0] * m : fmaf(xr[k], m, acc);
+            }
+            out[r * D + j] = acc;
+        }
+    }
+}
+
+void oracle_encode_ex(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
+                      const float* metric, int direct, int nb, int nc, int bd, const uint8_t* heavy, uint8_t* codes,
+                      float* pt) {
     float* cn = (float*)malloc(sizeof(float) * (size_t)nb * (size_t)nc);
     float* xp = (float*)malloc(sizeof(float) * (size_t)D);
     float* cm = NULL; /* codebook in the metric space, C_b @ E_b^T */
@@ -119,7 +162,8 @@ void oracle_encode_metric(const float* keys, int64_t n, int D, const int64_t* pe
             float best = INFINITY;
             int best_j = 0;
             for (int j = 0; j < nc; ++j) {
-                float v = mm_dist2(xb, xn, cb + (int64_t)j * bd, cn[b * nc + j], bd);
+                float v = direct ? direct_dist2(xb, cb + (int64_t)j * bd, bd)
+                                 : mm_dist2(xb, xn, cb + (int64_t)j * bd, cn[b * nc + j], bd);
                 float dj = sqrtf(v > 0.0f ? v : 0.0f);
                 if (dj < best) { /* strict: the first minimum wins */
                     best = dj;
@@ -134,7 +178,13 @@ void oracle_encode_metric(const float* keys, int64_t n, int D, const int64_t* pe
     free(cm);
 }
 
+void oracle_encode_metric(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
+                          const float* metric, int nb, int nc, int bd, const uint8_t* heavy, uint8_t* codes,
+                          float* pt) {
+    oracle_encode_ex(keys, n, D, perm, cent, metric, 0, nb, nc, bd, heavy, codes, pt);
+}
+
 void oracle_encode(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
                    int nb, int nc, int bd, const uint8_t* heavy, uint8_t* codes, float* pt) {
-    oracle_encode_metric(keys, n, D, perm, cent, NULL, nb, nc, bd, heavy, codes, pt);
+    oracle_encode_ex(keys, n, D, perm, cent, NULL, 0, nb, nc, bd, heavy, codes, pt);
 }

@@ -21,7 +21,11 @@ Pinning (tests/test_oracle_*.py) -- what checks each function:
   decode_attention            fp64 textbook softmax attention; torch.softmax/matmul
                               (the library calls the reference makes)
   encode (C library)          bit-for-bit against torch.cdist(...).argmin(-1) and
-                              torch's pre-sqrt mm formulation
+                              torch's pre-sqrt mm formulation; direct mode against torch's
+                              scalar cdist kernel (<= 25 rows) bit for bit
+  transform_rows              permutation matrices reproduce the gather exactly; orthogonal R
+                              gives q . inv(k) == fwd(q) . k; R vs R^T distinguished; torch
+                              matmul within fp32 rounding
   gather_pages                inverse of the page scatter used to build the layout
 """
 
@@ -152,10 +156,13 @@ def scores_from_lut(lut: np.ndarray, codes: np.ndarray,
 
 def dequantize(codes: np.ndarray, centroids: np.ndarray, perm: np.ndarray,
                heavy: Optional[np.ndarray] = None,
-               pt_values: Optional[np.ndarray] = None) -> np.ndarray:
+               pt_values: Optional[np.ndarray] = None,
+               rotation: Optional[np.ndarray] = None) -> np.ndarray:
     """k_hat = inverse_transform(concat_b C[b, codes[:, b]] or passthrough).
 
     sunshape/codec.py:387-398.  Returns fp32 [T, D] in the original basis.
+    rotation: the rotated mode's R [D, D]; the inverse transform is then k_hat @ R
+    (sunshape/codec.py:257-258) and ``perm`` is ignored.
     """
     codes = np.asarray(codes).astype(np.int64)
     c = np.asarray(centroids, dtype=np.float32)
@@ -169,17 +176,26 @@ def dequantize(codes: np.ndarray, centroids: np.ndarray, perm: np.ndarray,
             k_hat[:, b * bd:(b + 1) * bd] = pt_values[:, b, :]
         else:
             k_hat[:, b * bd:(b + 1) * bd] = c[b][codes[:, b]]
+    if rotation is not None:
+        return transform_rows(k_hat, rotation, transpose=True)
     return inverse_transform(k_hat, perm)
 
 
 def attention_scores(q: np.ndarray, codes: np.ndarray, centroids: np.ndarray, perm: np.ndarray,
                      heavy: Optional[np.ndarray] = None,
-                     pt_values: Optional[np.ndarray] = None) -> np.ndarray:
+                     pt_values: Optional[np.ndarray] = None,
+                     rotation: Optional[np.ndarray] = None) -> np.ndarray:
     """``sunshape_attention_scores(codec, q, quantized)``: unscaled fp32 [R, T].
 
     sunshape/triton_kernels.py:570-609 with the precomputed-LUT kernel
     (:416-482): q -> forward transform -> fp32 -> LUT -> gather-sum.
+    rotation: the rotated mode's R [D, D]; the forward transform is then q @ R^T
+    (sunshape/codec.py:250-251, applied at triton_kernels.py:427-428) and ``perm`` is ignored.
     """
+    if rotation is not None:
+        qp = transform_rows(np.asarray(q, dtype=np.float32), rotation)
+        lut = lut_build(qp, centroids)
+        return scores_from_lut(lut, codes, heavy, qp, pt_values)
     qp = forward_transform(np.asarray(q, dtype=np.float32), perm)
     lut = lut_build(qp, centroids)
     return scores_from_lut(lut, codes, heavy, qp, pt_values)
@@ -216,7 +232,8 @@ def decode_attention(q: np.ndarray, codes: np.ndarray, v: np.ndarray,
                      mask: Optional[np.ndarray] = None,
                      heavy: Optional[np.ndarray] = None,
                      pt_values: Optional[np.ndarray] = None,
-                     return_scores: bool = False):
+                     return_scores: bool = False,
+                     rotation: Optional[np.ndarray] = None):
     """Fused-decode semantics of ``_apply_quantized_attention``.
 
     sunshape/vllm_attn_backend.py:216-253, one (batch, kv head) at a time:
@@ -231,6 +248,7 @@ def decode_attention(q: np.ndarray, codes: np.ndarray, v: np.ndarray,
     pt_values: [B, Hkv, T, nb, bd] dense (zeros on light blocks) or None.
     Returns out fp32 [B, Hq, Lq, Dv] (already rounded to vdtype), and when
     return_scores: scores fp32 [B, Hq, Lq, T] and lse fp32 [B, Hq, Lq].
+    rotation: the rotated mode's R [D, D] in place of the permutation (attention_scores).
     """
     q = np.asarray(q, dtype=np.float32)
     B, Hq, Lq, D = q.shape
@@ -247,7 +265,7 @@ def decode_attention(q: np.ndarray, codes: np.ndarray, v: np.ndarray,
             qs = query_scale(q[b, kv * G:(kv + 1) * G], scale, qdtype)      # [G, Lq, D]
             qf = qs.reshape(G * Lq, D)
             pt = None if pt_values is None else pt_values[b, kv]
-            s = attention_scores(qf, codes[b, kv], cen, pm, heavy, pt).reshape(G, Lq, T)
+            s = attention_scores(qf, codes[b, kv], cen, pm, heavy, pt, rotation).reshape(G, Lq, T)
             ms = select_mask_slice(mask, b, kv * G, (kv + 1) * G, B)
             if ms is not None:
                 s = (s + np.asarray(ms, dtype=np.float32)).astype(np.float32)
@@ -339,6 +357,13 @@ def _lib():
         lib.oracle_encode_metric.restype = None
         lib.oracle_block_dist.argtypes = [vp, ctypes.c_int64, vp, ctypes.c_int, ctypes.c_int, vp, vp]
         lib.oracle_block_dist.restype = None
+        lib.oracle_block_dist_ex.argtypes = [vp, ctypes.c_int64, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
+        lib.oracle_block_dist_ex.restype = None
+        lib.oracle_encode_ex.argtypes = [vp, ctypes.c_int64, ctypes.c_int, vp, vp, vp, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, vp]
+        lib.oracle_encode_ex.restype = None
+        lib.oracle_transform_rows.argtypes = [vp, ctypes.c_int64, ctypes.c_int, vp, ctypes.c_int, vp]
+        lib.oracle_transform_rows.restype = None
         _LIB = lib
     return _LIB
 
@@ -347,16 +372,39 @@ def _ptr(a: Optional[np.ndarray]):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
 
 
+def transform_rows(x: np.ndarray, M: np.ndarray, transpose: bool = False) -> np.ndarray:
+    """x @ M^T (rotated mode's forward transform, sunshape/codec.py:250-251) or, with transpose,
+    x @ M (its inverse, :257-258), fp32 with the k-ascending fused order of oracle/vq_encode.c."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M = np.ascontiguousarray(M, dtype=np.float32)
+    shape = x.shape
+    D = shape[-1]
+    if M.shape != (D, D):
+        raise ValueError(f"matrix must be [{D}, {D}]")
+    flat = x.reshape(-1, D)
+    out = np.empty_like(flat)
+    _lib().oracle_transform_rows(_ptr(flat), flat.shape[0], D, _ptr(M), 1 if transpose else 0, _ptr(out))
+    return out.reshape(shape)
+
+
 def encode(keys: np.ndarray, perm: np.ndarray, centroids: np.ndarray,
-           heavy: Optional[np.ndarray] = None, metric: Optional[np.ndarray] = None):
+           heavy: Optional[np.ndarray] = None, metric: Optional[np.ndarray] = None,
+           direct: bool = False, rotation: Optional[np.ndarray] = None):
     """``codec.quantize(keys)``: codes uint8 [N, nb], passthrough fp32 [N, nb, bd] or None.
 
     sunshape/codec.py:362-385; exact arithmetic in oracle/vq_encode.c.
     keys: [N, D] values (bf16 keys pass as their exact fp32 upcast).
     metric: the codec's E [D, D] (SunShape-Pro block metric; only its diagonal
     bd x bd blocks are read, as codec.py:375-376 slices them), None = identity.
+    direct: torch.cdist's direct distance (both inputs at most 25 rows) in place of its
+    mm formulation.
+    rotation: the rotated mode's R [D, D]: keys go through x @ R^T (transform_rows) and
+    ``perm`` is ignored (sunshape/codec.py:364, :250-251).
     """
     keys = np.ascontiguousarray(keys, dtype=np.float32)
+    if rotation is not None:
+        keys = transform_rows(keys, rotation)
+        perm = np.arange(keys.shape[1])
     perm = np.ascontiguousarray(perm, dtype=np.int64)
     cen = np.ascontiguousarray(centroids, dtype=np.float32)
     nb, nc, bd = cen.shape
@@ -370,20 +418,21 @@ def encode(keys: np.ndarray, perm: np.ndarray, centroids: np.ndarray,
     met = None if metric is None else np.ascontiguousarray(metric, dtype=np.float32)
     if met is not None and met.shape != (D, D):
         raise ValueError(f"metric must be [{D}, {D}]")
-    _lib().oracle_encode_metric(_ptr(keys), n, D, _ptr(perm), _ptr(cen), _ptr(met), nb, nc, bd, _ptr(hv),
-                                _ptr(codes), _ptr(pt))
+    _lib().oracle_encode_ex(_ptr(keys), n, D, _ptr(perm), _ptr(cen), _ptr(met), 1 if direct else 0, nb, nc, bd,
+                            _ptr(hv), _ptr(codes), _ptr(pt))
     return codes, pt
 
 
-def block_distances(x: np.ndarray, c: np.ndarray):
-    """Pre-sqrt and post-sqrt cdist matrices for one block (x [n, bd], c [nc, bd])."""
+def block_distances(x: np.ndarray, c: np.ndarray, direct: bool = False):
+    """Pre-sqrt and post-sqrt cdist matrices for one block (x [n, bd], c [nc, bd]); direct: the
+    direct evaluation torch.cdist takes when both inputs have at most 25 rows."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     c = np.ascontiguousarray(c, dtype=np.float32)
     n, bd = x.shape
     nc = c.shape[0]
     e2 = np.empty((n, nc), dtype=np.float32)
     d = np.empty((n, nc), dtype=np.float32)
-    _lib().oracle_block_dist(_ptr(x), n, _ptr(c), nc, bd, _ptr(e2), _ptr(d))
+    _lib().oracle_block_dist_ex(_ptr(x), n, _ptr(c), nc, bd, 1 if direct else 0, _ptr(e2), _ptr(d))
     return e2, d
 
 

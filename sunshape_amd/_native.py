@@ -30,7 +30,7 @@ SSQ_CONTIGUOUS, SSQ_PAGED = 0, 1
 
 DTYPE_CODE = {torch.float32: SSQ_F32, torch.bfloat16: SSQ_BF16, torch.float16: SSQ_F16}
 
-ABI_VERSION = 4  # SSQ_ABI_VERSION in include/sunshape_amd.h
+ABI_VERSION = 5  # SSQ_ABI_VERSION in include/sunshape_amd.h
 NOALLOC_SCRATCH_BYTES = 32 << 20  # SSQ_NOALLOC_SCRATCH_BYTES
 
 # every function include/sunshape_amd.h declares
@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "ssq_encode_grid_bytes",
     "ssq_encode_grid_build",
     "ssq_dequantize",
+    "ssq_transform_rows",
     "ssq_pack_codes",
     "ssq_unpack_codes",
     "ssq_last_error",
@@ -108,6 +109,7 @@ class EncodeArgs(ctypes.Structure):
         ("slot_mapping", _vp), ("sm_sb", _i64), ("page_size", _i32),
         ("kernel", _i32),
         ("grid", _vp), ("grid_bytes", ctypes.c_uint64),
+        ("direct_dist", _i32),
     ]
 
     def __init__(self, **kw):
@@ -142,6 +144,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.ssq_dequantize.argtypes = [_vp, _i64, _i32, _vp, _vp, _i32, _i32, _i32, _vp, _i32, _vp, _i32, _i64,
                                    _vp, _i64, _vp]
     lib.ssq_dequantize.restype = ctypes.c_int
+    lib.ssq_transform_rows.argtypes = [_vp, _i32, _i64, _i64, _i32, _i32, _f32, _vp, _i32, _vp, _i64, _vp]
+    lib.ssq_transform_rows.restype = ctypes.c_int
     lib.ssq_pack_codes.argtypes = [_vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]
     lib.ssq_pack_codes.restype = ctypes.c_int
     lib.ssq_unpack_codes.argtypes = [_vp, _i64, _i64, _i32, _i32, _vp, _i64, _vp]

@@ -92,7 +92,8 @@ class SunShapeCodedKeys:
             pt = None
             if heavy is not None:
                 pt = self.passthrough[:, h].reshape(B * T, -1, self.passthrough.shape[-1])
-            k_hat = hip_ops.dequantize(codes, perm, cent, heavy=heavy, pt=pt, pt_dense=False)
+            k_hat = hip_ops.dequantize(codes, perm, cent, heavy=heavy, pt=pt, pt_dense=False,
+                                       rotation=self.codec.rotation_matrix())
             out[:, h] = k_hat.view(B, T, self.head_dim).to(self.dtype)
         return out
 
@@ -163,9 +164,14 @@ class SunShapeCodeLayer(DynamicLayer):
         self._reserve(B, Hkv, value_states.shape[-1], self._len + S, value_states.dtype)
         lo, hi = self._len, self._len + S
         perm, cent = _per_head_arrays(self.codec)
+        # SunShapeLayer quantizes the flattened [B * Hkv * S, D] keys in one cdist (per KV head for
+        # per-head codecs), which fixes torch's distance formulation
+        rows = B * S if getattr(self.codec, "num_kv_heads", None) else B * Hkv * S
         hip_ops.encode(key_states, perm, cent, heavy=self.heavy, codes_out=self._codes[:, :, lo:hi],
                        pt_out=None if self._pt is None else self._pt[:, :, lo:hi], metric=self.codec.encode_metric(),
-                       grid=self.codec.encode_search_grid(cent))
+                       grid=self.codec.encode_search_grid(cent),
+                       direct=hip_ops.cdist_direct(rows, self.codec.n_centroids),
+                       rotation=self.codec.rotation_matrix())
         self._vals[:, :, lo:hi] = value_states
         self._len = hi
         return self._views()
@@ -304,7 +310,8 @@ def sunshape_attention_forward(module: torch.nn.Module, query: torch.Tensor, key
             mask = mask[..., -T:]
         perm, cent = _per_head_arrays(key.codec)
         out = hip_ops.decode(query, key.codes, value, perm, cent, scale=scaling, mask=mask,
-                             heavy=key.codec.heavy_blocks(), pt=key.passthrough, pt_dense=False)
+                             heavy=key.codec.heavy_blocks(), pt=key.passthrough, pt_dense=False,
+                             rotation=key.codec.rotation_matrix())
         return out.transpose(1, 2).contiguous(), None
     # prefill / multi-token step: dense k_hat in the key dtype, as the reference's cache layer stores
     return sdpa_attention_forward(module, query, key.dequantize(), value, attention_mask, dropout=0.0,

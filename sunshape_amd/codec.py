@@ -209,6 +209,11 @@ class SunShapeBlockCodec(torch.nn.Module):
             self._grid_cache[slot] = hit
         return hit[1]
 
+    def rotation_matrix(self) -> torch.Tensor | None:
+        """The rotated mode's dense R [D, D] (forward transform x @ R^T, inverse x @ R,
+        sunshape/codec.py:247-259), or None in the other modes."""
+        return self.rotation if self.use_rotation else None
+
     def codebook(self, kv_head: int | None = None) -> torch.Tensor:
         cent = self.centroids
         if kv_head is not None and cent.ndim == 4:
@@ -222,8 +227,6 @@ class SunShapeBlockCodec(torch.nn.Module):
 
     def unsupported_reason(self) -> str | None:
         """Why the HIP kernels cannot serve this codec (None when they can)."""
-        if self.mode == "rotated" or self.use_rotation:
-            return "rotated mode applies a dense rotation, which the HIP kernels do not implement."
         if self.n_centroids > 256:
             return f"n_centroids={self.n_centroids} > 256 needs wider than uint8 codes."
         return None
@@ -273,9 +276,11 @@ class SunShapeBlockCodec(torch.nn.Module):
         metric = self.encode_metric(kv_head)
         if metric is not None and metric.ndim == 3:
             raise RuntimeError("per-KV-head metric: pass kv_head=")
-        codes, pt = hip_ops.encode(keys.reshape(1, 1, -1, self.head_dim), perm, cent, heavy=heavy,
-                                   pt_dtype=torch.float32, pt_dense=True, metric=metric,
-                                   grid=self.encode_search_grid(cent))
+        flat = keys.reshape(1, 1, -1, self.head_dim)
+        codes, pt = hip_ops.encode(flat, perm, cent, heavy=heavy, pt_dtype=torch.float32, pt_dense=True,
+                                   metric=metric, grid=self.encode_search_grid(cent),
+                                   direct=hip_ops.cdist_direct(flat.shape[2], self.n_centroids),
+                                   rotation=self.rotation_matrix())
         mixed = self.mode == "profileperm_mixed_precision"
         return SunShapeQuantized(
             indices=codes.reshape(-1, self.n_blocks),
@@ -305,7 +310,9 @@ class SunShapeBlockCodec(torch.nn.Module):
             if self.n_centroids > 256:
                 raise RuntimeError("indices wider than uint8 are not supported")
             idx = idx.to(torch.uint8)
-        return hip_ops.dequantize(idx, perm, cent, heavy=heavy, pt=pt, pt_dense=pt is not None and pt.shape[-2] == self.n_blocks)
+        return hip_ops.dequantize(idx, perm, cent, heavy=heavy, pt=pt,
+                                  pt_dense=pt is not None and pt.shape[-2] == self.n_blocks,
+                                  rotation=self.rotation_matrix())
 
     def forward(self, keys: torch.Tensor, kv_head: int | None = None) -> torch.Tensor:
         return self.dequantize(self.quantize(keys, kv_head), kv_head)

@@ -6,6 +6,10 @@
 //   d[c]  = sqrt(max(d2[c], 0))
 // with |v|^2 = left-to-right sum of rounded squares.  Every index this file returns is the
 // first argmin of d computed with exactly that arithmetic and a correctly rounded sqrt.
+// When both of cdist's inputs have at most 25 rows (a call that quantizes at most 25 keys with at
+// most 25 codewords, e.g. 16 at 2 bits/dim and block_dim 2) torch evaluates the distance directly
+// instead, d2[c] = sum_k (x_k - c_k)^2 with rounded squares summed in k order; the caller asks for
+// that with direct_dist, which the exact scan serves.
 //
 // Two kernels:
 //  * k_encode_scan  -- one thread per (key, block), exact formula for all codewords.
@@ -69,6 +73,19 @@ __device__ __forceinline__ float metric_row_n(const float* e, const float (&x)[N
     for (int j = 1; j < N; ++j)
         if (j < bd) acc = __builtin_fmaf(e[j], x[j], acc);
     return acc;
+}
+
+// pre-sqrt distance of torch.cdist's direct evaluation (the one it takes when both inputs have at
+// most 25 rows): sum over k ascending of the rounded squares (x_k - c_k)^2, summed left to right
+__device__ __forceinline__ float direct_dist2(const float* x, const float* c, int bd) {
+    float d = x[0] - c[0];
+    float s = d * d;
+    for (int k = 1; k < bd; ++k) {
+        d = x[k] - c[k];
+        const float t = d * d;
+        s = s + t;
+    }
+    return s;
 }
 
 // correctly rounded sqrt of max(v, 0)
@@ -165,11 +182,12 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
             for (int k = 0; k < bd; ++k) x[k] = y[k];
         }
         const float xn = sq_norm(x, bd);
+        const bool direct = a.direct_dist != 0;
         // pass 1: smallest pre-sqrt value (first index)
         float emin = INFINITY;
         int jm = 0;
         for (int j = 0; j < nc; ++j) {
-            const float e = mm_dist2(x, xn, cbb + j * bd, cnb[j], bd);
+            const float e = direct ? direct_dist2(x, cbb + j * bd, bd) : mm_dist2(x, xn, cbb + j * bd, cnb[j], bd);
             if (e < emin) { emin = e; jm = j; }
         }
         // pass 2: the first index whose sqrt equals the minimum's (sqrt merges values at most
@@ -178,7 +196,7 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
         const float thr = emin > 0.f ? emin * (1.0f + 0x1.0p-20f) : 0.f;
         int best = jm;
         for (int j = 0; j < jm; ++j) {
-            const float e = mm_dist2(x, xn, cbb + j * bd, cnb[j], bd);
+            const float e = direct ? direct_dist2(x, cbb + j * bd, bd) : mm_dist2(x, xn, cbb + j * bd, cnb[j], bd);
             if (e <= thr && dist_of(e) == fstar) { best = j; break; }
         }
         a.codes[crow + blk] = (uint8_t)best;
@@ -681,13 +699,19 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
     SSQ_REQUIRE(!any_heavy || a->pt, "heavy blocks need a passthrough output");
     if (any_heavy) SSQ_REQUIRE(a->pt_dtype >= SSQ_F32 && a->pt_dtype <= SSQ_F16, "bad pt_dtype");
     if (a->slot_mapping) SSQ_REQUIRE(a->page_size >= 1, "paged output needs page_size >= 1");
+    SSQ_REQUIRE(a->direct_dist == 0 || a->direct_dist == 1, "direct_dist must be 0 or 1");
     if (a->batch == 0 || a->seq_len == 0) return SSQ_OK;
     hipStream_t st = (hipStream_t)stream;
-    if (a->kernel == 3 || (a->kernel == 0 && a->grid && ssq_encode_grid_supported(a))) return ssq_encode_grid_run(a, st);
+    // the direct distance (a cdist over at most 25 x 25 rows) runs on the exact scan only: the MFMA
+    // screen and the grid search certify candidates against the mm formulation's rounding
+    SSQ_UNSUPPORTED(!a->direct_dist || a->kernel == 0 || a->kernel == 1,
+                    "direct_dist runs on the exact scan (kernel 0 or 1), not kernel %d", a->kernel);
+    if (!a->direct_dist && (a->kernel == 3 || (a->kernel == 0 && a->grid && ssq_encode_grid_supported(a))))
+        return ssq_encode_grid_run(a, st);
     EncodeParams p;
     p.a = *a;
     const int KS = (a->block_dim + 2 + 3) / 4;
-    const bool mfma_ok = a->n_centroids == 256 && KS <= 3;
+    const bool mfma_ok = a->n_centroids == 256 && KS <= 3 && !a->direct_dist;
     const int kernel = a->kernel == 0 ? (mfma_ok ? 2 : 1) : a->kernel;
     if (kernel == 2) {
         SSQ_UNSUPPORTED(mfma_ok, "MFMA encode needs n_centroids == 256 and block_dim <= 10");

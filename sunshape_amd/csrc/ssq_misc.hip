@@ -109,7 +109,95 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* codes, int64_t c
     out[(int64_t)t * o_st + perm[i]] = v;
 }
 
+// Dense transform of rows (the rotated mode's x @ R^T and x @ R, codec.py:247-259):
+// out[r, j] = sum_k xs[r, k] * m_jk with m_jk = M[j, k] (transpose 0) or M[k, j] (transpose 1),
+// k ascending, the first product rounded, then fused multiply-adds; xs = x, or x * scale rounded
+// to x's dtype (the query scaling of the decode).  A workgroup covers kTrCols output columns
+// (gridDim.y chunks of them) for 256 / cw row lanes x kTrAcc rows; M and the rows are staged in
+// LDS kTrK columns of k at a time.
+constexpr int kTrThreads = 256;
+constexpr int kTrAcc = 16;   // rows per thread
+constexpr int kTrK = 32;     // k per LDS stage
+constexpr int kTrRowsMax = kTrThreads / 64 * kTrAcc;
+
+__global__ __launch_bounds__(kTrThreads) void k_transform_rows(const void* x, int x_dtype, int64_t x_sr, int64_t rows,
+                                                               int dim, int cw, int has_scale, float scale,
+                                                               const float* M, int transpose, float* out,
+                                                               int64_t o_sr) {
+    __shared__ float ms[kTrK][kTrThreads + 1];
+    __shared__ float xs[kTrRowsMax][kTrK];
+    const int t = threadIdx.x;
+    const int lanes = kTrThreads / cw;
+    const int c = t % cw, lane = t / cw;
+    const int j0 = blockIdx.y * cw;
+    const int j = j0 + c;
+    const int wg_rows = lanes * kTrAcc;
+    const int64_t r0 = (int64_t)blockIdx.x * wg_rows;
+    float acc[kTrAcc];
+#pragma unroll
+    for (int i = 0; i < kTrAcc; ++i) acc[i] = 0.f;
+    for (int k0 = 0; k0 < dim; k0 += kTrK) {
+        const int kc = min(kTrK, dim - k0);
+        __syncthreads();
+        for (int e = t; e < cw * kTrK; e += kTrThreads) {
+            int jj, kk;
+            if (transpose) { kk = e / cw; jj = e - kk * cw; }     // M[k, j]: consecutive j
+            else { jj = e / kTrK; kk = e - jj * kTrK; }           // M[j, k]: consecutive k
+            const int gj = j0 + jj;
+            float v = 0.f;
+            if (gj < dim && kk < kc) v = transpose ? M[(int64_t)(k0 + kk) * dim + gj] : M[(int64_t)gj * dim + k0 + kk];
+            ms[kk][jj] = v;
+        }
+        for (int e = t; e < wg_rows * kTrK; e += kTrThreads) {
+            const int rr = e / kTrK, kk = e - rr * kTrK;
+            const int64_t r = r0 + rr;
+            float v = 0.f;
+            if (r < rows && kk < kc) {
+                v = ssq_load_elem(x, x_dtype, r * x_sr + k0 + kk);
+                if (has_scale) v = ssq_round_to(v * scale, x_dtype);
+            }
+            xs[rr][kk] = v;
+        }
+        __syncthreads();
+        for (int kk = 0; kk < kc; ++kk) {
+            const float m = ms[kk][c];
+            if (k0 + kk == 0) {
+#pragma unroll
+                for (int i = 0; i < kTrAcc; ++i) acc[i] = xs[lane + i * lanes][kk] * m;
+            } else {
+#pragma unroll
+                for (int i = 0; i < kTrAcc; ++i) acc[i] = fmaf(xs[lane + i * lanes][kk], m, acc[i]);
+            }
+        }
+    }
+    if (j >= dim) return;
+#pragma unroll
+    for (int i = 0; i < kTrAcc; ++i) {
+        const int64_t r = r0 + lane + i * lanes;
+        if (r < rows) out[r * o_sr + j] = acc[i];
+    }
+}
+
 }  // namespace
+
+extern "C" int ssq_transform_rows(const void* x, int32_t x_dtype, int64_t x_sr, int64_t rows, int32_t dim,
+                                  int32_t has_scale, float scale, const float* mat, int32_t transpose, float* out,
+                                  int64_t o_sr, void* stream) {
+    SSQ_REQUIRE(x_dtype >= SSQ_F32 && x_dtype <= SSQ_F16, "bad x_dtype");
+    SSQ_REQUIRE(rows >= 0 && dim >= 1 && dim <= 4096, "bad rows / dim");
+    SSQ_REQUIRE(x_sr >= dim && o_sr >= dim, "row strides too small");
+    SSQ_REQUIRE(transpose == 0 || transpose == 1, "transpose must be 0 or 1");
+    if (rows == 0) return SSQ_OK;
+    SSQ_REQUIRE(x && mat && out, "x, mat and out must be non-NULL");
+    const int cw = dim >= kTrThreads ? kTrThreads : (dim <= 64 ? 64 : (dim <= 128 ? 128 : kTrThreads));
+    const int wg_rows = kTrThreads / cw * kTrAcc;
+    const int64_t gx = (rows + wg_rows - 1) / wg_rows;
+    SSQ_REQUIRE(gx <= 0x7fffffff, "too many rows");
+    dim3 grid((unsigned)gx, (unsigned)((dim + cw - 1) / cw));
+    hipLaunchKernelGGL(k_transform_rows, grid, dim3(kTrThreads), 0, (hipStream_t)stream, x, x_dtype, x_sr, rows, dim,
+                       cw, has_scale, scale, mat, transpose, out, o_sr);
+    return ssq_check_hip(hipGetLastError(), "k_transform_rows launch");
+}
 
 extern "C" int ssq_lut_build(const void* q, int32_t q_dtype, int64_t q_sr, int32_t rows, int32_t head_dim,
                              const int64_t* perm, const float* cent, int32_t block_dim, int32_t n_centroids,

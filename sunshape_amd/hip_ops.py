@@ -54,6 +54,41 @@ def _codec_arrays(perm: torch.Tensor, cent: torch.Tensor, head_dim: int, n_kv: O
     return perm, cent, perm_sh, cent_sh, bd, nb, nc
 
 
+def transform_rows(x: torch.Tensor, mat: torch.Tensor, *, transpose: bool = False,
+                   scale: Optional[float] = None) -> torch.Tensor:
+    """fp32 ``xs @ mat.T`` (or ``xs @ mat`` with transpose) over the last dim, xs = x, or x * scale
+    rounded to x's dtype (the decode's query scaling).  The rotated mode's transforms,
+    sunshape/codec.py:247-259: forward ``x @ rotation.T``, inverse ``x @ rotation``.
+    """
+    _on_gpu("x", x)
+    _on_gpu("rotation", mat)
+    D = x.shape[-1]
+    _require(mat.shape == (D, D), f"rotation must be [{D}, {D}], got {tuple(mat.shape)}")
+    mat = mat.to(torch.float32).contiguous()
+    flat = x.reshape(-1, D)
+    flat = flat if flat.stride(-1) == 1 else flat.contiguous()
+    out = torch.empty((flat.shape[0], D), device=x.device, dtype=torch.float32)
+    if flat.shape[0]:
+        N.check(N.lib().ssq_transform_rows(N.ptr(flat), N.dtype_code(flat.dtype), flat.stride(0), flat.shape[0], D,
+                                           1 if scale is not None else 0, float(scale or 0.0), N.ptr(mat),
+                                           1 if transpose else 0, N.ptr(out), out.stride(0), N.stream_of(x.device)))
+    return out.view(*x.shape[:-1], D)
+
+
+_IDENT: dict = {}
+
+
+def _identity_like(perm: torch.Tensor) -> torch.Tensor:
+    """The identity permutation in perm's shape ([D] or [Hkv, D]): under a rotation the kernels see
+    queries and keys already in the codec basis."""
+    key = (perm.device, tuple(perm.shape))
+    t = _IDENT.get(key)
+    if t is None:
+        t = torch.arange(perm.shape[-1], device=perm.device, dtype=torch.int64).expand(perm.shape).contiguous()
+        _IDENT[key] = t
+    return t
+
+
 def lut_build(q: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, scale: Optional[float] = None) -> torch.Tensor:
     """LUT[r, b, c] = q_perm[r, b-block] . C[b, c]  (fp32 [R, nb, nc]).
 
@@ -137,17 +172,22 @@ def _pt_args(heavy: Optional[Sequence[bool]], pt: Optional[torch.Tensor], pt_den
 
 def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor,
                      heavy: Optional[Sequence[bool]] = None, pt: Optional[torch.Tensor] = None,
-                     pt_dense: bool = True, code_bits: int = 0, kernel: int = 0) -> torch.Tensor:
+                     pt_dense: bool = True, code_bits: int = 0, kernel: int = 0,
+                     rotation: Optional[torch.Tensor] = None) -> torch.Tensor:
     """scores[r, t] = q_r . k_hat_t in fp32 (q in the original basis, unscaled).
 
     q [R, D]; codes uint8 [T, nb] (or int32 packed words [T, nw] with code_bits);
-    pt [T, nb, bd] (dense) or [T, n_heavy, bd].
+    pt [T, nb, bd] (dense) or [T, n_heavy, bd].  rotation: the rotated mode's R [D, D]; q is then
+    taken to the codec basis by q @ R^T (transform_rows) and perm is not used.
     Reference: sunshape/triton_kernels.py:570-609 and sunshape/codec.py:403-422.
     """
     _on_gpu("query", q)
     _on_gpu("indices", codes)
     _require(q.ndim == 2, f"Expected query.ndim == 2, got {q.ndim}.")
     _require(codes.ndim == 2, f"Expected quantized_key.indices.ndim == 2, got {codes.ndim}.")
+    if rotation is not None:
+        q = transform_rows(q, rotation)
+        perm = _identity_like(perm)
     q = q if q.stride(-1) == 1 else q.contiguous()
     codes = codes if codes.stride(-1) == 1 else codes.contiguous()
     R, D = q.shape
@@ -180,15 +220,20 @@ def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, c
 def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
                scale: Optional[float] = None, heavy: Optional[Sequence[bool]] = None,
                pt: Optional[torch.Tensor] = None, pt_dense: bool = False, code_bits: int = 0,
-               num_splits: int = 0, kernel: int = 0) -> torch.Tensor:
+               num_splits: int = 0, kernel: int = 0, rotation: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Raw scores for every (batch, query head) in one launch: fp32 [B, Hq, Lq, T].
 
     q [B, Hq, Lq, D]; codes [B, Hkv, T, nb] uint8; query head h reads KV head
     h // (Hq/Hkv).  With ``scale`` the query is scaled in its own dtype first
     (sunshape/vllm_attn_backend.py:235-236) -- the logits the decode softmaxes.
+    rotation: the rotated mode's R [D, D] (see decode).
     """
     for name, t in (("query", q), ("codes", codes)):
         _on_gpu(name, t)
+    if rotation is not None:
+        q = transform_rows(q, rotation, scale=scale)
+        scale = None
+        perm = _identity_like(perm)
     _require(q.ndim == 4 and codes.ndim == 4, "gqa_scores expects q [B, Hq, Lq, D] and codes [B, Hkv, T, nb]")
     q = q if q.stride(-1) == 1 else q.contiguous()
     codes = codes if codes.stride(-1) == 1 else codes.contiguous()
@@ -226,7 +271,8 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
            heavy: Optional[Sequence[bool]] = None, pt: Optional[torch.Tensor] = None, pt_dense: bool = False,
            block_table: Optional[torch.Tensor] = None, seq_lens: Optional[torch.Tensor] = None,
            return_lse: bool = False, return_scores: bool = False,
-           num_splits: int = 0, kernel: int = 0, code_bits: int = 0, no_alloc: bool = False):
+           num_splits: int = 0, kernel: int = 0, code_bits: int = 0, no_alloc: bool = False,
+           rotation: Optional[torch.Tensor] = None):
     """Fused VQ-key decode attention for all batches and KV heads in one launch.
 
     q [B, Hq, Lq, D].  Contiguous layout: codes [B, Hkv, T, nb] uint8, v [B, Hkv, T, Dv],
@@ -240,11 +286,17 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
     hold -inf.
     no_alloc: run through ssq_decode_noalloc (split workspace in the library's per-device scratch
     instead of a torch allocation; calls that overlap on one device race).
+    rotation: the rotated mode's R [D, D] (sunshape/codec.py:250-251): the scaled query goes to the
+    codec basis as fp32 (q * scale in q's dtype) @ R^T, the reference's order, and perm is not used.
     Reference: sunshape/vllm_attn_backend.py:216-253.
     """
     for name, t in (("query", q), ("codes", codes), ("value", v)):
         _on_gpu(name, t)
     _require(q.ndim == 4, "Quantized attention expects query/value tensors with shape [batch, heads, seq, dim].")
+    if rotation is not None:
+        q = transform_rows(q, rotation, scale=scale)
+        scale = None
+        perm = _identity_like(perm)
     q = q if q.stride(-1) == 1 else q.contiguous()
     _require(codes.stride(-1) == 1, "codes must be contiguous in the last dim")
     B, Hq, Lq, D = q.shape
@@ -336,7 +388,7 @@ def encode_args(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
            heavy: Optional[Sequence[bool]] = None, pt_dtype: Optional[torch.dtype] = None, pt_dense: bool = False,
            codes_out: Optional[torch.Tensor] = None, pt_out: Optional[torch.Tensor] = None,
            slot_mapping: Optional[torch.Tensor] = None, metric: Optional[torch.Tensor] = None, kernel: int = 0,
-           grid: Optional[torch.Tensor] = None):
+           grid: Optional[torch.Tensor] = None, direct: bool = False, rotation: Optional[torch.Tensor] = None):
     """Validated ssq_encode arguments for encode(): (args, codes, pt, tensors the args point into).
 
     For callers that replay one launch many times through the C ABI (a benchmark, a serving
@@ -356,6 +408,9 @@ def encode_args(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
     """
     _on_gpu("key_states", keys)
     _require(keys.ndim == 4, "quantize_key_states expects key_states with shape [batch, kv_heads, seq_len, head_dim].")
+    if rotation is not None:  # the rotated mode's forward transform, fp32 keys @ R^T (codec.py:363-364)
+        keys = transform_rows(keys, rotation)
+        perm = _identity_like(perm)
     keys = keys if keys.stride(-1) == 1 else keys.contiguous()
     B, Hkv, S, D = keys.shape
     perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, Hkv)
@@ -424,9 +479,9 @@ def encode_args(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
         pt=N.ptr(pt), pt_dtype=N.dtype_code(pt_dtype), pt_dense=1 if pt_dense else 0,
         pt_sb=p_str[0], pt_sh=p_str[1], pt_st=p_str[2],
         slot_mapping=N.ptr(slot_mapping), sm_sb=slot_mapping.stride(0) if slot_mapping is not None else 0,
-        page_size=page, kernel=int(kernel),
+        page_size=page, kernel=int(kernel), direct_dist=1 if direct else 0,
     )
-    if grid is not None:
+    if grid is not None and not direct:
         _on_gpu("grid", grid)
         _require(grid.dtype == torch.uint8 and grid.is_contiguous(), "grid must be the uint8 tensor from encode_grid")
         a.grid, a.grid_bytes = N.ptr(grid), grid.numel()
@@ -434,11 +489,20 @@ def encode_args(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
     return a, codes, pt, (keys, perm, cent, metric, grid, slot_mapping)
 
 
+def cdist_direct(rows_per_call: int, n_centroids: int) -> bool:
+    """Whether torch.cdist evaluates the reference's distances directly rather than by its mm
+    formulation: both of its inputs have at most 25 rows (ATen's cdist, compute mode
+    use_mm_for_euclid_dist_if_necessary).  rows_per_call is the key count of one reference cdist
+    call: N for codec.quantize(keys[N, D]), seq_len for quantize_key_states (one call per batch
+    and KV head), B * Hkv * S for the HF cache layer's flattened keys."""
+    return rows_per_call <= 25 and n_centroids <= 25
+
+
 def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
            heavy: Optional[Sequence[bool]] = None, pt_dtype: Optional[torch.dtype] = None, pt_dense: bool = False,
            codes_out: Optional[torch.Tensor] = None, pt_out: Optional[torch.Tensor] = None,
            slot_mapping: Optional[torch.Tensor] = None, metric: Optional[torch.Tensor] = None, kernel: int = 0,
-           grid: Optional[torch.Tensor] = None):
+           grid: Optional[torch.Tensor] = None, direct: bool = False, rotation: Optional[torch.Tensor] = None):
     """Nearest-codeword encode of keys [B, Hkv, S, D] -> (codes uint8 [B, Hkv, S, nb], pt or None).
 
     Passthrough values (heavy blocks) are [B, Hkv, S, n_heavy, bd] (compact) or
@@ -451,11 +515,15 @@ def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
     grid: search grid from encode_grid(cent) (block_dim 2, no metric); with it the encode
     evaluates only each key's certified candidates (same codes).  kernel: 0 auto, 1 exact scan,
     2 MFMA screen, 3 grid search.
+    direct: torch.cdist's direct distance in place of its mm formulation (see cdist_direct; the
+    exact scan serves it and the grid is not used).
+    rotation: the rotated mode's R [D, D]: keys are encoded as fp32 keys @ R^T and perm is not used;
+    passthrough values are then the transformed values, as the reference stores them.
     Reference: sunshape/codec.py:362-385, sunshape/vllm_attn_backend.py:101-123.
     """
     a, codes, pt, _keep = encode_args(keys, perm, cent, heavy=heavy, pt_dtype=pt_dtype, pt_dense=pt_dense,
                                       codes_out=codes_out, pt_out=pt_out, slot_mapping=slot_mapping, metric=metric,
-                                      kernel=kernel, grid=grid)
+                                      kernel=kernel, grid=grid, direct=direct, rotation=rotation)
     N.check(N.lib().ssq_encode(ctypes.byref(a), N.stream_of(keys.device)))
     return codes, pt
 
@@ -486,11 +554,16 @@ def encode_grid(cent: torch.Tensor, num_kv_heads: int = 1) -> torch.Tensor:
 
 def dequantize(codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
                heavy: Optional[Sequence[bool]] = None, pt: Optional[torch.Tensor] = None,
-               pt_dense: bool = True) -> torch.Tensor:
+               pt_dense: bool = True, rotation: Optional[torch.Tensor] = None) -> torch.Tensor:
     """k_hat fp32 [T, D] in the original basis from codes uint8 [T, nb].
 
+    rotation: the rotated mode's R [D, D]: the codewords are taken back by k_hat @ R
+    (sunshape/codec.py:257-258) and perm is not used.
     Reference: sunshape/codec.py:387-398.
     """
+    if rotation is not None:
+        k_rot = dequantize(codes, _identity_like(perm), cent, heavy=heavy, pt=pt, pt_dense=pt_dense)
+        return transform_rows(k_rot, rotation, transpose=True)
     _on_gpu("indices", codes)
     _require(codes.ndim == 2 and codes.dtype == torch.uint8, "indices must be uint8 [T, nb]")
     codes = codes if codes.stride(-1) == 1 else codes.contiguous()

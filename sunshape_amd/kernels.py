@@ -92,14 +92,16 @@ def sunshape_attention_scores_strict(codec, query: torch.Tensor, quantized_key, 
             heavy = None
     pt = getattr(quantized_key, "passthrough_values", None)
     dense = pt is not None and pt.ndim == 3 and pt.shape[1] == codec.n_blocks
-    return hip_ops.attention_scores(query, idx, perm, cent, heavy=heavy, pt=pt, pt_dense=dense)
+    rot = codec.rotation_matrix() if hasattr(codec, "rotation_matrix") else None
+    return hip_ops.attention_scores(query, idx, perm, cent, heavy=heavy, pt=pt, pt_dense=dense, rotation=rot)
 
 
 def sunshape_attention_scores(codec, query: torch.Tensor, quantized_key, kv_head: int | None = None) -> torch.Tensor:
     """``<query, k_hat>`` fp32 [n_qh, T] against block-quantized keys (sunshape/triton_kernels.py:570-609).
 
     query is [n_qh, D] in the original model basis; it is permuted into the
-    codec basis inside the kernel.  Raises RuntimeError for unsupported inputs.
+    codec basis inside the kernel (rotated codecs: q @ R^T first, on the GPU).  Raises
+    RuntimeError for unsupported inputs.
     """
     return sunshape_attention_scores_strict(codec, query, quantized_key, kv_head=kv_head)
 

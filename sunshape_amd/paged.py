@@ -81,9 +81,12 @@ class PagedSunShapeCache:
             raise RuntimeError("key/value shapes do not match the cache")
         slots = self.slot_mapping(seq_ids, S)
         perm = self.codec.effective_permutation()
+        # as quantize_key_states: one reference cdist per (sequence, KV head) over its S new keys
         hip_ops.encode(key_states.to(self.device), perm, self.codec.centroids, heavy=self.heavy,
                        codes_out=self.code_pages, pt_out=self.pt_pages, slot_mapping=slots,
-                       metric=self.codec.encode_metric(), grid=self.codec.encode_search_grid(self.codec.centroids))
+                       metric=self.codec.encode_metric(), grid=self.codec.encode_search_grid(self.codec.centroids),
+                       direct=hip_ops.cdist_direct(S, self.codec.n_centroids),
+                       rotation=self.codec.rotation_matrix())
         flat = slots.reshape(-1)
         page, off = flat // self.page_size, flat % self.page_size
         vals = value_states.to(self.device, self.v_pages.dtype).permute(0, 2, 1, 3).reshape(B * S, Hkv, self.value_dim)
@@ -106,4 +109,5 @@ class PagedSunShapeCache:
         bt, lens = self.tables(seq_ids)
         return hip_ops.decode(query, self.code_pages, self.v_pages, self.codec.effective_permutation(),
                               self.codec.centroids, scale=scale, heavy=self.heavy, pt=self.pt_pages,
-                              pt_dense=False, block_table=bt, seq_lens=lens, return_lse=return_lse)
+                              pt_dense=False, block_table=bt, seq_lens=lens, return_lse=return_lse,
+                              rotation=self.codec.rotation_matrix())

@@ -145,8 +145,10 @@ def quantize_key_states(layer_idx: int, key_states: torch.Tensor) -> SunShapeQua
         keys = keys.float()
     metric = codec.encode_metric() if hasattr(codec, "encode_metric") else None
     grid = codec.encode_search_grid(cent) if hasattr(codec, "encode_search_grid") else None
+    # the reference quantizes one (batch, KV head) per call: seq_len keys per cdist
+    rot = codec.rotation_matrix() if hasattr(codec, "rotation_matrix") else None
     codes, pt = hip_ops.encode(keys, perm, cent, heavy=heavy, pt_dtype=torch.float32, pt_dense=True, metric=metric,
-                               grid=grid)
+                               grid=grid, direct=hip_ops.cdist_direct(seq_len, cent.shape[-2]), rotation=rot)
     mixed = codec.mode == "profileperm_mixed_precision"
     pblocks = codec.mixed_high_precision_blocks.detach().clone() if mixed else None
     heads = []
@@ -264,7 +266,9 @@ def _apply_quantized_attention(
     mask = _mask_view(attn_mask, batch_size, num_query_heads, query_len, seq_len)
     q = query if query.stride(-1) == 1 else query.contiguous()
     v = value if value.stride(-1) == 1 else value.contiguous()
-    return hip_ops.decode(q, codes, v, perm, cent, scale=scale, mask=mask, heavy=heavy, pt=pt, pt_dense=dense)
+    rot = codec.rotation_matrix() if hasattr(codec, "rotation_matrix") else None
+    return hip_ops.decode(q, codes, v, perm, cent, scale=scale, mask=mask, heavy=heavy, pt=pt, pt_dense=dense,
+                          rotation=rot)
 
 
 class SunShapeAttentionImpl:

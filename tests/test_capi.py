@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     lib = N.lib()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.ssq_abi_version() == N.ABI_VERSION == 4
+    assert lib.ssq_abi_version() == N.ABI_VERSION == 5
 
 
 def test_struct_layout_matches_library():

@@ -45,9 +45,11 @@ def test_layer_selection_mirrors_reference():
 
 
 def test_code_layer_rejects_codecs_the_kernels_cannot_serve():
+    wide = SunShapeBlockCodec(head_dim=32, block_dim=4, n_centroids=512, device="cpu")
+    with pytest.raises(RuntimeError, match="uint8"):
+        SunShapeCodeLayer(wide)
     rot = SunShapeBlockCodec(head_dim=32, block_dim=4, use_rotation=True, device="cpu")
-    with pytest.raises(RuntimeError, match="rotation"):
-        SunShapeCodeLayer(rot)
+    assert SunShapeCodeLayer(rot).codec is rot  # rotated codecs run on the kernels
 
 
 def test_sunshape_attention_delegates_dense_layers_exactly():

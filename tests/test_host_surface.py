@@ -64,10 +64,14 @@ def test_heavy_blocks_cached_and_refreshed():
 
 
 def test_unsupported_modes_raise_with_reason():
-    c = SunShapeBlockCodec(head_dim=64, block_dim=8, use_rotation=True, device="cpu")
-    assert "rotation" in c.unsupported_reason()
-    with pytest.raises(RuntimeError, match="rotation"):
+    c = SunShapeBlockCodec(head_dim=64, block_dim=8, n_centroids=1024, device="cpu")
+    assert "uint8" in c.unsupported_reason()
+    with pytest.raises(RuntimeError, match="uint8"):
         c.quantize(torch.randn(4, 64))
+    rot = SunShapeBlockCodec(head_dim=64, block_dim=8, use_rotation=True, device="cpu")
+    assert rot.unsupported_reason() is None and rot.rotation_matrix() is rot.rotation
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        rot.quantize(torch.randn(4, 64))
     pro = _codec(mode="profileperm_localmetric_dsq")
     with pytest.raises(NotImplementedError):
         pro.fit(torch.randn(4, 64), torch.randn(4, 64))

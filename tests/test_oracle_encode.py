@@ -218,3 +218,138 @@ def test_metric_keys_on_codewords():
     E = (np.eye(D) + 0.1 * rng.standard_normal((D, D))).astype(np.float32)
     codes, _ = O.encode(xp.astype(np.float32), perm, cent, metric=E)
     assert np.array_equal(codes, idx.astype(np.uint8))
+
+
+# ----------------------------------------------------------------------------- direct distance
+# torch.cdist evaluates sqrt(sum_k (x_k - c_k)^2) directly when both inputs have at most 25 rows.
+# Its scalar CPU kernel (ATEN_CPU_CAPABILITY=default) sums the rounded squares in k order, which
+# the oracle's direct mode restates bit for bit.  Vectorised builds (AVX2 / AVX-512) reorder that
+# sum for some block sizes, so against them only near-ties may differ.
+_DIRECT_SCRIPT = r"""
+import sys, numpy as np, torch
+d = np.load(sys.argv[1])
+out = {}
+for k in d.files:
+    if k.startswith("x"):
+        i = k[1:]
+        out["d" + i] = torch.cdist(torch.from_numpy(d["x" + i]), torch.from_numpy(d["c" + i])).numpy()
+np.savez(sys.argv[2], **out)
+"""
+
+
+def _direct_cases():
+    cases = []
+    for bd in (1, 2, 3, 4, 8):
+        for seed in range(6):
+            x, c = _data(900 + 10 * bd + seed, 25 - seed, bd, nc=16)
+            cases.append((x, c))
+    return cases
+
+
+def _torch_cdist_subprocess(cases, tmp_path, capability):
+    import os
+    import subprocess
+    import sys
+
+    src = tmp_path / "in.npz"
+    dst = tmp_path / "out.npz"
+    np.savez(src, **{f"x{i}": x for i, (x, _) in enumerate(cases)}, **{f"c{i}": c for i, (_, c) in enumerate(cases)})
+    env = dict(os.environ, ATEN_CPU_CAPABILITY=capability)
+    subprocess.run([sys.executable, "-c", _DIRECT_SCRIPT, str(src), str(dst)], check=True, env=env)
+    d = np.load(dst)
+    return [d[f"d{i}"] for i in range(len(cases))]
+
+
+def test_direct_distance_bit_exact_vs_torch_scalar_cdist(tmp_path):
+    cases = _direct_cases()
+    ref = _torch_cdist_subprocess(cases, tmp_path, "default")
+    for (x, c), r in zip(cases, ref):
+        _, d = O.block_distances(x, c, direct=True)
+        assert np.array_equal(d.view(np.uint32), r.view(np.uint32)), (x.shape, c.shape)
+        codes, _ = O.encode(x, np.arange(x.shape[1]), c[None], direct=True)
+        assert np.array_equal(codes[:, 0], np.argmin(r, axis=1))
+
+
+def test_direct_distance_vs_vectorised_torch_only_near_ties():
+    for x, c in _direct_cases():
+        r = torch.cdist(torch.from_numpy(x), torch.from_numpy(c)).numpy()
+        _, d = O.block_distances(x, c, direct=True)
+        assert np.all(np.abs(d - r) <= 2 * np.spacing(np.maximum(np.abs(r), 1e-30).astype(np.float32)))
+        got = O.encode(x, np.arange(x.shape[1]), c[None], direct=True)[0][:, 0]
+        want = np.argmin(r, axis=1)
+        for i in np.nonzero(got != want)[0]:
+            a, b = d[i, got[i]], d[i, want[i]]
+            assert abs(a - b) <= 4 * np.spacing(np.float32(max(min(a, b), 1e-30)))
+
+
+def _midpoint_keys(seed, n, bd, nc=16):
+    """Keys near the midpoints of codeword pairs: the distance formulation decides the winner."""
+    rng = np.random.default_rng(seed)
+    c = (rng.standard_normal((nc, bd)) * 2).astype(np.float32)
+    i, j = rng.integers(0, nc, n), rng.integers(0, nc, n)
+    x = (0.5 * (c[i] + c[j]) + rng.standard_normal((n, bd)) * 1e-6).astype(np.float32)
+    return x, c
+
+
+def test_mode_switch_changes_near_tie_codes_as_torch_does(tmp_path):
+    """On midpoint keys the two formulations pick different codewords in some rows; torch's own
+    choice follows the row count (direct at <= 25 rows, mm above), and so does the oracle's."""
+    xs, cs = zip(*[_midpoint_keys(2000 + s, 25, 2) for s in range(80)])
+    ref_direct = _torch_cdist_subprocess(list(zip(xs, cs)), tmp_path, "default")
+    n_diff = 0
+    for x, c, rd in zip(xs, cs, ref_direct):
+        cd = O.encode(x, np.arange(2), c[None], direct=True)[0][:, 0]
+        cm = O.encode(x, np.arange(2), c[None], direct=False)[0][:, 0]
+        assert np.array_equal(cd, np.argmin(rd, axis=1))
+        # the same keys inside a 26-row call take the mm formulation
+        x26 = np.concatenate([x, x[:1]])
+        rm = torch.cdist(torch.from_numpy(x26), torch.from_numpy(c)).numpy()[:25]
+        _assert_only_sqrt_ties(x, c, cm, np.argmin(rm, axis=1))
+        n_diff += int((cd != cm).sum())
+    assert n_diff > 0, "no midpoint key separated the two formulations"
+
+
+# ----------------------------------------------------------------------------- rotated mode
+def _orthogonal(D, seed):
+    g = torch.Generator().manual_seed(seed)
+    qm, _ = torch.linalg.qr(torch.randn(D, D, generator=g, dtype=torch.float64))
+    return qm.float().numpy()
+
+
+def test_transform_rows_permutation_matrix_is_the_gather():
+    rng = np.random.default_rng(31)
+    D = 64
+    perm = rng.permutation(D)
+    P = np.eye(D, dtype=np.float32)[perm]          # (x @ P^T)[j] = x[perm[j]]
+    x = (rng.standard_normal((50, D)) * 3).astype(np.float32)
+    assert np.array_equal(O.transform_rows(x, P), O.forward_transform(x, perm))
+    assert np.array_equal(O.transform_rows(O.forward_transform(x, perm), P, transpose=True), x)
+
+
+def test_transform_rows_orthogonal_adjointness_and_transpose_slip():
+    rng = np.random.default_rng(32)
+    D = 64
+    R = _orthogonal(D, 5)
+    q = rng.standard_normal((7, D)).astype(np.float32)
+    k = rng.standard_normal((40, D)).astype(np.float32)
+    lhs = q.astype(np.float64) @ O.transform_rows(k, R, transpose=True).astype(np.float64).T
+    rhs = O.transform_rows(q, R).astype(np.float64) @ k.astype(np.float64).T
+    assert np.abs(lhs - rhs).max() <= 1e-5 * np.abs(lhs).max()
+    # the plausible slip (R in place of R^T) breaks the identity
+    slip = O.transform_rows(q, R.T.copy()).astype(np.float64) @ k.astype(np.float64).T
+    assert np.abs(lhs - slip).max() > 0.1 * np.abs(lhs).max()
+    # torch's matmul (the reference's x @ rotation.T) agrees to fp32 rounding
+    ref = (torch.from_numpy(q) @ torch.from_numpy(R).T).numpy()
+    assert np.abs(O.transform_rows(q, R) - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_rotated_encode_with_permutation_matrix_equals_permutation_encode():
+    rng = np.random.default_rng(33)
+    D, bd = 64, 2
+    perm = rng.permutation(D)
+    P = np.eye(D, dtype=np.float32)[perm]
+    x, c = _data(34, 3000, D)
+    cent = (rng.standard_normal((D // bd, 256, bd))).astype(np.float32)
+    a, _ = O.encode(x, perm, cent)
+    b, _ = O.encode(x, np.zeros(D, np.int64), cent, rotation=P)  # perm ignored under rotation
+    assert np.array_equal(a, b)
