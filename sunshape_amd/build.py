@@ -56,18 +56,31 @@ def _compile(hipcc: str, src: str, obj: str) -> None:
         sys.stderr.write(err + "\n")
 
 
-def _stale(src: str, obj: str, dep_mtime: float) -> bool:
+def _includes(path: str, seen: set) -> None:
+    """Local headers path includes (#include "..."), recursively, into seen."""
+    for line in open(path):
+        line = line.strip()
+        if line.startswith("#include") and '"' in line:
+            dep = os.path.normpath(os.path.join(os.path.dirname(path), line.split('"')[1]))
+            if os.path.exists(dep) and dep not in seen:
+                seen.add(dep)
+                _includes(dep, seen)
+
+
+def _stale(src: str, obj: str) -> bool:
     if not os.path.exists(obj):
         return True
+    deps = {src}
+    _includes(src, deps)
     t = os.path.getmtime(obj)
-    return t < os.path.getmtime(src) or t < dep_mtime
+    return any(t < os.path.getmtime(d) for d in deps)
 
 
 def build(verbose: bool = False, incremental: bool = False) -> str:
     """Compile all HIP sources and link the shared library; returns its path.
 
-    incremental: recompile only sources whose object is older than the source or than any
-    header under csrc/ or include/ (a development shortcut; the default rebuilds everything).
+    incremental: recompile only sources whose object is older than the source or than a header
+    it includes (a development shortcut; the default rebuilds everything).
     """
     hipcc = _hipcc()
     obj_dir = os.path.join(OUT_DIR, "obj")
@@ -76,11 +89,7 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
     objs = [os.path.join(obj_dir, os.path.basename(s)[:-4] + ".o") for s in srcs]
     work = list(zip(srcs, objs))
     if incremental:
-        inc = os.path.join(os.path.dirname(HERE), "include")
-        hdrs = [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
-        hdrs += [os.path.join(inc, f) for f in os.listdir(inc) if f.endswith(".h")]
-        dep = max((os.path.getmtime(h) for h in hdrs), default=0.0)
-        work = [(s, o) for s, o in work if _stale(s, o, dep)]
+        work = [(s, o) for s, o in work if _stale(s, o)]
         if verbose:
             print("compiling:", " ".join(os.path.basename(s) for s, _ in work) or "(nothing)")
     if work:

@@ -829,6 +829,7 @@ int ssq_decode_contig(const ssq_decode_args* a, void* workspace, size_t ws_bytes
 namespace {
 // kernel choice: 2 = MFMA paged, 3 = MFMA contiguous, 1 = generic; 0 picks the first that serves
 int pick_kernel(const ssq_decode_args* a) {
+    if (a->kernel == 4) return 2;  // the paged MFMA path, with its 4x4-MFMA-scores kernel forced
     if (a->kernel != 0) return a->kernel;
     if (a->v && ssq_decode_mfma_supported(a)) return 2;
     if (!a->v) {

@@ -14,37 +14,18 @@
 //               read straight from the page: vLLM's value page is dim-major
 //               ([Dv][page]), so the 8 consecutive tokens of one dim that a lane
 //               supplies to the B operand are one 16-byte load.
-#include "ssq_common.h"
+#include "ssq_decode_paged.h"
 
 #include <math.h>
 
 int ssq_launch_merge(const ssq_decode_args& a, int n_splits, const float* ws_o, const float* ws_m,
                      const float* ws_l, hipStream_t st);
+// the 4x4-MFMA-scores kernel (ssq_decode_paged_q4.hip)
+bool ssq_decode_q4_shape(const ssq_decode_args* a);
+size_t ssq_decode_q4_smem(const ssq_decode_args* a, int rg, int split_len);
+int ssq_decode_q4_launch(const SsqPagedParams& mp, const dim3& grid, hipStream_t st);
 
 namespace {
-
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-
-#ifndef SSQ_DECODE_WAVES
-#define SSQ_DECODE_WAVES 4
-#endif
-constexpr int kWaves = SSQ_DECODE_WAVES;  // waves per workgroup
-constexpr int kThreads = kWaves * SSQ_WAVE;
-constexpr int kTileTok = 64;  // tokens per wave iteration (4 pages)
-constexpr int kPage = 16;
-constexpr int kNC = 256;      // codewords per block (uint8 codes)
-constexpr size_t kMaxSmem = 160 * 1024;
-
-struct MfmaParams {
-    ssq_decode_args a;
-    int G, rows, split_len, n_splits;
-    int rg;  // query rows per row group (blockIdx.z): a group's LUT fits the LDS, V streams once per group
-    float* ws_o;
-    float* ws_m;
-    float* ws_l;
-};
 
 // LUT codewords per block: 256, or 64 for 64-codeword codebooks (a table a quarter the size)
 __host__ __device__ inline int lut_nc(const ssq_decode_args& a) { return a.n_centroids == 64 ? 64 : kNC; }
@@ -64,128 +45,12 @@ inline size_t mfma_smem(const ssq_decode_args& a, int RP, int split_len) {
     return (main > merge ? main : merge) * sizeof(float);
 }
 
-template <int VT>
-__device__ __forceinline__ uint32_t to_vt16(float x) {
-    return VT == SSQ_BF16 ? ssq_f32_to_bf16(x) : ssq_f32_to_f16(x);
-}
-
-template <int VT>
-__device__ __forceinline__ v4f mfma(const uint4& a, const uint4& b, v4f c) {
-    if (VT == SSQ_BF16)
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0,
-                                                       0, 0);
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
-}
-
-// wave-wide max / sum: DPP rotations inside each 16-lane row, then the four row results by readlane
-template <int CTL>
-__device__ __forceinline__ float dpp_ror(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float wave_max(float v) {
-    v = fmaxf(v, dpp_ror<0x121>(v));
-    v = fmaxf(v, dpp_ror<0x122>(v));
-    v = fmaxf(v, dpp_ror<0x124>(v));
-    v = fmaxf(v, dpp_ror<0x128>(v));
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
-}
-__device__ __forceinline__ float wave_sum(float v) {
-    v += dpp_ror<0x121>(v);
-    v += dpp_ror<0x122>(v);
-    v += dpp_ror<0x124>(v);
-    v += dpp_ror<0x128>(v);
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return (r0 + r1) + (r2 + r3);
-}
-
-// 16-byte load of streamed (read-once) data: non-temporal, so the single pass over
-// the values does not evict the codebooks and block tables other workgroups reuse
-#ifndef SSQ_STREAM_NT
-#define SSQ_STREAM_NT 1
-#endif
-#ifndef SSQ_CODES_NT
-#define SSQ_CODES_NT 1
-#endif
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 load_stream(const uint16_t* p) {
-#if SSQ_STREAM_NT
-    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-#else
-    return *reinterpret_cast<const uint4*>(p);
-#endif
-}
-
-// packed code rows (PB bits per code, 32 / PB codes per little-endian int32 word, the low bits
-// first; sunshape/triton_kernels.py:250-266): int32 words per row
-__host__ __device__ constexpr int pk_words(int NB, int PB) { return PB ? (NB + 32 / PB - 1) / (32 / PB) : 1; }
-
-// registers of one 64-token tile in flight
-template <int NB, int DT, int PB = 0>
-struct TileRegs {
-    uint4 c[NB / 16 > 0 ? NB / 16 : 1];  // this lane's token codes (NB bytes)
-    uint2 c8;                            // NB == 8
-    uint32_t pk[pk_words(NB, PB)];       // PB-bit codes in words (PB > 0)
-    uint4 v[2][DT];                      // B-operand V fragments of the two 32-token K groups
-};
-
-// cbase: the KV head's codes (bytes; with PB > 0 int32 words, strides counting words)
-template <int NB, int DT, int PB = 0>
-__device__ __forceinline__ void issue_tile(const ssq_decode_args& a, const int* pages, int t_begin, int t_end, int tile,
-                                           int lane, const uint8_t* cbase, const uint16_t* vbase,
-                                           TileRegs<NB, DT, PB>& R) {
-    // Every load is issued unconditionally (straight-line code keeps the compiler's vmcnt
-    // bookkeeping exact, so waiting for this tile never drains the next one).  Lanes past the
-    // split's end read their split's last token / 8-token chunk instead: a valid address whose
-    // data compute_tile masks (scores by `valid`, V chunks by the tail zeroing).
-    const int rel = tile * kTileTok;  // tile start relative to the split
-    const int last = t_end - 1 - t_begin;
-    const int tr = min(rel + lane, last);
-    const int page = pages[tr >> 4];
-    const uint8_t* crow = cbase + (int64_t)page * a.c_sb + (int64_t)((t_begin + tr) & 15) * a.c_st;
-    if constexpr (PB > 0) {
-        const uint32_t* prow = reinterpret_cast<const uint32_t*>(cbase) + (int64_t)page * a.c_sb +
-                               (int64_t)((t_begin + tr) & 15) * a.c_st;
-#pragma unroll
-        for (int i = 0; i < pk_words(NB, PB); ++i) R.pk[i] = __builtin_nontemporal_load(prow + i);
-    } else if (NB >= 16) {
-#pragma unroll
-        for (int i = 0; i < NB / 16; ++i) {
-#if SSQ_CODES_NT
-            const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(crow) + i);
-            R.c[i] = make_uint4(v.x, v.y, v.z, v.w);
-#else
-            R.c[i] = reinterpret_cast<const uint4*>(crow)[i];
-#endif
-        }
-    } else {
-        R.c8 = *reinterpret_cast<const uint2*>(crow);
-    }
-    const int kchunk = 8 * (lane >> 4);
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        const int r = min(rel + 32 * g + kchunk, last & ~7);
-        const uint16_t* src = vbase + (int64_t)pages[r >> 4] * a.v_sb + (r & 15);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) R.v[g][dt] = load_stream(src + (int64_t)(16 * dt) * a.v_st);
-    }
-}
 
 template <int RP, int DT, int VT, int NB, int NC, int PB>
 __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* lut, uint16_t* pstrip, int b, int kv,
                                              int t_begin, int t_end, int tile, int lane, TileRegs<NB, DT, PB>& R,
                                              float (&m_run)[RP], float (&l_lane)[RP], v4f (&acc)[DT]) {
-    const ssq_decode_args& a = p.a;
     const int t0 = t_begin + tile * kTileTok;
-    const int t = t0 + lane;
-    const bool valid = t < t_end;
     float s[RP];
 #pragma unroll
     for (int r = 0; r < RP; ++r) s[r] = 0.f;
@@ -193,7 +58,7 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
         // LUT gathers a batch of KB blocks at a time: all KB reads are issued before the first
         // is consumed (one wave per SIMD hides no LDS latency otherwise); the sums still run in
         // block order from 0.  Lanes past the end gather too (their codes are a valid token's)
-        // and are dropped by `valid` below.
+        // and are dropped by tile_softmax_pv.
         constexpr int KB = RP >= 8 ? 4 : 8;
         constexpr int NV = RP >= 4 ? RP / 4 : 1;  // float4 (or one float2 / float) per block
 #pragma unroll
@@ -245,70 +110,7 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
             }
         }
     }
-    if (valid) {
-        if (a.scores) {
-            const int row0 = blockIdx.z * p.rg, nr = min(p.rg, p.rows - row0);
-#pragma unroll
-            for (int r = 0; r < RP; ++r) {
-                if (r < nr) {
-                    const int g = (row0 + r) / a.q_len, qi = row0 + r - g * a.q_len;
-                    const int h = kv * p.G + g;
-                    a.scores[(int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)qi * a.s_sl + t] = s[r];
-                }
-            }
-        }
-    }
-    // online softmax (wave-local)
-    float alpha[RP];
-    bool rescale = false;
-#pragma unroll
-    for (int r = 0; r < RP; ++r) {
-        const float tm = wave_max(valid ? s[r] : -INFINITY);
-        const float mn = fmaxf(m_run[r], tm);
-        alpha[r] = (mn == -INFINITY) ? 1.f : __expf(m_run[r] - mn);
-        rescale |= mn != m_run[r];
-        m_run[r] = mn;
-        const float pr = (valid && mn != -INFINITY) ? __expf(s[r] - mn) : 0.f;
-        l_lane[r] = l_lane[r] * alpha[r] + pr;
-        pstrip[r * kTileTok + lane] = (uint16_t)to_vt16<VT>(pr);
-    }
-    if (rescale) {  // wave-uniform
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = 4 * (lane >> 4) + i;
-            float f = 1.f;
-#pragma unroll
-            for (int r = 0; r < RP; ++r)
-                if (row == r) f = alpha[r];
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) acc[dt][i] *= f;
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int arow = lane & 15;
-    const int kchunk = 8 * (lane >> 4);
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        const int tk = t0 + 32 * g + kchunk;
-        uint4 af = make_uint4(0, 0, 0, 0);
-        if (arow < RP) af = *reinterpret_cast<const uint4*>(pstrip + arow * kTileTok + 32 * g + kchunk);
-        if (tk + 8 > t_end) {  // tail: values of slots past the end are unwritten; zero them
-            const int keep = t_end - tk;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                uint32_t w[4] = {R.v[g][dt].x, R.v[g][dt].y, R.v[g][dt].z, R.v[g][dt].w};
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (j >= keep) w[j >> 1] &= (j & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-                R.v[g][dt] = make_uint4(w[0], w[1], w[2], w[3]);
-            }
-        }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma<VT>(af, R.v[g][dt], acc[dt]);
-    }
-    __builtin_amdgcn_wave_barrier();
+    tile_softmax_pv<RP, DT, VT, NB, PB>(p, pstrip, b, kv, t0, t_end, lane, s, R, m_run, l_lane, acc);
 }
 
 // vector of N floats from memory (N = 1, 2, 4 or a multiple of 4; 4N-byte aligned)
@@ -920,7 +722,7 @@ int pow2_at_least(int x) {
 struct MPlan {
     int RP, DT, split_len, n_splits;
     int rg, n_groups;  // query rows per row group, row groups
-    bool mx;           // k_decode_paged_mx (MFMA scores) in place of the LUT kernel
+    bool q4;           // k_decode_paged_q4 (4x4-MFMA scores) in place of the LUT kernel
     size_t smem, ws_bytes;
 };
 
@@ -977,15 +779,17 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     pl.DT = a->value_dim / 16;
     const bool lut_ok = a->n_centroids == kNC ? cbits == 0 || cbits == 8
                                               : a->n_centroids == 64 && cbits != 4 && lut64_shape(*a, pl.RP, pl.DT);
-    // Where the LUT needs row groups (or cannot serve the codes), the MFMA-scores kernel serves
+    // Where the LUT needs row groups (or cannot serve the codes), the 4x4-MFMA-scores kernel serves
     // up to 16 rows per pass over the pages instead (its codebook is head_dim x nc fp32 whatever
-    // the block size)
-    if (!lut_ok && !mx_shape(a)) return false;
-    pl.mx = !lut_ok || (pl.n_groups > 1 && mx_shape(a));
-    if (pl.mx) {
+    // the block size); kernel 4 asks for it wherever it applies
+    const bool q4_ok = ssq_decode_q4_shape(a);
+    if (a->kernel == 4 && !q4_ok) return false;
+    if (!lut_ok && !q4_ok) return false;
+    pl.q4 = a->kernel == 4 || !lut_ok || (pl.n_groups > 1 && q4_ok);
+    if (pl.q4) {
         pl.rg = rows < 16 ? rows : 16;
         pl.n_groups = (rows + 15) / 16;
-        pl.RP = 16;
+        pl.RP = 4 * ((pl.rg + 3) / 4);
     }
     const int units = a->batch * a->num_kv_heads * pl.n_groups;
     const int tiles = (a->seq_len + kTileTok - 1) / kTileTok;
@@ -998,13 +802,13 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     pl.split_len = tiles_per_split * kTileTok;
     // the split's block-table slice lives in LDS too: long contexts split until it fits
     while (tiles_per_split > 1 &&
-           (pl.mx ? mx_smem(*a, pl.split_len) : mfma_smem(*a, pl.RP, pl.split_len)) > kMaxSmem) {
+           (pl.q4 ? ssq_decode_q4_smem(a, pl.rg, pl.split_len) : mfma_smem(*a, pl.RP, pl.split_len)) > kMaxSmem) {
         tiles_per_split = (tiles_per_split + 1) / 2;
         pl.split_len = tiles_per_split * kTileTok;
     }
     pl.n_splits = (a->seq_len + pl.split_len - 1) / pl.split_len;
     if (pl.n_splits < 1) pl.n_splits = 1;
-    pl.smem = pl.mx ? mx_smem(*a, pl.split_len) : mfma_smem(*a, pl.RP, pl.split_len);
+    pl.smem = pl.q4 ? ssq_decode_q4_smem(a, pl.rg, pl.split_len) : mfma_smem(*a, pl.RP, pl.split_len);
     if (pl.smem > kMaxSmem) return false;
     const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
     pl.ws_bytes = pl.n_splits > 1 ? (size_t)pl.n_splits * n_rows_all * (a->value_dim + 2) * 4 : 0;
@@ -1133,8 +937,8 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
     mp.ws_m = ws ? ws + (size_t)pl.n_splits * n_rows_all * a->value_dim : nullptr;
     mp.ws_l = ws ? mp.ws_m + (size_t)pl.n_splits * n_rows_all : nullptr;
     int rc;
-    if (pl.mx) {
-        rc = mp.a.v_dtype == SSQ_BF16 ? launch_mx_vt<SSQ_BF16>(mp, pl, st) : launch_mx_vt<SSQ_F16>(mp, pl, st);
+    if (pl.q4) {
+        rc = ssq_decode_q4_launch(mp, dim3(mp.a.batch * mp.a.num_kv_heads, pl.n_splits, pl.n_groups), st);
         if (rc) return rc;
         if (pl.n_splits > 1) rc = ssq_launch_merge(*a, pl.n_splits, mp.ws_o, mp.ws_m, mp.ws_l, st);
         return rc;

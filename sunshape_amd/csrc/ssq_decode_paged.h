@@ -1,0 +1,227 @@
+// Pieces shared by the paged decode kernels (ssq_decode_mfma.hip: LUT scores and 16x16 MFMA scores;
+// ssq_decode_paged_q4.hip: 4x4 MFMA scores): launch shape, parameters, the wave reductions, and the
+// 64-token tile loads (one token's codes per lane, V fragments straight from the dim-major pages).
+#pragma once
+
+#include "ssq_common.h"
+
+// Parameters of one paged decode launch (shared type: both kernels' host code fills it)
+struct SsqPagedParams {
+    ssq_decode_args a;
+    int G, rows, split_len, n_splits;
+    int rg;  // query rows per row group (blockIdx.z)
+    float* ws_o;
+    float* ws_m;
+    float* ws_l;
+};
+
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+#ifndef SSQ_DECODE_WAVES
+#define SSQ_DECODE_WAVES 4
+#endif
+constexpr int kWaves = SSQ_DECODE_WAVES;  // waves per workgroup
+constexpr int kThreads = kWaves * SSQ_WAVE;
+constexpr int kTileTok = 64;  // tokens per wave iteration (4 pages)
+constexpr int kPage = 16;
+constexpr int kNC = 256;      // codewords per block (uint8 codes)
+constexpr size_t kMaxSmem = 160 * 1024;
+
+using MfmaParams = SsqPagedParams;
+
+
+template <int VT>
+__device__ __forceinline__ uint32_t to_vt16(float x) {
+    return VT == SSQ_BF16 ? ssq_f32_to_bf16(x) : ssq_f32_to_f16(x);
+}
+
+template <int VT>
+__device__ __forceinline__ v4f mfma(const uint4& a, const uint4& b, v4f c) {
+    if (VT == SSQ_BF16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0,
+                                                       0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+}
+
+// wave-wide max / sum: DPP rotations inside each 16-lane row, then the four row results by readlane
+template <int CTL>
+__device__ __forceinline__ float dpp_ror(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_ror<0x121>(v));
+    v = fmaxf(v, dpp_ror<0x122>(v));
+    v = fmaxf(v, dpp_ror<0x124>(v));
+    v = fmaxf(v, dpp_ror<0x128>(v));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_ror<0x121>(v);
+    v += dpp_ror<0x122>(v);
+    v += dpp_ror<0x124>(v);
+    v += dpp_ror<0x128>(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+// 16-byte load of streamed (read-once) data: non-temporal, so the single pass over
+// the values does not evict the codebooks and block tables other workgroups reuse
+#ifndef SSQ_STREAM_NT
+#define SSQ_STREAM_NT 1
+#endif
+#ifndef SSQ_CODES_NT
+#define SSQ_CODES_NT 1
+#endif
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const uint16_t* p) {
+#if SSQ_STREAM_NT
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+#else
+    return *reinterpret_cast<const uint4*>(p);
+#endif
+}
+
+// packed code rows (PB bits per code, 32 / PB codes per little-endian int32 word, the low bits
+// first; sunshape/triton_kernels.py:250-266): int32 words per row
+__host__ __device__ constexpr int pk_words(int NB, int PB) { return PB ? (NB + 32 / PB - 1) / (32 / PB) : 1; }
+
+// registers of one 64-token tile in flight
+template <int NB, int DT, int PB = 0>
+struct TileRegs {
+    uint4 c[NB / 16 > 0 ? NB / 16 : 1];  // this lane's token codes (NB bytes)
+    uint2 c8;                            // NB == 8
+    uint32_t pk[pk_words(NB, PB)];       // PB-bit codes in words (PB > 0)
+    uint4 v[2][DT];                      // B-operand V fragments of the two 32-token K groups
+};
+
+// cbase: the KV head's codes (bytes; with PB > 0 int32 words, strides counting words)
+template <int NB, int DT, int PB = 0>
+__device__ __forceinline__ void issue_tile(const ssq_decode_args& a, const int* pages, int t_begin, int t_end, int tile,
+                                           int lane, const uint8_t* cbase, const uint16_t* vbase,
+                                           TileRegs<NB, DT, PB>& R) {
+    // Every load is issued unconditionally (straight-line code keeps the compiler's vmcnt
+    // bookkeeping exact, so waiting for this tile never drains the next one).  Lanes past the
+    // split's end read their split's last token / 8-token chunk instead: a valid address whose
+    // data compute_tile masks (scores by `valid`, V chunks by the tail zeroing).
+    const int rel = tile * kTileTok;  // tile start relative to the split
+    const int last = t_end - 1 - t_begin;
+    const int tr = min(rel + lane, last);
+    const int page = pages[tr >> 4];
+    const uint8_t* crow = cbase + (int64_t)page * a.c_sb + (int64_t)((t_begin + tr) & 15) * a.c_st;
+    if constexpr (PB > 0) {
+        const uint32_t* prow = reinterpret_cast<const uint32_t*>(cbase) + (int64_t)page * a.c_sb +
+                               (int64_t)((t_begin + tr) & 15) * a.c_st;
+#pragma unroll
+        for (int i = 0; i < pk_words(NB, PB); ++i) R.pk[i] = __builtin_nontemporal_load(prow + i);
+    } else if (NB >= 16) {
+#pragma unroll
+        for (int i = 0; i < NB / 16; ++i) {
+#if SSQ_CODES_NT
+            const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(crow) + i);
+            R.c[i] = make_uint4(v.x, v.y, v.z, v.w);
+#else
+            R.c[i] = reinterpret_cast<const uint4*>(crow)[i];
+#endif
+        }
+    } else {
+        R.c8 = *reinterpret_cast<const uint2*>(crow);
+    }
+    const int kchunk = 8 * (lane >> 4);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const int r = min(rel + 32 * g + kchunk, last & ~7);
+        const uint16_t* src = vbase + (int64_t)pages[r >> 4] * a.v_sb + (r & 15);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) R.v[g][dt] = load_stream(src + (int64_t)(16 * dt) * a.v_st);
+    }
+}
+
+// After a tile's scores s[r] (row r, this lane's token t0 + lane): the raw-score store, the online
+// softmax update (wave-local), the probabilities cast to the value dtype through the wave's P strip
+// [RP][64], and P.V on v_mfma_f32_16x16x32 with V fragments from the tile's registers.
+template <int RP, int DT, int VT, int NB, int PB>
+__device__ __forceinline__ void tile_softmax_pv(const MfmaParams& p, uint16_t* pstrip, int b, int kv, int t0, int t_end,
+                                                int lane, const float (&s)[RP], TileRegs<NB, DT, PB>& R,
+                                                float (&m_run)[RP], float (&l_lane)[RP], v4f (&acc)[DT]) {
+    const ssq_decode_args& a = p.a;
+    const int t = t0 + lane;
+    const bool valid = t < t_end;
+    if (valid) {
+        if (a.scores) {
+            const int row0 = blockIdx.z * p.rg, nr = min(p.rg, p.rows - row0);
+#pragma unroll
+            for (int r = 0; r < RP; ++r) {
+                if (r < nr) {
+                    const int g = (row0 + r) / a.q_len, qi = row0 + r - g * a.q_len;
+                    const int h = kv * p.G + g;
+                    a.scores[(int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)qi * a.s_sl + t] = s[r];
+                }
+            }
+        }
+    }
+    // online softmax (wave-local)
+    float alpha[RP];
+    bool rescale = false;
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+        const float tm = wave_max(valid ? s[r] : -INFINITY);
+        const float mn = fmaxf(m_run[r], tm);
+        alpha[r] = (mn == -INFINITY) ? 1.f : __expf(m_run[r] - mn);
+        rescale |= mn != m_run[r];
+        m_run[r] = mn;
+        const float pr = (valid && mn != -INFINITY) ? __expf(s[r] - mn) : 0.f;
+        l_lane[r] = l_lane[r] * alpha[r] + pr;
+        pstrip[r * kTileTok + lane] = (uint16_t)to_vt16<VT>(pr);
+    }
+    if (rescale) {  // wave-uniform
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * (lane >> 4) + i;
+            float f = 1.f;
+#pragma unroll
+            for (int r = 0; r < RP; ++r)
+                if (row == r) f = alpha[r];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) acc[dt][i] *= f;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int arow = lane & 15;
+    const int kchunk = 8 * (lane >> 4);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const int tk = t0 + 32 * g + kchunk;
+        uint4 af = make_uint4(0, 0, 0, 0);
+        if (arow < RP) af = *reinterpret_cast<const uint4*>(pstrip + arow * kTileTok + 32 * g + kchunk);
+        if (tk + 8 > t_end) {  // tail: values of slots past the end are unwritten; zero them
+            const int keep = t_end - tk;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                uint32_t w[4] = {R.v[g][dt].x, R.v[g][dt].y, R.v[g][dt].z, R.v[g][dt].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (j >= keep) w[j >> 1] &= (j & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+                R.v[g][dt] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma<VT>(af, R.v[g][dt], acc[dt]);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+}  // namespace

@@ -1,0 +1,361 @@
+// Paged decode with the scores on 4x4 matrix-core blocks (gfx950).  The kernel template; its
+// instantiations are spread over ssq_decode_paged_q4_*.hip (compiled in parallel) and dispatched
+// from ssq_decode_paged_q4.hip.
+//
+// Paged decode with the scores on 4x4 matrix-core blocks: for query-row counts whose LUT
+// does not fit the LDS (8 query heads per KV head, or 64 blocks of dim 2 at head_dim 128, the
+// reference's default 4 bits/dim), and for codebooks other than 256 / 64 codewords.
+//
+// Same mathematics as the LUT kernels (ssq_decode_mfma.hip): scores q_perm . k_hat in fp32
+// (triton_kernels.py:381-408, :174-196, summed here in MFMA order, so within fp32 rounding of the
+// LUT path), online softmax, probabilities cast to the value dtype before P.V
+// (vllm_attn_backend.py:251-252).  Mapping:
+//
+//   workgroup = 4 waves (one per SIMD) for one (batch, KV head, context split, group of <= 16
+//               query rows); the codebook [nb][nc][bd] fp32 sits in LDS (128 KiB at head_dim 128
+//               and 256 codewords), so one workgroup per CU.
+//   wave      = streams 64-token tiles (4 pages) with its own running (max, sum, O), two tiles of
+//               codes and values in flight; waves merge through LDS at the end.
+//   scores    = one token per lane.  v_mfma_f32_4x4x1_16b_f32 computes 16 blocks of 4 rows x 4
+//               tokens x 1 dim: with the A operand broadcast from one block (cbsz 4, abid j) every
+//               block multiplies the same 4 query rows, so one instruction adds dim k of all 64
+//               tokens for 4 rows, and lane l's output VGPR i is row i's score for token l (the
+//               lane layout was checked on the device).  Lane 4j + i holds q_perm[row i][16kk + j]
+//               in A register kk, so dim 16kk + j is register kk with abid j: head_dim / 16
+//               registers per 4 rows.  The B operand is the lane's own token's codeword element,
+//               gathered from the LDS codebook bd floats at a time (ds_read_b64 at block_dim 2).
+//               Cost per 64-token tile: head_dim x ceil(rows / 4) two-pass MFMAs; the 16x16x4
+//               form spends as much on 4 rows as on 16.
+//   P.V       = v_mfma_f32_16x16x32_bf16 / _f16 with V fragments straight from the dim-major page
+//               (tile_softmax_pv, shared with the LUT kernel).
+#pragma once
+
+#include "ssq_decode_paged.h"
+
+#include <math.h>
+
+#include <type_traits>
+
+namespace {
+
+// LDS carve-up (bytes): codebook [NB][nc][BD] fp32, padded to 1 KiB | P strips [waves][RP][64]
+// 16-bit (the query rows [RP][KD] fp32 pass through them in the prologue) | pages [split_len/16]
+// int32.  The waves' merge reuses the codebook region.
+__host__ __device__ constexpr int q4_cb_floats(int KD, int nc) { return (KD * nc + 255) / 256 * 256; }
+inline size_t q4_strip_bytes(int RP) { return (size_t)kWaves * RP * kTileTok * 2; }
+inline size_t q4_smem(const ssq_decode_args& a, int RP, int split_len) {
+    const size_t main = (size_t)q4_cb_floats(a.head_dim, a.n_centroids) * 4 + q4_strip_bytes(RP) +
+                        (size_t)split_len / kPage * 4;
+    const size_t merge = (size_t)kWaves * RP * (a.value_dim + 2) * 4;
+    return main > merge ? main : merge;
+}
+
+// code of block blk for this lane's token (byte rows, or PB-bit codes packed in words)
+template <int NB, int DT, int PB>
+__device__ __forceinline__ uint32_t token_code(const TileRegs<NB, DT, PB>& R, int blk) {
+    if constexpr (PB > 0) {
+        constexpr int kVpe = 32 / PB;
+        return (R.pk[blk / kVpe] >> ((blk % kVpe) * PB)) & ((1u << PB) - 1u);
+    } else {
+        const int wi = blk >> 2;
+        uint32_t word;
+        if constexpr (NB >= 16) {
+            const uint4 c = R.c[wi >> 2];
+            word = (wi & 3) == 0 ? c.x : (wi & 3) == 1 ? c.y : (wi & 3) == 2 ? c.z : c.w;
+        } else {
+            word = (wi & 1) ? R.c8.y : R.c8.x;
+        }
+        return __builtin_amdgcn_ubfe(word, 8 * (blk & 3), 8);
+    }
+}
+
+// BD consecutive floats from LDS (BD = 1, 2, 4 or 8; 4*BD-byte aligned)
+template <int BD>
+__device__ __forceinline__ void lds_vec(const float* src, float (&dst)[BD]) {
+    if constexpr (BD >= 4) {
+#pragma unroll
+        for (int i = 0; i < BD; i += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(src + i);
+            dst[i] = v.x; dst[i + 1] = v.y; dst[i + 2] = v.z; dst[i + 3] = v.w;
+        }
+    } else if constexpr (BD == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(src);
+        dst[0] = v.x; dst[1] = v.y;
+    } else {
+        dst[0] = src[0];
+    }
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = B .. E-1 (the MFMA's broadcast block
+// id must be an immediate).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// Scores of one tile: s[r] = row r's score for this lane's token.  Codeword gathers run KB blocks
+// ahead of their MFMAs; even and odd blocks accumulate into separate chains (two independent MFMA
+// dependency chains even with one row quad), added at the end.
+template <int KD, int BD, int R4, int DT, int PB>
+__device__ __forceinline__ void tile_scores_q4(const float* cb, int nc, const TileRegs<KD / BD, DT, PB>& R,
+                                               const float (&qa)[R4][KD / 16], float (&s)[4 * R4]) {
+    constexpr int NB = KD / BD;
+    constexpr int KB = BD >= 4 ? 4 : 8;  // blocks gathered per batch
+    static_assert(NB % KB == 0, "blocks per batch must divide the block count");
+    const uint32_t ncm1 = (uint32_t)(nc - 1);
+    v4f c0[R4], c1[R4];
+#pragma unroll
+    for (int q = 0; q < R4; ++q) {
+        c0[q] = (v4f){0.f, 0.f, 0.f, 0.f};
+        c1[q] = (v4f){0.f, 0.f, 0.f, 0.f};
+    }
+    static_for<0, NB / KB>([&](auto bc) {
+        constexpr int b0 = decltype(bc)::value * KB;
+        float ev[KB][BD];
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            const int blk = b0 + k;
+            const uint32_t code = min(token_code<NB, DT, PB>(R, blk), ncm1);
+            lds_vec<BD>(cb + ((uint32_t)blk * (uint32_t)nc + code) * BD, ev[k]);
+        }
+        static_for<0, KB * BD>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            constexpr int k = i / BD, d = i % BD;
+            constexpr int blk = b0 + k, kd = blk * BD + d;
+#pragma unroll
+            for (int q = 0; q < R4; ++q) {
+                if constexpr (blk & 1)
+                    c1[q] = __builtin_amdgcn_mfma_f32_4x4x1f32(qa[q][kd >> 4], ev[k][d], c1[q], 4, kd & 15, 0);
+                else
+                    c0[q] = __builtin_amdgcn_mfma_f32_4x4x1f32(qa[q][kd >> 4], ev[k][d], c0[q], 4, kd & 15, 0);
+            }
+        });
+    });
+#pragma unroll
+    for (int q = 0; q < R4; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[4 * q + i] = c0[q][i] + c1[q][i];
+}
+
+template <int KD, int BD, int R4, int DT, int VT, int PB>
+__global__ __launch_bounds__(kThreads) void k_decode_paged_q4(const MfmaParams p) {
+    constexpr int NB = KD / BD;
+    constexpr int RP = 4 * R4;
+    constexpr int KQ = KD / 16;  // A registers per row quad
+    extern __shared__ __align__(16) float smem[];
+    const ssq_decode_args& a = p.a;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int bk = blockIdx.x;
+    const int split = blockIdx.y;
+    const int b = bk / a.num_kv_heads;
+    const int kv = bk - b * a.num_kv_heads;
+    const int nc = a.n_centroids;
+    const int row0 = blockIdx.z * p.rg;       // this workgroup's query rows: row0 .. row0 + nr - 1
+    const int nr = min(p.rg, p.rows - row0);  // <= RP
+    const int T = min(a.seq_lens[b], a.seq_len);
+    const int t_begin = split * p.split_len;
+    const int t_end = min(T, t_begin + p.split_len);
+
+    float* cb = smem;
+    uint8_t* strips = reinterpret_cast<uint8_t*>(smem + q4_cb_floats(KD, nc));
+    uint16_t* pstrip = reinterpret_cast<uint16_t*>(strips) + wave * RP * kTileTok;
+    int* pages = reinterpret_cast<int*>(strips + (size_t)kWaves * RP * kTileTok * 2);
+
+    // ---- prologue: block-table slice, this lane's permutation entries, the query rows (scaled,
+    // unpermuted) through LDS into the A registers
+    const int32_t* btab = a.block_table + (int64_t)b * a.bt_sb + t_begin / kPage;
+    const int n_pages = t_end > t_begin ? (t_end - t_begin + kPage - 1) / kPage : 0;
+    for (int i = tid; i < n_pages; i += kThreads) pages[i] = btab[i];
+    const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
+    const int qi4 = lane & 3, qj = lane >> 2;
+    int64_t pj[KQ];
+#pragma unroll
+    for (int kk = 0; kk < KQ; ++kk) pj[kk] = perm[16 * kk + qj];
+    float* qs = reinterpret_cast<float*>(strips);  // [RP][KD] fp32: RP * KD * 4 <= the strips' RP * 512 bytes
+    {
+        constexpr int kQE = (RP * KD + kThreads - 1) / kThreads;
+        int64_t src[kQE];
+        bool ok[kQE];
+#pragma unroll
+        for (int k = 0; k < kQE; ++k) {
+            const int e = tid + k * kThreads;
+            const int r = e / KD, j = e - r * KD;
+            ok[k] = e < RP * KD && r < nr;
+            src[k] = 0;  // rows past nr read element 0 and are zeroed
+            if (ok[k]) {
+                const int g = (row0 + r) / a.q_len, qi = row0 + r - g * a.q_len;
+                const int h = kv * p.G + g;
+                src[k] = (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl + j;
+            }
+        }
+        float qv[kQE];
+        ssq_load_elems(a.q, a.q_dtype, src, qv);
+#pragma unroll
+        for (int k = 0; k < kQE; ++k) {
+            const int e = tid + k * kThreads;
+            if (e < RP * KD) qs[e] = !ok[k] ? 0.f : a.has_scale ? ssq_round_to(qv[k] * a.scale, a.q_dtype) : qv[k];
+        }
+    }
+    __syncthreads();  // qs and pages written
+    float qa[R4][KQ];
+#pragma unroll
+    for (int q = 0; q < R4; ++q)
+#pragma unroll
+        for (int kk = 0; kk < KQ; ++kk) qa[q][kk] = qs[(4 * q + qi4) * KD + (int)min((uint64_t)pj[kk], (uint64_t)(KD - 1))];
+    __syncthreads();  // every wave has its A registers: the strips are free
+
+    const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)kv * a.v_sh + (int64_t)(lane & 15) * a.v_st;
+    const uint8_t* cbase = PB > 0 ? reinterpret_cast<const uint8_t*>(reinterpret_cast<const uint32_t*>(a.codes) +
+                                                                     (int64_t)kv * a.c_sh)
+                                  : a.codes + (int64_t)kv * a.c_sh;
+    const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
+    const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
+    TileRegs<NB, DT, PB> RA, RB;
+    int tile = wave;
+    if (n_tiles > 0) issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, RA);
+    // the codebook goes global -> LDS directly: 1 KiB chunks, lane l's 16 bytes at chunk + 16 l;
+    // the tail chunk's lanes past the end re-read the last float4 into the padding
+    {
+        const float* cent = a.cent + (int64_t)kv * a.cent_sh;
+        const int n4 = KD * nc / 4;
+        const int n_chunks = (n4 + 63) / 64;
+        for (int c = wave; c < n_chunks; c += kWaves) {
+            const int i = min(c * 64 + lane, n4 - 1);
+            __builtin_amdgcn_global_load_lds(cent + 4 * i, (__attribute__((address_space(3))) void*)(cb + 256 * c), 16,
+                                             0, 0);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's codebook chunks (and its first tile) have landed
+    __syncthreads();
+
+    // ---- stream tiles, two in flight per wave (A/B register sets)
+    float m_run[RP], l_lane[RP];
+#pragma unroll
+    for (int r = 0; r < RP; ++r) { m_run[r] = -INFINITY; l_lane[r] = 0.f; }
+    v4f acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
+    while (tile < n_tiles) {
+        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RB);
+        {
+            float s[RP];
+            tile_scores_q4<KD, BD, R4, DT, PB>(cb, nc, RA, qa, s);
+            tile_softmax_pv<RP, DT, VT, NB, PB>(p, pstrip, b, kv, t_begin + tile * kTileTok, t_end, lane, s, RA, m_run,
+                                                l_lane, acc);
+        }
+        tile += kWaves;
+        if (tile >= n_tiles) break;
+        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RA);
+        {
+            float s[RP];
+            tile_scores_q4<KD, BD, R4, DT, PB>(cb, nc, RB, qa, s);
+            tile_softmax_pv<RP, DT, VT, NB, PB>(p, pstrip, b, kv, t_begin + tile * kTileTok, t_end, lane, s, RB, m_run,
+                                                l_lane, acc);
+        }
+        tile += kWaves;
+    }
+
+    // ---- merge the waves' (m, l, O) through LDS (the codebook is no longer needed)
+    float l_w[RP];
+#pragma unroll
+    for (int r = 0; r < RP; ++r) l_w[r] = wave_sum(l_lane[r]);
+    __syncthreads();
+    float* mbuf = smem;                // [waves][RP]
+    float* lbuf = mbuf + kWaves * RP;  // [waves][RP]
+    float* obuf = lbuf + kWaves * RP;  // [waves][RP][Dv]
+    constexpr int Dv = DT * 16;
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < RP; ++r) { mbuf[wave * RP + r] = m_run[r]; lbuf[wave * RP + r] = l_w[r]; }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = 4 * (lane >> 4) + i;
+        if (row < RP) {
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) obuf[((size_t)wave * RP + row) * Dv + 16 * dt + (lane & 15)] = acc[dt][i];
+        }
+    }
+    __syncthreads();
+    const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
+    for (int e = tid; e < nr * Dv; e += kThreads) {
+        const int r = e / Dv, dv = e - r * Dv;
+        float M = -INFINITY;
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mbuf[w * RP + r]);
+        float L = 0.f, o = 0.f;
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = mbuf[w * RP + r];
+            if (mw == -INFINITY) continue;
+            const float f = __expf(mw - M);
+            L += lbuf[w * RP + r] * f;
+            o += obuf[((size_t)w * RP + r) * Dv + dv] * f;
+        }
+        const int g = (row0 + r) / a.q_len, qi = row0 + r - g * a.q_len;
+        const int h = kv * p.G + g;
+        const int rid = (b * a.num_q_heads + h) * a.q_len + qi;
+        if (p.n_splits == 1) {
+            ssq_store_elem(a.out, a.v_dtype, (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)qi * a.o_sl + dv, o / L);
+            if (a.lse && dv == 0) a.lse[rid] = M + logf(L);
+        } else {
+            p.ws_o[((size_t)split * n_rows_all + rid) * Dv + dv] = o;
+            if (dv == 0) {
+                p.ws_m[(size_t)split * n_rows_all + rid] = M;
+                p.ws_l[(size_t)split * n_rows_all + rid] = L;
+            }
+        }
+    }
+}
+
+
+template <int KD, int BD, int R4, int DT, int VT, int PB>
+int launch_q4(const MfmaParams& mp, const dim3& grid, size_t smem, hipStream_t st) {
+    auto kern = k_decode_paged_q4<KD, BD, R4, DT, VT, PB>;
+    int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_paged_q4)");
+    if (rc) return rc;
+    hipLaunchKernelGGL(kern, grid, dim3(kThreads), smem, st, mp);
+    return ssq_check_hip(hipGetLastError(), "k_decode_paged_q4 launch");
+}
+template <int KD, int BD, int R4, int VT, int PB>
+int q4_dt(const MfmaParams& mp, int DT, const dim3& grid, size_t smem, hipStream_t st) {
+    return DT == 4 ? launch_q4<KD, BD, R4, 4, VT, PB>(mp, grid, smem, st) : launch_q4<KD, BD, R4, 8, VT, PB>(mp, grid, smem, st);
+}
+template <int KD, int BD, int VT, int PB>
+int q4_r4(const MfmaParams& mp, int R4, int DT, const dim3& grid, size_t smem, hipStream_t st) {
+    switch (R4) {
+        case 1: return q4_dt<KD, BD, 1, VT, PB>(mp, DT, grid, smem, st);
+        case 2: return q4_dt<KD, BD, 2, VT, PB>(mp, DT, grid, smem, st);
+        case 3: return q4_dt<KD, BD, 3, VT, PB>(mp, DT, grid, smem, st);
+        default: return q4_dt<KD, BD, 4, VT, PB>(mp, DT, grid, smem, st);
+    }
+}
+// every instantiation for one head_dim, value dtype and code width
+template <int KD, int VT, int PB>
+int q4_dispatch(const MfmaParams& mp, int R4, int DT, const dim3& grid, size_t smem, hipStream_t st) {
+    switch (mp.a.block_dim) {
+        case 1: if constexpr (KD <= 64) return q4_r4<KD, 1, VT, PB>(mp, R4, DT, grid, smem, st); break;
+        case 2: return q4_r4<KD, 2, VT, PB>(mp, R4, DT, grid, smem, st);
+        case 4: return q4_r4<KD, 4, VT, PB>(mp, R4, DT, grid, smem, st);
+        case 8: return q4_r4<KD, 8, VT, PB>(mp, R4, DT, grid, smem, st);
+        default: break;
+    }
+    return ssq_fail(SSQ_ERR_UNSUPPORTED, "4x4-MFMA decode: block_dim %d at head_dim %d", mp.a.block_dim, KD);
+}
+
+}  // namespace
+
+// the instantiation units (ssq_decode_paged_q4_<head_dim>_<value dtype>_<codes>.hip)
+#define SSQ_Q4_UNIT(name) \
+    int name(const SsqPagedParams& mp, int R4, int DT, const dim3& grid, size_t smem, hipStream_t st)
+SSQ_Q4_UNIT(ssq_q4_64_bf16_bytes);
+SSQ_Q4_UNIT(ssq_q4_64_bf16_packed);
+SSQ_Q4_UNIT(ssq_q4_64_f16_bytes);
+SSQ_Q4_UNIT(ssq_q4_64_f16_packed);
+SSQ_Q4_UNIT(ssq_q4_128_bf16_bytes);
+SSQ_Q4_UNIT(ssq_q4_128_bf16_packed);
+SSQ_Q4_UNIT(ssq_q4_128_f16_bytes);
+SSQ_Q4_UNIT(ssq_q4_128_f16_packed);

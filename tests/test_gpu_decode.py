@@ -390,3 +390,43 @@ def test_contiguous_mfma_scores_only_vs_oracle(bd):
             qs = O.query_scale(q[b, kv * G:(kv + 1) * G, 0].float().numpy(), 0.125, "bf16")
             ref = O.attention_scores(qs, codes[b, kv].numpy(), cb.centroids[kv].numpy(), cb.perm[kv].numpy())
             assert_rel(s3[b, kv * G:(kv + 1) * G, 0], ref, SCORE_TOL, f"b={b} kv={kv}")
+
+
+@pytest.mark.parametrize("G,bd,D,Dv,nc,vdt,splits", [
+    (1, 4, 128, 128, 256, torch.bfloat16, 0), (3, 2, 128, 128, 256, torch.bfloat16, 0),
+    (4, 2, 128, 128, 256, torch.float16, 3), (5, 1, 64, 64, 256, torch.bfloat16, 0),
+    (8, 4, 128, 128, 16, torch.bfloat16, 0), (13, 8, 64, 64, 64, torch.bfloat16, 2),
+    (16, 2, 64, 64, 256, torch.float16, 0), (4, 8, 128, 64, 256, torch.bfloat16, 0)])
+def test_paged_q4_kernel_vs_oracle(G, bd, D, Dv, nc, vdt, splits):
+    """The 4x4-MFMA-scores paged kernel (kernel 4) over its shape range: 1 to 16 query rows per KV
+    head (1 to 4 row quads), block_dim 1/2/4/8, head_dim 64/128, value_dim 64/128, 16/64/256
+    codewords, fp16 values, forced splits, ragged sequence lengths; outputs, lse and raw scores
+    against the oracle."""
+    log(f"paged q4 G={G} bd={bd} D={D} Dv={Dv} nc={nc} vdt={vdt} splits={splits}")
+    B, Hkv, T, page = 3, 2, 1024, 16
+    cb = synthetic.make_codebook(Hkv, D, bd, 70 + G + bd, n_centroids=nc)
+    g = torch.Generator().manual_seed(71 + G)
+    q = torch.randn(B, G * Hkv, 1, D, generator=g).to(torch.bfloat16)
+    P = B * T // page
+    table = torch.randperm(P, generator=g).to(torch.int32).view(B, T // page)
+    code_pages = torch.randint(0, nc, (P, Hkv, page, D // bd), generator=g, dtype=torch.uint8)
+    v_pages = torch.randn(P, Hkv, Dv, page, generator=g).to(vdt)
+    lens = torch.tensor([T, 517, 16 * 9 + 5], dtype=torch.int32)
+    out, lse, scores = hip_ops.decode(q.to(DEV), code_pages.to(DEV), v_pages.to(DEV), cb.perm.to(DEV),
+                                      cb.centroids.to(DEV), scale=1 / math.sqrt(D), block_table=table.to(DEV),
+                                      seq_lens=lens.to(DEV), return_lse=True, return_scores=True, kernel=4,
+                                      num_splits=splits)
+    o, l, sc = np_of(out), np_of(lse), np_of(scores)
+    vn = "f16" if vdt == torch.float16 else "bf16"
+    for b in range(B):
+        L = int(lens[b])
+        codes = O.gather_pages_codes(code_pages.numpy(), table[b].numpy(), L)
+        vals = O.gather_pages_values(v_pages.float().numpy(), table[b].numpy(), L)
+        for kv in range(Hkv):
+            ro, rs, rl = _oracle_unit(np_of(q)[b, kv * G:(kv + 1) * G], codes[kv], vals[kv], cb.centroids[kv].numpy(),
+                                      cb.perm[kv].numpy(), 1 / math.sqrt(D), vdt=vn)
+            sl = slice(kv * G, (kv + 1) * G)
+            assert_rel(o[b, sl], ro, BF16_TOL, f"q4 out b={b} kv={kv}")
+            assert_rel(l[b, sl], rl, SCORE_TOL, f"q4 lse b={b} kv={kv}")
+            assert_rel(sc[b, sl, :, :L], rs, SCORE_TOL, f"q4 scores b={b} kv={kv}")
+            assert np.all(sc[b, sl, :, L:] == -np.inf)
