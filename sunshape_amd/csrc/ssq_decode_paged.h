@@ -34,9 +34,18 @@ constexpr size_t kMaxSmem = 160 * 1024;
 using MfmaParams = SsqPagedParams;
 
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// round to the value dtype (round to nearest even; gfx950's v_cvt_pk_bf16_f32 for bf16)
 template <int VT>
 __device__ __forceinline__ uint32_t to_vt16(float x) {
-    return VT == SSQ_BF16 ? ssq_f32_to_bf16(x) : ssq_f32_to_f16(x);
+    if constexpr (VT == SSQ_BF16) {
+        const bf16x2_t r = __builtin_convertvector((f32x2_t){x, 0.f}, bf16x2_t);
+        return __builtin_bit_cast(uint32_t, r) & 0xFFFFu;
+    } else {
+        return ssq_f32_to_f16(x);
+    }
 }
 
 template <int VT>
@@ -186,13 +195,14 @@ __device__ __forceinline__ void tile_softmax_pv(const MfmaParams& p, uint16_t* p
         pstrip[r * kTileTok + lane] = (uint16_t)to_vt16<VT>(pr);
     }
     if (rescale) {  // wave-uniform
+        // accumulator row 4 g + i lives in lane group g = lane / 16
+        const int grp = lane >> 4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = 4 * (lane >> 4) + i;
             float f = 1.f;
 #pragma unroll
-            for (int r = 0; r < RP; ++r)
-                if (row == r) f = alpha[r];
+            for (int g = 0; g < 4; ++g)
+                if (4 * g + i < RP) f = grp == g ? alpha[4 * g + i] : f;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) acc[dt][i] *= f;
         }
@@ -202,12 +212,13 @@ __device__ __forceinline__ void tile_softmax_pv(const MfmaParams& p, uint16_t* p
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int arow = lane & 15;
     const int kchunk = 8 * (lane >> 4);
+    const bool tail = t0 + kTileTok > t_end;  // wave-uniform: the tile holds the split's end
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
         const int tk = t0 + 32 * g + kchunk;
         uint4 af = make_uint4(0, 0, 0, 0);
         if (arow < RP) af = *reinterpret_cast<const uint4*>(pstrip + arow * kTileTok + 32 * g + kchunk);
-        if (tk + 8 > t_end) {  // tail: values of slots past the end are unwritten; zero them
+        if (tail && tk + 8 > t_end) {  // values of slots past the end are unwritten; zero them
             const int keep = t_end - tk;
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {

@@ -36,18 +36,61 @@
 
 #include <type_traits>
 
+#ifndef SSQ_Q4_WAVES
+#define SSQ_Q4_WAVES 8
+#endif
+
 namespace {
 
 // LDS carve-up (bytes): codebook [NB][nc][BD] fp32, padded to 1 KiB | P strips [waves][RP][64]
 // 16-bit (the query rows [RP][KD] fp32 pass through them in the prologue) | pages [split_len/16]
 // int32.  The waves' merge reuses the codebook region.
 __host__ __device__ constexpr int q4_cb_floats(int KD, int nc) { return (KD * nc + 255) / 256 * 256; }
-inline size_t q4_strip_bytes(int RP) { return (size_t)kWaves * RP * kTileTok * 2; }
-inline size_t q4_smem(const ssq_decode_args& a, int RP, int split_len) {
-    const size_t main = (size_t)q4_cb_floats(a.head_dim, a.n_centroids) * 4 + q4_strip_bytes(RP) +
+inline size_t q4_strip_bytes(int RP, int W) { return (size_t)W * RP * kTileTok * 2; }
+inline size_t q4_smem(const ssq_decode_args& a, int RP, int split_len, int W) {
+    const size_t main = (size_t)q4_cb_floats(a.head_dim, a.n_centroids) * 4 + q4_strip_bytes(RP, W) +
                         (size_t)split_len / kPage * 4;
-    const size_t merge = (size_t)kWaves * RP * (a.value_dim + 2) * 4;
+    const size_t merge = (size_t)W * RP * (a.value_dim + 2) * 4;
     return main > merge ? main : merge;
+}
+
+// The halves of issue_tile (ssq_decode_paged.h), for the one-register-set pipeline: a tile's codes
+// are reloaded as soon as its scores are done, its values as soon as its P.V is done.
+template <int NB, int DT, int PB>
+__device__ __forceinline__ void issue_codes(const ssq_decode_args& a, const int* pages, int t_begin, int t_end, int tile,
+                                            int lane, const uint8_t* cbase, TileRegs<NB, DT, PB>& R) {
+    const int last = t_end - 1 - t_begin;
+    const int tr = min(tile * kTileTok + lane, last);
+    const int page = pages[tr >> 4];
+    if constexpr (PB > 0) {
+        const uint32_t* prow = reinterpret_cast<const uint32_t*>(cbase) + (int64_t)page * a.c_sb +
+                               (int64_t)((t_begin + tr) & 15) * a.c_st;
+#pragma unroll
+        for (int i = 0; i < pk_words(NB, PB); ++i) R.pk[i] = __builtin_nontemporal_load(prow + i);
+    } else if constexpr (NB >= 16) {
+        const uint8_t* crow = cbase + (int64_t)page * a.c_sb + (int64_t)((t_begin + tr) & 15) * a.c_st;
+#pragma unroll
+        for (int i = 0; i < NB / 16; ++i) {
+            const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(crow) + i);
+            R.c[i] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+    } else {
+        const uint8_t* crow = cbase + (int64_t)page * a.c_sb + (int64_t)((t_begin + tr) & 15) * a.c_st;
+        R.c8 = *reinterpret_cast<const uint2*>(crow);
+    }
+}
+template <int NB, int DT, int PB>
+__device__ __forceinline__ void issue_values(const ssq_decode_args& a, const int* pages, int t_begin, int t_end, int tile,
+                                             int lane, const uint16_t* vbase, TileRegs<NB, DT, PB>& R) {
+    const int last = t_end - 1 - t_begin;
+    const int kchunk = 8 * (lane >> 4);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const int r = min(tile * kTileTok + 32 * g + kchunk, last & ~7);
+        const uint16_t* src = vbase + (int64_t)pages[r >> 4] * a.v_sb + (r & 15);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) R.v[g][dt] = load_stream(src + (int64_t)(16 * dt) * a.v_st);
+    }
 }
 
 // code of block blk for this lane's token (byte rows, or PB-bit codes packed in words)
@@ -96,14 +139,27 @@ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
-// Scores of one tile: s[r] = row r's score for this lane's token.  Codeword gathers run KB blocks
-// ahead of their MFMAs; even and odd blocks accumulate into separate chains (two independent MFMA
-// dependency chains even with one row quad), added at the end.
+// Scores of one tile: s[r] = row r's score for this lane's token.  Codeword gathers are issued one
+// batch (KB blocks) ahead of the MFMAs that consume them, so an LDS latency overlaps a batch of
+// matrix-core work.  With one row quad, even and odd blocks accumulate into separate chains (two
+// independent MFMA dependency chains), added at the end; more quads interleave their own chains.
+template <int KB, int NB, int BD, int DT, int PB>
+__device__ __forceinline__ void gather_batch(const float* cb, int nc, uint32_t ncm1, const TileRegs<NB, DT, PB>& R,
+                                             int b0, float (&ev)[KB][BD]) {
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const int blk = b0 + k;
+        const uint32_t code = min(token_code<NB, DT, PB>(R, blk), ncm1);
+        lds_vec<BD>(cb + ((uint32_t)blk * (uint32_t)nc + code) * BD, ev[k]);
+    }
+}
+
 template <int KD, int BD, int R4, int DT, int PB>
 __device__ __forceinline__ void tile_scores_q4(const float* cb, int nc, const TileRegs<KD / BD, DT, PB>& R,
                                                const float (&qa)[R4][KD / 16], float (&s)[4 * R4]) {
     constexpr int NB = KD / BD;
     constexpr int KB = BD >= 4 ? 4 : 8;  // blocks gathered per batch
+    constexpr int NBATCH = NB / KB;
     static_assert(NB % KB == 0, "blocks per batch must divide the block count");
     const uint32_t ncm1 = (uint32_t)(nc - 1);
     v4f c0[R4], c1[R4];
@@ -112,36 +168,39 @@ __device__ __forceinline__ void tile_scores_q4(const float* cb, int nc, const Ti
         c0[q] = (v4f){0.f, 0.f, 0.f, 0.f};
         c1[q] = (v4f){0.f, 0.f, 0.f, 0.f};
     }
-    static_for<0, NB / KB>([&](auto bc) {
-        constexpr int b0 = decltype(bc)::value * KB;
-        float ev[KB][BD];
-#pragma unroll
-        for (int k = 0; k < KB; ++k) {
-            const int blk = b0 + k;
-            const uint32_t code = min(token_code<NB, DT, PB>(R, blk), ncm1);
-            lds_vec<BD>(cb + ((uint32_t)blk * (uint32_t)nc + code) * BD, ev[k]);
-        }
+    float ev[2][KB][BD];
+    gather_batch<KB, NB, BD, DT, PB>(cb, nc, ncm1, R, 0, ev[0]);
+    static_for<0, NBATCH>([&](auto bc) {
+        constexpr int bi = decltype(bc)::value;
+        constexpr int b0 = bi * KB;
+        if constexpr (bi + 1 < NBATCH) gather_batch<KB, NB, BD, DT, PB>(cb, nc, ncm1, R, b0 + KB, ev[(bi + 1) & 1]);
         static_for<0, KB * BD>([&](auto ic) {
             constexpr int i = decltype(ic)::value;
             constexpr int k = i / BD, d = i % BD;
             constexpr int blk = b0 + k, kd = blk * BD + d;
+            const float e = ev[bi & 1][k][d];
 #pragma unroll
             for (int q = 0; q < R4; ++q) {
-                if constexpr (blk & 1)
-                    c1[q] = __builtin_amdgcn_mfma_f32_4x4x1f32(qa[q][kd >> 4], ev[k][d], c1[q], 4, kd & 15, 0);
+                if constexpr (R4 == 1 && (blk & 1))
+                    c1[q] = __builtin_amdgcn_mfma_f32_4x4x1f32(qa[q][kd >> 4], e, c1[q], 4, kd & 15, 0);
                 else
-                    c0[q] = __builtin_amdgcn_mfma_f32_4x4x1f32(qa[q][kd >> 4], ev[k][d], c0[q], 4, kd & 15, 0);
+                    c0[q] = __builtin_amdgcn_mfma_f32_4x4x1f32(qa[q][kd >> 4], e, c0[q], 4, kd & 15, 0);
             }
         });
     });
 #pragma unroll
     for (int q = 0; q < R4; ++q)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s[4 * q + i] = c0[q][i] + c1[q][i];
+        for (int i = 0; i < 4; ++i) s[4 * q + i] = R4 == 1 ? c0[q][i] + c1[q][i] : c0[q][i];
 }
 
-template <int KD, int BD, int R4, int DT, int VT, int PB>
-__global__ __launch_bounds__(kThreads) void k_decode_paged_q4(const MfmaParams p) {
+// W waves per workgroup: 4 (one per SIMD) keep two tiles in flight per wave in two register sets;
+// 8 (two per SIMD, so one wave's matrix-core phase overlaps the other's VALU and LDS phases) keep
+// one set, reloading a tile's codes once its scores are done and its values once its P.V is done.
+template <int KD, int BD, int R4, int DT, int VT, int PB, int W>
+__global__ __launch_bounds__(W * SSQ_WAVE) void k_decode_paged_q4(const MfmaParams p) {
+    constexpr int kThreads = W * SSQ_WAVE;
+    constexpr int kWaves = W;
     constexpr int NB = KD / BD;
     constexpr int RP = 4 * R4;
     constexpr int KQ = KD / 16;  // A registers per row quad
@@ -218,6 +277,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_paged_q4(const MfmaParams p
     TileRegs<NB, DT, PB> RA, RB;
     int tile = wave;
     if (n_tiles > 0) issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, RA);
+    (void)RB;
     // the codebook goes global -> LDS directly: 1 KiB chunks, lane l's 16 bytes at chunk + 16 l;
     // the tail chunk's lanes past the end re-read the last float4 into the padding
     {
@@ -240,24 +300,39 @@ __global__ __launch_bounds__(kThreads) void k_decode_paged_q4(const MfmaParams p
     v4f acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
-    while (tile < n_tiles) {
-        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RB);
-        {
+    if constexpr (W == 4) {
+        while (tile < n_tiles) {
+            issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RB);
+            {
+                float s[RP];
+                tile_scores_q4<KD, BD, R4, DT, PB>(cb, nc, RA, qa, s);
+                tile_softmax_pv<RP, DT, VT, NB, PB>(p, pstrip, b, kv, t_begin + tile * kTileTok, t_end, lane, s, RA,
+                                                    m_run, l_lane, acc);
+            }
+            tile += kWaves;
+            if (tile >= n_tiles) break;
+            issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RA);
+            {
+                float s[RP];
+                tile_scores_q4<KD, BD, R4, DT, PB>(cb, nc, RB, qa, s);
+                tile_softmax_pv<RP, DT, VT, NB, PB>(p, pstrip, b, kv, t_begin + tile * kTileTok, t_end, lane, s, RB,
+                                                    m_run, l_lane, acc);
+            }
+            tile += kWaves;
+        }
+    } else {
+        // one register set: every load is issued unconditionally (clamped to the last tile), so the
+        // queue of outstanding loads is the same on every path
+        while (tile < n_tiles) {
+            const int next = min(tile + kWaves, last_tile);
             float s[RP];
             tile_scores_q4<KD, BD, R4, DT, PB>(cb, nc, RA, qa, s);
+            issue_codes<NB, DT, PB>(a, pages, t_begin, t_end, next, lane, cbase, RA);
             tile_softmax_pv<RP, DT, VT, NB, PB>(p, pstrip, b, kv, t_begin + tile * kTileTok, t_end, lane, s, RA, m_run,
                                                 l_lane, acc);
+            issue_values<NB, DT, PB>(a, pages, t_begin, t_end, next, lane, vbase, RA);
+            tile += kWaves;
         }
-        tile += kWaves;
-        if (tile >= n_tiles) break;
-        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RA);
-        {
-            float s[RP];
-            tile_scores_q4<KD, BD, R4, DT, PB>(cb, nc, RB, qa, s);
-            tile_softmax_pv<RP, DT, VT, NB, PB>(p, pstrip, b, kv, t_begin + tile * kTileTok, t_end, lane, s, RB, m_run,
-                                                l_lane, acc);
-        }
-        tile += kWaves;
     }
 
     // ---- merge the waves' (m, l, O) through LDS (the codebook is no longer needed)
@@ -312,12 +387,19 @@ __global__ __launch_bounds__(kThreads) void k_decode_paged_q4(const MfmaParams p
 }
 
 
+// waves per workgroup for this instantiation (see k_decode_paged_q4)
+template <int KD, int BD, int R4, int DT>
+constexpr int q4_waves() { return SSQ_Q4_WAVES; }
+
 template <int KD, int BD, int R4, int DT, int VT, int PB>
-int launch_q4(const MfmaParams& mp, const dim3& grid, size_t smem, hipStream_t st) {
-    auto kern = k_decode_paged_q4<KD, BD, R4, DT, VT, PB>;
+int launch_q4(const MfmaParams& mp, const dim3& grid, size_t, hipStream_t st) {
+    constexpr int W = q4_waves<KD, BD, R4, DT>();
+    auto kern = k_decode_paged_q4<KD, BD, R4, DT, VT, PB, W>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_paged_q4)");
     if (rc) return rc;
-    hipLaunchKernelGGL(kern, grid, dim3(kThreads), smem, st, mp);
+    const size_t smem = q4_smem(mp.a, 4 * R4, mp.split_len, W);
+    if (smem > kMaxSmem) return ssq_fail(SSQ_ERR_UNSUPPORTED, "4x4-MFMA decode: %zu bytes of LDS", smem);
+    hipLaunchKernelGGL(kern, grid, dim3(W * SSQ_WAVE), smem, st, mp);
     return ssq_check_hip(hipGetLastError(), "k_decode_paged_q4 launch");
 }
 template <int KD, int BD, int R4, int VT, int PB>

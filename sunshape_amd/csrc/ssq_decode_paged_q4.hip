@@ -15,7 +15,7 @@ bool ssq_decode_q4_shape(const ssq_decode_args* a) {
 
 // LDS bytes for rg query rows per group and split_len tokens per split
 size_t ssq_decode_q4_smem(const ssq_decode_args* a, int rg, int split_len) {
-    return q4_smem(*a, 4 * ((rg + 3) / 4), split_len);
+    return q4_smem(*a, 4 * ((rg + 3) / 4), split_len, SSQ_Q4_WAVES);
 }
 
 // Launches the 4x4-MFMA kernel for a planned problem (grid: batch*KV heads, splits, row groups);
@@ -23,7 +23,7 @@ size_t ssq_decode_q4_smem(const ssq_decode_args* a, int rg, int split_len) {
 int ssq_decode_q4_launch(const SsqPagedParams& mp, const dim3& grid, hipStream_t st) {
     const int R4 = (mp.rg + 3) / 4;
     const int DT = mp.a.value_dim / 16;
-    const size_t smem = q4_smem(mp.a, 4 * R4, mp.split_len);
+    const size_t smem = 0;  // launch_q4 sizes the LDS for its wave count
     const bool bf = mp.a.v_dtype == SSQ_BF16;
     const bool packed = mp.a.code_bits == 4 || mp.a.code_bits == 6;
     if (mp.a.head_dim == 64) {
