@@ -376,343 +376,6 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// k_decode_paged_mx: the same paged decode with the scores on the matrix cores, for shapes whose
-// LUT would need row groups (more query rows per KV head than a LUT of <= 128 KiB holds), whose
-// codebook has fewer than 256 codewords, or whose codes are 4- / 6-bit words (PB; unpacked to
-// bytes as the tile's codes are copied to LDS).
-//
-//   scores = v_mfma_f32_16x16x4f32 over Qp [16 rows x KD] . K_hat^T: the permuted, scaled query
-//            rows are a fixed A operand in registers; each lane gathers its B element
-//            K_hat[token][dim] = C[blk][code][d] from the codebook staged in LDS (KD x nc fp32,
-//            128 KiB at head_dim 128 and 256 codewords, whatever the block size).  No LUT, so up to 16 query rows
-//            share one pass over the pages.  fp32 products and sums in MFMA order, so scores
-//            match the LUT kernels within fp32 rounding.
-//   P.V    = as k_decode_mfma: P through a per-wave LDS strip, V fragments straight from the page.
-//
-// LDS (bytes): codebook [NB][nc][BD] fp32, padded to 1 KB chunks | per wave: codes [64][NB],
-// P strip [16][64] 16-bit | pages [split_len / 16] int32.  The query rows pass through the
-// per-wave regions in the prologue; the waves' merge reuses the codebook region.
-// ---------------------------------------------------------------------------
-__host__ __device__ constexpr int mx_cb_floats(int KD, int nc) { return (KD * nc + 255) / 256 * 256; }
-__host__ __device__ constexpr int mx_wave_bytes(int NB) { return kTileTok * NB + 16 * kTileTok * 2; }
-inline size_t mx_smem(const ssq_decode_args& a, int split_len) {
-    const int NB = a.n_blocks;
-    const size_t main = (size_t)mx_cb_floats(a.head_dim, a.n_centroids) * 4 + (size_t)kWaves * mx_wave_bytes(NB) +
-                        (size_t)split_len / kPage * 4;
-    const size_t merge = (size_t)kWaves * 16 * (a.value_dim + 2) * 4;
-    const size_t qrows = (size_t)mx_cb_floats(a.head_dim, a.n_centroids) * 4 + 16 * (size_t)a.head_dim * 4;
-    size_t m = main > merge ? main : merge;
-    return m > qrows ? m : qrows;
-}
-
-// max / sum over the 16 lanes of a row (every lane of the row receives the result)
-__device__ __forceinline__ float row_max16(float v) {
-    v = fmaxf(v, dpp_ror<0x121>(v)); v = fmaxf(v, dpp_ror<0x122>(v));
-    v = fmaxf(v, dpp_ror<0x124>(v)); v = fmaxf(v, dpp_ror<0x128>(v));
-    return v;
-}
-__device__ __forceinline__ float row_sum16(float v) {
-    v += dpp_ror<0x121>(v); v += dpp_ror<0x122>(v);
-    v += dpp_ror<0x124>(v); v += dpp_ror<0x128>(v);
-    return v;
-}
-
-template <int KD, int BD, int DT, int VT, int PB>
-__global__ __launch_bounds__(kThreads) void k_decode_paged_mx(const MfmaParams p) {
-    constexpr int NB = KD / BD;
-    constexpr int NBW = NB / 4;  // code row dwords
-    constexpr int KS = KD / 4;   // score k-steps
-    extern __shared__ __align__(16) float smem[];
-    const ssq_decode_args& a = p.a;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int l16 = lane & 15, lg = lane >> 4;
-    const int bk = blockIdx.x;
-    const int split = blockIdx.y;
-    const int b = bk / a.num_kv_heads;
-    const int kv = bk - b * a.num_kv_heads;
-    const int nc = a.n_centroids;
-    const int row0 = blockIdx.z * p.rg;       // this workgroup's query rows: row0 .. row0 + nr - 1
-    const int nr = min(p.rg, p.rows - row0);  // <= 16
-    const int T = min(a.seq_lens[b], a.seq_len);
-    const int t_begin = split * p.split_len;
-    const int t_end = min(T, t_begin + p.split_len);
-
-    float* cb = smem;  // codebook [NB][nc][BD]
-    uint8_t* wall = reinterpret_cast<uint8_t*>(smem + mx_cb_floats(KD, nc));
-    uint8_t* ct = wall + wave * mx_wave_bytes(NB);                                   // [64][NB]
-    uint16_t* pstrip = reinterpret_cast<uint16_t*>(ct + kTileTok * NB);              // [16][64]
-    int* pages = reinterpret_cast<int*>(wall + kWaves * mx_wave_bytes(NB));
-
-    // ---- prologue: block-table slice, permutation entries, query rows, first two tiles, codebook
-    const int32_t* btab = a.block_table + (int64_t)b * a.bt_sb + t_begin / kPage;
-    const int n_pages = t_end > t_begin ? (t_end - t_begin + kPage - 1) / kPage : 0;
-    for (int i = tid; i < n_pages; i += kThreads) pages[i] = btab[i];
-    const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
-    int64_t pj[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) pj[s] = perm[4 * s + lg];
-    {
-        // query rows unpermuted and scaled into LDS [16][KD] (rows past nr are zero): lane j
-        // loads dims j and j + 64 of every row
-        constexpr int kHalf = KD / 64;
-        int64_t src[16 * kHalf];
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-#pragma unroll
-            for (int hh = 0; hh < kHalf; ++hh) {
-                src[r * kHalf + hh] = lane + 64 * hh;  // rows past nr read element 0..KD-1 of row 0
-                if (r < nr) {
-                    const int g = (row0 + r) / a.q_len, qi = row0 + r - g * a.q_len;
-                    const int h = kv * p.G + g;
-                    src[r * kHalf + hh] += (int64_t)b * a.q_sb + (int64_t)h * a.q_sh + (int64_t)qi * a.q_sl;
-                }
-            }
-        }
-        float qv[16 * kHalf];
-        ssq_load_elems(a.q, a.q_dtype, src, qv);
-        float* qs = reinterpret_cast<float*>(wall);  // [16][KD], free until the first tile's codes
-        if (wave == 0) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r)
-#pragma unroll
-                for (int hh = 0; hh < kHalf; ++hh)
-                    qs[r * KD + lane + 64 * hh] =
-                        r >= nr ? 0.f : a.has_scale ? ssq_round_to(qv[r * kHalf + hh] * a.scale, a.q_dtype) : qv[r * kHalf + hh];
-        }
-    }
-    __syncthreads();  // qs and pages written
-    float qa[KS];
-    {
-        const float* qrow = reinterpret_cast<const float*>(wall) + l16 * KD;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) qa[s] = qrow[min((uint64_t)pj[s], (uint64_t)(KD - 1))];
-    }
-    __syncthreads();  // every wave has its A operand: the per-wave regions are free
-
-    const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)kv * a.v_sh + (int64_t)(lane & 15) * a.v_st;
-    const uint8_t* cbase = PB > 0 ? reinterpret_cast<const uint8_t*>(reinterpret_cast<const uint32_t*>(a.codes) +
-                                                                     (int64_t)kv * a.c_sh)
-                                  : a.codes + (int64_t)kv * a.c_sh;
-    const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
-    const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
-    TileRegs<NB, DT, PB> RA, RB;
-    if (n_tiles > 0) {
-        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(wave, last_tile), lane, cbase, vbase, RA);
-        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(wave + kWaves, last_tile), lane, cbase, vbase, RB);
-    }
-    // the codebook goes global -> LDS directly: 1 KB chunks, lane l's 16 bytes at chunk + 16 l;
-    // the tail chunk's lanes past the end re-read the last float4 into the padding
-    {
-        const float* cent = a.cent + (int64_t)kv * a.cent_sh;
-        const int n4 = KD * nc / 4;
-        const int n_chunks = (n4 + 63) / 64;
-        for (int c = wave; c < n_chunks; c += kWaves) {
-            const int i = min(c * 64 + lane, n4 - 1);
-            __builtin_amdgcn_global_load_lds(cent + 4 * i, (__attribute__((address_space(3))) void*)(cb + 256 * c), 16,
-                                             0, 0);
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's codebook chunks have landed
-    __syncthreads();
-
-    // Codebook gather of step s: this lane supplies head dim j = 4s + lg, i.e. dim j % BD of block
-    // j / BD: byte offset lane_off + step_off(s) + code * BD * 4, code bits at lane_sh + step_sh(s).
-    constexpr int kLogBD = BD == 1 ? 0 : BD == 2 ? 1 : BD == 4 ? 2 : 3;
-    const uint8_t* cbb = reinterpret_cast<const uint8_t*>(cb);
-    const uint32_t ncm1 = (uint32_t)(nc - 1);
-    const uint32_t lane_off = BD <= 4 ? (uint32_t)(((lg >> kLogBD) * nc * BD) + (lg & (BD - 1))) * 4u : 4u * lg;
-    const uint32_t lane_sh = BD == 1 ? 8u * lg : BD == 2 ? 8u * (lg >> 1) : 0u;
-    float m_run[4], l_run[4];
-    v4f acc[DT];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { m_run[i] = -INFINITY; l_run[i] = 0.f; }
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
-
-    auto step = [&](TileRegs<NB, DT, PB>& R, int tile) {
-        const int t0 = t_begin + tile * kTileTok;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if constexpr (PB > 0) {  // unpack to one byte per code: the score loop reads byte rows either way
-            constexpr int kVpe = 32 / PB;
-            constexpr uint32_t kMsk = (1u << PB) - 1u;
-            uint32_t u[NB / 4];
-#pragma unroll
-            for (int j = 0; j < NB / 4; ++j) u[j] = 0u;
-#pragma unroll
-            for (int i = 0; i < NB; ++i) u[i >> 2] |= ((R.pk[i / kVpe] >> ((i % kVpe) * PB)) & kMsk) << (8 * (i & 3));
-            if constexpr (NB >= 16) {
-#pragma unroll
-                for (int i = 0; i < NB / 16; ++i)
-                    *reinterpret_cast<uint4*>(ct + lane * NB + 16 * i) =
-                        make_uint4(u[4 * i], u[4 * i + 1], u[4 * i + 2], u[4 * i + 3]);
-            } else {
-                *reinterpret_cast<uint2*>(ct + lane * NB) = make_uint2(u[0], u[1]);
-            }
-        } else if constexpr (NB >= 16) {
-#pragma unroll
-            for (int i = 0; i < NB / 16; ++i) *reinterpret_cast<uint4*>(ct + lane * NB + 16 * i) = R.c[i];
-        } else {
-            *reinterpret_cast<uint2*>(ct + lane * NB) = R.c8;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        // ---- scores: S[row 4 lg + i][token 16 g + l16] for the tile's 4 groups of 16 tokens
-        // (group by group: the next group's gathers overlap the current group's MFMA chain)
-        v4f sc[4];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            uint32_t cw[NBW];
-            const uint8_t* crow = ct + (16 * g + l16) * NB;
-            if constexpr (NB >= 16) {
-#pragma unroll
-                for (int i = 0; i < NB / 16; ++i) {
-                    const uint4 w = *reinterpret_cast<const uint4*>(crow + 16 * i);
-                    cw[4 * i] = w.x; cw[4 * i + 1] = w.y; cw[4 * i + 2] = w.z; cw[4 * i + 3] = w.w;
-                }
-            } else {
-                const uint2 w = *reinterpret_cast<const uint2*>(crow);
-                cw[0] = w.x; cw[1] = w.y;
-            }
-            v4f c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < KS; ++s) {
-                const uint32_t word = cw[((4 * s) / BD) >> 2];
-                const uint32_t step_sh = BD == 1 ? 0u : BD == 2 ? 16u * (s & 1) : BD == 4 ? 8u * (s & 3) : 8u * ((s >> 1) & 3);
-                const uint32_t step_off = BD <= 4 ? (uint32_t)s * 16u * (uint32_t)nc
-                                                  : (uint32_t)(s >> 1) * 32u * (uint32_t)nc + 16u * (s & 1);
-                const uint32_t code = min(__builtin_amdgcn_ubfe(word, lane_sh + step_sh, 8), ncm1);
-                const float kval = *reinterpret_cast<const float*>(cbb + lane_off + step_off + (code << (2 + kLogBD)));
-                c = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kval, c, 0, 0, 0);
-            }
-            sc[g] = c;
-        }
-        if (a.scores) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int t = t0 + 16 * g + l16;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = 4 * lg + i;
-                    if (r < nr && t < t_end) {
-                        const int gq = (row0 + r) / a.q_len, qi = row0 + r - gq * a.q_len;
-                        const int h = kv * p.G + gq;
-                        a.scores[(int64_t)b * a.s_sb + (int64_t)h * a.s_sh + (int64_t)qi * a.s_sl + t] = sc[g][i];
-                    }
-                }
-            }
-        }
-
-        // ---- online softmax (rows 4 lg + i live in this lane's row of 16 lanes)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-                if (t0 + 16 * g + l16 < t_end) mx = fmaxf(mx, sc[g][i]);
-            mx = row_max16(mx);
-            const float mn = fmaxf(m_run[i], mx);
-            const float alpha = (mn == -INFINITY) ? 1.f : __expf(m_run[i] - mn);
-            m_run[i] = mn;
-            float lsum = 0.f;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const bool valid = t0 + 16 * g + l16 < t_end;
-                const float pr = (valid && mn != -INFINITY) ? __expf(sc[g][i] - mn) : 0.f;
-                lsum += pr;
-                pstrip[(4 * lg + i) * kTileTok + 16 * g + l16] = (uint16_t)to_vt16<VT>(pr);
-            }
-            l_run[i] = l_run[i] * alpha + lsum;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) acc[dt][i] *= alpha;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-        // ---- P.V: A = P [16 rows x 32 tokens] from the strip, B = V fragments from the page
-        const int kchunk = 8 * (lane >> 4);
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            const int tk = t0 + 32 * g + kchunk;
-            const uint4 af = *reinterpret_cast<const uint4*>(pstrip + l16 * kTileTok + 32 * g + kchunk);
-            if (tk + 8 > t_end) {  // tail: values of slots past the end are unwritten; zero them
-                const int keep = t_end - tk;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    uint32_t w[4] = {R.v[g][dt].x, R.v[g][dt].y, R.v[g][dt].z, R.v[g][dt].w};
-#pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        if (j >= keep) w[j >> 1] &= (j & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-                    R.v[g][dt] = make_uint4(w[0], w[1], w[2], w[3]);
-                }
-            }
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma<VT>(af, R.v[g][dt], acc[dt]);
-        }
-        // this set is consumed: load the tile two rounds ahead into it
-        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + 2 * kWaves, last_tile), lane, cbase, vbase, R);
-    };
-    // two steps per trip and a single exit (a break between the steps would let the loop-head
-    // waits drain both register sets); a step past the last tile sees only tokens past the end
-    for (int tile = wave; tile < n_tiles; tile += 2 * kWaves) {
-        step(RA, tile);
-        step(RB, tile + kWaves);
-    }
-
-    // ---- merge the waves' (m, l, O) through LDS (the codebook is no longer needed)
-    float l_w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) l_w[i] = row_sum16(l_run[i]);
-    __syncthreads();
-    constexpr int Dv = DT * 16;
-    float* mbuf = smem;                // [waves][16]
-    float* lbuf = mbuf + kWaves * 16;  // [waves][16]
-    float* obuf = lbuf + kWaves * 16;  // [waves][16][Dv]
-    if (l16 == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { mbuf[wave * 16 + 4 * lg + i] = m_run[i]; lbuf[wave * 16 + 4 * lg + i] = l_w[i]; }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) obuf[((size_t)wave * 16 + 4 * lg + i) * Dv + 16 * dt + l16] = acc[dt][i];
-    __syncthreads();
-    const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
-    for (int e = tid; e < nr * Dv; e += kThreads) {
-        const int r = e / Dv, dv = e - r * Dv;
-        float M = -INFINITY;
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, mbuf[w * 16 + r]);
-        float L = 0.f, o = 0.f;
-        for (int w = 0; w < kWaves; ++w) {
-            const float mw = mbuf[w * 16 + r];
-            if (mw == -INFINITY) continue;
-            const float f = __expf(mw - M);
-            L += lbuf[w * 16 + r] * f;
-            o += obuf[((size_t)w * 16 + r) * Dv + dv] * f;
-        }
-        const int g = (row0 + r) / a.q_len, qi = row0 + r - g * a.q_len;
-        const int h = kv * p.G + g;
-        const int rid = (b * a.num_q_heads + h) * a.q_len + qi;
-        if (p.n_splits == 1) {
-            ssq_store_elem(a.out, a.v_dtype, (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)qi * a.o_sl + dv, o / L);
-            if (a.lse && dv == 0) a.lse[rid] = M + logf(L);
-        } else {
-            p.ws_o[((size_t)split * n_rows_all + rid) * Dv + dv] = o;
-            if (dv == 0) {
-                p.ws_m[(size_t)split * n_rows_all + rid] = M;
-                p.ws_l[(size_t)split * n_rows_all + rid] = L;
-            }
-        }
-    }
-}
-
 int pow2_at_least(int x) {
     int q = 1;
     while (q < x) q <<= 1;
@@ -726,15 +389,6 @@ struct MPlan {
     size_t smem, ws_bytes;
 };
 
-// the MFMA-scores kernel's shapes: head_dim 64 or 128, block_dim 1/2/4/8 with at most 64 blocks
-bool mx_shape(const ssq_decode_args* a) {
-    if (a->head_dim != 64 && a->head_dim != 128) return false;
-    const int bd = a->block_dim;
-    if (bd != 1 && bd != 2 && bd != 4 && bd != 8) return false;
-    if (a->head_dim / bd > 64) return false;
-    return a->value_dim == 64 || a->value_dim == 128;
-}
-
 // the 64-codeword LUT kernel's instantiations
 bool lut64_shape(const ssq_decode_args& a, int RP, int DT) {
     return a.v_dtype == SSQ_BF16 && (DT == 4 || DT == 8) && (RP == 2 || RP == 4 || RP == 8) &&
@@ -745,7 +399,7 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     if (a->layout != SSQ_PAGED || a->page_size != kPage) return false;
     // Codes: bytes, 8-bit words (the byte rows, strides scaled to bytes), or 4- / 6-bit words.
     // The LUT kernel serves 256-codeword codebooks with byte codes, and 64-codeword codebooks
-    // with byte or 6-bit codes (bf16 V, 2-8 rows, 16-64 blocks: lut64_shape); the MFMA-scores
+    // with byte or 6-bit codes (bf16 V, 2-8 rows, 16-64 blocks: lut64_shape); the 4x4-MFMA-scores
     // kernel serves the rest of its shapes.  Other widths take the generic kernel.
     const int cbits = a->code_bits;
     if (cbits != 0 && cbits != 4 && cbits != 6 && cbits != 8) return false;
@@ -813,40 +467,6 @@ bool plan(const ssq_decode_args* a, MPlan& pl) {
     const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
     pl.ws_bytes = pl.n_splits > 1 ? (size_t)pl.n_splits * n_rows_all * (a->value_dim + 2) * 4 : 0;
     return true;
-}
-
-template <int KD, int BD, int DT, int VT, int PB>
-int launch_mx(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
-    auto kern = k_decode_paged_mx<KD, BD, DT, VT, PB>;
-    int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_paged_mx)");
-    if (rc) return rc;
-    dim3 grid(mp.a.batch * mp.a.num_kv_heads, pl.n_splits, pl.n_groups);
-    hipLaunchKernelGGL(kern, grid, dim3(kThreads), pl.smem, st, mp);
-    return ssq_check_hip(hipGetLastError(), "k_decode_paged_mx launch");
-}
-template <int KD, int DT, int VT, int PB>
-int launch_mx_bd(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
-    switch (mp.a.block_dim) {
-        case 1: if constexpr (KD <= 64) return launch_mx<KD, 1, DT, VT, PB>(mp, pl, st); break;
-        case 2: return launch_mx<KD, 2, DT, VT, PB>(mp, pl, st);
-        case 4: return launch_mx<KD, 4, DT, VT, PB>(mp, pl, st);
-        default: return launch_mx<KD, 8, DT, VT, PB>(mp, pl, st);
-    }
-    return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA-scores decode: more than 64 blocks");
-}
-template <int KD, int DT, int VT>
-int launch_mx_pb(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
-    switch (mp.a.code_bits) {
-        case 4: return launch_mx_bd<KD, DT, VT, 4>(mp, pl, st);
-        case 6: return launch_mx_bd<KD, DT, VT, 6>(mp, pl, st);
-        default: return launch_mx_bd<KD, DT, VT, 0>(mp, pl, st);
-    }
-}
-template <int VT>
-int launch_mx_vt(const MfmaParams& mp, const MPlan& pl, hipStream_t st) {
-    if (mp.a.head_dim == 64)
-        return pl.DT == 4 ? launch_mx_pb<64, 4, VT>(mp, pl, st) : launch_mx_pb<64, 8, VT>(mp, pl, st);
-    return pl.DT == 4 ? launch_mx_pb<128, 4, VT>(mp, pl, st) : launch_mx_pb<128, 8, VT>(mp, pl, st);
 }
 
 template <int RP, int DT, int VT, int NB, int NC = kNC, int PB = 0>

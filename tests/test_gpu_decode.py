@@ -160,8 +160,8 @@ def test_config4_paged_small_vs_oracle(kernel):
                                         (32, 2, 2, 128), (128, 4, 2, 128), (64, 2, 1, 64), (64, 8, 1, 256)])
 def test_paged_mfma_row_groups_vs_oracle(Hq, bd, lq, D):
     """More query rows per KV head than one LUT holds (8 or 16 heads at 32 blocks, 64 blocks of
-    dim 2 at head_dim 128, two query tokens): head_dim 64 and 128 take the MFMA-scores kernel (16
-    rows per pass, row groups beyond), head_dim 256 the LUT kernel in row groups.  Outputs, lse
+    dim 2 at head_dim 128, two query tokens): head_dim 64 and 128 take the 4x4-MFMA-scores kernel
+    (16 rows per pass, row groups beyond), head_dim 256 the LUT kernel in row groups.  Outputs, lse
     and raw scores against the oracle, per (sequence, KV head)."""
     log(f"paged MFMA row groups Hq={Hq} bd={bd} q_len={lq} D={D}")
     p = synthetic.config4(DEV, B=2, T=1024 if D <= 128 else 256, Hq=Hq, bd=bd, D=D)

@@ -143,8 +143,8 @@ def _pages(codes, v, seed):
 def test_paged_mfma_decode_over_packed_codes(bits, bd, nc, Hq, D, T):
     """Paged decode of 4- / 6-bit packed codes and of codebooks under 256 codewords: 64-codeword
     codebooks with 2-8 rows run the LUT kernel (a 64-entry table per block, codes unpacked from
-    the words in registers), the others the MFMA-scores kernel (words unpacked as the tile goes to
-    LDS).  Equal to the same kernel's uint8-code launch bit for bit (8-bit words are read as the
+    the words in registers), the others the 4x4-MFMA-scores kernel (codes taken from the words in
+    registers).  Equal to the same kernel's uint8-code launch bit for bit (8-bit words are read as the
     byte rows), and to the oracle."""
     log(f"packed paged decode bits={bits} bd={bd} nc={nc} Hq={Hq} D={D} T={T}")
     cb, codes, q, v = _case(nc=nc, bd=bd, D=D, Hq=Hq, T=T, seed=60 + bits + bd)
