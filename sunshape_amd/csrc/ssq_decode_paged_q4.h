@@ -174,6 +174,9 @@ __device__ __forceinline__ void tile_scores_q4(const float* cb, int nc, const Ti
         constexpr int bi = decltype(bc)::value;
         constexpr int b0 = bi * KB;
         if constexpr (bi + 1 < NBATCH) gather_batch<KB, NB, BD, DT, PB>(cb, nc, ncm1, R, b0 + KB, ev[(bi + 1) & 1]);
+        // keep the next batch's gathers ahead of this batch's MFMAs (the scheduler would otherwise
+        // sink each gather to its first use and wait on every one)
+        __builtin_amdgcn_sched_barrier(0);
         static_for<0, KB * BD>([&](auto ic) {
             constexpr int i = decltype(ic)::value;
             constexpr int k = i / BD, d = i % BD;
@@ -187,6 +190,7 @@ __device__ __forceinline__ void tile_scores_q4(const float* cb, int nc, const Ti
                     c0[q] = __builtin_amdgcn_mfma_f32_4x4x1f32(qa[q][kd >> 4], e, c0[q], 4, kd & 15, 0);
             }
         });
+        __builtin_amdgcn_sched_barrier(0);
     });
 #pragma unroll
     for (int q = 0; q < R4; ++q)
@@ -197,8 +201,12 @@ __device__ __forceinline__ void tile_scores_q4(const float* cb, int nc, const Ti
 // W waves per workgroup: 4 (one per SIMD) keep two tiles in flight per wave in two register sets;
 // 8 (two per SIMD, so one wave's matrix-core phase overlaps the other's VALU and LDS phases) keep
 // one set, reloading a tile's codes once its scores are done and its values once its P.V is done.
+// The LDS (codebook) limits a CU to one workgroup, i.e. W / 4 waves per SIMD: telling the compiler
+// so lets it spend registers on loads in flight instead of trimming them for an occupancy the LDS
+// never allows.
 template <int KD, int BD, int R4, int DT, int VT, int PB, int W>
-__global__ __launch_bounds__(W * SSQ_WAVE) void k_decode_paged_q4(const MfmaParams p) {
+__global__ __launch_bounds__(W * SSQ_WAVE) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4)))
+void k_decode_paged_q4(const MfmaParams p) {
     constexpr int kThreads = W * SSQ_WAVE;
     constexpr int kWaves = W;
     constexpr int NB = KD / BD;
