@@ -48,9 +48,7 @@ def test_config3_decode_vs_oracle(B, T):
     out, lse, scores = np_of(out), np_of(lse), np_of(scores)
     q, codes, v, perm, cent = (np_of(p[k]) for k in ("q", "codes", "v", "perm", "centroids"))
     G = 7
-    units = [(b, kv) for b in range(B) for kv in range(2)]
-    if B > 4:
-        units = units[:3] + units[-3:]
+    units = [(b, kv) for b in range(B) for kv in range(2)]  # every unit, also at full size
     for b, kv in units:
         ro, rs, rl = _oracle_unit(q[b, kv * G:(kv + 1) * G], codes[b, kv], v[b, kv], cent[kv], perm[kv], p.meta["scale"])
         sl = slice(kv * G, (kv + 1) * G)
@@ -193,20 +191,52 @@ def test_paged_ragged_sequence_lengths():
                         seq_lens=np_of(lens))
 
 
-def test_config4_full_size_sampled_units():
+def _paged_units_vs_oracle(p, out, lse, scores, units):
+    """Oracle check of paged-decode units, gathering each sequence's pages once for all its KV heads."""
+    bt = np_of(p["block_table"])
+    cp, vp = p["code_pages"], p["v_pages"]
+    G = p.meta["Hq"] // p.meta["Hkv"]
+    q, perm, cent = np_of(p["q"]), np_of(p["perm"]), np_of(p["centroids"])
+    T = p.meta["T"]
+    by_b = {}
+    for b, kv in units:
+        by_b.setdefault(b, []).append(kv)
+    for b, kvs in sorted(by_b.items()):
+        pages = torch.from_numpy(bt[b].astype(np.int64)).to(DEV)
+        codes = np_of(cp[pages].transpose(0, 1).reshape(cp.shape[1], -1, cp.shape[3]))      # [Hkv, T, nb]
+        vals = np_of(vp[pages].permute(1, 0, 3, 2).reshape(vp.shape[1], -1, vp.shape[2]))   # [Hkv, T, Dv]
+        for kv in kvs:
+            ro, rs, rl = _oracle_unit(q[b, kv * G:(kv + 1) * G], codes[kv, :T], vals[kv, :T], cent[kv], perm[kv],
+                                      p.meta["scale"])
+            sl = slice(kv * G, (kv + 1) * G)
+            assert_rel(out[b, sl], ro, BF16_TOL, f"c4 out b={b} kv={kv}")
+            assert_rel(lse[b, sl], rl, SCORE_TOL, f"c4 lse b={b} kv={kv}")
+            if scores is not None:
+                assert_rel(scores[b, sl], rs, SCORE_TOL, f"c4 scores b={b} kv={kv}")
+
+
+def test_config4_full_size_units():
+    """Config 4 at full size (64 x 8 x 32768, paged): every one of the 512 (batch, KV head) units'
+    output and lse against the oracle, then the launch that also returns the fp32 scores (config 4
+    lists them as an output), with 128 units' scores, outputs and lse against the oracle."""
     log("config4 full size")
     p = synthetic.config4(DEV)
-    out, lse = hip_ops.decode(p["q"], p["code_pages"], p["v_pages"], p["perm"], p["centroids"], scale=p.meta["scale"],
-                              block_table=p["block_table"], seq_lens=p["seq_lens"], return_lse=True)
+    kw = dict(scale=p.meta["scale"], block_table=p["block_table"], seq_lens=p["seq_lens"], return_lse=True)
+    out, lse = hip_ops.decode(p["q"], p["code_pages"], p["v_pages"], p["perm"], p["centroids"], **kw)
     torch.cuda.synchronize()
     o, l = np_of(out), np_of(lse)
     assert np.isfinite(o).all() and np.isfinite(l).all()
     # softmax over 32768 N(0,1)-valued keys: lse >= max score >= log-uniform floor
     assert (l > math.log(32768) - 5).all()
     rng = np.random.default_rng(0)
-    units = [(int(rng.integers(64)), int(rng.integers(8))) for _ in range(6)] + [(0, 0), (63, 7)]
-    _paged_oracle_check(p, o, l, None, units)
-
+    _paged_units_vs_oracle(p, o, l, None, [(b, kv) for b in range(64) for kv in range(8)])
+    log("config4 full size with scores")
+    out2, lse2, sc2 = hip_ops.decode(p["q"], p["code_pages"], p["v_pages"], p["perm"], p["centroids"],
+                                     return_scores=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out2, out) and torch.equal(lse2, lse)  # asking for scores changes nothing else
+    units = sorted({(int(rng.integers(64)), int(rng.integers(8))) for _ in range(200)} | {(0, 0), (63, 7)})[:128]
+    _paged_units_vs_oracle(p, o, l, np_of(sc2), units)
 
 def test_config4_layer_3bit_packed_full_size():
     """The config-4 layer at 3 bits/dim (64 codewords, bd 2) at full size: 6-bit words and byte
@@ -226,9 +256,16 @@ def test_config4_layer_3bit_packed_full_size():
     _paged_oracle_check(p, np_of(out6), np_of(lse6), None, units)
 
 
-def test_mixed_passthrough_decode_config5_shape():
-    log("mixed passthrough decode")
-    p = synthetic.config5(DEV, B=2, S=1200)
+@pytest.mark.parametrize("B,S", [(2, 1200), (16, 16384)])
+def test_mixed_passthrough_decode_config5_shape(B, S):
+    """SunShape-Mixed: encode the config-5 keys (28 VQ blocks + 4 bf16 passthrough), then decode
+    over the mixed cache; every (batch, KV head) unit's outputs and scores against the oracle, at a
+    small size and at config 5's full 16 x 2 x 16384.  Codes: every row against the oracle at the
+    small size; at full size 2000 sampled rows per unit (test_config5_full_encode checks every row
+    of the same keys across the three encode kernels), and the oracle decodes the cache the GPU
+    wrote (dense passthrough rebuilt from the compact one)."""
+    log(f"mixed passthrough decode B={B} S={S}")
+    p = synthetic.config5(DEV, B=B, S=S)
     heavy = p["heavy"].tolist()
     keys = p["keys"]
     codes, pt = hip_ops.encode(keys, p["perm"], p["centroids"], heavy=heavy)  # compact bf16 passthrough
@@ -237,10 +274,21 @@ def test_mixed_passthrough_decode_config5_shape():
     qn, vn, kn = np_of(p["q"]), np_of(p["v"]), np_of(keys)
     perm, cent, hv = np_of(p["perm"]), np_of(p["centroids"]), np.array(heavy)
     o, s = np_of(out), np_of(scores)
-    for b in range(2):
+    cn, ptn = np_of(codes), np_of(pt)
+    rng = np.random.default_rng(5)
+    for b in range(B):
         for kv in range(2):
-            rc, rpt = O.encode(kn[b, kv], perm, cent[kv], hv)
-            assert np.array_equal(np_of(codes[b, kv]), rc)
+            if S <= 4096:
+                rc, rpt = O.encode(kn[b, kv], perm, cent[kv], hv)
+                assert np.array_equal(cn[b, kv], rc)
+            else:
+                rows = rng.choice(S, 2000, replace=False)
+                rc_s, rpt_s = O.encode(kn[b, kv, rows], perm, cent[kv], hv)
+                assert np.array_equal(cn[b, kv, rows], rc_s)
+                assert np.array_equal(ptn[b, kv, rows], rpt_s[:, hv])
+                rc = cn[b, kv]
+                rpt = np.zeros((S, len(heavy), 2), np.float32)
+                rpt[:, hv] = ptn[b, kv]
             ro, rs, _ = _oracle_unit(qn[b, kv * 7:(kv + 1) * 7], rc, vn[b, kv], cent[kv], perm, p.meta["scale"],
                                      heavy=hv, pt=rpt)
             assert_rel(o[b, kv * 7:(kv + 1) * 7], ro, BF16_TOL, f"mixed out b={b} kv={kv}")

@@ -427,3 +427,27 @@ def test_grid_encode_rejections():
     small = torch.zeros(16, dtype=torch.uint8, device=DEV)
     with pytest.raises(RuntimeError, match="too small"):
         hip_ops.encode(k, torch.from_numpy(perm).to(DEV), torch.from_numpy(cent2).to(DEV), kernel=3, grid=small)
+
+
+def test_grid_encode_where_rounding_slack_decides():
+    """Codebooks clustered far from the origin, keys near codeword midpoints: the reference's fp32
+    mm rounding decides many winners, and many are listed only because of the grid's rounding
+    slack M_C (tests/test_grid_search.py).  The grid encode still equals the oracle bit for bit."""
+    log("grid encode, rounding slack decides")
+    from test_grid_search import far_cluster_case
+
+    cents, xs = [], []
+    for seed in (0, 3, 12, 21):
+        c, x, _, _ = far_cluster_case(seed, n=20000)
+        cents.append(c)
+        xs.append(x)
+    cent = np.stack(cents)                       # [4 blocks, 8 codewords, 2]
+    keys = np.concatenate(xs, axis=1)            # [n, 8]: block b's coordinates in dims 2b, 2b + 1
+    perm = np.arange(8)
+    ref, _ = O.encode(keys, perm, cent)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    grid = hip_ops.encode_grid(t(cent))
+    got, _ = hip_ops.encode(t(keys)[None, None], t(perm), t(cent), kernel=3, grid=grid)
+    assert np.array_equal(np_of(got[0, 0]), ref), int((np_of(got[0, 0]) != ref).sum())
+    scan, _ = hip_ops.encode(t(keys)[None, None], t(perm), t(cent), kernel=1)
+    assert np.array_equal(np_of(scan[0, 0]), ref)

@@ -124,3 +124,56 @@ def test_cell_lists_hold_the_oracle_winner(seed, nc):
     assert used.mean() > 0.9
     held = member[f0, f1, win]
     assert held[used].all(), np.flatnonzero(used & ~held)[:10]
+
+
+def _lists_without_slack(c, mid, inv):
+    """cell_lists with M_C = 0: dmin(C, c_j)^2 <= min_k dmax(C, c_k)^2 only."""
+    a0, b0 = widened(np.arange(KG), mid[0], inv[0])
+    a1, b1 = widened(np.arange(KG), mid[1], inv[1])
+    A0, B0 = a0[:, None, None], b0[:, None, None]
+    A1, B1 = a1[None, :, None], b1[None, :, None]
+    cx, cy = c[None, None, :, 0].astype(np.float64), c[None, None, :, 1].astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        dx = np.maximum(np.abs(A0 - cx), np.abs(B0 - cx))
+        dy = np.maximum(np.abs(A1 - cy), np.abs(B1 - cy))
+        dmm = np.min(dx * dx + dy * dy, axis=2)
+        ex = np.maximum(np.maximum(A0 - cx, cx - B0), 0)
+        ey = np.maximum(np.maximum(A1 - cy, cy - B1), 0)
+        member = (ex * ex + ey * ey) <= dmm[..., None]
+    member |= ~np.isfinite(dmm)[..., None]
+    return member
+
+
+def far_cluster_case(seed, n=20000):
+    """A small codebook clustered far from the origin (|c| ~ 1e2-1e3, spread ~0.01-1) and keys near
+    the midpoints of codeword pairs: the reference's mm formulation cancels |x|^2 against 2 x.c,
+    so its fp32 rounding, not the exact distance, decides many of these keys."""
+    rng = np.random.default_rng(seed)
+    nc = 8
+    base = np.float32(rng.uniform(200, 3000))
+    c = (base + rng.standard_normal((nc, 2)) * np.float32(rng.uniform(0.01, 1))).astype(np.float32)
+    i, j = rng.integers(0, nc, n), rng.integers(0, nc, n)
+    x = (0.5 * (c[i].astype(np.float64) + c[j]) + rng.standard_normal((n, 2)) * 1e-4).astype(np.float32)
+    lo, hi = c.min(0).astype(np.float64), c.max(0).astype(np.float64)
+    mid = (0.5 * (lo + hi)).astype(np.float32)
+    inv = (1.0 / c.astype(np.float64).std(0)).astype(np.float32)
+    return c, x, mid, inv
+
+
+@pytest.mark.parametrize("seed", [0, 3, 12])
+def test_rounding_slack_decides_lists_and_they_hold_the_winner(seed):
+    """Inputs where the slack M_C matters: on a far-from-origin cluster it adds codewords to many
+    lists, and for many keys the reference's fp32 winner is in the list only because of it.  With
+    it every used list holds the winner; without it some would not."""
+    c, x, mid, inv = far_cluster_case(seed)
+    cnt, member = cell_lists(c, mid, inv)
+    bare = _lists_without_slack(c, mid, inv)
+    assert (member != bare).any()
+    win = O.encode(x, np.arange(2), c[None])[0][:, 0].astype(np.int64)
+    f0, f1 = kernel_cell(x[:, 0], mid[0], inv[0]), kernel_cell(x[:, 1], mid[1], inv[1])
+    used = (cnt[f0, f1] >= 1) & (cnt[f0, f1] <= 31)
+    assert used.mean() > 0.5
+    held = member[f0, f1, win]
+    assert held[used].all(), np.flatnonzero(used & ~held)[:10]
+    only_with_slack = used & held & ~bare[f0, f1, win]
+    assert only_with_slack.sum() > 100, int(only_with_slack.sum())
