@@ -120,7 +120,9 @@ class EncodeArgs(ctypes.Structure):
 
 
 _lib = None
+_ops = None
 _lock = threading.Lock()
+TORCH_OPS_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libsunshape_torch_ops.so")
 
 
 def _declare(lib: ctypes.CDLL) -> None:
@@ -173,6 +175,54 @@ def lib() -> ctypes.CDLL:
                 raise RuntimeError("sunshape_amd library ABI version mismatch")
             _lib = handle
     return _lib
+
+
+def torch_ops():
+    """torch.ops.sunshape (operators of libsunshape_torch_ops.so, over the same library); raises if
+    it was not built."""
+    global _ops
+    if _ops is not None:
+        return _ops
+    lib()
+    with _lock:
+        if _ops is None:
+            if not os.path.exists(TORCH_OPS_PATH):
+                raise RuntimeError(
+                    f"sunshape_amd torch operators are not built ({TORCH_OPS_PATH}); run `python -m sunshape_amd.build`"
+                )
+            torch.ops.load_library(TORCH_OPS_PATH)
+            _ops = torch.ops.sunshape
+    return _ops
+
+
+_STATUS_RE = None
+
+
+def kernel_error(e: RuntimeError) -> RuntimeError:
+    """A torch operator's RuntimeError as SunShapeKernelError when the library returned a status."""
+    global _STATUS_RE
+    if _STATUS_RE is None:
+        import re
+
+        _STATUS_RE = re.compile(r"sunshape_amd status (\d+): ([^\n]*)")
+    m = _STATUS_RE.search(str(e))
+    if m is None:
+        return e
+    return SunShapeKernelError(int(m.group(1)), m.group(2))
+
+
+def mask_words_signed(mask) -> tuple[int, int]:
+    """heavy_mask_words as two signed int64 (the operators' int arguments), cached per mask tuple."""
+    key = None if mask is None else tuple(bool(x) for x in (mask.tolist() if hasattr(mask, "tolist") else mask))
+    hit = _WORDS.get(key)
+    if hit is None:
+        w0, w1 = heavy_mask_words(key)
+        hit = tuple(w - (1 << 64) if w >= (1 << 63) else w for w in (w0, w1))
+        _WORDS[key] = hit
+    return hit
+
+
+_WORDS: dict = {}
 
 
 class SunShapeKernelError(RuntimeError):

@@ -1,8 +1,9 @@
-"""Builds the sunshape_amd HIP library (gfx950) in-tree with hipcc.
+"""Builds the sunshape_amd HIP library (gfx950) and its torch operators in-tree.
 
 ``python -m sunshape_amd.build`` or ``sunshape_amd.build.build()`` compiles every
-``csrc/*.hip`` source into ``sunshape_amd/_lib/libsunshape_amd.so``.  Each source is
-compiled to an object in ``sunshape_amd/_lib/obj`` (in parallel), then linked.
+``csrc/*.hip`` source into ``sunshape_amd/_lib/libsunshape_amd.so`` (each source to an object in
+``sunshape_amd/_lib/obj``, in parallel, then linked) and ``csrc/torch_ops.cpp`` into
+``sunshape_amd/_lib/libsunshape_torch_ops.so`` (torch.ops.sunshape.*).
 """
 
 from __future__ import annotations
@@ -17,6 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_lib")
 LIB_PATH = os.path.join(OUT_DIR, "libsunshape_amd.so")
+TORCH_OPS_PATH = os.path.join(OUT_DIR, "libsunshape_torch_ops.so")
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 in generated code.
@@ -43,6 +45,26 @@ def _hipcc() -> str:
 
 def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def _build_torch_ops() -> None:
+    """torch.ops.sunshape.* (csrc/torch_ops.cpp): host C++ against torch's headers, linked to the
+    HIP library (found next to it through $ORIGIN) and to torch's libraries."""
+    import torch.utils.cpp_extension as ext
+
+    import torch
+
+    src = os.path.join(CSRC, "torch_ops.cpp")
+    tlib = ext.library_paths()[0]
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           *[f"-I{p}" for p in ext.include_paths()], "-I/opt/rocm/include", src,
+           "-o", TORCH_OPS_PATH + ".tmp", f"-L{OUT_DIR}", "-lsunshape_amd", f"-L{tlib}", "-lc10", "-lc10_hip",
+           "-ltorch_cpu", "-ltorch", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tlib}"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch operators failed to build:\n{res.stderr}")
+    os.replace(TORCH_OPS_PATH + ".tmp", TORCH_OPS_PATH)
 
 
 def _compile(hipcc: str, src: str, obj: str) -> None:
@@ -101,8 +123,13 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
+    if not incremental or not os.path.exists(TORCH_OPS_PATH) or \
+            os.path.getmtime(TORCH_OPS_PATH) < max(os.path.getmtime(os.path.join(CSRC, "torch_ops.cpp")),
+                                                   os.path.getmtime(os.path.join(os.path.dirname(HERE), "include",
+                                                                                 "sunshape_amd.h"))):
+        _build_torch_ops()
     if verbose:
-        print(f"built {LIB_PATH}")
+        print(f"built {LIB_PATH} and {TORCH_OPS_PATH}")
     return LIB_PATH
 
 

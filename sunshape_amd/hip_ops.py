@@ -292,96 +292,29 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
     """
     for name, t in (("query", q), ("codes", codes), ("value", v)):
         _on_gpu(name, t)
-    _require(q.ndim == 4, "Quantized attention expects query/value tensors with shape [batch, heads, seq, dim].")
     if rotation is not None:
+        _require(q.ndim == 4, "Quantized attention expects query/value tensors with shape [batch, heads, seq, dim].")
         q = transform_rows(q, rotation, scale=scale)
         scale = None
         perm = _identity_like(perm)
-    q = q if q.stride(-1) == 1 else q.contiguous()
-    _require(codes.stride(-1) == 1, "codes must be contiguous in the last dim")
-    B, Hq, Lq, D = q.shape
-    paged = block_table is not None
-    Hkv = codes.shape[1]
-    _require(Hq % Hkv == 0, "Query head count must be divisible by kv-head count.")
-    perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, Hkv)
-    _require(codes.ndim == 4, f"codes must be 4-D [.., {nb}]")
-    _check_codes(codes, nb, code_bits)
-    if paged:
-        _on_gpu("block_table", block_table)
-        _require(seq_lens is not None, "paged decode needs seq_lens")
-        _on_gpu("seq_lens", seq_lens)
-        _require(block_table.dtype == torch.int32 and seq_lens.dtype == torch.int32, "block_table/seq_lens must be int32")
-        _require(block_table.ndim == 2 and block_table.shape[0] == B and block_table.stride(1) == 1, "block_table [B, max_pages]")
-        page = codes.shape[2]
-        _require(v.ndim == 4 and v.shape[0] == codes.shape[0] and v.shape[1] == Hkv and v.shape[3] == page,
-                 "paged V must be [P, Hkv, Dv, page]")
-        _require(v.stride(-1) == 1, "paged V pages must be contiguous over tokens")
-        Dv = v.shape[2]
-        T = block_table.shape[1] * page
-        layout = N.SSQ_PAGED
-        v_strides = (v.stride(0), v.stride(1), v.stride(2))
-    else:
-        _require(codes.shape[0] == B, "Quantized key batch size does not match query batch size.")
-        _require(v.ndim == 4 and v.shape[0] == B, "Quantized key batch size does not match value batch size.")
-        _require(v.shape[1] == Hkv, "Quantized key kv-head count does not match value kv-head count.")
-        _require(v.shape[2] == codes.shape[2], "Quantized key sequence length does not match value sequence length.")
-        _require(v.stride(-1) == 1, "value must be contiguous in the last dim")
-        T = codes.shape[2]
-        Dv = v.shape[3]
-        page = 0
-        layout = N.SSQ_CONTIGUOUS
-        v_strides = (v.stride(0), v.stride(1), v.stride(2))
-    out = torch.empty((B, Hq, Lq, Dv), device=q.device, dtype=v.dtype)
-    lse = torch.empty((B, Hq, Lq), device=q.device, dtype=torch.float32) if return_lse else None
-    scores = None
-    if return_scores:  # paged: slots past a sequence's length are never scored and read -inf
-        scores = (torch.full((B, Hq, Lq, T), float("-inf"), device=q.device, dtype=torch.float32) if paged
-                  else torch.empty((B, Hq, Lq, T), device=q.device, dtype=torch.float32))
+    hm0, hm1 = N.mask_words_signed(heavy)
     if mask is not None:
         _on_gpu("attn_mask", mask)
-        mask = mask.to(torch.float32)
-        _require(mask.ndim == 4, "decode() takes a 4-D mask view broadcastable to [B, Hq, Lq, T]")
-        mask = mask.expand(B, Hq, Lq, T)
-    hm, pt, ptd, ptdt = _pt_args(heavy, pt, pt_dense)
-    if pt is not None:
-        pt_strides = (pt.stride(0), pt.stride(1), pt.stride(2))
-    else:
-        pt_strides = (0, 0, 0)
-    a = N.DecodeArgs(
-        q=N.ptr(q), q_dtype=N.dtype_code(q.dtype), q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
-        batch=B, num_q_heads=Hq, q_len=Lq, head_dim=D, num_kv_heads=Hkv,
-        has_scale=1 if scale is not None else 0, scale=float(scale or 0.0),
-        perm=N.ptr(perm), perm_sh=perm_sh, cent=N.ptr(cent), cent_sh=cent_sh,
-        block_dim=bd, n_blocks=nb, n_centroids=nc,
-        pt_dense=ptd, pt_dtype=ptdt, pt=N.ptr(pt), pt_sb=pt_strides[0], pt_sh=pt_strides[1], pt_st=pt_strides[2],
-        layout=layout, seq_len=T, codes=N.ptr(codes), c_sb=codes.stride(0), c_sh=codes.stride(1), c_st=codes.stride(2),
-        block_table=N.ptr(block_table), bt_sb=block_table.stride(0) if paged else 0,
-        seq_lens=N.ptr(seq_lens), page_size=page,
-        v=N.ptr(v), v_dtype=N.dtype_code(v.dtype), value_dim=Dv,
-        v_sb=v_strides[0], v_sh=v_strides[1], v_st=v_strides[2],
-        mask=N.ptr(mask),
-        m_sb=mask.stride(0) if mask is not None else 0, m_sh=mask.stride(1) if mask is not None else 0,
-        m_sl=mask.stride(2) if mask is not None else 0, m_st=mask.stride(3) if mask is not None else 0,
-        out=N.ptr(out), o_sb=out.stride(0), o_sh=out.stride(1), o_sl=out.stride(2),
-        lse=N.ptr(lse),
-        scores=N.ptr(scores), s_sb=scores.stride(0) if scores is not None else 0,
-        s_sh=scores.stride(1) if scores is not None else 0, s_sl=scores.stride(2) if scores is not None else 0,
-        num_splits=int(num_splits), kernel=int(kernel), code_bits=int(code_bits),
-    )
-    a.heavy_mask[0], a.heavy_mask[1] = hm
-    L = N.lib()
-    if no_alloc:
-        N.check(L.ssq_decode_noalloc(ctypes.byref(a), N.stream_of(q.device)))
-    else:
-        ws_bytes = L.ssq_decode_workspace_size(ctypes.byref(a))
-        ws = torch.empty((max(ws_bytes, 1),), device=q.device, dtype=torch.uint8) if ws_bytes else None
-        N.check(L.ssq_decode(ctypes.byref(a), N.ptr(ws), ws_bytes, N.stream_of(q.device)))
+    try:
+        out, lse, scores = N.torch_ops().decode(
+            q, codes, v, perm, cent, None if scale is None else float(scale), mask, hm0, hm1, pt, bool(pt_dense),
+            block_table, seq_lens, bool(return_lse), bool(return_scores), int(num_splits), int(kernel),
+            int(code_bits), bool(no_alloc))
+    except RuntimeError as e:
+        raise N.kernel_error(e) from None
+    if not (return_lse or return_scores):
+        return out
     res = [out]
     if return_lse:
         res.append(lse)
     if return_scores:
         res.append(scores)
-    return res[0] if len(res) == 1 else tuple(res)
+    return tuple(res)
 
 
 def encode_args(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
