@@ -177,7 +177,58 @@ def _decode_workload(name, dev, kernel):
     if code_bits:
         cfg["code_bits"] = code_bits
     unit_data = (p, paged)
+    step.surface = _surface_call(p, paged, q, codes, v, perm, cent, heavy, pt, code_bits, kernel, ref)
     return step, keys, algo_bytes, cfg, unit_data, "ssq_decode"
+
+
+def _surface_call(p, paged, q, codes, v, perm, cent, heavy, pt, code_bits, kernel, ref):
+    """(name, fn): the same decode through the Python drop-in surface.  Contiguous byte codes go
+    through SunShapeAttentionImpl.forward over a SunShapeQuantizedKeys payload (the reference's
+    vLLM decode call, sunshape/vllm_attn_backend.py:271-305); paged and packed codes, which that
+    payload does not carry, through hip_ops.decode."""
+    import torch
+
+    from sunshape_amd import hip_ops
+    from sunshape_amd import vllm_attn_backend as VB
+    from sunshape_amd.codec import SunShapeBlockCodec
+    from sunshape_amd.hf import SunShapeBundle
+    from sunshape_amd.integration.vllm import SunShapeVLLMRuntimeState
+
+    scale = p.meta["scale"]
+    if paged or code_bits:
+        kw = dict(block_table=p["block_table"], seq_lens=p["seq_lens"]) if paged else {}
+        return "hip_ops.decode", lambda: hip_ops.decode(q, codes, v, perm, cent, scale=scale, heavy=heavy, pt=pt,
+                                                        kernel=kernel, code_bits=code_bits, **kw)
+    mode = "profileperm_mixed_precision" if heavy is not None else "profileperm_baseline"
+    codec = SunShapeBlockCodec.from_buffers(perm, cent, mode=mode, device=q.device,
+                                            mixed_high_precision_blocks=None if heavy is None else torch.tensor(heavy))
+    bundle = SunShapeBundle("bench", [0], 0.0, codec.block_dim, mode, 0, 0, 0, {0: codec})
+    VB.register_runtime_state(SunShapeVLLMRuntimeState("bench", "bench", mode, 0.0, codec.block_dim, [0], bundle,
+                                                       "cuda"))
+    B, Hkv, T = codes.shape[0], codes.shape[1], codes.shape[2]
+    qk = VB.SunShapeQuantizedKeys(quantized_heads=(), batch_size=B, num_kv_heads=Hkv, seq_len=T, codes=codes,
+                                  passthrough=pt, passthrough_dense=False)
+    impl = VB.get_backend_factory().make_impl(layer_idx=0)
+    got = impl(q, qk, v, scale=scale)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref), "SunShapeAttentionImpl.forward differs from the checked launch"
+    return "SunShapeAttentionImpl.forward", lambda: impl(q, qk, v, scale=scale)
+
+
+def _time_surface(name, fn, n=100):
+    """Host time to issue one call and wall time per call (host and kernel overlapping), over n calls."""
+    import torch
+
+    for _ in range(5):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n):
+        fn()
+    host = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return {"api": name, "calls": n, "host_us_per_call": host / n * 1e6, "wall_us_per_call": wall / n * 1e6}
 
 
 def _scores_workload(dev):
@@ -516,6 +567,10 @@ def main():
                                 "algorithmic_flop_per_launch": flop}
     if args.workload != "copycal" and args.cold_steps > 0:
         line["cold"] = _cold_launches(step, args.cold_steps, algo_bytes, dev)
+    if getattr(step, "surface", None) is not None:
+        # the same decode through the Python drop-in, beside the prebuilt C-ABI replay timed above
+        line["python_surface"] = _time_surface(*step.surface)
+        line["python_surface"]["c_abi_kernel_avg_us"] = avg_ms * 1e3
     if not args.no_cpu and unit_data is not None:
         line["cpu_baseline"] = _cpu_baseline(unit_data, args.cpu_seconds)
     else:
