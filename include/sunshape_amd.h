@@ -187,11 +187,14 @@ int ssq_encode(const ssq_encode_args* a, void* stream);
  * Search grid for the encode (block_dim 2, no block metric; no counterpart in the reference: a
  * search structure of this library, built once per codebook and reused by every encode with
  * that codebook).  For each codebook (one, or one per KV head) and block, a 128 x 128 grid of
- * cells covers twice the codewords' bounding box; each cell lists, ascending, every codeword
- * that can be the reference's first minimum for a key in the cell (rounding of the reference's
- * fp32 evaluation included), up to 31 (more, or a key outside the grid, falls back to scanning
- * all codewords).  ssq_encode then evaluates only those candidates, with the reference's exact
- * arithmetic, so its codes equal kernels 1 and 2 bit for bit.
+ * cells covers the whole plane: each coordinate x maps to u = (x - mid) * inv, t = u / (1 + |u|),
+ * cell floor((t + 1) * 64), with mid the codewords' bounding-box centre and 1/inv their RMS
+ * spread, so cells are finest where codewords crowd and the end cells reach to +-infinity.
+ * Each cell lists, ascending, every codeword that can be the reference's first minimum for a
+ * key in the cell (rounding of the reference's fp32 evaluation included), up to 31 (a longer
+ * list, an unbounded end cell or a non-finite key falls back to scanning all codewords).  ssq_encode then evaluates
+ * only those candidates, with the reference's exact arithmetic, so its codes equal kernels 1
+ * and 2 bit for bit.
  * The grid depends only on perm-independent codebook values (cent, cent_sh, n_blocks,
  * n_centroids, num_kv_heads when cent_sh != 0); rebuild it when the codebook changes.  Each
  * block's header holds a fingerprint of its codebook: ssq_encode scans every codeword of a

@@ -11,11 +11,12 @@
 // LUT path), online softmax, probabilities cast to the value dtype before P.V
 // (vllm_attn_backend.py:251-252).  Mapping:
 //
-//   workgroup = 4 waves (one per SIMD) for one (batch, KV head, context split, group of <= 16
+//   workgroup = 8 waves (two per SIMD) for one (batch, KV head, context split, group of <= 16
 //               query rows); the codebook [nb][nc][bd] fp32 sits in LDS (128 KiB at head_dim 128
 //               and 256 codewords), so one workgroup per CU.
-//   wave      = streams 64-token tiles (4 pages) with its own running (max, sum, O), two tiles of
-//               codes and values in flight; waves merge through LDS at the end.
+//   wave      = streams 64-token tiles (4 pages) with its own running (max, sum, O) and one
+//               register set: a tile's codes are reloaded for the next tile as soon as its scores
+//               are done, its values as soon as its P.V is done; waves merge through LDS at the end.
 //   scores    = one token per lane.  v_mfma_f32_4x4x1_16b_f32 computes 16 blocks of 4 rows x 4
 //               tokens x 1 dim: with the A operand broadcast from one block (cbsz 4, abid j) every
 //               block multiplies the same 4 query rows, so one instruction adds dim k of all 64

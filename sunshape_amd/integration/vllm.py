@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import importlib
 import json
+import os
 from dataclasses import asdict, dataclass, field
 from pathlib import Path
 from typing import Any, Iterable
@@ -128,11 +129,41 @@ def load_runtime_state(
     )
 
 
-def install_hooks(config: SunShapeVLLMConfig, *args, **kwargs) -> SunShapeVLLMHandle:
-    """Register with a live vLLM; needs vLLM importable (sunshape/integration/vllm.py:284-341)."""
+def install_hooks(
+    *,
+    bundle_path: str | Path,
+    model_name: str,
+    mode: str,
+    bits_per_dim: float,
+    block_dim: int,
+    layers: Iterable[int],
+) -> SunShapeVLLMHandle:
+    """Register the bundle's runtime state with this library's attention backend inside a live
+    vLLM (keyword-only, as sunshape/integration/vllm.py:284-291).
+
+    Raises FileNotFoundError for a missing bundle and RuntimeError when vLLM is not importable
+    (the reference's order, :293-300).  With vLLM present it loads the bundle
+    (``load_runtime_state``), hands it to ``sunshape_amd.vllm_attn_backend`` and selects the
+    backend through ``VLLM_ATTENTION_BACKEND``; patching vLLM's own modules is not done here.
+    """
+    bundle_path = Path(bundle_path)
+    if not bundle_path.exists():
+        raise FileNotFoundError(f"SunShape vLLM bundle does not exist: {bundle_path}")
     try:
         vllm = importlib.import_module("vllm")
     except Exception as exc:  # vLLM is not a dependency
         raise RuntimeError("vLLM is not installed; SunShape hooks cannot be installed.") from exc
-    return SunShapeVLLMHandle(config=config, hooks_installed=True, backend_module=config.backend_module,
-                              vllm_version=getattr(vllm, "__version__", None))
+    layer_list = [int(x) for x in layers]
+    config = SunShapeVLLMConfig(model_name=model_name, bundle_path=str(bundle_path), mode=mode,
+                                bits_per_dim=float(bits_per_dim), block_dim=int(block_dim), layers=layer_list)
+    handle = SunShapeVLLMHandle(config=config, hooks_installed=False, backend_module=config.backend_module,
+                                vllm_version=getattr(vllm, "__version__", None))
+    backend = importlib.import_module(config.backend_module)
+    state = load_runtime_state(bundle_path=bundle_path, model_name=model_name, mode=mode,
+                               bits_per_dim=bits_per_dim, block_dim=block_dim, layers=layer_list,
+                               backend_module=config.backend_module)
+    backend.register_runtime_state(state)
+    os.environ["VLLM_ATTENTION_BACKEND"] = config.connector_name
+    handle.hooks_installed = True
+    handle.notes.append("Registered SunShape runtime state with the attention backend.")
+    return handle

@@ -281,3 +281,22 @@ def test_bench_refuses_more_than_one_gpu():
                        timeout=120)
     assert r.returncode != 0
     assert "one GPU" in (r.stderr + r.stdout)
+
+
+def test_install_hooks_keyword_only_and_error_order(tmp_path):
+    """sunshape/integration/vllm.py:284-300: keyword-only arguments; a missing bundle raises
+    FileNotFoundError before vLLM is looked up; without vLLM it raises RuntimeError."""
+    from sunshape_amd.integration.vllm import install_hooks
+
+    kw = dict(model_name="m", mode="sunshape_base", bits_per_dim=4.0, block_dim=2, layers=[0])
+    with pytest.raises(TypeError):
+        install_hooks(str(tmp_path / "b.pt"), **kw)  # positional bundle_path is refused
+    with pytest.raises(FileNotFoundError):
+        install_hooks(bundle_path=tmp_path / "missing.pt", **kw)
+    bundle = tmp_path / "b.pt"
+    bundle.write_bytes(b"")
+    try:
+        import vllm  # noqa: F401
+    except Exception:
+        with pytest.raises(RuntimeError, match="vLLM is not installed"):
+            install_hooks(bundle_path=bundle, **kw)
