@@ -1,0 +1,4 @@
+// Contiguous-layout decode instantiations: 64-dim bf16 values, passthrough (heavy-block) values.
+#include "ssq_decode_contig.h"
+
+SSQ_CONTIG_UNIT(ssq_contig_64_bf16_mixed) { return contig_mixed<4, SSQ_BF16, true>(cp, pl, st); }
