@@ -233,7 +233,7 @@ def _time_surface(name, fn, n=100):
     return {"api": name, "calls": n, "host_us_per_call": host / n * 1e6, "wall_us_per_call": wall / n * 1e6}
 
 
-def _scores_workload(dev):
+def _scores_workload(dev, kernel=0):
     import torch
 
     from sunshape_amd import _native as N
@@ -250,7 +250,7 @@ def _scores_workload(dev):
         perm=perm.data_ptr(), perm_sh=D, cent=cent.data_ptr(), cent_sh=nb * 256 * bd,
         block_dim=bd, n_blocks=nb, n_centroids=256, layout=N.SSQ_CONTIGUOUS, seq_len=T,
         codes=codes.data_ptr(), c_sb=codes.stride(0), c_sh=codes.stride(1), c_st=codes.stride(2),
-        scores=out.data_ptr(), s_sb=out.stride(0), s_sh=out.stride(1), s_sl=out.stride(2),
+        scores=out.data_ptr(), s_sb=out.stride(0), s_sh=out.stride(1), s_sl=out.stride(2), kernel=kernel,
     )
     L = N.lib()
     stream = torch.cuda.current_stream(dev).cuda_stream
@@ -501,7 +501,7 @@ def main():
     if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2", "c3p6", "c4p6"):
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
-        step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev)
+        step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev, args.kernel)
     elif args.workload in ("c4append", "c5append"):
         step, keys, algo_bytes, cfg, unit_data, kname = _append_workload(args.workload, dev, args.kernel)
     elif args.workload == "copycal":

@@ -832,13 +832,8 @@ int pick_kernel(const ssq_decode_args* a) {
     if (a->kernel == 4) return 2;  // the paged MFMA path, with its 4x4-MFMA-scores kernel forced
     if (a->kernel != 0) return a->kernel;
     if (a->v && ssq_decode_mfma_supported(a)) return 2;
-    if (!a->v) {
-        // scores only: the LUT kernel is the faster one while every query row fits one LUT of <= 64 KiB
-        const int rows = (a->num_q_heads / a->num_kv_heads) * a->q_len;
-        int rp = 1;
-        while (rp < rows) rp <<= 1;
-        if (rows <= kMaxRows && (size_t)a->n_blocks * a->n_centroids * rp * 4 <= 64 * 1024) return 1;
-    }
+    // scores only or decode: the contiguous MFMA kernel where it applies (its 4x4-MFMA scores need no
+    // per-workgroup LUT: config-2 scores 11.9 us against the LUT kernel's 18.3 us), else the generic one
     if (ssq_decode_contig_supported(a)) return 3;
     return 1;
 }

@@ -59,11 +59,12 @@ def test_config1_scores_vs_golden_and_oracle():
 
 
 @pytest.mark.parametrize("B,T", [(2, 1000), (16, 8192)])
-def test_config2_gqa_scores_vs_oracle(B, T):
-    log(f"config2 gqa scores B={B} T={T}")
+@pytest.mark.parametrize("kernel", [0, 1])  # auto (the contiguous 4x4-MFMA kernel), the LUT kernel
+def test_config2_gqa_scores_vs_oracle(B, T, kernel):
+    log(f"config2 gqa scores B={B} T={T} kernel={kernel}")
     p = synthetic.config2(DEV, B=B, T=T)
     scale = p.meta["scale"]
-    got = np_of(hip_ops.gqa_scores(p["q"], p["codes"], p["perm"], p["centroids"], scale=scale))
+    got = np_of(hip_ops.gqa_scores(p["q"], p["codes"], p["perm"], p["centroids"], scale=scale, kernel=kernel))
     q = np_of(p["q"])
     codes = np_of(p["codes"])
     perm = np_of(p["perm"])
@@ -76,8 +77,9 @@ def test_config2_gqa_scores_vs_oracle(B, T):
             assert_rel(got[b, kv * G:(kv + 1) * G, 0], ref, SCORE_TOL, f"c2 b={b} kv={kv}")
 
 
-def test_scores_single_head_shapes_and_ragged_T():
-    log("scores ragged T")
+@pytest.mark.parametrize("kernel", [0, 1])
+def test_scores_single_head_shapes_and_ragged_T(kernel):
+    log(f"scores ragged T kernel={kernel}")
     rng = np.random.default_rng(3)
     perm = rng.permutation(64)
     cent = rng.standard_normal((8, 256, 8)).astype(np.float32)
@@ -86,7 +88,8 @@ def test_scores_single_head_shapes_and_ragged_T():
             codes = rng.integers(0, 256, (T, 8)).astype(np.uint8)
             q = rng.standard_normal((R, 64)).astype(np.float32)
             got = hip_ops.attention_scores(torch.from_numpy(q).to(DEV), torch.from_numpy(codes).to(DEV),
-                                           torch.from_numpy(perm).to(DEV), torch.from_numpy(cent).to(DEV))
+                                           torch.from_numpy(perm).to(DEV), torch.from_numpy(cent).to(DEV),
+                                           kernel=kernel)
             assert_rel(np_of(got), O.attention_scores(q, codes, cent, perm), SCORE_TOL, f"T={T} R={R}")
 
 
