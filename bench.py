@@ -402,6 +402,66 @@ def _copy_workload(dev):
     return step, n // 2, 2 * n, cfg, None, "copy"
 
 
+# (workgroups per CU, loads in flight per thread, 1: a contiguous chunk per workgroup / 0: grid-stride)
+READ_PROBE_SHAPES = ((16, 4, 0), (8, 8, 0), (2, 8, 1), (4, 8, 1), (8, 4, 1), (2, 16, 1))
+
+
+def _stream_probe(dev, launches=10):
+    """Achievable HBM rates on this box, reference points for the roofline fraction: a 2 GiB
+    read-only stream (sunshape_amd/csrc/probe: 16-byte non-temporal loads, grid-stride) and a
+    1 GiB device-to-device copy (1 GiB read + 1 GiB written), each timed with events per launch,
+    median of `launches`.  Both buffers exceed the 256 MB Infinity Cache."""
+    import torch
+
+    from sunshape_amd import _native as N
+    from sunshape_amd.build import PROBE_PATH
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(launches)]
+        for s0, e0 in ev:
+            s0.record()
+            fn()
+            e0.record()
+        torch.cuda.synchronize()
+        return sorted(s0.elapsed_time(e0) for s0, e0 in ev)[launches // 2]
+
+    out = {"launches": launches}
+    n = 2 << 30
+    if os.path.exists(PROBE_PATH):
+        probe = ctypes.CDLL(PROBE_PATH)
+        probe.ssq_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int,
+                                                ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+        buf = torch.ones(n // 2, device=dev, dtype=torch.bfloat16)
+        sink = torch.zeros(1, device=dev, dtype=torch.int32)
+        stream = N.stream_of(dev)
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        best = None
+        for per_cu, unroll, chunked in READ_PROBE_SHAPES:  # the best of a small sweep of launch shapes
+            def read():
+                rc = probe.ssq_probe_stream_read(buf.data_ptr(), n, sink.data_ptr(), per_cu * cus, unroll, chunked,
+                                                 stream)
+                if rc:
+                    raise RuntimeError(f"stream probe launch failed: HIP error {rc}")
+
+            gbps = n / (timed(read) * 1e-3) / 1e9
+            out.setdefault("read_sweep", []).append([per_cu, unroll, chunked, round(gbps, 1)])
+            if best is None or gbps > best[0]:
+                best = (gbps, per_cu, unroll, chunked)
+        out["read"] = ("2 GiB read, 16-byte non-temporal loads (csrc/probe/ssq_probe_stream.hip), best of %d launch "
+                       "shapes: %d workgroups of 256 per CU, %d loads in flight per thread, %s"
+                       % (len(READ_PROBE_SHAPES), best[1], best[2], "a chunk per workgroup" if best[3] else "grid-stride"))
+        out["read_GBps"] = best[0]
+        del buf
+    src = torch.ones(1 << 29, device=dev, dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    out["copy"] = "1 GiB read + 1 GiB written (torch copy_)"
+    out["copy_GBps"] = 2 * (1 << 30) / (timed(lambda: dst.copy_(src)) * 1e-3) / 1e9
+    del src, dst
+    return out
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 def _cpu_model() -> str:
     try:
@@ -579,6 +639,10 @@ def main():
             line["roofline"] = {"bound": "mfma", "achieved": tf, "peak": MFMA_F32_PEAK_TFLOPS, "unit": "TFLOP/s",
                                 "frac": tf / MFMA_F32_PEAK_TFLOPS, "traffic": traffic, "kernel": kname,
                                 "algorithmic_flop_per_launch": flop}
+    if args.workload != "copycal":
+        line["hbm_stream"] = _stream_probe(dev)
+        if "read_GBps" in line["hbm_stream"]:
+            line["hbm_stream"]["frac_of_read"] = achieved_gbps / line["hbm_stream"]["read_GBps"]
     if args.workload != "copycal" and args.cold_steps > 0:
         line["cold"] = _cold_launches(step, args.cold_steps, algo_bytes, dev)
     if getattr(step, "surface", None) is not None:

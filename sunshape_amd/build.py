@@ -3,7 +3,9 @@
 ``python -m sunshape_amd.build`` or ``sunshape_amd.build.build()`` compiles every
 ``csrc/*.hip`` source into ``sunshape_amd/_lib/libsunshape_amd.so`` (each source to an object in
 ``sunshape_amd/_lib/obj``, in parallel, then linked) and ``csrc/torch_ops.cpp`` into
-``sunshape_amd/_lib/libsunshape_torch_ops.so`` (torch.ops.sunshape.*).
+``sunshape_amd/_lib/libsunshape_torch_ops.so`` (torch.ops.sunshape.*).  ``csrc/probe/*.hip`` (a
+bandwidth probe bench.py times beside the decode) links separately into
+``sunshape_amd/_lib/libsunshape_probe.so``.
 """
 
 from __future__ import annotations
@@ -19,6 +21,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_lib")
 LIB_PATH = os.path.join(OUT_DIR, "libsunshape_amd.so")
 TORCH_OPS_PATH = os.path.join(OUT_DIR, "libsunshape_torch_ops.so")
+PROBE_PATH = os.path.join(OUT_DIR, "libsunshape_probe.so")  # measurement probes (bench.py), not the library
 ARCH = "gfx950"
 
 # -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 in generated code.
@@ -128,8 +131,15 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
                                                    os.path.getmtime(os.path.join(os.path.dirname(HERE), "include",
                                                                                  "sunshape_amd.h"))):
         _build_torch_ops()
+    probe_src = os.path.join(CSRC, "probe", "ssq_probe_stream.hip")
+    if not incremental or not os.path.exists(PROBE_PATH) or os.path.getmtime(PROBE_PATH) < os.path.getmtime(probe_src):
+        cmd = [hipcc, *HIP_FLAGS, "-shared", probe_src, "-o", PROBE_PATH + ".tmp"]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"probe library failed to build:\n{res.stderr}")
+        os.replace(PROBE_PATH + ".tmp", PROBE_PATH)
     if verbose:
-        print(f"built {LIB_PATH} and {TORCH_OPS_PATH}")
+        print(f"built {LIB_PATH}, {TORCH_OPS_PATH} and {PROBE_PATH}")
     return LIB_PATH
 
 

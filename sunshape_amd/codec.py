@@ -195,12 +195,25 @@ class SunShapeBlockCodec(torch.nn.Module):
         No counterpart in the reference: a search structure whose encode results equal the
         exhaustive search bit for bit.  Built on first use and rebuilt when the centroid buffer
         changes (new storage or an in-place write, seen through its version counter).
+
+        Footprint: 32 B per cell, 128 x 128 cells per block and codebook head (0.5 MiB), plus a
+        32-byte header per block: 32 MiB for the config-5 layer (2 heads x 32 blocks), 256 MiB
+        for a Llama-3-8B layer at 4 bits/dim (8 heads x 64 blocks).  A
+        per-KV-head codebook has one grid: a single head's view (``codebook(kv_head)``) gets
+        that head's slice of it (the layout is head-major), not a grid of its own.  Set
+        ``use_encode_grid = False`` to run the exhaustive encode without any grid.
         """
         if not self.use_encode_grid or self.block_dim != 2 or self.mode in METRIC_MODES:
             return None
         if cent.shape[-2] > 256 or cent.shape[-3] > 128:
             return None
         buf = self.centroids
+        if buf.ndim == 4 and cent.ndim == 3 and cent.shape == buf.shape[1:] and buf.is_contiguous():
+            step = buf[0].numel() * buf.element_size()
+            off = cent.data_ptr() - buf.data_ptr()
+            if off % step == 0 and 0 <= off // step < buf.shape[0] and cent.is_contiguous():
+                full = self.encode_search_grid(buf)  # one head of the per-KV-head grid
+                return None if full is None else full.view(buf.shape[0], -1)[off // step]
         slot = (cent.data_ptr(), tuple(cent.shape))
         key = (buf.data_ptr(), buf._version)
         hit = self._grid_cache.get(slot)

@@ -41,13 +41,14 @@ constexpr int kMaxCand = kRec - 1;
 constexpr int kHdr = 8;        // floats per block header: mid0, mid1, inv0, inv1, Rc, valid, fingerprint
 constexpr int kThreads = 256;
 
+// Layout, head-major: per codebook head, its block headers (padded to 256 bytes) then its cells, so
+// one head's part of a per-KV-head grid is itself the grid of that head's codebook.
 inline int grid_heads(const ssq_encode_args& a) { return a.cent_sh == 0 ? 1 : a.num_kv_heads; }
-inline size_t grid_hdr_bytes(const ssq_encode_args& a) {
-    return ((size_t)grid_heads(a) * a.n_blocks * kHdr * 4 + 255) & ~(size_t)255;
+__host__ __device__ inline size_t grid_head_hdr_bytes(int nb) { return ((size_t)nb * kHdr * 4 + 255) & ~(size_t)255; }
+__host__ __device__ inline size_t grid_head_bytes(int nb) {
+    return grid_head_hdr_bytes(nb) + (size_t)nb * kG * kG * kRec;
 }
-inline size_t grid_total_bytes(const ssq_encode_args& a) {
-    return grid_hdr_bytes(a) + (size_t)grid_heads(a) * a.n_blocks * kG * kG * kRec;
-}
+inline size_t grid_total_bytes(const ssq_encode_args& a) { return (size_t)grid_heads(a) * grid_head_bytes(a.n_blocks); }
 
 // ---------------------------------------------------------------------------
 // build
@@ -68,7 +69,7 @@ __device__ __forceinline__ uint32_t cw_count_mix(int nc) { return (uint32_t)nc *
 
 // one lane per (block, codebook head), in fp64: the cell map's centre (the codewords' bounding-box
 // centre) and scale (their RMS spread about the mean) per dimension, and max |c|
-__global__ __launch_bounds__(64) void k_grid_header(const float* cent, int64_t cent_sh, int nb, int nc, float* hdr) {
+__global__ __launch_bounds__(64) void k_grid_header(const float* cent, int64_t cent_sh, int nb, int nc, uint8_t* grid) {
     if (threadIdx.x != 0) return;
     const int blk = blockIdx.x, h = blockIdx.y;
     const float* c = cent + (int64_t)h * cent_sh + (int64_t)blk * nc * 2;
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(64) void k_grid_header(const float* cent, int64_t c
         inv[d] = (float)(1.0 / sc);
         valid = valid && isfinite(mid[d]) && isfinite(inv[d]) && inv[d] > 0.f;
     }
-    float* out = hdr + ((int64_t)h * nb + blk) * kHdr;
+    float* out = reinterpret_cast<float*>(grid + (size_t)h * grid_head_bytes(nb)) + (int64_t)blk * kHdr;
     out[0] = mid[0]; out[1] = mid[1]; out[2] = inv[0]; out[3] = inv[1];
     uint32_t fp = cw_count_mix(nc);
     for (int j = 0; j < nc; ++j) fp ^= cw_mix(c[2 * j], c[2 * j + 1], j);
@@ -122,14 +123,15 @@ __device__ __forceinline__ double cell_edge(double t, double mid, double scale) 
 
 // one thread per cell
 __global__ __launch_bounds__(kThreads) void k_grid_cells(const float* cent, int64_t cent_sh, int nb, int nc,
-                                                         const float* hdr, uint8_t* cells) {
+                                                         uint8_t* grid) {
     __shared__ double cw[256][2];
     const int blk = blockIdx.y, h = blockIdx.z, tid = threadIdx.x;
     const int cell = blockIdx.x * kThreads + tid;
     const float* c = cent + (int64_t)h * cent_sh + (int64_t)blk * nc * 2;
     for (int j = tid; j < nc; j += kThreads) { cw[j][0] = c[2 * j]; cw[j][1] = c[2 * j + 1]; }
     __syncthreads();
-    const float* hd = hdr + ((int64_t)h * nb + blk) * kHdr;
+    uint8_t* head = grid + (size_t)h * grid_head_bytes(nb);
+    const float* hd = reinterpret_cast<const float*>(head) + (int64_t)blk * kHdr;
     uint8_t rec[kRec];
 #pragma unroll
     for (int i = 0; i < kRec; ++i) rec[i] = 0;
@@ -172,7 +174,7 @@ __global__ __launch_bounds__(kThreads) void k_grid_cells(const float* cent, int6
             for (int i = 1 + cnt; i < kRec; ++i) rec[i] = rec[cnt];
         }
     }
-    uint4* dst = reinterpret_cast<uint4*>(cells + (((int64_t)h * nb + blk) * kG * kG + cell) * kRec);
+    uint4* dst = reinterpret_cast<uint4*>(head + grid_head_hdr_bytes(nb) + ((int64_t)blk * kG * kG + cell) * kRec);
     const uint32_t* w = reinterpret_cast<const uint32_t*>(rec);
     dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
     dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
@@ -185,8 +187,7 @@ constexpr int kMaxLight = 128;
 
 struct GridParams {
     ssq_encode_args a;
-    const float* hdr;
-    const uint8_t* cells;
+    const uint8_t* grid;       // head-major: headers then cells per codebook head
     int n_light;
     int row_codes;             // whole code rows in 16-byte stores
     int row_q;                 // 16-byte pieces of a key row when rows are read whole (else 0)
@@ -310,7 +311,7 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) f ^= __shfl_xor(f, o);
         if (lane == 0) {
-            const float* h = p.hdr + ((int64_t)hsel * nb + blk) * kHdr;
+            const float* h = reinterpret_cast<const float*>(p.grid + (size_t)hsel * grid_head_bytes(nb)) + (int64_t)blk * kHdr;
             const bool ok = h[5] != 0.f && (f ^ cw_count_mix(nc)) == __float_as_uint(h[6]);
             hd[li] = ok ? make_float4(h[0], h[1], h[2], h[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
             poff[4 * li] = (int)perm[blk * 2];
@@ -323,7 +324,7 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
     __syncthreads();
 
     const uint64_t hm0 = a.heavy_mask[0], hm1 = a.heavy_mask[1];
-    const uint8_t* cells = p.cells + (int64_t)hsel * nb * kG * kG * kRec;
+    const uint8_t* cells = p.grid + (size_t)hsel * grid_head_bytes(nb) + grid_head_hdr_bytes(nb);
     const int keys_wg = waves * 64;
     const int key = blockIdx.x * keys_wg + wave * 64 + lane;  // this lane's key index
     const bool live = key < km.n_keys;
@@ -606,13 +607,12 @@ extern "C" int ssq_encode_grid_build(const ssq_encode_args* a, void* grid, uint6
                 (unsigned long long)grid_bytes, grid_total_bytes(*a));
     hipStream_t st = (hipStream_t)stream;
     const int nh = grid_heads(*a), nb = a->n_blocks, nc = a->n_centroids;
-    float* hdr = reinterpret_cast<float*>(grid);
-    uint8_t* cells = reinterpret_cast<uint8_t*>(grid) + grid_hdr_bytes(*a);
-    hipLaunchKernelGGL(k_grid_header, dim3(nb, nh), dim3(64), 0, st, a->cent, a->cent_sh, nb, nc, hdr);
+    uint8_t* g = static_cast<uint8_t*>(grid);
+    hipLaunchKernelGGL(k_grid_header, dim3(nb, nh), dim3(64), 0, st, a->cent, a->cent_sh, nb, nc, g);
     int rc = ssq_check_hip(hipGetLastError(), "k_grid_header launch");
     if (rc) return rc;
     hipLaunchKernelGGL(k_grid_cells, dim3(kG * kG / kThreads, nb, nh), dim3(kThreads), 0, st, a->cent, a->cent_sh, nb,
-                       nc, (const float*)hdr, cells);
+                       nc, g);
     return ssq_check_hip(hipGetLastError(), "k_grid_cells launch");
 }
 
@@ -626,8 +626,7 @@ int ssq_encode_grid_run(const ssq_encode_args* a, hipStream_t st) {
     GridParams gp;
     memset(&gp, 0, sizeof(gp));
     gp.a = *a;
-    gp.hdr = reinterpret_cast<const float*>(a->grid);
-    gp.cells = reinterpret_cast<const uint8_t*>(a->grid) + grid_hdr_bytes(*a);
+    gp.grid = static_cast<const uint8_t*>(a->grid);
     for (int blk = 0; blk < a->n_blocks; ++blk) {
         const bool heavy = blk < 64 ? ((a->heavy_mask[0] >> blk) & 1) : ((a->heavy_mask[1] >> (blk - 64)) & 1);
         if (!heavy) gp.light[gp.n_light++] = (uint8_t)blk;

@@ -79,3 +79,13 @@ def test_product_fails_loudly_without_library(monkeypatch):
     monkeypatch.setattr(N, "LIB_PATH", "/nonexistent/libsunshape_amd.so")
     with pytest.raises(RuntimeError, match="not built"):
         N.lib()
+
+
+def test_probe_library_exports_the_stream_read():
+    """bench.py's bandwidth probe lives in its own library (not the decode ABI); build() makes it."""
+    import ctypes as C
+
+    from sunshape_amd.build import PROBE_PATH
+
+    probe = C.CDLL(PROBE_PATH)
+    assert hasattr(probe, "ssq_probe_stream_read")

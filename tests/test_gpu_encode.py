@@ -10,6 +10,7 @@ import torch
 from _util import bf16_from_bits, log, np_of, torch_bf16_from_bits
 from oracle import vq_oracle as O
 from sunshape_amd import hip_ops, synthetic
+from sunshape_amd.codec import SunShapeBlockCodec
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -451,3 +452,24 @@ def test_grid_encode_where_rounding_slack_decides():
     assert np.array_equal(np_of(got[0, 0]), ref), int((np_of(got[0, 0]) != ref).sum())
     scan, _ = hip_ops.encode(t(keys)[None, None], t(perm), t(cent), kernel=1)
     assert np.array_equal(np_of(scan[0, 0]), ref)
+
+
+def test_per_head_grid_is_a_slice_of_the_per_kv_head_grid():
+    """The grid is head-major: head h's part of a grid built for [Hkv, nb, nc, 2] codebooks is
+    byte for byte the grid built for that head's codebook alone, and the codec hands a one-head
+    view that slice (no second grid)."""
+    log("encode grid: per-head slices of a per-KV-head grid")
+    g = torch.Generator().manual_seed(21)
+    cent = (torch.randn(3, 32, 256, 2, generator=g) * torch.linspace(0.5, 2.0, 32).view(1, 32, 1, 1)).to(DEV)
+    full = hip_ops.encode_grid(cent)
+    per = full.view(3, -1)
+    for h in range(3):
+        assert torch.equal(per[h], hip_ops.encode_grid(cent[h].contiguous())), f"head {h}"
+    codec = SunShapeBlockCodec.from_buffers(torch.stack([torch.randperm(64, generator=g) for _ in range(3)]),
+                                            cent.cpu(), device=DEV)
+    whole = codec.encode_search_grid(codec.centroids)
+    for h in range(3):
+        view = codec.encode_search_grid(codec.codebook(h))
+        assert view.data_ptr() == whole.data_ptr() + h * per.shape[1] and view.numel() == per.shape[1]
+        assert torch.equal(view, per[h])
+    assert len(codec._grid_cache) == 1
