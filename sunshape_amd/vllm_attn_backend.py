@@ -18,6 +18,8 @@ Differences by design:
 
 from __future__ import annotations
 
+import math
+
 import os
 from dataclasses import dataclass
 from typing import Any
@@ -173,6 +175,33 @@ def quantize_key_states(layer_idx: int, key_states: torch.Tensor) -> SunShapeQua
     )
 
 
+def _dequantize_key_payload_if_needed(layer_idx: int | None, key_states: Any) -> Any:
+    """Dense fp32 keys [B, Hkv, S, D] from a quantized payload, one ``codec.dequantize`` (the
+    ssq_dequantize kernel) per (batch, KV head), as sunshape/vllm_attn_backend.py:140-156 does;
+    other key states pass through."""
+    if not isinstance(key_states, SunShapeQuantizedKeys):
+        return key_states
+    runtime = get_registered_runtime()
+    if runtime is None or layer_idx is None:
+        raise RuntimeError("SunShape runtime state is required to dequantize quantized key payloads.")
+    codec = runtime.codec_for_layer(int(layer_idx))
+    if codec is None:
+        raise RuntimeError(f"No SunShape codec is registered for layer {layer_idx}.")
+    per_head = getattr(codec, "num_kv_heads", None) is not None
+    batches = []
+    for b in range(key_states.batch_size):
+        heads = [codec.dequantize(key_states.head(b, h), kv_head=h if per_head else None)
+                 for h in range(key_states.num_kv_heads)]
+        batches.append(torch.stack(heads, dim=0))
+    return torch.stack(batches, dim=0)
+
+
+def _causal_mask(query_len: int, seq_len: int, device) -> torch.Tensor:
+    """Additive fp32 [query_len, seq_len] mask of scaled_dot_product_attention(is_causal=True):
+    query row i sees tokens 0..i (torch aligns a non-square causal mask to the top left)."""
+    return torch.full((query_len, seq_len), float("-inf"), device=device, dtype=torch.float32).triu_(1)
+
+
 def _decode_keys_if_needed(layer_idx: int | None, key_states: torch.Tensor) -> torch.Tensor:
     """Dense keys through the codec round trip (sunshape/vllm_attn_backend.py:126-137)."""
     runtime = get_registered_runtime()
@@ -309,10 +338,24 @@ class SunShapeAttentionImpl:
             return _apply_quantized_attention(
                 codec=codec, query=query, key=key, value=value, attn_mask=attn_mask, scale=scale,
             )
-        if isinstance(key, SunShapeQuantizedKeys):
-            raise RuntimeError(reason)
-        key = _decode_keys_if_needed(layer, key)
         delegate = self.delegate
+        if (isinstance(key, SunShapeQuantizedKeys) and delegate is None and is_causal and attn_mask is None
+                and _quantized_fast_path_unavailable_reason(runtime_state=runtime_state, layer_idx=layer, query=query,
+                                                            key=key, value=value, attn_mask=None,
+                                                            is_causal=False) is None):
+            # Causal attention over more than one query row (chunked prefill): the reference
+            # dequantizes the payload and runs scaled_dot_product_attention(query * scale, key,
+            # value, is_causal=True) (:306-345), i.e. scores scaled by scale / sqrt(head_dim) (1 /
+            # sqrt(head_dim) without a scale) under a top-left causal mask.  The fused kernel
+            # computes the same attention from the codes.
+            codec = runtime_state.codec_for_layer(int(layer))
+            head_dim = int(query.shape[-1])
+            eff = (1.0 if scale is None else float(scale)) / math.sqrt(head_dim)
+            mask = _causal_mask(int(query.shape[2]), int(value.shape[2]), query.device)
+            return _apply_quantized_attention(codec=codec, query=query, key=key, value=value, attn_mask=mask,
+                                              scale=eff)
+        key = _dequantize_key_payload_if_needed(layer, key)
+        key = _decode_keys_if_needed(layer, key)
         if delegate is not None:
             if hasattr(delegate, "forward"):
                 return delegate.forward(query, key, value, attn_mask=attn_mask, is_causal=is_causal,

@@ -116,6 +116,84 @@ def test_quantize_key_states_and_impl_forward_per_kv_head_codec():
         VB.clear_registered_runtime()
 
 
+def _per_head_runtime(Hkv, D, bd, seed):
+    from sunshape_amd.integration.vllm import SunShapeVLLMRuntimeState
+
+    cb = synthetic.make_codebook(Hkv, D, bd, seed)
+    codec = SunShapeBlockCodec.from_buffers(cb.perm, cb.centroids, device=DEV)
+    bundle = SunShapeBundle("m", [0], 2.0, bd, "profileperm_baseline", 0, 0, 0, {0: codec})
+    return cb, codec, SunShapeVLLMRuntimeState("p", "m", "sunshape_base", 2.0, bd, [0], bundle, "cuda")
+
+
+@pytest.mark.parametrize("scale", [None, 0.5])
+def test_impl_forward_causal_rows_over_quantized_payload(scale):
+    """Causal attention with several query rows over a quantized payload (chunked prefill).  The
+    reference dequantizes the payload and runs scaled_dot_product_attention(query * scale, key,
+    value, is_causal=True) (sunshape/vllm_attn_backend.py:306-345): scores scaled by
+    scale / sqrt(D) (1 / sqrt(D) without a scale) under torch's top-left causal mask.  The fused
+    kernel computes that from the codes: checked against the oracle with the same mask and scale,
+    and against torch's fp32 scaled_dot_product_attention over the oracle's dequantized keys."""
+    import torch.nn.functional as F
+
+    log(f"backend causal rows over a quantized payload scale={scale}")
+    B, Hq, Hkv, S, D, bd, Lq = 2, 8, 2, 300, 64, 2, 3
+    cb, codec, rs = _per_head_runtime(Hkv, D, bd, 71)
+    VB.register_runtime_state(rs)
+    try:
+        g = torch.Generator().manual_seed(72)
+        keys = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+        qk = VB.quantize_key_states(0, keys.to(DEV))
+        q = torch.randn(B, Hq, Lq, D, generator=g).to(torch.bfloat16)
+        v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+        impl = VB.get_backend_factory().make_impl(layer_idx=0)
+        out = np_of(impl(q.to(DEV), qk, v.to(DEV), scale=scale, is_causal=True))
+        eff = (1.0 if scale is None else scale) / math.sqrt(D)
+        mask = np.triu(np.full((Lq, S), -np.inf, dtype=np.float32), 1)
+        codes = np_of(qk.codes)
+        ref = O.decode_attention(np_of(q), codes, np_of(v), cb.centroids.numpy(), cb.perm.numpy(), eff, "bf16", "bf16",
+                                 mask=mask)
+        assert_rel(out, ref, BF16_TOL, "causal rows vs oracle")
+        k_hat = np.stack([np.stack([O.dequantize(codes[b, h], cb.centroids[h].numpy(), cb.perm[h].numpy())
+                                    for h in range(Hkv)]) for b in range(B)])
+        qs = q.float() * (1.0 if scale is None else scale)
+        kk = torch.from_numpy(k_hat).repeat_interleave(Hq // Hkv, dim=1)
+        vv = v.float().repeat_interleave(Hq // Hkv, dim=1)
+        sdpa = F.scaled_dot_product_attention(qs, kk, vv, is_causal=True)
+        assert_rel(out, sdpa.numpy(), BF16_TOL, "causal rows vs fp32 SDPA on the dequantized keys")
+    finally:
+        VB.clear_registered_runtime()
+
+
+def test_impl_forward_quantized_payload_to_delegate_is_dequantized():
+    """Off the fused path with a delegate, the reference hands the delegate the dequantized keys
+    (sunshape/vllm_attn_backend.py:306-323): one codec.dequantize per (batch, KV head)."""
+    log("backend quantized payload to a delegate")
+    B, Hq, Hkv, S, D, bd = 2, 4, 2, 100, 64, 2
+    cb, codec, rs = _per_head_runtime(Hkv, D, bd, 81)
+    VB.register_runtime_state(rs)
+    seen = {}
+
+    def delegate(query, key, value, **kw):
+        seen["key"], seen["kw"] = key, kw
+        return torch.zeros_like(query)
+
+    try:
+        g = torch.Generator().manual_seed(82)
+        qk = VB.quantize_key_states(0, torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16).to(DEV))
+        q = torch.randn(B, Hq, 2, D, generator=g).to(torch.bfloat16).to(DEV)
+        v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16).to(DEV)
+        impl = VB.get_backend_factory().make_impl(layer_idx=0, delegate=delegate)
+        impl(q, qk, v, is_causal=True, scale=0.25)
+        codes = np_of(qk.codes)
+        want = np.stack([np.stack([O.dequantize(codes[b, h], cb.centroids[h].numpy(), cb.perm[h].numpy())
+                                   for h in range(Hkv)]) for b in range(B)])
+        assert seen["key"].shape == (B, Hkv, S, D)
+        assert_rel(np_of(seen["key"]), want, SCORE_TOL, "delegate keys")
+        assert seen["kw"]["is_causal"] is True and seen["kw"]["scale"] == 0.25
+    finally:
+        VB.clear_registered_runtime()
+
+
 def test_bundle_roundtrip_on_gpu_and_runtime_state(tmp_path):
     log("bundle round trip")
     codec, _ = _mixed_codec(seed=51)

@@ -135,9 +135,11 @@ def test_backend_gate_reasons():
     assert R(**{**kw, "query": torch.randn(2, 4, 2, 64), "is_causal": True}) == \
         "Causal quantized fast path currently targets decode (query_len == 1)."
     assert R(**{**kw, "attn_mask": torch.zeros(10)}) == "Unsupported attention-mask rank for quantized fast path."
+    # off the fused path a quantized payload is dequantized through the registered runtime, as the
+    # reference does (sunshape/vllm_attn_backend.py:140-148, :306): none registered -> RuntimeError
     impl = VB.SunShapeAttentionImpl(layer_idx=0, runtime_state=rs)
     bad = VB.SunShapeQuantizedKeys(quantized_heads=(), batch_size=3, num_kv_heads=2, seq_len=10)
-    with pytest.raises(RuntimeError, match="batch size"):
+    with pytest.raises(RuntimeError, match="runtime state is required to dequantize"):
         impl.forward(q, bad, v)
 
 
