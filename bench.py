@@ -233,6 +233,34 @@ def _time_surface(name, fn, n=100):
     return {"api": name, "calls": n, "host_us_per_call": host / n * 1e6, "wall_us_per_call": wall / n * 1e6}
 
 
+def _time_graph(name, fn, n=50):
+    """The same call captured once in a graph (torch.cuda.graph: HIP graphs, as a serving loop
+    captures its decode step) and replayed n times back to back: per-call time without the
+    host's launch cost, with the graph's outputs checked against an eager call."""
+    import torch
+
+    eager = fn().clone()
+    side = torch.cuda.Stream()  # default priority
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager), "graph replay differs from the eager call"
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(n):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return {"api": name, "replays": n, "us_per_call": start.elapsed_time(end) * 1e3 / n}
+
+
 def _scores_workload(dev, kernel=0):
     import torch
 
@@ -649,6 +677,10 @@ def main():
         # the same decode through the Python drop-in, beside the prebuilt C-ABI replay timed above
         line["python_surface"] = _time_surface(*step.surface)
         line["python_surface"]["c_abi_kernel_avg_us"] = avg_ms * 1e3
+        try:  # a measurement beside the contract's figures: never the reason the line is missing
+            line["graph_replay"] = _time_graph(*step.surface)
+        except Exception as exc:  # noqa: BLE001
+            line["graph_replay"] = {"error": f"{type(exc).__name__}: {exc}"}
     if not args.no_cpu and unit_data is not None:
         line["cpu_baseline"] = _cpu_baseline(unit_data, args.cpu_seconds)
     else:
