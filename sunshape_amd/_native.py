@@ -211,13 +211,18 @@ def kernel_error(e: RuntimeError) -> RuntimeError:
     return SunShapeKernelError(int(m.group(1)), m.group(2))
 
 
+def signed64(w: int) -> int:
+    """An unsigned 64-bit mask word as the signed int64 the operators' int arguments carry."""
+    return w - (1 << 64) if w >= (1 << 63) else w
+
+
 def mask_words_signed(mask) -> tuple[int, int]:
     """heavy_mask_words as two signed int64 (the operators' int arguments), cached per mask tuple."""
     key = None if mask is None else tuple(bool(x) for x in (mask.tolist() if hasattr(mask, "tolist") else mask))
     hit = _WORDS.get(key)
     if hit is None:
         w0, w1 = heavy_mask_words(key)
-        hit = tuple(w - (1 << 64) if w >= (1 << 63) else w for w in (w0, w1))
+        hit = (signed64(w0), signed64(w1))
         _WORDS[key] = hit
     return hit
 

@@ -1,9 +1,10 @@
 // Torch operators over the sunshape_amd C ABI (host code only; the kernels live in
-// libsunshape_amd.so): torch.ops.sunshape.decode, .scores and .encode.
+// libsunshape_amd.so): torch.ops.sunshape.decode, .scores and .encode_into.
 //
 // Each operator validates its tensors (the checks and messages of the Python surface,
-// sunshape_amd/hip_ops.py), allocates outputs and workspace through torch's caching allocator,
-// and calls the library on torch's current HIP stream of the query's device.  Registered for the
+// sunshape_amd/hip_ops.py), allocates outputs and workspace through torch's caching allocator
+// (encode_into writes into outputs its caller allocates: fresh tensors, or cache pages), and
+// calls the library on torch's current HIP stream of the first tensor's device.  Registered for the
 // CUDA dispatch key, which HIP tensors carry in PyTorch-ROCm, so the operators are visible to the
 // dispatcher and to graph capture.  A library error raises RuntimeError whose message starts with
 // "sunshape_amd status <code>: ".
@@ -237,12 +238,154 @@ std::tuple<Tensor, Tensor, Tensor> decode(const Tensor& q_in, const Tensor& code
     return {out, lse, scores};
 }
 
+// ---------------------------------------------------------------------------------------------
+// scores: sunshape/triton_kernels.py:570-609 (one query row set per KV head, all batches and KV
+// heads in one launch); q [B, Hq, Lq, D], codes [B, Hkv, T, nb] -> fp32 [B, Hq, Lq, T]
+// ---------------------------------------------------------------------------------------------
+Tensor scores(const Tensor& q_in, const Tensor& codes, const Tensor& perm_in, const Tensor& cent_in,
+              std::optional<double> scale, int64_t hm0, int64_t hm1, const std::optional<Tensor>& pt, bool pt_dense,
+              int64_t code_bits, int64_t num_splits, int64_t kernel) {
+    on_gpu("query", q_in);
+    on_gpu("codes", codes);
+    TORCH_CHECK(q_in.dim() == 4 && codes.dim() == 4, "scores expects q [B, Hq, Lq, D] and codes [B, Hkv, T, nb]");
+    const Tensor q = q_in.stride(-1) == 1 ? q_in : q_in.contiguous();
+    TORCH_CHECK(codes.stride(-1) == 1, "codes must be contiguous in the last dim");
+    const int64_t B = q.size(0), Hq = q.size(1), Lq = q.size(2), D = q.size(3);
+    const int64_t Hkv = codes.size(1), T = codes.size(2);
+    TORCH_CHECK(codes.size(0) == B, "Quantized key batch size does not match query batch size.");
+    TORCH_CHECK(Hq % Hkv == 0, "Query head count must be divisible by kv-head count.");
+    const Codec c = codec_arrays(perm_in, cent_in, D, Hkv);
+    check_codes(codes, c.nb, code_bits);
+    const bool any_heavy = hm0 != 0 || hm1 != 0;
+    check_pt(pt, any_heavy);
+    c10::hip::HIPGuard guard(q.device().index());
+    Tensor out = at::empty({B, Hq, Lq, T}, q.options().dtype(at::kFloat));
+    if (T == 0 || B * Hq * Lq == 0) return out;
+    ssq_decode_args a{};
+    a.struct_size = sizeof(ssq_decode_args);
+    a.q = q.data_ptr(); a.q_dtype = dtype_code(q);
+    a.q_sb = q.stride(0); a.q_sh = q.stride(1); a.q_sl = q.stride(2);
+    a.batch = (int32_t)B; a.num_q_heads = (int32_t)Hq; a.q_len = (int32_t)Lq; a.head_dim = (int32_t)D;
+    a.num_kv_heads = (int32_t)Hkv;
+    a.has_scale = scale.has_value() ? 1 : 0;
+    a.scale = scale.has_value() ? (float)*scale : 0.f;
+    a.perm = c.perm.data_ptr<int64_t>(); a.perm_sh = c.perm_sh;
+    a.cent = c.cent.data_ptr<float>(); a.cent_sh = c.cent_sh;
+    a.block_dim = (int32_t)c.bd; a.n_blocks = (int32_t)c.nb; a.n_centroids = (int32_t)c.nc;
+    a.heavy_mask[0] = (uint64_t)hm0; a.heavy_mask[1] = (uint64_t)hm1;
+    a.pt_dtype = SSQ_F32;
+    if (any_heavy) {
+        a.pt_dense = pt_dense ? 1 : 0;
+        a.pt_dtype = dtype_code(*pt);
+        a.pt = pt->data_ptr();
+        a.pt_sb = pt->stride(0); a.pt_sh = pt->stride(1); a.pt_st = pt->stride(2);
+    }
+    a.layout = SSQ_CONTIGUOUS;
+    a.seq_len = (int32_t)T;
+    a.codes = reinterpret_cast<const uint8_t*>(codes.data_ptr());
+    a.c_sb = codes.stride(0); a.c_sh = codes.stride(1); a.c_st = codes.stride(2);
+    a.scores = out.data_ptr<float>();
+    a.s_sb = out.stride(0); a.s_sh = out.stride(1); a.s_sl = out.stride(2);
+    a.num_splits = (int32_t)num_splits; a.kernel = (int32_t)kernel; a.code_bits = (int32_t)code_bits;
+    check_status(ssq_attention_scores(&a, stream_of(q)));
+    return out;
+}
+
+// ---------------------------------------------------------------------------------------------
+// encode_into: sunshape/codec.py:362-385 for keys [B, Hkv, S, D], written into the caller's codes
+// ([B, Hkv, S, nb] uint8, or pages [P, Hkv, page, nb] with slot_mapping [B, S]) and, for heavy
+// blocks, passthrough values ([B, Hkv, S, slots, bd], or pages [P, Hkv, page, slots, bd])
+// ---------------------------------------------------------------------------------------------
+void encode_into(const Tensor& keys_in, const Tensor& perm_in, const Tensor& cent_in, int64_t hm0, int64_t hm1,
+                 bool pt_dense, const Tensor& codes, const std::optional<Tensor>& pt,
+                 const std::optional<Tensor>& slot_mapping, const std::optional<Tensor>& metric_in,
+                 const std::optional<Tensor>& grid, int64_t kernel, bool direct) {
+    on_gpu("key_states", keys_in);
+    TORCH_CHECK(keys_in.dim() == 4,
+                "quantize_key_states expects key_states with shape [batch, kv_heads, seq_len, head_dim].");
+    const Tensor keys = keys_in.stride(-1) == 1 ? keys_in : keys_in.contiguous();
+    const int64_t B = keys.size(0), Hkv = keys.size(1), S = keys.size(2), D = keys.size(3);
+    const Codec c = codec_arrays(perm_in, cent_in, D, Hkv);
+    on_gpu("codes", codes);
+    TORCH_CHECK(codes.scalar_type() == at::kByte && codes.dim() == 4 && codes.size(1) == Hkv &&
+                    codes.size(3) == c.nb && codes.stride(3) == 1,
+                "codes must be uint8 [.., ", Hkv, ", .., ", c.nb, "] with unit last stride");
+    const bool any_heavy = hm0 != 0 || hm1 != 0;
+    const bool paged = slot_mapping.has_value() && slot_mapping->defined();
+    if (paged) {
+        on_gpu("slot_mapping", *slot_mapping);
+        TORCH_CHECK(slot_mapping->scalar_type() == at::kLong && slot_mapping->dim() == 2 &&
+                        slot_mapping->size(0) == B && slot_mapping->size(1) == S && slot_mapping->stride(1) == 1,
+                    "slot_mapping must be int64 [B, S]");
+    } else {
+        TORCH_CHECK(codes.size(0) == B && codes.size(2) == S, "codes must be [", B, ", ", Hkv, ", ", S, ", ", c.nb, "]");
+    }
+    if (any_heavy) {
+        TORCH_CHECK(pt.has_value() && pt->defined(), "heavy blocks need a passthrough output");
+        on_gpu("passthrough_values", *pt);
+        TORCH_CHECK(pt->dim() == 5 && pt->size(1) == Hkv && pt->size(4) == c.bd && pt->stride(4) == 1 &&
+                        pt->stride(3) == c.bd,
+                    "passthrough output must be [.., ", Hkv, ", .., slots, ", c.bd, "] with packed rows");
+    }
+    Tensor metric;
+    int64_t metric_sh = 0;
+    if (metric_in.has_value() && metric_in->defined()) {
+        on_gpu("metric", *metric_in);
+        metric = metric_in->to(at::kFloat).contiguous();
+        TORCH_CHECK((metric.dim() == 2 || metric.dim() == 3) && metric.size(-1) == D && metric.size(-2) == D,
+                    "metric must be [D, D] or [Hkv, D, D]");
+        if (metric.dim() == 3) {
+            TORCH_CHECK(metric.size(0) == Hkv, "per-head metric holds ", metric.size(0), " heads, keys have ", Hkv);
+            metric_sh = D * D;
+        }
+    }
+    if (B * S == 0) return;
+    c10::hip::HIPGuard guard(keys.device().index());
+    ssq_encode_args a{};
+    a.struct_size = sizeof(ssq_encode_args);
+    a.keys = keys.data_ptr(); a.k_dtype = dtype_code(keys);
+    a.k_sb = keys.stride(0); a.k_sh = keys.stride(1); a.k_ss = keys.stride(2);
+    a.batch = (int32_t)B; a.num_kv_heads = (int32_t)Hkv; a.seq_len = (int32_t)S; a.head_dim = (int32_t)D;
+    a.perm = c.perm.data_ptr<int64_t>(); a.perm_sh = c.perm_sh;
+    a.cent = c.cent.data_ptr<float>(); a.cent_sh = c.cent_sh;
+    a.metric = metric.defined() ? metric.data_ptr<float>() : nullptr; a.metric_sh = metric_sh;
+    a.block_dim = (int32_t)c.bd; a.n_blocks = (int32_t)c.nb; a.n_centroids = (int32_t)c.nc;
+    a.heavy_mask[0] = (uint64_t)hm0; a.heavy_mask[1] = (uint64_t)hm1;
+    a.codes = reinterpret_cast<uint8_t*>(codes.data_ptr());
+    a.c_sb = codes.stride(0); a.c_sh = codes.stride(1); a.c_st = codes.stride(2);
+    a.pt_dtype = SSQ_F32;
+    if (any_heavy) {
+        a.pt = pt->data_ptr(); a.pt_dtype = dtype_code(*pt); a.pt_dense = pt_dense ? 1 : 0;
+        a.pt_sb = pt->stride(0); a.pt_sh = pt->stride(1); a.pt_st = pt->stride(2);
+    }
+    if (paged) {
+        a.slot_mapping = slot_mapping->data_ptr<int64_t>(); a.sm_sb = slot_mapping->stride(0);
+        a.page_size = (int32_t)codes.size(2);
+    }
+    a.kernel = (int32_t)kernel;
+    a.direct_dist = direct ? 1 : 0;
+    if (grid.has_value() && grid->defined() && !direct) {
+        on_gpu("grid", *grid);
+        TORCH_CHECK(grid->scalar_type() == at::kByte && grid->is_contiguous(), "grid must be the uint8 tensor from encode_grid");
+        a.grid = grid->data_ptr(); a.grid_bytes = (uint64_t)grid->numel();
+    }
+    check_status(ssq_encode(&a, stream_of(keys)));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(sunshape, m) {
     m.def("decode(Tensor q, Tensor codes, Tensor v, Tensor perm, Tensor cent, float? scale, Tensor? mask, int hm0, "
           "int hm1, Tensor? pt, bool pt_dense, Tensor? block_table, Tensor? seq_lens, bool return_lse, "
           "bool return_scores, int num_splits, int kernel, int code_bits, bool no_alloc) -> (Tensor, Tensor, Tensor)");
+    m.def("scores(Tensor q, Tensor codes, Tensor perm, Tensor cent, float? scale, int hm0, int hm1, Tensor? pt, "
+          "bool pt_dense, int code_bits, int num_splits, int kernel) -> Tensor");
+    m.def("encode_into(Tensor keys, Tensor perm, Tensor cent, int hm0, int hm1, bool pt_dense, Tensor(a!) codes, "
+          "Tensor(b!)? pt, Tensor? slot_mapping, Tensor? metric, Tensor? grid, int kernel, bool direct) -> ()");
 }
 
-TORCH_LIBRARY_IMPL(sunshape, CUDA, m) { m.impl("decode", &decode); }
+TORCH_LIBRARY_IMPL(sunshape, CUDA, m) {
+    m.impl("decode", &decode);
+    m.impl("scores", &scores);
+    m.impl("encode_into", &encode_into);
+}

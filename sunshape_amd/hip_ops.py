@@ -10,6 +10,7 @@ all KV heads (the reference's per-layer codec: perm [D], centroids
 from __future__ import annotations
 
 import ctypes
+import types
 from typing import Optional, Sequence
 
 import torch
@@ -199,22 +200,17 @@ def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, c
         _require(codes.shape[1] == nb, "Quantized key block count does not match codec: "
                  f"indices.shape[1]={codes.shape[1]}, codec.n_blocks={nb}.")
     _check_codes(codes, nb, code_bits)
-    out = torch.empty((R, T), device=q.device, dtype=torch.float32)
     if R == 0 or T == 0:
-        return out
-    hm, pt, ptd, ptdt = _pt_args(heavy, pt, pt_dense)
-    a = N.DecodeArgs(
-        q=N.ptr(q), q_dtype=N.dtype_code(q.dtype), q_sb=0, q_sh=q.stride(0), q_sl=0,
-        batch=1, num_q_heads=R, q_len=1, head_dim=D, num_kv_heads=1, has_scale=0, scale=0.0,
-        perm=N.ptr(perm), perm_sh=0, cent=N.ptr(cent), cent_sh=0,
-        block_dim=bd, n_blocks=nb, n_centroids=nc,
-        pt_dense=ptd, pt_dtype=ptdt, pt=N.ptr(pt), pt_sb=0, pt_sh=0, pt_st=0 if pt is None else pt.stride(0),
-        layout=N.SSQ_CONTIGUOUS, seq_len=T, codes=N.ptr(codes), c_sb=0, c_sh=0, c_st=codes.stride(0),
-        scores=N.ptr(out), s_sb=0, s_sh=out.stride(0), s_sl=0, code_bits=int(code_bits), kernel=int(kernel),
-    )
-    a.heavy_mask[0], a.heavy_mask[1] = hm
-    N.check(N.lib().ssq_attention_scores(ctypes.byref(a), N.stream_of(q.device)))
-    return out
+        return torch.empty((R, T), device=q.device, dtype=torch.float32)
+    hm, pt, ptd, _ = _pt_args(heavy, pt, pt_dense)
+    # one KV head, one query row per head: the torch operator's [B, Hq, Lq, D] / [B, Hkv, T, ..] views
+    try:
+        out = N.torch_ops().scores(q[None, :, None], codes[None, None], perm, cent, None, N.signed64(hm[0]),
+                                   N.signed64(hm[1]), None if pt is None else pt[None, None], bool(ptd),
+                                   int(code_bits), 0, int(kernel))
+    except RuntimeError as e:
+        raise N.kernel_error(e) from None
+    return out.view(R, T)
 
 
 def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
@@ -243,26 +239,14 @@ def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: t
     _require(Hq % Hkv == 0, "Query head count must be divisible by kv-head count.")
     perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, Hkv)
     _check_codes(codes, nb, code_bits)
-    out = torch.empty((B, Hq, Lq, T), device=q.device, dtype=torch.float32)
     if T == 0:
-        return out
-    hm, pt, ptd, ptdt = _pt_args(heavy, pt, pt_dense)
-    ps = (pt.stride(0), pt.stride(1), pt.stride(2)) if pt is not None else (0, 0, 0)
-    a = N.DecodeArgs(
-        q=N.ptr(q), q_dtype=N.dtype_code(q.dtype), q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
-        batch=B, num_q_heads=Hq, q_len=Lq, head_dim=D, num_kv_heads=Hkv,
-        has_scale=1 if scale is not None else 0, scale=float(scale or 0.0),
-        perm=N.ptr(perm), perm_sh=perm_sh, cent=N.ptr(cent), cent_sh=cent_sh,
-        block_dim=bd, n_blocks=nb, n_centroids=nc,
-        pt_dense=ptd, pt_dtype=ptdt, pt=N.ptr(pt), pt_sb=ps[0], pt_sh=ps[1], pt_st=ps[2],
-        layout=N.SSQ_CONTIGUOUS, seq_len=T, codes=N.ptr(codes), c_sb=codes.stride(0), c_sh=codes.stride(1),
-        c_st=codes.stride(2),
-        scores=N.ptr(out), s_sb=out.stride(0), s_sh=out.stride(1), s_sl=out.stride(2), code_bits=int(code_bits),
-        num_splits=int(num_splits), kernel=int(kernel),
-    )
-    a.heavy_mask[0], a.heavy_mask[1] = hm
-    N.check(N.lib().ssq_attention_scores(ctypes.byref(a), N.stream_of(q.device)))
-    return out
+        return torch.empty((B, Hq, Lq, T), device=q.device, dtype=torch.float32)
+    hm, pt, ptd, _ = _pt_args(heavy, pt, pt_dense)
+    try:
+        return N.torch_ops().scores(q, codes, perm, cent, None if scale is None else float(scale), N.signed64(hm[0]),
+                                    N.signed64(hm[1]), pt, bool(ptd), int(code_bits), int(num_splits), int(kernel))
+    except RuntimeError as e:
+        raise N.kernel_error(e) from None
 
 
 def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
@@ -317,28 +301,10 @@ def decode(q: torch.Tensor, codes: torch.Tensor, v: torch.Tensor, perm: torch.Te
     return tuple(res)
 
 
-def encode_args(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
-           heavy: Optional[Sequence[bool]] = None, pt_dtype: Optional[torch.dtype] = None, pt_dense: bool = False,
-           codes_out: Optional[torch.Tensor] = None, pt_out: Optional[torch.Tensor] = None,
-           slot_mapping: Optional[torch.Tensor] = None, metric: Optional[torch.Tensor] = None, kernel: int = 0,
-           grid: Optional[torch.Tensor] = None, direct: bool = False, rotation: Optional[torch.Tensor] = None):
-    """Validated ssq_encode arguments for encode(): (args, codes, pt, tensors the args point into).
-
-    For callers that replay one launch many times through the C ABI (a benchmark, a serving
-    loop); keep the returned tensors alive while the args are in use.
-
-    Passthrough values (heavy blocks) are [B, Hkv, S, n_heavy, bd] (compact) or
-    [B, Hkv, S, nb, bd] zero-filled (pt_dense, the reference's layout).  With
-    slot_mapping [B, S] (int64) the outputs go into caller-provided pages:
-    codes_out [P, Hkv, page, nb], pt_out [P, Hkv, page, slots, bd].  Without it, codes_out /
-    pt_out (compact) may be given as [B, Hkv, S, ...] views to write into instead of allocating.
-    metric: SunShape-Pro block metric E [D, D] or per KV head [Hkv, D, D] (fp32); distances are
-    taken between E_b x and E_b c (sunshape/codec.py:375-376).  None = identity.
-    grid: search grid from encode_grid(cent) (block_dim 2, no metric); with it the encode
-    evaluates only each key's certified candidates (same codes).  kernel: 0 auto, 1 exact scan,
-    2 MFMA screen, 3 grid search.
-    Reference: sunshape/codec.py:362-385, sunshape/vllm_attn_backend.py:101-123.
-    """
+def _encode_prepare(keys, perm, cent, heavy, pt_dtype, pt_dense, codes_out, pt_out, slot_mapping, metric, rotation):
+    """Validated encode inputs and the outputs to write (allocated unless given): a namespace of
+    keys, perm, cent, perm_sh, cent_sh, bd, nb, nc, w0, w1, metric, metric_sh, codes, pt, pt_dtype,
+    c_str, p_str, page, slot_mapping."""
     _on_gpu("key_states", keys)
     _require(keys.ndim == 4, "quantize_key_states expects key_states with shape [batch, kv_heads, seq_len, head_dim].")
     if rotation is not None:  # the rotated mode's forward transform, fp32 keys @ R^T (codec.py:363-364)
@@ -402,23 +368,53 @@ def encode_args(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
             pt_dtype = pt.dtype
         c_str = (codes.stride(0), codes.stride(1), codes.stride(2))
         p_str = (pt.stride(0), pt.stride(1), pt.stride(2)) if pt is not None else (0, 0, 0)
+    return types.SimpleNamespace(keys=keys, perm=perm, cent=cent, perm_sh=perm_sh, cent_sh=cent_sh, bd=bd, nb=nb, nc=nc,
+                                 w0=w0, w1=w1, metric=metric, metric_sh=metric_sh, codes=codes, pt=pt,
+                                 pt_dtype=pt_dtype, c_str=c_str, p_str=p_str, page=page, slot_mapping=slot_mapping)
+
+
+def encode_args(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
+           heavy: Optional[Sequence[bool]] = None, pt_dtype: Optional[torch.dtype] = None, pt_dense: bool = False,
+           codes_out: Optional[torch.Tensor] = None, pt_out: Optional[torch.Tensor] = None,
+           slot_mapping: Optional[torch.Tensor] = None, metric: Optional[torch.Tensor] = None, kernel: int = 0,
+           grid: Optional[torch.Tensor] = None, direct: bool = False, rotation: Optional[torch.Tensor] = None):
+    """Validated ssq_encode arguments for encode(): (args, codes, pt, tensors the args point into).
+
+    For callers that replay one launch many times through the C ABI (a benchmark, a serving
+    loop); keep the returned tensors alive while the args are in use.
+
+    Passthrough values (heavy blocks) are [B, Hkv, S, n_heavy, bd] (compact) or
+    [B, Hkv, S, nb, bd] zero-filled (pt_dense, the reference's layout).  With
+    slot_mapping [B, S] (int64) the outputs go into caller-provided pages:
+    codes_out [P, Hkv, page, nb], pt_out [P, Hkv, page, slots, bd].  Without it, codes_out /
+    pt_out (compact) may be given as [B, Hkv, S, ...] views to write into instead of allocating.
+    metric: SunShape-Pro block metric E [D, D] or per KV head [Hkv, D, D] (fp32); distances are
+    taken between E_b x and E_b c (sunshape/codec.py:375-376).  None = identity.
+    grid: search grid from encode_grid(cent) (block_dim 2, no metric); with it the encode
+    evaluates only each key's certified candidates (same codes).  kernel: 0 auto, 1 exact scan,
+    2 MFMA screen, 3 grid search.
+    Reference: sunshape/codec.py:362-385, sunshape/vllm_attn_backend.py:101-123.
+    """
+    e = _encode_prepare(keys, perm, cent, heavy, pt_dtype, pt_dense, codes_out, pt_out, slot_mapping, metric,
+                        rotation)
+    keys, perm, cent, metric, codes, pt, c_str, p_str = e.keys, e.perm, e.cent, e.metric, e.codes, e.pt, e.c_str, e.p_str
     a = N.EncodeArgs(
         keys=N.ptr(keys), k_dtype=N.dtype_code(keys.dtype), k_sb=keys.stride(0), k_sh=keys.stride(1), k_ss=keys.stride(2),
-        batch=B, num_kv_heads=Hkv, seq_len=S, head_dim=D,
-        perm=N.ptr(perm), perm_sh=perm_sh, cent=N.ptr(cent), cent_sh=cent_sh,
-        metric=N.ptr(metric), metric_sh=metric_sh,
-        block_dim=bd, n_blocks=nb, n_centroids=nc,
+        batch=keys.shape[0], num_kv_heads=keys.shape[1], seq_len=keys.shape[2], head_dim=keys.shape[3],
+        perm=N.ptr(perm), perm_sh=e.perm_sh, cent=N.ptr(cent), cent_sh=e.cent_sh,
+        metric=N.ptr(metric), metric_sh=e.metric_sh,
+        block_dim=e.bd, n_blocks=e.nb, n_centroids=e.nc,
         codes=N.ptr(codes), c_sb=c_str[0], c_sh=c_str[1], c_st=c_str[2],
-        pt=N.ptr(pt), pt_dtype=N.dtype_code(pt_dtype), pt_dense=1 if pt_dense else 0,
+        pt=N.ptr(pt), pt_dtype=N.dtype_code(e.pt_dtype), pt_dense=1 if pt_dense else 0,
         pt_sb=p_str[0], pt_sh=p_str[1], pt_st=p_str[2],
         slot_mapping=N.ptr(slot_mapping), sm_sb=slot_mapping.stride(0) if slot_mapping is not None else 0,
-        page_size=page, kernel=int(kernel), direct_dist=1 if direct else 0,
+        page_size=e.page, kernel=int(kernel), direct_dist=1 if direct else 0,
     )
     if grid is not None and not direct:
         _on_gpu("grid", grid)
         _require(grid.dtype == torch.uint8 and grid.is_contiguous(), "grid must be the uint8 tensor from encode_grid")
         a.grid, a.grid_bytes = N.ptr(grid), grid.numel()
-    a.heavy_mask[0], a.heavy_mask[1] = w0, w1
+    a.heavy_mask[0], a.heavy_mask[1] = e.w0, e.w1
     return a, codes, pt, (keys, perm, cent, metric, grid, slot_mapping)
 
 
@@ -454,11 +450,17 @@ def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
     passthrough values are then the transformed values, as the reference stores them.
     Reference: sunshape/codec.py:362-385, sunshape/vllm_attn_backend.py:101-123.
     """
-    a, codes, pt, _keep = encode_args(keys, perm, cent, heavy=heavy, pt_dtype=pt_dtype, pt_dense=pt_dense,
-                                      codes_out=codes_out, pt_out=pt_out, slot_mapping=slot_mapping, metric=metric,
-                                      kernel=kernel, grid=grid, direct=direct, rotation=rotation)
-    N.check(N.lib().ssq_encode(ctypes.byref(a), N.stream_of(keys.device)))
-    return codes, pt
+    e = _encode_prepare(keys, perm, cent, heavy, pt_dtype, pt_dense, codes_out, pt_out, slot_mapping, metric,
+                        rotation)
+    if grid is not None and not direct:
+        _on_gpu("grid", grid)
+        _require(grid.dtype == torch.uint8 and grid.is_contiguous(), "grid must be the uint8 tensor from encode_grid")
+    try:
+        N.torch_ops().encode_into(e.keys, e.perm, e.cent, N.signed64(e.w0), N.signed64(e.w1), bool(pt_dense), e.codes,
+                                  e.pt, e.slot_mapping, e.metric, None if direct else grid, int(kernel), bool(direct))
+    except RuntimeError as exc:
+        raise N.kernel_error(exc) from None
+    return e.codes, e.pt
 
 
 def encode_grid(cent: torch.Tensor, num_kv_heads: int = 1) -> torch.Tensor:

@@ -1,11 +1,12 @@
-"""The decode operator under graph capture (torch.cuda.graph, i.e. HIP graphs).
+"""The decode and encode operators under graph capture (torch.cuda.graph, i.e. HIP graphs).
 
-torch.ops.sunshape.decode is captured once and the graph replayed several times, with eager work
-and synchronisations between the replays; every replay must equal the eager call bit for bit.
+torch.ops.sunshape.decode (and encode_into, a decode step's append) is captured once and the
+graph replayed several times, with eager work and synchronisations between the replays; every
+replay must equal the eager call bit for bit.
 Covered: a contiguous decode in context splits (the decode kernel and the split merge, two
-kernels) and a paged decode in one kernel.  The operator allocates its outputs and split
-workspace from torch's allocator, which under capture is the graph's private pool, and records
-no memset."""
+kernels), a paged decode in one kernel, and a grid-search append into cache pages.  The operators
+allocate outputs and split workspace from torch's allocator, which under capture is the graph's
+private pool, and record no memset."""
 
 import pytest
 import torch
@@ -58,3 +59,42 @@ def test_paged_decode_replays_from_a_graph():
                               block_table=p["block_table"], seq_lens=p["seq_lens"])
 
     _replays_equal_eager(fn, "config-4 layer B=8")
+
+
+def test_paged_append_replays_from_a_graph():
+    """A decode step's append (encode of one token per sequence into cache pages, grid search),
+    captured once: each replay writes the step's codes and passthrough values into the pages as
+    the eager call does."""
+    log("graph capture: paged append (encode into pages)")
+    p = synthetic.config5(DEV, B=16, S=1)
+    heavy = p["heavy"].tolist()
+    grid = hip_ops.encode_grid(p["centroids"])
+    page, Hkv, nb = 16, 2, 32
+    g = torch.Generator().manual_seed(5)
+    slots = (torch.randperm(64, generator=g)[:16] * page + 3).view(16, 1).to(torch.int64).to(DEV)
+    cpages = torch.zeros(64, Hkv, page, nb, dtype=torch.uint8, device=DEV)
+    ppages = torch.zeros(64, Hkv, page, 4, 2, dtype=torch.bfloat16, device=DEV)
+
+    def append():
+        hip_ops.encode(p["keys"], p["perm"], p["centroids"], heavy=heavy, codes_out=cpages, pt_out=ppages,
+                       slot_mapping=slots, grid=grid)
+
+    append()
+    torch.cuda.synchronize()
+    want_c, want_p = cpages.clone(), ppages.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        append()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        append()
+    for rep in range(3):
+        cpages.zero_()
+        ppages.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(cpages, want_c) and torch.equal(ppages, want_p), f"append replay {rep} differs"
