@@ -69,6 +69,7 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 constexpr int kTile = 64;  // tokens per wave iteration
 constexpr int kD = 64;     // head_dim served
 constexpr int kHP = 16;    // passthrough (heavy-block) dims per token served
+constexpr float kSlack = 8.f;  // online softmax: lag of the running maximum allowed (nats)
 constexpr size_t kMaxSmem = 160 * 1024;
 
 // per-wave LDS region (bytes): V tile [64][Dv] (16-bit) | P strip [16][64] (16-bit).  The scaled
@@ -528,26 +529,28 @@ __global__ __launch_bounds__(contig_waves(DT, HV, MK, R4) * SSQ_WAVE) void k_dec
         }
         if constexpr (!HAS_V) return;
 
-        // ---- online softmax per row over the wave's 64 tokens; rows past nr stay zero
-        float alpha[RP];
-        bool rescale = false;
+        // ---- online softmax per row over the wave's 64 tokens.  The running maximum m_run[r] is
+        // wave-uniform and moves only when some score of the tile exceeds it by more than kSlack,
+        // so most tiles skip the cross-lane maxima and the accumulator rescale; probabilities
+        // exp(s - m_run) then stay below e^kSlack.  Rows past nr come from zero query rows and
+        // are never stored.
+        float sv[RP];
+        bool over = false;
 #pragma unroll
         for (int r = 0; r < RP; ++r) {
-            alpha[r] = 1.f;
-            if (r >= nr) {  // wave-uniform
-                ps[r * kTile + lane] = 0;
-                continue;
-            }
-            const float tm = wave_max64(valid ? s[r] : -INFINITY);
-            const float mn = fmaxf(m_run[r], tm);
-            alpha[r] = (mn == -INFINITY) ? 1.f : __expf(m_run[r] - mn);
-            rescale |= mn != m_run[r];
-            m_run[r] = mn;
-            const float pr = (valid && mn != -INFINITY) ? __expf(s[r] - mn) : 0.f;
-            l_lane[r] = l_lane[r] * alpha[r] + pr;
-            ps[r * kTile + lane] = (uint16_t)to_vt16<VT>(pr);
+            sv[r] = valid ? s[r] : -INFINITY;
+            over |= sv[r] > m_run[r] + kSlack;
         }
-        if (rescale) {  // wave-uniform; accumulator row 4 g + i lives in lane group g = lane / 16
+        if (__builtin_amdgcn_ballot_w64(over) != 0) {  // wave-uniform
+            float alpha[RP];
+#pragma unroll
+            for (int r = 0; r < RP; ++r) {
+                const float mn = fmaxf(m_run[r], wave_max64(sv[r]));
+                alpha[r] = mn == -INFINITY ? 1.f : __expf(m_run[r] - mn);
+                l_lane[r] *= alpha[r];
+                m_run[r] = mn;
+            }
+            // accumulator row 4 g + i lives in lane group g = lane / 16
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 float f = 1.f;
@@ -557,6 +560,14 @@ __global__ __launch_bounds__(contig_waves(DT, HV, MK, R4) * SSQ_WAVE) void k_dec
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) acc[dt][i] *= f;
             }
+        }
+#pragma unroll
+        for (int r = 0; r < RP; ++r) {
+            // m_run is -inf only while every score seen is -inf (then p = exp(-inf) = 0)
+            const float mr = m_run[r] == -INFINITY ? 0.f : m_run[r];
+            const float pr = __expf(sv[r] - mr);
+            l_lane[r] += pr;
+            ps[r * kTile + lane] = (uint16_t)to_vt16<VT>(pr);
         }
         wave_sync();
 

@@ -399,6 +399,35 @@ def test_contiguous_mfma_kernel_edge_lengths(T, splits):
         assert_rel(og, ro, BF16_TOL, f"LUT kernel mask={m is not None}")
 
 
+@pytest.mark.parametrize("pattern,splits", [("rising", 1), ("falling", 1), ("step", 1), ("step", 3), ("wide", 1),
+                                            ("wide", 0)])
+def test_contiguous_running_max_patterns(pattern, splits):
+    """The contiguous kernel's running maximum may lag the true one by a slack and is raised only
+    when a score exceeds it by more.  Scores that rise across the context (raised again and
+    again), fall (set by the first tiles), jump by 40 halfway, or spread wide (scale 3, no mask)
+    must all match the oracle."""
+    log(f"contig running max {pattern} splits={splits}")
+    B, Hkv, Hq, Lq, D, bd, T = 2, 2, 8, 1, 64, 2, 3000
+    cb = synthetic.make_codebook(Hkv, D, bd, 131)
+    g = torch.Generator().manual_seed(132)
+    q = torch.randn(B, Hq, Lq, D, generator=g).to(torch.bfloat16)
+    codes = torch.randint(0, 256, (B, Hkv, T, D // bd), generator=g, dtype=torch.uint8)
+    v = torch.randn(B, Hkv, T, 64, generator=g).to(torch.bfloat16)
+    t = torch.arange(T, dtype=torch.float32)
+    bias = {"rising": 0.03 * t, "falling": -0.03 * t, "step": torch.where(t >= T // 2, 40.0, 0.0),
+            "wide": None}[pattern]
+    mask = None if bias is None else bias.expand(B, Hq, Lq, T).contiguous()
+    scale = 3.0 if pattern == "wide" else 1 / math.sqrt(D)
+    args = (q.to(DEV), codes.to(DEV), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+    out, lse = hip_ops.decode(*args, scale=scale, mask=None if mask is None else mask.to(DEV), return_lse=True,
+                              kernel=3, num_splits=splits)
+    ro, _, rl = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
+                                   cb.perm.numpy(), scale, "bf16", "bf16", mask=None if mask is None else mask.numpy(),
+                                   return_scores=True)
+    assert_rel(np_of(out), ro, BF16_TOL, f"out {pattern}")
+    assert_rel(np_of(lse), rl, SCORE_TOL, f"lse {pattern}")
+
+
 def test_contiguous_mfma_kernel_rejects_wide_passthrough():
     """More than 16 passthrough dims do not fit the kernel's passthrough pass: an explicit
     kernel 3 request is refused, and auto dispatch serves the call on the LUT kernel."""
