@@ -562,85 +562,86 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
 }
 
 // Combine split partials: out = sum_s o_s e^{m_s-M} / sum_s l_s e^{m_s-M}, lse = M + log L.
-// One workgroup per query row.  M and L are reduced over the splits by the whole workgroup (its
-// loads side by side, not one latency per split); the split weights e^{m_s-M} go to LDS in chunks,
-// and each thread sums its value dims over a chunk with 8 independent loads in flight.
-constexpr int kMergeThreads = 128;
-constexpr int kMergeChunk = 256;
+// One wave per query row, kMergeRows rows per workgroup.  Lane j merges value dims j, j + 64, ...;
+// every lane loads the row's (m_s, l_s) and its dims' o_s for up to kMergeSplits splits before
+// using any of them, so a merge of that many splits costs one memory round trip (more splits take
+// further passes, merged online).  No LDS and no workgroup barrier.
+constexpr int kMergeRows = 4;
+constexpr int kMergeSplits = 16;
+constexpr int kMergeDims = 4;  // value dims per lane per pass: 256 per wave
 
-__device__ __forceinline__ float merge_block_reduce(float v, bool is_max, float* red) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float w = __shfl_xor(v, o);
-        v = is_max ? fmaxf(v, w) : v + w;
-    }
-    __syncthreads();  // red may still be read from the previous reduction
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return is_max ? fmaxf(red[0], red[1]) : red[0] + red[1];
-}
-
-__global__ __launch_bounds__(kMergeThreads) void k_merge(const ssq_decode_args a, int n_splits, const float* ws_o,
-                                                         const float* ws_m, const float* ws_l) {
-    __shared__ float wt[kMergeChunk];
-    __shared__ float red[2];
-    const int rid = blockIdx.x;
-    const int tid = threadIdx.x;
+__global__ __launch_bounds__(kMergeRows * SSQ_WAVE) void k_merge(const ssq_decode_args a, int n_splits,
+                                                                  const float* ws_o, const float* ws_m,
+                                                                  const float* ws_l) {
+    const int lane = threadIdx.x & (SSQ_WAVE - 1);
     const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
+    const int rid = blockIdx.x * kMergeRows + (int)(threadIdx.x / SSQ_WAVE);
+    if (rid >= n_rows_all) return;  // whole waves
     const int qi = rid % a.q_len;
     const int h = (rid / a.q_len) % a.num_q_heads;
     const int b = rid / (a.q_len * a.num_q_heads);
-    float M = -INFINITY;
-    for (int s = tid; s < n_splits; s += kMergeThreads) M = fmaxf(M, ws_m[(size_t)s * n_rows_all + rid]);
-    M = merge_block_reduce(M, true, red);
-    float L = 0.f;
-    for (int s = tid; s < n_splits; s += kMergeThreads) {
-        const float ms = ws_m[(size_t)s * n_rows_all + rid];
-        if (ms != -INFINITY) L += ws_l[(size_t)s * n_rows_all + rid] * __expf(ms - M);
-    }
-    L = merge_block_reduce(L, false, red);
     const int Dv = a.value_dim;
-    constexpr int kDvPer = 2;  // value dims per thread (Dv <= 256); more take further passes
-    for (int d0 = 0; d0 < Dv; d0 += kDvPer * kMergeThreads) {
-        float o[kDvPer];
+    const size_t mstep = (size_t)n_rows_all;       // between splits in ws_m / ws_l
+    const size_t ostep = (size_t)n_rows_all * Dv;  // between splits in ws_o
+    float M = -INFINITY, L = 0.f;
+    for (int d0 = 0; d0 < Dv; d0 += kMergeDims * SSQ_WAVE) {
+        float Mr = -INFINITY, Lr = 0.f;
+        float o[kMergeDims];
 #pragma unroll
-        for (int k = 0; k < kDvPer; ++k) o[k] = 0.f;
-        for (int c0 = 0; c0 < n_splits; c0 += kMergeChunk) {
-            const int nch = min(kMergeChunk, n_splits - c0);
-            __syncthreads();
-            for (int i = tid; i < nch; i += kMergeThreads) {
-                const float ms = ws_m[(size_t)(c0 + i) * n_rows_all + rid];
-                wt[i] = ms != -INFINITY ? __expf(ms - M) : 0.f;
-            }
-            __syncthreads();
+        for (int k = 0; k < kMergeDims; ++k) o[k] = 0.f;
+        for (int c0 = 0; c0 < n_splits; c0 += kMergeSplits) {
+            float mv[kMergeSplits], lv[kMergeSplits], ov[kMergeSplits][kMergeDims];
 #pragma unroll
-            for (int k = 0; k < kDvPer; ++k) {
-                const int dv = d0 + k * kMergeThreads + tid;
-                if (dv >= Dv) continue;
-                const float* src = ws_o + ((size_t)c0 * n_rows_all + rid) * Dv + dv;
-                const size_t step = (size_t)n_rows_all * Dv;
-                float acc = o[k];
-                int i = 0;
-                for (; i + 8 <= nch; i += 8) {
-                    float x[8];
+            for (int i = 0; i < kMergeSplits; ++i) {
+                mv[i] = -INFINITY;
+                lv[i] = 0.f;
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) x[u] = src[(size_t)(i + u) * step];
+                for (int k = 0; k < kMergeDims; ++k) ov[i][k] = 0.f;
+                if (c0 + i < n_splits) {  // uniform
+                    const size_t s = (size_t)(c0 + i);
+                    mv[i] = ws_m[s * mstep + rid];
+                    lv[i] = ws_l[s * mstep + rid];
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) acc += x[u] * wt[i + u];
+                    for (int k = 0; k < kMergeDims; ++k)
+                        if (d0 + k * SSQ_WAVE < Dv)  // uniform; the lane's dim is clamped
+                            ov[i][k] = ws_o[s * ostep + (size_t)rid * Dv + min(d0 + k * SSQ_WAVE + lane, Dv - 1)];
                 }
-                for (; i < nch; ++i) acc += src[(size_t)i * step] * wt[i];
-                o[k] = acc;
             }
+            float Mc = Mr;
+#pragma unroll
+            for (int i = 0; i < kMergeSplits; ++i) Mc = fmaxf(Mc, mv[i]);
+            const float f = Mr == -INFINITY ? 0.f : __expf(Mr - Mc);  // earlier passes, rescaled
+            Lr *= f;
+#pragma unroll
+            for (int k = 0; k < kMergeDims; ++k) o[k] *= f;
+#pragma unroll
+            for (int i = 0; i < kMergeSplits; ++i) {
+                const float w = mv[i] == -INFINITY ? 0.f : __expf(mv[i] - Mc);
+                Lr += lv[i] * w;
+#pragma unroll
+                for (int k = 0; k < kMergeDims; ++k) o[k] += ov[i][k] * w;
+            }
+            Mr = Mc;
         }
 #pragma unroll
-        for (int k = 0; k < kDvPer; ++k) {
-            const int dv = d0 + k * kMergeThreads + tid;
+        for (int k = 0; k < kMergeDims; ++k) {
+            const int dv = d0 + k * SSQ_WAVE + lane;
             if (dv < Dv)
                 ssq_store_elem(a.out, a.v_dtype, (int64_t)b * a.o_sb + (int64_t)h * a.o_sh + (int64_t)qi * a.o_sl + dv,
-                               o[k] / L);
+                               o[k] / Lr);
         }
+        M = Mr;
+        L = Lr;
     }
-    if (a.lse && tid == 0) a.lse[rid] = M + logf(L);
+    if (a.lse && lane == 0) a.lse[rid] = M + logf(L);
+}
+
+static int launch_merge(const ssq_decode_args& a, int n_splits, const float* ws_o, const float* ws_m,
+                        const float* ws_l, hipStream_t st) {
+    const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
+    hipLaunchKernelGGL(k_merge, dim3((unsigned)((n_rows_all + kMergeRows - 1) / kMergeRows)),
+                       dim3(kMergeRows * SSQ_WAVE), 0, st, a, n_splits, ws_o, ws_m, ws_l);
+    return ssq_check_hip(hipGetLastError(), "k_merge launch");
 }
 
 // --------------------------------------------------------------------------
@@ -802,9 +803,7 @@ int run_generic(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipS
     }
     if (rc) return rc;
     if (pl.has_v && pl.n_splits > 1) {
-        hipLaunchKernelGGL(k_merge, dim3((unsigned)n_rows_all), dim3(kMergeThreads), 0, st, *a, pl.n_splits, dp.ws_o, dp.ws_m,
-                           dp.ws_l);
-        rc = ssq_check_hip(hipGetLastError(), "k_merge launch");
+        rc = launch_merge(*a, pl.n_splits, dp.ws_o, dp.ws_m, dp.ws_l, st);
     }
     return rc;
 }
@@ -814,9 +813,7 @@ int run_generic(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipS
 // Launches the split merge (shared with the MFMA decode kernel).
 int ssq_launch_merge(const ssq_decode_args& a, int n_splits, const float* ws_o, const float* ws_m,
                      const float* ws_l, hipStream_t st) {
-    const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
-    hipLaunchKernelGGL(k_merge, dim3((unsigned)n_rows_all), dim3(kMergeThreads), 0, st, a, n_splits, ws_o, ws_m, ws_l);
-    return ssq_check_hip(hipGetLastError(), "k_merge launch");
+    return launch_merge(a, n_splits, ws_o, ws_m, ws_l, st);
 }
 
 int ssq_decode_mfma_supported(const ssq_decode_args* a);

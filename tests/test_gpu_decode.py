@@ -62,9 +62,10 @@ def test_decode_split_counts_agree():
     p = synthetic.config3(DEV, B=2, T=4096)
     v32 = p["v"].float()
     outs = [np_of(hip_ops.decode(p["q"], p["codes"], v32, p["perm"], p["centroids"], scale=p.meta["scale"], num_splits=s))
-            for s in (1, 3, 16)]
+            for s in (1, 3, 16, 40)]
     assert_rel(outs[1], outs[0], 1e-5, "3 vs 1 splits")
     assert_rel(outs[2], outs[0], 1e-5, "16 vs 1 splits")
+    assert_rel(outs[3], outs[0], 1e-5, "40 vs 1 splits")  # the merge takes several passes
 
 
 @pytest.mark.parametrize("vdt", [torch.float16, torch.float32])
