@@ -197,7 +197,7 @@ int ssq_encode(const ssq_encode_args* a, void* stream);
  * and 2 bit for bit.  Layout, head-major: per codebook head, its block headers (32 bytes each,
  * padded to 256) then its cells (32 bytes each), so head h's bytes [h * size / heads,
  * (h + 1) * size / heads) of a per-KV-head grid are the grid of that head's codebook alone.
- * Size per head and block: 0.5 MiB.
+ * Size per head and block: 0.5 MiB.  The grid buffer must be 16-byte aligned.
  * The grid depends only on perm-independent codebook values (cent, cent_sh, n_blocks,
  * n_centroids, num_kv_heads when cent_sh != 0); rebuild it when the codebook changes.  Each
  * block's header holds a fingerprint of its codebook: ssq_encode scans every codeword of a

@@ -199,7 +199,7 @@ struct GridParams {
 // LDS layout (bytes): cb [nl][256] float2 | cn [nl][256] float | hd [nl] float4 | poff [nl][4] int |
 // codes [waves][64][nb]
 inline size_t grid_smem(int nl, int nb, int waves) {
-    return (size_t)nl * 256 * 12 + (size_t)nl * 16 + (size_t)nl * 16 + (size_t)waves * 64 * nb;
+    return (size_t)nl * 256 * 12 + (size_t)nl * 16 + (size_t)nl * 16 + (size_t)nb * 16 + (size_t)waves * 64 * nb;
 }
 
 struct Cand {  // running first minimum of sqrt(max(d2, 0)) over ascending codeword indices
@@ -280,8 +280,48 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
     float* cn = reinterpret_cast<float*>(cb + nl * 256);                   // [nl][256]
     float4* hd = reinterpret_cast<float4*>(cn + nl * 256);                 // [nl]: lo0, lo1, inv_h0, inv_h1
     int* poff = reinterpret_cast<int*>(hd + nl);                           // [nl]: perm0, perm1, block id, 0
-    uint8_t* cs = reinterpret_cast<uint8_t*>(poff + 4 * nl) + wave * 64 * nb;  // this wave's code rows
+    // [heavy blocks]: the block's two dims in the key row, its id, its passthrough slot (chunk 0)
+    int4* hinfo = reinterpret_cast<int4*>(poff + 4 * nl);
+    uint8_t* cs = reinterpret_cast<uint8_t*>(hinfo + nb) + wave * 64 * nb;  // this wave's code rows
 
+    const int keys_wg = waves * 64;
+    const int key = blockIdx.x * keys_wg + wave * 64 + lane;  // this lane's key index
+    const bool live = key < km.n_keys;
+    const int64_t krow = km.krow(a, live ? key : km.n_keys - 1);
+    // this lane's key's output rows (code row, passthrough row), resolved before the staging so
+    // that a slot-mapping load is not a round trip at the end
+    int64_t crow_k, prow_k;
+    {
+        int b, ss;
+        km.bs(a, live ? key : km.n_keys - 1, b, ss);
+        if (a.slot_mapping) {
+            const int64_t slot = a.slot_mapping[(int64_t)b * a.sm_sb + ss];
+            const int64_t page = slot / a.page_size, off = slot - page * a.page_size;
+            crow_k = page * a.c_sb + (int64_t)kv * a.c_sh + off * a.c_st;
+            prow_k = page * a.pt_sb + (int64_t)kv * a.pt_sh + off * a.pt_st;
+        } else {
+            crow_k = (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)ss * a.c_st;
+            prow_k = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)ss * a.pt_st;
+        }
+    }
+
+    const int kdt = a.k_dtype;
+    // ---- the key's permuted elements, issued before the staging below (they do not depend on
+    // it; issued after its barrier they would add a memory round trip to the chain).  ROWREG: the
+    // whole row (at most 128 bytes, 16-byte aligned) is loaded once with 16-byte loads into
+    // registers, and each block's two elements are picked out by a wave-uniform register index:
+    // one memory access per 16 bytes of key instead of one per element.  Otherwise each element
+    // is a load of its own, issued one block ahead of its use.
+    uint32_t row[32];
+    if constexpr (ROWREG) {
+        const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.keys) +
+                                                          krow * (kdt == SSQ_F32 ? 4 : 2));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint4 v = i < p.row_q ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+            row[4 * i] = v.x; row[4 * i + 1] = v.y; row[4 * i + 2] = v.z; row[4 * i + 3] = v.w;
+        }
+    }
     // ---- stage the light blocks, one wave per block: codewords, |c|^2 (rounded squares summed
     // left to right), the header, and the codebook fingerprint check (a grid built for another
     // codebook leaves the block without cells: every key scans all codewords)
@@ -290,9 +330,14 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
     for (int li = wave; li < nl; li += waves) {
         const int blk = p.light[l0 + li];
         const float* c = cent + (int64_t)blk * nc * 2;
+        // every load of the block first (codewords, header, permutation entries), then arithmetic
+        const float4* h4 = reinterpret_cast<const float4*>(p.grid + (size_t)hsel * grid_head_bytes(nb)) +
+                           (int64_t)blk * (kHdr / 4);
+        const float4 hA = h4[0], hB = h4[1];  // mid0, mid1, inv0, inv1 | Rc, valid, fingerprint, -
+        const int64_t pe0 = perm[blk * 2], pe1 = perm[blk * 2 + 1];
         float v0[4], v1[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {  // loads first, then arithmetic
+        for (int q = 0; q < 4; ++q) {
             const int j = lane + 64 * q;
             v0[q] = j < nc ? c[2 * j] : 0.f;
             v1[q] = j < nc ? c[2 * j + 1] : 0.f;
@@ -311,13 +356,21 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) f ^= __shfl_xor(f, o);
         if (lane == 0) {
-            const float* h = reinterpret_cast<const float*>(p.grid + (size_t)hsel * grid_head_bytes(nb)) + (int64_t)blk * kHdr;
-            const bool ok = h[5] != 0.f && (f ^ cw_count_mix(nc)) == __float_as_uint(h[6]);
-            hd[li] = ok ? make_float4(h[0], h[1], h[2], h[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
-            poff[4 * li] = (int)perm[blk * 2];
-            poff[4 * li + 1] = (int)perm[blk * 2 + 1];
+            const bool ok = hB.y != 0.f && (f ^ cw_count_mix(nc)) == __float_as_uint(hB.z);
+            hd[li] = ok ? hA : make_float4(0.f, 0.f, 0.f, 0.f);
+            poff[4 * li] = (int)pe0;
+            poff[4 * li + 1] = (int)pe1;
             poff[4 * li + 2] = blk;  // kept in LDS: a kernel-argument array indexed in the loop
             poff[4 * li + 3] = 0;    // would be a memory load that waits for every pending load
+        }
+    }
+    if (blockIdx.z == 0 && (a.heavy_mask[0] | a.heavy_mask[1])) {  // chunk 0 copies the heavy blocks
+        const uint64_t h0 = a.heavy_mask[0], h1 = a.heavy_mask[1];
+        for (int blk = threadIdx.x; blk < nb; blk += blockDim.x) {
+            if (!ssq_is_heavy(h0, h1, blk)) continue;
+            const int h = blk < 64 ? __popcll(h0 & ((1ull << blk) - 1ull))  // heavy blocks before blk
+                                   : __popcll(h0) + __popcll(h1 & ((1ull << (blk - 64)) - 1ull));
+            hinfo[h] = make_int4((int)perm[2 * blk], (int)perm[2 * blk + 1], blk, a.pt_dense ? blk : h);
         }
     }
     for (int i = lane; i < 16 * nb; i += 64) reinterpret_cast<uint32_t*>(cs)[i] = 0u;  // heavy blocks: code 0
@@ -325,27 +378,6 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
 
     const uint64_t hm0 = a.heavy_mask[0], hm1 = a.heavy_mask[1];
     const uint8_t* cells = p.grid + (size_t)hsel * grid_head_bytes(nb) + grid_head_hdr_bytes(nb);
-    const int keys_wg = waves * 64;
-    const int key = blockIdx.x * keys_wg + wave * 64 + lane;  // this lane's key index
-    const bool live = key < km.n_keys;
-    const int64_t krow = km.krow(a, live ? key : km.n_keys - 1);
-
-    const int kdt = a.k_dtype;
-    // ---- the key's permuted elements.  ROWREG: the whole row (at most 128 bytes, 16-byte
-    // aligned) is loaded once with 16-byte loads into registers, and each block's two elements
-    // are picked out by a wave-uniform register index: one memory access per 16 bytes of key
-    // instead of one per element.  Otherwise each element is a load of its own, issued one
-    // block ahead of its use.
-    uint32_t row[32];
-    if constexpr (ROWREG) {
-        const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.keys) +
-                                                          krow * (kdt == SSQ_F32 ? 4 : 2));
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint4 v = i < p.row_q ? src[i] : make_uint4(0u, 0u, 0u, 0u);
-            row[4 * i] = v.x; row[4 * i + 1] = v.y; row[4 * i + 2] = v.z; row[4 * i + 3] = v.w;
-        }
-    }
     // element e (wave-uniform) of the register row, as raw bits
     auto row_bits = [&](int e) -> uint32_t {
         if (kdt == SSQ_F32) return row[e & 31];
@@ -524,57 +556,71 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    auto out_rows = [&](int i, int64_t& crow, int64_t& prow) {  // key index i's output rows
-        int b, ss;
-        km.bs(a, i, b, ss);
-        if (a.slot_mapping) {
-            const int64_t slot = a.slot_mapping[(int64_t)b * a.sm_sb + ss];
-            const int64_t page = slot / a.page_size, off = slot - page * a.page_size;
-            crow = page * a.c_sb + (int64_t)kv * a.c_sh + off * a.c_st;
-            prow = page * a.pt_sb + (int64_t)kv * a.pt_sh + off * a.pt_st;
-        } else {
-            crow = (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)ss * a.c_st;
-            prow = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)ss * a.pt_st;
-        }
-    };
     const int s_wave = blockIdx.x * keys_wg + wave * 64;
     if (p.row_codes) {
         const int pieces = nb >> 4;
         for (int e = lane; e < 64 * pieces; e += 64) {
             const int m = e / pieces, q = e - m * pieces;
             const int i = s_wave + m;
+            // key m's code row, from lane m
+            const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)crow_k, m);
+            const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)crow_k >> 32), m);
+            const int64_t crow = (int64_t)(((uint64_t)hi << 32) | lo);
             if (i < km.n_keys) {
-                int64_t crow, prow;
-                out_rows(i, crow, prow);
                 const uint32_t* src = reinterpret_cast<const uint32_t*>(cs + m * nb + 16 * q);
                 *reinterpret_cast<uint4*>(a.codes + crow + 16 * q) = make_uint4(src[0], src[1], src[2], src[3]);
             }
         }
     } else if (live && gridDim.z == 1) {  // every block's code (heavy blocks' 0 included)
-        int64_t crow, prow;
-        out_rows(key, crow, prow);
+        const int64_t crow = crow_k;
         for (int blk = 0; blk < nb; ++blk) a.codes[crow + blk] = cs[lane * nb + blk];
     } else if (live) {  // one chunk of several: its blocks' codes; chunk 0 also the heavy blocks' 0
-        int64_t crow, prow;
-        out_rows(key, crow, prow);
+        const int64_t crow = crow_k;
         for (int li = 0; li < nl; ++li) {
             const int blk = __builtin_amdgcn_readfirstlane(poff[4 * li + 2]);
             a.codes[crow + blk] = cs[lane * nb + blk];
         }
-        if (blockIdx.z == 0)
-            for (int blk = 0; blk < nb; ++blk)
-                if (ssq_is_heavy(hm0, hm1, blk)) a.codes[crow + blk] = 0;
     }
+    // chunk 0: the heavy blocks' values as the key holds them, and (with several chunks, whose
+    // stores are per block) their code 0.  One pass over the heavy blocks listed in LDS, the
+    // stored dtype's branch taken once.
     if ((hm0 | hm1) && live && blockIdx.z == 0) {
-        int64_t crow, prow;
-        out_rows(key, crow, prow);
-        for (int blk = 0, hh = 0; blk < nb; ++blk) {
-            if (!ssq_is_heavy(hm0, hm1, blk)) continue;
-            const int slot = a.pt_dense ? blk : hh;
-            ++hh;
-            for (int d = 0; d < 2; ++d)
-                ssq_store_elem(a.pt, a.pt_dtype, prow + (int64_t)slot * 2 + d,
-                               ssq_load_elem(a.keys, a.k_dtype, krow + perm[blk * 2 + d]));
+        const int nh = __popcll(hm0) + __popcll(hm1);
+        const bool zero_codes = gridDim.z > 1;
+        auto heavy_pair = [&](int h, int& blk, int& slot, float& x0, float& x1) {
+            const int4 hi = hinfo[h];
+            const int e0 = __builtin_amdgcn_readfirstlane(hi.x), e1 = __builtin_amdgcn_readfirstlane(hi.y);
+            blk = __builtin_amdgcn_readfirstlane(hi.z);
+            slot = __builtin_amdgcn_readfirstlane(hi.w);
+            if constexpr (ROWREG) {
+                x0 = ssq_bits_to_f32(row_bits(e0), kdt);
+                x1 = ssq_bits_to_f32(row_bits(e1), kdt);
+            } else {
+                x0 = ssq_load_elem(a.keys, kdt, krow + e0);
+                x1 = ssq_load_elem(a.keys, kdt, krow + e1);
+            }
+        };
+        if (a.pt_dtype == SSQ_F32) {
+            float* dst = reinterpret_cast<float*>(a.pt) + prow_k;
+            for (int h = 0; h < nh; ++h) {
+                int blk, slot;
+                float x0, x1;
+                heavy_pair(h, blk, slot, x0, x1);
+                if (zero_codes) a.codes[crow_k + blk] = 0;
+                dst[2 * slot] = x0;
+                dst[2 * slot + 1] = x1;
+            }
+        } else {
+            const bool bf = a.pt_dtype == SSQ_BF16;
+            uint16_t* dst = reinterpret_cast<uint16_t*>(a.pt) + prow_k;
+            for (int h = 0; h < nh; ++h) {
+                int blk, slot;
+                float x0, x1;
+                heavy_pair(h, blk, slot, x0, x1);
+                if (zero_codes) a.codes[crow_k + blk] = 0;
+                dst[2 * slot] = (uint16_t)(bf ? ssq_f32_to_bf16(x0) : ssq_f32_to_f16(x0));
+                dst[2 * slot + 1] = (uint16_t)(bf ? ssq_f32_to_bf16(x1) : ssq_f32_to_f16(x1));
+            }
         }
     }
 }
@@ -601,6 +647,7 @@ extern "C" int ssq_encode_grid_build(const ssq_encode_args* a, void* grid, uint6
     if (a->struct_size != sizeof(ssq_encode_args))
         return ssq_fail(SSQ_ERR_ABI, "ssq_encode_args size %u != library's %zu", a->struct_size, sizeof(ssq_encode_args));
     SSQ_REQUIRE(a->cent && grid, "cent and grid must be non-NULL");
+    SSQ_REQUIRE((uintptr_t)grid % 16 == 0, "the grid must be 16-byte aligned");
     SSQ_REQUIRE(a->n_blocks >= 1 && a->num_kv_heads >= 1, "bad n_blocks/num_kv_heads");
     SSQ_UNSUPPORTED(ssq_encode_grid_supported(a), "the encode grid serves block_dim 2 without a block metric");
     SSQ_REQUIRE(grid_bytes >= grid_total_bytes(*a), "grid buffer too small (%llu < %zu bytes)",
@@ -621,6 +668,7 @@ extern "C" int ssq_encode_grid_build(const ssq_encode_args* a, void* grid, uint6
 int ssq_encode_grid_run(const ssq_encode_args* a, hipStream_t st) {
     SSQ_UNSUPPORTED(ssq_encode_grid_supported(a), "the grid encode serves block_dim 2 without a block metric");
     SSQ_REQUIRE(a->grid, "the grid encode needs a grid from ssq_encode_grid_build");
+    SSQ_REQUIRE((uintptr_t)a->grid % 16 == 0, "the grid must be 16-byte aligned");
     SSQ_REQUIRE(a->grid_bytes >= grid_total_bytes(*a), "grid too small for this codebook (%llu < %zu bytes)",
                 (unsigned long long)a->grid_bytes, grid_total_bytes(*a));
     GridParams gp;

@@ -308,11 +308,12 @@ def test_grid_encode_constructed_ties_duplicates_and_heavy():
     ref, rpt = O.encode(keys, perm, cent, heavy)
     k = torch.from_numpy(keys).to(DEV)[None, None]
     for dense in (True, False):
-        codes, pt = hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, heavy=heavy.tolist(), pt_dtype=torch.float32,
-                                   pt_dense=dense, kernel=3, grid=grid)
-        assert np.array_equal(np_of(codes[0, 0]), ref)
-        want = rpt if dense else rpt[:, heavy]
-        assert np.array_equal(np_of(pt[0, 0]), want)
+        for pdt in (torch.float32, torch.float16, torch.bfloat16):
+            codes, pt = hip_ops.encode(k, torch.from_numpy(perm).to(DEV), c, heavy=heavy.tolist(), pt_dtype=pdt,
+                                       pt_dense=dense, kernel=3, grid=grid)
+            assert np.array_equal(np_of(codes[0, 0]), ref)
+            want = torch.from_numpy(rpt if dense else rpt[:, heavy]).to(pdt)  # the stored dtype's rounding
+            assert torch.equal(pt[0, 0].cpu(), want), (dense, pdt)
 
 
 @pytest.mark.parametrize("kernel,bd,B,S", [(1, 4, 64, 1), (2, 4, 64, 1), (2, 4, 5, 300), (1, 2, 33, 3),
