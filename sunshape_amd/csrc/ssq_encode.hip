@@ -483,103 +483,156 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
 
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
     const int64_t* perm_g = a.perm + (int64_t)kv * a.perm_sh;
-    for (int j = threadIdx.x; j < D; j += kMfmaWaves * SSQ_WAVE) perm_l[j] = (int)perm_g[j];
-    for (int j = threadIdx.x; j < nbc * bd; j += kMfmaWaves * SSQ_WAVE) {
-        const int bl = j / bd, d = j - bl * bd;
-        poff[j] = (int)perm_g[p.light[l0 + bl] * bd + d];
-    }
-    for (int bl = threadIdx.x; bl < nbc; bl += kMfmaWaves * SSQ_WAVE) lightL[bl] = p.light[l0 + bl];
+    // key rows: lane (m = l/4, quarter q = l%4) loads elements [q*D/4, (q+1)*D/4) of row m, as
+    // D/32 16-byte loads (16-bit keys, D = 64 or 128), prefetched one round ahead
+    const int esz = a.k_dtype == SSQ_F32 ? 4 : 2;
+    const bool vec = (D == 64 || D == 128) && ((a.k_ss * esz) % 16 == 0) && ((a.k_sh * esz) % 16 == 0) &&
+                     ((a.k_sb * esz) % 16 == 0) && ((uintptr_t)a.keys % 16 == 0) && esz == 2;
+    const int nq = D / 32;  // 16-byte pieces per lane on the vector path
+    const int lm = lane >> 2, lq = lane & 3;
+    const int s_wg = blockIdx.x * (kMfmaWaves * kRounds * 16);  // first key index of the workgroup
+    constexpr int kPre = 4;
+    uint4 pre[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) pre[i] = make_uint4(0, 0, 0, 0);
+    auto fetch = [&](int round) {
+        const int s = s_wg + (round * kMfmaWaves + wave) * 16 + lm;
+        if (vec && s < n_keys) {
+            const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.keys) +
+                                                              km.krow(a, s) + lq * (D / 4));
+#pragma unroll
+            for (int i = 0; i < kPre; ++i)
+                if (i < nq) pre[i] = src[i];  // wave-uniform
+        }
+    };
+    fetch(0);
+
+    // Prologue loads, all in flight together before any is used: the key rows above, the
+    // permutation (up to 4 entries per thread), and the first pass of codeword rows (r0 + u kThr
+    // + tid of the chunk; a wave's 64 rows lie in one block, whose id is a wave-uniform kernel
+    // argument; rows past the end re-read the last one).
+    constexpr int kThr = kMfmaWaves * SSQ_WAVE;
+    static_assert(kThr % 256 == 0, "codeword passes of whole blocks");
+    const int tid = threadIdx.x;
+    constexpr int kPv = 4;
+    int pv[kPv];
+#pragma unroll
+    for (int k = 0; k < kPv; ++k) pv[k] = tid + k * kThr < D ? (int)perm_g[tid + k * kThr] : 0;
+    constexpr int kCB = 4 * KS - 2;  // >= bd
+    constexpr int kRB = 8;
+    const int n_rows = nbc * 256;
+    float cv[kRB][kCB];
+    auto cb_load = [&](int r0) {
+#pragma unroll
+        for (int u = 0; u < kRB; ++u) {
+            const int rw = r0 + u * kThr + wave * SSQ_WAVE;  // the wave's first row
+            const int bl = min(rw >> 8, nbc - 1);
+            const int r = min(rw + lane, n_rows - 1);
+            const float* c = cent + ((int64_t)p.light[l0 + bl] * 256 + (r & 255)) * bd;
+#pragma unroll
+            for (int d = 0; d < kCB; ++d) cv[u][d] = c[min(d, bd - 1)];
+        }
+    };
+    if (n_rows > 0) cb_load(0);
+
+#pragma unroll
+    for (int k = 0; k < kPv; ++k)
+        if (tid + k * kThr < D) perm_l[tid + k * kThr] = pv[k];
+    for (int j = tid + kPv * kThr; j < D; j += kThr) perm_l[j] = (int)perm_g[j];  // D > 4 kThr
+    for (int bl = tid; bl < nbc; bl += kThr) lightL[bl] = p.light[l0 + bl];
     if (MET) {
         const float* met = a.metric + (int64_t)kv * a.metric_sh;
-        for (int j = threadIdx.x; j < nbc * bd * bd; j += kMfmaWaves * SSQ_WAVE) {
+        for (int j = tid; j < nbc * bd * bd; j += kThr) {
             const int bl = j / (bd * bd), r = j - bl * bd * bd;
             const int k = r / bd, jj = r - k * bd;
             const int blk = p.light[l0 + bl];
             em[j] = met[(int64_t)(blk * bd + k) * D + blk * bd + jj];
         }
+        __syncthreads();  // em is read by the codeword transform
+    }
+    // B operands in lane order: bsw[bl][s][nt][l] = [c, 1, |c|^2, 0..][k = 4s + l/16] of codeword 16nt + l%16
+    // (with a block metric, c' = E_b c in place of c).  One codeword row per thread per pass.
+    for (int r0 = 0; r0 < n_rows; r0 += kRB * kThr) {
+        if (r0 > 0) cb_load(r0);
+#pragma unroll
+        for (int u = 0; u < kRB; ++u) {
+            const int r = r0 + u * kThr + tid;
+            if (r >= n_rows) break;
+            const int bl = r >> 8, j = r & 255;
+            float cp[kCB];
+#pragma unroll
+            for (int d = 0; d < kCB; ++d) cp[d] = cv[u][d];
+            if (MET) {
+#pragma unroll
+                for (int k = 0; k < kCB; ++k)
+                    if (k < bd) cp[k] = metric_row_n(em + (bl * bd + k) * bd, cv[u], bd);
+            }
+            const float cn = sq_norm_n(cp, bd);
+            float* dst = bsw + (size_t)bl * KS * 1024 + (j >> 4) * 64 + (j & 15);
+#pragma unroll
+            for (int k = 0; k < 4 * KS; ++k)
+                dst[(k >> 2) * 1024 + (k & 3) * 16] = k < bd ? cp[k] : k == bd ? 1.0f : k == bd + 1 ? cn : 0.0f;
+        }
     }
     __syncthreads();
-    // B operands in lane order: bsw[bl][s][nt][l] = [c, 1, |c|^2, 0..][k = 4s + l/16] of codeword 16nt + l%16
-    // (with a block metric, c' = E_b c in place of c).  One codeword row per thread per pass, the
-    // loads of a pass's kRB rows issued together (indexes clamped: no load behind a branch).
-    {
-        constexpr int kCB = 4 * KS - 2;  // >= bd
-        constexpr int kRB = 8;
-        constexpr int kThr = kMfmaWaves * SSQ_WAVE;
-        const int n_rows = nbc * 256;
-        for (int r0 = 0; r0 < n_rows; r0 += kRB * kThr) {
-            float cv[kRB][kCB];
-#pragma unroll
-            for (int u = 0; u < kRB; ++u) {
-                const int r = min(r0 + u * kThr + (int)threadIdx.x, n_rows - 1);
-                const float* c = cent + ((int64_t)lightL[r >> 8] * 256 + (r & 255)) * bd;
-#pragma unroll
-                for (int d = 0; d < kCB; ++d) cv[u][d] = c[min(d, bd - 1)];
-            }
-#pragma unroll
-            for (int u = 0; u < kRB; ++u) {
-                const int r = r0 + u * kThr + (int)threadIdx.x;
-                if (r >= n_rows) break;
-                const int bl = r >> 8, j = r & 255;
-                float cp[kCB];
-#pragma unroll
-                for (int d = 0; d < kCB; ++d) cp[d] = cv[u][d];
-                if (MET) {
-#pragma unroll
-                    for (int k = 0; k < kCB; ++k)
-                        if (k < bd) cp[k] = metric_row_n(em + (bl * bd + k) * bd, cv[u], bd);
-                }
-                const float cn = sq_norm_n(cp, bd);
-                float* dst = bsw + (size_t)bl * KS * 1024 + (j >> 4) * 64 + (j & 15);
-#pragma unroll
-                for (int k = 0; k < 4 * KS; ++k)
-                    dst[(k >> 2) * 1024 + (k & 3) * 16] = k < bd ? cp[k] : k == bd ? 1.0f : k == bd + 1 ? cn : 0.0f;
-            }
-        }
+    // poff[bl bd + d] = perm[light[bl] bd + d], from the staged permutation
+    for (int j = tid; j < nbc * bd; j += kThr) {
+        const int bl = j / bd, d = j - bl * bd;
+        poff[j] = perm_l[lightL[bl] * bd + d];
     }
     __syncthreads();
 
-    // key rows: lane (m = l/4, quarter q = l%4) loads elements [q*D/4, (q+1)*D/4) of row m
-    const int esz = a.k_dtype == SSQ_F32 ? 4 : 2;
-    const bool vec = (D % 32 == 0) && ((a.k_ss * esz) % 16 == 0) && ((a.k_sh * esz) % 16 == 0) &&
-                     ((a.k_sb * esz) % 16 == 0) && ((uintptr_t)a.keys % 16 == 0) && esz == 2;
-    const int lm = lane >> 2, lq = lane & 3;
-    const int s_wg = blockIdx.x * (kMfmaWaves * kRounds * 16);  // first key index of the workgroup
-    uint4 pre[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
-    auto fetch = [&](int round) {  // vector path: 16 bf16 (D=64) or the first 32 of a longer row quarter
-        const int s = s_wg + (round * kMfmaWaves + wave) * 16 + lm;
-        if (vec && s < n_keys && D == 64) {
-            const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.keys) +
-                                                              km.krow(a, s) + lq * 16);
-            pre[0] = src[0];
-            pre[1] = src[1];
-        }
-    };
-    fetch(0);
     const int lane16 = lane & 15;
     const int mrow = 4 * (lane >> 4);
 
     for (int round = 0; round < kRounds; ++round) {
         const int s0 = s_wg + (round * kMfmaWaves + wave) * 16;
         if (s0 >= n_keys) break;  // wave-uniform
+        // output rows of this lane's key (s0 + lane / 4), resolved now: a slot-mapping load then
+        // overlaps the round's arithmetic instead of delaying the code writes
+        int64_t crow_m, prow_m;
+        {
+            int b, s;
+            km.bs(a, min(s0 + lm, n_keys - 1), b, s);
+            out_rows(a, b, kv, s, crow_m, prow_m);
+        }
         // stage this round's 16 rows (unpermuted, fp32) into xs
-        if (vec && D == 64) {
-            const uint32_t w[8] = {pre[0].x, pre[0].y, pre[0].z, pre[0].w, pre[1].x, pre[1].y, pre[1].z, pre[1].w};
-            float* dst = xs + lm * XS + lq * 16;
+        if (vec) {
+            float* dst = xs + lm * XS + lq * (D / 4);
             const bool ok = s0 + lm < n_keys;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float lo = a.k_dtype == SSQ_BF16 ? __uint_as_float(w[i] << 16) : ssq_f16_to_f32(w[i] & 0xFFFFu);
-                const float hi = a.k_dtype == SSQ_BF16 ? __uint_as_float(w[i] & 0xFFFF0000u) : ssq_f16_to_f32(w[i] >> 16);
-                dst[2 * i] = ok ? lo : 0.f;
-                dst[2 * i + 1] = ok ? hi : 0.f;
+            for (int i = 0; i < kPre; ++i) {
+                if (i >= nq) break;  // wave-uniform
+                const uint32_t w[4] = {pre[i].x, pre[i].y, pre[i].z, pre[i].w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float lo = a.k_dtype == SSQ_BF16 ? __uint_as_float(w[k] << 16) : ssq_f16_to_f32(w[k] & 0xFFFFu);
+                    const float hi =
+                        a.k_dtype == SSQ_BF16 ? __uint_as_float(w[k] & 0xFFFF0000u) : ssq_f16_to_f32(w[k] >> 16);
+                    dst[8 * i + 2 * k] = ok ? lo : 0.f;
+                    dst[8 * i + 2 * k + 1] = ok ? hi : 0.f;
+                }
             }
             fetch(round + 1 < kRounds ? round + 1 : round);
-        } else {
-            for (int e = lane; e < 16 * D; e += 64) {
-                const int m = e / D, j = e - m * D;
-                const int s = s0 + m;
-                xs[m * XS + j] = s < n_keys ? ssq_load_elem(a.keys, a.k_dtype, km.krow(a, s) + j) : 0.f;
+        } else {  // element loads, 8 in flight per lane before their LDS stores
+            constexpr int kB = 8;
+            for (int e0 = lane; e0 < 16 * D; e0 += 64 * kB) {
+                float v[kB];
+#pragma unroll
+                for (int u = 0; u < kB; ++u) {
+                    const int e = min(e0 + 64 * u, 16 * D - 1);
+                    const int m = e / D, j = e - m * D;
+                    const int s = min(s0 + m, n_keys - 1);
+                    v[u] = ssq_load_elem(a.keys, a.k_dtype, km.krow(a, s) + j);
+                }
+#pragma unroll
+                for (int u = 0; u < kB; ++u) {
+                    const int e = e0 + 64 * u;
+                    if (e < 16 * D) {
+                        const int m = e / D, j = e - m * D;
+                        xs[m * XS + j] = s0 + m < n_keys ? v[u] : 0.f;
+                    }
+                }
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -625,14 +678,14 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
         // blocks' code 0 and passthrough values.
         if (p.row_codes) {
             const int pieces = nb >> 4;
-            for (int e = lane; e < 16 * pieces; e += 64) {
+            for (int e0 = 0; e0 < 16 * pieces; e0 += 64) {  // every lane runs every trip (the shuffles)
+                const int e = min(e0 + lane, 16 * pieces - 1);
                 const int m = e / pieces, q = e - m * pieces;
                 const int i = s0 + m;
-                if (i < n_keys) {
-                    int64_t crow, prow;
-                    int b, s;
-                    km.bs(a, i, b, s);
-                    out_rows(a, b, kv, s, crow, prow);
+                const uint32_t clo = (uint32_t)__shfl((int)(uint32_t)crow_m, 4 * m);  // key m's row, from lane 4m
+                const uint32_t chi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)crow_m >> 32), 4 * m);
+                const int64_t crow = (int64_t)(((uint64_t)chi << 32) | clo);
+                if (e0 + lane < 16 * pieces && i < n_keys) {
                     const uint32_t* src = reinterpret_cast<const uint32_t*>(cs + m * nb + 16 * q);
                     *reinterpret_cast<uint4*>(a.codes + crow + 16 * q) = make_uint4(src[0], src[1], src[2], src[3]);
                 }
@@ -640,10 +693,7 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
             const int m = lane >> 2;
             const int i = s0 + m;
             if (do_heavy && i < n_keys) {
-                int64_t crow, prow;
-                int b, s;
-                km.bs(a, i, b, s);
-                out_rows(a, b, kv, s, crow, prow);
+                const int64_t prow = prow_m;
                 for (int blk = lane & 3; blk < nb; blk += 4) {
                     if (!ssq_is_heavy(hm0, hm1, blk)) continue;
                     const int slot = a.pt_dense ? blk : heavy_ordinal(hm0, hm1, blk);
@@ -655,10 +705,7 @@ __global__ __launch_bounds__(kMfmaWaves * SSQ_WAVE, 1) void k_encode_mfma(const 
             const int m = lane >> 2;
             const int i = s0 + m;
             if (i < n_keys) {
-                int64_t crow, prow;
-                int b, s;
-                km.bs(a, i, b, s);
-                out_rows(a, b, kv, s, crow, prow);
+                const int64_t crow = crow_m, prow = prow_m;
                 for (int blk = lane & 3; blk < nb; blk += 4) {
                     const bool heavy = ssq_is_heavy(hm0, hm1, blk);
                     if (heavy) {
