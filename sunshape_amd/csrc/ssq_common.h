@@ -8,6 +8,11 @@
 
 #define SSQ_WAVE 64
 
+// Online softmax of the decode kernels: a row's running maximum may lag the scores seen by up to
+// this much (nats) before it is raised, so most tiles skip the cross-lane maxima and the
+// accumulator rescale; probabilities exp(s - m) then stay below e^8.
+constexpr float kSoftmaxSlack = 8.f;
+
 // ---------------------------------------------------------------------------
 // scalar conversions (bf16 / f16 stored as raw 16-bit words)
 // ---------------------------------------------------------------------------

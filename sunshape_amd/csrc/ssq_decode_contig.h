@@ -69,7 +69,6 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 constexpr int kTile = 64;  // tokens per wave iteration
 constexpr int kD = 64;     // head_dim served
 constexpr int kHP = 16;    // passthrough (heavy-block) dims per token served
-constexpr float kSlack = 8.f;  // online softmax: lag of the running maximum allowed (nats)
 constexpr size_t kMaxSmem = 160 * 1024;
 
 // per-wave LDS region (bytes): V tile [64][Dv] (16-bit) | P strip [16][64] (16-bit).  The scaled
@@ -530,16 +529,15 @@ __global__ __launch_bounds__(contig_waves(DT, HV, MK, R4) * SSQ_WAVE) void k_dec
         if constexpr (!HAS_V) return;
 
         // ---- online softmax per row over the wave's 64 tokens.  The running maximum m_run[r] is
-        // wave-uniform and moves only when some score of the tile exceeds it by more than kSlack,
-        // so most tiles skip the cross-lane maxima and the accumulator rescale; probabilities
-        // exp(s - m_run) then stay below e^kSlack.  Rows past nr come from zero query rows and
-        // are never stored.
+        // wave-uniform and moves only when some score of the tile exceeds it by more than
+        // kSoftmaxSlack, so most tiles skip the cross-lane maxima and the accumulator rescale.
+        // Rows past nr come from zero query rows and are never stored.
         float sv[RP];
         bool over = false;
 #pragma unroll
         for (int r = 0; r < RP; ++r) {
             sv[r] = valid ? s[r] : -INFINITY;
-            over |= sv[r] > m_run[r] + kSlack;
+            over |= sv[r] > m_run[r] + kSoftmaxSlack;
         }
         if (__builtin_amdgcn_ballot_w64(over) != 0) {  // wave-uniform
             float alpha[RP];

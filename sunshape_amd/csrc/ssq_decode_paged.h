@@ -180,21 +180,25 @@ __device__ __forceinline__ void tile_softmax_pv(const MfmaParams& p, uint16_t* p
             }
         }
     }
-    // online softmax (wave-local)
-    float alpha[RP];
-    bool rescale = false;
+    // online softmax (wave-local).  The running maximum m_run[r] is wave-uniform and moves only
+    // when some score of the tile exceeds it by more than kSoftmaxSlack: most tiles skip the
+    // cross-lane maxima and the accumulator rescale.
+    float sv[RP];
+    bool over = false;
 #pragma unroll
     for (int r = 0; r < RP; ++r) {
-        const float tm = wave_max(valid ? s[r] : -INFINITY);
-        const float mn = fmaxf(m_run[r], tm);
-        alpha[r] = (mn == -INFINITY) ? 1.f : __expf(m_run[r] - mn);
-        rescale |= mn != m_run[r];
-        m_run[r] = mn;
-        const float pr = (valid && mn != -INFINITY) ? __expf(s[r] - mn) : 0.f;
-        l_lane[r] = l_lane[r] * alpha[r] + pr;
-        pstrip[r * kTileTok + lane] = (uint16_t)to_vt16<VT>(pr);
+        sv[r] = valid ? s[r] : -INFINITY;
+        over |= sv[r] > m_run[r] + kSoftmaxSlack;
     }
-    if (rescale) {  // wave-uniform
+    if (__builtin_amdgcn_ballot_w64(over) != 0) {  // wave-uniform
+        float alpha[RP];
+#pragma unroll
+        for (int r = 0; r < RP; ++r) {
+            const float mn = fmaxf(m_run[r], wave_max(sv[r]));
+            alpha[r] = mn == -INFINITY ? 1.f : __expf(m_run[r] - mn);
+            l_lane[r] *= alpha[r];
+            m_run[r] = mn;
+        }
         // accumulator row 4 g + i lives in lane group g = lane / 16
         const int grp = lane >> 4;
 #pragma unroll
@@ -206,6 +210,14 @@ __device__ __forceinline__ void tile_softmax_pv(const MfmaParams& p, uint16_t* p
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) acc[dt][i] *= f;
         }
+    }
+#pragma unroll
+    for (int r = 0; r < RP; ++r) {
+        // m_run is -inf only while every score seen is -inf (then p = exp(-inf) = 0)
+        const float mr = m_run[r] == -INFINITY ? 0.f : m_run[r];
+        const float pr = __expf(sv[r] - mr);
+        l_lane[r] += pr;
+        pstrip[r * kTileTok + lane] = (uint16_t)to_vt16<VT>(pr);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
