@@ -273,6 +273,34 @@ def test_grid_encode_key_paths(dtype, D, odd_stride):
     assert np.array_equal(got, ref), int((got != ref).sum())
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("D,bd", [(64, 2), (128, 4)])
+@pytest.mark.parametrize("odd_stride", [False, True])
+def test_mfma_encode_key_paths(dtype, D, bd, odd_stride):
+    """Both ways the MFMA encode stages keys: 16-bit rows of 64 or 128 elements on 16-byte
+    boundaries come in with 16-byte loads (prefetched a round ahead); fp32 rows and rows at odd
+    strides are read element by element, 8 loads in flight per lane.  Each must equal the
+    oracle bit for bit, with several rounds per workgroup."""
+    log(f"mfma encode key path dtype={dtype} D={D} bd={bd} odd_stride={odd_stride}")
+    rng = np.random.default_rng(D + bd + int(odd_stride))
+    n = 2500
+    perm = rng.permutation(D)
+    sig = np.exp(rng.uniform(np.log(0.1), np.log(3), D)).astype(np.float32)
+    cent = (rng.standard_normal((D // bd, 256, bd)) * sig[perm].reshape(D // bd, 1, bd)).astype(np.float32)
+    kt = torch.from_numpy((rng.standard_normal((n, D)) * sig).astype(np.float32)).to(dtype)
+    ref, _ = O.encode(kt.float().numpy(), perm, cent)
+    if odd_stride:  # rows 3 elements apart beyond D: not 16-byte aligned
+        buf = torch.zeros(n, D + 3, dtype=dtype)
+        buf[:, :D] = kt
+        k = buf.to(DEV)[:, :D][None, None]
+        assert k.stride(2) == D + 3
+    else:
+        k = kt.to(DEV)[None, None]
+    codes, _ = hip_ops.encode(k, torch.from_numpy(perm).to(DEV), torch.from_numpy(cent).to(DEV), kernel=2)
+    got = np_of(codes[0, 0])
+    assert np.array_equal(got, ref), int((got != ref).sum())
+
+
 def test_grid_encode_constructed_ties_duplicates_and_heavy():
     """Duplicated codewords (lower index wins), one-ulp neighbours, keys on codewords, keys on cell
     boundaries, and passthrough blocks in both layouts."""
