@@ -315,14 +315,29 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     v4f acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
-    while (tile < n_tiles) {
-        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RB);
-        compute_tile<RP, DT, VT, NB, NC, PB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane, acc);
-        tile += kWaves;
-        if (tile >= n_tiles) break;
-        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RA);
-        compute_tile<RP, DT, VT, NB, NC, PB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RB, m_run, l_lane, acc);
-        tile += kWaves;
+    if constexpr (DT > 8) {
+        // 256-dim values: two tiles' V fragments would take all 256 registers, so one register
+        // set; a wave issues its next tile once this one is consumed (the other waves' loads keep
+        // the memory busy meanwhile)
+        while (tile < n_tiles) {
+            compute_tile<RP, DT, VT, NB, NC, PB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane,
+                                                 acc);
+            tile += kWaves;
+            if (tile >= n_tiles) break;
+            issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, tile, lane, cbase, vbase, RA);
+        }
+    } else {
+        while (tile < n_tiles) {
+            issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RB);
+            compute_tile<RP, DT, VT, NB, NC, PB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane,
+                                                 acc);
+            tile += kWaves;
+            if (tile >= n_tiles) break;
+            issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RA);
+            compute_tile<RP, DT, VT, NB, NC, PB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RB, m_run, l_lane,
+                                                 acc);
+            tile += kWaves;
+        }
     }
 
     // ---- merge the waves' (m, l, O) through LDS (the LUT is no longer needed)
