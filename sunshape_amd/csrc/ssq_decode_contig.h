@@ -38,6 +38,13 @@
 
 // Parameters of one contiguous decode launch (shared type: the host code and every instantiation
 // unit fill or read it)
+// Codes packed at a width the kernel takes at run time (PB < 0): bits per code, codes per int32
+// word (vpe = 32 / bits), words per token row, and mul = ceil(65536 / vpe), so that blk / vpe =
+// (blk * mul) >> 16 exactly for blk < 64.
+struct SsqPackFmt {
+    uint32_t bits, vpe, mul, nw;
+};
+
 struct SsqContigParams {
     ssq_decode_args a;
     int G, rows, split_len, n_splits;
@@ -50,6 +57,7 @@ struct SsqContigParams {
     int pt_vec;  // 1: the 8 passthrough values are contiguous 16-bit elements from slot 0, 16-byte aligned
     int hoff[16];
     int hdim[16];
+    SsqPackFmt pk;  // PB < 0 variants
 };
 
 // Launch shape chosen by the host: value tiles of 16 dims, waves per workgroup, row quads
@@ -134,7 +142,11 @@ __device__ __forceinline__ void wave_sync() {
 
 // packed code rows (PB bits per code, 32 / PB codes per little-endian int32 word, the low bits
 // first; sunshape/triton_kernels.py:250-266): int32 words per row
-__host__ __device__ constexpr int pk_words(int NB, int PB) { return PB ? (NB + 32 / PB - 1) / (32 / PB) : 1; }
+// int32 words per token row of PB-bit codes; PB < 0 (width at run time): room for 7-bit codes,
+// the widest below a byte
+__host__ __device__ constexpr int pk_words(int NB, int PB) {
+    return PB > 0 ? (NB + 32 / PB - 1) / (32 / PB) : PB < 0 ? (NB + 3) / 4 : 1;
+}
 
 // Bits of N elements of a tensor of dtype dt with no branch on the dtype (straight-line loads keep
 // the compiler's load-counter waits exact, so converting them later does not wait for loads issued
@@ -233,7 +245,11 @@ __device__ __forceinline__ void issue_codes(const SsqContigParams& p, int b, int
         const uint32_t* prow = reinterpret_cast<const uint32_t*>(a.codes) + (int64_t)b * a.c_sb +
                                (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st;
 #pragma unroll
-        for (int i = 0; i < pk_words(NB, PB); ++i) R.pk[i] = __builtin_nontemporal_load(prow + i);
+        for (int i = 0; i < pk_words(NB, PB); ++i) {
+            // width at run time: the row has p.pk.nw words, the rest of the registers re-read its last
+            const int wi = PB > 0 ? i : min(i, (int)p.pk.nw - 1);
+            R.pk[i] = __builtin_nontemporal_load(prow + wi);
+        }
     } else if constexpr (NB >= 16) {
         const uint8_t* crow = a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st;
 #pragma unroll
@@ -244,12 +260,19 @@ __device__ __forceinline__ void issue_codes(const SsqContigParams& p, int b, int
     }
 }
 
-// code of block blk for this lane's token
+// code of block blk for this lane's token (f: the packing of a run-time width, PB < 0)
 template <int NB, int DT, int HV, bool MK, int PB, int RP>
-__device__ __forceinline__ uint32_t token_code(const Tile<NB, DT, HV, MK, PB, RP>& R, int blk) {
+__device__ __forceinline__ uint32_t token_code(const Tile<NB, DT, HV, MK, PB, RP>& R, int blk, const SsqPackFmt& f) {
     if constexpr (PB > 0) {
         constexpr int kVpe = 32 / PB;
         return (R.pk[blk / kVpe] >> ((blk % kVpe) * PB)) & ((1u << PB) - 1u);
+    } else if constexpr (PB < 0) {  // word and shift are wave-uniform: a register index, not a load
+        const uint32_t w = ((uint32_t)blk * f.mul) >> 16;
+        const uint32_t sh = ((uint32_t)blk - w * f.vpe) * f.bits;
+        uint32_t words[pk_words(NB, PB)];  // a local copy, indexed in registers
+#pragma unroll
+        for (int i = 0; i < pk_words(NB, PB); ++i) words[i] = R.pk[i];
+        return (words[w] >> sh) & ((1u << f.bits) - 1u);
     } else {
         const int wi = blk >> 2;
         uint32_t word;
@@ -282,11 +305,11 @@ __device__ __forceinline__ void lds_vec(const float* src, float (&dst)[BD]) {
 
 template <int KB, int BD, class T>
 __device__ __forceinline__ void gather_batch(const float* cb, int nc, uint32_t ncm1, const T& R, int b0,
-                                             float (&ev)[KB][BD]) {
+                                             const SsqPackFmt& f, float (&ev)[KB][BD]) {
 #pragma unroll
     for (int k = 0; k < KB; ++k) {
         const int blk = b0 + k;
-        const uint32_t code = min(token_code(R, blk), ncm1);
+        const uint32_t code = min(token_code(R, blk, f), ncm1);
         lds_vec<BD>(cb + ((uint32_t)blk * (uint32_t)nc + code) * BD, ev[k]);
     }
 }
@@ -299,7 +322,7 @@ __device__ __forceinline__ void gather_batch(const float* cb, int nc, uint32_t n
 template <int BD, int R4, int NB, int DT, int HV, bool MK, int PB, int RP>
 __device__ __forceinline__ void tile_scores(const float* cb, int nc, const Tile<NB, DT, HV, MK, PB, RP>& R,
                                             const float (&qa)[R4][kD / 16], const float (&qh)[R4], int n_hd,
-                                            int pt_dtype, float (&s)[RP]) {
+                                            int pt_dtype, const SsqPackFmt& f, float (&s)[RP]) {
     constexpr int KB = BD >= 4 ? 4 : 8;  // blocks gathered per batch
     constexpr int NBATCH = NB / KB;
     static_assert(NB % KB == 0, "blocks per batch must divide the block count");
@@ -311,11 +334,11 @@ __device__ __forceinline__ void tile_scores(const float* cb, int nc, const Tile<
         c1[q] = (v4f){0.f, 0.f, 0.f, 0.f};
     }
     float ev[2][KB][BD];
-    gather_batch<KB, BD>(cb, nc, ncm1, R, 0, ev[0]);
+    gather_batch<KB, BD>(cb, nc, ncm1, R, 0, f, ev[0]);
     static_for<0, NBATCH>([&](auto bc) {
         constexpr int bi = decltype(bc)::value;
         constexpr int b0 = bi * KB;
-        if constexpr (bi + 1 < NBATCH) gather_batch<KB, BD>(cb, nc, ncm1, R, b0 + KB, ev[(bi + 1) & 1]);
+        if constexpr (bi + 1 < NBATCH) gather_batch<KB, BD>(cb, nc, ncm1, R, b0 + KB, f, ev[(bi + 1) & 1]);
         // keep the next batch's gathers ahead of this batch's MFMAs (the scheduler would otherwise
         // sink each gather to its first use and wait on every one)
         __builtin_amdgcn_sched_barrier(0);
@@ -508,7 +531,7 @@ __global__ __launch_bounds__(contig_waves(DT, HV, MK, R4) * SSQ_WAVE) void k_dec
             issue_values(p, b, kv, t_next, t_end, lane, R);
         }
         float s[RP];
-        tile_scores<BD, R4>(cb, nc, R, qa, qh, p.n_hd, a.pt_dtype, s);
+        tile_scores<BD, R4>(cb, nc, R, qa, qh, p.n_hd, a.pt_dtype, p.pk, s);
         if constexpr (MK) {
 #pragma unroll
             for (int r = 0; r < RP; ++r) s[r] += R.mk[r];
@@ -676,11 +699,13 @@ int contig_r4(const SsqContigParams& cp, const SsqContigPlan& pl, hipStream_t st
         default: return contig_bd<DT, VT, HAS_V, HV, MK, PB, 4>(cp, pl, st);
     }
 }
-// the variants without passthrough values: byte codes with or without a mask, 4- and 6-bit words
+// the variants without passthrough values: byte codes with or without a mask, 4- and 6-bit words,
+// other widths below 8 bits (taken at run time)
 template <int DT, int VT, bool HAS_V>
 int contig_plain(const SsqContigParams& cp, const SsqContigPlan& pl, hipStream_t st) {
     if (cp.a.code_bits == 4) return contig_r4<DT, VT, HAS_V, 0, false, 4>(cp, pl, st);
     if (cp.a.code_bits == 6) return contig_r4<DT, VT, HAS_V, 0, false, 6>(cp, pl, st);
+    if (cp.a.code_bits > 0) return contig_r4<DT, VT, HAS_V, 0, false, -1>(cp, pl, st);  // 1-3, 5, 7 bits
     if (HAS_V && cp.a.mask) return contig_r4<DT, VT, HAS_V, 0, HAS_V, 0>(cp, pl, st);
     return contig_r4<DT, VT, HAS_V, 0, false, 0>(cp, pl, st);
 }

@@ -37,11 +37,12 @@ PtLayout pt_layout(const ssq_decode_args& a) {
 
 bool plan(const ssq_decode_args* a, bool has_v, SsqContigPlan& pl) {
     if (a->layout != SSQ_CONTIGUOUS) return false;
-    // packed codes: 4- and 6-bit words are unpacked in the kernel (without passthrough or mask);
-    // 8-bit words are byte rows (strides scaled to bytes); other widths take the generic kernel
+    // packed codes: words of 1-7-bit codes are unpacked in the kernel (4 and 6 bits at compile
+    // time, other widths at run time; without passthrough or mask); 8-bit words are byte rows
+    // (strides scaled to bytes)
     const int cbits = a->code_bits;
-    if (cbits != 0 && cbits != 4 && cbits != 6 && cbits != 8) return false;
-    if ((cbits == 4 || cbits == 6) && (a->heavy_mask[0] || a->mask)) return false;
+    if (cbits < 0 || cbits > 8) return false;
+    if (cbits > 0 && cbits < 8 && (a->heavy_mask[0] || a->mask)) return false;
     if (!has_v && a->mask) return false;  // scores only: the reference's score kernels take no mask
     if (a->heavy_mask[1]) return false;
     if (a->heavy_mask[0]) {
@@ -56,7 +57,7 @@ bool plan(const ssq_decode_args* a, bool has_v, SsqContigPlan& pl) {
     if (rows > 16) return false;
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;
     const int nb = a->n_blocks;
-    if (cbits == 4 || cbits == 6) {  // word loads
+    if (cbits > 0 && cbits < 8) {  // word loads
         if ((uintptr_t)a->codes % 4) return false;
     } else {
         const int cal = nb >= 16 ? 16 : 8;  // code row loads of 16 (or 8) bytes
@@ -133,6 +134,12 @@ int ssq_decode_contig(const ssq_decode_args* a, void* workspace, size_t ws_bytes
     if (a->code_bits == 8) {  // 8-bit words are the byte rows: byte strides, the byte-code path
         cp.a.c_sb *= 4; cp.a.c_sh *= 4; cp.a.c_st *= 4;
         cp.a.code_bits = 0;
+    }
+    if (cp.a.code_bits > 0) {  // packing of the word rows (used by the run-time-width variants)
+        const uint32_t bits = (uint32_t)cp.a.code_bits, vpe = 32u / bits;
+        cp.pk = SsqPackFmt{bits, vpe, (65536u + vpe - 1u) / vpe, ((uint32_t)a->n_blocks + vpe - 1u) / vpe};
+    } else {
+        cp.pk = SsqPackFmt{8u, 4u, 16384u, 1u};
     }
     cp.G = a->num_q_heads / a->num_kv_heads;
     cp.rows = cp.G * a->q_len;

@@ -92,10 +92,14 @@ def test_decode_over_packed_codes_equals_uint8(paged):
 
 
 @pytest.mark.parametrize("bits,bd,nc,Hq,T", [(6, 2, 64, 14, 700), (4, 2, 16, 8, 640), (6, 1, 64, 4, 333),
-                                             (4, 4, 16, 16, 1000), (6, 8, 64, 2, 129), (8, 2, 256, 14, 700)])
+                                             (4, 4, 16, 16, 1000), (6, 8, 64, 2, 129), (8, 2, 256, 14, 700),
+                                             (1, 1, 2, 8, 300), (2, 2, 4, 14, 640), (3, 4, 8, 4, 517),
+                                             (5, 2, 32, 16, 700), (7, 8, 128, 6, 1000), (7, 1, 128, 14, 257),
+                                             (3, 1, 8, 2, 129)])
 def test_contig_mfma_decode_over_packed_codes_equals_uint8(bits, bd, nc, Hq, T):
-    """The contiguous MFMA kernel unpacks 4- and 6-bit words when the tile goes to LDS (8-bit words
-    are read as byte rows): output, LSE and raw scores equal its own uint8-code launch bit for bit."""
+    """The contiguous MFMA kernel unpacks packed words in registers (4 and 6 bits with the width
+    fixed at compile time, 1-3, 5 and 7 bits at run time; 8-bit words are read as byte rows):
+    output, LSE and raw scores equal its own uint8-code launch bit for bit."""
     log(f"packed contig decode bits={bits} bd={bd} nc={nc} Hq={Hq} T={T}")
     cb, codes, q, v = _case(nc=nc, bd=bd, Hq=Hq, T=T, seed=40 + bits + bd)
     perm, cent = cb.perm.to(DEV), cb.centroids.to(DEV)
