@@ -276,6 +276,11 @@ class SunShapeCache(DynamicCache):
 
 
 # ---------------------------------------------------------------------------- attention
+# multi-token steps take the fused decode up to this many query rows per KV head (the row count the
+# contiguous MFMA kernel holds in one pass); longer ones attend dequantized keys
+_FUSED_MAX_ROWS = 16
+
+
 def _additive_mask(mask: Optional[torch.Tensor], dtype=torch.float32) -> Optional[torch.Tensor]:
     if mask is None:
         return None
@@ -303,17 +308,26 @@ def sunshape_attention_forward(module: torch.nn.Module, query: torch.Tensor, key
     if kwargs.get("output_attentions", False):
         raise RuntimeError("SunShape attention over coded keys does not return attention weights")
     B, Hq, Lq, D = query.shape
-    if Lq == 1:  # decode step: fused LUT-score decode over the codes
-        T = key.codes.shape[2]
+    T = key.codes.shape[2]
+    rows = (Hq // value.shape[1]) * Lq  # query rows per KV head
+    if Lq == 1 or (T > Lq and rows <= _FUSED_MAX_ROWS):
+        # a decode step, or a short multi-token step over a filled cache (speculative verification,
+        # small chunks): the fused decode over the codes, masked as HF's mask builder says (or
+        # causally, the new tokens being the last Lq positions)
         mask = _additive_mask(attention_mask)
         if mask is not None:
             mask = mask[..., -T:]
+        elif Lq > 1:
+            pos = torch.arange(T, device=query.device)
+            last = T - Lq + torch.arange(Lq, device=query.device)
+            mask = torch.zeros(1, 1, Lq, T, device=query.device).masked_fill(pos[None, :] > last[:, None],
+                                                                              float("-inf"))
         perm, cent = _per_head_arrays(key.codec)
         out = hip_ops.decode(query, key.codes, value, perm, cent, scale=scaling, mask=mask,
                              heavy=key.codec.heavy_blocks(), pt=key.passthrough, pt_dense=False,
                              rotation=key.codec.rotation_matrix())
         return out.transpose(1, 2).contiguous(), None
-    # prefill / multi-token step: dense k_hat in the key dtype, as the reference's cache layer stores
+    # prefill / long multi-token step: dense k_hat in the key dtype, as the reference's cache layer stores
     return sdpa_attention_forward(module, query, key.dequantize(), value, attention_mask, dropout=0.0,
                                   scaling=scaling, is_causal=is_causal, **kwargs)
 

@@ -107,6 +107,15 @@ def test_code_layer_append_growth_and_decode():
                                codec.permutation.cpu().numpy(), 1 / math.sqrt(D), "bf16", "bf16", heavy=heavy,
                                pt_values=pt_ref, mask=add)
     assert_rel(np_of(out_m.transpose(1, 2)), ref_m, BF16_TOL, "code-layer decode masked")
+    # a 3-token step (speculative verification) without a mask: the fused decode, the new tokens
+    # being the last 3 positions (token i sees keys up to 300 + i)
+    q3 = torch.randn(B, Hq, 3, D, generator=g).to(torch.bfloat16)
+    out3, _ = sunshape_attention_forward(mod, q3.to(DEV), keys, values, None, scaling=1 / math.sqrt(D))
+    causal = np.where(np.arange(303)[None, :] > (300 + np.arange(3))[:, None], -np.inf, 0.0).astype(np.float32)
+    ref3 = O.decode_attention(q3.float().numpy(), codes_ref, allv.float().numpy(), codec.centroids.cpu().numpy(),
+                              codec.permutation.cpu().numpy(), 1 / math.sqrt(D), "bf16", "bf16", heavy=heavy,
+                              pt_values=pt_ref, mask=np.broadcast_to(causal, (B, Hq, 3, 303)))
+    assert_rel(np_of(out3.transpose(1, 2)), ref3, BF16_TOL, "code-layer 3-token step")
     layer.crop(-3)
     assert layer.get_seq_length() == 300
     layer.reorder_cache(torch.tensor([1, 0], device=DEV))
@@ -115,7 +124,8 @@ def test_code_layer_append_growth_and_decode():
 
 def test_tiny_llama_code_cache_tracks_dequant_cache():
     """Prefill through the code cache is bit-identical to the reference-mirroring cache (both attend
-    bf16 k_hat); decode steps use the fused LUT kernel and stay within bf16 tolerance of it."""
+    bf16 k_hat); decode steps and a 3-token step use the fused decode and stay within bf16
+    tolerance of it."""
     from transformers import LlamaConfig, LlamaForCausalLM
 
     log("tiny llama code cache")
@@ -126,18 +136,21 @@ def test_tiny_llama_code_cache_tracks_dequant_cache():
     codecs = {0: _codec(D=32, bd=4, seed=8)[0], 1: _codec(D=32, bd=2, seed=9)[0]}
     ids = torch.randint(0, 512, (2, 40), generator=torch.Generator().manual_seed(2)).to(DEV)
     steps = torch.randint(0, 512, (2, 4), generator=torch.Generator().manual_seed(3)).to(DEV)
+    multi = torch.randint(0, 512, (2, 3), generator=torch.Generator().manual_seed(4)).to(DEV)
     with torch.no_grad():
         model.set_attn_implementation("sdpa")
         ref_cache = SunShapeCache.from_codecs(codecs, config=cfg)
         ref_logits = [model(ids, past_key_values=ref_cache).logits]
         for i in range(steps.shape[1]):
             ref_logits.append(model(steps[:, i:i + 1], past_key_values=ref_cache).logits)
+        ref_logits.append(model(multi, past_key_values=ref_cache).logits)  # a 3-token step
         model.set_attn_implementation(register_sunshape_attention())
         cache = SunShapeCache.from_codecs(codecs, config=cfg, store_codes=True)
         logits = [model(ids, past_key_values=cache).logits]
         for i in range(steps.shape[1]):
             logits.append(model(steps[:, i:i + 1], past_key_values=cache).logits)
-    assert isinstance(cache.layers[0], SunShapeCodeLayer) and cache.get_seq_length() == 44
+        logits.append(model(multi, past_key_values=cache).logits)  # fused decode, 12 rows per KV head
+    assert isinstance(cache.layers[0], SunShapeCodeLayer) and cache.get_seq_length() == 47
     assert torch.equal(logits[0], ref_logits[0])
     for a, r in zip(logits[1:], ref_logits[1:]):
         assert_rel(a.float().cpu().numpy(), r.float().cpu().numpy(), 3e-2, "decode logits")
