@@ -1,4 +1,4 @@
-// Pieces shared by the paged decode kernels (ssq_decode_mfma.hip: LUT scores and 16x16 MFMA scores;
+// Pieces shared by the paged decode kernels (ssq_decode_mfma.h: LUT scores;
 // ssq_decode_paged_q4.hip: 4x4 MFMA scores): launch shape, parameters, the wave reductions, and the
 // 64-token tile loads (one token's codes per lane, V fragments straight from the dim-major pages).
 #pragma once

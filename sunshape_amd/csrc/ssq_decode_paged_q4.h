@@ -6,7 +6,7 @@
 // does not fit the LDS (8 query heads per KV head, or 64 blocks of dim 2 at head_dim 128, the
 // reference's default 4 bits/dim), and for codebooks other than 256 / 64 codewords.
 //
-// Same mathematics as the LUT kernels (ssq_decode_mfma.hip): scores q_perm . k_hat in fp32
+// Same mathematics as the LUT kernels (ssq_decode_mfma.h): scores q_perm . k_hat in fp32
 // (triton_kernels.py:381-408, :174-196, summed here in MFMA order, so within fp32 rounding of the
 // LUT path), online softmax, probabilities cast to the value dtype before P.V
 // (vllm_attn_backend.py:251-252).  Mapping:
