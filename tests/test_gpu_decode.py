@@ -182,6 +182,18 @@ def test_paged_mfma_row_groups_vs_oracle(Hq, bd, lq, D):
                             [(b, kv) for b in range(2) for kv in (1, 6)])
 
 
+def test_paged_lut_256_dim_values_several_tiles_per_wave():
+    """head_dim-256 values on the paged LUT kernel keep one register set per wave (two would not fit
+    the registers); a context of 2,000 tokens gives each wave several tiles in one split."""
+    log("paged LUT D256 several tiles per wave")
+    p = synthetic.config4(DEV, B=2, T=2048, Hq=8, bd=8, D=256)
+    lens = torch.tensor([2000, 1333], dtype=torch.int32, device=DEV)
+    out, lse, scores = hip_ops.decode(p["q"], p["code_pages"], p["v_pages"], p["perm"], p["centroids"],
+                                      scale=p.meta["scale"], block_table=p["block_table"], seq_lens=lens,
+                                      return_lse=True, return_scores=True, kernel=2, num_splits=1)
+    _paged_oracle_check(p, np_of(out), np_of(lse), np_of(scores), [(0, 0), (1, 5), (0, 7)], seq_lens=np_of(lens))
+
+
 def test_paged_ragged_sequence_lengths():
     log("paged ragged seq_lens")
     p = synthetic.config4(DEV, B=4, T=1024)
