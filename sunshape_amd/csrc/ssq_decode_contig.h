@@ -209,13 +209,17 @@ template <int NB, int DT, int HV, bool MK, int PB, int RP>
 __device__ __forceinline__ void issue_values(const SsqContigParams& p, int b, int kv, int t0, int t_end, int lane,
                                              Tile<NB, DT, HV, MK, PB, RP>& R) {
     const ssq_decode_args& a = p.a;
-    const uint16_t* vb = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kv * a.v_sh;
+    // a wave-uniform base at the tile's first token and 32-bit lane offsets (the host checks that
+    // a tile spans less than 2^31 elements), so each load is a scalar base plus one offset register
+    const uint16_t* vt = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kv * a.v_sh +
+                         (int64_t)t0 * a.v_st;
+    const int last = t_end - 1 - t0;  // tokens past it re-read the last one
     constexpr int kRowChunks = 2 * DT;  // 16-byte chunks per token row (Dv = 16 * DT)
 #pragma unroll
     for (int i = 0; i < 2 * DT; ++i) {
         const int chunk = i * SSQ_WAVE + lane;  // chunk of the tile, row-major
-        const int tok = min(t0 + chunk / kRowChunks, t_end - 1);
-        R.v[i] = ld16(vb + (int64_t)tok * a.v_st + (chunk % kRowChunks) * 8);
+        const uint32_t off = (uint32_t)min(chunk / kRowChunks, last) * (uint32_t)a.v_st + (chunk % kRowChunks) * 8;
+        R.v[i] = ld16(reinterpret_cast<const uint8_t*>(vt) + 2u * off);  // a 32-bit byte offset
     }
 }
 template <int NB, int DT, int HV, bool MK, int PB, int RP>
@@ -223,6 +227,7 @@ __device__ __forceinline__ void issue_codes(const SsqContigParams& p, int b, int
                                             Tile<NB, DT, HV, MK, PB, RP>& R) {
     const ssq_decode_args& a = p.a;
     const int tc = min(t0 + lane, t_end - 1);
+    const uint32_t rel = (uint32_t)(tc - t0);  // this lane's token within the tile (32-bit offsets below)
     if constexpr (MK) {  // rows past the query rows re-read the last row (never added)
 #pragma unroll
         for (int r = 0; r < RP; ++r) {
@@ -237,11 +242,12 @@ __device__ __forceinline__ void issue_codes(const SsqContigParams& p, int b, int
 #pragma unroll
         for (int i = 0; i < kHP; ++i) R.h[i] = ssq_load_bits(a.pt, a.pt_dtype, pb + p.hoff[i]);  // hoff clamped
     } else if constexpr (HV == 2) {
-        const int64_t pb = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)tc * a.pt_st;
-        const uint4 w = ld16(reinterpret_cast<const uint16_t*>(a.pt) + pb);
+        const uint16_t* pt0 = reinterpret_cast<const uint16_t*>(a.pt) + (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh +
+                              (int64_t)t0 * a.pt_st;
+        const uint4 w = ld16(reinterpret_cast<const uint8_t*>(pt0) + 2u * (rel * (uint32_t)a.pt_st));
         R.h[0] = w.x; R.h[1] = w.y; R.h[2] = w.z; R.h[3] = w.w;
     }
-    if constexpr (PB) {  // packed rows: strides count int32 words
+    if constexpr (PB) {  // packed rows: strides count int32 words (one row address, word offsets)
         const uint32_t* prow = reinterpret_cast<const uint32_t*>(a.codes) + (int64_t)b * a.c_sb +
                                (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st;
 #pragma unroll
@@ -250,13 +256,15 @@ __device__ __forceinline__ void issue_codes(const SsqContigParams& p, int b, int
             const int wi = PB > 0 ? i : min(i, (int)p.pk.nw - 1);
             R.pk[i] = __builtin_nontemporal_load(prow + wi);
         }
-    } else if constexpr (NB >= 16) {
-        const uint8_t* crow = a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st;
-#pragma unroll
-        for (int i = 0; i < NB / 16; ++i) R.c[i] = ld16(crow + 16 * i);
     } else {
-        const uint8_t* crow = a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)tc * a.c_st;
-        R.c8 = *reinterpret_cast<const uint2*>(crow);
+        const uint8_t* c0 = a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)t0 * a.c_st;
+        const uint32_t roff = rel * (uint32_t)a.c_st;
+        if constexpr (NB >= 16) {
+#pragma unroll
+            for (int i = 0; i < NB / 16; ++i) R.c[i] = ld16(c0 + roff + 16 * i);
+        } else {
+            R.c8 = *reinterpret_cast<const uint2*>(c0 + roff);
+        }
     }
 }
 
