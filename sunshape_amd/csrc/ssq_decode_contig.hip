@@ -65,8 +65,10 @@ bool plan(const ssq_decode_args* a, bool has_v, SsqContigPlan& pl) {
         if ((uintptr_t)a->codes % cal || (a->c_st * cs) % cal || (a->c_sh * cs) % cal || (a->c_sb * cs) % cal)
             return false;
     }
-    // tile loads take 32-bit offsets from the tile's first token: a tile must span < 2^31 elements
+    // tile loads take 32-bit offsets from the tile's first token: a tile must span < 2^31 elements,
+    // with non-negative token strides
     const int64_t kLim = (int64_t)1 << 31;
+    if (a->c_st < 0 || (has_v && a->v_st < 0) || (a->heavy_mask[0] && a->pt_st < 0)) return false;
     if ((int64_t)kTile * a->c_st * (cbits == 8 ? 4 : 1) + 64 >= kLim) return false;
     if (has_v && (int64_t)kTile * a->v_st + a->value_dim >= kLim) return false;
     if (a->heavy_mask[0] && (int64_t)kTile * a->pt_st + 64 >= kLim) return false;
