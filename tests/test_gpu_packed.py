@@ -95,7 +95,7 @@ def test_decode_over_packed_codes_equals_uint8(paged):
                                              (4, 4, 16, 16, 1000), (6, 8, 64, 2, 129), (8, 2, 256, 14, 700),
                                              (1, 1, 2, 8, 300), (2, 2, 4, 14, 640), (3, 4, 8, 4, 517),
                                              (5, 2, 32, 16, 700), (7, 8, 128, 6, 1000), (7, 1, 128, 14, 257),
-                                             (3, 1, 8, 2, 129)])
+                                             (3, 1, 8, 2, 129), (5, 2, 32, 8, 1), (1, 2, 2, 14, 63)])
 def test_contig_mfma_decode_over_packed_codes_equals_uint8(bits, bd, nc, Hq, T):
     """The contiguous MFMA kernel unpacks packed words in registers (4 and 6 bits with the width
     fixed at compile time, 1-3, 5 and 7 bits at run time; 8-bit words are read as byte rows):
