@@ -16,6 +16,11 @@
 //               read straight from the page: vLLM's value page is dim-major
 //               ([Dv][page]), so the 8 consecutive tokens of one dim that a lane
 //               supplies to the B operand are one 16-byte load.
+//
+// The same kernel with CT = true reads contiguous rows (codes [B, Hkv, T, nb], V [B, Hkv, T, 128],
+// token-major) for head dims past the contiguous MFMA kernel's 64: V tiles load as coalesced
+// 256-byte rows and pass through a per-wave LDS buffer 16 tokens at a time, read back transposed
+// (ds_read_b64_tr_b16) as B operands of v_mfma_f32_16x16x16.
 #pragma once
 
 #include "ssq_decode_paged.h"
@@ -27,6 +32,7 @@ struct SsqMfmaPlan {
     int RP, DT, split_len, n_splits;
     int rg, n_groups;  // query rows per row group, row groups
     bool q4;           // k_decode_paged_q4 (4x4-MFMA scores) in place of the LUT kernel
+    bool ct;           // contiguous rows (the LUT kernel with CT = true)
     size_t smem, ws_bytes;
 };
 
@@ -34,7 +40,9 @@ namespace {
 
 // LUT codewords per block: 256, or 64 for 64-codeword codebooks (a table a quarter the size)
 __host__ __device__ inline int lut_nc(const ssq_decode_args& a) { return a.n_centroids == 64 ? 64 : kNC; }
-// LDS carve-up (floats): lut [nb*nc*RP] | qp [RP*D] | pstrip [waves][RP][64] (16-bit) | pages [split_len/16] (int32)
+// LDS carve-up (floats): lut [nb*nc*RP] | qp [RP*D] | pstrip [waves][RP][64] (16-bit) | then either
+// pages [split_len/16] (int32) or, for contiguous rows, vbuf [waves][16][kVRow] (16-bit)
+constexpr int kVRow = 128 + 16;  // vbuf row: 128 dims and 16 of padding (the transposed reads' banks)
 __host__ __device__ inline size_t lut_floats(const ssq_decode_args& a, int RP) {
     return (size_t)a.n_blocks * lut_nc(a) * RP;
 }
@@ -44,17 +52,111 @@ __host__ __device__ inline size_t pstrip_offset(const ssq_decode_args& a, int RP
 __host__ __device__ inline size_t pages_offset(const ssq_decode_args& a, int RP) {
     return pstrip_offset(a, RP) + (size_t)kWaves * RP * kTileTok / 2;
 }
-inline size_t mfma_smem(const ssq_decode_args& a, int RP, int split_len) {
-    const size_t main = pages_offset(a, RP) + (size_t)split_len / kPage;
+inline size_t mfma_smem(const ssq_decode_args& a, int RP, int split_len, bool ct = false) {
+    const size_t main = pages_offset(a, RP) + (ct ? (size_t)kWaves * 16 * kVRow / 2 : (size_t)split_len / kPage);
     const size_t merge = (size_t)kWaves * RP * (a.value_dim + 2);
     return (main > merge ? main : merge) * sizeof(float);
 }
 
+// Contiguous rows (codes [B, Hkv, T, nb] bytes, V [B, Hkv, T, 128]): cb0 and vb0 (bytes) point at the
+// split's first token of this (batch, KV head).  A lane loads its token's code row; the values arrive
+// as four 16-token chunks, chunk c in the flat registers 4c .. 4c + 3 of R.v, register 4c + i holding
+// dims 8 (lane % 16) .. + 7 of token 16c + 4i + lane / 16 (16 lanes read one 256-byte row).  Tokens
+// past the split's end read its last token: finite values, given probability 0.  Offsets from the
+// tile's first token are 32-bit (the plan keeps 64 tokens' strides below 2^31 bytes).
+template <int NB, int DT>
+__device__ __forceinline__ void issue_tile_ct(const ssq_decode_args& a, int t_begin, int t_end, int tile, int lane,
+                                              const uint8_t* cb0, const uint8_t* vb0, TileRegs<NB, DT, 0>& R) {
+    static_assert(DT == 8, "contiguous LUT tiles carry 128-dim values");
+    const int rel = tile * kTileTok;
+    const int lim = t_end - 1 - t_begin - rel;  // the split's last token, from the tile's first (>= 0)
+    const uint8_t* ctile = cb0 + (int64_t)rel * a.c_st;
+    const uint8_t* vtile = vb0 + (int64_t)rel * 2 * a.v_st;
+    const uint32_t coff = (uint32_t)min(lane, lim) * (uint32_t)a.c_st;
+    if constexpr (NB >= 16) {
+#pragma unroll
+        for (int i = 0; i < NB / 16; ++i) R.c[i] = *reinterpret_cast<const uint4*>(ctile + coff + 16 * i);
+    } else {
+        R.c8 = *reinterpret_cast<const uint2*>(ctile + coff);
+    }
+    const uint32_t vst = 2u * (uint32_t)a.v_st, dcol = 16u * (uint32_t)(lane & 15);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const uint32_t tok = (uint32_t)min(16 * (k >> 2) + 4 * (k & 3) + (lane >> 4), lim);
+        const uint32_t off = tok * vst + dcol;  // one 32-bit offset: the uniform-base load form
+        R.v[k >> 3][k & 7] = load_stream(reinterpret_cast<const uint16_t*>(vtile + off));
+    }
+}
 
-template <int RP, int DT, int VT, int NB, int NC, int PB>
-__device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* lut, uint16_t* pstrip, int b, int kv,
-                                             int t_begin, int t_end, int tile, int lane, TileRegs<NB, DT, PB>& R,
-                                             float (&m_run)[RP], float (&l_lane)[RP], v4f (&acc)[DT]) {
+// the wave's LDS writes before this point are seen by its reads after it (an ordering point for the
+// compiler: one wave's LDS operations execute in order)
+__device__ __forceinline__ void lds_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ v4f mfma16_bf16(const uint2& a, const uint2& b, v4f c) {
+    typedef short v4s_t __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(v4s_t, a), __builtin_bit_cast(v4s_t, b), c, 0,
+                                                     0, 0);
+}
+__device__ __forceinline__ v4f mfma16_f16(const uint2& a, const uint2& b, v4f c) {
+    typedef _Float16 v4h_t __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4h_t, a), __builtin_bit_cast(v4h_t, b), c, 0, 0,
+                                                 0);
+}
+
+// P.V over a contiguous tile (after tile_probs): per 16-token chunk, the chunk's values go row-major
+// into the wave's LDS buffer [16][kVRow] and come back transposed with ds_read_b64_tr_b16 (within
+// each 16-lane group g = lane / 16, lane l reads 4 elements of row 4g + l / 4 and receives dim
+// 16 dt + l of rows 4g .. 4g + 3): the B operand of v_mfma_f32_16x16x16, tokens 4g .. 4g + 3 of one
+// dim.  A = P [16 rows x 16 tokens] from the strip.  The 16-element row padding puts a group's four
+// rows on distinct LDS banks.
+template <int RP, int DT, int VT, int NB>
+__device__ __forceinline__ void tile_pv_ct(const uint16_t* pstrip, uint16_t* vbuf, int lane,
+                                           const TileRegs<NB, DT, 0>& R, v4f (&acc)[DT]) {
+    typedef short v4s_t __attribute__((ext_vector_type(4)));
+    const int l16 = lane & 15, lg = lane >> 4;
+    const uint16_t* src = vbuf + (4 * lg + (l16 >> 2)) * kVRow + 4 * (l16 & 3);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int k = 4 * c + i;
+            *reinterpret_cast<uint4*>(vbuf + (4 * i + lg) * kVRow + 8 * l16) = R.v[k >> 3][k & 7];
+        }
+        lds_wave_sync();
+        uint2 af = make_uint2(0, 0);
+        if (l16 < RP) af = *reinterpret_cast<const uint2*>(pstrip + l16 * kTileTok + 16 * c + 4 * lg);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const v4s_t bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) v4s_t*)(src + 16 * dt));
+            const uint2 b2 = __builtin_bit_cast(uint2, bv);
+            acc[dt] = VT == SSQ_BF16 ? mfma16_bf16(af, b2, acc[dt]) : mfma16_f16(af, b2, acc[dt]);
+        }
+        lds_wave_sync();  // the chunk's transposed reads are done before the next chunk's writes
+    }
+}
+
+// one tile's loads: contiguous rows (CT) or pages
+template <bool CT, int NB, int DT, int PB>
+__device__ __forceinline__ void issue_any(const ssq_decode_args& a, const int* pages, int t_begin, int t_end, int tile,
+                                          int lane, const uint8_t* cbase, const uint16_t* vbase, const uint8_t* cb0,
+                                          const uint8_t* vb0, TileRegs<NB, DT, PB>& R) {
+    if constexpr (CT) {
+        issue_tile_ct<NB, DT>(a, t_begin, t_end, tile, lane, cb0, vb0, R);
+    } else {
+        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, tile, lane, cbase, vbase, R);
+    }
+}
+
+template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT = false>
+__device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* lut, uint16_t* pstrip, uint16_t* vbuf,
+                                             int b, int kv, int t_begin, int t_end, int tile, int lane,
+                                             TileRegs<NB, DT, PB>& R, float (&m_run)[RP], float (&l_lane)[RP],
+                                             v4f (&acc)[DT]) {
     const int t0 = t_begin + tile * kTileTok;
     float s[RP];
 #pragma unroll
@@ -115,7 +217,12 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
             }
         }
     }
-    tile_softmax_pv<RP, DT, VT, NB, PB>(p, pstrip, b, kv, t0, t_end, lane, s, R, m_run, l_lane, acc);
+    if constexpr (CT) {
+        tile_probs<RP, DT, VT>(p, pstrip, b, kv, t0, t_end, lane, s, m_run, l_lane, acc);
+        tile_pv_ct<RP, DT, VT, NB>(pstrip, vbuf, lane, R, acc);
+    } else {
+        tile_softmax_pv<RP, DT, VT, NB, PB>(p, pstrip, b, kv, t0, t_end, lane, s, R, m_run, l_lane, acc);
+    }
 }
 
 // vector of N floats from memory (N = 1, 2, 4 or a multiple of 4; 4N-byte aligned)
@@ -199,8 +306,8 @@ __device__ void build_lut_any(const float* __restrict__ cent, const float* __res
     }
 }
 
-// NC: LUT codewords per block (256, or 64); PB: packed code bits (0 = byte codes)
-template <int RP, int DT, int VT, int NB, int NC, int PB>
+// NC: LUT codewords per block (256, or 64); PB: packed code bits (0 = byte codes); CT: contiguous rows
+template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT>
 __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_decode_args& a = p.a;
@@ -214,7 +321,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     const int D = a.head_dim, bd = a.block_dim;
     const int row0 = blockIdx.z * p.rg;          // this workgroup's query rows: row0 .. row0 + nr - 1
     const int nr = min(p.rg, p.rows - row0);     // <= RP
-    const int T = min(a.seq_lens[b], a.seq_len);
+    const int T = CT ? a.seq_len : min(a.seq_lens[b], a.seq_len);
     const int t_begin = split * p.split_len;
     const int t_end = min(T, t_begin + p.split_len);
 
@@ -222,13 +329,14 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     float* qp = smem + lut_floats(a, RP);
     uint16_t* pstrip = reinterpret_cast<uint16_t*>(smem + pstrip_offset(a, RP)) + wave * RP * kTileTok;
     int* pages = reinterpret_cast<int*>(smem + pages_offset(a, RP));
+    uint16_t* vbuf = reinterpret_cast<uint16_t*>(smem + pages_offset(a, RP)) + wave * 16 * kVRow;  // CT
 
     // ---- prologue.  The query rows are loaded unpermuted (coalesced, independent of the
     // permutation) together with this thread's permutation entries and the first block-table
     // pass: one memory latency.  The rows are scaled into the LUT region (free until the LUT is
     // built), then permuted LDS-to-LDS into qp.
-    const int32_t* btab = a.block_table + (int64_t)b * a.bt_sb + t_begin / kPage;
-    const int n_pages = t_end > t_begin ? (t_end - t_begin + kPage - 1) / kPage : 0;
+    const int32_t* btab = CT ? nullptr : a.block_table + (int64_t)b * a.bt_sb + t_begin / kPage;
+    const int n_pages = !CT && t_end > t_begin ? (t_end - t_begin + kPage - 1) / kPage : 0;
     const float* cent = a.cent + (int64_t)kv * a.cent_sh;
     const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
     constexpr int kQP = (RP * 256 + kThreads - 1) / kThreads;  // head_dim <= 256 on this kernel
@@ -296,6 +404,9 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     const uint8_t* cbase = PB > 0 ? reinterpret_cast<const uint8_t*>(reinterpret_cast<const uint32_t*>(a.codes) +
                                                                      (int64_t)kv * a.c_sh)
                                   : a.codes + (int64_t)kv * a.c_sh;
+    const uint8_t* cb0 = a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)t_begin * a.c_st;  // CT
+    const uint8_t* vb0 = reinterpret_cast<const uint8_t*>(a.v) +
+                         2 * ((int64_t)b * a.v_sb + (int64_t)kv * a.v_sh + (int64_t)t_begin * a.v_st);  // CT
     const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
     TileRegs<NB, DT, PB> RA, RB;
     int tile = wave;
@@ -303,7 +414,8 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     // mostly from L2): every path then carries the same queue of outstanding loads, so the
     // compiler's vmcnt waits for the tile being computed never drain the tile behind it.
     const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
-    if (n_tiles > 0) issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, RA);
+    if (n_tiles > 0)
+        issue_any<CT, NB, DT, PB>(a, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, cb0, vb0, RA);
     switch (bd) {
         case 1: build_lut<RP, NB, 1, NC>(cent, qp, lut, D, tid); break;
         case 2: build_lut<RP, NB, 2, NC>(cent, qp, lut, D, tid); break;
@@ -325,22 +437,24 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
         // set; a wave issues its next tile once this one is consumed (the other waves' loads keep
         // the memory busy meanwhile)
         while (tile < n_tiles) {
-            compute_tile<RP, DT, VT, NB, NC, PB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane,
-                                                 acc);
+            compute_tile<RP, DT, VT, NB, NC, PB, CT>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RA, m_run,
+                                                     l_lane, acc);
             tile += kWaves;
             if (tile >= n_tiles) break;
-            issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, tile, lane, cbase, vbase, RA);
+            issue_any<CT, NB, DT, PB>(a, pages, t_begin, t_end, tile, lane, cbase, vbase, cb0, vb0, RA);
         }
     } else {
         while (tile < n_tiles) {
-            issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RB);
-            compute_tile<RP, DT, VT, NB, NC, PB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RA, m_run, l_lane,
-                                                 acc);
+            issue_any<CT, NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, cb0,
+                                      vb0, RB);
+            compute_tile<RP, DT, VT, NB, NC, PB, CT>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RA, m_run,
+                                                     l_lane, acc);
             tile += kWaves;
             if (tile >= n_tiles) break;
-            issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RA);
-            compute_tile<RP, DT, VT, NB, NC, PB>(p, lut, pstrip, b, kv, t_begin, t_end, tile, lane, RB, m_run, l_lane,
-                                                 acc);
+            issue_any<CT, NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, cb0,
+                                      vb0, RA);
+            compute_tile<RP, DT, VT, NB, NC, PB, CT>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RB, m_run,
+                                                     l_lane, acc);
             tile += kWaves;
         }
     }
@@ -396,9 +510,9 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     }
 }
 
-template <int RP, int DT, int VT, int NB, int NC = kNC, int PB = 0>
+template <int RP, int DT, int VT, int NB, int NC = kNC, int PB = 0, bool CT = false>
 int launch(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
-    auto kern = k_decode_mfma<RP, DT, VT, NB, NC, PB>;
+    auto kern = k_decode_mfma<RP, DT, VT, NB, NC, PB, CT>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_mfma)");
     if (rc) return rc;
     dim3 grid(mp.a.batch * mp.a.num_kv_heads, pl.n_splits, pl.n_groups);
@@ -449,6 +563,28 @@ int lut64_rp(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
     }
 }
 
+// contiguous rows (128-dim values, 256-codeword LUT, byte codes): at most 8 rows per LUT
+template <int RP, int VT>
+int launch_ct_nb(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
+    switch (mp.a.n_blocks) {
+        case 8: return launch<RP, 8, VT, 8, kNC, 0, true>(mp, pl, st);
+        case 16: if constexpr (RP <= 8) return launch<RP, 8, VT, 16, kNC, 0, true>(mp, pl, st); break;
+        case 32: if constexpr (RP <= 4) return launch<RP, 8, VT, 32, kNC, 0, true>(mp, pl, st); break;
+        default: if constexpr (RP <= 2) return launch<RP, 8, VT, 64, kNC, 0, true>(mp, pl, st); break;
+    }
+    return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode: LUT of %d rows x %d blocks exceeds LDS", RP, mp.a.n_blocks);
+}
+template <int VT>
+int launch_ct(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
+    switch (pl.RP) {
+        case 1: return launch_ct_nb<1, VT>(mp, pl, st);
+        case 2: return launch_ct_nb<2, VT>(mp, pl, st);
+        case 4: return launch_ct_nb<4, VT>(mp, pl, st);
+        case 8: return launch_ct_nb<8, VT>(mp, pl, st);
+        default: return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode: %d rows per contiguous LUT", pl.RP);
+    }
+}
+
 }  // namespace
 
 // the instantiation units: the 256-codeword LUT kernel by row count, and the 64-codeword one
@@ -458,3 +594,5 @@ SSQ_MFMA_UNIT(ssq_mfma_lut_rp2);
 SSQ_MFMA_UNIT(ssq_mfma_lut_rp4);
 SSQ_MFMA_UNIT(ssq_mfma_lut_rp8_16);
 SSQ_MFMA_UNIT(ssq_mfma_lut64);
+SSQ_MFMA_UNIT(ssq_mfma_lut_ct_bf16);
+SSQ_MFMA_UNIT(ssq_mfma_lut_ct_f16);

@@ -24,7 +24,10 @@ bool lut64_shape(const ssq_decode_args& a, int RP, int DT) {
 }
 
 bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
-    if (a->layout != SSQ_PAGED || a->page_size != kPage) return false;
+    // contiguous rows take this kernel (CT) for 128-dim values past head_dim 64, which the contiguous
+    // MFMA kernel (ssq_decode_contig.hip) serves
+    const bool ct = a->layout == SSQ_CONTIGUOUS;
+    if (!ct && (a->layout != SSQ_PAGED || a->page_size != kPage)) return false;
     // Codes: bytes, 8-bit words (the byte rows, strides scaled to bytes), or 4- / 6-bit words.
     // The LUT kernel serves 256-codeword codebooks with byte codes, and 64-codeword codebooks
     // with byte or 6-bit codes (bf16 V, 2-8 rows, 16-64 blocks: lut64_shape); the 4x4-MFMA-scores
@@ -38,6 +41,15 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;  // float4 codeword loads
     if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32 && a->n_blocks != 64) return false;
     if (a->head_dim > 256) return false;  // query staging covers at most 256 dims per row
+    if (ct) {
+        if (a->head_dim == 64 || a->value_dim != 128 || a->kernel == 4) return false;
+        if (a->n_centroids != kNC || (cbits != 0 && cbits != 8)) return false;
+        // tile loads take 32-bit byte offsets from the tile's first token, token strides >= 0
+        const int64_t kLim = (int64_t)1 << 31;
+        if (a->c_st < 0 || a->v_st < 0) return false;
+        if ((int64_t)kTileTok * a->c_st * (cbits == 8 ? 4 : 1) + 64 >= kLim) return false;
+        if ((int64_t)kTileTok * 2 * a->v_st + 256 >= kLim) return false;
+    }
     if (cbits == 4 || cbits == 6) {  // word loads
         if ((uintptr_t)a->codes % 4) return false;
     } else {  // code rows: 8-byte (nb 8) or 16-byte (nb >= 16) vector loads
@@ -54,7 +66,8 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     const int rows = (a->num_q_heads / a->num_kv_heads) * a->q_len;
     if (rows > 64) return false;
     const int lcap = 32768 / (a->n_blocks * lut_nc(*a));  // rows per 128 KiB LUT, a power of two
-    const int cap = lcap < 16 ? lcap : 16;
+    const int rcap = ct ? 8 : 16;  // contiguous: the V buffer leaves room for 8-row LUTs
+    const int cap = lcap < rcap ? lcap : rcap;
     pl.rg = rows < cap ? rows : cap;
     pl.n_groups = (rows + pl.rg - 1) / pl.rg;
     pl.RP = pow2_at_least(pl.rg);
@@ -64,10 +77,11 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     // Where the LUT needs row groups (or cannot serve the codes), the 4x4-MFMA-scores kernel serves
     // up to 16 rows per pass over the pages instead (its codebook is head_dim x nc fp32 whatever
     // the block size); kernel 4 asks for it wherever it applies
-    const bool q4_ok = ssq_decode_q4_shape(a);
+    const bool q4_ok = !ct && ssq_decode_q4_shape(a);
     if (a->kernel == 4 && !q4_ok) return false;
     if (!lut_ok && !q4_ok) return false;
-    pl.q4 = a->kernel == 4 || !lut_ok || (pl.n_groups > 1 && q4_ok);
+    pl.ct = ct;
+    pl.q4 = !ct && (a->kernel == 4 || !lut_ok || (pl.n_groups > 1 && q4_ok));
     if (pl.q4) {
         pl.rg = rows < 16 ? rows : 16;
         pl.n_groups = (rows + 15) / 16;
@@ -84,13 +98,13 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     pl.split_len = tiles_per_split * kTileTok;
     // the split's block-table slice lives in LDS too: long contexts split until it fits
     while (tiles_per_split > 1 &&
-           (pl.q4 ? ssq_decode_q4_smem(a, pl.rg, pl.split_len) : mfma_smem(*a, pl.RP, pl.split_len)) > kMaxSmem) {
+           (pl.q4 ? ssq_decode_q4_smem(a, pl.rg, pl.split_len) : mfma_smem(*a, pl.RP, pl.split_len, ct)) > kMaxSmem) {
         tiles_per_split = (tiles_per_split + 1) / 2;
         pl.split_len = tiles_per_split * kTileTok;
     }
     pl.n_splits = (a->seq_len + pl.split_len - 1) / pl.split_len;
     if (pl.n_splits < 1) pl.n_splits = 1;
-    pl.smem = pl.q4 ? ssq_decode_q4_smem(a, pl.rg, pl.split_len) : mfma_smem(*a, pl.RP, pl.split_len);
+    pl.smem = pl.q4 ? ssq_decode_q4_smem(a, pl.rg, pl.split_len) : mfma_smem(*a, pl.RP, pl.split_len, ct);
     if (pl.smem > kMaxSmem) return false;
     const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
     pl.ws_bytes = pl.n_splits > 1 ? (size_t)pl.n_splits * n_rows_all * (a->value_dim + 2) * 4 : 0;
@@ -134,6 +148,12 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
     int rc;
     if (pl.q4) {
         rc = ssq_decode_q4_launch(mp, dim3(mp.a.batch * mp.a.num_kv_heads, pl.n_splits, pl.n_groups), st);
+        if (rc) return rc;
+        if (pl.n_splits > 1) rc = ssq_launch_merge(*a, pl.n_splits, mp.ws_o, mp.ws_m, mp.ws_l, st);
+        return rc;
+    }
+    if (pl.ct) {
+        rc = a->v_dtype == SSQ_BF16 ? ssq_mfma_lut_ct_bf16(mp, pl, st) : ssq_mfma_lut_ct_f16(mp, pl, st);
         if (rc) return rc;
         if (pl.n_splits > 1) rc = ssq_launch_merge(*a, pl.n_splits, mp.ws_o, mp.ws_m, mp.ws_l, st);
         return rc;

@@ -158,12 +158,12 @@ __device__ __forceinline__ void issue_tile(const ssq_decode_args& a, const int* 
 }
 
 // After a tile's scores s[r] (row r, this lane's token t0 + lane): the raw-score store, the online
-// softmax update (wave-local), the probabilities cast to the value dtype through the wave's P strip
-// [RP][64], and P.V on v_mfma_f32_16x16x32 with V fragments from the tile's registers.
-template <int RP, int DT, int VT, int NB, int PB>
-__device__ __forceinline__ void tile_softmax_pv(const MfmaParams& p, uint16_t* pstrip, int b, int kv, int t0, int t_end,
-                                                int lane, const float (&s)[RP], TileRegs<NB, DT, PB>& R,
-                                                float (&m_run)[RP], float (&l_lane)[RP], v4f (&acc)[DT]) {
+// softmax update (wave-local) and the probabilities cast to the value dtype in the wave's P strip
+// [RP][64], visible to the whole wave on return.
+template <int RP, int DT, int VT>
+__device__ __forceinline__ void tile_probs(const MfmaParams& p, uint16_t* pstrip, int b, int kv, int t0, int t_end,
+                                           int lane, const float (&s)[RP], float (&m_run)[RP], float (&l_lane)[RP],
+                                           v4f (&acc)[DT]) {
     const ssq_decode_args& a = p.a;
     const int t = t0 + lane;
     const bool valid = t < t_end;
@@ -222,6 +222,14 @@ __device__ __forceinline__ void tile_softmax_pv(const MfmaParams& p, uint16_t* p
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// tile_probs, then P.V on v_mfma_f32_16x16x32 with V fragments from the tile's registers
+template <int RP, int DT, int VT, int NB, int PB>
+__device__ __forceinline__ void tile_softmax_pv(const MfmaParams& p, uint16_t* pstrip, int b, int kv, int t0, int t_end,
+                                                int lane, const float (&s)[RP], TileRegs<NB, DT, PB>& R,
+                                                float (&m_run)[RP], float (&l_lane)[RP], v4f (&acc)[DT]) {
+    tile_probs<RP, DT, VT>(p, pstrip, b, kv, t0, t_end, lane, s, m_run, l_lane, acc);
     const int arow = lane & 15;
     const int kchunk = 8 * (lane >> 4);
     const bool tail = t0 + kTileTok > t_end;  // wave-uniform: the tile holds the split's end

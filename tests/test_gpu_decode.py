@@ -441,6 +441,48 @@ def test_contiguous_running_max_patterns(pattern, splits):
     assert_rel(np_of(lse), rl, SCORE_TOL, f"lse {pattern}")
 
 
+# contiguous rows past head_dim 64 (128-dim values) on the LUT kernel, kernel 2: V tiles pass
+# through a per-wave LDS buffer 16 tokens at a time and come back transposed for the matrix cores
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,bd,T,vdt,splits,strided", [
+    (2, 32, 8, 1, 4, 777, torch.bfloat16, 0, False),   # Llama-shaped: 4 rows, 32 blocks
+    (2, 32, 8, 1, 4, 700, torch.bfloat16, 2, True),    # [B, T, Hkv, *] buffers viewed as [B, Hkv, T, *]
+    (2, 32, 8, 1, 2, 1000, torch.bfloat16, 3, False),  # 64 blocks: two row groups of 2
+    (1, 16, 2, 1, 8, 333, torch.float16, 0, False),    # 8 rows, 16 blocks
+    (2, 8, 8, 1, 4, 64, torch.bfloat16, 1, False),     # one row, exactly one tile
+    (2, 16, 4, 2, 4, 65, torch.bfloat16, 1, False),    # two query tokens: two row groups of 4; a tile + 1
+    (1, 12, 4, 1, 16, 1, torch.bfloat16, 0, False),    # 8 blocks of 16 dims (3 rows), one token
+])
+def test_contiguous_lut_kernel_128_dim(B, Hq, Hkv, Lq, bd, T, vdt, splits, strided):
+    log(f"contig LUT D128 B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} bd={bd} T={T} vdt={vdt} splits={splits} strided={strided}")
+    D = 128
+    cb = synthetic.make_codebook(Hkv, D, bd, 150 + bd + T)
+    g = torch.Generator().manual_seed(151 + T)
+    q = torch.randn(B, Hq, Lq, D, generator=g).to(torch.bfloat16)
+    if strided:
+        codes = torch.randint(0, 256, (B, T, Hkv, D // bd), generator=g, dtype=torch.uint8).transpose(1, 2)
+        v = torch.randn(B, T, Hkv, D, generator=g).to(vdt).transpose(1, 2)
+    else:
+        codes = torch.randint(0, 256, (B, Hkv, T, D // bd), generator=g, dtype=torch.uint8)
+        v = torch.randn(B, Hkv, T, D, generator=g).to(vdt)
+    scale = 1 / math.sqrt(D)
+    args = (q.to(DEV), codes.to(DEV), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+    if strided:
+        assert args[1].stride(2) == Hkv * (D // bd) and args[2].stride(2) == Hkv * D
+    out, lse, scores = hip_ops.decode(*args, scale=scale, return_lse=True, return_scores=True, kernel=2,
+                                      num_splits=splits)
+    vname = "bf16" if vdt == torch.bfloat16 else "f16"
+    ro, rs, rl = O.decode_attention(q.float().numpy(), codes.contiguous().numpy(), v.float().contiguous().numpy(),
+                                    cb.centroids.numpy(), cb.perm.numpy(), scale, "bf16", vname, return_scores=True)
+    assert_rel(np_of(out), ro, BF16_TOL, "out")
+    assert_rel(np_of(scores), rs, SCORE_TOL, "scores")
+    assert_rel(np_of(lse), rl, SCORE_TOL, "lse")
+    # the automatic choice is this kernel (bit-identical), and the generic kernel agrees
+    oa = np_of(hip_ops.decode(*args, scale=scale, num_splits=splits))
+    assert np.array_equal(oa, np_of(out))
+    og = np_of(hip_ops.decode(*args, scale=scale, kernel=1))
+    assert_rel(og, ro, BF16_TOL, "generic kernel")
+
+
 def test_contiguous_mfma_kernel_rejects_wide_passthrough():
     """More than 16 passthrough dims do not fit the kernel's passthrough pass: an explicit
     kernel 3 request is refused, and auto dispatch serves the call on the LUT kernel."""
