@@ -27,6 +27,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 // launch plan of the paged LUT kernel (and of the 4x4-MFMA-scores kernel it hands shapes to)
 struct SsqMfmaPlan {
     int RP, DT, split_len, n_splits;
@@ -64,10 +66,19 @@ inline size_t mfma_smem(const ssq_decode_args& a, int RP, int split_len, bool ct
 // dims 8 (lane % 16) .. + 7 of token 16c + 4i + lane / 16 (16 lanes read one 256-byte row).  Tokens
 // past the split's end read its last token: finite values, given probability 0.  Offsets from the
 // tile's first token are 32-bit (the plan keeps 64 tokens' strides below 2^31 bytes).
-template <int NB, int DT>
-__device__ __forceinline__ void issue_tile_ct(const ssq_decode_args& a, int t_begin, int t_end, int tile, int lane,
-                                              const uint8_t* cb0, const uint8_t* vb0, TileRegs<NB, DT, 0>& R) {
+// A contiguous tile's registers: the paged tile's, and with a mask (MK) the additive mask of each row
+// for this lane's token (rows past the workgroup's last one re-read that row's entry).
+template <int NB, int DT, int RP, bool MK>
+struct TileRegsCT : TileRegs<NB, DT, 0> {
+    float mk[MK ? RP : 1];
+};
+
+template <int NB, int DT, int RP, bool MK>
+__device__ __forceinline__ void issue_tile_ct(const MfmaParams& p, int b, int kv, int t_begin, int t_end, int tile,
+                                              int lane, const uint8_t* cb0, const uint8_t* vb0,
+                                              TileRegsCT<NB, DT, RP, MK>& R) {
     static_assert(DT == 8, "contiguous LUT tiles carry 128-dim values");
+    const ssq_decode_args& a = p.a;
     const int rel = tile * kTileTok;
     const int lim = t_end - 1 - t_begin - rel;  // the split's last token, from the tile's first (>= 0)
     const uint8_t* ctile = cb0 + (int64_t)rel * a.c_st;
@@ -85,6 +96,17 @@ __device__ __forceinline__ void issue_tile_ct(const ssq_decode_args& a, int t_be
         const uint32_t tok = (uint32_t)min(16 * (k >> 2) + 4 * (k & 3) + (lane >> 4), lim);
         const uint32_t off = tok * vst + dcol;  // one 32-bit offset: the uniform-base load form
         R.v[k >> 3][k & 7] = load_stream(reinterpret_cast<const uint16_t*>(vtile + off));
+    }
+    if constexpr (MK) {
+        const int row0 = blockIdx.z * p.rg, nr = min(p.rg, p.rows - row0);
+        const int64_t t = t_begin + rel + min(lane, lim);
+#pragma unroll
+        for (int r = 0; r < RP; ++r) {
+            const int rr = row0 + min(r, nr - 1);
+            const int g = rr / a.q_len, qi = rr - g * a.q_len;
+            const int h = kv * p.G + g;
+            R.mk[r] = a.mask[(int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qi * a.m_sl + t * a.m_st];
+        }
     }
 }
 
@@ -140,23 +162,22 @@ __device__ __forceinline__ void tile_pv_ct(const uint16_t* pstrip, uint16_t* vbu
     }
 }
 
-// one tile's loads: contiguous rows (CT) or pages
-template <bool CT, int NB, int DT, int PB>
-__device__ __forceinline__ void issue_any(const ssq_decode_args& a, const int* pages, int t_begin, int t_end, int tile,
-                                          int lane, const uint8_t* cbase, const uint16_t* vbase, const uint8_t* cb0,
-                                          const uint8_t* vb0, TileRegs<NB, DT, PB>& R) {
+// one tile's loads: contiguous rows (CT, with the mask when MK) or pages
+template <bool CT, bool MK, int RP, int NB, int DT, int PB, class TR>
+__device__ __forceinline__ void issue_any(const MfmaParams& p, int b, int kv, const int* pages, int t_begin, int t_end,
+                                          int tile, int lane, const uint8_t* cbase, const uint16_t* vbase,
+                                          const uint8_t* cb0, const uint8_t* vb0, TR& R) {
     if constexpr (CT) {
-        issue_tile_ct<NB, DT>(a, t_begin, t_end, tile, lane, cb0, vb0, R);
+        issue_tile_ct<NB, DT, RP, MK>(p, b, kv, t_begin, t_end, tile, lane, cb0, vb0, R);
     } else {
-        issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, tile, lane, cbase, vbase, R);
+        issue_tile<NB, DT, PB>(p.a, pages, t_begin, t_end, tile, lane, cbase, vbase, R);
     }
 }
 
-template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT = false>
+template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT, bool MK, class TR>
 __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* lut, uint16_t* pstrip, uint16_t* vbuf,
-                                             int b, int kv, int t_begin, int t_end, int tile, int lane,
-                                             TileRegs<NB, DT, PB>& R, float (&m_run)[RP], float (&l_lane)[RP],
-                                             v4f (&acc)[DT]) {
+                                             int b, int kv, int t_begin, int t_end, int tile, int lane, TR& R,
+                                             float (&m_run)[RP], float (&l_lane)[RP], v4f (&acc)[DT]) {
     const int t0 = t_begin + tile * kTileTok;
     float s[RP];
 #pragma unroll
@@ -218,6 +239,11 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
         }
     }
     if constexpr (CT) {
+        if constexpr (MK) {
+            const int nr = min(p.rg, p.rows - (int)blockIdx.z * p.rg);
+#pragma unroll
+            for (int r = 0; r < RP; ++r) s[r] += r < nr ? R.mk[r] : 0.f;
+        }
         tile_probs<RP, DT, VT>(p, pstrip, b, kv, t0, t_end, lane, s, m_run, l_lane, acc);
         tile_pv_ct<RP, DT, VT, NB>(pstrip, vbuf, lane, R, acc);
     } else {
@@ -306,8 +332,9 @@ __device__ void build_lut_any(const float* __restrict__ cent, const float* __res
     }
 }
 
-// NC: LUT codewords per block (256, or 64); PB: packed code bits (0 = byte codes); CT: contiguous rows
-template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT>
+// NC: LUT codewords per block (256, or 64); PB: packed code bits (0 = byte codes); CT: contiguous rows,
+// MK: with an additive mask (contiguous rows only)
+template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT, bool MK>
 __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_decode_args& a = p.a;
@@ -408,14 +435,17 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     const uint8_t* vb0 = reinterpret_cast<const uint8_t*>(a.v) +
                          2 * ((int64_t)b * a.v_sb + (int64_t)kv * a.v_sh + (int64_t)t_begin * a.v_st);  // CT
     const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
-    TileRegs<NB, DT, PB> RA, RB;
+    static_assert(CT || !MK, "masks are read on the contiguous path only");
+    using Regs = std::conditional_t<CT, TileRegsCT<NB, DT, RP, MK>, TileRegs<NB, DT, PB>>;
+    Regs RA, RB;
     int tile = wave;
     // Tile loads are issued unconditionally (a wave past the last tile re-reads tile n_tiles-1,
     // mostly from L2): every path then carries the same queue of outstanding loads, so the
     // compiler's vmcnt waits for the tile being computed never drain the tile behind it.
     const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
     if (n_tiles > 0)
-        issue_any<CT, NB, DT, PB>(a, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, cb0, vb0, RA);
+        issue_any<CT, MK, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, cb0,
+                                          vb0, RA);
     switch (bd) {
         case 1: build_lut<RP, NB, 1, NC>(cent, qp, lut, D, tid); break;
         case 2: build_lut<RP, NB, 2, NC>(cent, qp, lut, D, tid); break;
@@ -437,24 +467,24 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
         // set; a wave issues its next tile once this one is consumed (the other waves' loads keep
         // the memory busy meanwhile)
         while (tile < n_tiles) {
-            compute_tile<RP, DT, VT, NB, NC, PB, CT>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RA, m_run,
-                                                     l_lane, acc);
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RA,
+                                                         m_run, l_lane, acc);
             tile += kWaves;
             if (tile >= n_tiles) break;
-            issue_any<CT, NB, DT, PB>(a, pages, t_begin, t_end, tile, lane, cbase, vbase, cb0, vb0, RA);
+            issue_any<CT, MK, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, tile, lane, cbase, vbase, cb0, vb0, RA);
         }
     } else {
         while (tile < n_tiles) {
-            issue_any<CT, NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, cb0,
-                                      vb0, RB);
-            compute_tile<RP, DT, VT, NB, NC, PB, CT>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RA, m_run,
-                                                     l_lane, acc);
+            issue_any<CT, MK, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
+                                              cbase, vbase, cb0, vb0, RB);
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RA,
+                                                         m_run, l_lane, acc);
             tile += kWaves;
             if (tile >= n_tiles) break;
-            issue_any<CT, NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, cb0,
-                                      vb0, RA);
-            compute_tile<RP, DT, VT, NB, NC, PB, CT>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RB, m_run,
-                                                     l_lane, acc);
+            issue_any<CT, MK, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
+                                              cbase, vbase, cb0, vb0, RA);
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RB,
+                                                         m_run, l_lane, acc);
             tile += kWaves;
         }
     }
@@ -510,9 +540,9 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     }
 }
 
-template <int RP, int DT, int VT, int NB, int NC = kNC, int PB = 0, bool CT = false>
+template <int RP, int DT, int VT, int NB, int NC = kNC, int PB = 0, bool CT = false, bool MK = false>
 int launch(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
-    auto kern = k_decode_mfma<RP, DT, VT, NB, NC, PB, CT>;
+    auto kern = k_decode_mfma<RP, DT, VT, NB, NC, PB, CT, MK>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_mfma)");
     if (rc) return rc;
     dim3 grid(mp.a.batch * mp.a.num_kv_heads, pl.n_splits, pl.n_groups);
@@ -563,24 +593,25 @@ int lut64_rp(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
     }
 }
 
-// contiguous rows (128-dim values, 256-codeword LUT, byte codes): at most 8 rows per LUT
-template <int RP, int VT>
+// contiguous rows (128-dim values, 256-codeword LUT, byte codes, MK: with a mask): at most 8 rows
+// per LUT
+template <int RP, int VT, bool MK>
 int launch_ct_nb(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
     switch (mp.a.n_blocks) {
-        case 8: return launch<RP, 8, VT, 8, kNC, 0, true>(mp, pl, st);
-        case 16: if constexpr (RP <= 8) return launch<RP, 8, VT, 16, kNC, 0, true>(mp, pl, st); break;
-        case 32: if constexpr (RP <= 4) return launch<RP, 8, VT, 32, kNC, 0, true>(mp, pl, st); break;
-        default: if constexpr (RP <= 2) return launch<RP, 8, VT, 64, kNC, 0, true>(mp, pl, st); break;
+        case 8: return launch<RP, 8, VT, 8, kNC, 0, true, MK>(mp, pl, st);
+        case 16: if constexpr (RP <= 8) return launch<RP, 8, VT, 16, kNC, 0, true, MK>(mp, pl, st); break;
+        case 32: if constexpr (RP <= 4) return launch<RP, 8, VT, 32, kNC, 0, true, MK>(mp, pl, st); break;
+        default: if constexpr (RP <= 2) return launch<RP, 8, VT, 64, kNC, 0, true, MK>(mp, pl, st); break;
     }
     return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode: LUT of %d rows x %d blocks exceeds LDS", RP, mp.a.n_blocks);
 }
-template <int VT>
+template <int VT, bool MK>
 int launch_ct(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
     switch (pl.RP) {
-        case 1: return launch_ct_nb<1, VT>(mp, pl, st);
-        case 2: return launch_ct_nb<2, VT>(mp, pl, st);
-        case 4: return launch_ct_nb<4, VT>(mp, pl, st);
-        case 8: return launch_ct_nb<8, VT>(mp, pl, st);
+        case 1: return launch_ct_nb<1, VT, MK>(mp, pl, st);
+        case 2: return launch_ct_nb<2, VT, MK>(mp, pl, st);
+        case 4: return launch_ct_nb<4, VT, MK>(mp, pl, st);
+        case 8: return launch_ct_nb<8, VT, MK>(mp, pl, st);
         default: return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode: %d rows per contiguous LUT", pl.RP);
     }
 }
@@ -596,3 +627,5 @@ SSQ_MFMA_UNIT(ssq_mfma_lut_rp8_16);
 SSQ_MFMA_UNIT(ssq_mfma_lut64);
 SSQ_MFMA_UNIT(ssq_mfma_lut_ct_bf16);
 SSQ_MFMA_UNIT(ssq_mfma_lut_ct_f16);
+SSQ_MFMA_UNIT(ssq_mfma_lut_ct_bf16_mask);
+SSQ_MFMA_UNIT(ssq_mfma_lut_ct_f16_mask);

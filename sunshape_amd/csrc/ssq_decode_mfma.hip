@@ -36,7 +36,7 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     if (cbits != 0 && cbits != 4 && cbits != 6 && cbits != 8) return false;
     if (a->n_centroids > kNC) return false;
     if (a->v == nullptr || (a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16)) return false;
-    if (a->mask != nullptr || a->heavy_mask[0] || a->heavy_mask[1]) return false;
+    if ((a->mask != nullptr && !ct) || a->heavy_mask[0] || a->heavy_mask[1]) return false;  // masks: contiguous only
     if (a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;  // float4 codeword loads
     if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32 && a->n_blocks != 64) return false;
@@ -153,7 +153,10 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
         return rc;
     }
     if (pl.ct) {
-        rc = a->v_dtype == SSQ_BF16 ? ssq_mfma_lut_ct_bf16(mp, pl, st) : ssq_mfma_lut_ct_f16(mp, pl, st);
+        if (a->mask)
+            rc = a->v_dtype == SSQ_BF16 ? ssq_mfma_lut_ct_bf16_mask(mp, pl, st) : ssq_mfma_lut_ct_f16_mask(mp, pl, st);
+        else
+            rc = a->v_dtype == SSQ_BF16 ? ssq_mfma_lut_ct_bf16(mp, pl, st) : ssq_mfma_lut_ct_f16(mp, pl, st);
         if (rc) return rc;
         if (pl.n_splits > 1) rc = ssq_launch_merge(*a, pl.n_splits, mp.ws_o, mp.ws_m, mp.ws_l, st);
         return rc;

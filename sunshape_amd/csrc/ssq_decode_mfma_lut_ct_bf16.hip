@@ -3,5 +3,5 @@
 #include "ssq_decode_mfma.h"
 
 SSQ_MFMA_UNIT(ssq_mfma_lut_ct_bf16) {
-    return launch_ct<SSQ_BF16>(mp, pl, st);
+    return launch_ct<SSQ_BF16, false>(mp, pl, st);
 }

@@ -3,5 +3,5 @@
 #include "ssq_decode_mfma.h"
 
 SSQ_MFMA_UNIT(ssq_mfma_lut_ct_f16) {
-    return launch_ct<SSQ_F16>(mp, pl, st);
+    return launch_ct<SSQ_F16, false>(mp, pl, st);
 }

@@ -483,6 +483,50 @@ def test_contiguous_lut_kernel_128_dim(B, Hq, Hkv, Lq, bd, T, vdt, splits, strid
     assert_rel(og, ro, BF16_TOL, "generic kernel")
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,bd,T,kind,splits", [
+    (2, 32, 8, 1, 4, 777, "rows", 0),      # per-(batch, head) padding and a finite bias
+    (2, 16, 4, 3, 4, 500, "causal", 1),    # three new tokens, HF's causal mask broadcast over batch and heads
+    (1, 32, 8, 2, 2, 300, "causal", 2),    # 64 blocks: row groups of 2, causal over two tokens
+    (2, 8, 8, 1, 8, 129, "random", 0),     # one row, 16 blocks, a fifth of the keys masked
+])
+def test_contiguous_lut_kernel_128_dim_masks(B, Hq, Hkv, Lq, bd, T, kind, splits):
+    """Additive masks on the contiguous 128-dim LUT kernel: read with each tile's codes, added to
+    the scores before the softmax (and in the returned scores)."""
+    log(f"contig LUT D128 mask B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} bd={bd} T={T} kind={kind} splits={splits}")
+    D = 128
+    cb = synthetic.make_codebook(Hkv, D, bd, 170 + T)
+    g = torch.Generator().manual_seed(171 + T)
+    q = torch.randn(B, Hq, Lq, D, generator=g).to(torch.bfloat16)
+    codes = torch.randint(0, 256, (B, Hkv, T, D // bd), generator=g, dtype=torch.uint8)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+    if kind == "rows":
+        mask = torch.zeros(B, Hq, Lq, T)
+        mask[0, :, :, :37] = float("-inf")
+        mask[1, 3:9, :, 500:] = -2.5
+    elif kind == "causal":
+        pos = torch.arange(T)
+        last = T - Lq + torch.arange(Lq)
+        mask = torch.zeros(1, 1, Lq, T).masked_fill(pos[None, :] > last[:, None], float("-inf"))
+    else:
+        mask = torch.where(torch.rand(B, Hq, Lq, T, generator=g) < 0.2, float("-inf"), 0.0)
+        mask[..., 0] = 0.0  # every row keeps a key
+    full = mask.expand(B, Hq, Lq, T).contiguous()
+    scale = 1 / math.sqrt(D)
+    args = (q.to(DEV), codes.to(DEV), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+    md = mask.to(DEV)
+    out, lse, scores = hip_ops.decode(*args, scale=scale, mask=md, return_lse=True, return_scores=True, kernel=2,
+                                      num_splits=splits)
+    ro, rs, rl = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
+                                    cb.perm.numpy(), scale, "bf16", "bf16", mask=full.numpy(), return_scores=True)
+    assert_rel(np_of(out), ro, BF16_TOL, "out")
+    fin = np.isfinite(rs)
+    assert np.array_equal(np.isfinite(np_of(scores)), fin)
+    assert_rel(np_of(scores)[fin], rs[fin], SCORE_TOL, "scores")
+    assert_rel(np_of(lse), rl, SCORE_TOL, "lse")
+    oa = np_of(hip_ops.decode(*args, scale=scale, mask=md, num_splits=splits))
+    assert np.array_equal(oa, np_of(out))
+
+
 def test_contiguous_mfma_kernel_rejects_wide_passthrough():
     """More than 16 passthrough dims do not fit the kernel's passthrough pass: an explicit
     kernel 3 request is refused, and auto dispatch serves the call on the LUT kernel."""
