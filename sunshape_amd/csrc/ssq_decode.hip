@@ -828,7 +828,8 @@ namespace {
 int pick_kernel(const ssq_decode_args* a) {
     if (a->kernel == 4) return 2;  // the paged MFMA path, with its 4x4-MFMA-scores kernel forced
     if (a->kernel != 0) return a->kernel;
-    if (a->v && ssq_decode_mfma_supported(a)) return 2;
+    // (the MFMA kernel's plan takes scores-only problems on contiguous rows past head_dim 64)
+    if (ssq_decode_mfma_supported(a)) return 2;
     // scores only or decode: the contiguous MFMA kernel where it applies (its 4x4-MFMA scores need no
     // per-workgroup LUT: config-2 scores 11.9 us against the LUT kernel's 18.3 us), else the generic one
     if (ssq_decode_contig_supported(a)) return 3;
@@ -867,7 +868,10 @@ extern "C" int ssq_attention_scores(const ssq_decode_args* a, void* stream) {
     SSQ_REQUIRE(a->v == nullptr && a->scores != nullptr, "scores-only call needs v == NULL and scores != NULL");
     if (a->seq_len == 0) return SSQ_OK;
     const int k = pick_kernel(a);
-    SSQ_UNSUPPORTED(k != 2, "the MFMA paged kernel computes decode, not scores only");
+    if (k == 2) {
+        SSQ_UNSUPPORTED(ssq_decode_mfma_supported(a), "MFMA LUT kernel does not support this scores-only problem");
+        return ssq_decode_mfma(a, nullptr, 0, (hipStream_t)stream);
+    }
     if (k == 3) {
         SSQ_UNSUPPORTED(ssq_decode_contig_supported(a), "contiguous MFMA kernel does not support this problem");
         return ssq_decode_contig(a, nullptr, 0, (hipStream_t)stream);

@@ -73,7 +73,7 @@ struct TileRegsCT : TileRegs<NB, DT, 0> {
     float mk[MK ? RP : 1];
 };
 
-template <int NB, int DT, int RP, bool MK>
+template <int NB, int DT, int RP, bool MK, bool NV>
 __device__ __forceinline__ void issue_tile_ct(const MfmaParams& p, int b, int kv, int t_begin, int t_end, int tile,
                                               int lane, const uint8_t* cb0, const uint8_t* vb0,
                                               TileRegsCT<NB, DT, RP, MK>& R) {
@@ -90,12 +90,14 @@ __device__ __forceinline__ void issue_tile_ct(const MfmaParams& p, int b, int kv
     } else {
         R.c8 = *reinterpret_cast<const uint2*>(ctile + coff);
     }
-    const uint32_t vst = 2u * (uint32_t)a.v_st, dcol = 16u * (uint32_t)(lane & 15);
+    if constexpr (!NV) {
+        const uint32_t vst = 2u * (uint32_t)a.v_st, dcol = 16u * (uint32_t)(lane & 15);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const uint32_t tok = (uint32_t)min(16 * (k >> 2) + 4 * (k & 3) + (lane >> 4), lim);
-        const uint32_t off = tok * vst + dcol;  // one 32-bit offset: the uniform-base load form
-        R.v[k >> 3][k & 7] = load_stream(reinterpret_cast<const uint16_t*>(vtile + off));
+        for (int k = 0; k < 16; ++k) {
+            const uint32_t tok = (uint32_t)min(16 * (k >> 2) + 4 * (k & 3) + (lane >> 4), lim);
+            const uint32_t off = tok * vst + dcol;  // one 32-bit offset: the uniform-base load form
+            R.v[k >> 3][k & 7] = load_stream(reinterpret_cast<const uint16_t*>(vtile + off));
+        }
     }
     if constexpr (MK) {
         const int row0 = blockIdx.z * p.rg, nr = min(p.rg, p.rows - row0);
@@ -162,19 +164,19 @@ __device__ __forceinline__ void tile_pv_ct(const uint16_t* pstrip, uint16_t* vbu
     }
 }
 
-// one tile's loads: contiguous rows (CT, with the mask when MK) or pages
-template <bool CT, bool MK, int RP, int NB, int DT, int PB, class TR>
+// one tile's loads: contiguous rows (CT, with the mask when MK, codes only when NV) or pages
+template <bool CT, bool MK, bool NV, int RP, int NB, int DT, int PB, class TR>
 __device__ __forceinline__ void issue_any(const MfmaParams& p, int b, int kv, const int* pages, int t_begin, int t_end,
                                           int tile, int lane, const uint8_t* cbase, const uint16_t* vbase,
                                           const uint8_t* cb0, const uint8_t* vb0, TR& R) {
     if constexpr (CT) {
-        issue_tile_ct<NB, DT, RP, MK>(p, b, kv, t_begin, t_end, tile, lane, cb0, vb0, R);
+        issue_tile_ct<NB, DT, RP, MK, NV>(p, b, kv, t_begin, t_end, tile, lane, cb0, vb0, R);
     } else {
         issue_tile<NB, DT, PB>(p.a, pages, t_begin, t_end, tile, lane, cbase, vbase, R);
     }
 }
 
-template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT, bool MK, class TR>
+template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT, bool MK, bool NV, class TR>
 __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* lut, uint16_t* pstrip, uint16_t* vbuf,
                                              int b, int kv, int t_begin, int t_end, int tile, int lane, TR& R,
                                              float (&m_run)[RP], float (&l_lane)[RP], v4f (&acc)[DT]) {
@@ -188,10 +190,10 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
         // block order from 0.  Lanes past the end gather too (their codes are a valid token's)
         // and are dropped by tile_softmax_pv.
         constexpr int KB = RP >= 8 ? 4 : 8;
-        constexpr int NV = RP >= 4 ? RP / 4 : 1;  // float4 (or one float2 / float) per block
+        constexpr int NVEC = RP >= 4 ? RP / 4 : 1;  // float4 (or one float2 / float) per block
 #pragma unroll
         for (int b0 = 0; b0 < NB; b0 += KB) {
-            float4 ev[KB][NV];
+            float4 ev[KB][NVEC];
 #pragma unroll
             for (int k = 0; k < KB; ++k) {
                 const int blk = b0 + k;
@@ -214,7 +216,7 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
                 const float* e = lut + ((size_t)blk * NC + code) * RP;
                 if (RP >= 4) {
 #pragma unroll
-                    for (int j = 0; j < NV; ++j) ev[k][j] = *reinterpret_cast<const float4*>(e + 4 * j);
+                    for (int j = 0; j < NVEC; ++j) ev[k][j] = *reinterpret_cast<const float4*>(e + 4 * j);
                 } else if (RP == 2) {
                     const float2 v = *reinterpret_cast<const float2*>(e);
                     ev[k][0] = make_float4(v.x, v.y, 0.f, 0.f);
@@ -226,7 +228,7 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
             for (int k = 0; k < KB; ++k) {
                 if (RP >= 4) {
 #pragma unroll
-                    for (int j = 0; j < NV; ++j) {
+                    for (int j = 0; j < NVEC; ++j) {
                         s[4 * j] += ev[k][j].x; s[4 * j + 1] += ev[k][j].y;
                         s[4 * j + 2] += ev[k][j].z; s[4 * j + 3] += ev[k][j].w;
                     }
@@ -238,7 +240,9 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
             }
         }
     }
-    if constexpr (CT) {
+    if constexpr (NV) {  // scores only
+        tile_store_scores<RP>(p, b, kv, t0, t_end, lane, s);
+    } else if constexpr (CT) {
         if constexpr (MK) {
             const int nr = min(p.rg, p.rows - (int)blockIdx.z * p.rg);
 #pragma unroll
@@ -333,8 +337,8 @@ __device__ void build_lut_any(const float* __restrict__ cent, const float* __res
 }
 
 // NC: LUT codewords per block (256, or 64); PB: packed code bits (0 = byte codes); CT: contiguous rows,
-// MK: with an additive mask (contiguous rows only)
-template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT, bool MK>
+// MK: with an additive mask, NV: scores only (both on contiguous rows only)
+template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT, bool MK, bool NV>
 __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_decode_args& a = p.a;
@@ -435,7 +439,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     const uint8_t* vb0 = reinterpret_cast<const uint8_t*>(a.v) +
                          2 * ((int64_t)b * a.v_sb + (int64_t)kv * a.v_sh + (int64_t)t_begin * a.v_st);  // CT
     const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
-    static_assert(CT || !MK, "masks are read on the contiguous path only");
+    static_assert(CT || (!MK && !NV), "masks and scores-only launches are contiguous-path variants");
     using Regs = std::conditional_t<CT, TileRegsCT<NB, DT, RP, MK>, TileRegs<NB, DT, PB>>;
     Regs RA, RB;
     int tile = wave;
@@ -444,8 +448,8 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     // compiler's vmcnt waits for the tile being computed never drain the tile behind it.
     const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
     if (n_tiles > 0)
-        issue_any<CT, MK, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, cb0,
-                                          vb0, RA);
+        issue_any<CT, MK, NV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile, last_tile), lane, cbase,
+                                              vbase, cb0, vb0, RA);
     switch (bd) {
         case 1: build_lut<RP, NB, 1, NC>(cent, qp, lut, D, tid); break;
         case 2: build_lut<RP, NB, 2, NC>(cent, qp, lut, D, tid); break;
@@ -467,27 +471,30 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
         // set; a wave issues its next tile once this one is consumed (the other waves' loads keep
         // the memory busy meanwhile)
         while (tile < n_tiles) {
-            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RA,
-                                                         m_run, l_lane, acc);
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
+                                                             RA, m_run, l_lane, acc);
             tile += kWaves;
             if (tile >= n_tiles) break;
-            issue_any<CT, MK, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, tile, lane, cbase, vbase, cb0, vb0, RA);
+            issue_any<CT, MK, NV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, tile, lane, cbase, vbase, cb0, vb0,
+                                                  RA);
         }
     } else {
         while (tile < n_tiles) {
-            issue_any<CT, MK, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
-                                              cbase, vbase, cb0, vb0, RB);
-            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RA,
-                                                         m_run, l_lane, acc);
+            issue_any<CT, MK, NV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
+                                                  cbase, vbase, cb0, vb0, RB);
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
+                                                             RA, m_run, l_lane, acc);
             tile += kWaves;
             if (tile >= n_tiles) break;
-            issue_any<CT, MK, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
-                                              cbase, vbase, cb0, vb0, RA);
-            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane, RB,
-                                                         m_run, l_lane, acc);
+            issue_any<CT, MK, NV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
+                                                  cbase, vbase, cb0, vb0, RA);
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
+                                                             RB, m_run, l_lane, acc);
             tile += kWaves;
         }
     }
+
+    if constexpr (NV) return;  // scores only: every tile's scores are stored
 
     // ---- merge the waves' (m, l, O) through LDS (the LUT is no longer needed)
     float l_w[RP];
@@ -540,9 +547,10 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     }
 }
 
-template <int RP, int DT, int VT, int NB, int NC = kNC, int PB = 0, bool CT = false, bool MK = false>
+template <int RP, int DT, int VT, int NB, int NC = kNC, int PB = 0, bool CT = false, bool MK = false,
+          bool NV = false>
 int launch(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
-    auto kern = k_decode_mfma<RP, DT, VT, NB, NC, PB, CT, MK>;
+    auto kern = k_decode_mfma<RP, DT, VT, NB, NC, PB, CT, MK, NV>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_mfma)");
     if (rc) return rc;
     dim3 grid(mp.a.batch * mp.a.num_kv_heads, pl.n_splits, pl.n_groups);
@@ -593,25 +601,25 @@ int lut64_rp(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
     }
 }
 
-// contiguous rows (128-dim values, 256-codeword LUT, byte codes, MK: with a mask): at most 8 rows
-// per LUT
-template <int RP, int VT, bool MK>
+// contiguous rows (128-dim values, 256-codeword LUT, byte codes; MK: with a mask, NV: scores only):
+// at most 8 rows per LUT
+template <int RP, int VT, bool MK, bool NV>
 int launch_ct_nb(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
     switch (mp.a.n_blocks) {
-        case 8: return launch<RP, 8, VT, 8, kNC, 0, true, MK>(mp, pl, st);
-        case 16: if constexpr (RP <= 8) return launch<RP, 8, VT, 16, kNC, 0, true, MK>(mp, pl, st); break;
-        case 32: if constexpr (RP <= 4) return launch<RP, 8, VT, 32, kNC, 0, true, MK>(mp, pl, st); break;
-        default: if constexpr (RP <= 2) return launch<RP, 8, VT, 64, kNC, 0, true, MK>(mp, pl, st); break;
+        case 8: return launch<RP, 8, VT, 8, kNC, 0, true, MK, NV>(mp, pl, st);
+        case 16: if constexpr (RP <= 8) return launch<RP, 8, VT, 16, kNC, 0, true, MK, NV>(mp, pl, st); break;
+        case 32: if constexpr (RP <= 4) return launch<RP, 8, VT, 32, kNC, 0, true, MK, NV>(mp, pl, st); break;
+        default: if constexpr (RP <= 2) return launch<RP, 8, VT, 64, kNC, 0, true, MK, NV>(mp, pl, st); break;
     }
     return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode: LUT of %d rows x %d blocks exceeds LDS", RP, mp.a.n_blocks);
 }
-template <int VT, bool MK>
+template <int VT, bool MK, bool NV = false>
 int launch_ct(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
     switch (pl.RP) {
-        case 1: return launch_ct_nb<1, VT, MK>(mp, pl, st);
-        case 2: return launch_ct_nb<2, VT, MK>(mp, pl, st);
-        case 4: return launch_ct_nb<4, VT, MK>(mp, pl, st);
-        case 8: return launch_ct_nb<8, VT, MK>(mp, pl, st);
+        case 1: return launch_ct_nb<1, VT, MK, NV>(mp, pl, st);
+        case 2: return launch_ct_nb<2, VT, MK, NV>(mp, pl, st);
+        case 4: return launch_ct_nb<4, VT, MK, NV>(mp, pl, st);
+        case 8: return launch_ct_nb<8, VT, MK, NV>(mp, pl, st);
         default: return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode: %d rows per contiguous LUT", pl.RP);
     }
 }
@@ -629,3 +637,4 @@ SSQ_MFMA_UNIT(ssq_mfma_lut_ct_bf16);
 SSQ_MFMA_UNIT(ssq_mfma_lut_ct_f16);
 SSQ_MFMA_UNIT(ssq_mfma_lut_ct_bf16_mask);
 SSQ_MFMA_UNIT(ssq_mfma_lut_ct_f16_mask);
+SSQ_MFMA_UNIT(ssq_mfma_lut_ct_scores);

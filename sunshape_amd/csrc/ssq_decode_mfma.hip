@@ -35,20 +35,23 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     const int cbits = a->code_bits;
     if (cbits != 0 && cbits != 4 && cbits != 6 && cbits != 8) return false;
     if (a->n_centroids > kNC) return false;
-    if (a->v == nullptr || (a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16)) return false;
+    // scores only (no values, no mask): contiguous rows
+    const bool nv = a->v == nullptr;
+    if (nv && (!ct || !a->scores || a->mask)) return false;
+    if (!nv && a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16) return false;
     if ((a->mask != nullptr && !ct) || a->heavy_mask[0] || a->heavy_mask[1]) return false;  // masks: contiguous only
-    if (a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;
+    if (!nv && a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;  // float4 codeword loads
     if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32 && a->n_blocks != 64) return false;
     if (a->head_dim > 256) return false;  // query staging covers at most 256 dims per row
     if (ct) {
-        if (a->head_dim == 64 || a->value_dim != 128 || a->kernel == 4) return false;
+        if (a->head_dim == 64 || (!nv && a->value_dim != 128) || a->kernel == 4) return false;
         if (a->n_centroids != kNC || (cbits != 0 && cbits != 8)) return false;
         // tile loads take 32-bit byte offsets from the tile's first token, token strides >= 0
         const int64_t kLim = (int64_t)1 << 31;
-        if (a->c_st < 0 || a->v_st < 0) return false;
+        if (a->c_st < 0 || (!nv && a->v_st < 0)) return false;
         if ((int64_t)kTileTok * a->c_st * (cbits == 8 ? 4 : 1) + 64 >= kLim) return false;
-        if ((int64_t)kTileTok * 2 * a->v_st + 256 >= kLim) return false;
+        if (!nv && (int64_t)kTileTok * 2 * a->v_st + 256 >= kLim) return false;
     }
     if (cbits == 4 || cbits == 6) {  // word loads
         if ((uintptr_t)a->codes % 4) return false;
@@ -58,7 +61,7 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
         if ((a->c_st * cs) % cal || (a->c_sb * cs) % cal || (a->c_sh * cs) % cal || (uintptr_t)a->codes % cal)
             return false;
     }
-    if ((uintptr_t)a->v % 16 || (a->v_sb * 2) % 16 || (a->v_sh * 2) % 16 || (a->v_st * 2) % 16) return false;
+    if (!nv && ((uintptr_t)a->v % 16 || (a->v_sb * 2) % 16 || (a->v_sh * 2) % 16 || (a->v_st * 2) % 16)) return false;
     // Query rows of one (batch, KV head) share a LUT of n_blocks x nc x RP fp32 (<= 128 KiB).
     // More rows than one LUT holds split into row groups, each streaming the codes and values
     // again: twice the bytes at 8 query heads per KV head with 32 blocks, far less than the
@@ -71,7 +74,7 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     pl.rg = rows < cap ? rows : cap;
     pl.n_groups = (rows + pl.rg - 1) / pl.rg;
     pl.RP = pow2_at_least(pl.rg);
-    pl.DT = a->value_dim / 16;
+    pl.DT = nv ? 8 : a->value_dim / 16;
     const bool lut_ok = a->n_centroids == kNC ? cbits == 0 || cbits == 8
                                               : a->n_centroids == 64 && cbits != 4 && lut64_shape(*a, pl.RP, pl.DT);
     // Where the LUT needs row groups (or cannot serve the codes), the 4x4-MFMA-scores kernel serves
@@ -107,7 +110,7 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     pl.smem = pl.q4 ? ssq_decode_q4_smem(a, pl.rg, pl.split_len) : mfma_smem(*a, pl.RP, pl.split_len, ct);
     if (pl.smem > kMaxSmem) return false;
     const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
-    pl.ws_bytes = pl.n_splits > 1 ? (size_t)pl.n_splits * n_rows_all * (a->value_dim + 2) * 4 : 0;
+    pl.ws_bytes = !nv && pl.n_splits > 1 ? (size_t)pl.n_splits * n_rows_all * (a->value_dim + 2) * 4 : 0;
     return true;
 }
 
@@ -152,6 +155,7 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
         if (pl.n_splits > 1) rc = ssq_launch_merge(*a, pl.n_splits, mp.ws_o, mp.ws_m, mp.ws_l, st);
         return rc;
     }
+    if (pl.ct && !a->v) return ssq_mfma_lut_ct_scores(mp, pl, st);  // scores only: no merge
     if (pl.ct) {
         if (a->mask)
             rc = a->v_dtype == SSQ_BF16 ? ssq_mfma_lut_ct_bf16_mask(mp, pl, st) : ssq_mfma_lut_ct_f16_mask(mp, pl, st);

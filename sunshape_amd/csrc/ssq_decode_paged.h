@@ -157,17 +157,13 @@ __device__ __forceinline__ void issue_tile(const ssq_decode_args& a, const int* 
     }
 }
 
-// After a tile's scores s[r] (row r, this lane's token t0 + lane): the raw-score store, the online
-// softmax update (wave-local) and the probabilities cast to the value dtype in the wave's P strip
-// [RP][64], visible to the whole wave on return.
-template <int RP, int DT, int VT>
-__device__ __forceinline__ void tile_probs(const MfmaParams& p, uint16_t* pstrip, int b, int kv, int t0, int t_end,
-                                           int lane, const float (&s)[RP], float (&m_run)[RP], float (&l_lane)[RP],
-                                           v4f (&acc)[DT]) {
+// the raw-score store of a tile's scores s[r] (row r, this lane's token t0 + lane), if requested
+template <int RP>
+__device__ __forceinline__ void tile_store_scores(const MfmaParams& p, int b, int kv, int t0, int t_end, int lane,
+                                                  const float (&s)[RP]) {
     const ssq_decode_args& a = p.a;
     const int t = t0 + lane;
-    const bool valid = t < t_end;
-    if (valid) {
+    if (t < t_end) {
         if (a.scores) {
             const int row0 = blockIdx.z * p.rg, nr = min(p.rg, p.rows - row0);
 #pragma unroll
@@ -180,6 +176,17 @@ __device__ __forceinline__ void tile_probs(const MfmaParams& p, uint16_t* pstrip
             }
         }
     }
+}
+
+// After a tile's scores s[r] (row r, this lane's token t0 + lane): the raw-score store, the online
+// softmax update (wave-local) and the probabilities cast to the value dtype in the wave's P strip
+// [RP][64], visible to the whole wave on return.
+template <int RP, int DT, int VT>
+__device__ __forceinline__ void tile_probs(const MfmaParams& p, uint16_t* pstrip, int b, int kv, int t0, int t_end,
+                                           int lane, const float (&s)[RP], float (&m_run)[RP], float (&l_lane)[RP],
+                                           v4f (&acc)[DT]) {
+    tile_store_scores<RP>(p, b, kv, t0, t_end, lane, s);
+    const bool valid = t0 + lane < t_end;
     // online softmax (wave-local).  The running maximum m_run[r] is wave-uniform and moves only
     // when some score of the tile exceeds it by more than kSoftmaxSlack: most tiles skip the
     // cross-lane maxima and the accumulator rescale.

@@ -527,6 +527,33 @@ def test_contiguous_lut_kernel_128_dim_masks(B, Hq, Hkv, Lq, bd, T, kind, splits
     assert np.array_equal(oa, np_of(out))
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,bd,T,splits", [
+    (2, 32, 8, 1, 4, 1000, 0),  # 4 rows, 32 blocks
+    (1, 16, 2, 2, 2, 333, 3),   # 16 rows over 64 blocks: 8 row groups of 2
+    (2, 12, 4, 1, 8, 64, 1),    # 3 rows, 16 blocks, one tile
+    (1, 8, 8, 1, 16, 1, 0),     # one row, 8 blocks of 16 dims, one token
+])
+def test_contiguous_lut_kernel_128_dim_scores_only(B, Hq, Hkv, Lq, bd, T, splits):
+    """Scores only (gqa_scores) on contiguous rows at head_dim 128: the LUT kernel without values
+    stores every tile's scores; the automatic choice is this kernel."""
+    log(f"contig LUT D128 scores B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} bd={bd} T={T} splits={splits}")
+    D, scale = 128, 0.088
+    cb = synthetic.make_codebook(Hkv, D, bd, 190 + T)
+    g = torch.Generator().manual_seed(191 + T)
+    q = torch.randn(B, Hq, Lq, D, generator=g).to(torch.bfloat16)
+    codes = torch.randint(0, 256, (B, Hkv, T, D // bd), generator=g, dtype=torch.uint8)
+    args = (q.to(DEV), codes.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+    s2 = np_of(hip_ops.gqa_scores(*args, scale=scale, kernel=2, num_splits=splits))
+    s0 = np_of(hip_ops.gqa_scores(*args, scale=scale, num_splits=splits))
+    assert np.array_equal(s0, s2)
+    G = Hq // Hkv
+    for b in range(B):
+        for kv in range(Hkv):
+            qs = O.query_scale(q[b, kv * G:(kv + 1) * G].reshape(-1, D).float().numpy(), scale, "bf16")
+            ref = O.attention_scores(qs, codes[b, kv].numpy(), cb.centroids[kv].numpy(), cb.perm[kv].numpy())
+            assert_rel(s2[b, kv * G:(kv + 1) * G].reshape(-1, T), ref, SCORE_TOL, f"b={b} kv={kv}")
+
+
 def test_contiguous_mfma_kernel_rejects_wide_passthrough():
     """More than 16 passthrough dims do not fit the kernel's passthrough pass: an explicit
     kernel 3 request is refused, and auto dispatch serves the call on the LUT kernel."""
