@@ -66,8 +66,11 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     // More rows than one LUT holds split into row groups, each streaming the codes and values
     // again: twice the bytes at 8 query heads per KV head with 32 blocks, far less than the
     // LUT-less generic kernel costs.
+    // Contiguous rows take long causal chunks too (up to 2048 rows, e.g. 512 new tokens at 4 query
+    // heads per KV head): every row group re-streams the cache, as in the generic kernel's groups
+    // of 8, but at this kernel's rate.
     const int rows = (a->num_q_heads / a->num_kv_heads) * a->q_len;
-    if (rows > 64) return false;
+    if (rows > (ct ? 2048 : 64)) return false;
     const int lcap = 32768 / (a->n_blocks * lut_nc(*a));  // rows per 128 KiB LUT, a power of two
     const int rcap = ct ? 8 : 16;  // contiguous: the V buffer leaves room for 8-row LUTs
     const int cap = lcap < rcap ? lcap : rcap;

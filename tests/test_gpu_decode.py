@@ -488,6 +488,7 @@ def test_contiguous_lut_kernel_128_dim(B, Hq, Hkv, Lq, bd, T, vdt, splits, strid
     (2, 16, 4, 3, 4, 500, "causal", 1),    # three new tokens, HF's causal mask broadcast over batch and heads
     (1, 32, 8, 2, 2, 300, "causal", 2),    # 64 blocks: row groups of 2, causal over two tokens
     (2, 8, 8, 1, 8, 129, "random", 0),     # one row, 16 blocks, a fifth of the keys masked
+    (1, 8, 2, 64, 4, 300, "causal", 0),    # a 64-token causal chunk: 256 rows, 64 row groups of 4
 ])
 def test_contiguous_lut_kernel_128_dim_masks(B, Hq, Hkv, Lq, bd, T, kind, splits):
     """Additive masks on the contiguous 128-dim LUT kernel: read with each tile's codes, added to
