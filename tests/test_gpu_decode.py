@@ -479,6 +479,10 @@ def test_contiguous_lut_kernel_128_dim(B, Hq, Hkv, Lq, bd, T, vdt, splits, strid
     # the automatic choice is this kernel (bit-identical), and the generic kernel agrees
     oa = np_of(hip_ops.decode(*args, scale=scale, num_splits=splits))
     assert np.array_equal(oa, np_of(out))
+    if not strided:  # codes as 8-bit int32 words: the byte rows, the same result bit for bit
+        w8 = hip_ops.pack_codes(args[1], 8)
+        o8 = np_of(hip_ops.decode(args[0], w8, *args[2:], scale=scale, code_bits=8, kernel=2, num_splits=splits))
+        assert np.array_equal(o8, np_of(out))
     og = np_of(hip_ops.decode(*args, scale=scale, kernel=1))
     assert_rel(og, ro, BF16_TOL, "generic kernel")
 
@@ -487,7 +491,7 @@ def test_contiguous_lut_kernel_128_dim(B, Hq, Hkv, Lq, bd, T, vdt, splits, strid
     (2, 32, 8, 1, 4, 777, "rows", 0),      # per-(batch, head) padding and a finite bias
     (2, 16, 4, 3, 4, 500, "causal", 1),    # three new tokens, HF's causal mask broadcast over batch and heads
     (1, 32, 8, 2, 2, 300, "causal", 2),    # 64 blocks: row groups of 2, causal over two tokens
-    (2, 8, 8, 1, 8, 129, "random", 0),     # one row, 16 blocks, a fifth of the keys masked
+    (2, 8, 8, 1, 8, 129, "random-f16", 0),  # one row, 16 blocks, a fifth of the keys masked, f16 values
     (1, 8, 2, 64, 4, 300, "causal", 0),    # a 64-token causal chunk: 256 rows, 64 row groups of 4
 ])
 def test_contiguous_lut_kernel_128_dim_masks(B, Hq, Hkv, Lq, bd, T, kind, splits):
@@ -499,7 +503,8 @@ def test_contiguous_lut_kernel_128_dim_masks(B, Hq, Hkv, Lq, bd, T, kind, splits
     g = torch.Generator().manual_seed(171 + T)
     q = torch.randn(B, Hq, Lq, D, generator=g).to(torch.bfloat16)
     codes = torch.randint(0, 256, (B, Hkv, T, D // bd), generator=g, dtype=torch.uint8)
-    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+    vdt = torch.float16 if kind.endswith("f16") else torch.bfloat16
+    v = torch.randn(B, Hkv, T, D, generator=g).to(vdt)
     if kind == "rows":
         mask = torch.zeros(B, Hq, Lq, T)
         mask[0, :, :, :37] = float("-inf")
@@ -518,7 +523,8 @@ def test_contiguous_lut_kernel_128_dim_masks(B, Hq, Hkv, Lq, bd, T, kind, splits
     out, lse, scores = hip_ops.decode(*args, scale=scale, mask=md, return_lse=True, return_scores=True, kernel=2,
                                       num_splits=splits)
     ro, rs, rl = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
-                                    cb.perm.numpy(), scale, "bf16", "bf16", mask=full.numpy(), return_scores=True)
+                                    cb.perm.numpy(), scale, "bf16", "f16" if vdt == torch.float16 else "bf16",
+                                    mask=full.numpy(), return_scores=True)
     assert_rel(np_of(out), ro, BF16_TOL, "out")
     fin = np.isfinite(rs)
     assert np.array_equal(np.isfinite(np_of(scores)), fin)
