@@ -276,9 +276,13 @@ class SunShapeCache(DynamicCache):
 
 
 # ---------------------------------------------------------------------------- attention
-# multi-token steps take the fused decode up to this many query rows per KV head (the row count the
-# contiguous MFMA kernel holds in one pass); longer ones attend dequantized keys
+# multi-token steps take the fused decode up to this many query rows per KV head; longer ones attend
+# dequantized keys.  16 is the row count the head_dim-64 contiguous MFMA kernel holds in one pass.
+# Where the 128-dim LUT kernel serves the step (128-dim values past head_dim 64, no passthrough
+# blocks) the fused decode measured faster than dequantize + SDPA up to 256 rows per KV head
+# (B4 · 32/8 heads · T16384: 1.07 against 2.09 ms at 64 new tokens).
 _FUSED_MAX_ROWS = 16
+_FUSED_MAX_ROWS_LUT128 = 256
 
 
 def _additive_mask(mask: Optional[torch.Tensor], dtype=torch.float32) -> Optional[torch.Tensor]:
@@ -310,7 +314,8 @@ def sunshape_attention_forward(module: torch.nn.Module, query: torch.Tensor, key
     B, Hq, Lq, D = query.shape
     T = key.codes.shape[2]
     rows = (Hq // value.shape[1]) * Lq  # query rows per KV head
-    if Lq == 1 or (T > Lq and rows <= _FUSED_MAX_ROWS):
+    lut128 = D != 64 and value.shape[-1] == 128 and key.codec.heavy_blocks() is None
+    if Lq == 1 or (T > Lq and rows <= (_FUSED_MAX_ROWS_LUT128 if lut128 else _FUSED_MAX_ROWS)):
         # a decode step, or a short multi-token step over a filled cache (speculative verification,
         # small chunks): the fused decode over the codes, masked as HF's mask builder says (or
         # causally, the new tokens being the last Lq positions)

@@ -122,6 +122,32 @@ def test_code_layer_append_growth_and_decode():
     assert torch.equal(layer.keys[0], keys.codes[1, :, :300])
 
 
+def test_code_layer_head_dim_128_multi_token_step():
+    """At head_dim 128 (128-dim values, no passthrough blocks) a multi-token step of 8 new tokens
+    at 4 query heads per KV head (32 rows per KV head, past the head_dim-64 limit of 16) takes the
+    fused decode with a causal mask; it matches the oracle."""
+    log("SunShapeCodeLayer head_dim 128, 8-token step")
+    codec, sigma = _codec(D=128, bd=4, seed=11)
+    B, Hkv, Hq, D, S, L = 2, 2, 8, 128, 200, 8
+    layer = SunShapeCodeLayer(codec, block_tokens=256)
+    g = torch.Generator().manual_seed(12)
+    k = (torch.randn(B, Hkv, S, D, generator=g) * sigma).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    keys, values = layer.update(k.to(DEV), v.to(DEV))
+    kf = k.float().numpy()
+    codes_ref = np.stack([np.stack([_oracle_codes(codec, kf[b, h])[0] for h in range(Hkv)]) for b in range(B)])
+    assert np.array_equal(np_of(keys.codes), codes_ref)
+    q = torch.randn(B, Hq, L, D, generator=g).to(torch.bfloat16)
+    mod = torch.nn.Module()
+    mod.num_key_value_groups = Hq // Hkv
+    out, _ = sunshape_attention_forward(mod, q.to(DEV), keys, values, None, scaling=1 / math.sqrt(D))
+    causal = np.where(np.arange(S)[None, :] > (S - L + np.arange(L))[:, None], -np.inf, 0.0).astype(np.float32)
+    ref = O.decode_attention(q.float().numpy(), codes_ref, v.float().numpy(), codec.centroids.cpu().numpy(),
+                             codec.permutation.cpu().numpy(), 1 / math.sqrt(D), "bf16", "bf16",
+                             mask=np.broadcast_to(causal, (B, Hq, L, S)))
+    assert_rel(np_of(out.transpose(1, 2)), ref, BF16_TOL, "head_dim-128 8-token step")
+
+
 def test_tiny_llama_code_cache_tracks_dequant_cache():
     """Prefill through the code cache is bit-identical to the reference-mirroring cache (both attend
     bf16 k_hat); decode steps and a 3-token step use the fused decode and stay within bf16
