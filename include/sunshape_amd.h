@@ -101,9 +101,10 @@ typedef struct ssq_decode_args {
                                                  paged: entries t >= seq_lens[b] are not written */
     /* tuning: 0 = library heuristic */
     int32_t num_splits;
-    int32_t kernel;      /* 0 auto, 1 generic LUT/VALU kernel, 2 MFMA paged kernels (LUT scores, or 4x4-MFMA
-                            scores where the LUT does not fit), 3 MFMA contiguous kernel, 4 the paged
-                            4x4-MFMA-scores kernel wherever it applies */
+    int32_t kernel;      /* 0 auto, 1 generic LUT/VALU kernel, 2 MFMA LUT kernels (paged: LUT scores, or
+                            4x4-MFMA scores where the LUT does not fit; contiguous rows past head_dim 64
+                            with 128-dim values, or scores only), 3 MFMA contiguous kernel (head_dim 64),
+                            4 the paged 4x4-MFMA-scores kernel wherever it applies */
     /* code storage: 0 = one uint8 per block (c_* strides in bytes); 1..8 = packing in
      * uint32 words, vpe = 32 / code_bits codes per word, block blk = p*vpe + v at bits
      * [v*code_bits, (v+1)*code_bits) of word p (the layout of sunshape/triton_kernels.py:213-283);
