@@ -68,15 +68,16 @@ inline size_t mfma_smem(const ssq_decode_args& a, int RP, int split_len, bool ct
 // tile's first token are 32-bit (the plan keeps 64 tokens' strides below 2^31 bytes).
 // A contiguous tile's registers: the paged tile's, and with a mask (MK) the additive mask of each row
 // for this lane's token (rows past the workgroup's last one re-read that row's entry).
-template <int NB, int DT, int RP, bool MK>
+template <int NB, int DT, int RP, bool MK, bool HV>
 struct TileRegsCT : TileRegs<NB, DT, 0> {
     float mk[MK ? RP : 1];
+    uint32_t pt[HV ? 16 : 1];  // passthrough values (raw bits) of this lane's token
 };
 
-template <int NB, int DT, int RP, bool MK, bool NV>
+template <int NB, int DT, int RP, bool MK, bool NV, bool HV>
 __device__ __forceinline__ void issue_tile_ct(const MfmaParams& p, int b, int kv, int t_begin, int t_end, int tile,
                                               int lane, const uint8_t* cb0, const uint8_t* vb0,
-                                              TileRegsCT<NB, DT, RP, MK>& R) {
+                                              TileRegsCT<NB, DT, RP, MK, HV>& R) {
     static_assert(DT == 8, "contiguous LUT tiles carry 128-dim values");
     const ssq_decode_args& a = p.a;
     const int rel = tile * kTileTok;
@@ -109,6 +110,11 @@ __device__ __forceinline__ void issue_tile_ct(const MfmaParams& p, int b, int kv
             const int h = kv * p.G + g;
             R.mk[r] = a.mask[(int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qi * a.m_sl + t * a.m_st];
         }
+    }
+    if constexpr (HV) {  // dims past n_hd re-read the last one (unused)
+        const int64_t row = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)(t_begin + rel + min(lane, lim)) * a.pt_st;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) R.pt[i] = ssq_load_bits(a.pt, a.pt_dtype, row + p.hoff[min(i, p.n_hd - 1)]);
     }
 }
 
@@ -165,19 +171,20 @@ __device__ __forceinline__ void tile_pv_ct(const uint16_t* pstrip, uint16_t* vbu
 }
 
 // one tile's loads: contiguous rows (CT, with the mask when MK, codes only when NV) or pages
-template <bool CT, bool MK, bool NV, int RP, int NB, int DT, int PB, class TR>
+template <bool CT, bool MK, bool NV, bool HV, int RP, int NB, int DT, int PB, class TR>
 __device__ __forceinline__ void issue_any(const MfmaParams& p, int b, int kv, const int* pages, int t_begin, int t_end,
                                           int tile, int lane, const uint8_t* cbase, const uint16_t* vbase,
                                           const uint8_t* cb0, const uint8_t* vb0, TR& R) {
     if constexpr (CT) {
-        issue_tile_ct<NB, DT, RP, MK, NV>(p, b, kv, t_begin, t_end, tile, lane, cb0, vb0, R);
+        issue_tile_ct<NB, DT, RP, MK, NV, HV>(p, b, kv, t_begin, t_end, tile, lane, cb0, vb0, R);
     } else {
         issue_tile<NB, DT, PB>(p.a, pages, t_begin, t_end, tile, lane, cbase, vbase, R);
     }
 }
 
-template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT, bool MK, bool NV, class TR>
-__device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* lut, uint16_t* pstrip, uint16_t* vbuf,
+template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT, bool MK, bool NV, bool HV, class TR>
+__device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* lut, const float* qp, uint16_t* pstrip,
+                                             uint16_t* vbuf,
                                              int b, int kv, int t_begin, int t_end, int tile, int lane, TR& R,
                                              float (&m_run)[RP], float (&l_lane)[RP], v4f (&acc)[DT]) {
     const int t0 = t_begin + tile * kTileTok;
@@ -243,6 +250,17 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
     if constexpr (NV) {  // scores only
         tile_store_scores<RP>(p, b, kv, t0, t_end, lane, s);
     } else if constexpr (CT) {
+        if constexpr (HV) {  // passthrough dims: q_perm . stored value, after the LUT sums
+            const ssq_decode_args& a = p.a;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                if (i < p.n_hd) {  // wave-uniform
+                    const float x = ssq_bits_to_f32(R.pt[i], a.pt_dtype);
+#pragma unroll
+                    for (int r = 0; r < RP; ++r) s[r] = fmaf(qp[r * a.head_dim + p.hdim[i]], x, s[r]);
+                }
+            }
+        }
         if constexpr (MK) {
             const int nr = min(p.rg, p.rows - (int)blockIdx.z * p.rg);
 #pragma unroll
@@ -337,8 +355,8 @@ __device__ void build_lut_any(const float* __restrict__ cent, const float* __res
 }
 
 // NC: LUT codewords per block (256, or 64); PB: packed code bits (0 = byte codes); CT: contiguous rows,
-// MK: with an additive mask, NV: scores only (both on contiguous rows only)
-template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT, bool MK, bool NV>
+// MK: with an additive mask, NV: scores only, HV: passthrough blocks (all on contiguous rows only)
+template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT, bool MK, bool NV, bool HV>
 __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_decode_args& a = p.a;
@@ -439,8 +457,8 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     const uint8_t* vb0 = reinterpret_cast<const uint8_t*>(a.v) +
                          2 * ((int64_t)b * a.v_sb + (int64_t)kv * a.v_sh + (int64_t)t_begin * a.v_st);  // CT
     const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
-    static_assert(CT || (!MK && !NV), "masks and scores-only launches are contiguous-path variants");
-    using Regs = std::conditional_t<CT, TileRegsCT<NB, DT, RP, MK>, TileRegs<NB, DT, PB>>;
+    static_assert(CT || (!MK && !NV && !HV), "masks, scores only and passthrough are contiguous-path variants");
+    using Regs = std::conditional_t<CT, TileRegsCT<NB, DT, RP, MK, HV>, TileRegs<NB, DT, PB>>;
     Regs RA, RB;
     int tile = wave;
     // Tile loads are issued unconditionally (a wave past the last tile re-reads tile n_tiles-1,
@@ -448,7 +466,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
     // compiler's vmcnt waits for the tile being computed never drain the tile behind it.
     const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
     if (n_tiles > 0)
-        issue_any<CT, MK, NV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile, last_tile), lane, cbase,
+        issue_any<CT, MK, NV, HV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile, last_tile), lane, cbase,
                                               vbase, cb0, vb0, RA);
     switch (bd) {
         case 1: build_lut<RP, NB, 1, NC>(cent, qp, lut, D, tid); break;
@@ -456,6 +474,11 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
         case 4: build_lut<RP, NB, 4, NC>(cent, qp, lut, D, tid); break;
         case 8: build_lut<RP, NB, 8, NC>(cent, qp, lut, D, tid); break;
         default: build_lut_any<RP, NB, NC>(cent, qp, lut, D, bd, tid); break;
+    }
+    if constexpr (HV) {  // passthrough blocks score from their stored values: zero their LUT rows
+        __syncthreads();
+        for (int e = tid; e < NB * NC * RP; e += kThreads)
+            if ((a.heavy_mask[0] >> (e / (NC * RP))) & 1ull) lut[e] = 0.f;
     }
     __syncthreads();
 
@@ -471,24 +494,24 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
         // set; a wave issues its next tile once this one is consumed (the other waves' loads keep
         // the memory busy meanwhile)
         while (tile < n_tiles) {
-            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV, HV>(p, lut, qp, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
                                                              RA, m_run, l_lane, acc);
             tile += kWaves;
             if (tile >= n_tiles) break;
-            issue_any<CT, MK, NV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, tile, lane, cbase, vbase, cb0, vb0,
+            issue_any<CT, MK, NV, HV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, tile, lane, cbase, vbase, cb0, vb0,
                                                   RA);
         }
     } else {
         while (tile < n_tiles) {
-            issue_any<CT, MK, NV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
+            issue_any<CT, MK, NV, HV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
                                                   cbase, vbase, cb0, vb0, RB);
-            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV, HV>(p, lut, qp, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
                                                              RA, m_run, l_lane, acc);
             tile += kWaves;
             if (tile >= n_tiles) break;
-            issue_any<CT, MK, NV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
+            issue_any<CT, MK, NV, HV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
                                                   cbase, vbase, cb0, vb0, RA);
-            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV>(p, lut, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV, HV>(p, lut, qp, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
                                                              RB, m_run, l_lane, acc);
             tile += kWaves;
         }
@@ -548,9 +571,9 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
 }
 
 template <int RP, int DT, int VT, int NB, int NC = kNC, int PB = 0, bool CT = false, bool MK = false,
-          bool NV = false>
+          bool NV = false, bool HV = false>
 int launch(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
-    auto kern = k_decode_mfma<RP, DT, VT, NB, NC, PB, CT, MK, NV>;
+    auto kern = k_decode_mfma<RP, DT, VT, NB, NC, PB, CT, MK, NV, HV>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_mfma)");
     if (rc) return rc;
     dim3 grid(mp.a.batch * mp.a.num_kv_heads, pl.n_splits, pl.n_groups);
@@ -603,23 +626,23 @@ int lut64_rp(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
 
 // contiguous rows (128-dim values, 256-codeword LUT, byte codes; MK: with a mask, NV: scores only):
 // at most 8 rows per LUT
-template <int RP, int VT, bool MK, bool NV>
+template <int RP, int VT, bool MK, bool NV, bool HV>
 int launch_ct_nb(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
     switch (mp.a.n_blocks) {
-        case 8: return launch<RP, 8, VT, 8, kNC, 0, true, MK, NV>(mp, pl, st);
-        case 16: if constexpr (RP <= 8) return launch<RP, 8, VT, 16, kNC, 0, true, MK, NV>(mp, pl, st); break;
-        case 32: if constexpr (RP <= 4) return launch<RP, 8, VT, 32, kNC, 0, true, MK, NV>(mp, pl, st); break;
-        default: if constexpr (RP <= 2) return launch<RP, 8, VT, 64, kNC, 0, true, MK, NV>(mp, pl, st); break;
+        case 8: return launch<RP, 8, VT, 8, kNC, 0, true, MK, NV, HV>(mp, pl, st);
+        case 16: if constexpr (RP <= 8) return launch<RP, 8, VT, 16, kNC, 0, true, MK, NV, HV>(mp, pl, st); break;
+        case 32: if constexpr (RP <= 4) return launch<RP, 8, VT, 32, kNC, 0, true, MK, NV, HV>(mp, pl, st); break;
+        default: if constexpr (RP <= 2) return launch<RP, 8, VT, 64, kNC, 0, true, MK, NV, HV>(mp, pl, st); break;
     }
     return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode: LUT of %d rows x %d blocks exceeds LDS", RP, mp.a.n_blocks);
 }
-template <int VT, bool MK, bool NV = false>
+template <int VT, bool MK, bool NV = false, bool HV = false>
 int launch_ct(const MfmaParams& mp, const SsqMfmaPlan& pl, hipStream_t st) {
     switch (pl.RP) {
-        case 1: return launch_ct_nb<1, VT, MK, NV>(mp, pl, st);
-        case 2: return launch_ct_nb<2, VT, MK, NV>(mp, pl, st);
-        case 4: return launch_ct_nb<4, VT, MK, NV>(mp, pl, st);
-        case 8: return launch_ct_nb<8, VT, MK, NV>(mp, pl, st);
+        case 1: return launch_ct_nb<1, VT, MK, NV, HV>(mp, pl, st);
+        case 2: return launch_ct_nb<2, VT, MK, NV, HV>(mp, pl, st);
+        case 4: return launch_ct_nb<4, VT, MK, NV, HV>(mp, pl, st);
+        case 8: return launch_ct_nb<8, VT, MK, NV, HV>(mp, pl, st);
         default: return ssq_fail(SSQ_ERR_UNSUPPORTED, "MFMA decode: %d rows per contiguous LUT", pl.RP);
     }
 }
@@ -638,3 +661,5 @@ SSQ_MFMA_UNIT(ssq_mfma_lut_ct_f16);
 SSQ_MFMA_UNIT(ssq_mfma_lut_ct_bf16_mask);
 SSQ_MFMA_UNIT(ssq_mfma_lut_ct_f16_mask);
 SSQ_MFMA_UNIT(ssq_mfma_lut_ct_scores);
+SSQ_MFMA_UNIT(ssq_mfma_lut_ct_bf16_heavy);
+SSQ_MFMA_UNIT(ssq_mfma_lut_ct_f16_heavy);

@@ -39,7 +39,12 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     const bool nv = a->v == nullptr;
     if (nv && (!ct || !a->scores || a->mask)) return false;
     if (!nv && a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16) return false;
-    if ((a->mask != nullptr && !ct) || a->heavy_mask[0] || a->heavy_mask[1]) return false;  // masks: contiguous only
+    if (a->mask != nullptr && !ct) return false;  // masks: contiguous only
+    if (a->heavy_mask[0] || a->heavy_mask[1]) {  // passthrough: contiguous decode without a mask, <= 16 dims
+        if (!ct || nv || a->mask || a->heavy_mask[1] || !a->pt) return false;
+        if (a->pt_dtype != SSQ_F32 && a->pt_dtype != SSQ_BF16 && a->pt_dtype != SSQ_F16) return false;
+        if (__builtin_popcountll(a->heavy_mask[0]) * a->block_dim > 16) return false;
+    }
     if (!nv && a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;  // float4 codeword loads
     if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32 && a->n_blocks != 64) return false;
@@ -141,6 +146,18 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
         mp.a.c_sb *= 4; mp.a.c_sh *= 4; mp.a.c_st *= 4;
         mp.a.code_bits = 0;
     }
+    // passthrough dims (heavy blocks ascending, then d): record slot = block (dense) or ordinal
+    mp.n_hd = 0;
+    for (int blk = 0, h = 0; blk < a->n_blocks && blk < 64; ++blk) {
+        if (!((a->heavy_mask[0] >> blk) & 1ull)) continue;
+        const int slot = a->pt_dense ? blk : h;
+        for (int d = 0; d < a->block_dim && mp.n_hd < 16; ++d) {
+            mp.hoff[mp.n_hd] = slot * a->block_dim + d;
+            mp.hdim[mp.n_hd] = blk * a->block_dim + d;
+            ++mp.n_hd;
+        }
+        ++h;
+    }
     mp.G = a->num_q_heads / a->num_kv_heads;
     mp.rows = mp.G * a->q_len;
     mp.rg = pl.rg;
@@ -160,7 +177,9 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
     }
     if (pl.ct && !a->v) return ssq_mfma_lut_ct_scores(mp, pl, st);  // scores only: no merge
     if (pl.ct) {
-        if (a->mask)
+        if (a->heavy_mask[0])
+            rc = a->v_dtype == SSQ_BF16 ? ssq_mfma_lut_ct_bf16_heavy(mp, pl, st) : ssq_mfma_lut_ct_f16_heavy(mp, pl, st);
+        else if (a->mask)
             rc = a->v_dtype == SSQ_BF16 ? ssq_mfma_lut_ct_bf16_mask(mp, pl, st) : ssq_mfma_lut_ct_f16_mask(mp, pl, st);
         else
             rc = a->v_dtype == SSQ_BF16 ? ssq_mfma_lut_ct_bf16(mp, pl, st) : ssq_mfma_lut_ct_f16(mp, pl, st);

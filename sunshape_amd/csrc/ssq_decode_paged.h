@@ -10,6 +10,10 @@ struct SsqPagedParams {
     ssq_decode_args a;
     int G, rows, split_len, n_splits;
     int rg;  // query rows per row group (blockIdx.z)
+    // passthrough dims of the contiguous LUT kernel: n_hd (<= 16) dims, each at element hoff[i] of
+    // a token's passthrough row and permuted query dim hdim[i]
+    int n_hd;
+    int hoff[16], hdim[16];
     float* ws_o;
     float* ws_m;
     float* ws_l;

@@ -561,6 +561,42 @@ def test_contiguous_lut_kernel_128_dim_scores_only(B, Hq, Hkv, Lq, bd, T, splits
             assert_rel(s2[b, kv * G:(kv + 1) * G].reshape(-1, T), ref, SCORE_TOL, f"b={b} kv={kv}")
 
 
+@pytest.mark.parametrize("bd,n_heavy,dense,pdt,vdt", [(4, 4, False, torch.bfloat16, torch.bfloat16),
+                                                      (2, 8, True, torch.float32, torch.bfloat16),
+                                                      (8, 2, False, torch.float16, torch.float16),
+                                                      (4, 1, True, torch.bfloat16, torch.bfloat16)])
+def test_contiguous_lut_kernel_128_dim_passthrough(bd, n_heavy, dense, pdt, vdt):
+    """SunShape-Mixed passthrough blocks (up to 16 dims) on the contiguous 128-dim LUT kernel: the
+    heavy blocks' LUT rows are zero and their scores come from the stored values (dense or compact
+    slots, any pt dtype)."""
+    log(f"contig LUT D128 passthrough bd={bd} n_heavy={n_heavy} dense={dense} pdt={pdt} vdt={vdt}")
+    B, Hkv, Hq, T, D = 2, 8, 32, 555, 128
+    nb = D // bd
+    cb = synthetic.make_codebook(Hkv, D, bd, 210 + bd + n_heavy)
+    g = torch.Generator().manual_seed(211 + bd)
+    hidx = sorted(torch.randperm(nb, generator=g)[:n_heavy].tolist())
+    heavy = [i in hidx for i in range(nb)]
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    codes = torch.randint(0, 256, (B, Hkv, T, nb), generator=g, dtype=torch.uint8)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(vdt)
+    ptd = torch.zeros(B, Hkv, T, nb, bd)
+    ptd[:, :, :, hidx] = torch.randn(B, Hkv, T, n_heavy, bd, generator=g)
+    ptd = ptd.to(pdt)
+    pt = ptd if dense else ptd[:, :, :, hidx].contiguous()
+    scale = 1 / math.sqrt(D)
+    args = (q.to(DEV), codes.to(DEV), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+    kw = dict(scale=scale, heavy=heavy, pt=pt.to(DEV), pt_dense=dense)
+    out, lse, scores = hip_ops.decode(*args, **kw, return_lse=True, return_scores=True, kernel=2)
+    ro, rs, rl = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
+                                    cb.perm.numpy(), scale, "bf16", "f16" if vdt == torch.float16 else "bf16",
+                                    heavy=np.array(heavy), pt_values=ptd.float().numpy(), return_scores=True)
+    assert_rel(np_of(out), ro, BF16_TOL, "out")
+    assert_rel(np_of(scores), rs, SCORE_TOL, "scores")
+    assert_rel(np_of(lse), rl, SCORE_TOL, "lse")
+    oa = np_of(hip_ops.decode(*args, **kw))
+    assert np.array_equal(oa, np_of(out))
+
+
 def test_contiguous_mfma_kernel_rejects_wide_passthrough():
     """More than 16 passthrough dims do not fit the kernel's passthrough pass: an explicit
     kernel 3 request is refused, and auto dispatch serves the call on the LUT kernel."""
