@@ -113,8 +113,22 @@ __device__ __forceinline__ void issue_tile_ct(const MfmaParams& p, int b, int kv
     }
     if constexpr (HV) {  // dims past n_hd re-read the last one (unused)
         const int64_t row = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)(t_begin + rel + min(lane, lim)) * a.pt_st;
+        if (p.pt_vec) {  // wave-uniform: one or two 16-byte loads
+            const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.pt) + row + p.hoff[0]);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) R.pt[i] = ssq_load_bits(a.pt, a.pt_dtype, row + p.hoff[min(i, p.n_hd - 1)]);
+            for (int j = 0; j < 2; ++j) {
+                const uint4 w = src[min(j, p.n_hd / 8 - 1)];
+                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    R.pt[8 * j + 2 * k] = ww[k] & 0xFFFFu;
+                    R.pt[8 * j + 2 * k + 1] = ww[k] >> 16;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) R.pt[i] = ssq_load_bits(a.pt, a.pt_dtype, row + p.hoff[min(i, p.n_hd - 1)]);
+        }
     }
 }
 
@@ -183,8 +197,8 @@ __device__ __forceinline__ void issue_any(const MfmaParams& p, int b, int kv, co
 }
 
 template <int RP, int DT, int VT, int NB, int NC, int PB, bool CT, bool MK, bool NV, bool HV, class TR>
-__device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* lut, const float* qp, uint16_t* pstrip,
-                                             uint16_t* vbuf,
+__device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* lut, const float (&qh)[HV ? RP : 1][16],
+                                             uint16_t* pstrip, uint16_t* vbuf,
                                              int b, int kv, int t_begin, int t_end, int tile, int lane, TR& R,
                                              float (&m_run)[RP], float (&l_lane)[RP], v4f (&acc)[DT]) {
     const int t0 = t_begin + tile * kTileTok;
@@ -257,7 +271,7 @@ __device__ __forceinline__ void compute_tile(const MfmaParams& p, const float* l
                 if (i < p.n_hd) {  // wave-uniform
                     const float x = ssq_bits_to_f32(R.pt[i], a.pt_dtype);
 #pragma unroll
-                    for (int r = 0; r < RP; ++r) s[r] = fmaf(qp[r * a.head_dim + p.hdim[i]], x, s[r]);
+                    for (int r = 0; r < RP; ++r) s[r] = fmaf(qh[r][i], x, s[r]);
                 }
             }
         }
@@ -481,6 +495,13 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
             if ((a.heavy_mask[0] >> (e / (NC * RP))) & 1ull) lut[e] = 0.f;
     }
     __syncthreads();
+    // the permuted query rows at the passthrough dims, in registers for the whole stream
+    float qh[HV ? RP : 1][16];
+#pragma unroll
+    for (int r = 0; r < (HV ? RP : 1); ++r) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) qh[r][i] = HV && i < p.n_hd ? qp[r * D + p.hdim[i]] : 0.f;
+    }
 
     // ---- stream tiles, two in flight per wave (A/B register sets, no copies)
     float m_run[RP], l_lane[RP];
@@ -494,7 +515,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
         // set; a wave issues its next tile once this one is consumed (the other waves' loads keep
         // the memory busy meanwhile)
         while (tile < n_tiles) {
-            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV, HV>(p, lut, qp, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV, HV>(p, lut, qh, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
                                                              RA, m_run, l_lane, acc);
             tile += kWaves;
             if (tile >= n_tiles) break;
@@ -505,13 +526,13 @@ __global__ __launch_bounds__(kThreads) void k_decode_mfma(const MfmaParams p) {
         while (tile < n_tiles) {
             issue_any<CT, MK, NV, HV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
                                                   cbase, vbase, cb0, vb0, RB);
-            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV, HV>(p, lut, qp, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV, HV>(p, lut, qh, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
                                                              RA, m_run, l_lane, acc);
             tile += kWaves;
             if (tile >= n_tiles) break;
             issue_any<CT, MK, NV, HV, RP, NB, DT, PB>(p, b, kv, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane,
                                                   cbase, vbase, cb0, vb0, RA);
-            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV, HV>(p, lut, qp, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
+            compute_tile<RP, DT, VT, NB, NC, PB, CT, MK, NV, HV>(p, lut, qh, pstrip, vbuf, b, kv, t_begin, t_end, tile, lane,
                                                              RB, m_run, l_lane, acc);
             tile += kWaves;
         }

@@ -158,6 +158,10 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
         }
         ++h;
     }
+    mp.pt_vec = a->heavy_mask[0] && a->pt_dtype != SSQ_F32 && (mp.n_hd == 8 || mp.n_hd == 16) &&
+                ((uintptr_t)a->pt + 2 * (uintptr_t)mp.hoff[0]) % 16 == 0 && (a->pt_sb * 2) % 16 == 0 &&
+                (a->pt_sh * 2) % 16 == 0 && (a->pt_st * 2) % 16 == 0;
+    for (int i = 1; i < mp.n_hd; ++i) mp.pt_vec = mp.pt_vec && mp.hoff[i] == mp.hoff[0] + i;
     mp.G = a->num_q_heads / a->num_kv_heads;
     mp.rows = mp.G * a->q_len;
     mp.rg = pl.rg;
