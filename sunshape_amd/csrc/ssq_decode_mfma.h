@@ -111,23 +111,19 @@ __device__ __forceinline__ void issue_tile_ct(const MfmaParams& p, int b, int kv
             R.mk[r] = a.mask[(int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qi * a.m_sl + t * a.m_st];
         }
     }
-    if constexpr (HV) {  // dims past n_hd re-read the last one (unused)
+    if constexpr (HV) {  // n_hd (8 or 16) consecutive 16-bit values: two 16-byte loads (the second
+                         // re-reads the first with 8), straight-line like the tile's other loads
         const int64_t row = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)(t_begin + rel + min(lane, lim)) * a.pt_st;
-        if (p.pt_vec) {  // wave-uniform: one or two 16-byte loads
-            const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.pt) + row + p.hoff[0]);
+        const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.pt) + row + p.hoff[0]);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint4 w = src[min(j, p.n_hd / 8 - 1)];
-                const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        for (int j = 0; j < 2; ++j) {
+            const uint4 w = src[min(j, p.n_hd / 8 - 1)];
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    R.pt[8 * j + 2 * k] = ww[k] & 0xFFFFu;
-                    R.pt[8 * j + 2 * k + 1] = ww[k] >> 16;
-                }
+            for (int k = 0; k < 4; ++k) {
+                R.pt[8 * j + 2 * k] = ww[k] & 0xFFFFu;
+                R.pt[8 * j + 2 * k + 1] = ww[k] >> 16;
             }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) R.pt[i] = ssq_load_bits(a.pt, a.pt_dtype, row + p.hoff[min(i, p.n_hd - 1)]);
         }
     }
 }

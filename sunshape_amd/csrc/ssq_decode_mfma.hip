@@ -23,6 +23,26 @@ bool lut64_shape(const ssq_decode_args& a, int RP, int DT) {
            (a.n_blocks == 16 || a.n_blocks == 32 || a.n_blocks == 64);
 }
 
+// passthrough dims (heavy blocks ascending, then d): record slot = block (dense) or ordinal; pt_vec
+// when they are 8 or 16 consecutive 16-bit values with 16-byte aligned rows
+void pt_dims(const ssq_decode_args& a, SsqPagedParams& mp) {
+    mp.n_hd = 0;
+    for (int blk = 0, h = 0; blk < a.n_blocks && blk < 64; ++blk) {
+        if (!((a.heavy_mask[0] >> blk) & 1ull)) continue;
+        const int slot = a.pt_dense ? blk : h;
+        for (int d = 0; d < a.block_dim && mp.n_hd < 16; ++d) {
+            mp.hoff[mp.n_hd] = slot * a.block_dim + d;
+            mp.hdim[mp.n_hd] = blk * a.block_dim + d;
+            ++mp.n_hd;
+        }
+        ++h;
+    }
+    mp.pt_vec = a.heavy_mask[0] && a.pt_dtype != SSQ_F32 && (mp.n_hd == 8 || mp.n_hd == 16) &&
+                ((uintptr_t)a.pt + 2 * (uintptr_t)mp.hoff[0]) % 16 == 0 && (a.pt_sb * 2) % 16 == 0 &&
+                (a.pt_sh * 2) % 16 == 0 && (a.pt_st * 2) % 16 == 0;
+    for (int i = 1; i < mp.n_hd; ++i) mp.pt_vec = mp.pt_vec && mp.hoff[i] == mp.hoff[0] + i;
+}
+
 bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     // contiguous rows take this kernel (CT) for 128-dim values past head_dim 64, which the contiguous
     // MFMA kernel (ssq_decode_contig.hip) serves
@@ -44,6 +64,9 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
         if (!ct || nv || a->mask || a->heavy_mask[1] || !a->pt) return false;
         if (a->pt_dtype != SSQ_F32 && a->pt_dtype != SSQ_BF16 && a->pt_dtype != SSQ_F16) return false;
         if (__builtin_popcountll(a->heavy_mask[0]) * a->block_dim > 16) return false;
+        SsqPagedParams dims;
+        pt_dims(*a, dims);
+        if (!dims.pt_vec) return false;  // 8 or 16 consecutive 16-bit values per token
     }
     if (!nv && a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;  // float4 codeword loads
@@ -146,22 +169,7 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
         mp.a.c_sb *= 4; mp.a.c_sh *= 4; mp.a.c_st *= 4;
         mp.a.code_bits = 0;
     }
-    // passthrough dims (heavy blocks ascending, then d): record slot = block (dense) or ordinal
-    mp.n_hd = 0;
-    for (int blk = 0, h = 0; blk < a->n_blocks && blk < 64; ++blk) {
-        if (!((a->heavy_mask[0] >> blk) & 1ull)) continue;
-        const int slot = a->pt_dense ? blk : h;
-        for (int d = 0; d < a->block_dim && mp.n_hd < 16; ++d) {
-            mp.hoff[mp.n_hd] = slot * a->block_dim + d;
-            mp.hdim[mp.n_hd] = blk * a->block_dim + d;
-            ++mp.n_hd;
-        }
-        ++h;
-    }
-    mp.pt_vec = a->heavy_mask[0] && a->pt_dtype != SSQ_F32 && (mp.n_hd == 8 || mp.n_hd == 16) &&
-                ((uintptr_t)a->pt + 2 * (uintptr_t)mp.hoff[0]) % 16 == 0 && (a->pt_sb * 2) % 16 == 0 &&
-                (a->pt_sh * 2) % 16 == 0 && (a->pt_st * 2) % 16 == 0;
-    for (int i = 1; i < mp.n_hd; ++i) mp.pt_vec = mp.pt_vec && mp.hoff[i] == mp.hoff[0] + i;
+    pt_dims(*a, mp);
     mp.G = a->num_q_heads / a->num_kv_heads;
     mp.rows = mp.G * a->q_len;
     mp.rg = pl.rg;

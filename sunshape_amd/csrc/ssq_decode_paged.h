@@ -14,7 +14,8 @@ struct SsqPagedParams {
     // a token's passthrough row and permuted query dim hdim[i]
     int n_hd;
     int hoff[16], hdim[16];
-    int pt_vec;  // the n_hd (8 or 16) values are consecutive 16-bit elements, 16-byte aligned
+    int pt_vec;  // the n_hd (8 or 16) values are consecutive 16-bit elements, 16-byte aligned (the
+                 // contiguous LUT kernel's passthrough variant requires it)
     float* ws_o;
     float* ws_m;
     float* ws_l;

@@ -561,14 +561,16 @@ def test_contiguous_lut_kernel_128_dim_scores_only(B, Hq, Hkv, Lq, bd, T, splits
             assert_rel(s2[b, kv * G:(kv + 1) * G].reshape(-1, T), ref, SCORE_TOL, f"b={b} kv={kv}")
 
 
-@pytest.mark.parametrize("bd,n_heavy,dense,pdt,vdt", [(4, 4, False, torch.bfloat16, torch.bfloat16),
-                                                      (2, 8, True, torch.float32, torch.bfloat16),
-                                                      (8, 2, False, torch.float16, torch.float16),
-                                                      (4, 1, True, torch.bfloat16, torch.bfloat16)])
-def test_contiguous_lut_kernel_128_dim_passthrough(bd, n_heavy, dense, pdt, vdt):
-    """SunShape-Mixed passthrough blocks (up to 16 dims) on the contiguous 128-dim LUT kernel: the
-    heavy blocks' LUT rows are zero and their scores come from the stored values (dense or compact
-    slots, any pt dtype)."""
+@pytest.mark.parametrize("bd,n_heavy,dense,pdt,vdt,ct", [(4, 4, False, torch.bfloat16, torch.bfloat16, True),
+                                                         (4, 2, False, torch.bfloat16, torch.bfloat16, True),
+                                                         (8, 2, False, torch.float16, torch.float16, True),
+                                                         (2, 8, True, torch.float32, torch.bfloat16, False),
+                                                         (4, 1, True, torch.bfloat16, torch.bfloat16, False)])
+def test_contiguous_lut_kernel_128_dim_passthrough(bd, n_heavy, dense, pdt, vdt, ct):
+    """SunShape-Mixed passthrough blocks on the contiguous 128-dim LUT kernel (ct): 8 or 16
+    consecutive 16-bit stored values per token; the heavy blocks' LUT rows are zero and their
+    scores come from the stored values.  Other passthrough layouts (fp32, dense slots, 4 dims)
+    take the generic kernel; both match the oracle."""
     log(f"contig LUT D128 passthrough bd={bd} n_heavy={n_heavy} dense={dense} pdt={pdt} vdt={vdt}")
     B, Hkv, Hq, T, D = 2, 8, 32, 555, 128
     nb = D // bd
@@ -586,7 +588,7 @@ def test_contiguous_lut_kernel_128_dim_passthrough(bd, n_heavy, dense, pdt, vdt)
     scale = 1 / math.sqrt(D)
     args = (q.to(DEV), codes.to(DEV), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
     kw = dict(scale=scale, heavy=heavy, pt=pt.to(DEV), pt_dense=dense)
-    out, lse, scores = hip_ops.decode(*args, **kw, return_lse=True, return_scores=True, kernel=2)
+    out, lse, scores = hip_ops.decode(*args, **kw, return_lse=True, return_scores=True, kernel=2 if ct else 0)
     ro, rs, rl = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
                                     cb.perm.numpy(), scale, "bf16", "f16" if vdt == torch.float16 else "bf16",
                                     heavy=np.array(heavy), pt_values=ptd.float().numpy(), return_scores=True)
