@@ -12,7 +12,7 @@ from HIP events on its own stream, the same launch's time with cold caches (a 1 
 before each), and a bounded CPU baseline: the reference's eager torch decode path on the
 host's cores (oracle/torch_eager.py).
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c4ct|c5encpro] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c4ct|c4ctbd2|c4ctg8|c5encpro] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -40,7 +40,7 @@ def _args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "c4g8", "c4bd2", "c3p6",
-                                                     "c4p6", "c4ct", "c5encpro", "copycal"])
+                                                     "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c5encpro", "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -83,19 +83,14 @@ def _decode_workload(name, dev, kernel):
             p.tensors["code_words"] = hip_ops.pack_codes(p["code_pages"], code_bits)
         B, Hkv, T, D = 64, 8, 32768, 128
         paged = True
-    elif name == "c4ct":
+    elif name in ("c4ct", "c4ctbd2", "c4ctg8"):
         # the config-4 layer with the reference's contiguous rows (codes [B, Hkv, T, nb], V
-        # [B, Hkv, T, D]) in place of pages
-        B, Hq, Hkv, T, D, bd = 64, 32, 8, 32768, 128, 4
-        cb = synthetic.make_codebook(Hkv, D, bd, 4)
-        g = torch.Generator().manual_seed(104)
-        gd = torch.Generator(device=dev).manual_seed(204)
-        q4 = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16).to(dev)
-        c4 = torch.randint(0, nc, (B, Hkv, T, D // bd), generator=gd, device=dev, dtype=torch.uint8)
-        v4 = torch.randn(B, Hkv, T, D, generator=gd, device=dev, dtype=torch.bfloat16)
-        p = synthetic.Problem("C4ct", {"q": q4, "codes": c4, "v": v4, "perm": cb.perm.to(dev),
-                                       "centroids": cb.centroids.to(dev)},
-                              {"scale": 1.0 / math.sqrt(D), "B": B, "Hq": Hq, "Hkv": Hkv, "T": T})
+        # [B, Hkv, T, D]) in place of pages; c4ctbd2 at the reference's default 4 bits/dim (64 blocks
+        # of dim 2), c4ctg8 with 64 query heads (8 per KV head): the 4x4-MFMA-scores kernel
+        B, Hkv, T, D = 64, 8, 32768, 128
+        Hq = 64 if name == "c4ctg8" else 32
+        bd = 2 if name == "c4ctbd2" else 4
+        p = synthetic.config4_contiguous(dev, Hq=Hq, bd=bd)
         paged = False
     elif name == "c5":
         # SunShape-Mixed: the config-5 keys encoded once (28 VQ blocks + 4 bf16 passthrough blocks)
@@ -185,6 +180,8 @@ def _decode_workload(name, dev, kernel):
                         "c4bd2": "C4 layer at 4 bits/dim (64 blocks of dim 2), paged",
                         "c4p6": "C4 layer at 3 bits/dim: 64 codewords, 6-bit codes packed in int32 words, paged",
                         "c4ct": "C4 layer with contiguous rows (codes [B, Hkv, T, nb], V [B, Hkv, T, D]), 2 bits/dim",
+                        "c4ctbd2": "C4 layer with contiguous rows at 4 bits/dim (64 blocks of dim 2)",
+                        "c4ctg8": "C4 layer with contiguous rows, 64 query heads (8 per KV head), 2 bits/dim",
                         "c3": "C3 contiguous fused decode (Qwen2.5-0.5B layer, 4 bits/dim)",
                         "c5": "C5 SunShape-Mixed fused decode (config-5 keys: 28 VQ + 4 bf16 blocks of dim 2)",
                         "c3p6": "C3 layer at 3 bits/dim: 64 codewords, 6-bit codes packed in int32 words"}[name],
@@ -601,7 +598,7 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2", "c3p6", "c4p6", "c4ct"):
+    if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2", "c3p6", "c4p6", "c4ct", "c4ctbd2", "c4ctg8"):
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
         step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev, args.kernel)

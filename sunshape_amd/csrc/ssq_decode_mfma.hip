@@ -44,8 +44,9 @@ void pt_dims(const ssq_decode_args& a, SsqPagedParams& mp) {
 }
 
 bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
-    // contiguous rows take this kernel (CT) for 128-dim values past head_dim 64, which the contiguous
-    // MFMA kernel (ssq_decode_contig.hip) serves
+    // contiguous rows take the LUT kernel (CT) for 128-dim values past head_dim 64, which the
+    // contiguous MFMA kernel (ssq_decode_contig.hip) serves, and the 4x4-MFMA-scores kernel (CT) at
+    // head_dim 128 where the LUT would need row groups
     const bool ct = a->layout == SSQ_CONTIGUOUS;
     if (!ct && (a->layout != SSQ_PAGED || a->page_size != kPage)) return false;
     // Codes: bytes, 8-bit words (the byte rows, strides scaled to bytes), or 4- / 6-bit words.
@@ -72,13 +73,18 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;  // float4 codeword loads
     if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32 && a->n_blocks != 64) return false;
     if (a->head_dim > 256) return false;  // query staging covers at most 256 dims per row
+    // contiguous rows: the LUT kernel (CT) or the 4x4-MFMA-scores kernel (CT; head_dim 128, 128-dim
+    // values, no mask, no passthrough, not scores only)
+    const bool ct_lut = ct && a->head_dim != 64 && (nv || a->value_dim == 128) && a->kernel != 4 &&
+                        a->n_centroids == kNC && (cbits == 0 || cbits == 8);
+    const bool ct_q4 = ct && !nv && !a->mask && !(a->heavy_mask[0] || a->heavy_mask[1]) && a->head_dim == 128 &&
+                       a->value_dim == 128 && ssq_decode_q4_shape(a);
     if (ct) {
-        if (a->head_dim == 64 || (!nv && a->value_dim != 128) || a->kernel == 4) return false;
-        if (a->n_centroids != kNC || (cbits != 0 && cbits != 8)) return false;
+        if (!ct_lut && !ct_q4) return false;
         // tile loads take 32-bit byte offsets from the tile's first token, token strides >= 0
         const int64_t kLim = (int64_t)1 << 31;
         if (a->c_st < 0 || (!nv && a->v_st < 0)) return false;
-        if ((int64_t)kTileTok * a->c_st * (cbits == 8 ? 4 : 1) + 64 >= kLim) return false;
+        if ((int64_t)kTileTok * a->c_st * (cbits ? 4 : 1) + 64 >= kLim) return false;
         if (!nv && (int64_t)kTileTok * 2 * a->v_st + 256 >= kLim) return false;
     }
     if (cbits == 4 || cbits == 6) {  // word loads
@@ -106,16 +112,17 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     pl.n_groups = (rows + pl.rg - 1) / pl.rg;
     pl.RP = pow2_at_least(pl.rg);
     pl.DT = nv ? 8 : a->value_dim / 16;
-    const bool lut_ok = a->n_centroids == kNC ? cbits == 0 || cbits == 8
-                                              : a->n_centroids == 64 && cbits != 4 && lut64_shape(*a, pl.RP, pl.DT);
+    const bool lut_ok = ct ? ct_lut
+                           : a->n_centroids == kNC ? cbits == 0 || cbits == 8
+                                                   : a->n_centroids == 64 && cbits != 4 && lut64_shape(*a, pl.RP, pl.DT);
     // Where the LUT needs row groups (or cannot serve the codes), the 4x4-MFMA-scores kernel serves
-    // up to 16 rows per pass over the pages instead (its codebook is head_dim x nc fp32 whatever
-    // the block size); kernel 4 asks for it wherever it applies
-    const bool q4_ok = !ct && ssq_decode_q4_shape(a);
+    // up to 16 rows per pass over the pages or rows instead (its codebook is head_dim x nc fp32
+    // whatever the block size); kernel 4 asks for it wherever it applies
+    const bool q4_ok = ct ? ct_q4 : ssq_decode_q4_shape(a);
     if (a->kernel == 4 && !q4_ok) return false;
     if (!lut_ok && !q4_ok) return false;
     pl.ct = ct;
-    pl.q4 = !ct && (a->kernel == 4 || !lut_ok || (pl.n_groups > 1 && q4_ok));
+    pl.q4 = q4_ok && (a->kernel == 4 || !lut_ok || pl.n_groups > 1);
     if (pl.q4) {
         pl.rg = rows < 16 ? rows : 16;
         pl.n_groups = (rows + 15) / 16;

@@ -29,6 +29,17 @@
 //               form spends as much on 4 rows as on 16.
 //   P.V       = v_mfma_f32_16x16x32_bf16 / _f16 with V fragments straight from the dim-major page
 //               (tile_softmax_pv, shared with the LUT kernel).
+//
+// With CT = true the same kernel reads the reference's contiguous rows (codes [B, Hkv, T, nb], V
+// [B, Hkv, T, 128] token-major) at head_dim 128.  The scores are unchanged.  For P.V the matrix
+// core's B operand needs 8 consecutive tokens of one dim per lane, and a token-major row gives 8
+// consecutive dims of one token.  So lane l loads 16 bytes (dims 8 (l % 16) .. + 7) of each of the
+// 8 tokens 32 g + 8 (l / 16) .. + 7 of K group g -- 16 lanes read one 256-byte row, so every load
+// is coalesced -- and transposes that 8 x 8 block of 16-bit values inside its own registers (32
+// v_perm_b32 per K group).  Fragment e then holds tokens 8 (l / 16) .. + 7 of dim 8 (l % 16) + e:
+// the B operand of one 16x16x32 MFMA whose output column l % 16 is dim 8 (l % 16) + e.  The
+// A operand (P from the strip) is the paged kernel's.  No LDS buffer, so eight waves fit beside the
+// 128 KiB codebook.
 #pragma once
 
 #include "ssq_decode_paged.h"
@@ -49,8 +60,8 @@ namespace {
 __host__ __device__ constexpr int q4_cb_floats(int KD, int nc) { return (KD * nc + 255) / 256 * 256; }
 inline size_t q4_strip_bytes(int RP, int W) { return (size_t)W * RP * kTileTok * 2; }
 inline size_t q4_smem(const ssq_decode_args& a, int RP, int split_len, int W) {
-    const size_t main = (size_t)q4_cb_floats(a.head_dim, a.n_centroids) * 4 + q4_strip_bytes(RP, W) +
-                        (size_t)split_len / kPage * 4;
+    const size_t pages = a.layout == SSQ_PAGED ? (size_t)split_len / kPage * 4 : 0;
+    const size_t main = (size_t)q4_cb_floats(a.head_dim, a.n_centroids) * 4 + q4_strip_bytes(RP, W) + pages;
     const size_t merge = (size_t)W * RP * (a.value_dim + 2) * 4;
     return main > merge ? main : merge;
 }
@@ -92,6 +103,87 @@ __device__ __forceinline__ void issue_values(const ssq_decode_args& a, const int
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) R.v[g][dt] = load_stream(src + (int64_t)(16 * dt) * a.v_st);
     }
+}
+
+// Contiguous rows (CT).  cb0 / vb0 (bytes) point at the split's first token of this (batch, KV
+// head); lim = the split's last token counted from the tile's first (>= 0).  Lanes and tokens past
+// it read that token: a valid row whose probability is 0.  Offsets from the tile's first token are
+// 32-bit (the plan keeps 64 tokens' strides below 2^31 bytes), so every load is one uniform base
+// plus a lane offset.
+template <int NB, int DT, int PB>
+__device__ __forceinline__ void issue_codes_ct(const ssq_decode_args& a, int t_begin, int t_end, int tile, int lane,
+                                               const uint8_t* cb0, TileRegs<NB, DT, PB>& R) {
+    const int rel = tile * kTileTok;
+    const int lim = t_end - 1 - t_begin - rel;
+    const uint32_t tok = (uint32_t)min(lane, lim);
+    if constexpr (PB > 0) {  // c_st counts int32 words
+        const uint32_t* prow = reinterpret_cast<const uint32_t*>(cb0) + (int64_t)rel * a.c_st + tok * (uint32_t)a.c_st;
+#pragma unroll
+        for (int i = 0; i < pk_words(NB, PB); ++i) R.pk[i] = __builtin_nontemporal_load(prow + i);
+    } else if constexpr (NB >= 16) {
+        const uint8_t* crow = cb0 + (int64_t)rel * a.c_st + tok * (uint32_t)a.c_st;
+#pragma unroll
+        for (int i = 0; i < NB / 16; ++i) {
+            const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(crow) + i);
+            R.c[i] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+    } else {
+        R.c8 = *reinterpret_cast<const uint2*>(cb0 + (int64_t)rel * a.c_st + tok * (uint32_t)a.c_st);
+    }
+}
+// R.v[g][i]: dims 8 (lane % 16) .. + 7 of token 32 g + 8 (lane / 16) + i (128-dim rows)
+template <int NB, int DT, int PB>
+__device__ __forceinline__ void issue_values_ct(const ssq_decode_args& a, int t_begin, int t_end, int tile, int lane,
+                                                const uint8_t* vb0, TileRegs<NB, DT, PB>& R) {
+    static_assert(DT == 8, "contiguous 4x4-MFMA tiles carry 128-dim values");
+    const int rel = tile * kTileTok;
+    const int lim = t_end - 1 - t_begin - rel;
+    const uint8_t* vtile = vb0 + (int64_t)rel * 2 * a.v_st;
+    const uint32_t vst = 2u * (uint32_t)a.v_st, dcol = 16u * (uint32_t)(lane & 15);
+    const int k0 = 8 * (lane >> 4);
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t tok = (uint32_t)min(32 * g + k0 + i, lim);
+            R.v[g][i] = load_stream(reinterpret_cast<const uint16_t*>(vtile + tok * vst + dcol));
+        }
+}
+
+// Dim 8 (lane % 16) + E of the 8 tokens in rows v[0..7] (row i = one token's 8 dims, two to a
+// dword, the lower dim in the low half): 8 bf16 / f16 values, token j in half j % 2 of dword j / 2.
+template <int E>
+__device__ __forceinline__ uint4 column8(const uint4 (&v)[8]) {
+    constexpr uint32_t sel = (E & 1) ? 0x07060302u : 0x05040100u;  // high or low halves of both words
+    auto word = [](const uint4& x) -> uint32_t {
+        return (E >> 1) == 0 ? x.x : (E >> 1) == 1 ? x.y : (E >> 1) == 2 ? x.z : x.w;
+    };
+    return make_uint4(__builtin_amdgcn_perm(word(v[1]), word(v[0]), sel), __builtin_amdgcn_perm(word(v[3]), word(v[2]), sel),
+                      __builtin_amdgcn_perm(word(v[5]), word(v[4]), sel), __builtin_amdgcn_perm(word(v[7]), word(v[6]), sel));
+}
+
+// P.V of a contiguous tile after tile_probs: per K group g, A = P [16 rows x 32 tokens] from the strip
+// (as in tile_softmax_pv), B = the in-register transposes of R.v[g]; acc[e] accumulates dim
+// 8 (lane % 16) + e of rows 4 (lane / 16) .. + 3.
+template <int RP, int DT, int VT, int NB, int PB>
+__device__ __forceinline__ void tile_pv_q4ct(const uint16_t* pstrip, int lane, const TileRegs<NB, DT, PB>& R,
+                                             v4f (&acc)[DT]) {
+    const int arow = lane & 15;
+    const int kchunk = 8 * (lane >> 4);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        uint4 af = make_uint4(0, 0, 0, 0);
+        if (arow < RP) af = *reinterpret_cast<const uint4*>(pstrip + arow * kTileTok + 32 * g + kchunk);
+        acc[0] = mfma<VT>(af, column8<0>(R.v[g]), acc[0]);
+        acc[1] = mfma<VT>(af, column8<1>(R.v[g]), acc[1]);
+        acc[2] = mfma<VT>(af, column8<2>(R.v[g]), acc[2]);
+        acc[3] = mfma<VT>(af, column8<3>(R.v[g]), acc[3]);
+        acc[4] = mfma<VT>(af, column8<4>(R.v[g]), acc[4]);
+        acc[5] = mfma<VT>(af, column8<5>(R.v[g]), acc[5]);
+        acc[6] = mfma<VT>(af, column8<6>(R.v[g]), acc[6]);
+        acc[7] = mfma<VT>(af, column8<7>(R.v[g]), acc[7]);
+    }
+    __builtin_amdgcn_wave_barrier();
 }
 
 // code of block blk for this lane's token (byte rows, or PB-bit codes packed in words)
@@ -205,9 +297,10 @@ __device__ __forceinline__ void tile_scores_q4(const float* cb, int nc, const Ti
 // The LDS (codebook) limits a CU to one workgroup, i.e. W / 4 waves per SIMD: telling the compiler
 // so lets it spend registers on loads in flight instead of trimming them for an occupancy the LDS
 // never allows.
-template <int KD, int BD, int R4, int DT, int VT, int PB, int W>
+template <int KD, int BD, int R4, int DT, int VT, int PB, int W, bool CT>
 __global__ __launch_bounds__(W * SSQ_WAVE) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4)))
 void k_decode_paged_q4(const MfmaParams p) {
+    static_assert(!CT || (W == 8 && DT == 8), "contiguous rows: 8 waves, 128-dim values");
     constexpr int kThreads = W * SSQ_WAVE;
     constexpr int kWaves = W;
     constexpr int NB = KD / BD;
@@ -225,19 +318,19 @@ void k_decode_paged_q4(const MfmaParams p) {
     const int nc = a.n_centroids;
     const int row0 = blockIdx.z * p.rg;       // this workgroup's query rows: row0 .. row0 + nr - 1
     const int nr = min(p.rg, p.rows - row0);  // <= RP
-    const int T = min(a.seq_lens[b], a.seq_len);
+    const int T = CT ? a.seq_len : min(a.seq_lens[b], a.seq_len);
     const int t_begin = split * p.split_len;
     const int t_end = min(T, t_begin + p.split_len);
 
     float* cb = smem;
     uint8_t* strips = reinterpret_cast<uint8_t*>(smem + q4_cb_floats(KD, nc));
     uint16_t* pstrip = reinterpret_cast<uint16_t*>(strips) + wave * RP * kTileTok;
-    int* pages = reinterpret_cast<int*>(strips + (size_t)kWaves * RP * kTileTok * 2);
+    int* pages = reinterpret_cast<int*>(strips + (size_t)kWaves * RP * kTileTok * 2);  // paged only
 
     // ---- prologue: block-table slice, this lane's permutation entries, the query rows (scaled,
     // unpermuted) through LDS into the A registers
-    const int32_t* btab = a.block_table + (int64_t)b * a.bt_sb + t_begin / kPage;
-    const int n_pages = t_end > t_begin ? (t_end - t_begin + kPage - 1) / kPage : 0;
+    const int32_t* btab = CT ? nullptr : a.block_table + (int64_t)b * a.bt_sb + t_begin / kPage;
+    const int n_pages = !CT && t_end > t_begin ? (t_end - t_begin + kPage - 1) / kPage : 0;
     for (int i = tid; i < n_pages; i += kThreads) pages[i] = btab[i];
     const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh;
     const int qi4 = lane & 3, qj = lane >> 2;
@@ -281,11 +374,25 @@ void k_decode_paged_q4(const MfmaParams p) {
     const uint8_t* cbase = PB > 0 ? reinterpret_cast<const uint8_t*>(reinterpret_cast<const uint32_t*>(a.codes) +
                                                                      (int64_t)kv * a.c_sh)
                                   : a.codes + (int64_t)kv * a.c_sh;
+    // contiguous rows: the split's first token of this (batch, KV head), in bytes
+    const uint8_t* cb0 = PB > 0 ? reinterpret_cast<const uint8_t*>(reinterpret_cast<const uint32_t*>(a.codes) +
+                                                                   (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh +
+                                                                   (int64_t)t_begin * a.c_st)
+                                : a.codes + (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)t_begin * a.c_st;
+    const uint8_t* vb0 = reinterpret_cast<const uint8_t*>(a.v) +
+                         2 * ((int64_t)b * a.v_sb + (int64_t)kv * a.v_sh + (int64_t)t_begin * a.v_st);
     const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
     const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
     TileRegs<NB, DT, PB> RA, RB;
     int tile = wave;
-    if (n_tiles > 0) issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, RA);
+    if (n_tiles > 0) {
+        if constexpr (CT) {
+            issue_codes_ct<NB, DT, PB>(a, t_begin, t_end, min(tile, last_tile), lane, cb0, RA);
+            issue_values_ct<NB, DT, PB>(a, t_begin, t_end, min(tile, last_tile), lane, vb0, RA);
+        } else {
+            issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, RA);
+        }
+    }
     (void)RB;
     // the codebook goes global -> LDS directly: 1 KiB chunks, lane l's 16 bytes at chunk + 16 l;
     // the tail chunk's lanes past the end re-read the last float4 into the padding
@@ -309,7 +416,19 @@ void k_decode_paged_q4(const MfmaParams p) {
     v4f acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = (v4f){0.f, 0.f, 0.f, 0.f};
-    if constexpr (W == 4) {
+    if constexpr (CT) {
+        // one register set, every load unconditional (clamped to the last tile), as below
+        while (tile < n_tiles) {
+            const int next = min(tile + kWaves, last_tile);
+            float s[RP];
+            tile_scores_q4<KD, BD, R4, DT, PB>(cb, nc, RA, qa, s);
+            issue_codes_ct<NB, DT, PB>(a, t_begin, t_end, next, lane, cb0, RA);
+            tile_probs<RP, DT, VT>(p, pstrip, b, kv, t_begin + tile * kTileTok, t_end, lane, s, m_run, l_lane, acc);
+            tile_pv_q4ct<RP, DT, VT, NB, PB>(pstrip, lane, RA, acc);
+            issue_values_ct<NB, DT, PB>(a, t_begin, t_end, next, lane, vb0, RA);
+            tile += kWaves;
+        }
+    } else if constexpr (W == 4) {
         while (tile < n_tiles) {
             issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RB);
             {
@@ -362,7 +481,11 @@ void k_decode_paged_q4(const MfmaParams p) {
         const int row = 4 * (lane >> 4) + i;
         if (row < RP) {
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) obuf[((size_t)wave * RP + row) * Dv + 16 * dt + (lane & 15)] = acc[dt][i];
+            for (int dt = 0; dt < DT; ++dt) {
+                // contiguous rows: accumulator dt holds dim 8 (lane % 16) + dt; pages: dim 16 dt + lane % 16
+                const int dim = CT ? 8 * (lane & 15) + dt : 16 * dt + (lane & 15);
+                obuf[((size_t)wave * RP + row) * Dv + dim] = acc[dt][i];
+            }
         }
     }
     __syncthreads();
@@ -400,10 +523,10 @@ void k_decode_paged_q4(const MfmaParams p) {
 template <int KD, int BD, int R4, int DT>
 constexpr int q4_waves() { return SSQ_Q4_WAVES; }
 
-template <int KD, int BD, int R4, int DT, int VT, int PB>
+template <int KD, int BD, int R4, int DT, int VT, int PB, bool CT>
 int launch_q4(const MfmaParams& mp, const dim3& grid, size_t, hipStream_t st) {
     constexpr int W = q4_waves<KD, BD, R4, DT>();
-    auto kern = k_decode_paged_q4<KD, BD, R4, DT, VT, PB, W>;
+    auto kern = k_decode_paged_q4<KD, BD, R4, DT, VT, PB, W, CT>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_paged_q4)");
     if (rc) return rc;
     const size_t smem = q4_smem(mp.a, 4 * R4, mp.split_len, W);
@@ -411,27 +534,33 @@ int launch_q4(const MfmaParams& mp, const dim3& grid, size_t, hipStream_t st) {
     hipLaunchKernelGGL(kern, grid, dim3(W * SSQ_WAVE), smem, st, mp);
     return ssq_check_hip(hipGetLastError(), "k_decode_paged_q4 launch");
 }
-template <int KD, int BD, int R4, int VT, int PB>
+template <int KD, int BD, int R4, int VT, int PB, bool CT>
 int q4_dt(const MfmaParams& mp, int DT, const dim3& grid, size_t smem, hipStream_t st) {
-    return DT == 4 ? launch_q4<KD, BD, R4, 4, VT, PB>(mp, grid, smem, st) : launch_q4<KD, BD, R4, 8, VT, PB>(mp, grid, smem, st);
-}
-template <int KD, int BD, int VT, int PB>
-int q4_r4(const MfmaParams& mp, int R4, int DT, const dim3& grid, size_t smem, hipStream_t st) {
-    switch (R4) {
-        case 1: return q4_dt<KD, BD, 1, VT, PB>(mp, DT, grid, smem, st);
-        case 2: return q4_dt<KD, BD, 2, VT, PB>(mp, DT, grid, smem, st);
-        case 3: return q4_dt<KD, BD, 3, VT, PB>(mp, DT, grid, smem, st);
-        default: return q4_dt<KD, BD, 4, VT, PB>(mp, DT, grid, smem, st);
+    if constexpr (CT) {  // contiguous rows: 128-dim values only
+        return DT == 8 ? launch_q4<KD, BD, R4, 8, VT, PB, true>(mp, grid, smem, st)
+                       : ssq_fail(SSQ_ERR_UNSUPPORTED, "4x4-MFMA decode: contiguous rows need 128-dim values");
+    } else {
+        return DT == 4 ? launch_q4<KD, BD, R4, 4, VT, PB, false>(mp, grid, smem, st)
+                       : launch_q4<KD, BD, R4, 8, VT, PB, false>(mp, grid, smem, st);
     }
 }
-// every instantiation for one head_dim, value dtype and code width
-template <int KD, int VT, int PB>
+template <int KD, int BD, int VT, int PB, bool CT>
+int q4_r4(const MfmaParams& mp, int R4, int DT, const dim3& grid, size_t smem, hipStream_t st) {
+    switch (R4) {
+        case 1: return q4_dt<KD, BD, 1, VT, PB, CT>(mp, DT, grid, smem, st);
+        case 2: return q4_dt<KD, BD, 2, VT, PB, CT>(mp, DT, grid, smem, st);
+        case 3: return q4_dt<KD, BD, 3, VT, PB, CT>(mp, DT, grid, smem, st);
+        default: return q4_dt<KD, BD, 4, VT, PB, CT>(mp, DT, grid, smem, st);
+    }
+}
+// every instantiation for one head_dim, value dtype, code width and layout (CT: contiguous rows)
+template <int KD, int VT, int PB, bool CT = false>
 int q4_dispatch(const MfmaParams& mp, int R4, int DT, const dim3& grid, size_t smem, hipStream_t st) {
     switch (mp.a.block_dim) {
-        case 1: if constexpr (KD <= 64) return q4_r4<KD, 1, VT, PB>(mp, R4, DT, grid, smem, st); break;
-        case 2: return q4_r4<KD, 2, VT, PB>(mp, R4, DT, grid, smem, st);
-        case 4: return q4_r4<KD, 4, VT, PB>(mp, R4, DT, grid, smem, st);
-        case 8: return q4_r4<KD, 8, VT, PB>(mp, R4, DT, grid, smem, st);
+        case 1: if constexpr (KD <= 64) return q4_r4<KD, 1, VT, PB, CT>(mp, R4, DT, grid, smem, st); break;
+        case 2: return q4_r4<KD, 2, VT, PB, CT>(mp, R4, DT, grid, smem, st);
+        case 4: return q4_r4<KD, 4, VT, PB, CT>(mp, R4, DT, grid, smem, st);
+        case 8: return q4_r4<KD, 8, VT, PB, CT>(mp, R4, DT, grid, smem, st);
         default: break;
     }
     return ssq_fail(SSQ_ERR_UNSUPPORTED, "4x4-MFMA decode: block_dim %d at head_dim %d", mp.a.block_dim, KD);
@@ -450,3 +579,7 @@ SSQ_Q4_UNIT(ssq_q4_128_bf16_bytes);
 SSQ_Q4_UNIT(ssq_q4_128_bf16_packed);
 SSQ_Q4_UNIT(ssq_q4_128_f16_bytes);
 SSQ_Q4_UNIT(ssq_q4_128_f16_packed);
+SSQ_Q4_UNIT(ssq_q4ct_128_bf16_bytes);
+SSQ_Q4_UNIT(ssq_q4ct_128_bf16_packed);
+SSQ_Q4_UNIT(ssq_q4ct_128_f16_bytes);
+SSQ_Q4_UNIT(ssq_q4ct_128_f16_packed);

@@ -1,0 +1,6 @@
+// 4x4-MFMA decode instantiations over contiguous rows: head_dim 128, bf16 values, byte codes.
+#include "ssq_decode_paged_q4.h"
+
+SSQ_Q4_UNIT(ssq_q4ct_128_bf16_bytes) {
+    return q4_dispatch<128, SSQ_BF16, 0, true>(mp, R4, DT, grid, smem, st);
+}

@@ -117,6 +117,23 @@ def config4(device="cpu", seed: int = 4, *, B: int = 64, T: int = 32768, page: i
                              "B": B, "Hq": Hq, "Hkv": Hkv, "T": T, "page": page})
 
 
+def config4_contiguous(device="cpu", seed: int = 104, *, B: int = 64, T: int = 32768, Hq: int = 32, Hkv: int = 8,
+                       D: int = 128, bd: int = 4, n_centroids: int = N_CENTROIDS) -> Problem:
+    """The config-4 layer with the reference's contiguous rows in place of pages: codes
+    [B, Hkv, T, nb] uint8 and V [B, Hkv, T, D] bf16 (token-major), the layout
+    sunshape/vllm_attn_backend.py:216-253 hands its kernel.  Codes and V are drawn on the device."""
+    dev = torch.device(device)
+    cb = make_codebook(Hkv, D, bd, seed, n_centroids=n_centroids)
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
+    gd = torch.Generator(device=dev).manual_seed(seed + 100)
+    codes = torch.randint(0, n_centroids, (B, Hkv, T, D // bd), generator=gd, device=dev, dtype=torch.uint8)
+    v = torch.randn(B, Hkv, T, D, generator=gd, device=dev, dtype=torch.bfloat16)
+    t = {"q": q.to(dev), "codes": codes, "v": v, "perm": cb.perm.to(dev), "centroids": cb.centroids.to(dev)}
+    return Problem("C4ct", t, {"scale": 1.0 / math.sqrt(D), "keys": B * Hkv * T, "head_dim": D, "block_dim": bd,
+                               "B": B, "Hq": Hq, "Hkv": Hkv, "T": T})
+
+
 def heavy_blocks_by_sigma(sigma: torch.Tensor, perm: torch.Tensor, block_dim: int, n_heavy: int) -> torch.Tensor:
     """bool [nb]: the n_heavy blocks with the largest sum of sigma^2 in the permuted basis."""
     mass = (torch.gather(sigma, -1, perm) ** 2).reshape(*perm.shape[:-1], -1, block_dim).sum(-1)
