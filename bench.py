@@ -12,7 +12,7 @@ from HIP events on its own stream, the same launch's time with cold caches (a 1 
 before each), and a bounded CPU baseline: the reference's eager torch decode path on the
 host's cores (oracle/torch_eager.py).
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c4ct|c4ctbd2|c4ctg8|c5encpro] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c4ct|c4ctbd2|c4ctg8|c4ctmix|c4mix|c5encpro] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -40,7 +40,8 @@ def _args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "c4g8", "c4bd2", "c3p6",
-                                                     "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c5encpro", "copycal"])
+                                                     "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c4ctmix", "c4mix", "c5encpro",
+                                                     "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -69,7 +70,7 @@ def _decode_workload(name, dev, kernel):
 
     heavy, pt = None, None
     nc, code_bits = 256, 0
-    if name in ("c4", "c4g8", "c4bd2", "c4p6"):
+    if name in ("c4", "c4g8", "c4bd2", "c4p6", "c4mix"):
         # c4g8 / c4bd2: the config-4 layer with 64 query heads (8 per KV head) or at 4 bits/dim
         # (64 blocks of dim 2); their LUTs exceed the LDS, so they run the MFMA-scores kernel.
         # c4p6: the layer at 3 bits/dim (64 blocks of dim 2, 64 codewords), 6-bit codes packed
@@ -83,15 +84,31 @@ def _decode_workload(name, dev, kernel):
             p.tensors["code_words"] = hip_ops.pack_codes(p["code_pages"], code_bits)
         B, Hkv, T, D = 64, 8, 32768, 128
         paged = True
-    elif name in ("c4ct", "c4ctbd2", "c4ctg8"):
+        if name == "c4mix":
+            # SunShape-Mixed on pages: the 4 blocks of dim 4 with the largest sigma mass keep their
+            # bf16 key values (16 dims per token, compact [P, Hkv, 16, 4, 4]); 28 blocks are VQ-coded
+            cb = synthetic.make_codebook(Hkv, D, bd, 4)
+            heavy = synthetic.heavy_blocks_by_sigma(cb.sigma, cb.perm, bd, 4).tolist()
+            gd = torch.Generator(device=dev).manual_seed(304)
+            P = p["code_pages"].shape[0]
+            pt = torch.randn(P, Hkv, 16, 4, bd, generator=gd, device=dev, dtype=torch.bfloat16)
+            p.tensors["pt_pages"], p.tensors["heavy"] = pt, torch.tensor(heavy)
+    elif name in ("c4ct", "c4ctbd2", "c4ctg8", "c4ctmix"):
         # the config-4 layer with the reference's contiguous rows (codes [B, Hkv, T, nb], V
         # [B, Hkv, T, D]) in place of pages; c4ctbd2 at the reference's default 4 bits/dim (64 blocks
-        # of dim 2), c4ctg8 with 64 query heads (8 per KV head): the 4x4-MFMA-scores kernel
+        # of dim 2), c4ctg8 with 64 query heads (8 per KV head): the 4x4-MFMA-scores kernel;
+        # c4ctmix: SunShape-Mixed with 4 bf16 passthrough blocks of dim 4 (compact [B, Hkv, T, 4, 4])
         B, Hkv, T, D = 64, 8, 32768, 128
         Hq = 64 if name == "c4ctg8" else 32
         bd = 2 if name == "c4ctbd2" else 4
         p = synthetic.config4_contiguous(dev, Hq=Hq, bd=bd)
         paged = False
+        if name == "c4ctmix":
+            cb = synthetic.make_codebook(Hkv, D, bd, 104)
+            heavy = synthetic.heavy_blocks_by_sigma(cb.sigma, cb.perm, bd, 4).tolist()
+            gd = torch.Generator(device=dev).manual_seed(305)
+            pt = torch.randn(B, Hkv, T, 4, bd, generator=gd, device=dev, dtype=torch.bfloat16)
+            p.tensors["pt"], p.tensors["heavy"] = pt, torch.tensor(heavy)  # pt: the launch's passthrough
     elif name == "c5":
         # SunShape-Mixed: the config-5 keys encoded once (28 VQ blocks + 4 bf16 passthrough blocks)
         p = synthetic.config5(dev)
@@ -130,8 +147,9 @@ def _decode_workload(name, dev, kernel):
     if paged:
         codes, v = p.tensors.get("code_words", p["code_pages"]), p["v_pages"]
         bt, sl = p["block_table"], p["seq_lens"]
+        pt = p.tensors.get("pt_pages")
         ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], block_table=bt, seq_lens=sl, kernel=kernel,
-                             code_bits=code_bits)
+                             code_bits=code_bits, heavy=heavy, pt=pt)
     else:
         codes, v = p["codes"], p["v"]
         ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], heavy=heavy, pt=pt, kernel=kernel,
@@ -182,6 +200,8 @@ def _decode_workload(name, dev, kernel):
                         "c4ct": "C4 layer with contiguous rows (codes [B, Hkv, T, nb], V [B, Hkv, T, D]), 2 bits/dim",
                         "c4ctbd2": "C4 layer with contiguous rows at 4 bits/dim (64 blocks of dim 2)",
                         "c4ctg8": "C4 layer with contiguous rows, 64 query heads (8 per KV head), 2 bits/dim",
+                        "c4ctmix": "C4 layer with contiguous rows, SunShape-Mixed: 28 VQ blocks + 4 bf16 passthrough blocks of dim 4",
+                        "c4mix": "C4 paged, SunShape-Mixed: 28 VQ blocks + 4 bf16 passthrough blocks of dim 4",
                         "c3": "C3 contiguous fused decode (Qwen2.5-0.5B layer, 4 bits/dim)",
                         "c5": "C5 SunShape-Mixed fused decode (config-5 keys: 28 VQ + 4 bf16 blocks of dim 2)",
                         "c3p6": "C3 layer at 3 bits/dim: 64 codewords, 6-bit codes packed in int32 words"}[name],
@@ -549,10 +569,14 @@ def _cpu_baseline(unit_data, seconds):
             codes = p.tensors.get("codes_u8", p["codes"])[b, kv].cpu()  # byte codes (unpacked)
             v = p["v"][b, kv].cpu()
         heavy, ptv = None, None
-        if "pt" in p.tensors:  # SunShape-Mixed: the reference's dense fp32 passthrough layout
+        if "pt" in p.tensors or "pt_pages" in p.tensors:  # SunShape-Mixed: the reference's dense fp32 layout
             heavy = [bool(x) for x in p["heavy"].tolist()]
             ptv = torch.zeros(codes.shape + (cent.shape[-1],), dtype=torch.float32)
-            ptv[:, torch.tensor(heavy)] = p["pt"][b, kv].float().cpu()
+            if paged:
+                ptu = p["pt_pages"][pages][:, kv].reshape(-1, *p["pt_pages"].shape[-2:])
+            else:
+                ptu = p["pt"][b, kv]
+            ptv[:, torch.tensor(heavy)] = ptu.float().cpu()
         qu = q[b, kv * G:(kv + 1) * G]
         t0 = time.perf_counter()
         TE.decode_unit(qu, codes, v, cent[kv], inv[kv], p.meta["scale"], heavy, ptv)
@@ -598,7 +622,8 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2", "c3p6", "c4p6", "c4ct", "c4ctbd2", "c4ctg8"):
+    if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2", "c3p6", "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c4ctmix",
+                         "c4mix"):
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
         step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev, args.kernel)

@@ -27,6 +27,7 @@ bool lut64_shape(const ssq_decode_args& a, int RP, int DT) {
 // when they are 8 or 16 consecutive 16-bit values with 16-byte aligned rows
 void pt_dims(const ssq_decode_args& a, SsqPagedParams& mp) {
     mp.n_hd = 0;
+    for (int i = 0; i < 16; ++i) mp.hoff[i] = mp.hdim[i] = 0;  // entries past n_hd: dim 0, never an index past D
     for (int blk = 0, h = 0; blk < a.n_blocks && blk < 64; ++blk) {
         if (!((a.heavy_mask[0] >> blk) & 1ull)) continue;
         const int slot = a.pt_dense ? blk : h;
@@ -60,15 +61,20 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     const bool nv = a->v == nullptr;
     if (nv && (!ct || !a->scores || a->mask)) return false;
     if (!nv && a->v_dtype != SSQ_BF16 && a->v_dtype != SSQ_F16) return false;
-    if (a->mask != nullptr && !ct) return false;  // masks: contiguous only
-    if (a->heavy_mask[0] || a->heavy_mask[1]) {  // passthrough: contiguous decode without a mask, <= 16 dims
-        if (!ct || nv || a->mask || a->heavy_mask[1] || !a->pt) return false;
+    // Passthrough blocks (decode, <= 16 dims among the first 64 blocks) and additive masks: the
+    // contiguous LUT kernel takes passthrough as 8 or 16 consecutive 16-bit values per token without a
+    // mask, and masks without passthrough; the 4x4-MFMA-scores kernel takes both, in any layout, with
+    // byte codes, on pages and on contiguous rows.
+    const bool heavy = a->heavy_mask[0] || a->heavy_mask[1];
+    const bool masked = a->mask != nullptr;
+    SsqPagedParams dims;
+    pt_dims(*a, dims);
+    if (heavy) {
+        if (nv || a->heavy_mask[1] || !a->pt) return false;
         if (a->pt_dtype != SSQ_F32 && a->pt_dtype != SSQ_BF16 && a->pt_dtype != SSQ_F16) return false;
         if (__builtin_popcountll(a->heavy_mask[0]) * a->block_dim > 16) return false;
-        SsqPagedParams dims;
-        pt_dims(*a, dims);
-        if (!dims.pt_vec) return false;  // 8 or 16 consecutive 16-bit values per token
     }
+    const bool mixed_bytes = !(heavy || masked) || cbits == 0 || cbits == 8;  // q4 masks / passthrough
     if (!nv && a->value_dim != 64 && a->value_dim != 128 && a->value_dim != 256) return false;
     if ((uintptr_t)a->cent % 16 || (a->cent_sh * 4) % 16) return false;  // float4 codeword loads
     if (a->n_blocks != 8 && a->n_blocks != 16 && a->n_blocks != 32 && a->n_blocks != 64) return false;
@@ -76,9 +82,8 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     // contiguous rows: the LUT kernel (CT) or the 4x4-MFMA-scores kernel (CT; head_dim 128, 128-dim
     // values, no mask, no passthrough, not scores only)
     const bool ct_lut = ct && a->head_dim != 64 && (nv || a->value_dim == 128) && a->kernel != 4 &&
-                        a->n_centroids == kNC && (cbits == 0 || cbits == 8);
-    const bool ct_q4 = ct && !nv && !a->mask && !(a->heavy_mask[0] || a->heavy_mask[1]) && a->head_dim == 128 &&
-                       a->value_dim == 128 && ssq_decode_q4_shape(a);
+                        a->n_centroids == kNC && (cbits == 0 || cbits == 8) && (!heavy || (dims.pt_vec && !masked));
+    const bool ct_q4 = ct && !nv && mixed_bytes && a->head_dim == 128 && a->value_dim == 128 && ssq_decode_q4_shape(a);
     if (ct) {
         if (!ct_lut && !ct_q4) return false;
         // tile loads take 32-bit byte offsets from the tile's first token, token strides >= 0
@@ -113,12 +118,13 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     pl.RP = pow2_at_least(pl.rg);
     pl.DT = nv ? 8 : a->value_dim / 16;
     const bool lut_ok = ct ? ct_lut
+                           : heavy || masked ? false  // pages: masks and passthrough take the 4x4-MFMA kernel
                            : a->n_centroids == kNC ? cbits == 0 || cbits == 8
                                                    : a->n_centroids == 64 && cbits != 4 && lut64_shape(*a, pl.RP, pl.DT);
     // Where the LUT needs row groups (or cannot serve the codes), the 4x4-MFMA-scores kernel serves
     // up to 16 rows per pass over the pages or rows instead (its codebook is head_dim x nc fp32
     // whatever the block size); kernel 4 asks for it wherever it applies
-    const bool q4_ok = ct ? ct_q4 : ssq_decode_q4_shape(a);
+    const bool q4_ok = ct ? ct_q4 : mixed_bytes && ssq_decode_q4_shape(a);
     if (a->kernel == 4 && !q4_ok) return false;
     if (!lut_ok && !q4_ok) return false;
     pl.ct = ct;
@@ -170,7 +176,7 @@ int ssq_decode_mfma(const ssq_decode_args* a, void* workspace, size_t ws_bytes, 
     if (a->seq_len == 0) return ssq_fail(SSQ_ERR_INVALID, "seq_len == 0: softmax over an empty context");
     SSQ_REQUIRE(ws_bytes >= pl.ws_bytes, "workspace too small: %zu < %zu bytes", ws_bytes, pl.ws_bytes);
     SSQ_REQUIRE(pl.ws_bytes == 0 || workspace, "workspace is NULL");
-    MfmaParams mp;
+    MfmaParams mp{};
     mp.a = *a;
     if (a->code_bits == 8) {  // 8-bit words are the byte rows: byte strides, the byte-code path
         mp.a.c_sb *= 4; mp.a.c_sh *= 4; mp.a.c_st *= 4;

@@ -291,16 +291,117 @@ __device__ __forceinline__ void tile_scores_q4(const float* cb, int nc, const Ti
         for (int i = 0; i < 4; ++i) s[4 * q + i] = R4 == 1 ? c0[q][i] + c1[q][i] : c0[q][i];
 }
 
+// A tile's registers beside its codes and values: the additive mask of each row for this lane's
+// token (MK) and the passthrough values of this lane's token as raw bits (HV).
+template <int RP, bool MK, int HV>
+struct TileExtra {
+    float mk[MK ? RP : 1];
+    uint32_t pt[HV ? 16 : 1];
+};
+
+// Mask and passthrough loads of one tile for this lane's token (the split's last token past its end:
+// a valid address; its probability is 0).  Rows past the workgroup's last re-read that row's mask.
+// HV 1: the n_hd (8 or 16) values are consecutive 16-bit elements in 16-byte aligned rows, two
+// 16-byte loads (the second re-reads the first with 8); HV 2: one load per value (any dtype, any
+// slots), all 16 issued under one branch on the dtype.
+template <int RP, bool MK, int HV, bool CT>
+__device__ __forceinline__ void issue_extra(const MfmaParams& p, const int* pages, int b, int kv, int t_begin, int t_end,
+                                            int tile, int lane, TileExtra<RP, MK, HV>& X) {
+    if constexpr (MK || HV > 0) {
+        const ssq_decode_args& a = p.a;
+        const int tr = min(tile * kTileTok + lane, t_end - 1 - t_begin);  // from the split's first token
+        const int64_t t = (int64_t)t_begin + tr;
+        if constexpr (MK) {
+            const int row0 = blockIdx.z * p.rg, nr = min(p.rg, p.rows - row0);
+#pragma unroll
+            for (int r = 0; r < RP; ++r) {
+                const int rr = row0 + min(r, nr - 1);
+                const int g = rr / a.q_len, qi = rr - g * a.q_len;
+                const int h = kv * p.G + g;
+                X.mk[r] = a.mask[(int64_t)b * a.m_sb + (int64_t)h * a.m_sh + (int64_t)qi * a.m_sl + t * a.m_st];
+            }
+        }
+        if constexpr (HV > 0) {
+            const int64_t row = CT ? (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + t * a.pt_st
+                                   : (int64_t)pages[tr >> 4] * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)(t & 15) * a.pt_st;
+            if constexpr (HV == 1) {
+                const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.pt) + row + p.hoff[0]);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const uint4 w = src[min(j, p.n_hd / 8 - 1)];
+                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        X.pt[8 * j + 2 * k] = ww[k] & 0xFFFFu;
+                        X.pt[8 * j + 2 * k + 1] = ww[k] >> 16;
+                    }
+                }
+            } else {
+                // slots past n_hd re-read the last one (compile-time indices into the arguments)
+                int hlast = p.hoff[0];
+#pragma unroll
+                for (int j = 1; j < 16; ++j) hlast = j < p.n_hd ? p.hoff[j] : hlast;
+                int64_t idx[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) idx[i] = row + (i < p.n_hd ? p.hoff[i] : hlast);
+                if (a.pt_dtype == SSQ_F32) {
+                    const uint32_t* f = reinterpret_cast<const uint32_t*>(a.pt);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) X.pt[i] = f[idx[i]];
+                } else {
+                    const uint16_t* h = reinterpret_cast<const uint16_t*>(a.pt);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) X.pt[i] = h[idx[i]];
+                }
+            }
+        }
+    }
+}
+
+// Scores of the passthrough dims and the mask, added to a tile's scores s (whose MFMA pass saw zero
+// query values on those dims): one 4x4x1 MFMA per passthrough dim i and row quad q, the A operand
+// qh[q] broadcast from block i (lane 4 i + r holds q_perm[row 4 q + r][hdim[i]]), the B operand this
+// lane's stored value of dim i.
+template <int R4, bool MK, int HV>
+__device__ __forceinline__ void tile_extra_scores(const MfmaParams& p, const float (&qh)[R4], const TileExtra<4 * R4, MK, HV>& X,
+                                                  float (&s)[4 * R4]) {
+    if constexpr (HV > 0) {
+        v4f c[R4];
+#pragma unroll
+        for (int q = 0; q < R4; ++q) c[q] = (v4f){0.f, 0.f, 0.f, 0.f};
+        static_for<0, 16>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            if (i < p.n_hd) {  // wave-uniform
+                const float x = ssq_bits_to_f32(X.pt[i], p.a.pt_dtype);
+#pragma unroll
+                for (int q = 0; q < R4; ++q) c[q] = __builtin_amdgcn_mfma_f32_4x4x1f32(qh[q], x, c[q], 4, i, 0);
+            }
+        });
+#pragma unroll
+        for (int q = 0; q < R4; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[4 * q + i] += c[q][i];
+    }
+    if constexpr (MK) {
+        const int nr = min(p.rg, p.rows - (int)blockIdx.z * p.rg);
+#pragma unroll
+        for (int r = 0; r < 4 * R4; ++r) s[r] += r < nr ? X.mk[r] : 0.f;
+    }
+}
+
 // W waves per workgroup: 4 (one per SIMD) keep two tiles in flight per wave in two register sets;
 // 8 (two per SIMD, so one wave's matrix-core phase overlaps the other's VALU and LDS phases) keep
 // one set, reloading a tile's codes once its scores are done and its values once its P.V is done.
 // The LDS (codebook) limits a CU to one workgroup, i.e. W / 4 waves per SIMD: telling the compiler
 // so lets it spend registers on loads in flight instead of trimming them for an occupancy the LDS
 // never allows.
-template <int KD, int BD, int R4, int DT, int VT, int PB, int W, bool CT>
+// MK: an additive mask; HV: passthrough blocks (1: 8 or 16 consecutive 16-bit values per token, 2:
+// any layout and dtype); both with byte codes only.
+template <int KD, int BD, int R4, int DT, int VT, int PB, int W, bool CT, bool MK, int HV>
 __global__ __launch_bounds__(W * SSQ_WAVE) __attribute__((amdgpu_waves_per_eu(W / 4, W / 4)))
 void k_decode_paged_q4(const MfmaParams p) {
     static_assert(!CT || (W == 8 && DT == 8), "contiguous rows: 8 waves, 128-dim values");
+    static_assert(!(MK || HV) || (W == 8 && PB == 0), "masks and passthrough: 8 waves, byte codes");
     constexpr int kThreads = W * SSQ_WAVE;
     constexpr int kWaves = W;
     constexpr int NB = KD / BD;
@@ -367,7 +468,22 @@ void k_decode_paged_q4(const MfmaParams p) {
 #pragma unroll
     for (int q = 0; q < R4; ++q)
 #pragma unroll
-        for (int kk = 0; kk < KQ; ++kk) qa[q][kk] = qs[(4 * q + qi4) * KD + (int)min((uint64_t)pj[kk], (uint64_t)(KD - 1))];
+        for (int kk = 0; kk < KQ; ++kk) {
+            qa[q][kk] = qs[(4 * q + qi4) * KD + (int)min((uint64_t)pj[kk], (uint64_t)(KD - 1))];
+            // passthrough blocks score from their stored values (tile_extra_scores): no codeword term
+            if constexpr (HV > 0)
+                if ((a.heavy_mask[0] >> ((16 * kk + qj) / BD)) & 1ull) qa[q][kk] = 0.f;
+        }
+    // the query rows at the passthrough dims: lane 4 j + r holds q_perm[row 4 q + r][hdim[j]] (j < n_hd)
+    float qh[R4];  // (unused without passthrough)
+    if constexpr (HV > 0) {
+        int hd = 0;  // lanes past the last passthrough dim keep dim 0 (their query value is not used)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) hd = j == qj && j < p.n_hd ? p.hdim[j] : hd;
+        const int pd = (int)min((uint64_t)perm[hd], (uint64_t)(KD - 1));
+#pragma unroll
+        for (int q = 0; q < R4; ++q) qh[q] = qj < p.n_hd ? qs[(4 * q + qi4) * KD + pd] : 0.f;
+    }
     __syncthreads();  // every wave has its A registers: the strips are free
 
     const uint16_t* vbase = reinterpret_cast<const uint16_t*>(a.v) + (int64_t)kv * a.v_sh + (int64_t)(lane & 15) * a.v_st;
@@ -384,6 +500,7 @@ void k_decode_paged_q4(const MfmaParams p) {
     const int n_tiles = (t_end - t_begin + kTileTok - 1) / kTileTok;
     const int last_tile = n_tiles > 0 ? n_tiles - 1 : 0;
     TileRegs<NB, DT, PB> RA, RB;
+    TileExtra<RP, MK, HV> XA;
     int tile = wave;
     if (n_tiles > 0) {
         if constexpr (CT) {
@@ -392,6 +509,7 @@ void k_decode_paged_q4(const MfmaParams p) {
         } else {
             issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile, last_tile), lane, cbase, vbase, RA);
         }
+        issue_extra<RP, MK, HV, CT>(p, pages, b, kv, t_begin, t_end, min(tile, last_tile), lane, XA);
     }
     (void)RB;
     // the codebook goes global -> LDS directly: 1 KiB chunks, lane l's 16 bytes at chunk + 16 l;
@@ -422,13 +540,16 @@ void k_decode_paged_q4(const MfmaParams p) {
             const int next = min(tile + kWaves, last_tile);
             float s[RP];
             tile_scores_q4<KD, BD, R4, DT, PB>(cb, nc, RA, qa, s);
+            tile_extra_scores<R4, MK, HV>(p, qh, XA, s);
             issue_codes_ct<NB, DT, PB>(a, t_begin, t_end, next, lane, cb0, RA);
+            issue_extra<RP, MK, HV, CT>(p, pages, b, kv, t_begin, t_end, next, lane, XA);
             tile_probs<RP, DT, VT>(p, pstrip, b, kv, t_begin + tile * kTileTok, t_end, lane, s, m_run, l_lane, acc);
             tile_pv_q4ct<RP, DT, VT, NB, PB>(pstrip, lane, RA, acc);
             issue_values_ct<NB, DT, PB>(a, t_begin, t_end, next, lane, vb0, RA);
             tile += kWaves;
         }
     } else if constexpr (W == 4) {
+        static_assert(!MK && HV == 0, "4-wave build: no mask or passthrough variants");
         while (tile < n_tiles) {
             issue_tile<NB, DT, PB>(a, pages, t_begin, t_end, min(tile + kWaves, last_tile), lane, cbase, vbase, RB);
             {
@@ -455,7 +576,9 @@ void k_decode_paged_q4(const MfmaParams p) {
             const int next = min(tile + kWaves, last_tile);
             float s[RP];
             tile_scores_q4<KD, BD, R4, DT, PB>(cb, nc, RA, qa, s);
+            tile_extra_scores<R4, MK, HV>(p, qh, XA, s);
             issue_codes<NB, DT, PB>(a, pages, t_begin, t_end, next, lane, cbase, RA);
+            issue_extra<RP, MK, HV, CT>(p, pages, b, kv, t_begin, t_end, next, lane, XA);
             tile_softmax_pv<RP, DT, VT, NB, PB>(p, pstrip, b, kv, t_begin + tile * kTileTok, t_end, lane, s, RA, m_run,
                                                 l_lane, acc);
             issue_values<NB, DT, PB>(a, pages, t_begin, t_end, next, lane, vbase, RA);
@@ -523,10 +646,10 @@ void k_decode_paged_q4(const MfmaParams p) {
 template <int KD, int BD, int R4, int DT>
 constexpr int q4_waves() { return SSQ_Q4_WAVES; }
 
-template <int KD, int BD, int R4, int DT, int VT, int PB, bool CT>
+template <int KD, int BD, int R4, int DT, int VT, int PB, bool CT, bool MK, int HV>
 int launch_q4(const MfmaParams& mp, const dim3& grid, size_t, hipStream_t st) {
     constexpr int W = q4_waves<KD, BD, R4, DT>();
-    auto kern = k_decode_paged_q4<KD, BD, R4, DT, VT, PB, W, CT>;
+    auto kern = k_decode_paged_q4<KD, BD, R4, DT, VT, PB, W, CT, MK, HV>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode_paged_q4)");
     if (rc) return rc;
     const size_t smem = q4_smem(mp.a, 4 * R4, mp.split_len, W);
@@ -534,36 +657,48 @@ int launch_q4(const MfmaParams& mp, const dim3& grid, size_t, hipStream_t st) {
     hipLaunchKernelGGL(kern, grid, dim3(W * SSQ_WAVE), smem, st, mp);
     return ssq_check_hip(hipGetLastError(), "k_decode_paged_q4 launch");
 }
-template <int KD, int BD, int R4, int VT, int PB, bool CT>
+template <int KD, int BD, int R4, int VT, int PB, bool CT, bool MK, int HV>
 int q4_dt(const MfmaParams& mp, int DT, const dim3& grid, size_t smem, hipStream_t st) {
     if constexpr (CT) {  // contiguous rows: 128-dim values only
-        return DT == 8 ? launch_q4<KD, BD, R4, 8, VT, PB, true>(mp, grid, smem, st)
+        return DT == 8 ? launch_q4<KD, BD, R4, 8, VT, PB, true, MK, HV>(mp, grid, smem, st)
                        : ssq_fail(SSQ_ERR_UNSUPPORTED, "4x4-MFMA decode: contiguous rows need 128-dim values");
     } else {
-        return DT == 4 ? launch_q4<KD, BD, R4, 4, VT, PB, false>(mp, grid, smem, st)
-                       : launch_q4<KD, BD, R4, 8, VT, PB, false>(mp, grid, smem, st);
+        return DT == 4 ? launch_q4<KD, BD, R4, 4, VT, PB, false, MK, HV>(mp, grid, smem, st)
+                       : launch_q4<KD, BD, R4, 8, VT, PB, false, MK, HV>(mp, grid, smem, st);
     }
 }
-template <int KD, int BD, int VT, int PB, bool CT>
+template <int KD, int BD, int VT, int PB, bool CT, bool MK, int HV>
 int q4_r4(const MfmaParams& mp, int R4, int DT, const dim3& grid, size_t smem, hipStream_t st) {
     switch (R4) {
-        case 1: return q4_dt<KD, BD, 1, VT, PB, CT>(mp, DT, grid, smem, st);
-        case 2: return q4_dt<KD, BD, 2, VT, PB, CT>(mp, DT, grid, smem, st);
-        case 3: return q4_dt<KD, BD, 3, VT, PB, CT>(mp, DT, grid, smem, st);
-        default: return q4_dt<KD, BD, 4, VT, PB, CT>(mp, DT, grid, smem, st);
+        case 1: return q4_dt<KD, BD, 1, VT, PB, CT, MK, HV>(mp, DT, grid, smem, st);
+        case 2: return q4_dt<KD, BD, 2, VT, PB, CT, MK, HV>(mp, DT, grid, smem, st);
+        case 3: return q4_dt<KD, BD, 3, VT, PB, CT, MK, HV>(mp, DT, grid, smem, st);
+        default: return q4_dt<KD, BD, 4, VT, PB, CT, MK, HV>(mp, DT, grid, smem, st);
     }
 }
-// every instantiation for one head_dim, value dtype, code width and layout (CT: contiguous rows)
-template <int KD, int VT, int PB, bool CT = false>
+// every instantiation for one head_dim, value dtype, code width and layout (CT: contiguous rows), with
+// a mask (MK) and passthrough blocks (HV) or without
+template <int KD, int VT, int PB, bool CT = false, bool MK = false, int HV = 0>
 int q4_dispatch(const MfmaParams& mp, int R4, int DT, const dim3& grid, size_t smem, hipStream_t st) {
     switch (mp.a.block_dim) {
-        case 1: if constexpr (KD <= 64) return q4_r4<KD, 1, VT, PB, CT>(mp, R4, DT, grid, smem, st); break;
-        case 2: return q4_r4<KD, 2, VT, PB, CT>(mp, R4, DT, grid, smem, st);
-        case 4: return q4_r4<KD, 4, VT, PB, CT>(mp, R4, DT, grid, smem, st);
-        case 8: return q4_r4<KD, 8, VT, PB, CT>(mp, R4, DT, grid, smem, st);
+        case 1: if constexpr (KD <= 64) return q4_r4<KD, 1, VT, PB, CT, MK, HV>(mp, R4, DT, grid, smem, st); break;
+        case 2: return q4_r4<KD, 2, VT, PB, CT, MK, HV>(mp, R4, DT, grid, smem, st);
+        case 4: return q4_r4<KD, 4, VT, PB, CT, MK, HV>(mp, R4, DT, grid, smem, st);
+        case 8: return q4_r4<KD, 8, VT, PB, CT, MK, HV>(mp, R4, DT, grid, smem, st);
         default: break;
     }
     return ssq_fail(SSQ_ERR_UNSUPPORTED, "4x4-MFMA decode: block_dim %d at head_dim %d", mp.a.block_dim, KD);
+}
+// the mask / passthrough variants of one head_dim, value dtype and layout (byte codes): passthrough
+// values loaded as vectors (HV 1) without a mask, element by element (HV 2) otherwise
+template <int KD, int VT, bool CT>
+int q4_dispatch_mixed(const MfmaParams& mp, int R4, int DT, const dim3& grid, size_t smem, hipStream_t st) {
+    const bool mk = mp.a.mask != nullptr;
+    const bool hv = mp.a.heavy_mask[0] != 0;
+    if (!hv) return q4_dispatch<KD, VT, 0, CT, true, 0>(mp, R4, DT, grid, smem, st);
+    if (mk) return q4_dispatch<KD, VT, 0, CT, true, 2>(mp, R4, DT, grid, smem, st);
+    if (mp.pt_vec) return q4_dispatch<KD, VT, 0, CT, false, 1>(mp, R4, DT, grid, smem, st);
+    return q4_dispatch<KD, VT, 0, CT, false, 2>(mp, R4, DT, grid, smem, st);
 }
 
 }  // namespace
@@ -583,3 +718,9 @@ SSQ_Q4_UNIT(ssq_q4ct_128_bf16_bytes);
 SSQ_Q4_UNIT(ssq_q4ct_128_bf16_packed);
 SSQ_Q4_UNIT(ssq_q4ct_128_f16_bytes);
 SSQ_Q4_UNIT(ssq_q4ct_128_f16_packed);
+SSQ_Q4_UNIT(ssq_q4_64_bf16_mixed);
+SSQ_Q4_UNIT(ssq_q4_64_f16_mixed);
+SSQ_Q4_UNIT(ssq_q4_128_bf16_mixed);
+SSQ_Q4_UNIT(ssq_q4_128_f16_mixed);
+SSQ_Q4_UNIT(ssq_q4ct_128_bf16_mixed);
+SSQ_Q4_UNIT(ssq_q4ct_128_f16_mixed);

@@ -1,0 +1,7 @@
+// 4x4-MFMA paged decode instantiations: head_dim 64, f16 values, byte codes, with an additive
+// mask and / or passthrough blocks.
+#include "ssq_decode_paged_q4.h"
+
+SSQ_Q4_UNIT(ssq_q4_64_f16_mixed) {
+    return q4_dispatch_mixed<64, SSQ_F16, false>(mp, R4, DT, grid, smem, st);
+}
