@@ -229,7 +229,7 @@ def _surface_call(p, paged, q, codes, v, perm, cent, heavy, pt, code_bits, kerne
     from sunshape_amd.integration.vllm import SunShapeVLLMRuntimeState
 
     scale = p.meta["scale"]
-    if paged or code_bits:
+    if paged or code_bits or kernel:  # an explicit kernel choice: the drop-in surface has no such argument
         kw = dict(block_table=p["block_table"], seq_lens=p["seq_lens"]) if paged else {}
         return "hip_ops.decode", lambda: hip_ops.decode(q, codes, v, perm, cent, scale=scale, heavy=heavy, pt=pt,
                                                         kernel=kernel, code_bits=code_bits, **kw)

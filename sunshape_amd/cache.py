@@ -247,8 +247,8 @@ class SunShapeCache(DynamicCache):
             else:
                 continue
             if sliding is not None:
-                if self.store_codes and i in layer_codecs:
-                    raise NotImplementedError("SunShapeCodeLayer does not implement sliding-window eviction")
+                # As the reference's layer (sunshape/cache.py:86-104): every token is kept and HF's
+                # sliding-window mask limits attention (the code layer's attention takes that mask).
                 new_layer.sliding_window = sliding
             self.layers[i] = new_layer
 
@@ -278,11 +278,12 @@ class SunShapeCache(DynamicCache):
 # ---------------------------------------------------------------------------- attention
 # multi-token steps take the fused decode up to this many query rows per KV head; longer ones attend
 # dequantized keys.  16 is the row count the head_dim-64 contiguous MFMA kernel holds in one pass.
-# Where the 128-dim LUT kernel serves the step (128-dim values past head_dim 64, no passthrough
-# blocks) the fused decode measured faster than dequantize + SDPA up to 256 rows per KV head
-# (B4 · 32/8 heads · T16384: 1.07 against 2.09 ms at 64 new tokens).
+# At head_dim 128 with 128-dim values the step runs on the contiguous LUT kernel or, with more rows
+# than its LUT holds, with passthrough blocks (at most 16 dims) or both, on the 4x4-MFMA kernel (16
+# rows per pass); the fused decode measured faster than dequantize + SDPA up to 256 rows per KV
+# head there (B4 · 32/8 heads · T16384: 1.07 against 2.09 ms at 64 new tokens, LUT kernel).
 _FUSED_MAX_ROWS = 16
-_FUSED_MAX_ROWS_LUT128 = 256
+_FUSED_MAX_ROWS_128 = 256
 
 
 def _additive_mask(mask: Optional[torch.Tensor], dtype=torch.float32) -> Optional[torch.Tensor]:
@@ -314,19 +315,25 @@ def sunshape_attention_forward(module: torch.nn.Module, query: torch.Tensor, key
     B, Hq, Lq, D = query.shape
     T = key.codes.shape[2]
     rows = (Hq // value.shape[1]) * Lq  # query rows per KV head
-    lut128 = D != 64 and value.shape[-1] == 128 and key.codec.heavy_blocks() is None
-    if Lq == 1 or (T > Lq and rows <= (_FUSED_MAX_ROWS_LUT128 if lut128 else _FUSED_MAX_ROWS)):
+    heavy = key.codec.heavy_blocks()
+    pt_dims = 0 if heavy is None else sum(heavy) * key.codec.block_dim
+    fused128 = D == 128 and value.shape[-1] == 128 and pt_dims <= 16
+    if Lq == 1 or (T > Lq and rows <= (_FUSED_MAX_ROWS_128 if fused128 else _FUSED_MAX_ROWS)):
         # a decode step, or a short multi-token step over a filled cache (speculative verification,
-        # small chunks): the fused decode over the codes, masked as HF's mask builder says (or
-        # causally, the new tokens being the last Lq positions)
+        # small chunks): the fused decode over the codes, masked as HF's mask builder says, or without
+        # a mask causally (the new tokens being the last Lq positions) when the call is causal, as
+        # HF's SDPA function decides it (is_causal, else the module's is_causal, else causal)
         mask = _additive_mask(attention_mask)
+        causal = is_causal if is_causal is not None else getattr(module, "is_causal", True)
         if mask is not None:
             mask = mask[..., -T:]
-        elif Lq > 1:
+        elif Lq > 1 and causal:
             pos = torch.arange(T, device=query.device)
             last = T - Lq + torch.arange(Lq, device=query.device)
             mask = torch.zeros(1, 1, Lq, T, device=query.device).masked_fill(pos[None, :] > last[:, None],
                                                                               float("-inf"))
+        if scaling is None:  # SDPA's default scale
+            scaling = 1.0 / D ** 0.5
         perm, cent = _per_head_arrays(key.codec)
         out = hip_ops.decode(query, key.codes, value, perm, cent, scale=scaling, mask=mask,
                              heavy=key.codec.heavy_blocks(), pt=key.passthrough, pt_dense=False,

@@ -65,6 +65,18 @@ class SunShapeBundle:
     codecs: dict[int, SunShapeBlockCodec]
     trace_meta: dict = field(default_factory=dict)
 
+    def make_cache(self, *, config=None, num_layers: int | None = None, store_codes: bool = False):
+        """An HF cache whose bundle layers hold this bundle's codecs (sunshape/hf.py:267-268).
+
+        store_codes=False is the reference's cache (keys quantised and dequantised, stored dense);
+        store_codes=True keeps the codes (``SunShapeCodeLayer``; the model then attends with the
+        ``"sunshape"`` attention implementation, ``cache.register_sunshape_attention``).
+        """
+        from .cache import SunShapeCache
+
+        return SunShapeCache.from_codecs(codecs_dict=self.codecs, config=config, num_layers=num_layers,
+                                         store_codes=store_codes)
+
     def state_dict(self) -> dict:
         """sunshape/hf.py:273-297."""
         codec_state = {}

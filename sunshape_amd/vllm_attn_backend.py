@@ -8,12 +8,17 @@ reference's Python loop (:230-252).
 
 Differences by design:
 * ``SunShapeQuantizedKeys`` may carry the batched code tensor it was built from
-  (``codes`` [B, Hkv, S, nb], ``passthrough`` [B, Hkv, S, slots, bd]); the
-  per-head tuple view ``quantized_heads`` is still provided.
-* A quantized payload that fails the fast-path gate raises
-  ``RuntimeError(reason)`` instead of being dequantized and re-routed
-  (sunshape/vllm_attn_backend.py:306-307); dense keys still go to the delegate
-  or SDPA exactly as in the reference (:307-345), after the codec round trip.
+  (``codes`` [B, Hkv, S, nb]) and the passthrough values of SunShape-Mixed codecs
+  in the compact layout (``passthrough`` [B, Hkv, S, n_heavy, bd] in the key dtype:
+  the reference's dense fp32 [S, nb, bd] holds ``keys.float()`` on heavy blocks and
+  zeros elsewhere, so the compact values are the same numbers in 1/8-1/32 of the
+  bytes).  The per-head view ``quantized_heads`` still yields the reference's
+  ``SunShapeQuantized`` payloads, each built (with its dense fp32 passthrough) when
+  it is read.
+* A causal call with several query rows over a quantized payload runs the fused
+  kernel from the codes with the mask and scale the reference's SDPA route applies
+  (:306-345); any other payload that fails the fast-path gate is dequantized in
+  one batched launch and handed to the delegate or SDPA as in the reference.
 """
 
 from __future__ import annotations
@@ -21,6 +26,7 @@ from __future__ import annotations
 import math
 
 import os
+from collections.abc import Sequence
 from dataclasses import dataclass
 from typing import Any
 
@@ -38,6 +44,42 @@ MODE_OFF = "off"
 _MODE = MODE_OFF
 _ACTIVE_HANDLE: SunShapeVLLMHandle | None = None
 _RUNTIME_STATE: SunShapeVLLMRuntimeState | None = None
+
+
+class _HeadPayloads(Sequence):
+    """The per-(batch, KV head) ``SunShapeQuantized`` payloads of one batched encode, index
+    ``b * Hkv + h`` (the reference's tuple order, sunshape/vllm_attn_backend.py:112-123).  Each is
+    built when read: indices are a view of the batched codes, and a SunShape-Mixed payload's
+    passthrough_values the reference's dense fp32 [S, nb, bd] (zeros on light blocks) expanded from
+    the compact values."""
+
+    def __init__(self, codes: torch.Tensor, passthrough: torch.Tensor | None, passthrough_blocks: torch.Tensor | None,
+                 head_dim: int, block_dim: int, n_blocks: int):
+        self._codes = codes
+        self._pt = passthrough
+        self._pblocks = passthrough_blocks
+        self._dims = (int(head_dim), int(block_dim), int(n_blocks))
+        self._hkv = int(codes.shape[1])
+
+    def __len__(self) -> int:
+        return int(self._codes.shape[0]) * self._hkv
+
+    def __getitem__(self, i):
+        if isinstance(i, slice):
+            return tuple(self[j] for j in range(*i.indices(len(self))))
+        n = len(self)
+        if not -n <= i < n:
+            raise IndexError("quantized head index out of range")
+        b, h = divmod(i % n, self._hkv)
+        head_dim, block_dim, n_blocks = self._dims
+        dense = None
+        if self._pt is not None:
+            heavy = self._pblocks.to(self._pt.device, torch.bool)
+            dense = torch.zeros(self._codes.shape[2], n_blocks, block_dim, device=self._pt.device, dtype=torch.float32)
+            dense[:, heavy] = self._pt[b, h].float()
+        return SunShapeQuantized(indices=self._codes[b, h], head_dim=head_dim, block_dim=block_dim, n_blocks=n_blocks,
+                                 passthrough_blocks=None if self._pblocks is None else self._pblocks.clone(),
+                                 passthrough_values=dense)
 
 
 @dataclass(frozen=True)
@@ -147,38 +189,32 @@ def quantize_key_states(layer_idx: int, key_states: torch.Tensor) -> SunShapeQua
         keys = keys.float()
     metric = codec.encode_metric() if hasattr(codec, "encode_metric") else None
     grid = codec.encode_search_grid(cent) if hasattr(codec, "encode_search_grid") else None
-    # the reference quantizes one (batch, KV head) per call: seq_len keys per cdist
     rot = codec.rotation_matrix() if hasattr(codec, "rotation_matrix") else None
-    codes, pt = hip_ops.encode(keys, perm, cent, heavy=heavy, pt_dtype=torch.float32, pt_dense=True, metric=metric,
+    # Passthrough values compact [B, Hkv, S, n_heavy, bd] in the key dtype: the reference stores
+    # keys.float() there (sunshape/codec.py:368-372), which the key dtype holds exactly.  Under a
+    # rotation they are transformed values, kept in fp32.
+    pt_dtype = torch.float32 if rot is not None else keys.dtype
+    # the reference quantizes one (batch, KV head) per call: seq_len keys per cdist
+    codes, pt = hip_ops.encode(keys, perm, cent, heavy=heavy, pt_dtype=pt_dtype, pt_dense=False, metric=metric,
                                grid=grid, direct=hip_ops.cdist_direct(seq_len, cent.shape[-2]), rotation=rot)
     mixed = codec.mode == "profileperm_mixed_precision"
     pblocks = codec.mixed_high_precision_blocks.detach().clone() if mixed else None
-    heads = []
-    for b in range(batch_size):
-        for h in range(num_kv_heads):
-            heads.append(SunShapeQuantized(
-                indices=codes[b, h],
-                head_dim=codec.head_dim,
-                block_dim=codec.block_dim,
-                n_blocks=codec.n_blocks,
-                passthrough_blocks=pblocks,
-                passthrough_values=None if pt is None else pt[b, h],
-            ))
     return SunShapeQuantizedKeys(
-        quantized_heads=tuple(heads),
+        quantized_heads=_HeadPayloads(codes, pt, pblocks, codec.head_dim, codec.block_dim, codec.n_blocks),
         batch_size=int(batch_size),
         num_kv_heads=int(num_kv_heads),
         seq_len=int(seq_len),
         codes=codes,
         passthrough=pt,
-        passthrough_dense=True,
+        passthrough_dense=False,
     )
 
 
 def _dequantize_key_payload_if_needed(layer_idx: int | None, key_states: Any) -> Any:
-    """Dense fp32 keys [B, Hkv, S, D] from a quantized payload, one ``codec.dequantize`` (the
-    ssq_dequantize kernel) per (batch, KV head), as sunshape/vllm_attn_backend.py:140-156 does;
-    other key states pass through."""
+    """Dense fp32 keys [B, Hkv, S, D] from a quantized payload (what the reference's per-head
+    ``codec.dequantize`` loop gives, sunshape/vllm_attn_backend.py:140-156): one ssq_dequantize
+    launch over every (batch, KV head) of a per-layer codec, one per KV head of a per-KV-head
+    codec.  Other key states pass through."""
     if not isinstance(key_states, SunShapeQuantizedKeys):
         return key_states
     runtime = get_registered_runtime()
@@ -186,14 +222,24 @@ def _dequantize_key_payload_if_needed(layer_idx: int | None, key_states: Any) ->
         raise RuntimeError("SunShape runtime state is required to dequantize quantized key payloads.")
     codec = runtime.codec_for_layer(int(layer_idx))
     if codec is None:
-        raise RuntimeError(f"No SunShape codec is registered for layer {layer_idx}.")
-    per_head = getattr(codec, "num_kv_heads", None) is not None
-    batches = []
-    for b in range(key_states.batch_size):
-        heads = [codec.dequantize(key_states.head(b, h), kv_head=h if per_head else None)
-                 for h in range(key_states.num_kv_heads)]
-        batches.append(torch.stack(heads, dim=0))
-    return torch.stack(batches, dim=0)
+        raise RuntimeError(f"No codec is registered for layer {layer_idx}.")
+    B, Hkv, S = key_states.batch_size, key_states.num_kv_heads, key_states.seq_len
+    codes, pt, dense = key_states.batched()
+    heavy = codec.heavy_blocks() if hasattr(codec, "heavy_blocks") else None
+    if heavy is not None and pt is None:
+        raise ValueError("Mixed-precision quantized keys are missing passthrough values.")
+    rot = codec.rotation_matrix() if hasattr(codec, "rotation_matrix") else None
+    nb = codes.shape[-1]
+    out = torch.empty(B, Hkv, S, codec.head_dim, device=codes.device, dtype=torch.float32)
+    heads = range(Hkv) if getattr(codec, "num_kv_heads", None) is not None else [None]
+    for h in heads:
+        sel = slice(None) if h is None else h
+        c = codes[:, sel].reshape(-1, nb)
+        p = None if heavy is None else pt[:, sel].reshape(-1, *pt.shape[-2:])
+        k = hip_ops.dequantize(c, codec.effective_permutation(h), codec.codebook(h), heavy=heavy, pt=p,
+                               pt_dense=dense, rotation=rot)
+        out[:, sel] = k.view(B, -1, S, codec.head_dim) if h is None else k.view(B, S, codec.head_dim)
+    return out
 
 
 def _causal_mask(query_len: int, seq_len: int, device) -> torch.Tensor:

@@ -678,3 +678,42 @@ def test_paged_q4_kernel_vs_oracle(G, bd, D, Dv, nc, vdt, splits):
             assert_rel(l[b, sl], rl, SCORE_TOL, f"q4 lse b={b} kv={kv}")
             assert_rel(sc[b, sl, :, :L], rs, SCORE_TOL, f"q4 scores b={b} kv={kv}")
             assert np.all(sc[b, sl, :, L:] == -np.inf)
+
+
+@pytest.mark.parametrize("Hq,Hkv,Lq,bd,hidx,dense,splits", [
+    (8, 8, 1, 4, [5, 20], False, 0),         # one row per KV head (RP 1), 8 passthrough dims
+    (16, 8, 1, 4, [3, 9, 11, 30], False, 2),  # two rows (RP 2), 16 dims, two splits
+    (16, 2, 1, 8, [1, 6], False, 0),         # eight rows (RP 8) over 16 blocks of dim 8, 16 dims
+    (4, 2, 3, 8, [4, 12], False, 3),         # three query tokens: 6 rows in an 8-row LUT, three splits
+    (8, 8, 1, 4, [2, 3], True, 0),           # dense slots of adjacent heavy blocks: values 8..15 of each row
+    (32, 8, 1, 4, [2, 3, 4, 5], True, 1),    # dense slots, four adjacent blocks: values 8..23
+])
+def test_contiguous_lut_kernel_128_dim_passthrough_rows(Hq, Hkv, Lq, bd, hidx, dense, splits):
+    """The contiguous 128-dim LUT kernel's passthrough variant (8 or 16 consecutive 16-bit values per
+    token in 16-byte aligned rows) at 1, 2 and 8 rows per LUT, with several query tokens and splits,
+    and with the reference's dense slots where the heavy blocks are adjacent (so their values are
+    consecutive from a 16-byte aligned slot); against the oracle."""
+    log(f"contig LUT D128 passthrough rows Hq={Hq} Hkv={Hkv} Lq={Lq} bd={bd} heavy={hidx} dense={dense}")
+    B, T, D = 2, 431, 128
+    nb = D // bd
+    cb = synthetic.make_codebook(Hkv, D, bd, 230 + Hq + bd)
+    g = torch.Generator().manual_seed(231 + Hq + bd)
+    heavy = [i in hidx for i in range(nb)]
+    q = torch.randn(B, Hq, Lq, D, generator=g).to(torch.bfloat16)
+    codes = torch.randint(0, 256, (B, Hkv, T, nb), generator=g, dtype=torch.uint8)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+    ptd = torch.zeros(B, Hkv, T, nb, bd)
+    ptd[:, :, :, hidx] = torch.randn(B, Hkv, T, len(hidx), bd, generator=g)
+    ptd = ptd.to(torch.bfloat16)
+    pt = ptd if dense else ptd[:, :, :, hidx].contiguous()
+    scale = 1 / math.sqrt(D)
+    args = (q.to(DEV), codes.to(DEV), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+    kw = dict(scale=scale, heavy=heavy, pt=pt.to(DEV), pt_dense=dense, num_splits=splits)
+    out, lse, scores = hip_ops.decode(*args, **kw, return_lse=True, return_scores=True, kernel=2)
+    ro, rs, rl = O.decode_attention(q.float().numpy(), codes.numpy(), v.float().numpy(), cb.centroids.numpy(),
+                                    cb.perm.numpy(), scale, "bf16", "bf16", heavy=np.array(heavy),
+                                    pt_values=ptd.float().numpy(), return_scores=True)
+    assert_rel(np_of(out), ro, BF16_TOL, "out")
+    assert_rel(np_of(scores), rs, SCORE_TOL, "scores")
+    assert_rel(np_of(lse), rl, SCORE_TOL, "lse")
+    assert torch.equal(hip_ops.decode(*args, **kw), out)  # the automatic choice

@@ -180,3 +180,71 @@ def test_tiny_llama_code_cache_tracks_dequant_cache():
     assert torch.equal(logits[0], ref_logits[0])
     for a, r in zip(logits[1:], ref_logits[1:]):
         assert_rel(a.float().cpu().numpy(), r.float().cpu().numpy(), 3e-2, "decode logits")
+
+
+def test_code_layer_multi_token_step_not_causal_and_default_scale():
+    """A multi-token step with no mask attends causally only when the call is causal (is_causal, else the
+    module's is_causal), as HF's SDPA function decides; scaling=None is SDPA's 1/sqrt(head_dim)."""
+    log("SunShapeCodeLayer is_causal=False, scaling=None")
+    codec, sigma = _codec(D=64, bd=4, seed=13)
+    B, Hkv, Hq, D, S, L = 2, 2, 8, 64, 120, 3
+    layer = SunShapeCodeLayer(codec, block_tokens=256)
+    g = torch.Generator().manual_seed(14)
+    k = (torch.randn(B, Hkv, S, D, generator=g) * sigma).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    keys, values = layer.update(k.to(DEV), v.to(DEV))
+    kf = k.float().numpy()
+    codes_ref = np.stack([np.stack([_oracle_codes(codec, kf[b, h])[0] for h in range(Hkv)]) for b in range(B)])
+    q = torch.randn(B, Hq, L, D, generator=g).to(torch.bfloat16)
+    args = (q.float().numpy(), codes_ref, v.float().numpy(), codec.centroids.cpu().numpy(),
+            codec.permutation.cpu().numpy(), 1 / math.sqrt(D), "bf16", "bf16")
+    full = O.decode_attention(*args)
+    causal = np.where(np.arange(S)[None, :] > (S - L + np.arange(L))[:, None], -np.inf, 0.0).astype(np.float32)
+    ref_causal = O.decode_attention(*args, mask=np.broadcast_to(causal, (B, Hq, L, S)))
+    mod = torch.nn.Module()
+    mod.num_key_value_groups = Hq // Hkv
+    out, _ = sunshape_attention_forward(mod, q.to(DEV), keys, values, None, scaling=None, is_causal=False)
+    assert_rel(np_of(out.transpose(1, 2)), full, BF16_TOL, "is_causal=False")
+    mod.is_causal = False
+    out, _ = sunshape_attention_forward(mod, q.to(DEV), keys, values, None)
+    assert_rel(np_of(out.transpose(1, 2)), full, BF16_TOL, "module.is_causal=False")
+    mod.is_causal = True
+    out, _ = sunshape_attention_forward(mod, q.to(DEV), keys, values, None)
+    assert_rel(np_of(out.transpose(1, 2)), ref_causal, BF16_TOL, "module.is_causal=True")
+
+
+def test_tiny_sliding_window_code_cache_tracks_dequant_cache():
+    """Sliding-window layers (a tiny Mistral, window 16): both SunShape caches keep every token, as the
+    reference's layer does (sunshape/cache.py:86-104), and HF's sliding mask limits attention.  The code
+    cache's prefill equals the dequantising cache's bit for bit, and its decode steps (47 tokens, past the
+    window: the mask is what keeps them equal) track it within bf16 tolerance."""
+    from transformers import MistralConfig, MistralForCausalLM
+
+    from sunshape_amd.hf import SunShapeBundle
+
+    log("tiny mistral sliding-window code cache")
+    cfg = MistralConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                        num_attention_heads=8, num_key_value_heads=2, head_dim=32, max_position_embeddings=256,
+                        sliding_window=16)
+    torch.manual_seed(0)
+    model = MistralForCausalLM(cfg).to(DEV, torch.bfloat16).eval()
+    codecs = {0: _codec(D=32, bd=4, seed=18)[0], 1: _codec(D=32, bd=2, seed=19)[0]}
+    bundle = SunShapeBundle("tiny-mistral", [0, 1], 2.0, 4, "profileperm_baseline", 0, 0, 0, codecs)
+    ids = torch.randint(0, 512, (2, 40), generator=torch.Generator().manual_seed(6)).to(DEV)
+    steps = torch.randint(0, 512, (2, 5), generator=torch.Generator().manual_seed(7)).to(DEV)
+    with torch.no_grad():
+        model.set_attn_implementation("sdpa")
+        ref_cache = bundle.make_cache(config=cfg)
+        ref_logits = [model(ids, past_key_values=ref_cache).logits]
+        for i in range(steps.shape[1]):
+            ref_logits.append(model(steps[:, i:i + 1], past_key_values=ref_cache).logits)
+        model.set_attn_implementation(register_sunshape_attention())
+        cache = bundle.make_cache(config=cfg, store_codes=True)
+        logits = [model(ids, past_key_values=cache).logits]
+        for i in range(steps.shape[1]):
+            logits.append(model(steps[:, i:i + 1], past_key_values=cache).logits)
+    assert isinstance(cache.layers[0], SunShapeCodeLayer) and cache.layers[0].sliding_window == 16
+    assert cache.layers[0].get_seq_length() == 45 and cache.layers[1].get_seq_length() == 45
+    assert torch.equal(logits[0], ref_logits[0])
+    for a, r in zip(logits[1:], ref_logits[1:]):
+        assert_rel(a.float().cpu().numpy(), r.float().cpu().numpy(), 3e-2, "decode logits")

@@ -69,3 +69,32 @@ def test_sunshape_attention_delegates_dense_layers_exactly():
         out2 = model(nxt, past_key_values=cache).logits
     assert torch.equal(out, ref) and torch.equal(out2, ref2)
     assert cache.has_previous_state() and cache.get_seq_length() == 11
+
+
+def test_bundle_make_cache():
+    """SunShapeBundle.make_cache (sunshape/hf.py:267-268): the bundle's codecs on their layers, in the
+    reference's dequantising cache or, with store_codes, the code-storing one."""
+    from sunshape_amd.hf import SunShapeBundle
+
+    c = _codec()
+    bundle = SunShapeBundle("m", [1], 2.0, 4, "profileperm_baseline", 0, 0, 0, {1: c})
+    cache = bundle.make_cache(config=_cfg(3))
+    assert [type(l) for l in cache.layers] == [DynamicLayer, SunShapeLayer, DynamicLayer]
+    assert cache.layers[1].codec is c
+    coded = bundle.make_cache(num_layers=2, store_codes=True)
+    assert isinstance(coded.layers[1], SunShapeCodeLayer) and coded.layers[1].codec is c
+
+
+def test_sliding_window_layers_keep_their_window():
+    """Sliding-window layers become SunShape layers with the window copied (sunshape/cache.py:86-104),
+    for the code-storing cache too: every token is kept and HF's sliding mask limits attention."""
+    from transformers import MistralConfig
+
+    cfg = MistralConfig(vocab_size=256, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                        num_attention_heads=4, num_key_value_heads=2, head_dim=32, max_position_embeddings=128,
+                        sliding_window=16)
+    c = _codec()
+    for store in (False, True):
+        cache = SunShapeCache(config=cfg, layer_codecs={0: c}, store_codes=store)
+        assert isinstance(cache.layers[0], SunShapeCodeLayer if store else SunShapeLayer)
+        assert cache.layers[0].sliding_window == 16 and cache.layers[1].sliding_window == 16
