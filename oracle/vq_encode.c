@@ -122,9 +122,11 @@ void oracle_transform_rows(const float* x, int64_t n, int D, const float* M, int
     }
 }
 
-void oracle_encode_ex(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
-                      const float* metric, int direct, int nb, int nc, int bd, const uint8_t* heavy, uint8_t* codes,
-                      float* pt) {
+/* Indices go to codes (uint8) or, for codebooks of more than 256 codewords (the reference's int16 /
+ * int32 indices, sunshape/codec.py:78-83), to codes32 (one int32 per index). */
+static void encode_core(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
+                        const float* metric, int direct, int nb, int nc, int bd, const uint8_t* heavy, uint8_t* codes,
+                        int32_t* codes32, float* pt) {
     float* cn = (float*)malloc(sizeof(float) * (size_t)nb * (size_t)nc);
     float* xp = (float*)malloc(sizeof(float) * (size_t)D);
     float* cm = NULL; /* codebook in the metric space, C_b @ E_b^T */
@@ -146,7 +148,8 @@ void oracle_encode_ex(const float* keys, int64_t n, int D, const int64_t* perm, 
         for (int b = 0; b < nb; ++b) {
             const float* xb = xp + b * bd;
             if (heavy && heavy[b]) {
-                codes[i * nb + b] = 0;
+                if (codes32) codes32[i * nb + b] = 0;
+                else codes[i * nb + b] = 0;
                 if (pt)
                     for (int d = 0; d < bd; ++d) pt[(i * nb + b) * bd + d] = xb[d];
                 continue;
@@ -170,12 +173,26 @@ void oracle_encode_ex(const float* keys, int64_t n, int D, const int64_t* perm, 
                     best_j = j;
                 }
             }
-            codes[i * nb + b] = (uint8_t)best_j;
+            if (codes32) codes32[i * nb + b] = best_j;
+            else codes[i * nb + b] = (uint8_t)best_j;
         }
     }
     free(xp);
     free(cn);
     free(cm);
+}
+
+void oracle_encode_ex(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
+                      const float* metric, int direct, int nb, int nc, int bd, const uint8_t* heavy, uint8_t* codes,
+                      float* pt) {
+    encode_core(keys, n, D, perm, cent, metric, direct, nb, nc, bd, heavy, codes, NULL, pt);
+}
+
+/* The same with int32 indices (any codebook size). */
+void oracle_encode_wide(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,
+                        const float* metric, int direct, int nb, int nc, int bd, const uint8_t* heavy,
+                        int32_t* codes, float* pt) {
+    encode_core(keys, n, D, perm, cent, metric, direct, nb, nc, bd, heavy, NULL, codes, pt);
 }
 
 void oracle_encode_metric(const float* keys, int64_t n, int D, const int64_t* perm, const float* cent,

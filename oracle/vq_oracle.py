@@ -362,6 +362,9 @@ def _lib():
         lib.oracle_encode_ex.argtypes = [vp, ctypes.c_int64, ctypes.c_int, vp, vp, vp, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, vp]
         lib.oracle_encode_ex.restype = None
+        lib.oracle_encode_wide.argtypes = [vp, ctypes.c_int64, ctypes.c_int, vp, vp, vp, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, vp]
+        lib.oracle_encode_wide.restype = None
         lib.oracle_transform_rows.argtypes = [vp, ctypes.c_int64, ctypes.c_int, vp, ctypes.c_int, vp]
         lib.oracle_transform_rows.restype = None
         _LIB = lib
@@ -387,10 +390,16 @@ def transform_rows(x: np.ndarray, M: np.ndarray, transpose: bool = False) -> np.
     return out.reshape(shape)
 
 
+def index_dtype(n_centroids: int):
+    """Stored index dtype: sunshape/codec.py:78-83 (_compact_index_dtype), with the 16-bit case
+    unsigned so indices up to 65535 keep their value (the reference's int16 holds the same bits)."""
+    return np.uint8 if n_centroids <= 256 else np.uint16 if n_centroids <= 65535 else np.int32
+
+
 def encode(keys: np.ndarray, perm: np.ndarray, centroids: np.ndarray,
            heavy: Optional[np.ndarray] = None, metric: Optional[np.ndarray] = None,
-           direct: bool = False, rotation: Optional[np.ndarray] = None):
-    """``codec.quantize(keys)``: codes uint8 [N, nb], passthrough fp32 [N, nb, bd] or None.
+           direct: bool = False, rotation: Optional[np.ndarray] = None, threads: int = 1):
+    """``codec.quantize(keys)``: codes [N, nb] (index_dtype), passthrough fp32 [N, nb, bd] or None.
 
     sunshape/codec.py:362-385; exact arithmetic in oracle/vq_encode.c.
     keys: [N, D] values (bf16 keys pass as their exact fp32 upcast).
@@ -400,6 +409,8 @@ def encode(keys: np.ndarray, perm: np.ndarray, centroids: np.ndarray,
     mm formulation.
     rotation: the rotated mode's R [D, D]: keys go through x @ R^T (transform_rows) and
     ``perm`` is ignored (sunshape/codec.py:364, :250-251).
+    threads: row chunks encoded on that many host threads (the C code runs without the GIL);
+    the result does not depend on it.
     """
     keys = np.ascontiguousarray(keys, dtype=np.float32)
     if rotation is not None:
@@ -409,7 +420,8 @@ def encode(keys: np.ndarray, perm: np.ndarray, centroids: np.ndarray,
     cen = np.ascontiguousarray(centroids, dtype=np.float32)
     nb, nc, bd = cen.shape
     n, D = keys.shape
-    codes = np.empty((n, nb), dtype=np.uint8)
+    wide = nc > 256
+    codes = np.empty((n, nb), dtype=np.int32 if wide else np.uint8)
     hv = None
     pt = None
     if heavy is not None and np.any(heavy):
@@ -418,9 +430,22 @@ def encode(keys: np.ndarray, perm: np.ndarray, centroids: np.ndarray,
     met = None if metric is None else np.ascontiguousarray(metric, dtype=np.float32)
     if met is not None and met.shape != (D, D):
         raise ValueError(f"metric must be [{D}, {D}]")
-    _lib().oracle_encode_ex(_ptr(keys), n, D, _ptr(perm), _ptr(cen), _ptr(met), 1 if direct else 0, nb, nc, bd,
-                            _ptr(hv), _ptr(codes), _ptr(pt))
-    return codes, pt
+    fn = _lib().oracle_encode_wide if wide else _lib().oracle_encode_ex
+
+    def run(lo: int, hi: int) -> None:
+        if hi > lo:
+            fn(_ptr(keys[lo:hi]), hi - lo, D, _ptr(perm), _ptr(cen), _ptr(met), 1 if direct else 0, nb, nc, bd,
+               _ptr(hv), _ptr(codes[lo:hi]), None if pt is None else _ptr(pt[lo:hi]))
+
+    if threads > 1 and n > 1:
+        from concurrent.futures import ThreadPoolExecutor
+
+        step = (n + threads - 1) // threads
+        with ThreadPoolExecutor(threads) as ex:
+            list(ex.map(lambda lo: run(lo, min(lo + step, n)), range(0, n, step)))
+    else:
+        run(0, n)
+    return (codes.astype(index_dtype(nc)) if wide else codes), pt
 
 
 def block_distances(x: np.ndarray, c: np.ndarray, direct: bool = False):

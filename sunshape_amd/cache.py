@@ -6,8 +6,8 @@ Two layer kinds, selected per layer by ``SunShapeCache``:
   quantised and immediately dequantised through the codec (HIP encode + dequantize
   kernels, bit-exact with the reference's arithmetic) and stored dense, so the
   model's own attention runs unchanged.  A fidelity path: it saves no memory.
-* ``SunShapeCodeLayer`` -- stores the uint8 codes (plus compact passthrough values for
-  SunShape-Mixed heavy blocks) and dense values in preallocated, geometrically grown
+* ``SunShapeCodeLayer`` -- stores the codes (uint8, or int16 / int32 past 256 codewords; plus
+  compact passthrough values for SunShape-Mixed heavy blocks) and dense values in preallocated, geometrically grown
   buffers, and hands attention a ``SunShapeCodedKeys`` payload instead of a key
   tensor.  The ``"sunshape"`` attention implementation (``register_sunshape_attention``)
   runs single-token decode steps through the fused decode kernel on the codes (fp32
@@ -60,7 +60,7 @@ class IdentityLayer(DynamicLayer):
 
 @dataclass(frozen=True)
 class SunShapeCodedKeys:
-    """Keys of one SunShapeCodeLayer as attention sees them: codes [B, Hkv, T, nb] uint8 and
+    """Keys of one SunShapeCodeLayer as attention sees them: codes [B, Hkv, T, nb] (the codec's index dtype) and
     optional compact passthrough [B, Hkv, T, n_heavy, bd], views of the layer's buffers."""
 
     codes: torch.Tensor
@@ -133,7 +133,7 @@ class SunShapeCodeLayer(DynamicLayer):
         new_cap = max(need, 2 * cap)
         new_cap = (new_cap + step - 1) // step * step
         nb, bd = self.codec.n_blocks, self.codec.block_dim
-        codes = torch.empty((B, Hkv, new_cap, nb), device=self.device, dtype=torch.uint8)
+        codes = torch.empty((B, Hkv, new_cap, nb), device=self.device, dtype=hip_ops.index_dtype(self.codec.n_centroids))
         vals = torch.empty((B, Hkv, new_cap, Dv), device=self.device, dtype=vdtype)
         pt = None
         if self.heavy is not None:

@@ -240,8 +240,8 @@ class SunShapeBlockCodec(torch.nn.Module):
 
     def unsupported_reason(self) -> str | None:
         """Why the HIP kernels cannot serve this codec (None when they can)."""
-        if self.n_centroids > 256:
-            return f"n_centroids={self.n_centroids} > 256 needs wider than uint8 codes."
+        if self.n_centroids > 1 << 20:
+            return f"n_centroids={self.n_centroids} exceeds the kernels' 2^20 codewords per block."
         return None
 
     # --------------------------------------------------------------- transforms
@@ -274,9 +274,10 @@ class SunShapeBlockCodec(torch.nn.Module):
     def quantize(self, keys: torch.Tensor, kv_head: int | None = None) -> SunShapeQuantized:
         """Nearest-codeword encode on the GPU (sunshape/codec.py:362-385).
 
-        Returns uint8 indices [N, nb]; in SunShape-Mixed mode the heavy blocks'
-        indices are 0 and passthrough_values is the reference's dense fp32
-        [N, nb, bd] (zeros on light blocks).
+        Returns indices [N, nb] in the reference's compact dtype (uint8 up to 256
+        codewords, int16 up to 65535, int32 beyond; sunshape/codec.py:78-83); in
+        SunShape-Mixed mode the heavy blocks' indices are 0 and passthrough_values is
+        the reference's dense fp32 [N, nb, bd] (zeros on light blocks).
         """
         reason = self.unsupported_reason()
         if reason is not None:
@@ -319,10 +320,9 @@ class SunShapeBlockCodec(torch.nn.Module):
         if heavy is not None and pt is None:
             raise ValueError("Mixed-precision quantized keys are missing passthrough values.")
         idx = quantized.indices
-        if idx.dtype != torch.uint8:
-            if self.n_centroids > 256:
-                raise RuntimeError("indices wider than uint8 are not supported")
-            idx = idx.to(torch.uint8)
+        want = _compact_index_dtype(self.n_centroids)
+        if idx.dtype != want:  # e.g. int64 indices: the stored dtype's bits (16-bit codes read unsigned)
+            idx = idx.to(want)
         return hip_ops.dequantize(idx, perm, cent, heavy=heavy, pt=pt,
                                   pt_dense=pt is not None and pt.shape[-2] == self.n_blocks,
                                   rotation=self.rotation_matrix())

@@ -121,6 +121,21 @@ inline bool ssq_encode_fold(const ssq_encode_args* a, int keys_per_wg) {
     return a->seq_len < keys_per_wg && (int64_t)a->batch * a->seq_len <= 0x7fffffff;
 }
 
+// Stored code width in bytes, as the reference's _compact_index_dtype (sunshape/codec.py:78-83):
+// one byte up to 256 codewords, 16 bits up to 65535, 32 bits beyond.  16-bit codes are read as
+// unsigned, so every index below 65536 round-trips (the reference's int16 storage holds indices up
+// to 32767 as the same bits).
+constexpr int kMaxCentroids = 1 << 20;
+__host__ __device__ inline int ssq_code_width(int n_centroids) {
+    return n_centroids <= 256 ? 1 : n_centroids <= 65535 ? 2 : 4;
+}
+// code element i (in units of the code width) of a row buffer
+__device__ __forceinline__ uint32_t ssq_load_code(const uint8_t* codes, int width, int64_t i) {
+    return width == 1 ? (uint32_t)codes[i]
+                      : width == 2 ? (uint32_t)reinterpret_cast<const uint16_t*>(codes)[i]
+                                   : reinterpret_cast<const uint32_t*>(codes)[i];
+}
+
 __device__ __forceinline__ bool ssq_is_heavy(const uint64_t hm0, const uint64_t hm1, int blk) {
     return blk < 64 ? ((hm0 >> blk) & 1ull) : ((hm1 >> (blk - 64)) & 1ull);
 }
@@ -150,6 +165,8 @@ int ssq_device_cus();
 // grid-search encode (ssq_encode_grid.hip)
 bool ssq_encode_grid_supported(const ssq_encode_args* a);
 int ssq_encode_grid_run(const ssq_encode_args* a, hipStream_t st);
+// exact encode for codebooks of more than 256 codewords (ssq_encode_wide.hip)
+int ssq_encode_wide_run(const ssq_encode_args* a, hipStream_t st);
 
 #define SSQ_REQUIRE(cond, ...)                                  \
     do {                                                        \

@@ -9,6 +9,12 @@
 //      in block order (triton_kernels.py:174-196), + passthrough blocks, + mask;
 //      optional raw-score store; online softmax; P.V accumulated in fp32.
 //   4. Per split: normalised output + lse, or (m, l, o) partials merged by k_merge.
+// Codebooks of more than 256 codewords (16- or 32-bit codes, ssq_code_width) have no LUT: a
+// nb x nc x RP table would not fit the LDS (4,096 codewords at 32 blocks: 512 KiB per query row).
+// Each token's codewords are gathered from the codebook in global memory instead (L2 / Infinity
+// Cache resident: 2 MiB per head at 4,096 codewords of dim 4 and 32 blocks) and dotted with the
+// query rows block by block: the LUT entry's FMA chain from the first product, summed in block
+// order, so the scores are the LUT path's arithmetic.
 #include "ssq_common.h"
 
 #include <math.h>
@@ -28,6 +34,7 @@ struct DecodeParams {
     int n_splits;
     int word_codes; // 1: code rows are 4-byte aligned with nb % 4 == 0
     int vec_cent;   // 1: codebook 16-byte aligned (per head too), head_dim % 4 == 0, nb*nc % 4 == 0
+    int cw;         // code width in bytes (ssq_code_width): > 1 gathers codewords instead of a LUT
     float* ws_o;    // [n_splits, B*Hq*Lq, Dv]
     float* ws_m;    // [n_splits, B*Hq*Lq]
     float* ws_l;
@@ -132,9 +139,14 @@ __device__ __forceinline__ void build_lut_vec(const ssq_decode_args& a, const fl
     }
 }
 
+// LUT floats in LDS: none for codebooks past 256 codewords (gathered from global memory)
+__host__ __device__ inline size_t lut_floats(const ssq_decode_args& a, int RP) {
+    return a.n_centroids > 256 ? 0 : (size_t)a.n_blocks * a.n_centroids * RP;
+}
+
 // float offset of the reduction scratch; identical on host and device
 __host__ __device__ inline size_t red_offset(const ssq_decode_args& a, int RP, bool has_v) {
-    size_t main = (size_t)a.n_blocks * a.n_centroids * RP + (size_t)RP * a.head_dim + (has_v ? (size_t)RP * kTile : 0);
+    size_t main = lut_floats(a, RP) + (size_t)RP * a.head_dim + (has_v ? (size_t)RP * kTile : 0);
     if (has_v) {
         const int dchunks = a.layout == SSQ_PAGED ? a.value_dim : a.value_dim / 8;
         const size_t epi = (size_t)(kThreads / dchunks) * RP * a.value_dim;
@@ -166,7 +178,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
     // LDS: lut [nb*nc][RP] | qp [RP][D] | ptile [RP][kTile] ... red [2][4][RP] after the
     // larger of that carve-out and the epilogue's [tpar][RP][Dv] output buffer.
     float* lut = smem;
-    float* qp = lut + (size_t)nb * nc * RP;
+    float* qp = lut + lut_floats(a, RP);
     float* ptile = qp + RP * D;
     float* red = smem + red_offset(a, RP, HAS_V);
 
@@ -208,7 +220,9 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
     // vector codeword / query loads need a 16-byte aligned codebook (host-checked: vec_cent)
     // and a 4-aligned head_dim
     const int vb = p.vec_cent ? bd : 0;
-    if (vb == 1) build_lut_vec<RP, 1>(a, cent, qp, lut, tid);
+    if (p.cw > 1) {
+        // no LUT: codewords are gathered per token
+    } else if (vb == 1) build_lut_vec<RP, 1>(a, cent, qp, lut, tid);
     else if (vb == 2) build_lut_vec<RP, 2>(a, cent, qp, lut, tid);
     else if (vb == 4) build_lut_vec<RP, 4>(a, cent, qp, lut, tid);
     else if (vb == 8) build_lut_vec<RP, 8>(a, cent, qp, lut, tid);
@@ -325,6 +339,22 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
                     }
 #pragma unroll
                     for (int r = 0; r < RP; ++r) s[r] += d_acc[r];
+                } else if (p.cw > 1) {
+                    // the LUT entry's arithmetic on a gathered codeword: FMA chain over the block's
+                    // dims from the first product, then added in block order
+                    const uint32_t cc = code < (uint32_t)nc ? code : (uint32_t)(nc - 1);
+                    const float* c = cent + ((int64_t)blk * nc + cc) * bd;
+                    float e_acc[RP];
+                    const float c0 = c[0];
+#pragma unroll
+                    for (int r = 0; r < RP; ++r) e_acc[r] = qp[r * D + blk * bd] * c0;
+                    for (int d = 1; d < bd; ++d) {
+                        const float cd = c[d];
+#pragma unroll
+                        for (int r = 0; r < RP; ++r) e_acc[r] = fmaf(qp[r * D + blk * bd + d], cd, e_acc[r]);
+                    }
+#pragma unroll
+                    for (int r = 0; r < RP; ++r) s[r] += e_acc[r];
                 } else {
                     const int cc = (int)code < nc ? (int)code : nc - 1;
                     const float* e = lut + ((size_t)blk * nc + cc) * RP;
@@ -340,7 +370,9 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
                     }
                 }
             };
-            if (a.code_bits) {  // sub-byte codes packed into uint32 words
+            if (p.cw > 1) {  // 16- / 32-bit codes (code strides count elements of that width)
+                for (int blk = 0; blk < nb; ++blk) add_block(blk, ssq_load_code(a.codes, p.cw, cofs + blk));
+            } else if (a.code_bits) {  // sub-byte codes packed into uint32 words
                 const uint32_t* w = reinterpret_cast<const uint32_t*>(a.codes) + cofs;
                 const int bits = a.code_bits, vpe = 32 / bits;
                 const uint32_t msk = (1u << bits) - 1u;
@@ -707,9 +739,15 @@ int validate(const ssq_decode_args* a, bool need_v) {
     SSQ_REQUIRE(a->block_dim >= 1 && a->head_dim % a->block_dim == 0, "head_dim must be divisible by block_dim");
     SSQ_REQUIRE(a->n_blocks == a->head_dim / a->block_dim, "n_blocks != head_dim / block_dim");
     SSQ_REQUIRE(a->head_dim <= 1024, "head_dim > 1024");
-    SSQ_REQUIRE(a->n_centroids >= 1 && a->n_centroids <= 256, "n_centroids must be in [1, 256] for uint8 codes");
+    SSQ_REQUIRE(a->n_centroids >= 1 && a->n_centroids <= kMaxCentroids, "n_centroids must be in [1, %d]", kMaxCentroids);
     SSQ_REQUIRE(a->n_blocks <= 128, "n_blocks > 128");
     SSQ_REQUIRE(a->code_bits >= 0 && a->code_bits <= 8, "code_bits must be 0 (uint8) or 1..8 (packed)");
+    SSQ_REQUIRE(a->n_centroids <= 256 || a->code_bits == 0,
+                "n_centroids=%d takes 16- or 32-bit codes (code_bits 0)", a->n_centroids);
+    if (a->n_centroids > 256) {
+        const int cw = ssq_code_width(a->n_centroids);
+        SSQ_REQUIRE((uintptr_t)a->codes % cw == 0, "%d-bit codes must be %d-byte aligned", 8 * cw, cw);
+    }
     if (a->code_bits) {
         SSQ_REQUIRE(a->n_centroids <= (1 << a->code_bits), "n_centroids=%d needs more than %d-bit codes",
                     a->n_centroids, a->code_bits);
@@ -778,7 +816,8 @@ int run_generic(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipS
     dp.R = pl.R;
     dp.split_len = pl.split_len;
     dp.n_splits = pl.n_splits;
-    const bool aligned = a->code_bits == 0 && ((uintptr_t)a->codes % 4 == 0) && a->n_blocks % 4 == 0 &&
+    dp.cw = ssq_code_width(a->n_centroids);
+    const bool aligned = dp.cw == 1 && a->code_bits == 0 && ((uintptr_t)a->codes % 4 == 0) && a->n_blocks % 4 == 0 &&
                          a->c_st % 4 == 0 && a->c_sh % 4 == 0 && a->c_sb % 4 == 0;
     dp.word_codes = aligned ? 1 : 0;
     dp.vec_cent = ((uintptr_t)a->cent % 16 == 0 && (a->cent_sh * 4) % 16 == 0 && a->head_dim % 4 == 0 &&

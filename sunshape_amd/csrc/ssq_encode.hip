@@ -18,7 +18,7 @@
 //    bound of the row minimum is re-evaluated with the exact formula on the VALU and the
 //    winner is chosen among those (lexicographic (d, index)).  The index is therefore
 //    exact whatever the MFMA's internal rounding order.
-#include "ssq_common.h"
+#include "ssq_encode_math.h"
 
 #include <math.h>
 #include <string.h>
@@ -27,35 +27,8 @@ namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-// |v|^2 as x.pow(2).sum(-1): squares rounded, summed left to right (no contraction:
-// this file is compiled with -ffp-contract=off)
-__device__ __forceinline__ float sq_norm(const float* v, int bd) {
-    float s = v[0] * v[0];
-    for (int d = 1; d < bd; ++d) {
-        const float t = v[d] * v[d];
-        s = s + t;
-    }
-    return s;
-}
-
-// pre-sqrt distance: k ascending FMA chain over [-2x, xn, 1] . [c, 1, cn]
-__device__ __forceinline__ float mm_dist2(const float* x, float xn, const float* c, float cn, int bd) {
-    float acc = (-2.0f * x[0]) * c[0];
-    for (int d = 1; d < bd; ++d) acc = __builtin_fmaf(-2.0f * x[d], c[d], acc);
-    acc = __builtin_fmaf(xn, 1.0f, acc);
-    acc = __builtin_fmaf(1.0f, cn, acc);
-    return acc;
-}
-
-// y_k = sum_j e[k*ld + j] * x[j] for one row k of a SunShape-Pro block metric E_b:
-// j ascending, first product rounded, then fused multiply-adds
-__device__ __forceinline__ float metric_row(const float* e, const float* x, int bd) {
-    float acc = e[0] * x[0];
-    for (int j = 1; j < bd; ++j) acc = __builtin_fmaf(e[j], x[j], acc);
-    return acc;
-}
-
-// the same two, for register arrays of N >= bd entries (unrolled, static indexes)
+// sq_norm and metric_row (ssq_encode_math.h) for register arrays of N >= bd entries (unrolled,
+// static indexes)
 template <int N>
 __device__ __forceinline__ float sq_norm_n(const float (&v)[N], int bd) {
     float s = v[0] * v[0];
@@ -75,47 +48,12 @@ __device__ __forceinline__ float metric_row_n(const float* e, const float (&x)[N
     return acc;
 }
 
-// pre-sqrt distance of torch.cdist's direct evaluation (the one it takes when both inputs have at
-// most 25 rows): sum over k ascending of the rounded squares (x_k - c_k)^2, summed left to right
-__device__ __forceinline__ float direct_dist2(const float* x, const float* c, int bd) {
-    float d = x[0] - c[0];
-    float s = d * d;
-    for (int k = 1; k < bd; ++k) {
-        d = x[k] - c[k];
-        const float t = d * d;
-        s = s + t;
-    }
-    return s;
-}
-
-// correctly rounded sqrt of max(v, 0)
-__device__ __forceinline__ float dist_of(float v) { return __builtin_sqrtf(v > 0.f ? v : 0.f); }
-
 struct EncodeParams {
     ssq_encode_args a;
     int nbc;           // blocks per workgroup chunk
     int fold;          // short sequences: all sequences of a KV head share one key range (SsqKeyMap)
     int passes;        // key passes per workgroup (scan)
 };
-
-__device__ __forceinline__ int heavy_ordinal(uint64_t hm0, uint64_t hm1, int blk) {
-    if (blk < 64) return __popcll(hm0 & ((1ull << blk) - 1ull));
-    return __popcll(hm0) + __popcll(hm1 & ((1ull << (blk - 64)) - 1ull));
-}
-
-// output row bases for key (b, kv, s): codes and passthrough
-__device__ __forceinline__ void out_rows(const ssq_encode_args& a, int b, int kv, int s, int64_t& crow,
-                                         int64_t& prow) {
-    if (a.slot_mapping) {
-        const int64_t slot = a.slot_mapping[(int64_t)b * a.sm_sb + s];
-        const int64_t page = slot / a.page_size, off = slot - page * a.page_size;
-        crow = page * a.c_sb + (int64_t)kv * a.c_sh + off * a.c_st;
-        prow = page * a.pt_sb + (int64_t)kv * a.pt_sh + off * a.pt_st;
-    } else {
-        crow = (int64_t)b * a.c_sb + (int64_t)kv * a.c_sh + (int64_t)s * a.c_st;
-        prow = (int64_t)b * a.pt_sb + (int64_t)kv * a.pt_sh + (int64_t)s * a.pt_st;
-    }
-}
 
 // ---------------------------------------------------------------------------
 // exact scan: thread per (key, block); codebook chunk + norms in LDS
@@ -741,7 +679,7 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
     SSQ_REQUIRE(a->block_dim >= 1 && a->block_dim <= 16 && a->head_dim % a->block_dim == 0,
                 "head_dim must be divisible by block_dim (block_dim <= 16)");
     SSQ_REQUIRE(a->n_blocks == a->head_dim / a->block_dim && a->n_blocks <= 128, "bad n_blocks");
-    SSQ_REQUIRE(a->n_centroids >= 1 && a->n_centroids <= 256, "n_centroids must be in [1, 256] for uint8 codes");
+    SSQ_REQUIRE(a->n_centroids >= 1 && a->n_centroids <= kMaxCentroids, "n_centroids must be in [1, %d]", kMaxCentroids);
     const bool any_heavy = a->heavy_mask[0] || a->heavy_mask[1];
     SSQ_REQUIRE(!any_heavy || a->pt, "heavy blocks need a passthrough output");
     if (any_heavy) SSQ_REQUIRE(a->pt_dtype >= SSQ_F32 && a->pt_dtype <= SSQ_F16, "bad pt_dtype");
@@ -753,6 +691,14 @@ extern "C" int ssq_encode(const ssq_encode_args* a, void* stream) {
     // screen and the grid search certify candidates against the mm formulation's rounding
     SSQ_UNSUPPORTED(!a->direct_dist || a->kernel == 0 || a->kernel == 1,
                     "direct_dist runs on the exact scan (kernel 0 or 1), not kernel %d", a->kernel);
+    if (a->n_centroids > 256) {  // 16- / 32-bit codes: the chunked exact scan
+        SSQ_UNSUPPORTED(a->kernel == 0 || a->kernel == 1,
+                        "n_centroids=%d encodes on the exact scan (kernel 0 or 1), not kernel %d", a->n_centroids,
+                        a->kernel);
+        const int cw = ssq_code_width(a->n_centroids);
+        SSQ_REQUIRE((uintptr_t)a->codes % cw == 0, "%d-bit codes must be %d-byte aligned", 8 * cw, cw);
+        return ssq_encode_wide_run(a, st);
+    }
     if (!a->direct_dist && (a->kernel == 3 || (a->kernel == 0 && a->grid && ssq_encode_grid_supported(a))))
         return ssq_encode_grid_run(a, st);
     EncodeParams p;

@@ -102,8 +102,8 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* codes, int64_t c
                             : __popcll(hm0) + __popcll(hm1 & ((1ull << (blk - 64)) - 1ull));
         v = ssq_load_elem(pt, pt_dtype, (int64_t)t * pt_st + slot * bd + d);
     } else {
-        int c = codes[(int64_t)t * c_st + blk];
-        if (c >= nc) c = nc - 1;
+        uint32_t c = ssq_load_code(codes, ssq_code_width(nc), (int64_t)t * c_st + blk);
+        if (c >= (uint32_t)nc) c = nc - 1;
         v = cent[((int64_t)blk * nc + c) * bd + d];
     }
     out[(int64_t)t * o_st + perm[i]] = v;
@@ -221,7 +221,7 @@ extern "C" int ssq_dequantize(const uint8_t* codes, int64_t c_st, int32_t tokens
                               int64_t pt_st, float* out, int64_t o_st, void* stream) {
     SSQ_REQUIRE(codes && perm && cent && out, "NULL pointer argument");
     SSQ_REQUIRE(block_dim >= 1 && head_dim % block_dim == 0, "head_dim must be divisible by block_dim");
-    SSQ_REQUIRE(n_centroids >= 1 && n_centroids <= 256, "n_centroids must be in [1, 256]");
+    SSQ_REQUIRE(n_centroids >= 1 && n_centroids <= kMaxCentroids, "n_centroids must be in [1, %d]", kMaxCentroids);
     SSQ_REQUIRE(head_dim / block_dim <= 128, "n_blocks > 128");
     SSQ_REQUIRE(tokens >= 0, "negative token count");
     const uint64_t hm0 = heavy_mask ? heavy_mask[0] : 0, hm1 = heavy_mask ? heavy_mask[1] : 0;

@@ -94,12 +94,17 @@ int64_t words_per_row(int64_t nb, int64_t bits) {
     return (nb + vpe - 1) / vpe;
 }
 
-void check_codes(const Tensor& codes, int64_t nb, int64_t code_bits) {
+// the stored index dtype, as the reference's _compact_index_dtype (sunshape/codec.py:78-83)
+at::ScalarType index_dtype(int64_t nc) { return nc <= 256 ? at::kByte : nc <= 65535 ? at::kShort : at::kInt; }
+
+void check_codes(const Tensor& codes, int64_t nb, int64_t nc, int64_t code_bits) {
     if (code_bits == 0) {
-        TORCH_CHECK(codes.scalar_type() == at::kByte, "codes must be uint8 (n_centroids <= 256), got ",
+        const at::ScalarType want = index_dtype(nc);
+        TORCH_CHECK(codes.scalar_type() == want, "codes must be ", want, " for n_centroids=", nc, ", got ",
                     codes.scalar_type());
-        TORCH_CHECK(codes.size(-1) == nb, "codes must be [.., ", nb, "] uint8");
+        TORCH_CHECK(codes.size(-1) == nb, "codes must be [.., ", nb, "] ", want);
     } else {
+        TORCH_CHECK(nc <= 256, "n_centroids=", nc, " takes 16- or 32-bit codes, not packed words");
         TORCH_CHECK(code_bits >= 1 && code_bits <= 8, "code_bits must be 0 (uint8) or 1..8 (packed words)");
         const int64_t nw = words_per_row(nb, code_bits);
         TORCH_CHECK(codes.scalar_type() == at::kInt, "packed codes must be int32 words, got ", codes.scalar_type());
@@ -138,7 +143,7 @@ std::tuple<Tensor, Tensor, Tensor> decode(const Tensor& q_in, const Tensor& code
     TORCH_CHECK(Hq % Hkv == 0, "Query head count must be divisible by kv-head count.");
     const Codec c = codec_arrays(perm_in, cent_in, D, Hkv);
     TORCH_CHECK(codes.dim() == 4, "codes must be 4-D [.., ", c.nb, "]");
-    check_codes(codes, c.nb, code_bits);
+    check_codes(codes, c.nb, c.nc, code_bits);
     int64_t T, Dv, page, layout;
     if (paged) {
         const Tensor& bt = *block_table;
@@ -255,7 +260,7 @@ Tensor scores(const Tensor& q_in, const Tensor& codes, const Tensor& perm_in, co
     TORCH_CHECK(codes.size(0) == B, "Quantized key batch size does not match query batch size.");
     TORCH_CHECK(Hq % Hkv == 0, "Query head count must be divisible by kv-head count.");
     const Codec c = codec_arrays(perm_in, cent_in, D, Hkv);
-    check_codes(codes, c.nb, code_bits);
+    check_codes(codes, c.nb, c.nc, code_bits);
     const bool any_heavy = hm0 != 0 || hm1 != 0;
     check_pt(pt, any_heavy);
     c10::hip::HIPGuard guard(q.device().index());
@@ -307,9 +312,9 @@ void encode_into(const Tensor& keys_in, const Tensor& perm_in, const Tensor& cen
     const int64_t B = keys.size(0), Hkv = keys.size(1), S = keys.size(2), D = keys.size(3);
     const Codec c = codec_arrays(perm_in, cent_in, D, Hkv);
     on_gpu("codes", codes);
-    TORCH_CHECK(codes.scalar_type() == at::kByte && codes.dim() == 4 && codes.size(1) == Hkv &&
+    TORCH_CHECK(codes.scalar_type() == index_dtype(c.nc) && codes.dim() == 4 && codes.size(1) == Hkv &&
                     codes.size(3) == c.nb && codes.stride(3) == 1,
-                "codes must be uint8 [.., ", Hkv, ", .., ", c.nb, "] with unit last stride");
+                "codes must be ", index_dtype(c.nc), " [.., ", Hkv, ", .., ", c.nb, "] with unit last stride");
     const bool any_heavy = hm0 != 0 || hm1 != 0;
     const bool paged = slot_mapping.has_value() && slot_mapping->defined();
     if (paged) {

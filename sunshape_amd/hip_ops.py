@@ -110,17 +110,29 @@ def lut_build(q: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, scale: Op
     return out
 
 
+def index_dtype(n_centroids: int) -> torch.dtype:
+    """The stored index dtype: uint8 up to 256 codewords, int16 up to 65535, int32 beyond
+    (sunshape/codec.py:78-83, _compact_index_dtype).  The kernels read int16 codes as unsigned."""
+    if n_centroids <= 256:
+        return torch.uint8
+    if n_centroids <= 65535:
+        return torch.int16
+    return torch.int32
+
+
 def words_per_row(n_blocks: int, bits: int) -> int:
     """uint32 words of one packed code row: ceil(nb / (32 // bits))."""
     vpe = 32 // bits
     return (n_blocks + vpe - 1) // vpe
 
 
-def _check_codes(codes: torch.Tensor, nb: int, code_bits: int) -> None:
+def _check_codes(codes: torch.Tensor, nb: int, code_bits: int, nc: int = 256) -> None:
     if code_bits == 0:
-        _require(codes.dtype == torch.uint8, f"codes must be uint8 (n_centroids <= 256), got {codes.dtype}")
-        _require(codes.shape[-1] == nb, f"codes must be [.., {nb}] uint8")
+        want = index_dtype(nc)
+        _require(codes.dtype == want, f"codes must be {want} for n_centroids={nc}, got {codes.dtype}")
+        _require(codes.shape[-1] == nb, f"codes must be [.., {nb}] {want}")
     else:
+        _require(nc <= 256, f"n_centroids={nc} takes 16- or 32-bit codes, not packed words")
         _require(1 <= code_bits <= 8, "code_bits must be 0 (uint8) or 1..8 (packed words)")
         nw = words_per_row(nb, code_bits)
         _require(codes.dtype == torch.int32, f"packed codes must be int32 words, got {codes.dtype}")
@@ -196,10 +208,11 @@ def attention_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, c
     perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, None)
     _require(perm.ndim == 1 and cent.ndim == 3, "attention_scores takes one codec (perm [D], centroids [nb, nc, bd])")
     if code_bits == 0:
-        _require(codes.dtype == torch.uint8, f"indices must be uint8 codes (n_centroids <= 256), got {codes.dtype}")
+        want = index_dtype(nc)
+        _require(codes.dtype == want, f"indices must be {want} codes (n_centroids={nc}), got {codes.dtype}")
         _require(codes.shape[1] == nb, "Quantized key block count does not match codec: "
                  f"indices.shape[1]={codes.shape[1]}, codec.n_blocks={nb}.")
-    _check_codes(codes, nb, code_bits)
+    _check_codes(codes, nb, code_bits, nc)
     if R == 0 or T == 0:
         return torch.empty((R, T), device=q.device, dtype=torch.float32)
     hm, pt, ptd, _ = _pt_args(heavy, pt, pt_dense)
@@ -238,7 +251,7 @@ def gqa_scores(q: torch.Tensor, codes: torch.Tensor, perm: torch.Tensor, cent: t
     _require(codes.shape[0] == B, "Quantized key batch size does not match query batch size.")
     _require(Hq % Hkv == 0, "Query head count must be divisible by kv-head count.")
     perm, cent, perm_sh, cent_sh, bd, nb, nc = _codec_arrays(perm, cent, D, Hkv)
-    _check_codes(codes, nb, code_bits)
+    _check_codes(codes, nb, code_bits, nc)
     if T == 0:
         return torch.empty((B, Hq, Lq, T), device=q.device, dtype=torch.float32)
     hm, pt, ptd, _ = _pt_args(heavy, pt, pt_dense)
@@ -324,14 +337,15 @@ def _encode_prepare(keys, perm, cent, heavy, pt_dtype, pt_dense, codes_out, pt_o
         if metric.ndim == 3:
             _require(metric.shape[0] == Hkv, f"per-head metric holds {metric.shape[0]} heads, keys have {Hkv}")
             metric_sh = D * D
+    idt = index_dtype(nc)
     if slot_mapping is None:
         if codes_out is not None:  # caller's buffer (e.g. a slice of a preallocated cache)
             _on_gpu("codes_out", codes_out)
-            _require(codes_out.dtype == torch.uint8 and tuple(codes_out.shape) == (B, Hkv, S, nb)
-                     and codes_out.stride(3) == 1, f"codes_out must be uint8 [{B}, {Hkv}, {S}, {nb}] with unit last stride")
+            _require(codes_out.dtype == idt and tuple(codes_out.shape) == (B, Hkv, S, nb)
+                     and codes_out.stride(3) == 1, f"codes_out must be {idt} [{B}, {Hkv}, {S}, {nb}] with unit last stride")
             codes = codes_out
         else:
-            codes = torch.empty((B, Hkv, S, nb), device=keys.device, dtype=torch.uint8)
+            codes = torch.empty((B, Hkv, S, nb), device=keys.device, dtype=idt)
         pt = None
         if n_heavy:
             if pt_out is not None:
@@ -353,9 +367,9 @@ def _encode_prepare(keys, perm, cent, heavy, pt_dtype, pt_dense, codes_out, pt_o
         _on_gpu("slot_mapping", slot_mapping)
         _require(slot_mapping.dtype == torch.int64 and slot_mapping.shape == (B, S) and slot_mapping.stride(1) == 1,
                  "slot_mapping must be int64 [B, S]")
-        _require(codes_out is not None and codes_out.dtype == torch.uint8 and codes_out.ndim == 4
+        _require(codes_out is not None and codes_out.dtype == idt and codes_out.ndim == 4
                  and codes_out.shape[1] == Hkv and codes_out.shape[3] == nb and codes_out.stride(3) == 1,
-                 "paged encode needs codes_out [P, Hkv, page, nb] uint8")
+                 f"paged encode needs codes_out [P, Hkv, page, nb] {idt}")
         codes = codes_out
         page = codes_out.shape[2]
         pt = pt_out
@@ -432,7 +446,8 @@ def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
            codes_out: Optional[torch.Tensor] = None, pt_out: Optional[torch.Tensor] = None,
            slot_mapping: Optional[torch.Tensor] = None, metric: Optional[torch.Tensor] = None, kernel: int = 0,
            grid: Optional[torch.Tensor] = None, direct: bool = False, rotation: Optional[torch.Tensor] = None):
-    """Nearest-codeword encode of keys [B, Hkv, S, D] -> (codes uint8 [B, Hkv, S, nb], pt or None).
+    """Nearest-codeword encode of keys [B, Hkv, S, D] -> (codes [B, Hkv, S, nb], pt or None); codes are
+    uint8, or int16 / int32 past 256 codewords (index_dtype).
 
     Passthrough values (heavy blocks) are [B, Hkv, S, n_heavy, bd] (compact) or
     [B, Hkv, S, nb, bd] zero-filled (pt_dense, the reference's layout).  With
@@ -490,7 +505,8 @@ def encode_grid(cent: torch.Tensor, num_kv_heads: int = 1) -> torch.Tensor:
 def dequantize(codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
                heavy: Optional[Sequence[bool]] = None, pt: Optional[torch.Tensor] = None,
                pt_dense: bool = True, rotation: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """k_hat fp32 [T, D] in the original basis from codes uint8 [T, nb].
+    """k_hat fp32 [T, D] in the original basis from codes [T, nb] (uint8, or int16 / int32 past 256
+    codewords: index_dtype).
 
     rotation: the rotated mode's R [D, D]: the codewords are taken back by k_hat @ R
     (sunshape/codec.py:257-258) and perm is not used.
@@ -500,10 +516,10 @@ def dequantize(codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
         k_rot = dequantize(codes, _identity_like(perm), cent, heavy=heavy, pt=pt, pt_dense=pt_dense)
         return transform_rows(k_rot, rotation, transpose=True)
     _on_gpu("indices", codes)
-    _require(codes.ndim == 2 and codes.dtype == torch.uint8, "indices must be uint8 [T, nb]")
-    codes = codes if codes.stride(-1) == 1 else codes.contiguous()
     _require(cent.ndim == 3 and perm.ndim == 1, "dequantize takes one codec (perm [D], centroids [nb, nc, bd])")
     nb, nc, bd = cent.shape
+    _require(codes.ndim == 2 and codes.dtype == index_dtype(nc), f"indices must be {index_dtype(nc)} [T, nb]")
+    codes = codes if codes.stride(-1) == 1 else codes.contiguous()
     D = nb * bd
     perm, cent, _, _, bd, nb, nc = _codec_arrays(perm, cent, D, None)
     _require(codes.shape[1] == nb, f"indices.shape[1]={codes.shape[1]} != n_blocks={nb}")

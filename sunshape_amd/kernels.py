@@ -80,8 +80,9 @@ def sunshape_attention_scores_strict(codec, query: torch.Tensor, quantized_key, 
     require_triton_fast_path(codec, query, quantized_key, kv_head)
     perm, cent = _codec_arrays(codec, kv_head)
     idx = quantized_key.indices
-    if idx.dtype != torch.uint8:
-        idx = idx.to(torch.uint8)
+    want = hip_ops.index_dtype(int(cent.shape[-2]))
+    if idx.dtype != want:  # e.g. int64 indices: the stored dtype's bits (16-bit codes read unsigned)
+        idx = idx.to(want)
     heavy = None
     pb = getattr(quantized_key, "passthrough_blocks", None)
     if pb is not None:

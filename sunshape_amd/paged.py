@@ -4,7 +4,7 @@ No counterpart in the reference: its quantized keys are one contiguous [T, nb] c
 tensor per (batch, KV head) (sunshape/vllm_attn_backend.py:99-123), and it has no paged
 layout.  This is the caller on the write side of the decode kernel:
 
-* key pages   [P, Hkv, page, nb] uint8 codes, filled by the encode kernel through
+* key pages   [P, Hkv, page, nb] codes (uint8, or int16 / int32 past 256 codewords), filled by the encode kernel through
   a slot mapping (token slot = page * page_size + offset), no dense key tensor;
 * passthrough [P, Hkv, page, n_heavy, bd] for SunShape-Mixed heavy blocks;
 * value pages [P, Hkv, Dv, page] -- vLLM's dim-major value layout, which the
@@ -35,7 +35,8 @@ class PagedSunShapeCache:
         self.num_kv_heads = int(num_kv_heads)
         self.value_dim = int(value_dim)
         nb, bd = codec.n_blocks, codec.block_dim
-        self.code_pages = torch.zeros(num_pages, num_kv_heads, page_size, nb, dtype=torch.uint8, device=self.device)
+        self.code_pages = torch.zeros(num_pages, num_kv_heads, page_size, nb, device=self.device,
+                                      dtype=hip_ops.index_dtype(self.codec.n_centroids))
         self.v_pages = torch.zeros(num_pages, num_kv_heads, value_dim, page_size, dtype=value_dtype, device=self.device)
         heavy = codec.heavy_blocks()
         self.heavy = heavy

@@ -90,7 +90,7 @@ class SunShapeQuantizedKeys:
     batch_size: int
     num_kv_heads: int
     seq_len: int
-    codes: torch.Tensor | None = None          # [B, Hkv, S, nb] uint8 backing store
+    codes: torch.Tensor | None = None          # [B, Hkv, S, nb] backing store (the codec's index dtype)
     passthrough: torch.Tensor | None = None    # [B, Hkv, S, slots, bd]
     passthrough_dense: bool = False
 
@@ -103,7 +103,7 @@ class SunShapeQuantizedKeys:
             return self.codes, self.passthrough, self.passthrough_dense
         heads = self.quantized_heads
         codes = torch.stack([h.indices for h in heads]).reshape(self.batch_size, self.num_kv_heads, self.seq_len, -1)
-        if codes.dtype != torch.uint8:
+        if codes.dtype not in (torch.uint8, torch.int16, torch.int32):  # the reference's compact index dtypes
             codes = codes.to(torch.uint8)
         pt = None
         if heads and getattr(heads[0], "passthrough_values", None) is not None:

@@ -45,9 +45,11 @@ def test_layer_selection_mirrors_reference():
 
 
 def test_code_layer_rejects_codecs_the_kernels_cannot_serve():
-    wide = SunShapeBlockCodec(head_dim=32, block_dim=4, n_centroids=512, device="cpu")
-    with pytest.raises(RuntimeError, match="uint8"):
-        SunShapeCodeLayer(wide)
+    wide = SunShapeBlockCodec(head_dim=32, block_dim=4, n_centroids=4096, device="cpu")
+    assert SunShapeCodeLayer(wide).codec is wide  # 16-bit codes (the reference's int16 indices)
+    huge = SunShapeBlockCodec(head_dim=4, block_dim=4, n_centroids=(1 << 20) + 1, device="cpu")
+    with pytest.raises(RuntimeError, match="2\\^20"):
+        SunShapeCodeLayer(huge)
     rot = SunShapeBlockCodec(head_dim=32, block_dim=4, use_rotation=True, device="cpu")
     assert SunShapeCodeLayer(rot).codec is rot  # rotated codecs run on the kernels
 

@@ -64,10 +64,14 @@ def test_heavy_blocks_cached_and_refreshed():
 
 
 def test_unsupported_modes_raise_with_reason():
-    c = SunShapeBlockCodec(head_dim=64, block_dim=8, n_centroids=1024, device="cpu")
-    assert "uint8" in c.unsupported_reason()
-    with pytest.raises(RuntimeError, match="uint8"):
-        c.quantize(torch.randn(4, 64))
+    wide = SunShapeBlockCodec(head_dim=64, block_dim=8, n_centroids=1024, device="cpu")
+    assert wide.unsupported_reason() is None  # 16-bit codes (the reference's int16 indices)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        wide.quantize(torch.randn(4, 64))
+    c = SunShapeBlockCodec(head_dim=4, block_dim=4, n_centroids=(1 << 20) + 1, device="cpu")
+    assert "2^20" in c.unsupported_reason()
+    with pytest.raises(RuntimeError, match="2\\^20"):
+        c.quantize(torch.randn(4, 4))
     rot = SunShapeBlockCodec(head_dim=64, block_dim=8, use_rotation=True, device="cpu")
     assert rot.unsupported_reason() is None and rot.rotation_matrix() is rot.rotation
     with pytest.raises(RuntimeError, match="no CPU path"):

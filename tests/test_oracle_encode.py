@@ -353,3 +353,56 @@ def test_rotated_encode_with_permutation_matrix_equals_permutation_encode():
     a, _ = O.encode(x, perm, cent)
     b, _ = O.encode(x, np.zeros(D, np.int64), cent, rotation=P)  # perm ignored under rotation
     assert np.array_equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# codebooks past 256 codewords: the reference stores int16 / int32 indices (sunshape/codec.py:78-83);
+# its default fitter gives 4,096 codewords at 3 bits/dim and block_dim 4 (sunshape/hf.py:594)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("nc,bd", [(512, 2), (4096, 4), (65536, 1)])
+def test_wide_encode_vs_torch_cdist(nc, bd):
+    """Indices over 512 / 4,096 / 65,536 codewords against torch.cdist(...).argmin(-1), the reference's
+    call: every difference is a sqrt-rounding tie of the pre-sqrt values.  The dtype is the
+    reference's compact one (16-bit below 65,536 codewords, int32 from there)."""
+    D = 4 * bd
+    x, _ = _data(300 + nc, 700, D, nc=1)
+    rng = np.random.default_rng(301 + nc)
+    cent = (rng.standard_normal((D // bd, nc, bd)) * 1.3).astype(np.float32)
+    codes, _ = O.encode(x, np.arange(D), cent)
+    assert codes.dtype == (np.uint16 if nc <= 65535 else np.int32)
+    for b in range(D // bd):
+        xb = np.ascontiguousarray(x[:, b * bd:(b + 1) * bd])
+        ref = torch.cdist(torch.from_numpy(xb), torch.from_numpy(cent[b])).argmin(-1).numpy()
+        got = codes[:, b].astype(np.int64)
+        _assert_only_sqrt_ties(xb, cent[b], got, ref)
+        assert (got == ref).mean() > 0.99
+
+
+def test_wide_encode_agrees_with_byte_encode_and_brute_force():
+    """The int32-index entry point equals the uint8 one on a 256-codeword codebook bit for bit (the same
+    search), codewords placed at keys give their own (first) index past 256, and duplicated codewords
+    resolve to the lowest index; a row-chunked, multi-threaded run equals the single-threaded one."""
+    rng = np.random.default_rng(9)
+    D, bd = 8, 4
+    cent = rng.standard_normal((2, 256, bd)).astype(np.float32)
+    x = rng.standard_normal((400, D)).astype(np.float32)
+    perm = rng.permutation(D)
+    c8, _ = O.encode(x, perm, cent)
+    wide = np.zeros((2, 1000, bd), np.float32)
+    wide[:, :256] = cent
+    wide[:, 256:] = 1e6  # far away: the search over 1,000 codewords must pick the same ones
+    cw, _ = O.encode(x, perm, wide)
+    assert cw.dtype == np.uint16 and np.array_equal(cw.astype(np.int64), c8.astype(np.int64))
+    # keys on codewords 700 (block 0) and 999 (block 1), with 999 duplicated at 300
+    wide2 = rng.standard_normal((2, 1000, bd)).astype(np.float32)
+    wide2[1, 300] = wide2[1, 999]
+    xp = np.concatenate([wide2[0, 700], wide2[1, 999]])[None]
+    keys = np.empty_like(xp)
+    keys[:, perm] = xp
+    got, _ = O.encode(keys, perm, wide2)
+    assert got.tolist() == [[700, 300]]
+    big = rng.standard_normal((3000, D)).astype(np.float32)
+    one, _ = O.encode(big, perm, wide2)
+    many, _ = O.encode(big, perm, wide2, threads=5)
+    assert np.array_equal(one, many)
