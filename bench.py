@@ -12,7 +12,7 @@ from HIP events on its own stream, the same launch's time with cold caches (a 1 
 before each), and a bounded CPU baseline: the reference's eager torch decode path on the
 host's cores (oracle/torch_eager.py).
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c4ct|c4ctbd2|c4ctg8|c4ctmix|c4mix|c5encpro] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c4ct|c4ctbd2|c4ctg8|c4ctmix|c4mix|c4scores|c5encpro] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -40,7 +40,7 @@ def _args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "c4g8", "c4bd2", "c3p6",
-                                                     "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c4ctmix", "c4mix", "c5encpro",
+                                                     "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c4ctmix", "c4mix", "c4scores", "c5encpro",
                                                      "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -70,7 +70,7 @@ def _decode_workload(name, dev, kernel):
 
     heavy, pt = None, None
     nc, code_bits = 256, 0
-    if name in ("c4", "c4g8", "c4bd2", "c4p6", "c4mix"):
+    if name in ("c4", "c4g8", "c4bd2", "c4p6", "c4mix", "c4scores"):
         # c4g8 / c4bd2: the config-4 layer with 64 query heads (8 per KV head) or at 4 bits/dim
         # (64 blocks of dim 2); their LUTs exceed the LDS, so they run the MFMA-scores kernel.
         # c4p6: the layer at 3 bits/dim (64 blocks of dim 2, 64 codewords), 6-bit codes packed
@@ -154,6 +154,10 @@ def _decode_workload(name, dev, kernel):
         codes, v = p["codes"], p["v"]
         ref = hip_ops.decode(q, codes, v, perm, cent, scale=p.meta["scale"], heavy=heavy, pt=pt, kernel=kernel,
                              code_bits=code_bits)
+    scores = None
+    if name == "c4scores":  # config 4 also lists the raw fp32 scores [B, Hq, 1, T] as an output
+        scores = torch.empty(B, Hq, 1, T, device=dev, dtype=torch.float32)
+        ref = ref if not isinstance(ref, tuple) else ref[0]
     a = N.DecodeArgs(
         q=q.data_ptr(), q_dtype=N.SSQ_BF16, q_sb=q.stride(0), q_sh=q.stride(1), q_sl=q.stride(2),
         batch=B, num_q_heads=Hq, q_len=1, head_dim=D, num_kv_heads=Hkv, has_scale=1, scale=p.meta["scale"],
@@ -166,6 +170,8 @@ def _decode_workload(name, dev, kernel):
         v=v.data_ptr(), v_dtype=N.SSQ_BF16, value_dim=Dv, v_sb=v.stride(0), v_sh=v.stride(1), v_st=v.stride(2),
         out=out.data_ptr(), o_sb=out.stride(0), o_sh=out.stride(1), o_sl=out.stride(2), kernel=kernel,
     )
+    if scores is not None:
+        a.scores, a.s_sb, a.s_sh, a.s_sl = scores.data_ptr(), scores.stride(0), scores.stride(1), scores.stride(2)
     if heavy is not None:
         a.heavy_mask[0], a.heavy_mask[1] = N.heavy_mask_words(heavy)
         a.pt, a.pt_dtype, a.pt_dense = pt.data_ptr(), N.SSQ_BF16, 0
@@ -192,7 +198,8 @@ def _decode_workload(name, dev, kernel):
                   + Hkv * nb * nc * bd * 4         # fp32 codebooks
                   + Hkv * D * 8                    # int64 permutations
                   + (B * (T // 16) * 4 if paged else 0)  # int32 block table
-                  + (pt.numel() * 2 if pt is not None else 0))  # bf16 passthrough values
+                  + (pt.numel() * 2 if pt is not None else 0)  # bf16 passthrough values
+                  + (scores.numel() * 4 if scores is not None else 0))  # fp32 raw scores
     cfg = {"workload": {"c4": "C4 paged fused decode (Llama-3-8B layer, 2 bits/dim)",
                         "c4g8": "C4 layer with 64 query heads (8 per KV head), paged, 2 bits/dim",
                         "c4bd2": "C4 layer at 4 bits/dim (64 blocks of dim 2), paged",
@@ -202,6 +209,7 @@ def _decode_workload(name, dev, kernel):
                         "c4ctg8": "C4 layer with contiguous rows, 64 query heads (8 per KV head), 2 bits/dim",
                         "c4ctmix": "C4 layer with contiguous rows, SunShape-Mixed: 28 VQ blocks + 4 bf16 passthrough blocks of dim 4",
                         "c4mix": "C4 paged, SunShape-Mixed: 28 VQ blocks + 4 bf16 passthrough blocks of dim 4",
+                        "c4scores": "C4 paged fused decode that also writes the fp32 scores [B, Hq, 1, T]",
                         "c3": "C3 contiguous fused decode (Qwen2.5-0.5B layer, 4 bits/dim)",
                         "c5": "C5 SunShape-Mixed fused decode (config-5 keys: 28 VQ + 4 bf16 blocks of dim 2)",
                         "c3p6": "C3 layer at 3 bits/dim: 64 codewords, 6-bit codes packed in int32 words"}[name],
@@ -623,7 +631,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2", "c3p6", "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c4ctmix",
-                         "c4mix"):
+                         "c4mix", "c4scores"):
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
         step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev, args.kernel)

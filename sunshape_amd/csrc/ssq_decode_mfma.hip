@@ -128,7 +128,11 @@ bool plan(const ssq_decode_args* a, SsqMfmaPlan& pl) {
     if (a->kernel == 4 && !q4_ok) return false;
     if (!lut_ok && !q4_ok) return false;
     pl.ct = ct;
-    pl.q4 = q4_ok && (a->kernel == 4 || !lut_ok || pl.n_groups > 1);
+    // Contiguous passthrough blocks at head_dim 128 also take the 4x4-MFMA kernel: its passthrough
+    // dims cost one MFMA each where the LUT kernel adds a VALU product per row (config-4 layer with 4
+    // bf16 blocks of dim 4: 0.806 against 0.889 ms); kernel 2 still asks for the LUT kernel.
+    const bool q4_pt = ct && heavy && a->kernel != 2;
+    pl.q4 = q4_ok && (a->kernel == 4 || !lut_ok || pl.n_groups > 1 || q4_pt);
     if (pl.q4) {
         pl.rg = rows < 16 ? rows : 16;
         pl.n_groups = (rows + 15) / 16;

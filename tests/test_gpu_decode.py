@@ -567,10 +567,11 @@ def test_contiguous_lut_kernel_128_dim_scores_only(B, Hq, Hkv, Lq, bd, T, splits
                                                          (2, 8, True, torch.float32, torch.bfloat16, False),
                                                          (4, 1, True, torch.bfloat16, torch.bfloat16, False)])
 def test_contiguous_lut_kernel_128_dim_passthrough(bd, n_heavy, dense, pdt, vdt, ct):
-    """SunShape-Mixed passthrough blocks on the contiguous 128-dim LUT kernel (ct): 8 or 16
+    """SunShape-Mixed passthrough blocks on the contiguous 128-dim LUT kernel (ct, kernel 2): 8 or 16
     consecutive 16-bit stored values per token; the heavy blocks' LUT rows are zero and their
-    scores come from the stored values.  Other passthrough layouts (fp32, dense slots, 4 dims)
-    take the generic kernel; both match the oracle."""
+    scores come from the stored values.  Other passthrough layouts (fp32, dense slots of blocks that
+    are not adjacent, 4 dims) take the 4x4-MFMA kernel, as does the automatic choice; all match the
+    oracle."""
     log(f"contig LUT D128 passthrough bd={bd} n_heavy={n_heavy} dense={dense} pdt={pdt} vdt={vdt}")
     B, Hkv, Hq, T, D = 2, 8, 32, 555, 128
     nb = D // bd
@@ -595,8 +596,10 @@ def test_contiguous_lut_kernel_128_dim_passthrough(bd, n_heavy, dense, pdt, vdt,
     assert_rel(np_of(out), ro, BF16_TOL, "out")
     assert_rel(np_of(scores), rs, SCORE_TOL, "scores")
     assert_rel(np_of(lse), rl, SCORE_TOL, "lse")
-    oa = np_of(hip_ops.decode(*args, **kw))
-    assert np.array_equal(oa, np_of(out))
+    # the automatic choice: the 4x4-MFMA kernel, which takes contiguous passthrough at head_dim 128
+    oa = hip_ops.decode(*args, **kw)
+    assert torch.equal(oa, hip_ops.decode(*args, **kw, kernel=4))
+    assert_rel(np_of(oa), ro, BF16_TOL, "out, automatic choice")
 
 
 def test_contiguous_mfma_kernel_rejects_wide_passthrough():
@@ -716,4 +719,7 @@ def test_contiguous_lut_kernel_128_dim_passthrough_rows(Hq, Hkv, Lq, bd, hidx, d
     assert_rel(np_of(out), ro, BF16_TOL, "out")
     assert_rel(np_of(scores), rs, SCORE_TOL, "scores")
     assert_rel(np_of(lse), rl, SCORE_TOL, "lse")
-    assert torch.equal(hip_ops.decode(*args, **kw), out)  # the automatic choice
+    # the automatic choice: the 4x4-MFMA kernel, which takes contiguous passthrough at head_dim 128
+    oa = hip_ops.decode(*args, **kw)
+    assert torch.equal(oa, hip_ops.decode(*args, **kw, kernel=4))
+    assert_rel(np_of(oa), ro, BF16_TOL, "out, automatic choice")
