@@ -385,8 +385,16 @@ def _encode_workload(dev, kernel, pro=False):
                         (" under a SunShape-Pro block metric" if pro else "")), "keys": n,
            "head_dim": D, "block_dim": 2, "heavy_blocks": 4, "kernel": kernel,
            "search": "grid" if grid is not None else "exhaustive", "grid_build_ms": grid_ms, "metric": pro,
-           "grid_bytes": None if grid is None else grid.numel()}
+           "grid_bytes": None if grid is None else grid.numel(),
+           "grid_budget_bytes": _grid_budget()}
     return step, n, algo, cfg, None, "ssq_encode" if grid is None else "ssq_encode_grid"
+
+
+def _grid_budget():
+    """The process-wide byte budget the codecs' cached encode grids share."""
+    from sunshape_amd import codec as C
+
+    return C._GRID_BUDGET[0]
 
 
 def _append_workload(name, dev, kernel):

@@ -16,11 +16,55 @@ layout.
 from __future__ import annotations
 
 import math
+import os
+import weakref
+from collections import OrderedDict
 from typing import NamedTuple, Optional
 
 import torch
 
 from . import hip_ops
+
+# Encode search grids are cached per codec and codebook, within one process-wide byte budget shared
+# by every codec (a model has one codec per layer): the least recently used grids are dropped to
+# make room, and a grid larger than the whole budget is not built (that encode then scans every
+# codeword: the same codes, more time).  SUNSHAPE_AMD_GRID_BUDGET_MB sets the budget (default
+# 1024 MiB); set_encode_grid_budget changes it at run time.
+_GRID_BUDGET = [int(os.environ.get("SUNSHAPE_AMD_GRID_BUDGET_MB", "1024")) << 20]
+_GRID_LRU: "OrderedDict[tuple, tuple]" = OrderedDict()  # (id(codec), slot) -> (weakref to codec, bytes)
+
+
+def _grid_lru_live():
+    """Drop entries whose codec is gone or no longer holds the grid; yield (key, codec, slot, bytes)."""
+    for key in list(_GRID_LRU):
+        ref, nbytes = _GRID_LRU[key]
+        codec = ref()
+        if codec is None or key[1] not in codec._grid_cache:
+            del _GRID_LRU[key]
+            continue
+        yield key, codec, key[1], nbytes
+
+
+def encode_grid_footprint() -> int:
+    """Device bytes held by cached encode search grids, over every codec of the process."""
+    return sum(n for *_, n in _grid_lru_live())
+
+
+def set_encode_grid_budget(nbytes: int) -> None:
+    """Process-wide byte budget for cached encode search grids; grids past it are dropped, least
+    recently used first."""
+    _GRID_BUDGET[0] = int(nbytes)
+    _grid_lru_evict(_GRID_BUDGET[0])
+
+
+def _grid_lru_evict(limit: int) -> None:
+    used = encode_grid_footprint()
+    for key, codec, slot, nbytes in list(_grid_lru_live()):
+        if used <= limit:
+            break
+        codec._grid_cache.pop(slot, None)
+        del _GRID_LRU[key]
+        used -= nbytes
 
 PERMUTATION_MODES = frozenset({"profileperm_baseline", "profileperm_localmetric_dsq", "profileperm_mixed_precision"})
 # modes whose fitted E is the identity (sunshape/codec.py:279-312): encode takes no metric
@@ -201,7 +245,11 @@ class SunShapeBlockCodec(torch.nn.Module):
         for a Llama-3-8B layer at 4 bits/dim (8 heads x 64 blocks).  A
         per-KV-head codebook has one grid: a single head's view (``codebook(kv_head)``) gets
         that head's slice of it (the layout is head-major), not a grid of its own.  Set
-        ``use_encode_grid = False`` to run the exhaustive encode without any grid.
+        ``use_encode_grid = False`` to run the exhaustive encode without any grid.  Every codec's
+        grids count against one process-wide budget (``set_encode_grid_budget``,
+        ``encode_grid_footprint``; 1 GiB unless SUNSHAPE_AMD_GRID_BUDGET_MB says otherwise): the
+        least recently used are dropped first, and an encode whose grid is dropped or would not
+        fit scans every codeword instead (the same codes).
         """
         if not self.use_encode_grid or self.block_dim != 2 or self.mode in METRIC_MODES:
             return None
@@ -216,10 +264,21 @@ class SunShapeBlockCodec(torch.nn.Module):
                 return None if full is None else full.view(buf.shape[0], -1)[off // step]
         slot = (cent.data_ptr(), tuple(cent.shape))
         key = (buf.data_ptr(), buf._version)
+        lru_key = (id(self), slot)
         hit = self._grid_cache.get(slot)
-        if hit is None or hit[0] != key:
-            hit = (key, hip_ops.encode_grid(cent))
-            self._grid_cache[slot] = hit
+        if hit is not None and hit[0] == key:
+            if lru_key in _GRID_LRU:
+                _GRID_LRU.move_to_end(lru_key)
+            return hit[1]
+        self._grid_cache.pop(slot, None)  # stale (the codebook changed): its bytes are freed below
+        _GRID_LRU.pop(lru_key, None)
+        nbytes = hip_ops.encode_grid_bytes(cent)
+        if nbytes > _GRID_BUDGET[0]:
+            return None  # larger than the whole budget: the exhaustive encode (same codes)
+        _grid_lru_evict(_GRID_BUDGET[0] - nbytes)
+        hit = (key, hip_ops.encode_grid(cent))
+        self._grid_cache[slot] = hit
+        _GRID_LRU[lru_key] = (weakref.ref(self), nbytes)
         return hit[1]
 
     def rotation_matrix(self) -> torch.Tensor | None:

@@ -478,6 +478,20 @@ def encode(keys: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
     return e.codes, e.pt
 
 
+def _grid_args(cent: torch.Tensor, num_kv_heads: int):
+    nb, nc = cent.shape[-3], cent.shape[-2]
+    return N.EncodeArgs(num_kv_heads=int(cent.shape[0] if cent.ndim == 4 else num_kv_heads), cent=N.ptr(cent),
+                        cent_sh=nb * nc * 2 if cent.ndim == 4 else 0, block_dim=2, n_blocks=nb, n_centroids=nc,
+                        head_dim=2 * nb)
+
+
+def encode_grid_bytes(cent: torch.Tensor, num_kv_heads: int = 1) -> int:
+    """Device bytes of encode_grid(cent) (0 where the grid does not apply), without building it."""
+    if cent.ndim not in (3, 4) or cent.shape[-1] != 2:
+        return 0
+    return int(N.lib().ssq_encode_grid_bytes(ctypes.byref(_grid_args(cent, num_kv_heads))))
+
+
 def encode_grid(cent: torch.Tensor, num_kv_heads: int = 1) -> torch.Tensor:
     """Search grid for encode(..., grid=) from codebooks [nb, nc, 2] or [Hkv, nb, nc, 2] (fp32).
 
@@ -488,12 +502,7 @@ def encode_grid(cent: torch.Tensor, num_kv_heads: int = 1) -> torch.Tensor:
     _on_gpu("centroids", cent)
     cent = cent.to(torch.float32).contiguous()
     _require(cent.ndim in (3, 4) and cent.shape[-1] == 2, "the encode grid serves block_dim 2 codebooks")
-    if cent.ndim == 4:
-        num_kv_heads = cent.shape[0]
-    nb, nc = cent.shape[-3], cent.shape[-2]
-    a = N.EncodeArgs(num_kv_heads=int(num_kv_heads), cent=N.ptr(cent),
-                     cent_sh=nb * nc * 2 if cent.ndim == 4 else 0,
-                     block_dim=2, n_blocks=nb, n_centroids=nc, head_dim=2 * nb)
+    a = _grid_args(cent, num_kv_heads)
     lib = N.lib()
     size = lib.ssq_encode_grid_bytes(ctypes.byref(a))
     _require(size > 0, "the encode grid serves block_dim 2 codebooks with at most 128 blocks of 256 codewords")

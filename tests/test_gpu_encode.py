@@ -539,3 +539,31 @@ def test_per_head_grid_is_a_slice_of_the_per_kv_head_grid():
         assert view.data_ptr() == whole.data_ptr() + h * per.shape[1] and view.numel() == per.shape[1]
         assert torch.equal(view, per[h])
     assert len(codec._grid_cache) == 1
+
+
+def test_encode_grid_budget_32_layers():
+    """A 32-layer model with per-KV-head block_dim-2 codecs (32 MiB of grid per layer, 1 GiB in all)
+    under a 128 MiB grid budget: the cached grids never exceed the budget, and every layer's codes
+    equal the exhaustive encode's."""
+    from sunshape_amd import codec as C
+
+    log("encode grid budget, 32 layers")
+    B, Hkv, S, D, bd = 2, 2, 1500, 64, 2
+    old = C._GRID_BUDGET[0]
+    codecs = []  # every layer's codec stays alive, as in a loaded model
+    try:
+        C.set_encode_grid_budget(128 << 20)
+        for layer in range(32):
+            cb = synthetic.make_codebook(Hkv, D, bd, 700 + layer)
+            codec = SunShapeBlockCodec.from_buffers(cb.perm, cb.centroids, device=DEV)
+            codecs.append(codec)
+            g = torch.Generator().manual_seed(800 + layer)
+            keys = (torch.randn(B, Hkv, S, D, generator=g) * cb.sigma[:, None, :]).to(torch.bfloat16).to(DEV)
+            grid = codec.encode_search_grid(codec.centroids)
+            assert grid is not None and C.encode_grid_footprint() <= 128 << 20
+            with_grid, _ = hip_ops.encode(keys, codec.permutation, codec.centroids, grid=grid)
+            exhaustive, _ = hip_ops.encode(keys, codec.permutation, codec.centroids, kernel=1)
+            assert torch.equal(with_grid, exhaustive), f"layer {layer}"
+        assert 96 << 20 <= C.encode_grid_footprint() <= 128 << 20  # the 3 most recent layers' grids
+    finally:
+        C.set_encode_grid_budget(old)

@@ -306,3 +306,41 @@ def test_install_hooks_keyword_only_and_error_order(tmp_path):
     except Exception:
         with pytest.raises(RuntimeError, match="vLLM is not installed"):
             install_hooks(bundle_path=bundle, **kw)
+
+
+def test_encode_grid_budget_is_process_wide_lru(monkeypatch):
+    """Encode search grids of every codec share one byte budget: the least recently used are dropped
+    first, a grid larger than the budget is not built (the encode then scans every codeword), and a
+    per-KV-head codec's one-head views share its grid.  Grids are stood in for by host buffers of the
+    library's stated size (ssq_encode_grid_bytes)."""
+    from sunshape_amd import codec as C
+    from sunshape_amd import hip_ops
+
+    built = []
+
+    def fake_grid(cent, num_kv_heads=1):
+        built.append(cent.data_ptr())
+        return torch.empty(hip_ops.encode_grid_bytes(cent, num_kv_heads), dtype=torch.uint8)
+
+    monkeypatch.setattr(C.hip_ops, "encode_grid", fake_grid)
+    codecs = [SunShapeBlockCodec(head_dim=64, block_dim=2, num_kv_heads=2, device="cpu") for _ in range(32)]
+    per = hip_ops.encode_grid_bytes(codecs[0].centroids)
+    assert 32 << 20 <= per < 33 << 20  # 0.5 MiB per head and block, plus block headers
+    old = C._GRID_BUDGET[0]
+    try:
+        C.set_encode_grid_budget(4 * per + 100)
+        for c in codecs:
+            assert c.encode_search_grid(c.centroids) is not None
+            assert C.encode_grid_footprint() <= 4 * per + 100
+        assert C.encode_grid_footprint() == 4 * per and len(built) == 32
+        codecs[28].encode_search_grid(codecs[28].centroids)  # among the 4 most recent: a hit
+        assert len(built) == 32
+        head = codecs[28].encode_search_grid(codecs[28].codebook(1))  # one head's view of the same grid
+        assert len(built) == 32 and head.numel() == per // 2
+        codecs[0].encode_search_grid(codecs[0].centroids)  # evicted long ago: rebuilt, evicting the oldest
+        assert len(built) == 33 and C.encode_grid_footprint() == 4 * per
+        C.set_encode_grid_budget(per - 1)  # smaller than one grid: everything dropped, nothing built
+        assert C.encode_grid_footprint() == 0
+        assert codecs[5].encode_search_grid(codecs[5].centroids) is None and len(built) == 33
+    finally:
+        C.set_encode_grid_budget(old)
