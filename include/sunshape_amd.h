@@ -44,10 +44,16 @@ enum ssq_status {
 
 enum ssq_dtype { SSQ_F32 = 0, SSQ_BF16 = 1, SSQ_F16 = 2 };
 
+/* Width of the stored codes, as the reference's _compact_index_dtype (sunshape/codec.py:78-83):
+ * one byte for n_centroids <= 256, 16 bits (read unsigned) up to 65535, 32 bits beyond, at most
+ * SSQ_MAX_CENTROIDS.  Every `codes` pointer below has that element type; code strides count
+ * elements of it (int32 words for the packed codes of code_bits 1..8, which take n_centroids <= 256). */
+#define SSQ_MAX_CENTROIDS (1 << 20)
+
 /* Layout of the key codes and values. */
 enum ssq_layout {
-    SSQ_CONTIGUOUS = 0, /* codes [B, Hkv, T, nb] uint8, V [B, Hkv, T, Dv] (token-major) */
-    SSQ_PAGED = 1       /* vLLM-style pages: codes [P, Hkv, page, nb] uint8,
+    SSQ_CONTIGUOUS = 0, /* codes [B, Hkv, T, nb], V [B, Hkv, T, Dv] (token-major) */
+    SSQ_PAGED = 1       /* vLLM-style pages: codes [P, Hkv, page, nb],
                            V [P, Hkv, Dv, page] (dim-major inside a page, vLLM's value layout),
                            block_table [B, max_pages] int32, seq_lens [B] int32 */
 };
@@ -87,7 +93,8 @@ typedef struct ssq_decode_args {
     /* keys */
     int32_t layout;      /* enum ssq_layout */
     int32_t seq_len;     /* T (contiguous) / max context (paged) */
-    const uint8_t* codes; int64_t c_sb, c_sh, c_st;  /* contiguous: b,kv,t strides; paged: page,kv,t strides */
+    const uint8_t* codes; int64_t c_sb, c_sh, c_st;  /* contiguous: b,kv,t strides; paged: page,kv,t strides
+                                                        (elements of the code width, SSQ_MAX_CENTROIDS) */
     const int32_t* block_table; int64_t bt_sb; const int32_t* seq_lens; int32_t page_size;
     /* values (NULL for scores-only); Dv contiguous (contiguous) / page contiguous (paged) */
     const void* v; int32_t v_dtype; int32_t value_dim;
@@ -101,15 +108,19 @@ typedef struct ssq_decode_args {
                                                  paged: entries t >= seq_lens[b] are not written */
     /* tuning: 0 = library heuristic */
     int32_t num_splits;
-    int32_t kernel;      /* 0 auto, 1 generic LUT/VALU kernel, 2 MFMA LUT kernels (paged: LUT scores, or
-                            4x4-MFMA scores where the LUT does not fit; contiguous rows past head_dim 64
-                            with 128-dim values, or scores only), 3 MFMA contiguous kernel (head_dim 64),
-                            4 the paged 4x4-MFMA-scores kernel wherever it applies */
-    /* code storage: 0 = one uint8 per block (c_* strides in bytes); 1..8 = packing in
-     * uint32 words, vpe = 32 / code_bits codes per word, block blk = p*vpe + v at bits
+    int32_t kernel;      /* 0 auto, 1 generic LUT/VALU kernel (codewords gathered from memory past 256
+                            codewords), 2 MFMA LUT kernels (paged: LUT scores, or 4x4-MFMA scores where the
+                            LUT does not fit or a mask / passthrough blocks come; contiguous rows past
+                            head_dim 64 with 128-dim values, or scores only; at head_dim 128 the 4x4-MFMA
+                            kernel where the LUT needs row groups), 3 MFMA contiguous kernel (head_dim 64),
+                            4 the 4x4-MFMA-scores kernel (paged, or contiguous at head_dim 128) wherever it
+                            applies */
+    /* code storage: 0 = one code per block, of the width n_centroids gives (SSQ_MAX_CENTROIDS; c_*
+     * strides in those elements); 1..8 (n_centroids <= 256) = packing in uint32 words,
+     * vpe = 32 / code_bits codes per word, block blk = p*vpe + v at bits
      * [v*code_bits, (v+1)*code_bits) of word p (the layout of sunshape/triton_kernels.py:213-283);
      * c_* strides then count words.  8-bit words are read as byte rows; 6-bit words run on
-     * every MFMA decode kernel and 4-bit words on the contiguous and paged MFMA-scores ones
+     * every MFMA decode kernel and 4-bit words on the contiguous and 4x4-MFMA-scores ones
      * (without mask or passthrough); other widths take the generic kernel.  Results equal the
      * same kernel's launch over uint8 codes bit for bit. */
     int32_t code_bits;
@@ -170,10 +181,12 @@ typedef struct ssq_encode_args {
     const float* metric; int64_t metric_sh;   /* SunShape-Pro E [D, D] or NULL (identity) */
     int32_t block_dim, n_blocks, n_centroids;
     uint64_t heavy_mask[2];
-    uint8_t* codes; int64_t c_sb, c_sh, c_st;
+    uint8_t* codes; int64_t c_sb, c_sh, c_st;   /* code width per n_centroids (SSQ_MAX_CENTROIDS) */
     void* pt; int32_t pt_dtype; int32_t pt_dense; int64_t pt_sb, pt_sh, pt_st;
     const int64_t* slot_mapping; int64_t sm_sb; int32_t page_size;
-    int32_t kernel;      /* 0 auto, 1 VALU exact scan, 2 MFMA screen + exact certification, 3 grid search */
+    int32_t kernel;      /* 0 auto, 1 VALU exact scan, 2 MFMA screen + exact certification, 3 grid search
+                            (2 and 3 serve at most 256 codewords; more run the exact scan over LDS chunks
+                            of the codebook) */
     const void* grid; uint64_t grid_bytes;  /* optional search grid from ssq_encode_grid_build (or NULL) */
     /* 1: torch.cdist's direct evaluation, sqrt(sum_k (x_k - c_k)^2) with the rounded squares summed
      * in k order, which torch takes in place of the mm formulation when both of its inputs have at
@@ -218,8 +231,8 @@ int ssq_transform_rows(const void* x, int32_t x_dtype, int64_t x_sr, int64_t row
                        int32_t has_scale, float scale, const float* mat, int32_t transpose,
                        float* out, int64_t o_sr, void* stream);
 
-/* k_hat[t, j] (original basis, fp32 [T, D] with row stride o_st) from codes [T, nb]
- * (row stride c_st) and optional passthrough pt (dense [T, nb, bd] fp32 when pt_dense,
+/* k_hat[t, j] (original basis, fp32 [T, D] with row stride o_st) from codes [T, nb] of the width
+ * n_centroids gives (row stride c_st elements) and optional passthrough pt (dense [T, nb, bd] fp32 when pt_dense,
  * else compact [T, n_heavy, bd]; row stride pt_st).  Replaces sunshape/codec.py:387-398. */
 int ssq_dequantize(const uint8_t* codes, int64_t c_st, int32_t tokens,
                    const int64_t* perm, const float* cent, int32_t head_dim, int32_t block_dim,

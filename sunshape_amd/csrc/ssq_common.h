@@ -125,7 +125,7 @@ inline bool ssq_encode_fold(const ssq_encode_args* a, int keys_per_wg) {
 // one byte up to 256 codewords, 16 bits up to 65535, 32 bits beyond.  16-bit codes are read as
 // unsigned, so every index below 65536 round-trips (the reference's int16 storage holds indices up
 // to 32767 as the same bits).
-constexpr int kMaxCentroids = 1 << 20;
+constexpr int kMaxCentroids = SSQ_MAX_CENTROIDS;
 __host__ __device__ inline int ssq_code_width(int n_centroids) {
     return n_centroids <= 256 ? 1 : n_centroids <= 65535 ? 2 : 4;
 }
