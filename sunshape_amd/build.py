@@ -143,5 +143,63 @@ def build(verbose: bool = False, incremental: bool = False) -> str:
     return LIB_PATH
 
 
+SAN_DIR = os.path.join(OUT_DIR, "san")
+SAN_LIB_PATH = os.path.join(SAN_DIR, "libsunshape_amd_hostsan.so")
+
+
+def asan_runtime() -> str | None:
+    """The compiler's shared AddressSanitizer runtime (to LD_PRELOAD into a process that loads the
+    host-sanitized library), or None."""
+    import glob
+
+    hits = sorted(glob.glob("/opt/rocm/lib/llvm/lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so"))
+    return hits[-1] if hits else None
+
+
+def build_host_sanitized(verbose: bool = False) -> str:
+    """The library with its host code under AddressSanitizer and UndefinedBehaviorSanitizer (each
+    -fsanitize= behind -Xarch_host: the device code is built plainly, at -O1, since a host-only
+    object would reference a fatbin nothing defines), for CPU tests that drive the argument checks
+    and launch planning with arbitrary inputs in a process that sees no GPU.  Rebuilt when a source
+    or header is newer than the library.  Returns the library's path."""
+    hipcc = _hipcc()
+    os.makedirs(SAN_DIR, exist_ok=True)
+    srcs = sources()
+    if os.path.exists(SAN_LIB_PATH):
+        t = os.path.getmtime(SAN_LIB_PATH)
+        deps = set(srcs)
+        for s in srcs:
+            _includes(s, deps)
+        if all(os.path.getmtime(d) <= t for d in deps):
+            return SAN_LIB_PATH
+    san = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+           "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer"]
+    flags = [f"--offload-arch={ARCH}", "-O1", "-Xarch_host", "-g", "-std=c++17", "-fPIC", "-ffp-contract=off",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", *san]
+    objs = [os.path.join(SAN_DIR, os.path.basename(s)[:-4] + ".o") for s in srcs]
+
+    def one(so):
+        src, obj = so
+        res = subprocess.run([hipcc, *flags, "-c", src, "-o", obj], capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"host-sanitized compile failed for {os.path.basename(src)}:\n{res.stderr}")
+
+    with cf.ThreadPoolExecutor(max_workers=8) as ex:
+        list(ex.map(one, zip(srcs, objs)))
+    tmp = SAN_LIB_PATH + ".tmp"
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libsan", "-Xarch_host", "-fsanitize=address",
+           "-Xarch_host", "-fsanitize=undefined", *objs, "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"host-sanitized link failed:\n{res.stderr}")
+    os.replace(tmp, SAN_LIB_PATH)
+    if verbose:
+        print(f"built {SAN_LIB_PATH}")
+    return SAN_LIB_PATH
+
+
 if __name__ == "__main__":
-    build(verbose=True, incremental="--incremental" in sys.argv[1:])
+    if "--host-sanitized" in sys.argv[1:]:
+        build_host_sanitized(verbose=True)
+    else:
+        build(verbose=True, incremental="--incremental" in sys.argv[1:])
