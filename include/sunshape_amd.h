@@ -205,13 +205,14 @@ int ssq_encode(const ssq_encode_args* a, void* stream);
  * cell floor((t + 1) * 64), with mid the codewords' bounding-box centre and 1/inv their RMS
  * spread, so cells are finest where codewords crowd and the end cells reach to +-infinity.
  * Each cell lists, ascending, every codeword that can be the reference's first minimum for a
- * key in the cell (rounding of the reference's fp32 evaluation included), up to 31 (a longer
- * list, an unbounded end cell or a non-finite key falls back to scanning all codewords).  ssq_encode then evaluates
- * only those candidates, with the reference's exact arithmetic, so its codes equal kernels 1
- * and 2 bit for bit.  Layout, head-major: per codebook head, its block headers (32 bytes each,
- * padded to 256) then its cells (32 bytes each), so head h's bytes [h * size / heads,
- * (h + 1) * size / heads) of a per-KV-head grid are the grid of that head's codebook alone.
- * Size per head and block: 0.5 MiB.  The grid buffer must be 16-byte aligned.
+ * key in the cell (rounding of the reference's fp32 evaluation included), up to 15 (a longer
+ * list, an unbounded end cell, a block whose codewords are all one point or a non-finite key
+ * falls back to scanning all codewords).  ssq_encode then evaluates only those candidates, with
+ * the reference's exact arithmetic, so its codes equal kernels 1 and 2 bit for bit.  Layout,
+ * head-major: per codebook head, its block headers (32 bytes each, padded to 256), the cells'
+ * first 4 bytes (count and three indices), then the cells' other 16 bytes, so head h's bytes
+ * [h * size / heads, (h + 1) * size / heads) of a per-KV-head grid are the grid of that head's
+ * codebook alone.  Size per head and block: 320 KiB.  The grid buffer must be 16-byte aligned.
  * The grid depends only on perm-independent codebook values (cent, cent_sh, n_blocks,
  * n_centroids, num_kv_heads when cent_sh != 0); rebuild it when the codebook changes.  Each
  * block's header holds a fingerprint of its codebook: ssq_encode scans every codeword of a

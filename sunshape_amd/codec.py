@@ -240,9 +240,10 @@ class SunShapeBlockCodec(torch.nn.Module):
         exhaustive search bit for bit.  Built on first use and rebuilt when the centroid buffer
         changes (new storage or an in-place write, seen through its version counter).
 
-        Footprint: 32 B per cell, 128 x 128 cells per block and codebook head (0.5 MiB), plus a
-        32-byte header per block: 32 MiB for the config-5 layer (2 heads x 32 blocks), 256 MiB
-        for a Llama-3-8B layer at 4 bits/dim (8 heads x 64 blocks).  A
+        Footprint: 20 B per cell, 128 x 128 cells per block and codebook head (320 KiB; a lookup
+        reads the first 4 B of a cell), plus a 32-byte header per block: 20 MiB for the config-5
+        layer (2 heads x 32 blocks), 160 MiB for a Llama-3-8B layer at 4 bits/dim (8 heads x 64
+        blocks).  A
         per-KV-head codebook has one grid: a single head's view (``codebook(kv_head)``) gets
         that head's slice of it (the layout is head-major), not a grid of its own.  Set
         ``use_encode_grid = False`` to run the exhaustive encode without any grid.  Every codec's

@@ -100,6 +100,10 @@ struct SsqKeyMap {
         b_blk = fold ? 0 : y / a.num_kv_heads;
         n_keys = fold ? a.batch * a.seq_len : a.seq_len;
     }
+    // a kernel that orders its workgroups itself names the KV head and the sequence (ignored
+    // when folded)
+    __device__ __forceinline__ SsqKeyMap(const ssq_encode_args& a, int fold_, int kv_, int b_)
+        : fold(fold_), b_blk(fold_ ? 0 : b_), kv(kv_), n_keys(fold_ ? a.batch * a.seq_len : a.seq_len) {}
     __device__ __forceinline__ void bs(const ssq_encode_args& a, int i, int& b, int& s) const {
         if (fold) {
             b = i / a.seq_len;

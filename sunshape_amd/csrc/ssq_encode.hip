@@ -121,12 +121,15 @@ __global__ __launch_bounds__(kScanThreads) void k_encode_scan(const EncodeParams
         }
         const float xn = sq_norm(x, bd);
         const bool direct = a.direct_dist != 0;
-        // pass 1: smallest pre-sqrt value (first index)
+        // pass 1: smallest clamped pre-sqrt value max(e, 0) (first index).  A NaN value (a key
+        // with a non-finite element or one whose norm overflows) clamps to 0 as in the
+        // reference's sqrt(clamp_min(., 0)) followed by its first argmin of a row holding NaN.
         float emin = INFINITY;
         int jm = 0;
         for (int j = 0; j < nc; ++j) {
             const float e = direct ? direct_dist2(x, cbb + j * bd, bd) : mm_dist2(x, xn, cbb + j * bd, cnb[j], bd);
-            if (e < emin) { emin = e; jm = j; }
+            const float ec = e > 0.f ? e : 0.f;
+            if (ec < emin) { emin = ec; jm = j; }
         }
         // pass 2: the first index whose sqrt equals the minimum's (sqrt merges values at most
         // ~2^-22 apart relatively; indices above jm cannot win).  thr bounds that interval.
@@ -312,16 +315,21 @@ __device__ __forceinline__ void reduce_block(const float* bsw, const float* xs, 
     const int pk = key_min_i((t1 & -256) | ((t1 & 60) << 2) | (grp << 2) | (t1 & 3));
     const float mp = fmaxf(__int_as_float(pk & -256), 0.f);
     const float thr = mp * (1.0f + 0x1.0p-14f) + 5.0f * (e1 * xnv + e2 * mp) + 0x1.0p-100f;
-    // 3. decided keys: one lane's minimum under thr, no lane's second minimum under thr
+    // 3. decided keys: one lane's minimum under thr, no lane's second minimum under thr.  A key
+    // whose norm is not finite (a non-finite element, or an overflow) has no bound: every codeword
+    // is a candidate
+    const bool wild = !(thr < INFINITY);
     const int flag = (__int_as_float(t1 & -256) <= thr ? 1 : 0) + (__int_as_float(m2 & -256) <= thr ? 2 : 0);
-    const bool undecided = key_sum_i(flag) != 1;
+    const bool undecided = key_sum_i(flag) != 1 || wild;
     int code = pk & 255;
     if (__builtin_amdgcn_ballot_w64(undecided)) {  // rare: several candidates -> exact arithmetic decides
         // This lane's candidates of an undecided key (bit 4nt + i).  While its second minimum is
         // over thr the lane holds at most one value <= thr, and then it is the minimum's slot;
         // only a lane with two candidates scans all 64 values.
         uint64_t cand = 0;
-        if (undecided) {
+        if (wild) {
+            cand = ~0ull;
+        } else if (undecided) {
             if (flag & 2) {
 #pragma unroll
                 for (int nt = 0; nt < 16; ++nt)

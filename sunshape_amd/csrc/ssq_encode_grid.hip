@@ -7,13 +7,19 @@
 //
 //  * k_grid_header / k_grid_cells (built once per codebook, ssq_encode_grid_build): per block, a
 //    kG x kG grid of cells under a per-dimension map that is finest where the codewords crowd and
-//    whose end cells reach to infinity (cell_edge).  Cell C lists, ascending, every codeword j
-//    with dmin(C, c_j)^2 <= min_k dmax(C, c_k)^2 + M_C, where M_C bounds the rounding terms
-//    below; more than 31 such codewords (or an unbounded cell) mark the cell "scan all".
+//    whose end cells reach to infinity (cell_edge).  Cell C lists, ascending, every codeword j whose
+//    Voronoi region, widened by the rounding terms below, meets C: the part of C where
+//    |x - c_j|^2 <= |x - c_k|^2 + M_jk for every competitor k (each condition a half-plane) is
+//    clipped out of C, and j is listed when it is not empty.  Competitors are the codewords with
+//    dmin(C, c_k)^2 <= min_i dmax(C, c_i)^2 + M (a necessary condition for a winner, which also
+//    pre-selects the j tried); a j that one competitor's half-plane misses on all four corners of C
+//    is dropped before any clipping.  A cell's record is a 32-bit word with the count and the first
+//    three indices, and 16 bytes with up to twelve more (read only for longer lists); more than 15
+//    codewords, an unbounded cell or a codebook with non-finite values mark it "scan all" (count 0).
 //  * k_encode_grid: lane = key.  Per light block: the key's two permuted elements, its cell, the
-//    cell's record (16 or 32 bytes from the grid), then the reference chain on each listed
-//    candidate in ascending order, keeping the first minimum of the correctly rounded sqrt.
-//    Non-finite keys and "scan all" cells evaluate every codeword.
+//    cell's first word (and, for the rare list longer than 3, its second), then the reference chain
+//    on each listed candidate in ascending order, keeping the first minimum of the correctly
+//    rounded sqrt.  Non-finite keys and "scan all" cells evaluate every codeword.
 //
 // Why the list holds the winner.  Let r_j be the reference's value for codeword j, D_j the exact
 // value of the same expression on the same (rounded) norms, d_j = |x - c_j|.  Then |r_j - D_j| <=
@@ -22,12 +28,14 @@
 // The winner j* has sqrt(max(r_j*, 0)) <= sqrt(max(r_k, 0)) for every k, so max(r_j*, 0) <=
 // max(r_k, 0)(1 + 2^-21) (correctly rounded sqrt).  Chaining the bounds, for every k:
 //   d_j*^2 <= d_k^2 + 2|alpha| + |beta_j*| + |beta_k| + e_j* + e_k + (d_k^2 + |alpha| + |beta_k| + e_k) 2^-21.
-// For x in C (R = max |x| over C, Rc = max |c|): d_j*^2 >= dmin(C, c_j*)^2 and, for the k that
-// minimises dmax(C, c_k), d_k^2 <= dmax(C, c_k)^2 =: dmm, giving dmin(C, c_j*)^2 <= dmm + M_C with
-//   M_C = 1.01 (4.002u (R^2 + Rc^2) + 2.0002 g (R + Rc)^2 + (dmm + 2.001u (R^2 + Rc^2) + g (R + Rc)^2) 2^-21).
-// Cells are widened by 0.001 of a cell on each side, far more than the fp32 rounding of the
-// search kernel's cell map, so a key always lies in the cell it is looked up in.  The build
-// runs in fp64.
+// For x in C (R = max |x| over C, Rc = max |c|) and d_k^2 <= dmax(C, c_k)^2 =: D_k this is at most
+//   M_jk = 1.01 (4.002u (R^2 + Rc^2) + 2.0002 g (R + Rc)^2 + (D_k + 2.001u (R^2 + Rc^2) + g (R + Rc)^2) 2^-21),
+// so the key x itself lies in j*'s clipped polygon (and no corner test drops j*); with k the
+// codeword minimising D_k it gives dmin(C, c_j*)^2 <= min D + M, the pre-selection.  At x every
+// condition holds with a slack of 1 % of M_jk and x lies 0.001 of a cell inside the widened cell,
+// so the polygon around x is far wider than the fp64 rounding of the clipping.  Cells are widened
+// by 0.001 of a cell on each side, far more than the fp32 rounding of the search kernel's cell map,
+// so a key always lies in the cell it is looked up in.  The build runs in fp64.
 #include "ssq_common.h"
 
 #include <math.h>
@@ -36,18 +44,19 @@
 namespace {
 
 constexpr int kG = 128;        // cells per dimension
-constexpr int kRec = 32;       // bytes per cell record: count (255 = scan all), then indices, padded
-constexpr int kMaxCand = kRec - 1;
+constexpr int kMaxCand = 15;   // listed codewords per cell: 3 in the first word, 12 in the rest
 constexpr int kHdr = 8;        // floats per block header: mid0, mid1, inv0, inv1, Rc, valid, fingerprint
-constexpr int kThreads = 256;
+constexpr int kBuildThreads = 64;  // cells per build workgroup (one wave: per-lane polygons in LDS)
+constexpr int kPoly = 16;      // vertex capacity of a clipped cell polygon
 
-// Layout, head-major: per codebook head, its block headers (padded to 256 bytes) then its cells, so
-// one head's part of a per-KV-head grid is itself the grid of that head's codebook.
+// Layout, head-major: per codebook head, its block headers (padded to 256 bytes), the cells' first
+// words [nb][kG * kG] (uint32: count, three indices) and then the rest of their lists
+// [nb][kG * kG] (16 bytes: twelve indices, padded), so one head's part of a per-KV-head grid is
+// itself the grid of that head's codebook, and the words nearly every lookup reads (1 MiB per head
+// at 16 blocks) are contiguous; the rest is read only for lists longer than 3.
 inline int grid_heads(const ssq_encode_args& a) { return a.cent_sh == 0 ? 1 : a.num_kv_heads; }
 __host__ __device__ inline size_t grid_head_hdr_bytes(int nb) { return ((size_t)nb * kHdr * 4 + 255) & ~(size_t)255; }
-__host__ __device__ inline size_t grid_head_bytes(int nb) {
-    return grid_head_hdr_bytes(nb) + (size_t)nb * kG * kG * kRec;
-}
+__host__ __device__ inline size_t grid_head_bytes(int nb) { return grid_head_hdr_bytes(nb) + (size_t)nb * kG * kG * 20; }
 inline size_t grid_total_bytes(const ssq_encode_args& a) { return (size_t)grid_heads(a) * grid_head_bytes(a.n_blocks); }
 
 // ---------------------------------------------------------------------------
@@ -85,7 +94,9 @@ __global__ __launch_bounds__(64) void k_grid_header(const float* cent, int64_t c
         nrm = fmax(nrm, (double)(float)((double)c[2 * j] * c[2 * j] + (double)c[2 * j + 1] * c[2 * j + 1]));
     }
     float mid[2], inv[2];
-    bool valid = finite;
+    // a block whose codewords are all one point (a SunShape-Mixed codec's passthrough blocks hold
+    // zeros) gets no grid: every key ties every codeword, and the search scans them all
+    bool valid = finite && (lo[0] < hi[0] || lo[1] < hi[1]);
     for (int d = 0; d < 2; ++d) {
         const double mean = sum[d] / nc;
         double var = 0.0;
@@ -98,13 +109,16 @@ __global__ __launch_bounds__(64) void k_grid_header(const float* cent, int64_t c
         if (!(sc > fabs(m) * 0x1.0p-20)) sc = fmax(fabs(m) * 0x1.0p-20, 0x1.0p-60);
         mid[d] = (float)m;
         inv[d] = (float)(1.0 / sc);
-        valid = valid && isfinite(mid[d]) && isfinite(inv[d]) && inv[d] > 0.f;
+        // finite cells reach |x| <= |mid| + 65 sc; beyond 2^40 the reference's fp32 chain could
+        // overflow on keys there, which the list bound does not model: no grid
+        valid = valid && isfinite(mid[d]) && isfinite(inv[d]) && inv[d] > 0.f && fabs(m) + 65.0 * sc < 0x1.0p40;
     }
     float* out = reinterpret_cast<float*>(grid + (size_t)h * grid_head_bytes(nb)) + (int64_t)blk * kHdr;
     out[0] = mid[0]; out[1] = mid[1]; out[2] = inv[0]; out[3] = inv[1];
     uint32_t fp = cw_count_mix(nc);
     for (int j = 0; j < nc; ++j) fp ^= cw_mix(c[2 * j], c[2 * j + 1], j);
     out[4] = finite ? (float)(sqrt(nrm) * (1.0 + 0x1.0p-20)) : INFINITY;
+    valid = valid && out[4] < 0x1.0p40f;  // codewords up to 2^40: no fp32 overflow in the chain
     out[5] = valid ? 1.f : 0.f;
     out[6] = __uint_as_float(fp);
     out[7] = 0.f;
@@ -121,63 +135,200 @@ __device__ __forceinline__ double cell_edge(double t, double mid, double scale) 
     return mid + scale * (t / (1.0 - fabs(t)));
 }
 
-// one thread per cell
-__global__ __launch_bounds__(kThreads) void k_grid_cells(const float* cent, int64_t cent_sh, int nb, int nc,
-                                                         uint8_t* grid) {
+// one thread per cell, one wave per workgroup
+__global__ __launch_bounds__(kBuildThreads) void k_grid_cells(const float* cent, int64_t cent_sh, int nb, int nc,
+                                                              uint8_t* grid) {
     __shared__ double cw[256][2];
-    const int blk = blockIdx.y, h = blockIdx.z, tid = threadIdx.x;
-    const int cell = blockIdx.x * kThreads + tid;
+    // per-lane clipping polygons, two buffers: vertex v of buffer b of lane l at [b][v][l]
+    __shared__ double2 poly[2][kPoly][kBuildThreads];
+    const int blk = blockIdx.y, h = blockIdx.z, lane = threadIdx.x;
+    const int cell = blockIdx.x * kBuildThreads + lane;
     const float* c = cent + (int64_t)h * cent_sh + (int64_t)blk * nc * 2;
-    for (int j = tid; j < nc; j += kThreads) { cw[j][0] = c[2 * j]; cw[j][1] = c[2 * j + 1]; }
+    for (int j = lane; j < nc; j += kBuildThreads) { cw[j][0] = c[2 * j]; cw[j][1] = c[2 * j + 1]; }
     __syncthreads();
     uint8_t* head = grid + (size_t)h * grid_head_bytes(nb);
     const float* hd = reinterpret_cast<const float*>(head) + (int64_t)blk * kHdr;
-    uint8_t rec[kRec];
-#pragma unroll
-    for (int i = 0; i < kRec; ++i) rec[i] = 0;
-    if (hd[5] == 0.f) {
-        rec[0] = 255;
-    } else {
-        const int i0 = cell / kG, i1 = cell - (cell / kG) * kG;
-        const double w = 2.0 / kG, sc0 = 1.0 / (double)hd[2], sc1 = 1.0 / (double)hd[3];
-        const double a0 = cell_edge(-1.0 + w * (i0 - 0.001), hd[0], sc0);
-        const double b0 = cell_edge(-1.0 + w * (i0 + 1.001), hd[0], sc0);
-        const double a1 = cell_edge(-1.0 + w * (i1 - 0.001), hd[1], sc1);
-        const double b1 = cell_edge(-1.0 + w * (i1 + 1.001), hd[1], sc1);
+    uint32_t list[4] = {0u, 0u, 0u, 0u};  // byte i + 1: listed codeword i (byte 0: the count)
+    int found = 0;
+    bool scan_all = true;
+    const int i0 = cell / kG, i1 = cell - (cell / kG) * kG;
+    const double w = 2.0 / kG, sc0 = 1.0 / (double)hd[2], sc1 = 1.0 / (double)hd[3];
+    const double a0 = cell_edge(-1.0 + w * (i0 - 0.001), hd[0], sc0);
+    const double b0 = cell_edge(-1.0 + w * (i0 + 1.001), hd[0], sc0);
+    const double a1 = cell_edge(-1.0 + w * (i1 - 0.001), hd[1], sc1);
+    const double b1 = cell_edge(-1.0 + w * (i1 + 1.001), hd[1], sc1);
+    // end cells (unbounded) and codebooks with non-finite values: scan all
+    if (hd[5] != 0.f && isfinite(a0) && isfinite(b0) && isfinite(a1) && isfinite(b1)) {
+        scan_all = false;
         const double R2 = fmax(a0 * a0, b0 * b0) + fmax(a1 * a1, b1 * b1);
         const double R = sqrt(R2), Rc = hd[4];
-        double dmm = INFINITY;
-        for (int j = 0; j < nc; ++j) {
+        auto dmax2 = [&](int j) {
             const double dx = fmax(fabs(a0 - cw[j][0]), fabs(b0 - cw[j][0]));
             const double dy = fmax(fabs(a1 - cw[j][1]), fabs(b1 - cw[j][1]));
-            dmm = fmin(dmm, dx * dx + dy * dy);
+            return dx * dx + dy * dy;
+        };
+        auto dmin2 = [&](int j) {
+            const double dx = fmax(fmax(a0 - cw[j][0], cw[j][0] - b0), 0.0);
+            const double dy = fmax(fmax(a1 - cw[j][1], cw[j][1] - b1), 0.0);
+            return dx * dx + dy * dy;
+        };
+        double dmm = INFINITY;
+        int kstar = 0;
+        for (int j = 0; j < nc; ++j) {
+            const double d = dmax2(j);
+            if (d < dmm) { dmm = d; kstar = j; }
         }
         const double u = 0x1.0p-24, g = 1.001 * 4 * 0x1.0p-23;  // K = bd + 2 = 4
         const double S = (R + Rc) * (R + Rc), N2 = R2 + Rc * Rc;
-        const double M = 1.01 * (4.002 * u * N2 + 2.0002 * g * S + (dmm + 2.001 * u * N2 + g * S) * 0x1.0p-21);
-        const double bound = dmm + M;
-        int cnt = 0;
-        for (int j = 0; j < nc; ++j) {
-            const double dx = fmax(fmax(a0 - cw[j][0], cw[j][0] - b0), 0.0);
-            const double dy = fmax(fmax(a1 - cw[j][1], cw[j][1] - b1), 0.0);
-            if (dx * dx + dy * dy <= bound) {
-                if (cnt < kMaxCand) rec[1 + cnt] = (uint8_t)j;
-                ++cnt;
+        const double M0 = 1.01 * (4.002 * u * N2 + 2.0002 * g * S + (2.001 * u * N2 + g * S) * 0x1.0p-21);
+        const double Mk = 1.01 * 0x1.0p-21;  // M_jk = M0 + Mk D_k
+        const double bound = dmm + M0 + Mk * dmm;
+        // the pre-selected codewords as a bit set (j is the same for every lane: a uniform
+        // register index)
+        uint32_t pre[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        for (int j = 0; j < nc; ++j)
+            if (dmin2(j) <= bound) pre[j >> 5] |= 1u << (j & 31);
+        auto is_pre = [&](int j) { return (pre[j >> 5] >> (j & 31)) & 1u; };
+        // the codewords pre-selected in any cell of the wave: the only j and k worth a trip
+        uint32_t any_pre[8];
+#pragma unroll
+        for (int w8 = 0; w8 < 8; ++w8) {
+            uint32_t v = pre[w8];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) v |= (uint32_t)__shfl_xor((int)v, o);
+            any_pre[w8] = __builtin_amdgcn_readfirstlane(v);
+        }
+        // calls body(k) for every k of any_pre, ascending (a wave-uniform loop); body returns
+        // false to stop early
+        auto for_any_pre = [&](auto&& body) {
+            for (int w8 = 0; w8 < 8; ++w8)
+                for (uint32_t bits = any_pre[w8]; bits; bits &= bits - 1u)
+                    if (!body(w8 * 32 + __builtin_ctz(bits))) return;
+        };
+        // half-plane of j against k: |x - c_j|^2 - |x - c_k|^2 <= M_jk, i.e.
+        // 2 (c_k - c_j) . x <= M_jk + |c_k|^2 - |c_j|^2 =: rhs
+        auto halfplane = [&](int j, int k, double& nx, double& ny, double& rhs) {
+            nx = 2.0 * (cw[k][0] - cw[j][0]);
+            ny = 2.0 * (cw[k][1] - cw[j][1]);
+            const double nj = cw[j][0] * cw[j][0] + cw[j][1] * cw[j][1];
+            const double nk = cw[k][0] * cw[k][0] + cw[k][1] * cw[k][1];
+            rhs = M0 + Mk * dmax2(k) + nk - nj;
+        };
+        // k drops j outright when the half-plane misses all four corners of the cell
+        auto drops = [&](int k, int j) {
+            double nx, ny, rhs;
+            halfplane(j, k, nx, ny, rhs);
+            return fmin(nx * a0, nx * b0) + fmin(ny * a1, ny * b1) > rhs;
+        };
+        // Sutherland-Hodgman: the polygon in buffer src (n vertices) clipped to the half-plane into
+        // buffer 1 - src; returns the new count, 0 when nothing is left, -1 when it would exceed
+        // kPoly vertices (the caller then keeps j: listing one too many costs time only)
+        auto clip = [&](int src, int n, double nx, double ny, double rhs) {
+            int m = 0;
+            double2 P = poly[src][0][lane];
+            double f = nx * P.x + ny * P.y - rhs;
+            for (int i = 0; i < n; ++i) {
+                const double2 Q = poly[src][i + 1 == n ? 0 : i + 1][lane];
+                const double f2 = nx * Q.x + ny * Q.y - rhs;
+                if (f <= 0.0) {
+                    if (m < kPoly) poly[1 - src][m][lane] = P;
+                    ++m;
+                }
+                if ((f <= 0.0) != (f2 <= 0.0)) {
+                    const double t = f / (f - f2);
+                    if (m < kPoly) poly[1 - src][m][lane] = make_double2(P.x + t * (Q.x - P.x), P.y + t * (Q.y - P.y));
+                    ++m;
+                }
+                P = Q;
+                f = f2;
             }
+            return m > kPoly ? -1 : m;
+        };
+        auto byte_of = [](const uint32_t (&l)[4], int i) { return (int)((l[i >> 2] >> (8 * (i & 3))) & 255u); };
+        // the polygon of j: the cell, clipped by competitor k's half-plane (n vertices in buffer src)
+        auto start = [&](int& n, int& src) {
+            poly[0][0][lane] = make_double2(a0, a1);
+            poly[0][1][lane] = make_double2(b0, a1);
+            poly[0][2][lane] = make_double2(b0, b1);
+            poly[0][3][lane] = make_double2(a0, b1);
+            n = 4;
+            src = 0;
+        };
+        auto cut = [&](int& n, int& src, int j, int k) {
+            double nx, ny, rhs;
+            halfplane(j, k, nx, ny, rhs);
+            n = clip(src, n, nx, ny, rhs);
+            src ^= 1;
+        };
+        // 1. corner tests, the codeword nearest the whole cell first: they drop most candidates.
+        // The survivors (up to 16 kept in cand, bytes 0-15) hold every codeword that can win in the
+        // cell, so only their half-planes shape the winners' regions inside it.
+        uint32_t cand[4] = {0u, 0u, 0u, 0u};
+        int n_surv = 0;
+        constexpr int kMaxSurv = 64;  // more survivors (a degenerate codebook): the cell scans all
+        for_any_pre([&](int j) {
+            bool alive = n_surv <= kMaxSurv && is_pre(j) && !(j != kstar && drops(kstar, j));
+            if (__builtin_amdgcn_ballot_w64(alive))
+                for_any_pre([&](int k) {
+                    if (alive && k != j && k != kstar && is_pre(k) && drops(k, j)) alive = false;
+                    return __builtin_amdgcn_ballot_w64(alive) != 0;
+                });
+            if (alive) {
+                if (n_surv < 16) cand[n_surv >> 2] |= (uint32_t)j << (8 * (n_surv & 3));
+                ++n_surv;
+            }
+            return __builtin_amdgcn_ballot_w64(n_surv <= kMaxSurv) != 0;
+        });
+        auto keep = [&](int j) {
+            if (found < kMaxCand) list[(found + 1) >> 2] |= (uint32_t)j << (8 * ((found + 1) & 3));
+            ++found;
+        };
+        // 2. each survivor's polygon clipped by the other survivors' half-planes (kstar first)
+        for (int si = 0; si < 16 && __builtin_amdgcn_ballot_w64(si < n_surv && n_surv <= 16); ++si) {
+            const bool act = si < n_surv && n_surv <= 16;
+            const int j = byte_of(cand, si);
+            int n = 0, src = 0;
+            if (act) start(n, src);
+            if (act && n_surv > 1 && j != kstar) cut(n, src, j, kstar);
+            for (int ti = 0; ti < 16 && __builtin_amdgcn_ballot_w64(n > 0 && n_surv > 1 && ti < n_surv); ++ti) {
+                const int k = byte_of(cand, ti);
+                if (n > 0 && n_surv > 1 && ti < n_surv && k != j && k != kstar) cut(n, src, j, k);
+            }
+            if (act && n != 0) keep(j);  // left over, or out of vertex room (n < 0): listed
         }
-        // count 0 (non-finite values) or more than 31: scan all.  Bytes past the list repeat
-        // its last index, so evaluating them again cannot change the search's result.
-        if (cnt == 0 || cnt > kMaxCand) {
-            rec[0] = 255;
-        } else {
-            rec[0] = (uint8_t)cnt;
-            for (int i = 1 + cnt; i < kRec; ++i) rec[i] = rec[cnt];
+        // 17 to 64 survivors (rare): every pre-selected codeword against every pre-selected one,
+        // until the list overflows
+        const bool wide = n_surv > 16 && n_surv <= kMaxSurv;
+        if (__builtin_amdgcn_ballot_w64(wide)) {
+            for_any_pre([&](int j) {
+                const bool act = wide && is_pre(j) && found <= kMaxCand;
+                int n = 0, src = 0;
+                if (act) start(n, src);
+                if (act && j != kstar) cut(n, src, j, kstar);
+                if (__builtin_amdgcn_ballot_w64(n > 0))
+                    for_any_pre([&](int k) {
+                        if (n > 0 && k != j && k != kstar && is_pre(k)) cut(n, src, j, k);
+                        return __builtin_amdgcn_ballot_w64(n > 0) != 0;
+                    });
+                if (act && n != 0) keep(j);
+                return __builtin_amdgcn_ballot_w64(wide && found <= kMaxCand) != 0;
+            });
         }
+        if (found == 0 || found > kMaxCand || n_surv > kMaxSurv) scan_all = true;  // every codeword
     }
-    uint4* dst = reinterpret_cast<uint4*>(head + grid_head_hdr_bytes(nb) + ((int64_t)blk * kG * kG + cell) * kRec);
-    const uint32_t* w = reinterpret_cast<const uint32_t*>(rec);
-    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    // count and indices, bytes past the list repeating its last index (evaluating a codeword again
+    // cannot change the search's result); scan-all cells hold zeros
+    uint32_t wd[4] = {0u, 0u, 0u, 0u};
+    if (!scan_all) {
+        wd[0] = list[0] | (uint32_t)found;
+        wd[1] = list[1]; wd[2] = list[2]; wd[3] = list[3];
+        const uint32_t last = (wd[found >> 2] >> (8 * (found & 3))) & 255u;
+        for (int b = found + 1; b < 16; ++b) wd[b >> 2] |= last << (8 * (b & 3));
+    }
+    uint32_t* first = reinterpret_cast<uint32_t*>(head + grid_head_hdr_bytes(nb));
+    first[(int64_t)blk * kG * kG + cell] = wd[0];
+    uint4* rest = reinterpret_cast<uint4*>(head + grid_head_hdr_bytes(nb) + (size_t)nb * kG * kG * 4);
+    rest[(int64_t)blk * kG * kG + cell] = make_uint4(wd[1], wd[2], wd[3], 0u);
 }
 
 // ---------------------------------------------------------------------------
@@ -187,19 +338,27 @@ constexpr int kMaxLight = 128;
 
 struct GridParams {
     ssq_encode_args a;
-    const uint8_t* grid;       // head-major: headers then cells per codebook head
+    const uint8_t* grid;       // head-major: headers, first words, second words per codebook head
     int n_light;
     int row_codes;             // whole code rows in 16-byte stores
     int row_q;                 // 16-byte pieces of a key row when rows are read whole (else 0)
-    int fold;                  // short sequences: all sequences of a KV head share one key range (SsqKeyMap)
+    int fold;                  // short sequences: all sequences of a KV head share one key range
     int nlc;                   // light blocks per workgroup chunk (blockIdx.z picks the chunk)
+    int xcd_order;             // workgroup ids regrouped so each XCD takes a contiguous range
     uint8_t light[kMaxLight];  // light block ids, ascending
 };
 
+// A lane's staged code row: nb bytes padded to an odd number of 32-bit words, so the 64 lanes'
+// one-byte writes of a block land in 64 different LDS banks
+__host__ __device__ inline int code_row_bytes(int nb) {
+    const int w = (nb + 3) >> 2;
+    return 4 * (w | 1);
+}
 // LDS layout (bytes): cb [nl][256] float2 | cn [nl][256] float | hd [nl] float4 | poff [nl][4] int |
-// codes [waves][64][nb]
+// hinfo [nb] int4 | codes [waves][64][code_row_bytes(nb)]
 inline size_t grid_smem(int nl, int nb, int waves) {
-    return (size_t)nl * 256 * 12 + (size_t)nl * 16 + (size_t)nl * 16 + (size_t)nb * 16 + (size_t)waves * 64 * nb;
+    return (size_t)nl * 256 * 12 + (size_t)nl * 16 + (size_t)nl * 16 + (size_t)nb * 16 +
+           (size_t)waves * 64 * code_row_bytes(nb);
 }
 
 struct Cand {  // running first minimum of sqrt(max(d2, 0)) over ascending codeword indices
@@ -233,7 +392,6 @@ __device__ __forceinline__ void eval_val(float2 c, float cq, int j, float m0, fl
     st.bj = take ? j : st.bj;
 }
 
-
 // the reference's value for codeword (c, |c|^2), clamped at 0
 __device__ __forceinline__ float chain_val(float2 c, float cq, float m0, float m1, float xn) {
     float d2 = m0 * c.x;
@@ -263,14 +421,23 @@ __device__ __forceinline__ void next_val(float2 c, float cq, int j, float m0, fl
     st.bj = take ? j : st.bj;
 }
 
-template <bool ROWREG>
+template <bool ROWREG, int KDT>
 __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_encode_args& a = p.a;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int waves = blockDim.x >> 6;
-    const SsqKeyMap km(a, p.fold);
+    // Workgroup order.  The hardware deals consecutive workgroup ids to the 8 XCDs in turn; with
+    // xcd_order each XCD's ids are regrouped into one contiguous range of (KV head, sequence, key
+    // range) in KV-head-major order, so an XCD's L2 holds the cell words of one codebook head
+    // (per-KV-head codebooks) instead of all of them.
+    const uint32_t gx = gridDim.x, n_wg = gx * gridDim.y;
+    uint32_t id = blockIdx.x + gx * blockIdx.y;
+    if (p.xcd_order) id = (id & 7u) * (n_wg >> 3) + (id >> 3);
+    const int gxi = (int)(id % gx), gyi = (int)(id / gx);
+    const int nbat = p.fold ? 1 : a.batch;
+    const SsqKeyMap km(a, p.fold, gyi / nbat, gyi % nbat);
     const int kv = km.kv;
     const int l0 = blockIdx.z * p.nlc;  // this chunk's first light block
     const int nl = min(p.nlc, p.n_light - l0), nb = a.n_blocks, nc = a.n_centroids;
@@ -278,14 +445,15 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
 
     float2* cb = reinterpret_cast<float2*>(smem);                          // [nl][256]
     float* cn = reinterpret_cast<float*>(cb + nl * 256);                   // [nl][256]
-    float4* hd = reinterpret_cast<float4*>(cn + nl * 256);                 // [nl]: lo0, lo1, inv_h0, inv_h1
+    float4* hd = reinterpret_cast<float4*>(cn + nl * 256);                 // [nl]: mid0, mid1, inv0, inv1
     int* poff = reinterpret_cast<int*>(hd + nl);                           // [nl]: perm0, perm1, block id, 0
     // [heavy blocks]: the block's two dims in the key row, its id, its passthrough slot (chunk 0)
     int4* hinfo = reinterpret_cast<int4*>(poff + 4 * nl);
-    uint8_t* cs = reinterpret_cast<uint8_t*>(hinfo + nb) + wave * 64 * nb;  // this wave's code rows
+    const int crb = code_row_bytes(nb);
+    uint8_t* cs = reinterpret_cast<uint8_t*>(hinfo + nb) + wave * 64 * crb;  // this wave's code rows
 
     const int keys_wg = waves * 64;
-    const int key = blockIdx.x * keys_wg + wave * 64 + lane;  // this lane's key index
+    const int key = gxi * keys_wg + wave * 64 + lane;  // this lane's key index
     const bool live = key < km.n_keys;
     const int64_t krow = km.krow(a, live ? key : km.n_keys - 1);
     // this lane's key's output rows (code row, passthrough row), resolved before the staging so
@@ -305,13 +473,13 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
         }
     }
 
-    const int kdt = a.k_dtype;
+    constexpr int kdt = KDT;
     // ---- the key's permuted elements, issued before the staging below (they do not depend on
     // it; issued after its barrier they would add a memory round trip to the chain).  ROWREG: the
     // whole row (at most 128 bytes, 16-byte aligned) is loaded once with 16-byte loads into
-    // registers, and each block's two elements are picked out by a wave-uniform register index:
-    // one memory access per 16 bytes of key instead of one per element.  Otherwise each element
-    // is a load of its own, issued one block ahead of its use.
+    // registers, and each block's two elements are picked out by a wave-uniform register index
+    // (non-temporal loads were measured 20 % slower here).  Otherwise each element is a load of
+    // its own, issued one block ahead of its use.
     uint32_t row[32];
     if constexpr (ROWREG) {
         const uint4* src = reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(a.keys) +
@@ -356,8 +524,10 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) f ^= __shfl_xor(f, o);
         if (lane == 0) {
+            // no grid (or one built for another codebook): a NaN centre sends every key to cell
+            // (0, 0), an end cell, which scans all codewords
             const bool ok = hB.y != 0.f && (f ^ cw_count_mix(nc)) == __float_as_uint(hB.z);
-            hd[li] = ok ? hA : make_float4(0.f, 0.f, 0.f, 0.f);
+            hd[li] = ok ? hA : make_float4(__builtin_nanf(""), __builtin_nanf(""), 0.f, 0.f);
             poff[4 * li] = (int)pe0;
             poff[4 * li + 1] = (int)pe1;
             poff[4 * li + 2] = blk;  // kept in LDS: a kernel-argument array indexed in the loop
@@ -373,163 +543,151 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
             hinfo[h] = make_int4((int)perm[2 * blk], (int)perm[2 * blk + 1], blk, a.pt_dense ? blk : h);
         }
     }
-    for (int i = lane; i < 16 * nb; i += 64) reinterpret_cast<uint32_t*>(cs)[i] = 0u;  // heavy blocks: code 0
+    for (int i = lane; i < 16 * crb; i += 64) reinterpret_cast<uint32_t*>(cs)[i] = 0u;  // heavy blocks: code 0
     __syncthreads();
 
     const uint64_t hm0 = a.heavy_mask[0], hm1 = a.heavy_mask[1];
-    const uint8_t* cells = p.grid + (size_t)hsel * grid_head_bytes(nb) + grid_head_hdr_bytes(nb);
+    // the cells' first words of this head's table, and the rest of their lists
+    const uint32_t* words = reinterpret_cast<const uint32_t*>(p.grid + (size_t)hsel * grid_head_bytes(nb) +
+                                                              grid_head_hdr_bytes(nb));
+    const uint4* rest = reinterpret_cast<const uint4*>(words + (size_t)nb * kG * kG);
     // element e (wave-uniform) of the register row, as raw bits
     auto row_bits = [&](int e) -> uint32_t {
-        if (kdt == SSQ_F32) return row[e & 31];
-        const uint32_t w = row[(e >> 1) & 31];
-        return (e & 1) ? (w >> 16) : (w & 0xffffu);
+        if constexpr (KDT == SSQ_F32) {
+            return row[e & 31];
+        } else {
+            const uint32_t w = row[(e >> 1) & 31];
+            return (e & 1) ? (w >> 16) : (w & 0xffffu);
+        }
     };
-    // light block li's permuted element positions and block id, wave-uniform
-    auto block_info = [&](int li, int& e0, int& e1, int& blk) {
-        const int4 v = reinterpret_cast<const int4*>(poff)[li];
-        e0 = __builtin_amdgcn_readfirstlane(v.x);
-        e1 = __builtin_amdgcn_readfirstlane(v.y);
-        blk = __builtin_amdgcn_readfirstlane(v.z);
+    // the word index of (x0, x1)'s cell in block blk of this head's table under the block's map h
+    // (mid0, mid1, inv0, inv1).  t within rounding of +-1 may land one past the ends: the end cells
+    // take it.  |u| of 2^100 or more (whose reciprocal would leave the normal range) is +-1
+    // outright; a non-finite key element, or a block without a grid (NaN centre), gives NaN, and
+    // t = -1.  Either way the key lands in an end cell, whose record says "scan all".
+    auto map_t = [](float u) {
+        return fabsf(u) < 0x1.0p100f ? u * __builtin_amdgcn_rcpf(1.0f + fabsf(u)) : (u > 0.f ? 1.f : -1.f);
     };
-    // the byte offset of (x0, x1)'s cell record in block blk of this head's table; inside =
-    // false means "scan all" (the offset is then cell (0, 0)'s, a valid record)
-    auto cell_off = [&](int li, int blk, float x0, float x1, bool& inside) -> uint32_t {
-        const float4 h = hd[li];  // mid0, mid1, inv0, inv1 (inv 0: no grid)
+    auto cell_of = [&](const float4& h, int blk, float x0, float x1) -> uint32_t {
         const float u0 = (x0 - h.x) * h.z, u1 = (x1 - h.y) * h.w;
-        const float t0 = u0 * __builtin_amdgcn_rcpf(1.0f + fabsf(u0));
-        const float t1 = u1 * __builtin_amdgcn_rcpf(1.0f + fabsf(u1));
+        const float t0 = map_t(u0), t1 = map_t(u1);
         const float f0 = floorf((t0 + 1.0f) * (0.5f * kG)), f1 = floorf((t1 + 1.0f) * (0.5f * kG));
-        // t within rounding of +-1 may land one past the ends: the end cells take it.  NaN
-        // (a non-finite key element) has no cell
-        inside = h.z > 0.f && f0 >= -1.f && f0 <= (float)kG && f1 >= -1.f && f1 <= (float)kG;
-        const int c0 = inside ? min(max((int)f0, 0), kG - 1) : 0, c1 = inside ? min(max((int)f1, 0), kG - 1) : 0;
-        return (uint32_t)((blk * kG * kG + c0 * kG + c1) * kRec);
+        const int c0 = (int)fminf(fmaxf(f0, 0.f), (float)(kG - 1));  // fmaxf(NaN, 0) = 0
+        const int c1 = (int)fminf(fmaxf(f1, 0.f), (float)(kG - 1));
+        return (uint32_t)(blk * kG * kG + c0 * kG + c1);
     };
-    auto rec_lo = [&](uint32_t off) { return *reinterpret_cast<const uint4*>(cells + off); };
-    auto rec_hi = [&](uint32_t off) { return *reinterpret_cast<const uint4*>(cells + off + 16); };
-    // lists of 16 to 31 candidates continue in the record's second 16 bytes
-    auto needs_hi = [](const uint4& r, bool inside) {
-        const uint32_t c = r.x & 255u;
-        return inside && c > 15u && c != 255u;
-    };
-    const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
+    // a key row's element (element path), as raw bits
+    auto key_bits = [&](int e) { return ssq_load_bits(a.keys, KDT, krow + e); };
+    // the rest of a cell's list, loaded by every lane: lanes whose list ends in the first word read
+    // one 16-byte dummy that every such lane shares (an exact count of loads in flight lets each
+    // wait name the load it needs); the evaluation picks the padding for them
+    auto rest_raw = [&](uint32_t w0, uint32_t cell) -> uint4 { return rest[(w0 & 255u) > 3u ? cell : 0u]; };
 
-    // Software pipeline over the light blocks, one block apart: at trip li the loads of trip
-    // li - 1 have landed; the trip issues the second half of block li + 1's record (lanes
-    // with long lists only) and the first half of block li + 2's, then evaluates block li.
-    // Indices past the last block are clamped to it.  Stage names: *0 = block li, *1 = li + 1.
-    float xa0 = 0.f, xb0 = 0.f, xa1 = 0.f, xb1 = 0.f;
-    uint4 lo0 = zero4, lo1 = zero4, hi0 = zero4;
-    uint32_t off1 = 0;
-    bool in0 = false, in1 = false;
-    uint32_t ua = 0, ub = 0;  // element path: raw bits of block li + 2
-    auto elems = [&](int li, float& x0, float& x1, int& blk) {
-        int e0, e1;
-        block_info(li, e0, e1, blk);
-        if constexpr (ROWREG) {
-            x0 = ssq_bits_to_f32(row_bits(e0), kdt);
-            x1 = ssq_bits_to_f32(row_bits(e1), kdt);
-        } else {
-            x0 = ssq_load_elem(a.keys, kdt, krow + e0);
-            x1 = ssq_load_elem(a.keys, kdt, krow + e1);
-        }
-    };
-    auto issue_bits = [&](int li) {
-        if constexpr (!ROWREG) {
-            const int4 v = reinterpret_cast<const int4*>(poff)[li];
-            ua = ssq_load_bits(a.keys, kdt, krow + __builtin_amdgcn_readfirstlane(v.x));
-            ub = ssq_load_bits(a.keys, kdt, krow + __builtin_amdgcn_readfirstlane(v.y));
-        }
-    };
+    // Software pipeline over the light blocks.  Trip li evaluates block li while blocks li + 1 ..
+    // li + 3 are in flight:
+    //   1. block li + 3: its elements, cell, and the cell's first word (a load);
+    //   2. element path: the raw key elements of block li + 4 (loads);
+    //   3. block li + 2: its first word (loaded a trip ago) gives its count, and the rest of its
+    //      list is loaded: two trips before its use, since it is rarely in the L2;
+    //   4. block li is evaluated;
+    //   5. the LDS entries (element positions, block id, cell map) that the next trip's steps 1
+    //      and 2 use are read ahead.
+    // Loads are issued unconditionally, so each wait names the load it needs.  Indices past the
+    // last block are clamped to it.  Stage S holds block li + S.
+    const int4* pinfo = reinterpret_cast<const int4*>(poff);
+    auto clampb = [&](int l) { return min(l, nl - 1); };
+    float x0a = 0.f, x0b = 0.f, x1a = 0.f, x1b = 0.f, x2a = 0.f, x2b = 0.f;
+    uint32_t w0s = 0u, w1s = 0u, w2s = 0u, cell1 = 0u, cell2 = 0u;
+    uint4 r0s = make_uint4(0u, 0u, 0u, 0u), r1s = r0s;  // raw rests of stages 0 and 1
+    int blk0 = 0, blk1 = 0, blk2 = 0;
+    int4 pi3 = make_int4(0, 0, 0, 0), pi4 = pi3;  // LDS entries of blocks li + 3 (and li + 4: element path)
+    float4 hi3 = make_float4(0.f, 0.f, 0.f, 0.f);
+    uint32_t ua3 = 0u, ub3 = 0u;                  // element path: raw elements of block li + 3
     if (nl > 0) {
-        int blk;
-        elems(0, xa0, xb0, blk);
-        const uint32_t off0 = cell_off(0, blk, xa0, xb0, in0);
-        lo0 = rec_lo(off0);
-        elems(min(1, nl - 1), xa1, xb1, blk);
-        off1 = cell_off(min(1, nl - 1), blk, xa1, xb1, in1);
-        lo1 = rec_lo(off1);
-        issue_bits(min(2, nl - 1));
-        if (needs_hi(lo0, in0)) {
-            hi0 = rec_hi(off0);
-        } else {
-            const uint32_t pad = (lo0.w >> 24) * 0x01010101u;
-            hi0 = make_uint4(pad, pad, pad, pad);
+        float xa[3], xb[3];
+        uint32_t wv[3], cv[3];
+        int bv[3];
+#pragma unroll
+        for (int s3 = 0; s3 < 3; ++s3) {
+            const int l = clampb(s3);
+            const int4 v = pinfo[l];
+            const int e0 = __builtin_amdgcn_readfirstlane(v.x), e1 = __builtin_amdgcn_readfirstlane(v.y);
+            bv[s3] = __builtin_amdgcn_readfirstlane(v.z);
+            if constexpr (ROWREG) {
+                xa[s3] = ssq_bits_to_f32(row_bits(e0), KDT);
+                xb[s3] = ssq_bits_to_f32(row_bits(e1), KDT);
+            } else {
+                xa[s3] = ssq_bits_to_f32(key_bits(e0), KDT);
+                xb[s3] = ssq_bits_to_f32(key_bits(e1), KDT);
+            }
+            cv[s3] = cell_of(hd[l], bv[s3], xa[s3], xb[s3]);
+            wv[s3] = words[cv[s3]];
+        }
+        x0a = xa[0]; x0b = xb[0]; w0s = wv[0]; blk0 = bv[0];
+        x1a = xa[1]; x1b = xb[1]; w1s = wv[1]; blk1 = bv[1]; cell1 = cv[1];
+        x2a = xa[2]; x2b = xb[2]; w2s = wv[2]; blk2 = bv[2]; cell2 = cv[2];
+        r0s = rest_raw(w0s, cv[0]);
+        r1s = rest_raw(w1s, cell1);
+        pi3 = pinfo[clampb(3)];
+        hi3 = hd[clampb(3)];
+        if constexpr (!ROWREG) {
+            ua3 = key_bits(__builtin_amdgcn_readfirstlane(pi3.x));
+            ub3 = key_bits(__builtin_amdgcn_readfirstlane(pi3.y));
+            pi4 = pinfo[clampb(4)];
         }
     }
     for (int li = 0; li < nl; ++li) {
-        // ---- block li + 1: the record's second half where the list needs it
-        uint4 hi1;
-        if (needs_hi(lo1, in1)) {
-            hi1 = rec_hi(off1);
-        } else {  // the list ends in the first half: its padding continues
-            const uint32_t pad = (lo1.w >> 24) * 0x01010101u;
-            hi1 = make_uint4(pad, pad, pad, pad);
-        }
-        // ---- block li + 2: key elements, cell, the record's first half
-        const int l2 = min(li + 2, nl - 1);
-        float xa2, xb2;
-        int blk2;
+        // ---- 1. block li + 3: elements, cell, first word
+        const int blk3 = __builtin_amdgcn_readfirstlane(pi3.z);
+        float x3a, x3b;
         if constexpr (ROWREG) {
-            elems(l2, xa2, xb2, blk2);
+            x3a = ssq_bits_to_f32(row_bits(__builtin_amdgcn_readfirstlane(pi3.x)), KDT);
+            x3b = ssq_bits_to_f32(row_bits(__builtin_amdgcn_readfirstlane(pi3.y)), KDT);
         } else {
-            int e0, e1;
-            block_info(l2, e0, e1, blk2);
-            xa2 = ssq_bits_to_f32(ua, kdt);
-            xb2 = ssq_bits_to_f32(ub, kdt);
-            issue_bits(min(li + 3, nl - 1));
+            x3a = ssq_bits_to_f32(ua3, KDT);
+            x3b = ssq_bits_to_f32(ub3, KDT);
         }
-        bool in2;
-        const uint32_t off2 = cell_off(l2, blk2, xa2, xb2, in2);
-        const uint4 lo2 = rec_lo(off2);
+        const uint32_t cell3 = cell_of(hi3, blk3, x3a, x3b);
+        const uint32_t w3s = words[cell3];
+        // ---- 2. element path: block li + 4's raw elements
+        if constexpr (!ROWREG) {
+            ua3 = key_bits(__builtin_amdgcn_readfirstlane(pi4.x));
+            ub3 = key_bits(__builtin_amdgcn_readfirstlane(pi4.y));
+        }
+        // ---- 3. block li + 2: the rest of its list
+        const uint4 r2s = rest_raw(w2s, cell2);
 
-        // ---- candidates of block li
-        const float m0 = -2.0f * xa0, m1 = -2.0f * xb0;
-        const float xn = xa0 * xa0 + xb0 * xb0;
+        // ---- 4. block li: candidates 0-2 in bytes 1-3 of the first word, 3-14 in the rest
+        const float m0 = -2.0f * x0a, m1 = -2.0f * x0b;
+        const float xn = x0a * x0a + x0b * x0b;
         const float2* cbl = cb + li * 256;
         const float* cnl = cn + li * 256;
-        const uint32_t w[8] = {lo0.x, lo0.y, lo0.z, lo0.w, hi0.x, hi0.y, hi0.z, hi0.w};
-        const int cnt = (int)(w[0] & 255u);
-        const bool full = !in0 || cnt == 255;
-        const int lcnt = full ? 0 : cnt;
-        Cand st{INFINITY, -1};
-        // Record word g holds bytes 4g .. 4g+3, candidates 4g-1 .. 4g+2 (byte 0 is the count).
-        // The codewords of word g + 1 are read while word g is evaluated, so each word costs one
-        // LDS latency, not four.  The first candidate starts the running minimum; bytes past a
-        // lane's count repeat its last candidate and cannot win.  Lanes that scan all codewords
-        // start over below.
-        float2 cc[4];
-        float cq[4];
-        auto fetch = [&](uint32_t wd, int i0, float2 (&c)[4], float (&q)[4]) {
-#pragma unroll
-            for (int i = i0; i < 4; ++i) {
-                const int j = (int)((wd >> (8 * i)) & 255u);
-                c[i] = cbl[j];
-                q[i] = cnl[j];
-            }
+        const int cnt = (int)(w0s & 255u);  // 0: every codeword
+        const uint32_t pad = (w0s >> 24) * 0x01010101u;
+        const uint32_t rw[3] = {cnt > 3 ? r0s.x : pad, cnt > 3 ? r0s.y : pad, cnt > 3 ? r0s.z : pad};
+        auto cand = [&](int i) {  // i is a compile-time constant in the unrolled loop below
+            return (int)(i < 3 ? (w0s >> (8 * (i + 1))) & 255u : (rw[(i - 3) >> 2] >> (8 * ((i - 3) & 3))) & 255u);
         };
-        fetch(w[0], 1, cc, cq);
+        // The first candidate starts the running minimum; each trip reads the next candidate's
+        // codeword while it evaluates its own.  Bytes past a lane's count repeat its last
+        // candidate and cannot win.  Lanes that scan all codewords start over below.
+        float2 cc = cbl[cand(0)];
+        float cq = cnl[cand(0)];
+        float2 nc2 = cbl[cand(1)];
+        float nq = cnl[cand(1)];
+        Cand st{chain_val(cc, cq, m0, m1, xn), cand(0)};
 #pragma unroll
-        for (int g = 0; g < 8; ++g) {
-            if (!__builtin_amdgcn_ballot_w64((g == 0 ? 0 : 4 * g - 1) < lcnt)) break;  // the wave's lists are done
-            float2 nc2[4];
-            float nq[4];
-            if (g < 7) fetch(w[g + 1], 0, nc2, nq);
-#pragma unroll
-            for (int i = (g == 0 ? 1 : 0); i < 4; ++i) {
-                const int j = (int)((w[g] >> (8 * i)) & 255u);
-                if (g == 0 && i == 1) {
-                    st.bd = chain_val(cc[i], cq[i], m0, m1, xn);
-                    st.bj = j;
-                } else {
-                    next_val(cc[i], cq[i], j, m0, m1, xn, st);
-                }
+        for (int i = 1; i < kMaxCand; ++i) {
+            if (!__builtin_amdgcn_ballot_w64(i < cnt)) break;  // the wave's lists are done
+            cc = nc2;
+            cq = nq;
+            if (i + 1 < kMaxCand) {
+                nc2 = cbl[cand(i + 1)];
+                nq = cnl[cand(i + 1)];
             }
-            if (g < 7) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) { cc[i] = nc2[i]; cq[i] = nq[i]; }
-            }
+            next_val(cc, cq, cand(i), m0, m1, xn, st);
         }
+        const bool full = cnt == 0;
         if (__builtin_amdgcn_ballot_w64(full)) {  // rare: every codeword, 8 read ahead of their use
             if (full) st = Cand{INFINITY, -1};
             for (int j0 = 0; j0 < nc; j0 += 8) {
@@ -545,18 +703,28 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
                 for (int u = 0; u < 8; ++u) eval_val(c8[u], q8[u], j0 + u, m0, m1, xn, full && j0 + u < nc, st);
             }
         }
-        cs[lane * nb + __builtin_amdgcn_readfirstlane(poff[4 * li + 2])] = (uint8_t)(st.bj < 0 ? 0 : st.bj);
+        cs[lane * crb + blk0] = (uint8_t)(st.bj < 0 ? 0 : st.bj);
+
+        // ---- 5. the next trip's LDS entries
+        if constexpr (ROWREG) {
+            pi3 = pinfo[clampb(li + 4)];
+        } else {
+            pi3 = pi4;
+            pi4 = pinfo[clampb(li + 5)];
+        }
+        hi3 = hd[clampb(li + 4)];
 
         // ---- rotate the stages
-        xa0 = xa1; xb0 = xb1; lo0 = lo1; hi0 = hi1; in0 = in1;
-        xa1 = xa2; xb1 = xb2; lo1 = lo2; off1 = off2; in1 = in2;
+        x0a = x1a; x0b = x1b; w0s = w1s; r0s = r1s; blk0 = blk1;
+        x1a = x2a; x1b = x2b; w1s = w2s; r1s = r2s; blk1 = blk2; cell1 = cell2;
+        x2a = x3a; x2b = x3b; w2s = w3s; blk2 = blk3; cell2 = cell3;
     }
 
     // ---- outputs: code rows, heavy blocks' passthrough values
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int s_wave = blockIdx.x * keys_wg + wave * 64;
+    const int s_wave = gxi * keys_wg + wave * 64;
     if (p.row_codes) {
         const int pieces = nb >> 4;
         for (int e = lane; e < 64 * pieces; e += 64) {
@@ -567,18 +735,18 @@ __global__ __launch_bounds__(1024) void k_encode_grid(const GridParams p) {
             const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)((uint64_t)crow_k >> 32), m);
             const int64_t crow = (int64_t)(((uint64_t)hi << 32) | lo);
             if (i < km.n_keys) {
-                const uint32_t* src = reinterpret_cast<const uint32_t*>(cs + m * nb + 16 * q);
+                const uint32_t* src = reinterpret_cast<const uint32_t*>(cs + m * crb + 16 * q);
                 *reinterpret_cast<uint4*>(a.codes + crow + 16 * q) = make_uint4(src[0], src[1], src[2], src[3]);
             }
         }
     } else if (live && gridDim.z == 1) {  // every block's code (heavy blocks' 0 included)
         const int64_t crow = crow_k;
-        for (int blk = 0; blk < nb; ++blk) a.codes[crow + blk] = cs[lane * nb + blk];
+        for (int blk = 0; blk < nb; ++blk) a.codes[crow + blk] = cs[lane * crb + blk];
     } else if (live) {  // one chunk of several: its blocks' codes; chunk 0 also the heavy blocks' 0
         const int64_t crow = crow_k;
         for (int li = 0; li < nl; ++li) {
             const int blk = __builtin_amdgcn_readfirstlane(poff[4 * li + 2]);
-            a.codes[crow + blk] = cs[lane * nb + blk];
+            a.codes[crow + blk] = cs[lane * crb + blk];
         }
     }
     // chunk 0: the heavy blocks' values as the key holds them, and (with several chunks, whose
@@ -658,7 +826,8 @@ extern "C" int ssq_encode_grid_build(const ssq_encode_args* a, void* grid, uint6
     hipLaunchKernelGGL(k_grid_header, dim3(nb, nh), dim3(64), 0, st, a->cent, a->cent_sh, nb, nc, g);
     int rc = ssq_check_hip(hipGetLastError(), "k_grid_header launch");
     if (rc) return rc;
-    hipLaunchKernelGGL(k_grid_cells, dim3(kG * kG / kThreads, nb, nh), dim3(kThreads), 0, st, a->cent, a->cent_sh, nb,
+    hipLaunchKernelGGL(k_grid_cells, dim3(kG * kG / kBuildThreads, nb, nh), dim3(kBuildThreads), 0, st, a->cent,
+                       a->cent_sh, nb,
                        nc, g);
     return ssq_check_hip(hipGetLastError(), "k_grid_cells launch");
 }
@@ -708,14 +877,17 @@ int ssq_encode_grid_run(const ssq_encode_args* a, hipStream_t st) {
     const bool rowreg = row_bytes % 16 == 0 && row_bytes <= 128 && (uintptr_t)a->keys % 16 == 0 &&
                         (a->k_sb * esz) % 16 == 0 && (a->k_sh * esz) % 16 == 0 && (a->k_ss * esz) % 16 == 0;
     gp.row_q = rowreg ? (int)(row_bytes / 16) : 0;
-    const void* fn = rowreg ? reinterpret_cast<const void*>(k_encode_grid<true>)
-                            : reinterpret_cast<const void*>(k_encode_grid<false>);
-    const int rc = ssq_allow_lds(fn, 160 * 1024, "hipFuncSetAttribute(k_encode_grid)");
+    // one instantiation per (row path, key dtype)
+    using Kern = void (*)(const GridParams);
+    const int dsel = a->k_dtype == SSQ_F32 ? 0 : a->k_dtype == SSQ_BF16 ? 1 : 2;
+    static const Kern kerns[2][3] = {
+        {k_encode_grid<false, SSQ_F32>, k_encode_grid<false, SSQ_BF16>, k_encode_grid<false, SSQ_F16>},
+        {k_encode_grid<true, SSQ_F32>, k_encode_grid<true, SSQ_BF16>, k_encode_grid<true, SSQ_F16>}};
+    const Kern fn = kerns[rowreg ? 1 : 0][dsel];
+    const int rc = ssq_allow_lds(reinterpret_cast<const void*>(fn), 160 * 1024, "hipFuncSetAttribute(k_encode_grid)");
     if (rc) return rc;
     dim3 grid((unsigned)((n_keys + keys_wg - 1) / keys_wg), (unsigned)gy, chunks);
-    if (rowreg)
-        hipLaunchKernelGGL(k_encode_grid<true>, grid, dim3(waves * 64), smem, st, gp);
-    else
-        hipLaunchKernelGGL(k_encode_grid<false>, grid, dim3(waves * 64), smem, st, gp);
+    gp.xcd_order = ((uint64_t)grid.x * grid.y) % 8 == 0;
+    hipLaunchKernelGGL(fn, grid, dim3(waves * 64), smem, st, gp);
     return ssq_check_hip(hipGetLastError(), "k_encode_grid launch");
 }

@@ -91,9 +91,11 @@ __global__ __launch_bounds__(kWideThreads) void k_encode_wide(const WideEncodePa
         if (live) {
             for (int j = 0; j < n; ++j) {
                 const float* c = cb + (size_t)j * bd;
+                // clamped as the reference's sqrt(clamp_min(., 0)): NaN (a non-finite key) is 0
                 const float v = direct ? direct_dist2(x, c, bd) : mm_dist2(x, xn, c, cn[j], bd);
-                if (v < e_min) {
-                    e_min = v;
+                const float vc = v > 0.f ? v : 0.f;
+                if (vc < e_min) {
+                    e_min = vc;
                     const float f = dist_of(v);
                     if (f < f_best) {
                         f_best = f;

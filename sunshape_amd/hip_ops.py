@@ -495,7 +495,7 @@ def encode_grid_bytes(cent: torch.Tensor, num_kv_heads: int = 1) -> int:
 def encode_grid(cent: torch.Tensor, num_kv_heads: int = 1) -> torch.Tensor:
     """Search grid for encode(..., grid=) from codebooks [nb, nc, 2] or [Hkv, nb, nc, 2] (fp32).
 
-    Built once per codebook (a uint8 buffer of about 0.5 MiB per block and head); rebuild it
+    Built once per codebook (a uint8 buffer of 320 KiB per block and head); rebuild it
     whenever the codebook changes.  No counterpart in the reference: a search structure of this
     library, whose encode results equal the exhaustive ones bit for bit.
     """

@@ -1,5 +1,8 @@
-"""CPU checks of the grid-search encode's two claims (no GPU): a key always lies in the (widened)
-cell the search kernel computes for it, and a cell's list always holds the oracle's winner.
+"""CPU checks of the grid-search encode's claims (no GPU): a key always lies in the (widened) cell
+the search kernel computes for it; the builder's pre-selection (dmin(C, c_j)^2 <= min_k dmax(C, c_k)^2
++ M) holds the oracle's winner; and the winner meets every half-plane condition the builder clips a
+cell with (|x - c_j|^2 - |x - c_k|^2 <= M_jk for each pre-selected k) at the key itself, so the
+key lies in the winner's clipped polygon and the winner is listed.
 
 The grid is this library's search structure (no reference counterpart); the winner it must
 contain is the reference's first argmin (sunshape/codec.py:362-385), computed here by the
@@ -95,6 +98,54 @@ def cell_lists(c, mid, inv):
     return member.sum(2), member
 
 
+def bounded_cell(x, mid, inv):
+    """Per key: is its cell bounded (the unbounded end cells are scanned exhaustively)?"""
+    f0, f1 = kernel_cell(x[:, 0], mid[0], inv[0]), kernel_cell(x[:, 1], mid[1], inv[1])
+    a0, b0 = widened(f0, mid[0], inv[0])
+    a1, b1 = widened(f1, mid[1], inv[1])
+    return np.isfinite(a0) & np.isfinite(b0) & np.isfinite(a1) & np.isfinite(b1)
+
+
+def winner_in_polygon(c, mid, inv, x, win, slack=True):
+    """Per key: does the winner meet every half-plane condition of its cell's clipping at the
+    key itself, 2 (c_k - c_w) . x <= M_wk + |c_k|^2 - |c_w|^2 for each pre-selected competitor k
+    (fp64, as the builder)?  Keys in unbounded end cells (scanned exhaustively) count as held.
+    slack=False drops the rounding margin M (a planted mistake the far cluster case exposes)."""
+    f0, f1 = kernel_cell(x[:, 0], mid[0], inv[0]), kernel_cell(x[:, 1], mid[1], inv[1])
+    a0, b0 = widened(f0, mid[0], inv[0])
+    a1, b1 = widened(f1, mid[1], inv[1])
+    cd = c.astype(np.float64)
+    cx, cy = cd[None, :, 0], cd[None, :, 1]
+    A0, B0, A1, B1 = a0[:, None], b0[:, None], a1[:, None], b1[:, None]
+    ok = np.ones(len(x), dtype=bool)
+    fin = np.isfinite(a0) & np.isfinite(b0) & np.isfinite(a1) & np.isfinite(b1)
+    with np.errstate(invalid="ignore", over="ignore"):
+        dmax = np.maximum(np.abs(A0 - cx), np.abs(B0 - cx)) ** 2 + np.maximum(np.abs(A1 - cy), np.abs(B1 - cy)) ** 2
+        dmin = np.maximum(np.maximum(A0 - cx, cx - B0), 0) ** 2 + np.maximum(np.maximum(A1 - cy, cy - B1), 0) ** 2
+        dmm = dmax.min(1)
+        R2 = np.maximum(a0 ** 2, b0 ** 2) + np.maximum(a1 ** 2, b1 ** 2)
+        R = np.sqrt(R2)
+        nrm = np.float32(cd[:, 0] ** 2 + cd[:, 1] ** 2).max()
+        Rc = np.sqrt(np.float64(nrm)) * (1 + 2.0 ** -20)
+        S, N2 = (R + Rc) ** 2, R2 + Rc * Rc
+        M0 = 1.01 * (4.002 * U24 * N2 + 2.0002 * G * S + (2.001 * U24 * N2 + G * S) * 2.0 ** -21)
+        Mk = 1.01 * 2.0 ** -21
+        if not slack:
+            M0, Mk = 0.0 * M0, 0.0
+        bound = dmm + M0 + Mk * dmm
+        pre = dmin <= bound[:, None]
+        cw = cd[win]
+        nk = (cd ** 2).sum(1)[None, :]
+        nw = (cw ** 2).sum(1)[:, None]
+        xd = x.astype(np.float64)
+        lhs = 2 * ((cx - cw[:, 0:1]) * xd[:, 0:1] + (cy - cw[:, 1:2]) * xd[:, 1:2])
+        rhs = M0[:, None] + Mk * dmax + nk - nw
+        held = (lhs <= rhs) | ~pre
+    held[np.arange(len(x)), win] = True
+    ok = held.all(1) | ~fin
+    return ok
+
+
 @pytest.mark.parametrize("seed,nc", [(0, 256), (1, 256), (2, 64), (3, 17)])
 def test_cell_lists_hold_the_oracle_winner(seed, nc):
     """Random codebook (with duplicated and one-ulp-apart codewords); keys near Voronoi edges
@@ -120,10 +171,12 @@ def test_cell_lists_hold_the_oracle_winner(seed, nc):
     x = np.concatenate(keys).astype(np.float32)
     win = O.encode(x, np.arange(2), c[None])[0][:, 0].astype(np.int64)
     f0, f1 = kernel_cell(x[:, 0], mid[0], inv[0]), kernel_cell(x[:, 1], mid[1], inv[1])
-    used = (cnt[f0, f1] >= 1) & (cnt[f0, f1] <= 31)  # longer (or empty) lists scan every codeword
-    assert used.mean() > 0.9
+    bounded = bounded_cell(x, mid, inv)  # unbounded end cells: the builder scans them all
+    assert bounded.mean() > 0.9
     held = member[f0, f1, win]
-    assert held[used].all(), np.flatnonzero(used & ~held)[:10]
+    assert held[bounded].all(), np.flatnonzero(bounded & ~held)[:10]
+    poly = winner_in_polygon(c, mid, inv, x, win)
+    assert poly.all(), np.flatnonzero(~poly)[:10]
 
 
 def _lists_without_slack(c, mid, inv):
@@ -171,9 +224,14 @@ def test_rounding_slack_decides_lists_and_they_hold_the_winner(seed):
     assert (member != bare).any()
     win = O.encode(x, np.arange(2), c[None])[0][:, 0].astype(np.int64)
     f0, f1 = kernel_cell(x[:, 0], mid[0], inv[0]), kernel_cell(x[:, 1], mid[1], inv[1])
-    used = (cnt[f0, f1] >= 1) & (cnt[f0, f1] <= 31)
+    used = bounded_cell(x, mid, inv)
     assert used.mean() > 0.5
     held = member[f0, f1, win]
     assert held[used].all(), np.flatnonzero(used & ~held)[:10]
     only_with_slack = used & held & ~bare[f0, f1, win]
     assert only_with_slack.sum() > 100, int(only_with_slack.sum())
+    # the clipping's half-planes: the winner meets them all with the margin, and without it many
+    # winners would be cut from their own cell's list
+    assert winner_in_polygon(c, mid, inv, x, win).all()
+    cut = ~winner_in_polygon(c, mid, inv, x, win, slack=False)
+    assert cut.sum() > 100, int(cut.sum())

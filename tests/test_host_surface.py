@@ -325,7 +325,7 @@ def test_encode_grid_budget_is_process_wide_lru(monkeypatch):
     monkeypatch.setattr(C.hip_ops, "encode_grid", fake_grid)
     codecs = [SunShapeBlockCodec(head_dim=64, block_dim=2, num_kv_heads=2, device="cpu") for _ in range(32)]
     per = hip_ops.encode_grid_bytes(codecs[0].centroids)
-    assert 32 << 20 <= per < 33 << 20  # 0.5 MiB per head and block, plus block headers
+    assert 20 << 20 <= per < 21 << 20  # 320 KiB per head and block, plus block headers
     old = C._GRID_BUDGET[0]
     try:
         C.set_encode_grid_budget(4 * per + 100)
