@@ -273,10 +273,14 @@ def _time_surface(name, fn, n=100):
     return {"api": name, "calls": n, "host_us_per_call": host / n * 1e6, "wall_us_per_call": wall / n * 1e6}
 
 
-def _time_graph(name, fn, n=50):
-    """The same call captured once in a graph (torch.cuda.graph: HIP graphs, as a serving loop
-    captures its decode step) and replayed n times back to back: per-call time without the
-    host's launch cost, with the graph's outputs checked against an eager call."""
+def _time_graph(name, fn, n=50, per_graph=10):
+    """The same call captured in graphs (torch.cuda.graph: HIP graphs, as a serving loop captures
+    its decode step): one call per graph replayed n times back to back, and per_graph calls per
+    graph (a serving step captures every layer's call in one graph) replayed n / per_graph times.
+    Per-call GPU time from events and the host's time per replay; every replay's outputs are
+    checked against an eager call.  On this ROCm a graph launch costs the host 17-29 us, more than
+    a small call's two direct launches (4-6 us), so one-call replays of a ~20 us call are bound by
+    the host; a many-call graph amortises it."""
     import torch
 
     eager = fn().clone()
@@ -286,19 +290,29 @@ def _time_graph(name, fn, n=50):
         fn()
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        out = fn()
-    graph.replay()
-    torch.cuda.synchronize()
-    assert torch.equal(out, eager), "graph replay differs from the eager call"
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(n):
+    res = {"api": name}
+    for calls, key in ((1, "one_call"), (per_graph, f"{per_graph}_calls")):
+        graph = torch.cuda.CUDAGraph()
+        outs = []
+        with torch.cuda.graph(graph):
+            for _ in range(calls):
+                outs.append(fn())
         graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    return {"api": name, "replays": n, "us_per_call": start.elapsed_time(end) * 1e3 / n}
+        torch.cuda.synchronize()
+        assert all(torch.equal(o, eager) for o in outs), "graph replay differs from the eager call"
+        reps = max(1, n // calls)
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(reps):
+            graph.replay()
+        end.record()
+        host = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        res[key] = {"replays": reps, "us_per_call": start.elapsed_time(end) * 1e3 / (reps * calls),
+                    "host_us_per_replay": host * 1e6 / reps}
+    res["us_per_call"] = res["one_call"]["us_per_call"]
+    return res
 
 
 def _scores_workload(dev, kernel=0):
