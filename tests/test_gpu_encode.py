@@ -458,7 +458,8 @@ def test_encode_non_finite_keys_every_kernel(bd, nc, kernels, dtype):
     """Keys with NaN, +-inf and huge finite elements, whose distances are NaN (clamped to 0, so the
     first such codeword wins, as the reference's first argmin of a row holding NaN) or inf, and
     blocks whose codewords are all one point (zeros, as a SunShape-Mixed codec's passthrough
-    blocks hold, or another constant: the grid has no cells there): every encode kernel equals the
+    blocks hold, or another constant: the grid has no cells there), and a block of codewords near
+    1e13 (no grid either): every encode kernel equals the
     oracle bit for bit.  The grid sends such keys to its end cells, which scan every codeword; the
     MFMA screen makes every codeword a candidate of a key whose norm is not finite."""
     log(f"encode non-finite keys bd={bd} nc={nc} kernels={kernels} {dtype}")
@@ -469,7 +470,10 @@ def test_encode_non_finite_keys_every_kernel(bd, nc, kernels, dtype):
     cent = (rng.standard_normal((D // bd, nc, bd)) * sig[perm].reshape(D // bd, 1, bd)).astype(np.float32)
     cent[3] = 0.0
     cent[11] = np.float32(-1.25)
+    hb = D // bd - 2  # codewords past 2^40: such a block gets no grid (its fp32 chain could overflow)
+    cent[hb] *= np.float32(1e13)
     keys = (rng.standard_normal((1500, D)) * sig).astype(np.float32)
+    keys[:, perm[hb * bd:(hb + 1) * bd]] *= np.float32(1e13)
     bad = rng.integers(0, keys.size, 400)
     keys.reshape(-1)[bad] = rng.choice(np.array([np.nan, np.inf, -np.inf, 1e30, -1e30, 3e38], dtype=np.float32),
                                        bad.size)
