@@ -370,7 +370,56 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
                     }
                 }
             };
-            if (p.cw > 1) {  // 16- / 32-bit codes (code strides count elements of that width)
+            if (p.cw > 1 && bd <= 4) {
+                // 16- / 32-bit codes (code strides count elements of that width), codewords of at most
+                // 4 dims: per batch of 8 blocks the codes are loaded together, then the codewords,
+                // then the blocks are added in order (the arithmetic of add_block; two memory round
+                // trips per batch instead of two per block)
+                constexpr int kBat = 8;
+                for (int b0 = 0; b0 < nb; b0 += kBat) {
+                    uint32_t code[kBat];
+#pragma unroll
+                    for (int k = 0; k < kBat; ++k)
+                        code[k] = b0 + k < nb ? ssq_load_code(a.codes, p.cw, cofs + b0 + k) : 0u;
+                    float cv[kBat][4];
+#pragma unroll
+                    for (int k = 0; k < kBat; ++k) {
+                        const uint32_t cc = code[k] < (uint32_t)nc ? code[k] : (uint32_t)(nc - 1);
+                        const float* c = cent + ((int64_t)min(b0 + k, nb - 1) * nc + cc) * bd;
+                        if (bd == 4 && p.vec_cent) {  // one 16-byte load (the codebook is 16-byte aligned)
+                            const float4 v4 = *reinterpret_cast<const float4*>(c);
+                            cv[k][0] = v4.x; cv[k][1] = v4.y; cv[k][2] = v4.z; cv[k][3] = v4.w;
+                        } else if (bd == 2 && p.vec_cent) {
+                            const float2 v2 = *reinterpret_cast<const float2*>(c);
+                            cv[k][0] = v2.x; cv[k][1] = v2.y; cv[k][2] = 0.f; cv[k][3] = 0.f;
+                        } else {
+#pragma unroll
+                            for (int d = 0; d < 4; ++d) cv[k][d] = d < bd ? c[d] : 0.f;
+                        }
+                    }
+#pragma unroll
+                    for (int k = 0; k < kBat; ++k) {
+                        const int blk = b0 + k;
+                        if (blk >= nb) break;
+                        if (ssq_is_heavy(a.heavy_mask[0], a.heavy_mask[1], blk)) {
+                            add_block(blk, code[k]);
+                            continue;
+                        }
+                        float e_acc[RP];
+#pragma unroll
+                        for (int r = 0; r < RP; ++r) e_acc[r] = qp[r * D + blk * bd] * cv[k][0];
+#pragma unroll
+                        for (int d = 1; d < 4; ++d) {
+                            if (d < bd) {
+#pragma unroll
+                                for (int r = 0; r < RP; ++r) e_acc[r] = fmaf(qp[r * D + blk * bd + d], cv[k][d], e_acc[r]);
+                            }
+                        }
+#pragma unroll
+                        for (int r = 0; r < RP; ++r) s[r] += e_acc[r];
+                    }
+                }
+            } else if (p.cw > 1) {  // 16- / 32-bit codes, wider codewords: block by block
                 for (int blk = 0; blk < nb; ++blk) add_block(blk, ssq_load_code(a.codes, p.cw, cofs + blk));
             } else if (a.code_bits) {  // sub-byte codes packed into uint32 words
                 const uint32_t* w = reinterpret_cast<const uint32_t*>(a.codes) + cofs;
