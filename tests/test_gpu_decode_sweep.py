@@ -1,12 +1,15 @@
 """A seeded sweep of decode problems against the oracle: each case draws its layout (contiguous
 rows or vLLM-style pages with ragged lengths), head_dim, block_dim, codebook size (16 to 1,024
 codewords: byte and 16-bit codes), KV heads, query heads per KV head, new tokens, value dtype,
-passthrough blocks, additive mask (random with a finite bias, or causal) and split count, and
-compares output, lse and raw scores with the reference semantics
+passthrough blocks, additive mask (random with a finite bias, or causal), split count and code
+storage (bytes, 16-bit, or int32 words of 4 to 8 bits), and compares output, lse and raw scores
+with the reference semantics
 (sunshape/vllm_attn_backend.py:216-253 via the oracle) within the north-star tolerances.  The
 hand-picked tests cover each kernel's shapes; this sweep covers their combinations, on the
 planner's pick and on every kernel forced (1 generic, 2 MFMA LUT, 3 MFMA contiguous, 4
-4x4-MFMA scores) that accepts the problem: one that does not returns SSQ_ERR_UNSUPPORTED."""
+4x4-MFMA scores) that accepts the problem: one that does not returns SSQ_ERR_UNSUPPORTED.  On
+contiguous rows the scores-only entry point (gqa_scores) runs the same problem without values
+or mask, on every kernel that accepts it."""
 
 import math
 
@@ -35,6 +38,9 @@ def _draw(seed):
              vdt=torch.bfloat16 if rng.integers(0, 3) else torch.float16,
              n_heavy=int(rng.choice([0, 0, 1, 3])) if nb >= 4 else 0, splits=int(rng.choice([0, 0, 1, 3])))
     c["mask"] = ["none", "random", "causal"][int(rng.integers(0, 3))]
+    c["bits"] = 0  # sub-byte packed code words (int32) where the codebook fits
+    if c["nc"] <= 256 and rng.integers(0, 3) == 0:
+        c["bits"] = int(rng.integers(int(math.log2(c["nc"])), 9))
     return c
 
 
@@ -94,14 +100,20 @@ def test_decode_sweep_vs_oracle(seed):
                                                                                                         span)
         mask = mask.contiguous()
     scale = 1 / math.sqrt(D)
+    bits = c["bits"]
+
+    def dev_codes(x):
+        x = x.to(DEV)
+        return hip_ops.pack_codes(x, bits) if bits else x
+
     kw = dict(scale=scale, num_splits=c["splits"], heavy=heavy, mask=None if mask is None else mask.to(DEV),
-              return_lse=True, return_scores=True)
-    args = (q.to(DEV), codes.to(DEV), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+              return_lse=True, return_scores=True, code_bits=bits)
+    args = (q.to(DEV), dev_codes(codes), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
     if c["paged"]:
         cp, vp, pp, table = _paginate(codes, v, stored, lens, gen)
         kw.update(block_table=table.to(DEV), seq_lens=torch.tensor(lens, dtype=torch.int32).to(DEV),
                   pt=None if pp is None else pp.to(DEV))
-        args = (q.to(DEV), cp.to(DEV), vp.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+        args = (q.to(DEV), dev_codes(cp), vp.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
     else:
         kw.update(pt=None if stored is None else stored.to(DEV))
     runs = {}
@@ -112,6 +124,17 @@ def test_decode_sweep_vs_oracle(seed):
             assert e.status == N.SSQ_ERR_UNSUPPORTED and kernel >= 2, (kernel, e.status, str(e))
     log(f"kernels run: {sorted(runs)}")
     assert 0 in runs and 1 in runs
+    sruns = {}
+    if not c["paged"]:
+        for kernel in (0, 1, 2, 3, 4):
+            try:
+                sruns[kernel] = np_of(hip_ops.gqa_scores(args[0], args[1], args[3], args[4], scale=scale, heavy=heavy,
+                                                         pt=kw["pt"], code_bits=bits, num_splits=c["splits"],
+                                                         kernel=kernel))
+            except N.SunShapeKernelError as e:
+                assert e.status == N.SSQ_ERR_UNSUPPORTED and kernel >= 2, (kernel, e.status, str(e))
+        log(f"scores-only kernels run: {sorted(sruns)}")
+        assert 0 in sruns and 1 in sruns
     vdt = "bf16" if c["vdt"] == torch.bfloat16 else "f16"
     hv = np.array(heavy) if heavy else None
     for b in range(B):
@@ -124,6 +147,13 @@ def test_decode_sweep_vs_oracle(seed):
                                         return_scores=True)
         fin = np.isfinite(rs)
         rows = np.isfinite(rl)  # a row whose every score is masked has no defined output
+        if sruns:  # scores-only launches carry no mask
+            rs0 = rs if m is None else O.decode_attention(
+                q[b:b + 1].float().numpy(), codes[b:b + 1, :, :L].numpy().astype(np.int64),
+                v[b:b + 1, :, :L].float().numpy(), cb.centroids.numpy(), cb.perm.numpy(), scale, "bf16", vdt,
+                heavy=hv, pt_values=None if hv is None else ptd[b:b + 1, :, :L].numpy(), return_scores=True)[1]
+            for kernel, so in sruns.items():
+                assert_rel(so[b:b + 1], rs0, SCORE_TOL, f"scores-only kernel {kernel} b={b}")
         for kernel, (o, l, sc) in runs.items():
             what = f"kernel {kernel} b={b}"
             assert np.array_equal(np.isfinite(sc[b:b + 1, ..., :L]), fin), f"finite scores {what}"
