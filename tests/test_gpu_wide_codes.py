@@ -95,21 +95,25 @@ def test_wide_dequantize_and_scores(nc, bd):
     assert_rel(np_of(s), O.attention_scores(q.numpy(), idx.numpy(), cent.numpy(), perm.numpy()), SCORE_TOL, "scores")
 
 
-@pytest.mark.parametrize("B,Hq,Hkv,Lq,D,bd,nc,T,paged,mask,heavy_n,splits", [
-    (2, 32, 8, 1, 128, 4, 4096, 600, False, False, 0, 0),   # Llama-shaped layer at 3 bits/dim
-    (2, 14, 2, 1, 64, 2, 512, 777, False, True, 0, 3),      # Qwen-shaped, 512 codewords, a mask, 3 splits
-    (2, 16, 4, 2, 64, 4, 4096, 500, True, False, 2, 0),     # paged, two query tokens, passthrough blocks
-    (1, 8, 2, 1, 32, 2, 65536, 300, False, False, 0, 2),    # int32 indices
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,D,bd,nc,T,paged,mask,heavy_n,splits,Dv", [
+    (2, 32, 8, 1, 128, 4, 4096, 600, False, False, 0, 0, 128),   # Llama-shaped layer at 3 bits/dim
+    (2, 14, 2, 1, 64, 2, 512, 777, False, True, 0, 3, 64),       # Qwen-shaped, 512 codewords, a mask, 3 splits
+    (2, 16, 4, 2, 64, 4, 4096, 500, True, False, 2, 0, 64),      # paged, two query tokens, passthrough blocks
+    (1, 8, 2, 1, 32, 2, 65536, 300, False, False, 0, 2, 32),     # int32 indices
+    # 16-bit codes read 16 blocks per batch: 24 blocks end in a half batch, 8 blocks fill half of one
+    (2, 8, 2, 1, 96, 4, 4096, 333, False, True, 2, 3, 64),       # 24 blocks, mask, passthrough, 3 splits
+    (2, 8, 2, 2, 32, 4, 1024, 250, True, False, 0, 0, 32),       # 8 blocks, pages, two query tokens
+    (1, 4, 1, 1, 48, 2, 2048, 400, True, False, 2, 2, 64),       # 24 blocks of dim 2, pages, passthrough
 ])
-def test_wide_decode_vs_oracle(B, Hq, Hkv, Lq, D, bd, nc, T, paged, mask, heavy_n, splits):
+def test_wide_decode_vs_oracle(B, Hq, Hkv, Lq, D, bd, nc, T, paged, mask, heavy_n, splits, Dv):
     log(f"wide decode B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} D={D} bd={bd} nc={nc} T={T} paged={paged} mask={mask} "
-        f"heavy={heavy_n}")
+        f"heavy={heavy_n} Dv={Dv}")
     nb = D // bd
     cb = synthetic.make_codebook(Hkv, D, bd, 620 + nc + T, n_centroids=nc)
     g = torch.Generator().manual_seed(621 + T)
     q = torch.randn(B, Hq, Lq, D, generator=g).to(torch.bfloat16)
     idx = torch.randint(0, nc, (B, Hkv, T, nb), generator=g)
-    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, T, Dv, generator=g).to(torch.bfloat16)
     heavy = [i in (1, 3) for i in range(nb)] if heavy_n else None
     ptd = torch.zeros(B, Hkv, T, nb, bd)
     if heavy_n:
@@ -126,7 +130,7 @@ def test_wide_decode_vs_oracle(B, Hq, Hkv, Lq, D, bd, nc, T, paged, mask, heavy_
         n = (T + page - 1) // page
         table = torch.randperm(B * n, generator=g).view(B, n).to(torch.int32)
         cp = torch.zeros(B * n, Hkv, page, nb, dtype=codes.dtype)
-        vp = torch.zeros(B * n, Hkv, D, page, dtype=v.dtype)
+        vp = torch.zeros(B * n, Hkv, Dv, page, dtype=v.dtype)
         pp = torch.zeros(B * n, Hkv, page, 2, bd, dtype=torch.bfloat16)
         for b in range(B):
             for j in range(n):
