@@ -12,7 +12,7 @@ from HIP events on its own stream, the same launch's time with cold caches (a 1 
 before each), and a bounded CPU baseline: the reference's eager torch decode path on the
 host's cores (oracle/torch_eager.py).
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c4ct|c4ctbd2|c4ctg8|c4ctmix|c4mix|c4scores|c5encpro] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c4ct|c4ctbd2|c4ctg8|c4ctmix|c4mix|c4scores|c4w|c4ctw|c5encpro] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -40,7 +40,7 @@ def _args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "c4g8", "c4bd2", "c3p6",
-                                                     "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c4ctmix", "c4mix", "c4scores", "c5encpro",
+                                                     "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c4ctmix", "c4mix", "c4scores", "c4w", "c4ctw", "c5encpro",
                                                      "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -70,15 +70,19 @@ def _decode_workload(name, dev, kernel):
 
     heavy, pt = None, None
     nc, code_bits = 256, 0
-    if name in ("c4", "c4g8", "c4bd2", "c4p6", "c4mix", "c4scores"):
+    if name in ("c4", "c4g8", "c4bd2", "c4p6", "c4mix", "c4scores", "c4w"):
         # c4g8 / c4bd2: the config-4 layer with 64 query heads (8 per KV head) or at 4 bits/dim
         # (64 blocks of dim 2); their LUTs exceed the LDS, so they run the MFMA-scores kernel.
         # c4p6: the layer at 3 bits/dim (64 blocks of dim 2, 64 codewords), 6-bit codes packed
-        # five to an int32 word in the pages
+        # five to an int32 word in the pages; c4w: the layer at 3 bits/dim and block_dim 4, 4,096
+        # codewords per block with int16 codes (the reference fitter's codebook size for that
+        # setting, sunshape/hf.py:594)
         Hq = 64 if name == "c4g8" else 32
         bd = 2 if name in ("c4bd2", "c4p6") else 4
         if name == "c4p6":
             nc, code_bits = 64, 6
+        if name == "c4w":
+            nc = 4096
         p = synthetic.config4(dev, Hq=Hq, bd=bd, n_centroids=nc)
         if code_bits:
             p.tensors["code_words"] = hip_ops.pack_codes(p["code_pages"], code_bits)
@@ -93,15 +97,18 @@ def _decode_workload(name, dev, kernel):
             P = p["code_pages"].shape[0]
             pt = torch.randn(P, Hkv, 16, 4, bd, generator=gd, device=dev, dtype=torch.bfloat16)
             p.tensors["pt_pages"], p.tensors["heavy"] = pt, torch.tensor(heavy)
-    elif name in ("c4ct", "c4ctbd2", "c4ctg8", "c4ctmix"):
+    elif name in ("c4ct", "c4ctbd2", "c4ctg8", "c4ctmix", "c4ctw"):
         # the config-4 layer with the reference's contiguous rows (codes [B, Hkv, T, nb], V
         # [B, Hkv, T, D]) in place of pages; c4ctbd2 at the reference's default 4 bits/dim (64 blocks
         # of dim 2), c4ctg8 with 64 query heads (8 per KV head): the 4x4-MFMA-scores kernel;
-        # c4ctmix: SunShape-Mixed with 4 bf16 passthrough blocks of dim 4 (compact [B, Hkv, T, 4, 4])
+        # c4ctmix: SunShape-Mixed with 4 bf16 passthrough blocks of dim 4 (compact [B, Hkv, T, 4, 4]);
+        # c4ctw: 3 bits/dim at block_dim 4, 4,096 codewords per block, int16 codes
         B, Hkv, T, D = 64, 8, 32768, 128
         Hq = 64 if name == "c4ctg8" else 32
         bd = 2 if name == "c4ctbd2" else 4
-        p = synthetic.config4_contiguous(dev, Hq=Hq, bd=bd)
+        if name == "c4ctw":
+            nc = 4096
+        p = synthetic.config4_contiguous(dev, Hq=Hq, bd=bd, n_centroids=nc)
         paged = False
         if name == "c4ctmix":
             cb = synthetic.make_codebook(Hkv, D, bd, 104)
@@ -190,8 +197,8 @@ def _decode_workload(name, dev, kernel):
     torch.cuda.synchronize()
     assert torch.equal(out, ref), "timed launch differs from the checked Python-surface launch"
     keys = B * Hkv * T
-    code_bytes = codes.numel() * codes.element_size() if code_bits else B * Hkv * T * nb
-    algo_bytes = (code_bytes                       # uint8 codes (or packed words)
+    code_bytes = codes.numel() * codes.element_size() if code_bits or nc > 256 else B * Hkv * T * nb
+    algo_bytes = (code_bytes                       # uint8 codes (or packed words, or int16 codes)
                   + B * Hkv * T * Dv * 2           # bf16 V
                   + B * Hq * D * 2                 # bf16 q
                   + B * Hq * Dv * 2                # bf16 out
@@ -210,11 +217,13 @@ def _decode_workload(name, dev, kernel):
                         "c4ctmix": "C4 layer with contiguous rows, SunShape-Mixed: 28 VQ blocks + 4 bf16 passthrough blocks of dim 4",
                         "c4mix": "C4 paged, SunShape-Mixed: 28 VQ blocks + 4 bf16 passthrough blocks of dim 4",
                         "c4scores": "C4 paged fused decode that also writes the fp32 scores [B, Hq, 1, T]",
+                        "c4w": "C4 layer at 3 bits/dim: 4,096 codewords per block of dim 4, int16 codes, paged",
+                        "c4ctw": "C4 layer with contiguous rows at 3 bits/dim: 4,096 codewords per block of dim 4, int16 codes",
                         "c3": "C3 contiguous fused decode (Qwen2.5-0.5B layer, 4 bits/dim)",
                         "c5": "C5 SunShape-Mixed fused decode (config-5 keys: 28 VQ + 4 bf16 blocks of dim 2)",
                         "c3p6": "C3 layer at 3 bits/dim: 64 codewords, 6-bit codes packed in int32 words"}[name],
            "batch": B, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "context": T, "block_dim": bd,
-           "bits_per_dim": (code_bits or 8) / bd, "n_centroids": nc,
+           "bits_per_dim": (code_bits or math.log2(nc)) / bd, "n_centroids": nc,
            "layout": "paged16" if paged else "contiguous", "kernel": kernel}
     if code_bits:
         cfg["code_bits"] = code_bits
@@ -653,7 +662,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.workload in ("c4", "c3", "c5", "c4g8", "c4bd2", "c3p6", "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c4ctmix",
-                         "c4mix", "c4scores"):
+                         "c4mix", "c4scores", "c4w", "c4ctw"):
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
         step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev, args.kernel)

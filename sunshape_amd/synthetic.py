@@ -93,6 +93,17 @@ def config3(device="cpu", seed: int = 3, *, B: int = 16, T: int = 8192) -> Probl
     return _gqa("C3", device, seed, B=B, Hq=14, Hkv=2, D=64, bd=2, T=T, with_v=True)
 
 
+def _codes(n_centroids: int, shape, gen: torch.Generator, dev) -> torch.Tensor:
+    """Uniform codes: uint8 up to 256 codewords, else int16 holding each index's 16 bits (the
+    reference's compact index dtype, sunshape/codec.py:78-83)."""
+    if n_centroids <= 256:
+        return torch.randint(0, n_centroids, shape, generator=gen, device=dev, dtype=torch.uint8)
+    if n_centroids > 65536:
+        raise ValueError("synthetic codes take at most 65,536 codewords")
+    idx = torch.randint(0, n_centroids, shape, generator=gen, device=dev, dtype=torch.int32)
+    return torch.where(idx >= 32768, idx - 65536, idx).to(torch.int16)
+
+
 def config4(device="cpu", seed: int = 4, *, B: int = 64, T: int = 32768, page: int = 16,
             Hq: int = 32, Hkv: int = 8, D: int = 128, bd: int = 4, n_centroids: int = N_CENTROIDS) -> Problem:
     """Llama-3-8B-shaped paged decode at 2 bits/dim.
@@ -108,7 +119,7 @@ def config4(device="cpu", seed: int = 4, *, B: int = 64, T: int = 32768, page: i
     P = B * T // page
     table = torch.randperm(P, generator=g).to(torch.int32).view(B, T // page)
     gd = torch.Generator(device=dev).manual_seed(seed + 200)
-    code_pages = torch.randint(0, n_centroids, (P, Hkv, page, D // bd), generator=gd, device=dev, dtype=torch.uint8)
+    code_pages = _codes(n_centroids, (P, Hkv, page, D // bd), gd, dev)
     v_pages = torch.randn(P, Hkv, D, page, generator=gd, device=dev, dtype=torch.bfloat16)
     t = {"q": q.to(dev), "code_pages": code_pages, "v_pages": v_pages, "block_table": table.to(dev),
          "seq_lens": torch.full((B,), T, dtype=torch.int32, device=dev),
@@ -127,7 +138,7 @@ def config4_contiguous(device="cpu", seed: int = 104, *, B: int = 64, T: int = 3
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(B, Hq, 1, D, generator=g).to(torch.bfloat16)
     gd = torch.Generator(device=dev).manual_seed(seed + 100)
-    codes = torch.randint(0, n_centroids, (B, Hkv, T, D // bd), generator=gd, device=dev, dtype=torch.uint8)
+    codes = _codes(n_centroids, (B, Hkv, T, D // bd), gd, dev)
     v = torch.randn(B, Hkv, T, D, generator=gd, device=dev, dtype=torch.bfloat16)
     t = {"q": q.to(dev), "codes": codes, "v": v, "perm": cb.perm.to(dev), "centroids": cb.centroids.to(dev)}
     return Problem("C4ct", t, {"scale": 1.0 / math.sqrt(D), "keys": B * Hkv * T, "head_dim": D, "block_dim": bd,
