@@ -27,9 +27,11 @@ DEV = torch.device("cuda:0")
 PAGE = 16
 
 
-def _draw(seed):
+def _draw(seed, more=False):
+    """One problem; ``more`` widens it: head_dim 256, a value width apart from head_dim, up to six
+    new tokens (so more query rows than one workgroup takes), and masks given as broadcast views."""
     rng = np.random.default_rng(seed)
-    D = int(rng.choice([64, 128]))
+    D = int(rng.choice([64, 128, 256] if more else [64, 128]))
     bd = int(rng.choice([b for b in (1, 2, 4, 8) if D // b <= 64]))
     nb = D // bd
     c = dict(seed=seed, D=D, bd=bd, nb=nb, nc=int(rng.choice([16, 64, 256, 256, 1024])),
@@ -41,6 +43,11 @@ def _draw(seed):
     c["bits"] = 0  # sub-byte packed code words (int32) where the codebook fits
     if c["nc"] <= 256 and rng.integers(0, 3) == 0:
         c["bits"] = int(rng.integers(int(math.log2(c["nc"])), 9))
+    c["Dv"], c["mask_view"] = D, "full"
+    if more:
+        c["Dv"] = int(rng.choice([64, 128] + ([256] if D == 256 else [])))
+        c["Lq"] = int(rng.integers(1, 7))
+        c["mask_view"] = str(rng.choice(["full", "per_batch", "per_head"]))
     return c
 
 
@@ -68,16 +75,25 @@ def _paginate(codes, v, stored, lens, gen):
 
 @pytest.mark.parametrize("seed", list(range(900, 960)))
 def test_decode_sweep_vs_oracle(seed):
-    c = _draw(seed)
+    _sweep_case(_draw(seed))
+
+
+@pytest.mark.parametrize("seed", list(range(1000, 1040)))
+def test_decode_sweep_more_shapes_vs_oracle(seed):
+    _sweep_case(_draw(seed, more=True))
+
+
+def _sweep_case(c):
     log(f"decode sweep {c}")
-    D, bd, nb, nc, Hkv, G, B, Lq, T = (c[k] for k in ("D", "bd", "nb", "nc", "Hkv", "G", "B", "Lq", "T"))
+    D, bd, nb, nc, Hkv, G, B, Lq, T, Dv = (c[k] for k in ("D", "bd", "nb", "nc", "Hkv", "G", "B", "Lq", "T", "Dv"))
+    seed = c["seed"]
     Hq = Hkv * G
     gen = torch.Generator().manual_seed(seed)
     cb = synthetic.make_codebook(Hkv, D, bd, seed, n_centroids=nc)
     q = torch.randn(B, Hq, Lq, D, generator=gen).to(torch.bfloat16)
     codes = torch.randint(0, nc, (B, Hkv, T, nb), generator=gen, dtype=torch.int32)
     codes = codes.to(torch.uint8 if nc <= 256 else torch.int16)
-    v = torch.randn(B, Hkv, T, D, generator=gen).to(c["vdt"])
+    v = torch.randn(B, Hkv, T, Dv, generator=gen).to(c["vdt"])
     heavy = None
     ptd = stored = None
     if c["n_heavy"]:
@@ -90,7 +106,10 @@ def test_decode_sweep_vs_oracle(seed):
     span = ((T + PAGE - 1) // PAGE) * PAGE if c["paged"] else T
     mask = None
     if c["mask"] == "random":
-        mask = torch.where(torch.rand(B, Hq, Lq, span, generator=gen) < 0.2, float("-inf"), 0.0)
+        # per_batch / per_head: one mask row set per sequence or per query head, handed to the
+        # kernel as a broadcast (stride-0) view
+        mshape = {"full": (B, Hq), "per_batch": (B, 1), "per_head": (1, Hq)}[c["mask_view"]]
+        mask = torch.where(torch.rand(*mshape, Lq, span, generator=gen) < 0.2, float("-inf"), 0.0)
         mask[..., 0] = 0.0
         mask[0, 0] += -1.5
     elif c["mask"] == "causal":
@@ -106,8 +125,10 @@ def test_decode_sweep_vs_oracle(seed):
         x = x.to(DEV)
         return hip_ops.pack_codes(x, bits) if bits else x
 
-    kw = dict(scale=scale, num_splits=c["splits"], heavy=heavy, mask=None if mask is None else mask.to(DEV),
-              return_lse=True, return_scores=True, code_bits=bits)
+    dmask = None if mask is None else mask.to(DEV).expand(B, Hq, Lq, span)
+    mask = None if mask is None else mask.expand(B, Hq, Lq, span).contiguous()
+    kw = dict(scale=scale, num_splits=c["splits"], heavy=heavy, mask=dmask, return_lse=True, return_scores=True,
+              code_bits=bits)
     args = (q.to(DEV), dev_codes(codes), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
     if c["paged"]:
         cp, vp, pp, table = _paginate(codes, v, stored, lens, gen)
