@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import math
 import os
+import threading
 import weakref
 from collections import OrderedDict
 from typing import NamedTuple, Optional
@@ -32,6 +33,7 @@ from . import hip_ops
 # 1024 MiB); set_encode_grid_budget changes it at run time.
 _GRID_BUDGET = [int(os.environ.get("SUNSHAPE_AMD_GRID_BUDGET_MB", "1024")) << 20]
 _GRID_LRU: "OrderedDict[tuple, tuple]" = OrderedDict()  # (id(codec), slot) -> (weakref to codec, bytes)
+_GRID_LOCK = threading.RLock()  # the LRU and every codec's grid cache, across threads that encode
 
 
 def _grid_lru_live():
@@ -47,24 +49,27 @@ def _grid_lru_live():
 
 def encode_grid_footprint() -> int:
     """Device bytes held by cached encode search grids, over every codec of the process."""
-    return sum(n for *_, n in _grid_lru_live())
+    with _GRID_LOCK:
+        return sum(n for *_, n in _grid_lru_live())
 
 
 def set_encode_grid_budget(nbytes: int) -> None:
     """Process-wide byte budget for cached encode search grids; grids past it are dropped, least
     recently used first."""
-    _GRID_BUDGET[0] = int(nbytes)
-    _grid_lru_evict(_GRID_BUDGET[0])
+    with _GRID_LOCK:
+        _GRID_BUDGET[0] = int(nbytes)
+        _grid_lru_evict(_GRID_BUDGET[0])
 
 
 def _grid_lru_evict(limit: int) -> None:
-    used = encode_grid_footprint()
-    for key, codec, slot, nbytes in list(_grid_lru_live()):
-        if used <= limit:
-            break
-        codec._grid_cache.pop(slot, None)
-        del _GRID_LRU[key]
-        used -= nbytes
+    with _GRID_LOCK:
+        used = encode_grid_footprint()
+        for key, codec, slot, nbytes in list(_grid_lru_live()):
+            if used <= limit:
+                break
+            codec._grid_cache.pop(slot, None)
+            del _GRID_LRU[key]
+            used -= nbytes
 
 PERMUTATION_MODES = frozenset({"profileperm_baseline", "profileperm_localmetric_dsq", "profileperm_mixed_precision"})
 # modes whose fitted E is the identity (sunshape/codec.py:279-312): encode takes no metric
@@ -266,21 +271,22 @@ class SunShapeBlockCodec(torch.nn.Module):
         slot = (cent.data_ptr(), tuple(cent.shape))
         key = (buf.data_ptr(), buf._version)
         lru_key = (id(self), slot)
-        hit = self._grid_cache.get(slot)
-        if hit is not None and hit[0] == key:
-            if lru_key in _GRID_LRU:
-                _GRID_LRU.move_to_end(lru_key)
+        with _GRID_LOCK:
+            hit = self._grid_cache.get(slot)
+            if hit is not None and hit[0] == key:
+                if lru_key in _GRID_LRU:
+                    _GRID_LRU.move_to_end(lru_key)
+                return hit[1]
+            self._grid_cache.pop(slot, None)  # stale (the codebook changed): its bytes are freed below
+            _GRID_LRU.pop(lru_key, None)
+            nbytes = hip_ops.encode_grid_bytes(cent)
+            if nbytes > _GRID_BUDGET[0]:
+                return None  # larger than the whole budget: the exhaustive encode (same codes)
+            _grid_lru_evict(_GRID_BUDGET[0] - nbytes)
+            hit = (key, hip_ops.encode_grid(cent))
+            self._grid_cache[slot] = hit
+            _GRID_LRU[lru_key] = (weakref.ref(self), nbytes)
             return hit[1]
-        self._grid_cache.pop(slot, None)  # stale (the codebook changed): its bytes are freed below
-        _GRID_LRU.pop(lru_key, None)
-        nbytes = hip_ops.encode_grid_bytes(cent)
-        if nbytes > _GRID_BUDGET[0]:
-            return None  # larger than the whole budget: the exhaustive encode (same codes)
-        _grid_lru_evict(_GRID_BUDGET[0] - nbytes)
-        hit = (key, hip_ops.encode_grid(cent))
-        self._grid_cache[slot] = hit
-        _GRID_LRU[lru_key] = (weakref.ref(self), nbytes)
-        return hit[1]
 
     def rotation_matrix(self) -> torch.Tensor | None:
         """The rotated mode's dense R [D, D] (forward transform x @ R^T, inverse x @ R,

@@ -344,3 +344,46 @@ def test_encode_grid_budget_is_process_wide_lru(monkeypatch):
         assert codecs[5].encode_search_grid(codecs[5].centroids) is None and len(built) == 33
     finally:
         C.set_encode_grid_budget(old)
+
+
+def test_encode_grid_cache_from_threads(monkeypatch):
+    """Encodes on several threads share the grid budget: concurrent lookups, builds and evictions
+    leave every returned grid whole and the footprint within the budget.  Grids are host stand-ins
+    of the library's stated size."""
+    import random
+    import threading
+
+    from sunshape_amd import codec as C
+    from sunshape_amd import hip_ops
+
+    monkeypatch.setattr(C.hip_ops, "encode_grid",
+                        lambda cent, num_kv_heads=1: torch.empty(hip_ops.encode_grid_bytes(cent, num_kv_heads),
+                                                                 dtype=torch.uint8))
+    codecs = [SunShapeBlockCodec(head_dim=32, block_dim=2, device="cpu") for _ in range(12)]
+    per = hip_ops.encode_grid_bytes(codecs[0].centroids)
+    old = C._GRID_BUDGET[0]
+    errors, done = [], []
+
+    def work(seed):
+        try:
+            rng = random.Random(seed)
+            for _ in range(150):
+                c = codecs[rng.randrange(len(codecs))]
+                g = c.encode_search_grid(c.centroids)
+                assert g is not None and g.numel() == per
+            done.append(seed)
+        except Exception as e:  # reported below, with the thread's seed
+            errors.append((seed, repr(e)))
+
+    try:
+        C.set_encode_grid_budget(3 * per)
+        threads = [threading.Thread(target=work, args=(s,)) for s in range(8)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        assert not errors, errors
+        assert len(done) == 8  # every thread ran its lookups to the end
+        assert C.encode_grid_footprint() <= 3 * per
+    finally:
+        C.set_encode_grid_budget(old)
