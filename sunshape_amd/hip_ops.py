@@ -70,9 +70,10 @@ def transform_rows(x: torch.Tensor, mat: torch.Tensor, *, transpose: bool = Fals
     flat = flat if flat.stride(-1) == 1 else flat.contiguous()
     out = torch.empty((flat.shape[0], D), device=x.device, dtype=torch.float32)
     if flat.shape[0]:
-        N.check(N.lib().ssq_transform_rows(N.ptr(flat), N.dtype_code(flat.dtype), flat.stride(0), flat.shape[0], D,
-                                           1 if scale is not None else 0, float(scale or 0.0), N.ptr(mat),
-                                           1 if transpose else 0, N.ptr(out), out.stride(0), N.stream_of(x.device)))
+        with torch.cuda.device(x.device):  # the library reads the current device
+            N.check(N.lib().ssq_transform_rows(N.ptr(flat), N.dtype_code(flat.dtype), flat.stride(0), flat.shape[0], D,
+                                               1 if scale is not None else 0, float(scale or 0.0), N.ptr(mat),
+                                               1 if transpose else 0, N.ptr(out), out.stride(0), N.stream_of(x.device)))
     return out.view(*x.shape[:-1], D)
 
 
@@ -104,8 +105,9 @@ def lut_build(q: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, scale: Op
     out = torch.empty((R, nb, nc), device=q.device, dtype=torch.float32)
     if R == 0:
         return out
-    rc = N.lib().ssq_lut_build(N.ptr(q), N.dtype_code(q.dtype), q.stride(0), R, D, N.ptr(perm), N.ptr(cent), bd, nc,
-                               1 if scale is not None else 0, float(scale or 0.0), N.ptr(out), N.stream_of(q.device))
+    with torch.cuda.device(q.device):  # the library reads the current device
+        rc = N.lib().ssq_lut_build(N.ptr(q), N.dtype_code(q.dtype), q.stride(0), R, D, N.ptr(perm), N.ptr(cent), bd, nc,
+                                   1 if scale is not None else 0, float(scale or 0.0), N.ptr(out), N.stream_of(q.device))
     N.check(rc)
     return out
 
@@ -155,8 +157,9 @@ def pack_codes(codes: torch.Tensor, bits: int, *, check: bool = True) -> torch.T
     flat = codes.reshape(-1, nb)
     flat = flat if flat.stride(-1) == 1 else flat.contiguous()
     out = torch.empty((flat.shape[0], words_per_row(nb, bits)), device=codes.device, dtype=torch.int32)
-    N.check(N.lib().ssq_pack_codes(N.ptr(flat), flat.stride(0), flat.shape[0], nb, bits, N.ptr(out), out.stride(0),
-                                   N.stream_of(codes.device)))
+    with torch.cuda.device(codes.device):  # the library reads the current device
+        N.check(N.lib().ssq_pack_codes(N.ptr(flat), flat.stride(0), flat.shape[0], nb, bits, N.ptr(out), out.stride(0),
+                                       N.stream_of(codes.device)))
     return out.view(*codes.shape[:-1], out.shape[-1])
 
 
@@ -168,8 +171,9 @@ def unpack_codes(packed: torch.Tensor, n_blocks: int, bits: int) -> torch.Tensor
     flat = packed.reshape(-1, nw)
     flat = flat if flat.stride(-1) == 1 else flat.contiguous()
     out = torch.empty((flat.shape[0], n_blocks), device=packed.device, dtype=torch.uint8)
-    N.check(N.lib().ssq_unpack_codes(N.ptr(flat), flat.stride(0), flat.shape[0], n_blocks, bits, N.ptr(out),
-                                     out.stride(0), N.stream_of(packed.device)))
+    with torch.cuda.device(packed.device):  # the library reads the current device
+        N.check(N.lib().ssq_unpack_codes(N.ptr(flat), flat.stride(0), flat.shape[0], n_blocks, bits, N.ptr(out),
+                                         out.stride(0), N.stream_of(packed.device)))
     return out.view(*packed.shape[:-1], n_blocks)
 
 
@@ -507,7 +511,8 @@ def encode_grid(cent: torch.Tensor, num_kv_heads: int = 1) -> torch.Tensor:
     size = lib.ssq_encode_grid_bytes(ctypes.byref(a))
     _require(size > 0, "the encode grid serves block_dim 2 codebooks with at most 128 blocks of 256 codewords")
     grid = torch.empty(size, device=cent.device, dtype=torch.uint8)
-    N.check(lib.ssq_encode_grid_build(ctypes.byref(a), N.ptr(grid), size, N.stream_of(cent.device)))
+    with torch.cuda.device(cent.device):  # the library reads the current device
+        N.check(lib.ssq_encode_grid_build(ctypes.byref(a), N.ptr(grid), size, N.stream_of(cent.device)))
     return grid
 
 
@@ -536,8 +541,9 @@ def dequantize(codes: torch.Tensor, perm: torch.Tensor, cent: torch.Tensor, *,
     out = torch.empty((T, D), device=codes.device, dtype=torch.float32)
     (w0, w1), pt, ptd, ptdt = _pt_args(heavy, pt, pt_dense)
     hm = (ctypes.c_uint64 * 2)(w0, w1)
-    N.check(N.lib().ssq_dequantize(N.ptr(codes), codes.stride(0), T, N.ptr(perm), N.ptr(cent), D, bd, nc,
-                                   ctypes.cast(hm, ctypes.c_void_p), ptd, N.ptr(pt), ptdt,
-                                   0 if pt is None else pt.stride(0), N.ptr(out), out.stride(0),
-                                   N.stream_of(codes.device)))
+    with torch.cuda.device(codes.device):  # the library reads the current device
+        N.check(N.lib().ssq_dequantize(N.ptr(codes), codes.stride(0), T, N.ptr(perm), N.ptr(cent), D, bd, nc,
+                                       ctypes.cast(hm, ctypes.c_void_p), ptd, N.ptr(pt), ptdt,
+                                       0 if pt is None else pt.stride(0), N.ptr(out), out.stride(0),
+                                       N.stream_of(codes.device)))
     return out
