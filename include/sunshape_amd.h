@@ -5,7 +5,9 @@
  * pointer; strides are in ELEMENTS of the tensor's own dtype.  `stream` is a
  * hipStream_t passed as void* (NULL = the null stream).  All entry points are
  * asynchronous on `stream`, allocate no device memory, and return SSQ_OK or an
- * error code whose message ssq_last_error() returns (thread-local).
+ * error code whose message ssq_last_error() returns (thread-local).  Call them with
+ * the device that holds the tensors and `stream` current (hipSetDevice): launch
+ * planning reads that device's properties.
  *
  * Each argument struct starts with `struct_size`; the library rejects a caller
  * whose struct layout differs from this header (SSQ_ERR_ABI).
