@@ -604,3 +604,56 @@ def test_encode_grid_budget_32_layers():
         assert 120 << 20 <= C.encode_grid_footprint() <= 128 << 20  # the 6 most recent layers' grids
     finally:
         C.set_encode_grid_budget(old)
+
+
+@pytest.mark.parametrize("bd,kernel", [(4, 0), (2, 0), (2, 1)])
+def test_encode_args_replayed_as_a_serving_loop(bd, kernel):
+    """The append pattern of a serving loop: ssq_encode arguments built once with
+    hip_ops.encode_args (paged outputs through a slot mapping), each step's keys and slots written
+    into the tensors the arguments point into, and the call replayed through the C ABI.  Every
+    step's codes (and, with passthrough blocks, values) land in its slots, bit-exact with the
+    oracle's encode of that step's keys.  block_dim 2 runs the grid search with the codec's grid
+    (kernel 0) or the exact scan (kernel 1); block_dim 4 the MFMA encode."""
+    import ctypes
+
+    from sunshape_amd import _native as N
+
+    log(f"encode_args replay bd={bd} kernel={kernel}")
+    B, Hkv, D, page, P = 4, 2, 64, 16, 64
+    nb = D // bd
+    cb = synthetic.make_codebook(Hkv, D, bd, 150 + bd)
+    heavy = synthetic.heavy_blocks_by_sigma(cb.sigma, cb.perm, bd, 3).tolist() if bd == 2 else None
+    perm, cent = cb.perm.to(DEV), cb.centroids.to(DEV)
+    grid = hip_ops.encode_grid(cent, Hkv) if bd == 2 and kernel == 0 else None
+    code_pages = torch.zeros(P, Hkv, page, nb, dtype=torch.uint8, device=DEV)
+    pt_pages = None if heavy is None else torch.zeros(P, Hkv, page, sum(heavy), bd, dtype=torch.bfloat16, device=DEV)
+    table = torch.randperm(P, generator=torch.Generator().manual_seed(151))[:B * 4].view(B, 4)
+    g = torch.Generator().manual_seed(152)
+
+    def draw(step):
+        keys = (torch.randn(B, Hkv, 1, D, generator=g) * cb.sigma[:, None, :]).to(torch.bfloat16)
+        pos = 20 + step  # each sequence's next position
+        slots = (table[:, pos // page] * page + pos % page).view(B, 1).to(torch.int64)
+        return keys, slots
+
+    keys0, slots0 = draw(0)
+    a, _, _, keep = hip_ops.encode_args(keys0.to(DEV), perm, cent, heavy=heavy, codes_out=code_pages,
+                                        pt_out=pt_pages, slot_mapping=slots0.to(DEV), kernel=kernel, grid=grid)
+    keys_buf, slot_buf = keep[0], keep[5]
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    hv = None if heavy is None else np.array(heavy)
+    for step in range(6):
+        keys, slots = draw(step) if step else (keys0, slots0)
+        keys_buf.copy_(keys.to(DEV).view_as(keys_buf))
+        slot_buf.copy_(slots.to(DEV))
+        N.check(N.lib().ssq_encode(ctypes.byref(a), ctypes.c_void_p(stream)))
+        torch.cuda.synchronize()
+        pg, off = slots[:, 0] // page, slots[:, 0] % page
+        got = np_of(code_pages[pg.to(DEV), :, off.to(DEV)])  # [B, Hkv, nb]
+        for b in range(B):
+            for h in range(Hkv):
+                rc, rpt = O.encode(keys[b, h].float().numpy(), cb.perm[h].numpy(), cb.centroids[h].numpy(), hv)
+                assert np.array_equal(got[b, h], rc[0]), f"step {step} b={b} h={h}"
+                if hv is not None:
+                    gpt = np_of(pt_pages[int(pg[b]), h, int(off[b])].float())
+                    assert np.array_equal(gpt, rpt[0][hv]), f"passthrough step {step} b={b} h={h}"
