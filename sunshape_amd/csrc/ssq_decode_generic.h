@@ -88,15 +88,28 @@ struct VRaw8 {
     uint4 w[VT == SSQ_F32 ? 2 : 1];
 };
 
-template <int VT>
+typedef unsigned int ssq_v4u __attribute__((ext_vector_type(4)));
+
+// a 16-byte load that streams past the caches (NT) or a plain one
+template <bool NT>
+__device__ __forceinline__ uint4 ld16g(const void* p) {
+    if constexpr (NT) {
+        const ssq_v4u v = __builtin_nontemporal_load(reinterpret_cast<const ssq_v4u*>(p));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+        return *reinterpret_cast<const uint4*>(p);
+    }
+}
+
+template <int VT, bool NT = false>
 __device__ __forceinline__ VRaw8<VT> load_v8_raw(const void* base, int64_t elem_off) {
     VRaw8<VT> r;
     if constexpr (VT == SSQ_F32) {
-        const uint4* q = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(base) + elem_off);
-        r.w[0] = q[0];
-        r.w[1] = q[1];
+        const float* q = reinterpret_cast<const float*>(base) + elem_off;
+        r.w[0] = ld16g<NT>(q);
+        r.w[1] = ld16g<NT>(q + 4);
     } else {
-        r.w[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + elem_off);
+        r.w[0] = ld16g<NT>(reinterpret_cast<const uint16_t*>(base) + elem_off);
     }
     return r;
 }
@@ -423,7 +436,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
                 // last block gather codeword 0 of the last block and are not used.
                 constexpr int kBat = 16;
                 const uint4* cr4 = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.codes) + cofs);
-                uint4 cn0 = cr4[0], cn1 = nb > 8 ? cr4[1] : make_uint4(0u, 0u, 0u, 0u);
+                uint4 cn0 = ld16g<true>(cr4), cn1 = nb > 8 ? ld16g<true>(cr4 + 1) : make_uint4(0u, 0u, 0u, 0u);
                 for (int b0 = 0; b0 < nb; b0 += kBat) {
                     const uint32_t cw16[8] = {cn0.x, cn0.y, cn0.z, cn0.w, cn1.x, cn1.y, cn1.z, cn1.w};
                     float cv[kBat][4];
@@ -444,8 +457,8 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
 #pragma unroll
                     for (int k = 0; k < kBat; ++k) code_k[k] = (k & 1) ? (cw16[k >> 1] >> 16) : (cw16[k >> 1] & 0xFFFFu);
                     if (b0 + kBat < nb) {  // the next batch's codes
-                        cn0 = cr4[(b0 + kBat) >> 3];
-                        cn1 = b0 + kBat + 8 < nb ? cr4[((b0 + kBat) >> 3) + 1] : make_uint4(0u, 0u, 0u, 0u);
+                        cn0 = ld16g<true>(cr4 + ((b0 + kBat) >> 3));
+                        cn1 = b0 + kBat + 8 < nb ? ld16g<true>(cr4 + ((b0 + kBat) >> 3) + 1) : make_uint4(0u, 0u, 0u, 0u);
                     }
 #pragma unroll
                     for (int k = 0; k < kBat; ++k) {
@@ -666,7 +679,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
                     VRaw8<VT> raw[kVB];
 #pragma unroll
                     for (int k = 0; k < kVB; ++k)
-                        raw[k] = load_v8_raw<VT>(a.v, vbase + (int64_t)(t0 + min(tt0 + k * tpar, nt - 1)) * a.v_st);
+                        raw[k] = load_v8_raw<VT, W16>(a.v, vbase + (int64_t)(t0 + min(tt0 + k * tpar, nt - 1)) * a.v_st);
 #pragma unroll
                     for (int k = 0; k < kVB; ++k) {
                         const int tt = tt0 + k * tpar;
@@ -696,7 +709,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
                         const int tt = min(c0 + k * tpar, nchunks - 1) * 8;
                         const int t = t0 + tt;
                         const int off = t - (t / a.page_size) * a.page_size;
-                        raw[k] = load_v8_raw<VT>(a.v, (int64_t)pgl[tt] * a.v_sb + vhead + off);
+                        raw[k] = load_v8_raw<VT, W16>(a.v, (int64_t)pgl[tt] * a.v_sb + vhead + off);
                     }
 #pragma unroll
                     for (int k = 0; k < kVB; ++k) {
