@@ -430,7 +430,8 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
             if constexpr (W16) {
                 // 16 blocks per batch: their codes are two 16-byte pieces of the token's code row,
                 // loaded a batch ahead (issued after the current batch's gathers, so waiting for
-                // those never waits for them); the batch's codewords are gathered together, then
+                // those never waits for them) and non-temporal (the rows stream; the codebook
+                // keeps the L2); the batch's codewords are gathered together, then
                 // added in block order with add_block's arithmetic (FMA chain from the first
                 // product), so the scores equal the block-by-block path's.  Batch slots past the
                 // last block gather codeword 0 of the last block and are not used.
@@ -439,11 +440,13 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
                 uint4 cn0 = ld16g<true>(cr4), cn1 = nb > 8 ? ld16g<true>(cr4 + 1) : make_uint4(0u, 0u, 0u, 0u);
                 for (int b0 = 0; b0 < nb; b0 += kBat) {
                     const uint32_t cw16[8] = {cn0.x, cn0.y, cn0.z, cn0.w, cn1.x, cn1.y, cn1.z, cn1.w};
+                    uint32_t code_k[kBat];
+#pragma unroll
+                    for (int k = 0; k < kBat; ++k) code_k[k] = (k & 1) ? (cw16[k >> 1] >> 16) : (cw16[k >> 1] & 0xFFFFu);
                     float cv[kBat][4];
 #pragma unroll
                     for (int k = 0; k < kBat; ++k) {
-                        const uint32_t code = (k & 1) ? (cw16[k >> 1] >> 16) : (cw16[k >> 1] & 0xFFFFu);
-                        const uint32_t cc = code < (uint32_t)nc ? code : (uint32_t)(nc - 1);
+                        const uint32_t cc = code_k[k] < (uint32_t)nc ? code_k[k] : (uint32_t)(nc - 1);
                         const float* c = cent + ((int64_t)min(b0 + k, nb - 1) * nc + cc) * bd;
                         if (bd == 4) {
                             const float4 v4 = *reinterpret_cast<const float4*>(c);
@@ -453,9 +456,6 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
                             cv[k][0] = v2.x; cv[k][1] = v2.y; cv[k][2] = 0.f; cv[k][3] = 0.f;
                         }
                     }
-                    uint32_t code_k[kBat];
-#pragma unroll
-                    for (int k = 0; k < kBat; ++k) code_k[k] = (k & 1) ? (cw16[k >> 1] >> 16) : (cw16[k >> 1] & 0xFFFFu);
                     if (b0 + kBat < nb) {  // the next batch's codes
                         cn0 = ld16g<true>(cr4 + ((b0 + kBat) >> 3));
                         cn1 = b0 + kBat + 8 < nb ? ld16g<true>(cr4 + ((b0 + kBat) >> 3) + 1) : make_uint4(0u, 0u, 0u, 0u);
