@@ -20,12 +20,14 @@
 namespace {
 
 constexpr int kWideThreads = 256;
-constexpr int kWideStageFloats = 16384;  // 64 KiB per LDS stage: chunk * (bd + 1) floats
+constexpr int kWideStageFloats = 4096;  // 16 KiB per LDS stage: chunk * (bd + 1) floats
 
 struct WideEncodeParams {
     ssq_encode_args a;
-    int fold;   // short sequences: all sequences of a KV head share one key range (SsqKeyMap)
-    int chunk;  // codewords per LDS stage
+    int fold;     // short sequences: all sequences of a KV head share one key range (SsqKeyMap)
+    int chunk;    // codewords per LDS stage
+    int slices;   // lanes per (key, block), a power of two <= 64: lane s scans codewords s, s + slices, ...
+    int vec;      // 1: each codeword row is 4 * block_dim-byte aligned (vector staging loads)
 };
 
 __device__ __forceinline__ void store_code(uint8_t* codes, int width, int64_t i, uint32_t v) {
@@ -33,35 +35,53 @@ __device__ __forceinline__ void store_code(uint8_t* codes, int width, int64_t i,
     else reinterpret_cast<uint32_t*>(codes)[i] = v;
 }
 
+// BD: the block dim at compile time (1, 2, 4 or 8), or 0 for any other (read from the arguments).
+// A workgroup serves kWideThreads / slices keys of one block; the slices lanes of a key sit next
+// to each other in a wave and split the codebook between them (lane s takes codewords s,
+// s + slices, ... in ascending order), each finding the first minimum of its own codewords; the
+// lanes then combine (smaller distance, then smaller index), which gives the first argmin over
+// the whole codebook.
+template <int BD>
 __global__ __launch_bounds__(kWideThreads) void k_encode_wide(const WideEncodeParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_encode_args& a = p.a;
     const SsqKeyMap km(a, p.fold);
     const int kv = km.kv;
     const int blk = blockIdx.z;
-    const int bd = a.block_dim, nc = a.n_centroids, D = a.head_dim;
+    const int bd = BD ? BD : a.block_dim, nc = a.n_centroids, D = a.head_dim;
+    constexpr int kX = BD ? BD : 16;
     const int cw = ssq_code_width(nc);
     const bool heavy = ssq_is_heavy(a.heavy_mask[0], a.heavy_mask[1], blk);  // uniform per workgroup
-    const int i = blockIdx.x * kWideThreads + threadIdx.x;
+    const int S = p.slices;
+    const int sl = threadIdx.x & (S - 1);
+    const int i = blockIdx.x * (kWideThreads / S) + (int)(threadIdx.x / S);
     const bool live = i < km.n_keys;
     const float* met = a.metric ? a.metric + (int64_t)kv * a.metric_sh + (int64_t)blk * bd * D + blk * bd : nullptr;
-    float x[16];
+    float x[kX];
     int64_t crow = 0, prow = 0;
     if (live) {
         int b, s;
         km.bs(a, i, b, s);
         const int64_t kbase = (int64_t)b * a.k_sb + (int64_t)kv * a.k_sh + (int64_t)s * a.k_ss;
         const int64_t* perm = a.perm + (int64_t)kv * a.perm_sh + blk * bd;
-        for (int d = 0; d < bd; ++d) x[d] = ssq_load_elem(a.keys, a.k_dtype, kbase + perm[d]);
+#pragma unroll
+        for (int d = 0; d < kX; ++d)
+            if (d < bd) x[d] = ssq_load_elem(a.keys, a.k_dtype, kbase + perm[d]);
         out_rows(a, b, kv, s, crow, prow);
         if (heavy) {  // passthrough block: code 0, values copied (sunshape/codec.py:367-372)
-            store_code(a.codes, cw, crow + blk, 0u);
-            const int slot = a.pt_dense ? blk : heavy_ordinal(a.heavy_mask[0], a.heavy_mask[1], blk);
-            for (int d = 0; d < bd; ++d) ssq_store_elem(a.pt, a.pt_dtype, prow + (int64_t)slot * bd + d, x[d]);
+            if (sl == 0) {
+                store_code(a.codes, cw, crow + blk, 0u);
+                const int slot = a.pt_dense ? blk : heavy_ordinal(a.heavy_mask[0], a.heavy_mask[1], blk);
+                for (int d = 0; d < bd; ++d) ssq_store_elem(a.pt, a.pt_dtype, prow + (int64_t)slot * bd + d, x[d]);
+            }
         } else if (met) {
-            float y[16];
-            for (int k = 0; k < bd; ++k) y[k] = metric_row(met + (int64_t)k * D, x, bd);
-            for (int k = 0; k < bd; ++k) x[k] = y[k];
+            float y[kX];
+#pragma unroll
+            for (int k = 0; k < kX; ++k)
+                if (k < bd) y[k] = metric_row(met + (int64_t)k * D, x, bd);
+#pragma unroll
+            for (int k = 0; k < kX; ++k)
+                if (k < bd) x[k] = y[k];
         }
     }
     if (heavy) return;  // the whole workgroup: no barrier follows for it
@@ -77,19 +97,35 @@ __global__ __launch_bounds__(kWideThreads) void k_encode_wide(const WideEncodePa
         __syncthreads();  // the previous chunk's reads are done
         for (int e = threadIdx.x; e < n; e += kWideThreads) {
             const float* c = cent + (int64_t)(j0 + e) * bd;
-            float cv[16];
-            for (int d = 0; d < bd; ++d) cv[d] = c[d];
-            if (met) {
-                float y[16];
-                for (int k = 0; k < bd; ++k) y[k] = metric_row(met + (int64_t)k * D, cv, bd);
-                for (int k = 0; k < bd; ++k) cv[k] = y[k];
+            float cv[kX];
+            if (BD == 4 && p.vec) {
+                const float4 v = *reinterpret_cast<const float4*>(c);
+                cv[0] = v.x; cv[1] = v.y; cv[2] = v.z; cv[3] = v.w;
+            } else if (BD == 2 && p.vec) {
+                const float2 v = *reinterpret_cast<const float2*>(c);
+                cv[0] = v.x; cv[1] = v.y;
+            } else {
+#pragma unroll
+                for (int d = 0; d < kX; ++d)
+                    if (d < bd) cv[d] = c[d];
             }
-            for (int d = 0; d < bd; ++d) cb[(size_t)e * bd + d] = cv[d];
+            if (met) {
+                float y[kX];
+#pragma unroll
+                for (int k = 0; k < kX; ++k)
+                    if (k < bd) y[k] = metric_row(met + (int64_t)k * D, cv, bd);
+#pragma unroll
+                for (int k = 0; k < kX; ++k)
+                    if (k < bd) cv[k] = y[k];
+            }
+#pragma unroll
+            for (int d = 0; d < kX; ++d)
+                if (d < bd) cb[(size_t)e * bd + d] = cv[d];
             cn[e] = sq_norm(cv, bd);
         }
         __syncthreads();
         if (live) {
-            for (int j = 0; j < n; ++j) {
+            for (int j = sl; j < n; j += S) {
                 const float* c = cb + (size_t)j * bd;
                 // clamped as the reference's sqrt(clamp_min(., 0)): NaN (a non-finite key) is 0
                 const float v = direct ? direct_dist2(x, c, bd) : mm_dist2(x, xn, c, cn[j], bd);
@@ -105,7 +141,17 @@ __global__ __launch_bounds__(kWideThreads) void k_encode_wide(const WideEncodePa
             }
         }
     }
-    if (live) store_code(a.codes, cw, crow + blk, j_best);
+    // combine the key's lanes: the smaller distance, then the smaller index (every lane of a
+    // workgroup reaches this point; lanes of keys past the end carry infinities and are not stored)
+    for (int o = S >> 1; o > 0; o >>= 1) {
+        const float of = __shfl_xor(f_best, o);
+        const uint32_t oj = (uint32_t)__shfl_xor((int)j_best, o);
+        if (of < f_best || (of == f_best && oj < j_best)) {
+            f_best = of;
+            j_best = oj;
+        }
+    }
+    if (live && sl == 0) store_code(a.codes, cw, crow + blk, j_best);
 }
 
 }  // namespace
@@ -117,9 +163,25 @@ int ssq_encode_wide_run(const ssq_encode_args* a, hipStream_t st) {
     p.chunk = a->n_centroids < stage ? a->n_centroids : stage;
     p.fold = ssq_encode_fold(a, kWideThreads);
     const int64_t n_keys = p.fold ? (int64_t)a->batch * a->seq_len : a->seq_len;
-    dim3 grid((unsigned)((n_keys + kWideThreads - 1) / kWideThreads), p.fold ? a->num_kv_heads : a->batch * a->num_kv_heads,
+    const int64_t units = n_keys * (p.fold ? a->num_kv_heads : (int64_t)a->batch * a->num_kv_heads) * a->n_blocks;
+    // a launch with few (key, block) pairs (a decode step's append) splits each codebook scan over
+    // several lanes, up to about 2^18 lanes in all, and at least 16 codewords per lane
+    p.slices = 1;
+    while (p.slices < 64 && units * p.slices < (1 << 18) && p.slices * 16 <= a->n_centroids) p.slices *= 2;
+    const int bd = a->block_dim;
+    const int64_t row_bytes = (int64_t)bd * 4;
+    p.vec = ((uintptr_t)a->cent % (bd == 4 ? 16 : 8) == 0 && (a->cent_sh * 4) % (bd == 4 ? 16 : 8) == 0 &&
+             ((int64_t)a->n_centroids * row_bytes) % (bd == 4 ? 16 : 8) == 0) ? 1 : 0;
+    const int keys_wg = kWideThreads / p.slices;
+    dim3 grid((unsigned)((n_keys + keys_wg - 1) / keys_wg), p.fold ? a->num_kv_heads : a->batch * a->num_kv_heads,
               a->n_blocks);
-    const size_t smem = (size_t)p.chunk * (a->block_dim + 1) * sizeof(float);
-    hipLaunchKernelGGL(k_encode_wide, grid, dim3(kWideThreads), smem, st, p);
+    const size_t smem = (size_t)p.chunk * (bd + 1) * sizeof(float);
+    switch (bd) {
+        case 1: hipLaunchKernelGGL(k_encode_wide<1>, grid, dim3(kWideThreads), smem, st, p); break;
+        case 2: hipLaunchKernelGGL(k_encode_wide<2>, grid, dim3(kWideThreads), smem, st, p); break;
+        case 4: hipLaunchKernelGGL(k_encode_wide<4>, grid, dim3(kWideThreads), smem, st, p); break;
+        case 8: hipLaunchKernelGGL(k_encode_wide<8>, grid, dim3(kWideThreads), smem, st, p); break;
+        default: hipLaunchKernelGGL(k_encode_wide<0>, grid, dim3(kWideThreads), smem, st, p); break;
+    }
     return ssq_check_hip(hipGetLastError(), "k_encode_wide launch");
 }
