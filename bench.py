@@ -12,7 +12,7 @@ from HIP events on its own stream, the same launch's time with cold caches (a 1 
 before each), and a bounded CPU baseline: the reference's eager torch decode path on the
 host's cores (oracle/torch_eager.py).
 
-  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c4ct|c4ctbd2|c4ctg8|c4ctmix|c4mix|c4scores|c4w|c4ctw|c5encpro] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--workload c4|c3|c2|c5|c5enc|c4append|c5append|c4g8|c4bd2|c3p6|c4p6|c4ct|c4ctbd2|c4ctg8|c4ctmix|c4mix|c4scores|c4w|c4ctw|c4appendw|c5encpro] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -40,7 +40,7 @@ def _args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c4", choices=["c4", "c3", "c2", "c5", "c5enc", "c4append", "c5append", "c4g8", "c4bd2", "c3p6",
-                                                     "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c4ctmix", "c4mix", "c4scores", "c4w", "c4ctw", "c5encpro",
+                                                     "c4p6", "c4ct", "c4ctbd2", "c4ctg8", "c4ctmix", "c4mix", "c4scores", "c4w", "c4ctw", "c4appendw", "c5encpro",
                                                      "copycal"])
     ap.add_argument("--kernel", type=int, default=0, help="0 auto, 1 generic, 2 MFMA")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -424,7 +424,8 @@ def _append_workload(name, dev, kernel):
     """One serving step's append: the new key of every (sequence, KV head) encoded into its slot of
     the 16-token pages.  c4append: the config-4 codec (64 x 8 keys, 32 blocks of dim 4, per-head
     codebooks, the MFMA encode); c5append: the config-5 codec (16 x 2 keys, 28 VQ blocks of dim 2 +
-    4 passthrough, the grid search with the codec's grid)."""
+    4 passthrough, the grid search with the codec's grid); c4appendw: the config-4 step with a
+    4,096-codeword codec of dim 4 (3 bits/dim, int16 codes; the exhaustive scan split over lanes)."""
     import torch
 
     from sunshape_amd import hip_ops, synthetic
@@ -432,8 +433,10 @@ def _append_workload(name, dev, kernel):
     page = 16
     g = torch.Generator(device=dev).manual_seed(44)
     heavy, grid, pt_pages = None, None, None
-    if name == "c4append":
-        p = synthetic.config4(dev, T=256)
+    nc = 256
+    if name in ("c4append", "c4appendw"):
+        nc = 4096 if name == "c4appendw" else 256
+        p = synthetic.config4(dev, T=256, n_centroids=nc)
         B, Hkv, D, bd, T = 64, 8, 128, 4, 256
         bt = p["block_table"]
         perm, cent = p["perm"], p["centroids"]
@@ -450,10 +453,10 @@ def _append_workload(name, dev, kernel):
             grid = hip_ops.encode_grid(cent)
         pt_pages = torch.zeros(B * T // page, Hkv, page, sum(heavy), bd, device=dev, dtype=torch.bfloat16)
     nb = D // bd
-    code_pages = torch.zeros(B * T // page, Hkv, page, nb, device=dev, dtype=torch.uint8)
+    code_pages = torch.zeros(B * T // page, Hkv, page, nb, device=dev, dtype=hip_ops.index_dtype(nc))
     pos = T - 1  # the step's token lands in the last slot of each sequence's last page
     slots = (bt[:, pos // page].to(torch.int64) * page + pos % page).view(B, 1).contiguous()
-    ref, _ = hip_ops.encode(keys_t, perm, cent, heavy=heavy, kernel=2 if bd == 4 else 1)
+    ref, _ = hip_ops.encode(keys_t, perm, cent, heavy=heavy, kernel=2 if bd == 4 and nc == 256 else 1)
 
     # the timed loop replays one prebuilt C-ABI call: at a few microseconds per launch, the
     # Python wrapper's checks would otherwise be what the events measure
@@ -476,12 +479,15 @@ def _append_workload(name, dev, kernel):
     assert torch.equal(got, ref[:, :, 0]), "paged append differs from the contiguous encode"
     n = B * Hkv
     nlight = nb - (sum(heavy) if heavy else 0)
-    algo = n * D * 2 + n * nb + Hkv * nlight * 256 * bd * 4 + Hkv * D * 8 + B * 8 + n * (nb - nlight) * bd * 2
+    cbytes = 1 if nc <= 256 else 2
+    algo = n * D * 2 + n * nb * cbytes + Hkv * nlight * nc * bd * 4 + Hkv * D * 8 + B * 8 + n * (nb - nlight) * bd * 2
     cfg = {"workload": {"c4append": "F1 paged append, one decode step at the config-4 shape "
                                     "(64 x 8 keys, 32 blocks of dim 4)",
                         "c5append": "F1 paged append, one decode step with the config-5 codec "
-                                    "(16 x 2 keys, 28 VQ blocks of dim 2 + 4 bf16 passthrough)"}[name],
-           "keys": n, "head_dim": D, "block_dim": bd, "page_size": page, "kernel": kernel,
+                                    "(16 x 2 keys, 28 VQ blocks of dim 2 + 4 bf16 passthrough)",
+                        "c4appendw": "F1 paged append, one decode step at the config-4 shape with a 4,096-codeword "
+                                     "codec (64 x 8 keys, 32 blocks of dim 4, int16 codes)"}[name],
+           "keys": n, "head_dim": D, "block_dim": bd, "n_centroids": nc, "page_size": page, "kernel": kernel,
            "search": "grid" if grid is not None else "exhaustive"}
     return step, n, algo, cfg, None, "ssq_encode"
 
@@ -666,7 +672,7 @@ def main():
         step, keys, algo_bytes, cfg, unit_data, kname = _decode_workload(args.workload, dev, args.kernel)
     elif args.workload == "c2":
         step, keys, algo_bytes, cfg, unit_data, kname = _scores_workload(dev, args.kernel)
-    elif args.workload in ("c4append", "c5append"):
+    elif args.workload in ("c4append", "c5append", "c4appendw"):
         step, keys, algo_bytes, cfg, unit_data, kname = _append_workload(args.workload, dev, args.kernel)
     elif args.workload == "copycal":
         step, keys, algo_bytes, cfg, unit_data, kname = _copy_workload(dev)
