@@ -9,10 +9,10 @@
 // norms.  The index is the first argmin of the reference's fp32 distance, sqrt(max(d2, 0)) with d2
 // in torch.cdist's mm formulation (or its direct one), in one pass: a correctly rounded sqrt is
 // non-decreasing, so a codeword whose pre-sqrt value is not below the smallest seen so far cannot
-// have a strictly smaller distance, and only new minima take a sqrt.  The first index reaching the
-// final minimum distance was a new minimum when it was reached (every earlier index has a larger
-// distance, hence a larger pre-sqrt value), and a later index with an equal distance does not
-// replace it (strict comparison).
+// have a strictly smaller distance, and only new pre-sqrt minima are examined further (take_min).
+// The first index reaching the final minimum distance was a new minimum when it was reached (every
+// earlier index has a larger distance, hence a larger pre-sqrt value), and a later index with an
+// equal distance does not replace it (strict comparison).
 #include "ssq_encode_math.h"
 
 #include <math.h>
@@ -33,6 +33,60 @@ struct WideEncodeParams {
 __device__ __forceinline__ void store_code(uint8_t* codes, int width, int64_t i, uint32_t v) {
     if (width == 2) reinterpret_cast<uint16_t*>(codes)[i] = (uint16_t)v;
     else reinterpret_cast<uint32_t*>(codes)[i] = v;
+}
+
+// one codeword's pre-sqrt distance v (not yet clamped)
+template <int BD, bool MM>
+__device__ __forceinline__ float stage_dist(const float* x, float xn, const float* cb, const float* cn, int j, int bd) {
+    const int w = BD ? BD : bd;
+    const float* c = cb + (size_t)j * w;
+    return MM ? mm_dist2(x, xn, c, cn[j], w) : direct_dist2(x, c, w);
+}
+
+// A codeword's pre-sqrt value v, clamped as the reference's sqrt(clamp_min(., 0)) clamps it (NaN
+// and negatives: 0), against the smallest clamped value so far, e_min >= 0.  The common test,
+// !(v >= e_min), holds whenever the clamped value is below e_min (v < e_min, or v NaN, or v <= 0
+// while e_min > 0); the clamp and the exact test follow only then.  New minima are rare after a
+// lane's first codewords, and the empty volatile asm statements keep these branches, so that
+// nothing past the common test is evaluated for every codeword.  The index moves when the new
+// value's correctly rounded sqrt is below e_min's.  A correctly rounded sqrt merges
+// pre-sqrt values less than 2^-21 apart relatively at most (below 2^-126, a few units of the
+// smallest subnormal), so a value below t = e_min (1 - 2^-20) - 2^-146 has the smaller sqrt;
+// between t and e_min the two sqrts are compared.
+__device__ __forceinline__ void take_min(float v, uint32_t j, float& e_min, uint32_t& j_best) {
+    if (!(v >= e_min)) {
+        __asm__ volatile("");
+        const float vc = v > 0.f ? v : 0.f;
+        if (!(vc < e_min)) return;
+        const float t = e_min * 0x1.ffffep-1f - 0x1.0p-146f;
+        if (vc < t) {
+            j_best = j;
+        } else {
+            __asm__ volatile("");
+            if (__builtin_sqrtf(vc) < __builtin_sqrtf(e_min)) j_best = j;
+        }
+        e_min = vc;
+    }
+}
+
+// one LDS stage's codewords sl, sl + S, ... < n (ONE: S == 1) in ascending order; with the block
+// dim known, eight codewords' distances are computed before their minimum checks, so that their
+// LDS reads are in flight together
+template <int BD, bool MM, bool ONE>
+__device__ __forceinline__ void scan_stage(const float* x, float xn, const float* cb, const float* cn, int bd, int sl,
+                                           int S, int n, int j0, float& e_min, uint32_t& j_best) {
+    const int st = ONE ? 1 : S;
+    int j = ONE ? 0 : sl;
+    if (BD) {
+        for (; j + 7 * st < n; j += 8 * st) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = stage_dist<BD, MM>(x, xn, cb, cn, j + u * st, bd);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) take_min(v[u], (uint32_t)(j0 + j + u * st), e_min, j_best);
+        }
+    }
+    for (; j < n; j += st) take_min(stage_dist<BD, MM>(x, xn, cb, cn, j, bd), (uint32_t)(j0 + j), e_min, j_best);
 }
 
 // BD: the block dim at compile time (1, 2, 4 or 8), or 0 for any other (read from the arguments).
@@ -90,7 +144,7 @@ __global__ __launch_bounds__(kWideThreads) void k_encode_wide(const WideEncodePa
     float* cb = smem;                          // [chunk][bd]
     float* cn = smem + (size_t)p.chunk * bd;   // [chunk]
     const float* cent = a.cent + (int64_t)kv * a.cent_sh + (int64_t)blk * nc * bd;
-    float e_min = INFINITY, f_best = INFINITY;
+    float e_min = INFINITY;  // the smallest clamped pre-sqrt value; its sqrt is the lane's distance
     uint32_t j_best = 0;
     for (int j0 = 0; j0 < nc; j0 += p.chunk) {
         const int n = min(p.chunk, nc - j0);
@@ -125,24 +179,18 @@ __global__ __launch_bounds__(kWideThreads) void k_encode_wide(const WideEncodePa
         }
         __syncthreads();
         if (live) {
-            for (int j = sl; j < n; j += S) {
-                const float* c = cb + (size_t)j * bd;
-                // clamped as the reference's sqrt(clamp_min(., 0)): NaN (a non-finite key) is 0
-                const float v = direct ? direct_dist2(x, c, bd) : mm_dist2(x, xn, c, cn[j], bd);
-                const float vc = v > 0.f ? v : 0.f;
-                if (vc < e_min) {
-                    e_min = vc;
-                    const float f = dist_of(v);
-                    if (f < f_best) {
-                        f_best = f;
-                        j_best = (uint32_t)(j0 + j);
-                    }
-                }
+            if (S == 1) {
+                if (direct) scan_stage<BD, false, true>(x, xn, cb, cn, bd, sl, S, n, j0, e_min, j_best);
+                else scan_stage<BD, true, true>(x, xn, cb, cn, bd, sl, S, n, j0, e_min, j_best);
+            } else {
+                if (direct) scan_stage<BD, false, false>(x, xn, cb, cn, bd, sl, S, n, j0, e_min, j_best);
+                else scan_stage<BD, true, false>(x, xn, cb, cn, bd, sl, S, n, j0, e_min, j_best);
             }
         }
     }
     // combine the key's lanes: the smaller distance, then the smaller index (every lane of a
     // workgroup reaches this point; lanes of keys past the end carry infinities and are not stored)
+    float f_best = __builtin_sqrtf(e_min);
     for (int o = S >> 1; o > 0; o >>= 1) {
         const float of = __shfl_xor(f_best, o);
         const uint32_t oj = (uint32_t)__shfl_xor((int)j_best, o);

@@ -78,6 +78,48 @@ def test_wide_encode_bit_exact(D, bd, nc, heavy_n, metric, paged):
         hip_ops.encode(keys.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV), kernel=2)
 
 
+def _merge_codebook(seed, nb, nc, bd, n):
+    """Codewords in pairs one to three ulps apart in one coordinate (shuffled), and keys far from the
+    codebook's cloud: nearest distances then often differ by less than a sqrt rounding, so the
+    first argmin of the distance often is not the first argmin of the pre-sqrt value, and successive
+    pre-sqrt minima fall within 2^-20 of each other."""
+    rng = np.random.default_rng(seed)
+    cent = np.empty((nb, nc, bd), np.float32)
+    for b in range(nb):
+        base = (rng.standard_normal((nc // 2, bd)) * 0.05).astype(np.float32)
+        part = base.copy()
+        bits = part.view(np.int32)
+        steps = rng.integers(1, 4, nc // 2) * rng.choice([-1, 1], nc // 2)
+        bits[np.arange(nc // 2), rng.integers(0, bd, nc // 2)] += steps.astype(np.int32)
+        cent[b] = np.concatenate([base, part])[rng.permutation(nc)]
+    x = (rng.standard_normal((n, nb * bd)) * 0.6).astype(np.float32)
+    return cent, x
+
+
+@pytest.mark.parametrize("n,direct", [(66000, False), (2000, False), (20, True)])
+def test_wide_encode_sqrt_merges(n, direct):
+    """4,096 codewords of dim 4 built so that sqrt merges are common (the first argmin of the
+    distance has a larger pre-sqrt value than another codeword in hundreds of (key, block) pairs):
+    bit-exact with the oracle with one lane per scan (66,000 keys), split scans (2,000 keys) and
+    torch.cdist's direct distance (20 keys)."""
+    log(f"wide encode sqrt merges n={n} direct={direct}")
+    nb, nc, bd = 4, 4096, 4
+    cent, x = _merge_codebook(11 + n, nb, nc, bd, n)
+    perm = np.arange(nb * bd)
+    keep = 0
+    for b in range(nb):
+        e2, d = O.block_distances(x[:, b * bd:(b + 1) * bd], cent[b], direct=direct)
+        jd = d.argmin(1)
+        keep += int((np.maximum(e2[np.arange(n), jd], 0) > np.maximum(e2, 0).min(1)).sum())
+    if n >= 2000:
+        assert keep > 50, keep  # the construction reaches the tie cases it is for
+    ref, _ = O.encode(x, perm, cent, direct=direct, threads=8)
+    codes, _ = hip_ops.encode(torch.from_numpy(x)[None, None].to(DEV), torch.from_numpy(perm)[None].to(DEV),
+                              torch.from_numpy(cent)[None].to(DEV), direct=direct)
+    got = _idx(codes)[0, 0]
+    assert np.array_equal(got, ref.astype(np.int64)), int((got != ref.astype(np.int64)).sum())
+
+
 @pytest.mark.parametrize("nc,bd", [(4096, 4), (65536, 2)])
 def test_wide_dequantize_and_scores(nc, bd):
     log(f"wide dequantize/scores nc={nc} bd={bd}")
