@@ -95,6 +95,7 @@ struct Plan {
     size_t smem;
     size_t ws_bytes;
     bool has_v;
+    bool wide;  // the staged-codebook kernel (ssq_decode_wide.hip)
 };
 
 int pow2_at_least(int x) {
@@ -107,25 +108,30 @@ size_t smem_bytes(const ssq_decode_args& a, int RP, bool has_v) {
     return (red_offset(a, RP, has_v) + 2 * (kThreads / SSQ_WAVE) * RP) * sizeof(float);
 }
 
-int make_plan(const ssq_decode_args& a, Plan& pl) {
-    pl.has_v = a.v != nullptr;
-    pl.G = a.num_q_heads / a.num_kv_heads;
-    pl.rows = pl.G * a.q_len;
-    int R = pl.rows < kMaxRows ? pl.rows : kMaxRows;
-    for (; R >= 1; --R) {
-        if (smem_bytes(a, pow2_at_least(R), pl.has_v) <= kMaxSmem) break;
-    }
-    SSQ_UNSUPPORTED(R >= 1, "codebook too large for LDS: n_blocks*n_centroids=%d", a.n_blocks * a.n_centroids);
-    pl.R = R;
-    pl.RP = pow2_at_least(R);
-    pl.n_groups = (pl.rows + R - 1) / R;
-    pl.smem = smem_bytes(a, pl.RP, pl.has_v);
+// the codebook is 16-byte aligned (per head too) and so is qp after the LUT: vector loads of both
+bool vec_cent_ok(const ssq_decode_args& a) {
+    return (uintptr_t)a.cent % 16 == 0 && (a.cent_sh * 4) % 16 == 0 && a.head_dim % 4 == 0 &&
+           (a.n_blocks * a.n_centroids) % 4 == 0;
+}
+
+// 16-bit codes in 16-byte aligned rows of a multiple of 8 blocks (at most 64) with codewords of 2
+// or 4 dims in a 16-byte aligned codebook: the generic kernel's variants that load a token's code
+// row in 16-byte pieces and gather its codewords in batches (ssq_decode_generic_w16.hip), and the
+// staged-codebook kernel
+bool use_w16(const ssq_decode_args& a) {
+    return ssq_code_width(a.n_centroids) == 2 && a.code_bits == 0 && vec_cent_ok(a) && a.n_blocks % 8 == 0 &&
+           a.n_blocks <= 64 && (a.block_dim == 2 || a.block_dim == 4) && (uintptr_t)a.codes % 16 == 0 &&
+           a.c_sb % 8 == 0 && a.c_sh % 8 == 0 && a.c_st % 8 == 0;
+}
+
+// Splits of at least this many tokens take the staged-codebook kernel: below it a split's codebook
+// copies (nb * nc * bd floats per super-tile) cost more than the per-token gathers they replace.
+constexpr int kWideMinTokens = 2048;
+
+// the splits of a plan with `slots` workgroups running at once
+void plan_splits(const ssq_decode_args& a, Plan& pl, int slots) {
     const int units = a.batch * a.num_kv_heads * pl.n_groups;
     const int tiles = (a.seq_len + kTile - 1) / kTile;
-    // one round of workgroups: as many as the device runs at once at this LDS footprint
-    // (each split rebuilds the LUT, so a second round costs more than it hides)
-    const int per_cu = pl.smem > 0 ? (int)(kMaxSmem / pl.smem) : 1;
-    const int slots = ssq_device_cus() * (per_cu < 1 ? 1 : per_cu > 2 ? 2 : per_cu);
     int splits = a.num_splits > 0 ? a.num_splits : (slots + units - 1) / units;
     if (splits > tiles) splits = tiles;
     if (splits < 1) splits = 1;
@@ -135,6 +141,40 @@ int make_plan(const ssq_decode_args& a, Plan& pl) {
     if (pl.n_splits < 1) pl.n_splits = 1;
     const size_t n_rows_all = (size_t)a.batch * a.num_q_heads * a.q_len;
     pl.ws_bytes = (pl.has_v && pl.n_splits > 1) ? (size_t)pl.n_splits * n_rows_all * (a.value_dim + 2) * 4 : 0;
+}
+
+int make_plan(const ssq_decode_args& a, Plan& pl) {
+    pl.has_v = a.v != nullptr;
+    pl.G = a.num_q_heads / a.num_kv_heads;
+    pl.rows = pl.G * a.q_len;
+    pl.wide = false;
+    if (pl.has_v && use_w16(a) && (a.heavy_mask[0] | a.heavy_mask[1]) == 0 && ssq_decode_wide_fits(a)) {
+        // one workgroup per CU (its LDS), up to 4 rows per workgroup
+        pl.R = pl.rows < 4 ? pl.rows : 4;
+        pl.RP = pow2_at_least(pl.R);
+        pl.n_groups = (pl.rows + pl.R - 1) / pl.R;
+        pl.smem = ssq_decode_wide_smem(a, pl.RP);
+        if (pl.smem <= kMaxSmem) {
+            plan_splits(a, pl, ssq_device_cus());
+            if (pl.split_len >= kWideMinTokens) {
+                pl.wide = true;
+                return SSQ_OK;
+            }
+        }
+    }
+    int R = pl.rows < kMaxRows ? pl.rows : kMaxRows;
+    for (; R >= 1; --R) {
+        if (smem_bytes(a, pow2_at_least(R), pl.has_v) <= kMaxSmem) break;
+    }
+    SSQ_UNSUPPORTED(R >= 1, "codebook too large for LDS: n_blocks*n_centroids=%d", a.n_blocks * a.n_centroids);
+    pl.R = R;
+    pl.RP = pow2_at_least(R);
+    pl.n_groups = (pl.rows + R - 1) / R;
+    pl.smem = smem_bytes(a, pl.RP, pl.has_v);
+    // one round of workgroups: as many as the device runs at once at this LDS footprint
+    // (each split rebuilds the LUT, so a second round costs more than it hides)
+    const int per_cu = pl.smem > 0 ? (int)(kMaxSmem / pl.smem) : 1;
+    plan_splits(a, pl, ssq_device_cus() * (per_cu < 1 ? 1 : per_cu > 2 ? 2 : per_cu));
     return SSQ_OK;
 }
 
@@ -202,8 +242,7 @@ int run_generic(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipS
     const bool aligned = dp.cw == 1 && a->code_bits == 0 && ((uintptr_t)a->codes % 4 == 0) && a->n_blocks % 4 == 0 &&
                          a->c_st % 4 == 0 && a->c_sh % 4 == 0 && a->c_sb % 4 == 0;
     dp.word_codes = aligned ? 1 : 0;
-    dp.vec_cent = ((uintptr_t)a->cent % 16 == 0 && (a->cent_sh * 4) % 16 == 0 && a->head_dim % 4 == 0 &&
-                   (a->n_blocks * a->n_centroids) % 4 == 0) ? 1 : 0;  // qp (after the LUT) 16-byte aligned
+    dp.vec_cent = vec_cent_ok(*a) ? 1 : 0;
     const size_t n_rows_all = (size_t)a->batch * a->num_q_heads * a->q_len;
     float* ws = reinterpret_cast<float*>(workspace);
     dp.ws_o = ws;
@@ -216,19 +255,18 @@ int run_generic(const ssq_decode_args* a, void* workspace, size_t ws_bytes, hipS
                         (a->v_st * esz) % 16 == 0,
                     "V must be 16-byte aligned with 16-byte aligned strides");
     }
+    if (pl.wide) {
+        rc = ssq_decode_wide(dp, pl.RP, pl.n_groups, pl.smem, st);
+        if (rc == SSQ_OK && pl.n_splits > 1) rc = launch_merge(*a, pl.n_splits, dp.ws_o, dp.ws_m, dp.ws_l, st);
+        return rc;
+    }
     SsqGenericLaunch gl;
     gl.RP = pl.RP;
     gl.n_splits = pl.n_splits;
     gl.n_groups = pl.n_groups;
     gl.smem = pl.smem;
     gl.has_v = pl.has_v;
-    // 16-bit codes in 16-byte aligned rows of a multiple of 8 blocks (at most 64) with codewords of
-    // 2 or 4 dims in a 16-byte aligned codebook: the variants that load a token's code row in
-    // 16-byte pieces and gather its codewords in batches (ssq_decode_generic_w16.hip)
-    const bool w16 = dp.cw == 2 && a->code_bits == 0 && dp.vec_cent && a->n_blocks % 8 == 0 && a->n_blocks <= 64 &&
-                     (a->block_dim == 2 || a->block_dim == 4) && (uintptr_t)a->codes % 16 == 0 &&
-                     a->c_sb % 8 == 0 && a->c_sh % 8 == 0 && a->c_st % 8 == 0;
-    rc = w16 ? ssq_generic_w16(dp, gl, st) : launch_generic<false>(dp, gl, st);
+    rc = use_w16(*a) ? ssq_generic_w16(dp, gl, st) : launch_generic<false>(dp, gl, st);
     if (rc) return rc;
     if (pl.has_v && pl.n_splits > 1) {
         rc = launch_merge(*a, pl.n_splits, dp.ws_o, dp.ws_m, dp.ws_l, st);

@@ -824,3 +824,9 @@ int launch_generic(const DecodeParams& dp, const SsqGenericLaunch& gl, hipStream
 
 // the 16-bit-code variants (ssq_decode_generic_w16.hip)
 int ssq_generic_w16(const SsqGenericParams& dp, const SsqGenericLaunch& gl, hipStream_t st);
+
+// the staged-codebook kernel for 16-bit codes over long contexts (ssq_decode_wide.hip): its LDS
+// bytes at RP rows per workgroup, whether the codebook and values suit it, and its launch
+size_t ssq_decode_wide_smem(const ssq_decode_args& a, int RP);
+bool ssq_decode_wide_fits(const ssq_decode_args& a);
+int ssq_decode_wide(const SsqGenericParams& dp, int RP, int n_groups, size_t smem, hipStream_t st);

@@ -201,6 +201,66 @@ def test_wide_decode_vs_oracle(B, Hq, Hkv, Lq, D, bd, nc, T, paged, mask, heavy_
     assert_rel(np_of(lse), rl, SCORE_TOL, "lse")
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,D,bd,nc,T,paged,mask,splits", [
+    (2, 32, 8, 1, 128, 4, 4096, 4500, False, False, 1),  # 3 bits/dim, Llama-shaped: two super-tiles, the last partial
+    (2, 32, 8, 1, 128, 4, 4096, 5000, False, True, 2),   # two splits of 2,560 tokens, a mask
+    (1, 16, 4, 2, 128, 4, 4096, 2300, True, False, 1),   # pages, two query tokens (8 rows: 4-tile super-tiles)
+    (2, 14, 2, 1, 64, 2, 1024, 3000, False, True, 1),    # 5 bits/dim at block_dim 2, 7 query heads per KV head
+    (1, 8, 2, 1, 64, 2, 2048, 2100, True, True, 1),      # pages, a mask, 52 tokens past the first super-tile
+])
+def test_wide_decode_staged_codebook(B, Hq, Hkv, Lq, D, bd, nc, T, paged, mask, splits):
+    """Long contexts (at least 2,048 tokens per split) take k_decode_wide, which stages each block's
+    codebook in LDS for a super-tile of tokens instead of gathering codewords per token.  Output,
+    lse and raw scores against the oracle; the raw scores also equal bit for bit those of the same
+    call split finely enough (256 tokens per split) to take the per-token gathers of
+    k_decode_generic."""
+    log(f"wide staged decode B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} D={D} bd={bd} nc={nc} T={T} paged={paged} "
+        f"mask={mask} splits={splits}")
+    nb = D // bd
+    cb = synthetic.make_codebook(Hkv, D, bd, 640 + nc + T, n_centroids=nc)
+    g = torch.Generator().manual_seed(641 + T)
+    q = torch.randn(B, Hq, Lq, D, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, nc, (B, Hkv, T, nb), generator=g)
+    v = torch.randn(B, Hkv, T, D, generator=g).to(torch.bfloat16)
+    m = None
+    if mask:
+        m = torch.where(torch.rand(B, Hq, Lq, T, generator=g) < 0.2, float("-inf"), 0.0)
+        m[..., 0] = 0.0
+    scale = 1 / math.sqrt(D)
+    codes = idx.to(hip_ops.index_dtype(nc))
+    if paged:
+        page = 16
+        n = (T + page - 1) // page
+        table = torch.randperm(B * n, generator=g).view(B, n).to(torch.int32)
+        cp = torch.zeros(B * n, Hkv, page, nb, dtype=codes.dtype)
+        vp = torch.zeros(B * n, Hkv, D, page, dtype=v.dtype)
+        for b in range(B):
+            for j in range(n):
+                t0, t1 = j * page, min((j + 1) * page, T)
+                cp[table[b, j], :, :t1 - t0] = codes[b, :, t0:t1]
+                vp[table[b, j], :, :, :t1 - t0] = v[b, :, t0:t1].transpose(-1, -2)
+        args = (q.to(DEV), cp.to(DEV), vp.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+        kw = dict(block_table=table.to(DEV), seq_lens=torch.full((B,), T, dtype=torch.int32, device=DEV))
+        md = None if m is None else torch.nn.functional.pad(m, (0, n * page - T))  # over the table's capacity
+    else:
+        args = (q.to(DEV), codes.to(DEV), v.to(DEV), cb.perm.to(DEV), cb.centroids.to(DEV))
+        kw = {}
+        md = m
+    kw.update(scale=scale, mask=None if md is None else md.to(DEV), return_lse=True, return_scores=True)
+    out, lse, sc = hip_ops.decode(*args, num_splits=splits, **kw)
+    _, _, sc_g = hip_ops.decode(*args, num_splits=(T + 255) // 256, **kw)
+    assert torch.equal(sc[..., :T], sc_g[..., :T]), "staged and gathered scores differ"
+    ro, rs, rl = O.decode_attention(q.float().numpy(), idx.numpy(), v.float().numpy(), cb.centroids.numpy(),
+                                    cb.perm.numpy(), scale, "bf16", "bf16", mask=None if m is None else m.numpy(),
+                                    return_scores=True)
+    assert_rel(np_of(out), ro, BF16_TOL, "out")
+    got = np_of(sc[..., :T])
+    fin = np.isfinite(rs)
+    assert np.array_equal(np.isfinite(got), fin)
+    assert_rel(got[fin], rs[fin], SCORE_TOL, "scores")
+    assert_rel(np_of(lse), rl, SCORE_TOL, "lse")
+
+
 def test_wide_codec_backend_and_caches_end_to_end():
     """A 4,096-codeword codec (3 bits/dim at block_dim 4) through the reference's surfaces: codec
     quantize (int16 indices, bit-exact) / dequantize / attention_scores, quantize_key_states +
