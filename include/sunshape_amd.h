@@ -110,8 +110,9 @@ typedef struct ssq_decode_args {
                                                  paged: entries t >= seq_lens[b] are not written */
     /* tuning: 0 = library heuristic */
     int32_t num_splits;
-    int32_t kernel;      /* 0 auto, 1 generic LUT/VALU kernel (codewords gathered from memory past 256
-                            codewords), 2 MFMA LUT kernels (paged: LUT scores, or 4x4-MFMA scores where the
+    int32_t kernel;      /* 0 auto, 1 generic LUT/VALU kernel (past 256 codewords: codewords gathered from
+                            memory, or with 16-bit codes over splits of >= 2048 tokens each block's
+                            codebook staged in LDS per super-tile), 2 MFMA LUT kernels (paged: LUT scores, or 4x4-MFMA scores where the
                             LUT does not fit or a mask / passthrough blocks come; contiguous rows past
                             head_dim 64 with 128-dim values, or scores only; at head_dim 128 the 4x4-MFMA
                             kernel where the LUT needs row groups), 3 MFMA contiguous kernel (head_dim 64),
