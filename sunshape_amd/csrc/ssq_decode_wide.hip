@@ -192,8 +192,7 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
             const int kb = blk & 7;
 #pragma unroll
             for (int k = 0; k < kK; ++k) {
-                const uint32_t ww = (kb >> 1) == 0 ? w[k].x : (kb >> 1) == 1 ? w[k].y : (kb >> 1) == 2 ? w[k].z : w[k].w;
-                const uint32_t code = (kb & 1) ? (ww >> 16) : (ww & 0xFFFFu);
+                const uint32_t code = (kb & 1) ? (w[k].x >> 16) : (w[k].x & 0xFFFFu);  // w[k].x: this pair's word
                 const uint32_t cc = code < (uint32_t)nc ? code : (uint32_t)(nc - 1);
                 float c[4];
                 if (bd == 4) {
@@ -215,6 +214,10 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
                 }
 #pragma unroll
                 for (int r = 0; r < RP; ++r) ss[k][r] += e_acc[r];
+            }
+            if (kb & 1) {  // the next pair's codes move to .x
+#pragma unroll
+                for (int k = 0; k < kK; ++k) w[k] = ssq_v4u{w[k].y, w[k].z, w[k].w, 0u};
             }
             if (more) {  // the other half was last read in the previous block, before its barrier
                 wide_f4* nxt = reinterpret_cast<wide_f4*>(stage + (size_t)((blk + 1) & 1) * ncb);
