@@ -305,6 +305,7 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
 #pragma unroll
                 for (int k = 0; k < kVB; ++k)
                     raw[k] = load_v8_raw<VT, true>(a.v, vbase + (int64_t)(T0 + min(tt0 + k * tpar, nt - 1)) * a.v_st);
+                __asm__ volatile("" ::: "memory");  // the batch's loads stay ahead of every use
 #pragma unroll
                 for (int k = 0; k < kVB; ++k) {
                     const int tt = tt0 + k * tpar;
@@ -320,20 +321,24 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
                 }
             }
         } else {
+            // 8-token chunks in pairs: a thread loads both halves of a 16-token run of its dim back
+            // to back, so the run's line is fetched once
             const int nchunks = (nt + 7) >> 3;
+            const int npairs = (nchunks + 1) >> 1;
             const int64_t vhead = (int64_t)kv * a.v_sh + (int64_t)pv_d * a.v_st;
-            for (int c0 = pv_t; c0 < nchunks; c0 += kVB * tpar) {
+            for (int c0 = pv_t; c0 < npairs; c0 += (kVB / 2) * tpar) {
                 VRaw8<VT> raw[kVB];
 #pragma unroll
                 for (int k = 0; k < kVB; ++k) {
-                    const int tt = min(c0 + k * tpar, nchunks - 1) * 8;
+                    const int tt = min(2 * (c0 + (k >> 1) * tpar) + (k & 1), nchunks - 1) * 8;
                     const int t = T0 + tt;
                     const int off = t - (t / a.page_size) * a.page_size;
                     raw[k] = load_v8_raw<VT, true>(a.v, (int64_t)pgl[tt >> 3] * a.v_sb + vhead + off);
                 }
+                __asm__ volatile("" ::: "memory");  // the batch's loads stay ahead of every use
 #pragma unroll
                 for (int k = 0; k < kVB; ++k) {
-                    const int ch = c0 + k * tpar;
+                    const int ch = 2 * (c0 + (k >> 1) * tpar) + (k & 1);  // increasing in k
                     if (ch >= nchunks) break;
                     const int tt = ch * 8;
                     float v[8];
