@@ -6,11 +6,12 @@
 // and the gathers bound it.  Here a workgroup takes a super-tile of 4,096 tokens of one
 // (batch, KV head) and walks the blocks in order: block blk's codebook (nc * bd floats, at most
 // 64 KiB) is copied into LDS once, every token's codeword of that block is read from there, and
-// its scores (one per query row, at most 4 rows per workgroup) are accumulated in registers.  The copy of block blk + 1 goes
-// into the other half of a double buffer while blk is computed, its loads issued before blk's
-// arithmetic, so one workgroup barrier per block separates them.  The score arithmetic is the
-// per-token path's (the LUT entry's FMA chain over the block's dims from the first product, blocks
-// added in order), so the raw scores equal it bit for bit.
+// its scores (one per query row, at most 4 rows per workgroup) are accumulated in registers.
+// Block blk + 1's codebook goes into the other half of a double buffer while blk is computed
+// (direct global-to-LDS loads issued before blk's arithmetic), so one workgroup barrier per
+// block separates them.  The score arithmetic is the per-token path's (the LUT entry's FMA chain
+// over the block's dims from the first product, blocks added in order), so the raw scores equal it
+// bit for bit.
 //
 // Then per super-tile: mask, optional raw-score store, the softmax update (the super-tile's row
 // maximum), P.V over the super-tile's V rows (streamed, 16 loads in flight per thread), and at the
@@ -25,8 +26,6 @@
 #include "ssq_decode_generic.h"
 
 namespace {
-
-typedef float wide_f4 __attribute__((ext_vector_type(4)));  // register arrays of these stay in VGPRs
 
 constexpr int kWT = 512;                 // threads per workgroup
 constexpr int kWWaves = kWT / SSQ_WAVE;  // 8
@@ -51,6 +50,21 @@ __host__ __device__ inline WideLds wide_lds(const ssq_decode_args& a, int RP) {
     l.pgl = l.red + 2 * kWWaves * RP;
     l.total = l.pgl + sup / 8;
     return l;
+}
+
+// One block's codebook (n4 16-byte pieces, at most 8 * kWT) into an LDS stage half with direct
+// global-to-LDS loads: wave w's u-th load puts its 64 lanes' pieces u * kWT + 64 w + lane at the
+// wave's LDS base + 16 * lane (lanes past n4 are inactive).  Completion is waited for with vmcnt.
+__device__ __forceinline__ void stage_block_lds(const float* src_blk, float* half, int n4, int tid) {
+    const int wbase = tid & ~(SSQ_WAVE - 1);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int i = u * kWT + tid;
+        if (i < n4)
+            __builtin_amdgcn_global_load_lds(static_cast<const void*>(src_blk + (size_t)i * 4),
+                                             (__attribute__((address_space(3))) void*)(half + (size_t)(u * kWT + wbase) * 4),
+                                             16, 0, 0);
+    }
 }
 
 template <int RP, bool PAGED, int VT>
@@ -159,15 +173,8 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
 
         // block 0's codebook into stage half 0 (the previous super-tile's p reads are done: the
         // barrier that ended its P.V)
-        wide_f4 pre[8];
-        {
-            const wide_f4* src = reinterpret_cast<const wide_f4*>(cent);
-#pragma unroll
-            for (int u = 0; u < 8; ++u) pre[u] = src[min(tid + u * kWT, n4 - 1)];
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (tid + u * kWT < n4) reinterpret_cast<wide_f4*>(stage)[tid + u * kWT] = pre[u];
-        }
+        stage_block_lds(cent, stage, n4, tid);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         // 8 blocks' codes of each token: one 16-byte piece of its row
         ssq_v4u w[kK];
@@ -179,11 +186,9 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
             }
             const float* cur = stage + (size_t)(blk & 1) * ncb;
             const bool more = blk + 1 < nb;
-            if (more) {  // the next block's codebook, in flight during this block's arithmetic
-                const wide_f4* src = reinterpret_cast<const wide_f4*>(cent + (int64_t)(blk + 1) * ncb);
-#pragma unroll
-                for (int u = 0; u < 8; ++u) pre[u] = src[min(tid + u * kWT, n4 - 1)];
-            }
+            // the next block's codebook into the other half (last read in the previous block, before
+            // its barrier), in flight during this block's arithmetic
+            if (more) stage_block_lds(cent + (int64_t)(blk + 1) * ncb, stage + (size_t)((blk + 1) & 1) * ncb, n4, tid);
             float qv[RP][4];
 #pragma unroll
             for (int r = 0; r < RP; ++r)
@@ -219,12 +224,7 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
 #pragma unroll
                 for (int k = 0; k < kK; ++k) w[k] = ssq_v4u{w[k].y, w[k].z, w[k].w, 0u};
             }
-            if (more) {  // the other half was last read in the previous block, before its barrier
-                wide_f4* nxt = reinterpret_cast<wide_f4*>(stage + (size_t)((blk + 1) & 1) * ncb);
-#pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    if (tid + u * kWT < n4) nxt[tid + u * kWT] = pre[u];
-            }
+            __builtin_amdgcn_s_waitcnt(0);  // the next half has landed
             __syncthreads();
         }
 
