@@ -67,7 +67,9 @@ __device__ __forceinline__ void stage_block_lds(const float* src_blk, float* hal
     }
 }
 
-template <int RP, bool PAGED, int VT>
+// BD: the block dim, 2 or 4 (the plan's condition), fixed at compile time so that each token's
+// codeword is one LDS read and its FMA chain carries no branches
+template <int RP, bool PAGED, int VT, int BD>
 __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
     extern __shared__ __align__(16) float smem[];
     const ssq_decode_args& a = p.a;
@@ -82,7 +84,8 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
     const int bk = blockIdx.z;
     const int b = bk / a.num_kv_heads;
     const int kv = bk - b * a.num_kv_heads;
-    const int nb = a.n_blocks, nc = a.n_centroids, D = a.head_dim, bd = a.block_dim, Dv = a.value_dim;
+    const int nb = a.n_blocks, nc = a.n_centroids, D = a.head_dim, Dv = a.value_dim;
+    constexpr int bd = BD;
     const int r0 = grp * p.R;
     const int nr = min(p.R, p.rows - r0);
     const int T = PAGED ? min(a.seq_lens[b], a.seq_len) : a.seq_len;
@@ -189,34 +192,31 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
             // the next block's codebook into the other half (last read in the previous block, before
             // its barrier), in flight during this block's arithmetic
             if (more) stage_block_lds(cent + (int64_t)(blk + 1) * ncb, stage + (size_t)((blk + 1) & 1) * ncb, n4, tid);
-            float qv[RP][4];
+            float qv[RP][BD];
 #pragma unroll
             for (int r = 0; r < RP; ++r)
 #pragma unroll
-                for (int d = 0; d < 4; ++d) qv[r][d] = d < bd ? qp[r * D + blk * bd + d] : 0.f;
+                for (int d = 0; d < BD; ++d) qv[r][d] = qp[r * D + blk * BD + d];
             const int kb = blk & 7;
 #pragma unroll
             for (int k = 0; k < kK; ++k) {
                 const uint32_t code = (kb & 1) ? (w[k].x >> 16) : (w[k].x & 0xFFFFu);  // w[k].x: this pair's word
                 const uint32_t cc = code < (uint32_t)nc ? code : (uint32_t)(nc - 1);
-                float c[4];
-                if (bd == 4) {
+                float c[BD];
+                if constexpr (BD == 4) {
                     const float4 v4 = *reinterpret_cast<const float4*>(cur + (size_t)cc * 4);
                     c[0] = v4.x; c[1] = v4.y; c[2] = v4.z; c[3] = v4.w;
                 } else {
                     const float2 v2 = *reinterpret_cast<const float2*>(cur + (size_t)cc * 2);
-                    c[0] = v2.x; c[1] = v2.y; c[2] = 0.f; c[3] = 0.f;
+                    c[0] = v2.x; c[1] = v2.y;
                 }
                 float e_acc[RP];
 #pragma unroll
                 for (int r = 0; r < RP; ++r) e_acc[r] = qv[r][0] * c[0];
 #pragma unroll
-                for (int d = 1; d < 4; ++d) {
-                    if (d < bd) {
+                for (int d = 1; d < BD; ++d)
 #pragma unroll
-                        for (int r = 0; r < RP; ++r) e_acc[r] = fmaf(qv[r][d], c[d], e_acc[r]);
-                    }
-                }
+                    for (int r = 0; r < RP; ++r) e_acc[r] = fmaf(qv[r][d], c[d], e_acc[r]);
 #pragma unroll
                 for (int r = 0; r < RP; ++r) ss[k][r] += e_acc[r];
             }
@@ -422,7 +422,7 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
 
 template <int RP, bool PAGED, int VT>
 int launch_wide_t(const SsqGenericParams& dp, int n_groups, size_t smem, hipStream_t st) {
-    auto kern = k_decode_wide<RP, PAGED, VT>;
+    auto kern = dp.a.block_dim == 4 ? k_decode_wide<RP, PAGED, VT, 4> : k_decode_wide<RP, PAGED, VT, 2>;
     int rc = ssq_allow_lds((const void*)kern, (int)kMaxSmem, "hipFuncSetAttribute(decode wide)");
     if (rc) return rc;
     dim3 grid(dp.n_splits, n_groups, dp.a.batch * dp.a.num_kv_heads);
@@ -446,7 +446,8 @@ size_t ssq_decode_wide_smem(const ssq_decode_args& a, int RP) { return wide_lds(
 
 bool ssq_decode_wide_fits(const ssq_decode_args& a) {
     const size_t ncb = (size_t)a.n_centroids * a.block_dim;
-    return ncb % 4 == 0 && ncb / 4 <= (size_t)8 * kWT && (a.value_dim == 64 || a.value_dim == 128) &&
+    return (a.block_dim == 2 || a.block_dim == 4) && ncb % 4 == 0 && ncb / 4 <= (size_t)8 * kWT &&
+           (a.value_dim == 64 || a.value_dim == 128) &&
            (a.v_dtype == SSQ_BF16 || a.v_dtype == SSQ_F16);
 }
 
