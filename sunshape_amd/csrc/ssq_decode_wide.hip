@@ -157,6 +157,7 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
                 const int t = min(T0 + 8 * c, t_end - 1);
                 pgl[c] = a.block_table[(int64_t)b * a.bt_sb + t / a.page_size];
             }
+            __syncthreads();  // the page list is read below (code rows) by other threads
         }
         // the code row (16-bit elements) of this thread's k-th token
         auto code_row = [&](int k) -> int64_t {
@@ -174,18 +175,32 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
 #pragma unroll
             for (int r = 0; r < RP; ++r) ss[k][r] = 0.f;
 
-        // block 0's codebook into stage half 0 (the previous super-tile's p reads are done: the
+        // 8 blocks' codes of each token: one 16-byte piece of its row, the first one loaded beside
+        // block 0's codebook copy into stage half 0 (the previous super-tile's p reads are done: the
         // barrier that ended its P.V)
+        ssq_v4u w[kK];
+#pragma unroll
+        for (int k = 0; k < kK; ++k) w[k] = *reinterpret_cast<const ssq_v4u*>(codes + code_row(k));
         stage_block_lds(cent, stage, n4, tid);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        // 8 blocks' codes of each token: one 16-byte piece of its row
-        ssq_v4u w[kK];
 #pragma unroll 1
         for (int blk = 0; blk < nb; ++blk) {
-            if ((blk & 7) == 0) {
+            const int kb = blk & 7;
+            uint32_t cw[kK];  // this block's codeword of each token (w[k].x: this block pair's word)
 #pragma unroll
-                for (int k = 0; k < kK; ++k) w[k] = *reinterpret_cast<const ssq_v4u*>(codes + code_row(k) + blk);
+            for (int k = 0; k < kK; ++k) {
+                const uint32_t code = (kb & 1) ? (w[k].x >> 16) : (w[k].x & 0xFFFFu);
+                cw[k] = code < (uint32_t)nc ? code : (uint32_t)(nc - 1);
+            }
+            if (kb == 7) {  // w is spent: the next 8 blocks' piece loads during this block's arithmetic
+                if (blk + 1 < nb) {
+#pragma unroll
+                    for (int k = 0; k < kK; ++k) w[k] = *reinterpret_cast<const ssq_v4u*>(codes + code_row(k) + blk + 1);
+                }
+            } else if (kb & 1) {  // the next pair's codes move to .x
+#pragma unroll
+                for (int k = 0; k < kK; ++k) w[k] = ssq_v4u{w[k].y, w[k].z, w[k].w, 0u};
             }
             const float* cur = stage + (size_t)(blk & 1) * ncb;
             const bool more = blk + 1 < nb;
@@ -197,11 +212,9 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
             for (int r = 0; r < RP; ++r)
 #pragma unroll
                 for (int d = 0; d < BD; ++d) qv[r][d] = qp[r * D + blk * BD + d];
-            const int kb = blk & 7;
 #pragma unroll
             for (int k = 0; k < kK; ++k) {
-                const uint32_t code = (kb & 1) ? (w[k].x >> 16) : (w[k].x & 0xFFFFu);  // w[k].x: this pair's word
-                const uint32_t cc = code < (uint32_t)nc ? code : (uint32_t)(nc - 1);
+                const uint32_t cc = cw[k];
                 float c[BD];
                 if constexpr (BD == 4) {
                     const float4 v4 = *reinterpret_cast<const float4*>(cur + (size_t)cc * 4);
@@ -220,11 +233,7 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
 #pragma unroll
                 for (int r = 0; r < RP; ++r) ss[k][r] += e_acc[r];
             }
-            if (kb & 1) {  // the next pair's codes move to .x
-#pragma unroll
-                for (int k = 0; k < kK; ++k) w[k] = ssq_v4u{w[k].y, w[k].z, w[k].w, 0u};
-            }
-            __builtin_amdgcn_s_waitcnt(0);  // the next half has landed
+            __builtin_amdgcn_s_waitcnt(0);  // the next half (and at kb 7 the next code piece) has landed
             __syncthreads();
         }
 
