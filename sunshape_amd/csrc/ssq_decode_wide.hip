@@ -29,6 +29,7 @@ namespace {
 
 constexpr int kWT = 512;                 // threads per workgroup
 constexpr int kWWaves = kWT / SSQ_WAVE;  // 8
+constexpr int kPD = 4;                   // value dims per thread in the paged P.V
 
 // tokens per thread per super-tile (the super-tile is kWT times that); at most 4 query rows per
 // workgroup (more rows take further workgroups)
@@ -44,6 +45,7 @@ __host__ __device__ inline WideLds wide_lds(const ssq_decode_args& a, int RP) {
     size_t r0 = 2 * ncb;                                              // double-buffered codebook stage
     if ((size_t)RP * sup > r0) r0 = (size_t)RP * sup;                 // the super-tile's p
     if ((size_t)kWWaves * RP * a.value_dim > r0) r0 = (size_t)kWWaves * RP * a.value_dim;  // epilogue
+    if ((size_t)kWT * kPD * RP > r0) r0 = (size_t)kWT * kPD * RP;     // paged epilogue: kWT*kPD/Dv slots
     WideLds l;
     l.qp = (r0 + 3) & ~(size_t)3;
     l.red = l.qp + (size_t)RP * a.head_dim;
@@ -136,9 +138,10 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
 #pragma unroll
     for (int r = 0; r < RP; ++r) { m_run[r] = -INFINITY; l_thr[r] = 0.f; }
     // P.V mapping: contiguous rows, 8 dims of one token per thread and load; pages [P, Hkv, Dv,
-    // page], 8 tokens of one dim per thread and load
-    constexpr int kAccW = PAGED ? 1 : 8;
-    const int dchunks = PAGED ? Dv : Dv / 8;
+    // page], 8 tokens of one dim per load and kPD dims per thread, pv_d + dd * dchunks (one read of
+    // the chunk's p for kPD loads; a load's lanes stay on consecutive dims)
+    constexpr int kAccW = PAGED ? kPD : 8;
+    const int dchunks = PAGED ? Dv / kPD : Dv / 8;
     const int tpar = kWT / dchunks;
     const int pv_t = tid / dchunks;
     const int pv_d = tid - pv_t * dchunks;
@@ -334,37 +337,50 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
             // to back, so the run's line is fetched once
             const int nchunks = (nt + 7) >> 3;
             const int npairs = (nchunks + 1) >> 1;
+            // load k of a batch: pair q = k / (2 kPD), dim dd = (k / 2) % kPD, half h = k % 2
+            constexpr int kPairs = kVB / (2 * kPD);
             const int64_t vhead = (int64_t)kv * a.v_sh + (int64_t)pv_d * a.v_st;
-            for (int c0 = pv_t; c0 < npairs; c0 += (kVB / 2) * tpar) {
+            for (int c0 = pv_t; c0 < npairs; c0 += kPairs * tpar) {
                 VRaw8<VT> raw[kVB];
 #pragma unroll
                 for (int k = 0; k < kVB; ++k) {
-                    const int tt = min(2 * (c0 + (k >> 1) * tpar) + (k & 1), nchunks - 1) * 8;
+                    const int q = k / (2 * kPD), dd = (k >> 1) % kPD;
+                    const int tt = min(2 * (c0 + q * tpar) + (k & 1), nchunks - 1) * 8;
                     const int t = T0 + tt;
                     const int off = t - (t / a.page_size) * a.page_size;
-                    raw[k] = load_v8_raw<VT, true>(a.v, (int64_t)pgl[tt >> 3] * a.v_sb + vhead + off);
+                    raw[k] = load_v8_raw<VT, true>(a.v, (int64_t)pgl[tt >> 3] * a.v_sb + vhead + (int64_t)(dd * dchunks) * a.v_st + off);
                 }
                 __asm__ volatile("" ::: "memory");  // the batch's loads stay ahead of every use
 #pragma unroll
-                for (int k = 0; k < kVB; ++k) {
-                    const int ch = 2 * (c0 + (k >> 1) * tpar) + (k & 1);  // increasing in k
-                    if (ch >= nchunks) break;
-                    const int tt = ch * 8;
-                    float v[8];
-                    unpack_v8<VT>(raw[k], v);
+                for (int q = 0; q < kPairs; ++q) {
 #pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        if (tt + j >= nt) v[j] = 0.f;  // tokens past the end: p = 0 and V unwritten
+                    for (int h = 0; h < 2; ++h) {
+                        const int ch = 2 * (c0 + q * tpar) + h;  // increasing in (q, h)
+                        if (ch >= nchunks) break;
+                        const int tt = ch * 8;
+                        float4 p0[RP], p1[RP];
 #pragma unroll
-                    for (int r = 0; r < RP; ++r) {
-                        const float4 p0 = *reinterpret_cast<const float4*>(pbuf + (size_t)r * kSup + tt);
-                        const float4 p1 = *reinterpret_cast<const float4*>(pbuf + (size_t)r * kSup + tt + 4);
-                        float x = acc[r][0];
-                        x = fmaf(p0.x, v[0], x); x = fmaf(p0.y, v[1], x);
-                        x = fmaf(p0.z, v[2], x); x = fmaf(p0.w, v[3], x);
-                        x = fmaf(p1.x, v[4], x); x = fmaf(p1.y, v[5], x);
-                        x = fmaf(p1.z, v[6], x); x = fmaf(p1.w, v[7], x);
-                        acc[r][0] = x;
+                        for (int r = 0; r < RP; ++r) {
+                            p0[r] = *reinterpret_cast<const float4*>(pbuf + (size_t)r * kSup + tt);
+                            p1[r] = *reinterpret_cast<const float4*>(pbuf + (size_t)r * kSup + tt + 4);
+                        }
+#pragma unroll
+                        for (int dd = 0; dd < kPD; ++dd) {
+                            float v[8];
+                            unpack_v8<VT>(raw[(q * kPD + dd) * 2 + h], v);
+#pragma unroll
+                            for (int j = 0; j < 8; ++j)
+                                if (tt + j >= nt) v[j] = 0.f;  // tokens past the end: p = 0 and V unwritten
+#pragma unroll
+                            for (int r = 0; r < RP; ++r) {
+                                float x = acc[r][dd];
+                                x = fmaf(p0[r].x, v[0], x); x = fmaf(p0[r].y, v[1], x);
+                                x = fmaf(p0[r].z, v[2], x); x = fmaf(p0[r].w, v[3], x);
+                                x = fmaf(p1[r].x, v[4], x); x = fmaf(p1[r].y, v[5], x);
+                                x = fmaf(p1[r].z, v[6], x); x = fmaf(p1[r].w, v[7], x);
+                                acc[r][dd] = x;
+                            }
+                        }
                     }
                 }
             }
@@ -398,7 +414,9 @@ __global__ __launch_bounds__(kWT) void k_decode_wide(const SsqGenericParams p) {
     } else {
         slots = tpar;
 #pragma unroll
-        for (int r = 0; r < RP; ++r) obuf[((size_t)pv_t * RP + r) * Dv + pv_d] = acc[r][0];
+        for (int r = 0; r < RP; ++r)
+#pragma unroll
+            for (int dd = 0; dd < kAccW; ++dd) obuf[((size_t)pv_t * RP + r) * Dv + pv_d + dd * dchunks] = acc[r][dd];
     }
     __syncthreads();
     const int n_rows_all = a.batch * a.num_q_heads * a.q_len;
