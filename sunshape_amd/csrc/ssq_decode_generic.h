@@ -438,50 +438,54 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(const DecodeParams 
                 constexpr int kBat = 16;
                 const uint4* cr4 = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.codes) + cofs);
                 uint4 cn0 = ld16g<true>(cr4), cn1 = nb > 8 ? ld16g<true>(cr4 + 1) : make_uint4(0u, 0u, 0u, 0u);
-                for (int b0 = 0; b0 < nb; b0 += kBat) {
-                    const uint32_t cw16[8] = {cn0.x, cn0.y, cn0.z, cn0.w, cn1.x, cn1.y, cn1.z, cn1.w};
-                    uint32_t code_k[kBat];
+                // the block dim (2 or 4, a condition of this variant) fixed at compile time: each
+                // codeword is one vector load and the FMA chain carries no per-dim branches
+                auto batches = [&](auto bd_c) {
+                    constexpr int BD = decltype(bd_c)::value;
+                    for (int b0 = 0; b0 < nb; b0 += kBat) {
+                        const uint32_t cw16[8] = {cn0.x, cn0.y, cn0.z, cn0.w, cn1.x, cn1.y, cn1.z, cn1.w};
+                        uint32_t code_k[kBat];
 #pragma unroll
-                    for (int k = 0; k < kBat; ++k) code_k[k] = (k & 1) ? (cw16[k >> 1] >> 16) : (cw16[k >> 1] & 0xFFFFu);
-                    float cv[kBat][4];
+                        for (int k = 0; k < kBat; ++k) code_k[k] = (k & 1) ? (cw16[k >> 1] >> 16) : (cw16[k >> 1] & 0xFFFFu);
+                        float cv[kBat][BD];
 #pragma unroll
-                    for (int k = 0; k < kBat; ++k) {
-                        const uint32_t cc = code_k[k] < (uint32_t)nc ? code_k[k] : (uint32_t)(nc - 1);
-                        const float* c = cent + ((int64_t)min(b0 + k, nb - 1) * nc + cc) * bd;
-                        if (bd == 4) {
-                            const float4 v4 = *reinterpret_cast<const float4*>(c);
-                            cv[k][0] = v4.x; cv[k][1] = v4.y; cv[k][2] = v4.z; cv[k][3] = v4.w;
-                        } else {
-                            const float2 v2 = *reinterpret_cast<const float2*>(c);
-                            cv[k][0] = v2.x; cv[k][1] = v2.y; cv[k][2] = 0.f; cv[k][3] = 0.f;
-                        }
-                    }
-                    if (b0 + kBat < nb) {  // the next batch's codes
-                        cn0 = ld16g<true>(cr4 + ((b0 + kBat) >> 3));
-                        cn1 = b0 + kBat + 8 < nb ? ld16g<true>(cr4 + ((b0 + kBat) >> 3) + 1) : make_uint4(0u, 0u, 0u, 0u);
-                    }
-#pragma unroll
-                    for (int k = 0; k < kBat; ++k) {
-                        const int blk = b0 + k;
-                        if (blk >= nb) break;
-                        if (ssq_is_heavy(a.heavy_mask[0], a.heavy_mask[1], blk)) {
-                            add_block(blk, code_k[k]);
-                            continue;
-                        }
-                        float e_acc[RP];
-#pragma unroll
-                        for (int r = 0; r < RP; ++r) e_acc[r] = qp[r * D + blk * bd] * cv[k][0];
-#pragma unroll
-                        for (int d = 1; d < 4; ++d) {
-                            if (d < bd) {
-#pragma unroll
-                                for (int r = 0; r < RP; ++r) e_acc[r] = fmaf(qp[r * D + blk * bd + d], cv[k][d], e_acc[r]);
+                        for (int k = 0; k < kBat; ++k) {
+                            const uint32_t cc = code_k[k] < (uint32_t)nc ? code_k[k] : (uint32_t)(nc - 1);
+                            const float* c = cent + ((int64_t)min(b0 + k, nb - 1) * nc + cc) * BD;
+                            if constexpr (BD == 4) {
+                                const float4 v4 = *reinterpret_cast<const float4*>(c);
+                                cv[k][0] = v4.x; cv[k][1] = v4.y; cv[k][2] = v4.z; cv[k][3] = v4.w;
+                            } else {
+                                const float2 v2 = *reinterpret_cast<const float2*>(c);
+                                cv[k][0] = v2.x; cv[k][1] = v2.y;
                             }
                         }
+                        if (b0 + kBat < nb) {  // the next batch's codes
+                            cn0 = ld16g<true>(cr4 + ((b0 + kBat) >> 3));
+                            cn1 = b0 + kBat + 8 < nb ? ld16g<true>(cr4 + ((b0 + kBat) >> 3) + 1) : make_uint4(0u, 0u, 0u, 0u);
+                        }
 #pragma unroll
-                        for (int r = 0; r < RP; ++r) s[r] += e_acc[r];
+                        for (int k = 0; k < kBat; ++k) {
+                            const int blk = b0 + k;
+                            if (blk >= nb) break;
+                            if (ssq_is_heavy(a.heavy_mask[0], a.heavy_mask[1], blk)) {
+                                add_block(blk, code_k[k]);
+                                continue;
+                            }
+                            float e_acc[RP];
+#pragma unroll
+                            for (int r = 0; r < RP; ++r) e_acc[r] = qp[r * D + blk * BD] * cv[k][0];
+#pragma unroll
+                            for (int d = 1; d < BD; ++d)
+#pragma unroll
+                                for (int r = 0; r < RP; ++r) e_acc[r] = fmaf(qp[r * D + blk * BD + d], cv[k][d], e_acc[r]);
+#pragma unroll
+                            for (int r = 0; r < RP; ++r) s[r] += e_acc[r];
+                        }
                     }
-                }
+                };
+                if (bd == 4) batches(std::integral_constant<int, 4>{});
+                else batches(std::integral_constant<int, 2>{});
             } else if (p.cw > 1 && bd <= 4) {
                 // 16- / 32-bit codes (code strides count elements of that width), codewords of at most
                 // 4 dims: per batch of 8 blocks the codes are loaded together, then the codewords,
